@@ -1,0 +1,205 @@
+"""Depthformer streaming-decode benchmark on one MI355X.
+
+Workload (one "step" = one 2 s chunk): bf16 model d_model 1024 / 16 heads x 64 /
+d_ff 2816 / 12 encoder, 20 temporal, 4 depth layers / vocab 29824, seeded
+random weights; batch 1 stream (2 CFG rows); per chunk the encoder re-runs on
+the sliding 10 s context (1006 tokens), then 50 frames x 16 RVQ levels are
+decoded with free-running CFG (w=5) top-k 40 / T 1.1 sampling on the device.
+Chunks are consecutive: the context carries the generated tokens and the seed
+is base + chunk index.
+
+Prints one JSON line: value = RVQ tokens/s (800 tokens per chunk / chunk
+seconds), plus chunk ms p50/p99, RTF, the HBM roofline of the decode and the
+CPU baseline (the numpy restatement timed on a bounded sample on this host).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG = ROOT / "magenta-realtime-mlx-cpp_amd"
+for p in (ROOT, PKG):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def percentile(sorted_vals, p):
+    """Interpolated percentile as the reference CLI computes it (cli/main.cpp:496-505)."""
+    if not sorted_vals:
+        return 0.0
+    idx = p / 100.0 * (len(sorted_vals) - 1)
+    lo = int(np.floor(idx))
+    hi = min(lo + 1, len(sorted_vals) - 1)
+    frac = idx - lo
+    return sorted_vals[lo] * (1 - frac) + sorted_vals[hi] * frac
+
+
+def algorithmic_bytes(cfg, esz=2, rows=2, frames=50, enc_len=1006, codebook=1024):
+    """HBM bytes one chunk's decode must move: every weight once per use plus KV reads."""
+    D, HD, F, H = cfg.d_model, cfg.num_heads * cfg.d_kv, cfg.d_ff, cfg.num_heads
+    L = cfg.rvq_depth
+    self_layer = (3 * HD * D + HD * D + 3 * F * D) * esz + 2 * D * esz  # qkv, o, ffn, 2 norms
+    depth_step = cfg.num_depth_layers * self_layer + D * esz + codebook * D * esz
+    temporal_layer = self_layer + (2 * HD * D + D) * esz  # + cross q, o, norm
+    cross_kv = cfg.num_temporal_layers * 2 * rows * H * enc_len * 64 * esz
+    temporal_step = cfg.num_temporal_layers * temporal_layer + cross_kv
+    kv_row = 2 * rows * H * 64 * esz  # K and V of one position
+    depth_kv = sum(cfg.num_depth_layers * kv_row * (l + 1) for l in range(L)) * frames
+    temporal_kv = sum(cfg.num_temporal_layers * kv_row * (f + 1) for f in range(frames))
+    total = frames * (temporal_step + L * depth_step) + depth_kv + temporal_kv
+    return dict(depth_step=depth_step, temporal_step=temporal_step, chunk=total)
+
+
+def cpu_baseline(weights, cfg, enc_tokens, budget_s=20.0):
+    """Time the numpy restatement (fp32) on a bounded sample of the same chunk."""
+    import dataclasses
+    from oracle import depthformer_oracle as O
+    om = O.OracleDepthformer(weights, O.DepthformerConfig(**dataclasses.asdict(cfg)), mode="fp32")
+    t0 = time.perf_counter()
+    enc = om.encode(enc_tokens)
+    t_enc = time.perf_counter() - t0
+    cache = om.empty_temporal_cache()
+    x = om.embed(np.zeros((2, 1), dtype=np.int64))
+    t_temporal, t_depth, n_t, n_d = 0.0, 0.0, 0, 0
+    t_start = time.perf_counter()
+    f = 0
+    while (time.perf_counter() - t_start) < budget_s - t_enc and f < 50:
+        t1 = time.perf_counter()
+        y = om.temporal_step(x, enc, cache, f)
+        t_temporal += time.perf_counter() - t1
+        n_t += 1
+        dcache = om.empty_depth_cache()
+        d_in = y
+        for l in range(cfg.rvq_depth):
+            t1 = time.perf_counter()
+            om.depth_step(d_in, dcache, l)
+            t_depth += time.perf_counter() - t1
+            n_d += 1
+            d_in = om.embed(np.full((2, 1), 2 + 1024 * l, dtype=np.int64))
+        f += 1
+    chunk_s = t_enc + 50 * (t_temporal / n_t) + 800 * (t_depth / n_d)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    threads = int(os.environ.get("OMP_NUM_THREADS", cores))
+    return {
+        "value": 800.0 / chunk_s,
+        "unit": "RVQ tokens/s",
+        "cores": min(cores, threads),
+        "kind": "port",
+        "sample": (f"numpy fp32 restatement: 1 encoder pass + {n_t} temporal steps + {n_d} depth "
+                   f"steps, extrapolated to one 50x16 chunk ({chunk_s * 1e3:.0f} ms/chunk)"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30, help="timed chunks")
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--seed", type=int, default=1234)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it "
+                                   "(independent streams would each take a GPU with zero communication)"}))
+        sys.exit(2)
+
+    import torch
+    import mrt_df
+    import synth_bundle
+    import system
+
+    cfg = mrt_df.Config.bench()
+    t0 = time.perf_counter()
+    weights = synth_bundle.make_weights(cfg, seed=args.seed, threads=16)
+    t_gen = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    model = mrt_df.Depthformer(weights, cfg, dtype=args.dtype, device=0)
+    t_load = time.perf_counter() - t0
+    print(f"[bench] weights generated in {t_gen:.1f}s, uploaded in {t_load:.1f}s", file=sys.stderr, flush=True)
+
+    scfg = system.SystemConfig()
+    rng = np.random.default_rng(42)
+    style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+    sess = system.StreamingSession(model, scfg, style=style, seed=args.seed, temperature=1.1, top_k=40,
+                                   guidance_weight=5.0, use_graph=not args.no_graph)
+    stream = torch.cuda.ExternalStream(sess.state.stream_handle())
+
+    for i in range(args.warmup):
+        t0 = time.perf_counter()
+        sess.generate_chunk()
+        print(f"[bench] warmup chunk {i}: {(time.perf_counter() - t0) * 1e3:.1f} ms", file=sys.stderr, flush=True)
+
+    torch.cuda.synchronize()
+    wall, gpu = [], []
+    t_all = time.perf_counter()
+    for i in range(args.steps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        sess.generate_chunk()
+        e1.record(stream)
+        e1.synchronize()
+        wall.append((time.perf_counter() - t0) * 1e3)
+        gpu.append(e0.elapsed_time(e1))
+    torch.cuda.synchronize()
+    total_s = time.perf_counter() - t_all
+    ms = sorted(wall)
+    mean_ms = float(np.mean(wall))
+    ab = algorithmic_bytes(cfg, esz=2 if args.dtype == "bf16" else 4)
+    gpu_mean = float(np.mean(gpu))
+    achieved = ab["chunk"] / (gpu_mean * 1e-3) / 1e9
+    print(f"[bench] chunk ms mean {mean_ms:.2f} p50 {percentile(ms, 50):.2f} p99 {percentile(ms, 99):.2f}; "
+          f"gpu {gpu_mean:.2f} ms; {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        enc = system.build_encoder_inputs(sess.context, scfg, style)
+        cpu = cpu_baseline(weights, cfg, enc, budget_s=args.cpu_budget)
+
+    out = {
+        "metric": "RVQ tokens/s per 2 s chunk (batch 1, 2 CFG rows)",
+        "value": 800.0 * args.steps / total_s,
+        "unit": "RVQ tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": mean_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic (seeded random weights, free-running sampled tokens)",
+        "config": {"workload": "streaming chunks: encoder 12L over 1006 ctx tokens + 50 frames x "
+                               "(temporal 20L + 16 x depth 4L) decode, top-k 40, T 1.1, CFG w 5",
+                   "d_model": 1024, "heads": 16, "d_ff": 2816, "vocab": 29824, "rows": 2,
+                   "graph": not args.no_graph},
+        "chunk_ms_p50": percentile(ms, 50),
+        "chunk_ms_p99": percentile(ms, 99),
+        "rtf": 2000.0 / mean_ms,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "unit_of_work": "one chunk (encoder + 50 temporal + 800 depth steps)",
+                     "algorithmic_bytes": ab["chunk"]},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

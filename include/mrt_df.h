@@ -1,0 +1,176 @@
+/*
+ * mrt_df.h -- C ABI of the MI355X (gfx950) Depthformer streaming-decode backend.
+ *
+ * Drop-in for the Depthformer hot path of magenta-realtime-mlx-cpp: the
+ * `Depthformer::{encode, temporal_step, depth_step}` methods, the `.mlxfn`
+ * imported-function ABI they dispatch to, and the `generate_tokens` 50x16
+ * block-autoregressive loop.  Citations are to files of that project.
+ *
+ * Conventions
+ *   - Every function returns MRT_OK (0) or an error code; the message of the
+ *     last error on the calling thread is `mrt_last_error()`.  No C++
+ *     exception crosses this boundary (the reference throws
+ *     std::runtime_error / std::out_of_range at the same places).
+ *   - Activation tensors passed to step functions are DEVICE pointers in the
+ *     model dtype (fp32 or bf16 raw bits) on the handle's device; logits are
+ *     fp32 device buffers.  Token arrays are HOST int32.
+ *   - A model handle owns the weights; a state handle owns one decode stream's
+ *     encoder output, cross-attention K/V, ring KV caches, scratch and HIP
+ *     stream.  Calls on one state are not thread-safe; distinct states may be
+ *     driven from distinct threads.
+ */
+#ifndef MRT_DF_H_
+#define MRT_DF_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MRT_OK 0
+#define MRT_ERR_INVALID 1     /* bad argument / shape / cache length   */
+#define MRT_ERR_STATE 2       /* call order violated (e.g. no encoder)  */
+#define MRT_ERR_HIP 3         /* HIP runtime failure                    */
+#define MRT_ERR_MISSING_KEY 4 /* weight bundle lacks a tensor           */
+#define MRT_ERR_FORMAT 5      /* malformed bundle                       */
+#define MRT_ERR_INTERNAL 6
+
+#define MRT_DTYPE_F32 0
+#define MRT_DTYPE_BF16 1
+
+/* DepthformerConfig (src/magenta_realtime_mlx/depthformer/model.h:47-68). */
+typedef struct mrt_df_config {
+  int32_t vocab_size;
+  int32_t d_model;
+  int32_t d_kv;
+  int32_t d_ff;
+  int32_t num_heads;
+  int32_t num_encoder_layers;
+  int32_t num_temporal_layers;
+  int32_t num_depth_layers;
+  int32_t max_encoder_length;
+  int32_t rvq_depth;
+  int32_t temporal_num_buckets;
+  int32_t temporal_max_distance;
+  int32_t depth_num_buckets;
+  int32_t depth_max_distance;
+} mrt_df_config;
+
+/* GenerateOptions (depthformer/decode.h:48-57) plus the vocabulary layout
+ * of SystemConfig (system.h:44-83) that build_vocab_masks encodes
+ * (system.cpp:135-157). */
+typedef struct mrt_gen_opts {
+  int32_t num_frames;      /* 50 */
+  int32_t rvq_depth;       /* 16 */
+  float temperature;       /* 1.1; 0 -> argmax */
+  int32_t top_k;           /* 40; <= 0 -> no top-k */
+  float guidance_weight;   /* 5.0 streaming, 4.0 GenerateOptions default */
+  uint64_t seed;           /* per-chunk seed (base seed + chunk index) */
+  int32_t codebook_size;   /* 1024 */
+  int32_t codec_offset;    /* 2 */
+  const int32_t* teacher;  /* optional host (num_frames, rvq_depth) ids fed back instead of draws */
+  int32_t use_graph;       /* replay the decode loop from a captured hipGraph */
+  /* Optional DEVICE buffers filled during the loop (parity / inspection): */
+  float* record_slices;    /* (F, L, rows, codebook) level-slice logits (fp32) */
+  void* record_temporal;   /* (F, rows, d_model) temporal_step outputs (model dtype) */
+  int32_t* record_drawn;   /* (F, L) the model's own draws (device) */
+  void* record_frame_mean; /* (F, rows, d_model) mean of each frame's 16 level embeddings */
+} mrt_gen_opts;
+
+typedef struct mrt_df mrt_df;
+typedef struct mrt_df_state mrt_df_state;
+
+/* Thread-local message of the last failing call ("" when none). */
+const char* mrt_last_error(void);
+
+/* DepthformerConfig::base() / ::large() (depthformer/model.cpp:34-48). */
+void mrt_df_config_base(mrt_df_config* cfg);
+void mrt_df_config_large(mrt_df_config* cfg);
+
+/* Depthformer::Depthformer(bundle, config, dtype) (model.cpp:173-213) with
+ * WeightBundle loading (weights.cpp:118-133): reads the fp32 .safetensors
+ * bundle (key layout model.cpp:177-198, modules.cpp:342-381), casts to
+ * `dtype`, repacks and uploads to `device`. */
+int mrt_df_create(const char* bundle_path, const mrt_df_config* cfg, int dtype, int device,
+                  mrt_df** out);
+/* Same, from caller-owned fp32 host arrays named with the bundle keys. */
+int mrt_df_create_from_tensors(int n, const char* const* names, const float* const* data,
+                               const int64_t* const* shapes, const int32_t* ndims,
+                               const mrt_df_config* cfg, int dtype, int device, mrt_df** out);
+void mrt_df_destroy(mrt_df* h);
+int mrt_df_get_config(const mrt_df* h, mrt_df_config* cfg, int* dtype);
+
+/* Per-stream state: rows = 2 (CFG pair) per stream; KV rings sized for
+ * `max_frames` temporal steps and cfg.rvq_depth depth steps; encoder
+ * length `enc_len` (<= max_encoder_length).  Replaces the caller-owned
+ * std::vector<LayerCache> of empty_{temporal,depth}_cache (model.cpp:280-300). */
+int mrt_df_state_create(mrt_df* h, int rows, int max_frames, int enc_len, mrt_df_state** out);
+void mrt_df_state_destroy(mrt_df_state* st);
+/* The state's hipStream_t (all work of the state is ordered on it). */
+int mrt_df_state_stream(mrt_df_state* st, void** hip_stream);
+int mrt_df_sync(mrt_df_state* st);
+
+/* Depthformer::encode (model.cpp:226-241): tokens (rows, enc_len) host int32
+ * -> encoder output, then the cross-attention K/V of every temporal layer
+ * (DecoderLayer::precompute_cross_kv, modules.cpp:448-455), kept in the state. */
+int mrt_df_encode(mrt_df_state* st, const int32_t* tokens);
+
+/* Depthformer::temporal_step (model.cpp:322-514): frame_emb (rows, d_model)
+ * device, model dtype -> out (rows, d_model) (no final norm).  If
+ * `enc_out` is non-null and frame_idx == 0, the cross K/V are projected from
+ * it first (the eager frame-0 path, modules.cpp:397-404); otherwise those of
+ * the last mrt_df_encode are used.  The temporal cache must hold exactly
+ * frame_idx entries (it is reset by frame_idx == 0). */
+int mrt_df_temporal_step(mrt_df_state* st, const void* frame_emb, const void* enc_out,
+                         int frame_idx, void* out);
+
+/* Depthformer::depth_step (model.cpp:516-659): tok_emb (rows, d_model) device
+ * -> logits.  level < 0: full vocabulary (rows, vocab_size) fp32 (the
+ * reference's return value); level >= 0: only lm_head rows
+ * [codec_offset + codebook*level, +codebook) as (rows, codebook) fp32 --
+ * exact under the level's vocabulary mask (system.cpp:135-157).  The depth
+ * cache must hold exactly depth_idx entries (reset by depth_idx == 0). */
+int mrt_df_depth_step(mrt_df_state* st, const void* tok_emb, int depth_idx, int level,
+                      int codebook_size, int codec_offset, float* logits);
+
+/* generate_tokens (depthformer/decode.cpp:239-573), non-speculative path:
+ * enc_tokens (rows, enc_len) host int32 (NULL: reuse the last encode) ->
+ * out_tokens (num_frames, rvq_depth) host int32 LLM ids.  CFG, level mask,
+ * temperature/top-k sampling, token feedback and the frame mean all run on
+ * the device; the host syncs once at the end. */
+int mrt_df_generate_tokens(mrt_df_state* st, const int32_t* enc_tokens, const mrt_gen_opts* opts,
+                           int32_t* out_tokens);
+
+/* One draw of the decode loop (decode.cpp:465-474): cfg_combine
+ * (decode.cpp:71-85) of rows 0/1 of `slice` (device fp32, (2, codebook) --
+ * one level's logits, i.e. apply_vocab_mask of decode.cpp:87-91 already
+ * applied by slicing), then sample_with_temperature (decode.cpp:124-148):
+ * argmax at temperature 0, else top_k_logits (ties at the threshold kept,
+ * decode.cpp:104-122) and a categorical draw by Gumbel-max with Philox noise
+ * keyed by (seed, frame, level, candidate).  Writes the LLM id
+ * codec_offset + codebook*level + index to *token (host). */
+int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts* opts, int frame,
+                        int level, int32_t* token);
+
+/* State buffers exposed for parity checks (device-to-device copies). */
+#define MRT_BUF_ENC_OUT 0     /* (rows, enc_len, d_model)                       */
+#define MRT_BUF_CROSS_K 1     /* layer: (rows, heads, enc_len, d_kv)            */
+#define MRT_BUF_CROSS_V 2
+#define MRT_BUF_TEMPORAL_K 3  /* layer: (rows, heads, max_frames, d_kv) ring    */
+#define MRT_BUF_TEMPORAL_V 4
+#define MRT_BUF_DEPTH_K 5     /* layer: (rows, heads, rvq_depth, d_kv) ring     */
+#define MRT_BUF_DEPTH_V 6
+int mrt_df_state_buffer_bytes(mrt_df_state* st, int which, size_t* bytes);
+int mrt_df_state_read(mrt_df_state* st, int which, int layer, void* dst, size_t bytes);
+int mrt_df_state_write(mrt_df_state* st, int which, int layer, const void* src, size_t bytes);
+/* Declare how many ring slots hold valid K/V (kind 0: temporal, 1: depth), e.g.
+ * after mrt_df_state_write for a step micro-benchmark at a given cache length. */
+int mrt_df_state_set_cache_length(mrt_df_state* st, int kind, int length);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MRT_DF_H_ */

@@ -1,0 +1,258 @@
+// extern "C" boundary of the Depthformer HIP backend (include/mrt_df.h).
+// Every entry point converts C++ exceptions into a status code and a
+// thread-local message; nothing throws across the ABI.
+#include "../../include/mrt_df.h"
+
+#include <memory>
+#include <string>
+
+#include "model.hpp"
+
+struct mrt_df {
+  std::unique_ptr<mrt::Model> model;
+};
+
+struct mrt_df_state {
+  mrt_df* owner;
+  std::unique_ptr<mrt::State> state;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <class Fn>
+int guarded(Fn&& fn) {
+  try {
+    g_last_error.clear();
+    fn();
+    return MRT_OK;
+  } catch (const mrt::Error& e) {
+    g_last_error = e.what();
+    return e.code;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return MRT_ERR_INTERNAL;
+  } catch (...) {
+    g_last_error = "unknown error";
+    return MRT_ERR_INTERNAL;
+  }
+}
+
+mrt::Config to_config(const mrt_df_config* c) {
+  mrt::Config k;
+  k.vocab_size = c->vocab_size;
+  k.d_model = c->d_model;
+  k.d_kv = c->d_kv;
+  k.d_ff = c->d_ff;
+  k.num_heads = c->num_heads;
+  k.num_encoder_layers = c->num_encoder_layers;
+  k.num_temporal_layers = c->num_temporal_layers;
+  k.num_depth_layers = c->num_depth_layers;
+  k.max_encoder_length = c->max_encoder_length;
+  k.rvq_depth = c->rvq_depth;
+  k.temporal_num_buckets = c->temporal_num_buckets;
+  k.temporal_max_distance = c->temporal_max_distance;
+  k.depth_num_buckets = c->depth_num_buckets;
+  k.depth_max_distance = c->depth_max_distance;
+  return k;
+}
+
+void from_config(const mrt::Config& k, mrt_df_config* c) {
+  c->vocab_size = k.vocab_size;
+  c->d_model = k.d_model;
+  c->d_kv = k.d_kv;
+  c->d_ff = k.d_ff;
+  c->num_heads = k.num_heads;
+  c->num_encoder_layers = k.num_encoder_layers;
+  c->num_temporal_layers = k.num_temporal_layers;
+  c->num_depth_layers = k.num_depth_layers;
+  c->max_encoder_length = k.max_encoder_length;
+  c->rvq_depth = k.rvq_depth;
+  c->temporal_num_buckets = k.temporal_num_buckets;
+  c->temporal_max_distance = k.temporal_max_distance;
+  c->depth_num_buckets = k.depth_num_buckets;
+  c->depth_max_distance = k.depth_max_distance;
+}
+
+mrt::DType to_dtype(int d) {
+  if (d == MRT_DTYPE_F32) return mrt::DType::F32;
+  if (d == MRT_DTYPE_BF16) return mrt::DType::BF16;
+  throw mrt::Error(MRT_ERR_INVALID, "unknown dtype " + std::to_string(d) + "; expected fp32|bf16");
+}
+
+mrt::GenOpts to_opts(const mrt_gen_opts* opts) {
+  mrt::GenOpts o;
+  o.num_frames = opts->num_frames;
+  o.rvq_depth = opts->rvq_depth;
+  o.temperature = opts->temperature;
+  o.top_k = opts->top_k;
+  o.guidance_weight = opts->guidance_weight;
+  o.seed = opts->seed;
+  o.codebook = opts->codebook_size;
+  o.codec_offset = opts->codec_offset;
+  o.teacher = opts->teacher;
+  o.use_graph = opts->use_graph != 0;
+  o.record_slices = opts->record_slices;
+  o.record_temporal = opts->record_temporal;
+  o.record_drawn = opts->record_drawn;
+  o.record_frame_mean = opts->record_frame_mean;
+  return o;
+}
+
+mrt::State& S(mrt_df_state* st) {
+  if (!st || !st->state) throw mrt::Error(MRT_ERR_INVALID, "null state handle");
+  return *st->state;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mrt_last_error(void) { return g_last_error.c_str(); }
+
+void mrt_df_config_base(mrt_df_config* cfg) {
+  if (cfg) from_config(mrt::Config::base(), cfg);
+}
+
+void mrt_df_config_large(mrt_df_config* cfg) {
+  if (cfg) from_config(mrt::Config::large(), cfg);
+}
+
+int mrt_df_create(const char* bundle_path, const mrt_df_config* cfg, int dtype, int device, mrt_df** out) {
+  return guarded([&] {
+    if (!bundle_path || !cfg || !out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *out = nullptr;
+    mrt::SafetensorsFile src(bundle_path);
+    auto h = std::make_unique<mrt_df>();
+    h->model = std::make_unique<mrt::Model>(src, to_config(cfg), to_dtype(dtype), device);
+    *out = h.release();
+  });
+}
+
+int mrt_df_create_from_tensors(int n, const char* const* names, const float* const* data,
+                               const int64_t* const* shapes, const int32_t* ndims, const mrt_df_config* cfg,
+                               int dtype, int device, mrt_df** out) {
+  return guarded([&] {
+    if (!names || !data || !shapes || !ndims || !cfg || !out || n < 0)
+      throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *out = nullptr;
+    mrt::TensorList src;
+    for (int i = 0; i < n; ++i) {
+      if (!names[i] || !data[i] || ndims[i] < 0) throw mrt::Error(MRT_ERR_INVALID, "bad tensor entry");
+      src.add(names[i], data[i], std::vector<int64_t>(shapes[i], shapes[i] + ndims[i]));
+    }
+    auto h = std::make_unique<mrt_df>();
+    h->model = std::make_unique<mrt::Model>(src, to_config(cfg), to_dtype(dtype), device);
+    *out = h.release();
+  });
+}
+
+void mrt_df_destroy(mrt_df* h) { delete h; }
+
+int mrt_df_get_config(const mrt_df* h, mrt_df_config* cfg, int* dtype) {
+  return guarded([&] {
+    if (!h || !h->model) throw mrt::Error(MRT_ERR_INVALID, "null model handle");
+    if (cfg) from_config(h->model->cfg, cfg);
+    if (dtype) *dtype = h->model->dt == mrt::DType::F32 ? MRT_DTYPE_F32 : MRT_DTYPE_BF16;
+  });
+}
+
+int mrt_df_state_create(mrt_df* h, int rows, int max_frames, int enc_len, mrt_df_state** out) {
+  return guarded([&] {
+    if (!h || !h->model || !out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *out = nullptr;
+    auto st = std::make_unique<mrt_df_state>();
+    st->owner = h;
+    st->state = std::make_unique<mrt::State>(*h->model, rows, max_frames, enc_len);
+    *out = st.release();
+  });
+}
+
+void mrt_df_state_destroy(mrt_df_state* st) { delete st; }
+
+int mrt_df_state_stream(mrt_df_state* st, void** hip_stream) {
+  return guarded([&] {
+    if (!hip_stream) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *hip_stream = S(st).stream;
+  });
+}
+
+int mrt_df_sync(mrt_df_state* st) {
+  return guarded([&] { S(st).sync(); });
+}
+
+int mrt_df_encode(mrt_df_state* st, const int32_t* tokens) {
+  return guarded([&] {
+    if (!tokens) throw mrt::Error(MRT_ERR_INVALID, "null tokens");
+    S(st).encode(tokens);
+  });
+}
+
+int mrt_df_temporal_step(mrt_df_state* st, const void* frame_emb, const void* enc_out, int frame_idx,
+                         void* out) {
+  return guarded([&] {
+    if (!frame_emb || !out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    S(st).temporal_step(frame_emb, enc_out, frame_idx, out);
+  });
+}
+
+int mrt_df_depth_step(mrt_df_state* st, const void* tok_emb, int depth_idx, int level, int codebook_size,
+                      int codec_offset, float* logits) {
+  return guarded([&] {
+    if (!tok_emb || !logits) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    S(st).depth_step(tok_emb, depth_idx, level, codebook_size, codec_offset, logits);
+  });
+}
+
+int mrt_df_generate_tokens(mrt_df_state* st, const int32_t* enc_tokens, const mrt_gen_opts* opts,
+                           int32_t* out_tokens) {
+  return guarded([&] {
+    if (!opts || !out_tokens) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    S(st).generate(enc_tokens, to_opts(opts), out_tokens);
+  });
+}
+
+int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts* opts, int frame, int level,
+                        int32_t* token) {
+  return guarded([&] {
+    if (!slice || !opts || !token) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *token = S(st).sample(slice, to_opts(opts), frame, level);
+  });
+}
+
+int mrt_df_state_buffer_bytes(mrt_df_state* st, int which, size_t* bytes) {
+  return guarded([&] {
+    if (!bytes) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    S(st).buffer(which, 0, bytes);
+  });
+}
+
+int mrt_df_state_read(mrt_df_state* st, int which, int layer, void* dst, size_t bytes) {
+  return guarded([&] {
+    if (!dst) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    size_t n = 0;
+    void* src = S(st).buffer(which, layer, &n);
+    if (bytes != n) throw mrt::Error(MRT_ERR_INVALID, "state_read: size mismatch (" + std::to_string(n) + " bytes)");
+    MRT_HIP_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, S(st).stream));
+    S(st).sync();
+  });
+}
+
+int mrt_df_state_write(mrt_df_state* st, int which, int layer, const void* src, size_t bytes) {
+  return guarded([&] {
+    if (!src) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    size_t n = 0;
+    void* dst = S(st).buffer(which, layer, &n);
+    if (bytes != n) throw mrt::Error(MRT_ERR_INVALID, "state_write: size mismatch (" + std::to_string(n) + " bytes)");
+    MRT_HIP_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, S(st).stream));
+    S(st).sync();
+    if (which == MRT_BUF_CROSS_K || which == MRT_BUF_CROSS_V) S(st).set_cache_length(2, 1);
+  });
+}
+
+int mrt_df_state_set_cache_length(mrt_df_state* st, int kind, int length) {
+  return guarded([&] { S(st).set_cache_length(kind, length); });
+}
+
+}  // extern "C"

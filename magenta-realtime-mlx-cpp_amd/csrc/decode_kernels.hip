@@ -1,0 +1,513 @@
+// Batch-1 (2 CFG rows) decode kernels for gfx950: GEMVs with fused RMSNorm
+// prologue and fused epilogues, ring-KV self-attention with the T5 relative
+// position bias, split-key cross-attention, embedding gathers.
+//
+// Every weight byte is read exactly once per call with 16-byte vector loads
+// (one 1 KiB coalesced segment per wave instruction); the work per byte is 2
+// FMAs (2 CFG rows), so these kernels are HBM/MALL-bandwidth bound.
+#include <algorithm>
+#include <cmath>
+
+#include "device_utils.hpp"
+#include "kernels.hpp"
+
+namespace mrt {
+namespace {
+
+constexpr int kGemvThreads = 256;
+constexpr int kMaxSelfLen = 1024;
+constexpr int kMaxCrossChunk = 256;
+
+// ---- epilogues ----------------------------------------------------------------
+
+template <typename T, int NB>
+struct EpiStore {
+  T* y;
+  int ldy;
+  __device__ void operator()(int n, const float (&a)[1][NB]) const {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) y[(size_t)b * ldy + n] = St<T>::st(a[0][b]);
+  }
+};
+
+template <typename T, int NB>
+struct EpiF32 {
+  float* y;
+  int ldy;
+  __device__ void operator()(int n, const float (&a)[1][NB]) const {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) y[(size_t)b * ldy + n] = St<T>::rnd(a[0][b]);
+  }
+};
+
+template <typename T, int NB>
+struct EpiResid {
+  T* r;
+  int ldr;
+  __device__ void operator()(int n, const float (&a)[1][NB]) const {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      T* p = r + (size_t)b * ldr + n;
+      *p = St<T>::st(St<T>::ld(*p) + St<T>::rnd(a[0][b]));
+    }
+  }
+};
+
+template <typename T, int NB>
+struct EpiQKV {
+  T* q;
+  T* kc;
+  T* vc;
+  int HD, H, Lmax, pos;
+  __device__ void operator()(int n, const float (&a)[1][NB]) const {
+    const int which = n / HD;
+    const int nn = n - which * HD;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const T v = St<T>::st(a[0][b]);
+      if (which == 0) {
+        q[(size_t)b * HD + nn] = v;
+      } else {
+        const int h = nn >> 6, d = nn & 63;
+        T* c = which == 1 ? kc : vc;
+        c[(((size_t)b * H + h) * Lmax + pos) * 64 + d] = v;
+      }
+    }
+  }
+};
+
+template <typename T, int NB>
+struct EpiGeglu {
+  T* h;
+  int ldh;
+  __device__ void operator()(int j, const float (&a)[2][NB]) const {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float g = gelu_t<T>(St<T>::rnd(a[0][b]));
+      h[(size_t)b * ldh + j] = St<T>::st(g * St<T>::rnd(a[1][b]));
+    }
+  }
+};
+
+// ---- GEMV ---------------------------------------------------------------------
+// Block = 4 waves; each wave owns R consecutive outputs.  P = 1: output n is
+// weight row n.  P = 2: output j reads the gate/up row pair of the 32-row
+// packed wi_0/wi_1 matrix.  Lane l covers 16-byte chunks l, l+64, ... of each
+// row, so one wave instruction streams a contiguous 1 KiB of the row.
+template <typename T, int NB, int R, int P, class Epi>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv(const T* __restrict__ W, int nout, int K,
+                                                     const T* __restrict__ X, int ldx,
+                                                     const T* __restrict__ g, float eps, Epi epi) {
+  using S = St<T>;
+  constexpr int V = S::kVec;
+  extern __shared__ float xs[];  // NB * K activations (normalised when g != null)
+  __shared__ float red[4][NB];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+
+  float ss[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    ss[b] = 0.f;
+    for (int k = tid; k < K; k += kGemvThreads) {
+      const float v = S::ld(X[(size_t)b * ldx + k]);
+      xs[b * K + k] = v;
+      ss[b] += v * v;
+    }
+  }
+  if (g != nullptr) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float t = wave_sum(ss[b]);
+      if (lane == 0) red[wid][b] = t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float tot = red[0][b] + red[1][b] + red[2][b] + red[3][b];
+      const float inv = 1.0f / sqrtf(tot / (float)K + eps);
+      for (int k = tid; k < K; k += kGemvThreads)
+        xs[b * K + k] = S::rnd(S::rnd(xs[b * K + k] * inv) * S::ld(g[k]));
+    }
+  }
+  __syncthreads();
+
+  const int o0 = (blockIdx.x * 4 + wid) * R;
+  if (o0 >= nout) return;  // no barrier below this point
+  const T* wrow[R][P];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int o = (o0 + r < nout) ? o0 + r : o0;
+    if constexpr (P == 1) {
+      wrow[r][0] = W + (size_t)o * K;
+    } else {
+      const size_t gr = (size_t)(o >> 5) * 64 + (o & 31);
+      wrow[r][0] = W + gr * K;
+      wrow[r][1] = W + (gr + 32) * K;
+    }
+  }
+  float acc[R][P][NB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[r][p][b] = 0.f;
+
+  const int nch = K / V;
+  for (int c = lane; c < nch; c += 64) {
+    uint4 wv[R][P];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        wv[r][p] = ld_nt16(wrow[r][p] + (size_t)c * V);
+    float xv[NB][V];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int e = 0; e < V; ++e) xv[b][e] = xs[b * K + c * V + e];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const T* we = reinterpret_cast<const T*>(&wv[r][p]);
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float w = S::ld(we[e]);
+#pragma unroll
+          for (int b = 0; b < NB; ++b) acc[r][p][b] = fmaf(w, xv[b][e], acc[r][p][b]);
+        }
+      }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[r][p][b] = wave_sum(acc[r][p][b]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (o0 + r < nout) epi(o0 + r, acc[r]);
+  }
+}
+
+template <typename T, int NB, int P, class Epi>
+void launch_gemv_t(const void* W, int nout, int K, const void* X, int ldx, NormArg norm, Epi epi,
+                   hipStream_t s) {
+  MRT_REQUIRE(K % St<T>::kVec == 0, "gemv: K must be a multiple of the vector width");
+  const size_t lds = (size_t)NB * K * sizeof(float);
+  MRT_REQUIRE(lds <= 64 * 1024, "gemv: activation tile exceeds 64 KiB of LDS");
+  auto go = [&](auto rtag) {
+    constexpr int R = decltype(rtag)::value;
+    const int blocks = (nout + 4 * R - 1) / (4 * R);
+    hipLaunchKernelGGL((k_gemv<T, NB, R, P, Epi>), dim3(blocks), dim3(kGemvThreads), lds, s,
+                       static_cast<const T*>(W), nout, K, static_cast<const T*>(X), ldx,
+                       static_cast<const T*>(norm.g), norm.eps, epi);
+  };
+  // Aim for >= 256 workgroups (one per CU) while keeping >= 2 rows in flight
+  // per wave on the larger matrices.
+  if (nout >= 8192 * P)
+    go(std::integral_constant<int, 4>{});
+  else if (nout >= 2048)
+    go(std::integral_constant<int, 2>{});
+  else
+    go(std::integral_constant<int, 1>{});
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace
+
+// The public launchers spell out the (dtype, nb) dispatch explicitly.
+#define MRT_NB_DISPATCH(nb, BODY)                                          \
+  switch (nb) {                                                            \
+    case 1: { constexpr int NB = 1; BODY; break; }                         \
+    case 2: { constexpr int NB = 2; BODY; break; }                         \
+    case 4: { constexpr int NB = 4; BODY; break; }                         \
+    default: throw Error(1, "decode kernels support nb in {1, 2, 4}");      \
+  }
+
+void gemv_store(DType dt, int nb, const void* W, int N, int K, const void* X, int ldx,
+                NormArg norm, void* Y, int ldy, hipStream_t s) {
+  if (dt == DType::F32) {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 1>(W, N, K, X, ldx, norm,
+                                                     EpiStore<float, NB>{static_cast<float*>(Y), ldy}, s)));
+  } else {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 1>(W, N, K, X, ldx, norm,
+                                                    EpiStore<bf16, NB>{static_cast<bf16*>(Y), ldy}, s)));
+  }
+}
+
+void gemv_f32(DType dt, int nb, const void* W, int N, int K, const void* X, int ldx,
+              NormArg norm, float* Y, int ldy, hipStream_t s) {
+  if (dt == DType::F32) {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 1>(W, N, K, X, ldx, norm, EpiF32<float, NB>{Y, ldy}, s)));
+  } else {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 1>(W, N, K, X, ldx, norm, EpiF32<bf16, NB>{Y, ldy}, s)));
+  }
+}
+
+void gemv_resid(DType dt, int nb, const void* W, int N, int K, const void* X, int ldx,
+                NormArg norm, void* R, int ldr, hipStream_t s) {
+  if (dt == DType::F32) {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 1>(W, N, K, X, ldx, norm,
+                                                     EpiResid<float, NB>{static_cast<float*>(R), ldr}, s)));
+  } else {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 1>(W, N, K, X, ldx, norm,
+                                                    EpiResid<bf16, NB>{static_cast<bf16*>(R), ldr}, s)));
+  }
+}
+
+void gemv_qkv(DType dt, int nb, const void* W, int HD, int K, const void* X, int ldx,
+              NormArg norm, void* Q, void* Kc, void* Vc, int H, int Lmax, int pos,
+              hipStream_t s) {
+  MRT_REQUIRE(HD == H * 64, "gemv_qkv: head dim must be 64");
+  MRT_REQUIRE(pos >= 0 && pos < Lmax, "gemv_qkv: ring position out of range");
+  if (dt == DType::F32) {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 1>(
+                            W, 3 * HD, K, X, ldx, norm,
+                            EpiQKV<float, NB>{static_cast<float*>(Q), static_cast<float*>(Kc),
+                                              static_cast<float*>(Vc), HD, H, Lmax, pos},
+                            s)));
+  } else {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 1>(
+                            W, 3 * HD, K, X, ldx, norm,
+                            EpiQKV<bf16, NB>{static_cast<bf16*>(Q), static_cast<bf16*>(Kc),
+                                             static_cast<bf16*>(Vc), HD, H, Lmax, pos},
+                            s)));
+  }
+}
+
+void gemv_geglu(DType dt, int nb, const void* W01, int F, int K, const void* X, int ldx,
+                NormArg norm, void* Hout, int ldh, hipStream_t s) {
+  MRT_REQUIRE(F % 32 == 0, "gemv_geglu: d_ff must be a multiple of 32");
+  if (dt == DType::F32) {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 2>(W01, F, K, X, ldx, norm,
+                                                     EpiGeglu<float, NB>{static_cast<float*>(Hout), ldh}, s)));
+  } else {
+    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 2>(W01, F, K, X, ldx, norm,
+                                                    EpiGeglu<bf16, NB>{static_cast<bf16*>(Hout), ldh}, s)));
+  }
+}
+
+// ---- self-attention over the ring KV ----------------------------------------------
+namespace {
+
+template <typename T>
+__global__ __launch_bounds__(64) void k_self_attn(const T* __restrict__ Q, const T* __restrict__ Kc,
+                                                  const T* __restrict__ Vc, int H, int Lmax, int len,
+                                                  int qpos, const T* __restrict__ bias_tab,
+                                                  const int* __restrict__ buckets, T* __restrict__ out) {
+  using S = St<T>;
+  constexpr int V = S::kVec;
+  const int bh = blockIdx.x, b = bh / H, h = bh - b * H, lane = threadIdx.x;
+  const int HD = H * 64;
+  __shared__ float qs[64];
+  __shared__ float ps[kMaxSelfLen];
+  qs[lane] = S::ld(Q[(size_t)b * HD + h * 64 + lane]);
+  __syncthreads();
+  const T* Kp = Kc + (size_t)bh * Lmax * 64;
+  const T* Vp = Vc + (size_t)bh * Lmax * 64;
+  float mx = -INFINITY;
+  for (int j = lane; j < len; j += 64) {
+    const T* kr = Kp + (size_t)j * 64;
+    float sc = 0.f;
+#pragma unroll
+    for (int d = 0; d < 64; d += V) {
+      const uint4 kv = *reinterpret_cast<const uint4*>(kr + d);
+      const T* ke = reinterpret_cast<const T*>(&kv);
+#pragma unroll
+      for (int e = 0; e < V; ++e) sc = fmaf(qs[d + e], S::ld(ke[e]), sc);
+    }
+    sc += S::ld(bias_tab[buckets[qpos - j] * H + h]);
+    ps[j] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int j = lane; j < len; j += 64) {
+    const float p = expf(ps[j] - mx);
+    ps[j] = p;
+    sum += p;
+  }
+  sum = wave_sum(sum);
+  __syncthreads();
+  float o = 0.f;
+  for (int j = 0; j < len; ++j) o = fmaf(ps[j], S::ld(Vp[(size_t)j * 64 + lane]), o);
+  out[(size_t)b * HD + h * 64 + lane] = S::st(o / sum);
+}
+
+// Partial softmax-attention of one (row, head) over one block of keys.
+template <typename T>
+__global__ __launch_bounds__(64) void k_cross_part(const T* __restrict__ Q, const T* __restrict__ Kc,
+                                                   const T* __restrict__ Vc, int H, int S, int nsplit,
+                                                   float* __restrict__ part) {
+  using St_ = St<T>;
+  constexpr int V = St_::kVec;
+  const int blk = blockIdx.x, bh = blk / nsplit, sp = blk - bh * nsplit;
+  const int b = bh / H, h = bh - b * H, lane = threadIdx.x;
+  const int HD = H * 64;
+  const int chunk = (S + nsplit - 1) / nsplit;
+  const int j0 = sp * chunk, j1 = min(S, j0 + chunk);
+  __shared__ float qs[64];
+  __shared__ float ps[kMaxCrossChunk];
+  qs[lane] = St_::ld(Q[(size_t)b * HD + h * 64 + lane]);
+  __syncthreads();
+  const T* Kp = Kc + (size_t)bh * S * 64;
+  const T* Vp = Vc + (size_t)bh * S * 64;
+  float mx = -INFINITY;
+  for (int j = j0 + lane; j < j1; j += 64) {
+    const T* kr = Kp + (size_t)j * 64;
+    float sc = 0.f;
+#pragma unroll
+    for (int d = 0; d < 64; d += V) {
+      const uint4 kv = ld_nt16(kr + d);
+      const T* ke = reinterpret_cast<const T*>(&kv);
+#pragma unroll
+      for (int e = 0; e < V; ++e) sc = fmaf(qs[d + e], St_::ld(ke[e]), sc);
+    }
+    ps[j - j0] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int j = j0 + lane; j < j1; j += 64) {
+    const float p = expf(ps[j - j0] - mx);
+    ps[j - j0] = p;
+    sum += p;
+  }
+  sum = wave_sum(sum);
+  __syncthreads();
+  float o = 0.f;
+  for (int j = j0; j < j1; ++j) o = fmaf(ps[j - j0], St_::ld(Vp[(size_t)j * 64 + lane]), o);
+  float* dst = part + (size_t)blk * 66;
+  if (lane == 0) {
+    dst[0] = mx;
+    dst[1] = sum;
+  }
+  dst[2 + lane] = o;
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void k_cross_combine(const float* __restrict__ part, int H, int nsplit,
+                                                      T* __restrict__ out) {
+  const int bh = blockIdx.x, b = bh / H, h = bh - b * H, lane = threadIdx.x;
+  const float* p = part + (size_t)bh * nsplit * 66;
+  float M = -INFINITY;
+  for (int i = 0; i < nsplit; ++i) M = fmaxf(M, p[i * 66]);
+  float L = 0.f, O = 0.f;
+  for (int i = 0; i < nsplit; ++i) {
+    const float m = p[i * 66];
+    if (m == -INFINITY) continue;
+    const float c = expf(m - M);
+    L = fmaf(p[i * 66 + 1], c, L);
+    O = fmaf(p[i * 66 + 2 + lane], c, O);
+  }
+  out[(size_t)b * H * 64 + h * 64 + lane] = St<T>::st(O / L);
+}
+
+template <typename T>
+__global__ void k_embed_rows(const T* __restrict__ emb, int D, const int* __restrict__ ids,
+                             T* __restrict__ out) {
+  const int r = blockIdx.x;
+  const T* src = emb + (size_t)ids[r] * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) out[(size_t)r * D + d] = src[d];
+}
+
+__global__ void k_copy16(uint4* __restrict__ dst, const uint4* __restrict__ src, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+__global__ void k_copy1(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+template <typename T>
+__global__ void k_embed_fill(const T* __restrict__ emb, int D, int id, T* __restrict__ out) {
+  const int r = blockIdx.x;
+  const T* src = emb + (size_t)id * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) out[(size_t)r * D + d] = src[d];
+}
+
+}  // namespace
+
+void self_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H, int Lmax,
+               int len, int qpos, const void* bias_tab, const int* buckets, void* out,
+               hipStream_t s) {
+  MRT_REQUIRE(len >= 1 && len <= kMaxSelfLen && len <= Lmax, "self_attn: bad cache length");
+  MRT_REQUIRE(qpos >= len - 1, "self_attn: query precedes keys");
+  if (dt == DType::F32)
+    hipLaunchKernelGGL(k_self_attn<float>, dim3(nb * H), dim3(64), 0, s, (const float*)Q,
+                       (const float*)Kc, (const float*)Vc, H, Lmax, len, qpos,
+                       (const float*)bias_tab, buckets, (float*)out);
+  else
+    hipLaunchKernelGGL(k_self_attn<bf16>, dim3(nb * H), dim3(64), 0, s, (const bf16*)Q,
+                       (const bf16*)Kc, (const bf16*)Vc, H, Lmax, len, qpos,
+                       (const bf16*)bias_tab, buckets, (bf16*)out);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+int cross_attn_splits(int S) {
+  int n = (S + 63) / 64;
+  return n < 1 ? 1 : n;
+}
+
+void cross_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H, int S,
+                void* out, float* part, int nsplit, hipStream_t s) {
+  MRT_REQUIRE(S >= 1, "cross_attn: empty encoder output");
+  MRT_REQUIRE((S + nsplit - 1) / nsplit <= kMaxCrossChunk, "cross_attn: key block too large");
+  if (dt == DType::F32) {
+    hipLaunchKernelGGL(k_cross_part<float>, dim3(nb * H * nsplit), dim3(64), 0, s, (const float*)Q,
+                       (const float*)Kc, (const float*)Vc, H, S, nsplit, part);
+    hipLaunchKernelGGL(k_cross_combine<float>, dim3(nb * H), dim3(64), 0, s, part, H, nsplit,
+                       (float*)out);
+  } else {
+    hipLaunchKernelGGL(k_cross_part<bf16>, dim3(nb * H * nsplit), dim3(64), 0, s, (const bf16*)Q,
+                       (const bf16*)Kc, (const bf16*)Vc, H, S, nsplit, part);
+    hipLaunchKernelGGL(k_cross_combine<bf16>, dim3(nb * H), dim3(64), 0, s, part, H, nsplit,
+                       (bf16*)out);
+  }
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void embed_rows(DType dt, const void* emb, int D, const int* ids, int rows, void* out,
+                hipStream_t s) {
+  if (rows <= 0) return;
+  if (dt == DType::F32)
+    hipLaunchKernelGGL(k_embed_rows<float>, dim3(rows), dim3(256), 0, s, (const float*)emb, D, ids,
+                       (float*)out);
+  else
+    hipLaunchKernelGGL(k_embed_rows<bf16>, dim3(rows), dim3(256), 0, s, (const bf16*)emb, D, ids,
+                       (bf16*)out);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void copy_dev(void* dst, const void* src, size_t bytes, hipStream_t s) {
+  if (bytes == 0 || dst == src) return;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src) | bytes) & 15) == 0;
+  if (aligned) {
+    const size_t n = bytes / 16;
+    const int blocks = (int)std::min<size_t>((n + 255) / 256, 1024);
+    hipLaunchKernelGGL(k_copy16, dim3(blocks), dim3(256), 0, s, static_cast<uint4*>(dst),
+                       static_cast<const uint4*>(src), n);
+  } else {
+    const int blocks = (int)std::min<size_t>((bytes + 255) / 256, 1024);
+    hipLaunchKernelGGL(k_copy1, dim3(blocks), dim3(256), 0, s, static_cast<uint8_t*>(dst),
+                       static_cast<const uint8_t*>(src), bytes);
+  }
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void embed_fill(DType dt, const void* emb, int D, int id, int rows, void* out, hipStream_t s) {
+  if (dt == DType::F32)
+    hipLaunchKernelGGL(k_embed_fill<float>, dim3(rows), dim3(256), 0, s, (const float*)emb, D, id,
+                       (float*)out);
+  else
+    hipLaunchKernelGGL(k_embed_fill<bf16>, dim3(rows), dim3(256), 0, s, (const bf16*)emb, D, id,
+                       (bf16*)out);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace mrt

@@ -1,0 +1,341 @@
+// Once-per-chunk encoder prefill kernels for gfx950 (model.cpp:226-241,
+// modules.cpp:339-358) and the cross-attention K/V projection of every
+// temporal layer (modules.cpp:448-455) as one wide GEMM.
+//
+// GEMM operands are both K-contiguous ("NT": activations (M, K) row-major,
+// weights (N, K) row-major as the bundle stores them).  bf16 uses
+// v_mfma_f32_32x32x16_bf16 with a 128x128x64 LDS-double-buffered tile; fp32
+// uses a VALU tile (parity mode).
+#include <cmath>
+
+#include "device_utils.hpp"
+#include "kernels.hpp"
+
+namespace mrt {
+namespace {
+
+// ---- embedding + position embedding ------------------------------------------
+template <typename T>
+__global__ void k_encoder_embed(const T* __restrict__ emb, const T* __restrict__ pe,
+                                const int* __restrict__ tok, int S, int D, T* __restrict__ x) {
+  const int r = blockIdx.x, s = r % S;
+  const T* e = emb + (size_t)tok[r] * D;
+  const T* p = pe + (size_t)s * D;
+  for (int d = threadIdx.x; d < D; d += blockDim.x)
+    x[(size_t)r * D + d] = St<T>::st(St<T>::ld(e[d]) + St<T>::ld(p[d]));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, const T* __restrict__ g,
+                                                      float eps, int D, T* __restrict__ y) {
+  using S = St<T>;
+  __shared__ float red[4];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const T* xr = x + (size_t)r * D;
+  float ss = 0.f;
+  for (int d = tid; d < D; d += 256) {
+    const float v = S::ld(xr[d]);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + eps);
+  for (int d = tid; d < D; d += 256)
+    y[(size_t)r * D + d] = S::st(S::rnd(S::ld(xr[d]) * inv) * S::ld(g[d]));
+}
+
+// ---- GEMM epilogue ----------------------------------------------------------------
+template <typename T>
+struct GemmOut {
+  GemmEpiArgs a;
+  int N;
+  __device__ __forceinline__ void put(int m, int n, float acc) const {
+    using S = St<T>;
+    T* C = static_cast<T*>(a.C);
+    if (a.kind == GemmEpi::Store) {
+      C[(size_t)m * N + n] = S::st(acc);
+    } else if (a.kind == GemmEpi::Resid) {
+      T* p = C + (size_t)m * N + n;
+      *p = S::st(S::ld(*p) + S::rnd(acc));
+    } else {  // CrossKV
+      const int lk = n / a.HD, nn = n - lk * a.HD;
+      const int h = nn >> 6, d = nn & 63;
+      const int b = m / a.S, s = m - b * a.S;
+      C[((((size_t)lk * a.nb + b) * a.H + h) * a.S + s) * 64 + d] = S::st(acc);
+    }
+  }
+  // Gated-GELU pair: packed column n (gate, n % 64 < 32) and n + 32 (up).
+  __device__ __forceinline__ void put_geglu(int m, int n, float g, float u) const {
+    using S = St<T>;
+    T* C = static_cast<T*>(a.C);
+    const int j = (n >> 6) * 32 + (n & 31);
+    const float gl = gelu_t<T>(S::rnd(g));
+    C[(size_t)m * (N / 2) + j] = S::st(gl * S::rnd(u));
+  }
+};
+
+// ---- VALU tiled GEMM (fp32 parity path; also a bf16 fallback) ---------------------
+// 64x64 tile, BK 16, 256 threads, 4x4 outputs per thread at rows ty+16i and
+// columns tx+16j, so columns j and j+2 form a packed gate/up pair.
+template <typename T>
+__global__ __launch_bounds__(256) void k_gemm_valu(const T* __restrict__ A, const T* __restrict__ B,
+                                                   int M, int N, int K, GemmOut<T> out) {
+  using S = St<T>;
+  __shared__ float As[16][64 + 4];
+  __shared__ float Bs[16][64 + 4];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i, r = idx >> 4, c = idx & 15;
+      const int gm = m0 + r, gn = n0 + r, gk = k0 + c;
+      As[c][r] = (gm < M && gk < K) ? S::ld(A[(size_t)gm * K + gk]) : 0.f;
+      Bs[c][r] = (gn < N && gk < K) ? S::ld(B[(size_t)gn * K + gk]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = As[kk][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) b[j] = Bs[kk][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + ty + 16 * i;
+    if (m >= M) continue;
+    if (out.a.kind == GemmEpi::Geglu) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) out.put_geglu(m, n0 + tx + 16 * j, acc[i][j], acc[i][j + 2]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = n0 + tx + 16 * j;
+        if (n < N) out.put(m, n, acc[i][j]);
+      }
+    }
+  }
+}
+
+// ---- bf16 MFMA GEMM ------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 128, kBN = 128, kBK = 64, kLDK = kBK + 8;  // padded LDS row (bf16)
+
+// 4 waves in a 2x2 grid, each owning a 64x64 sub-tile = 2x2 32x32 MFMA tiles.
+// Operand fragments of v_mfma_f32_32x32x16_bf16: lane l holds row (l % 32)
+// and k = 8*(l / 32) .. +7 of both A (32x16) and B^T (32x16); the 16
+// accumulators of lane l hold column l % 32, rows 8*(r/4) + 4*(l/32) + r%4.
+__global__ __launch_bounds__(256) void k_gemm_mfma(const bf16* __restrict__ A, const bf16* __restrict__ B,
+                                                   int M, int N, int K, GemmOut<bf16> out) {
+  __shared__ __attribute__((aligned(16))) bf16 As[2][kBM * kLDK];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2][kBN * kLDK];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid >> 1, wn = wid & 1;
+  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+
+  uint4 ra[4], rb[4];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int id = tid + 256 * i, r = id >> 3, c = (id & 7) * 8;
+      const int gm = m0 + r;
+      ra[i] = gm < M ? *reinterpret_cast<const uint4*>(A + (size_t)gm * K + k0 + c) : make_uint4(0, 0, 0, 0);
+      rb[i] = *reinterpret_cast<const uint4*>(B + (size_t)(n0 + r) * K + k0 + c);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int id = tid + 256 * i, r = id >> 3, c = (id & 7) * 8;
+      *reinterpret_cast<uint4*>(&As[buf][r * kLDK + c]) = ra[i];
+      *reinterpret_cast<uint4*>(&Bs[buf][r * kLDK + c]) = rb[i];
+    }
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int nk = K / kBK;
+  const int lr = lane & 31, lk = (lane >> 5) * 8;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * kBK);
+#pragma unroll
+    for (int ks = 0; ks < kBK; ks += 16) {
+      bf16x8_t a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a[i] = *reinterpret_cast<const bf16x8_t*>(&As[cur][(wm * 64 + i * 32 + lr) * kLDK + ks + lk]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        b[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[cur][(wn * 64 + j * 32 + lr) * kLDK + ks + lk]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  const int col_l = lane & 31, row_l = 4 * (lane >> 5);
+  if (out.a.kind == GemmEpi::Geglu) {
+    const int n = n0 + wn * 64 + col_l;  // gate column; up is n + 32
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
+        if (m < M) out.put_geglu(m, n, acc[i][0][r], acc[i][1][r]);
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
+          if (m < M) out.put(m, n0 + wn * 64 + j * 32 + col_l, acc[i][j][r]);
+        }
+  }
+}
+
+// ---- encoder self-attention (bidirectional, no mask, no bias, scale 1.0) -------------
+// One lane per query row, 64 rows per block; K/V tiles of 64 keys staged in
+// LDS; online softmax per 64-key tile.
+template <typename T>
+__global__ __launch_bounds__(64) void k_enc_attn(const T* __restrict__ qkv, int S, int H,
+                                                 T* __restrict__ out) {
+  using St_ = St<T>;
+  const int bh = blockIdx.y, b = bh / H, h = bh - b * H, lane = threadIdx.x;
+  const int HD = H * 64, ld = 3 * HD;
+  const int qi = blockIdx.x * 64 + lane;
+  __shared__ float Ks[64][64 + 1];
+  __shared__ float Vs[64][64];
+  float q[64], o[64];
+  const T* qrow = qkv + ((size_t)b * S + (qi < S ? qi : 0)) * ld + h * 64;
+#pragma unroll
+  for (int d = 0; d < 64; ++d) {
+    q[d] = St_::ld(qrow[d]);
+    o[d] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  for (int j0 = 0; j0 < S; j0 += 64) {
+    const int nk = min(64, S - j0);
+    for (int r = 0; r < nk; ++r) {
+      const T* row = qkv + ((size_t)b * S + j0 + r) * ld + h * 64;
+      Ks[r][lane] = St_::ld(row[HD + lane]);
+      Vs[r][lane] = St_::ld(row[2 * HD + lane]);
+    }
+    __syncthreads();
+    float sc[64];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 64; ++r) {
+      float acc = 0.f;
+#pragma unroll
+      for (int d = 0; d < 64; ++d) acc = fmaf(q[d], Ks[r][d], acc);
+      sc[r] = r < nk ? acc : -INFINITY;
+      mt = fmaxf(mt, sc[r]);
+    }
+    const float mn = fmaxf(m, mt);
+    const float corr = expf(m - mn);
+    l *= corr;
+#pragma unroll
+    for (int d = 0; d < 64; ++d) o[d] *= corr;
+#pragma unroll
+    for (int r = 0; r < 64; ++r) {
+      const float p = r < nk ? expf(sc[r] - mn) : 0.f;
+      l += p;
+#pragma unroll
+      for (int d = 0; d < 64; ++d) o[d] = fmaf(p, Vs[r][d], o[d]);
+    }
+    m = mn;
+    __syncthreads();
+  }
+  if (qi < S) {
+    T* orow = out + ((size_t)b * S + qi) * HD + h * 64;
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int d = 0; d < 64; ++d) orow[d] = St_::st(o[d] * inv);
+  }
+}
+
+}  // namespace
+
+void encoder_embed(DType dt, const void* emb, const void* pe, const int* tok, int M, int S, int D,
+                   void* x, hipStream_t s) {
+  if (dt == DType::F32)
+    hipLaunchKernelGGL(k_encoder_embed<float>, dim3(M), dim3(256), 0, s, (const float*)emb,
+                       (const float*)pe, tok, S, D, (float*)x);
+  else
+    hipLaunchKernelGGL(k_encoder_embed<bf16>, dim3(M), dim3(256), 0, s, (const bf16*)emb,
+                       (const bf16*)pe, tok, S, D, (bf16*)x);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void rmsnorm_rows(DType dt, const void* x, const void* g, float eps, int M, int D, void* y,
+                  hipStream_t s) {
+  if (dt == DType::F32)
+    hipLaunchKernelGGL(k_rmsnorm_rows<float>, dim3(M), dim3(256), 0, s, (const float*)x,
+                       (const float*)g, eps, D, (float*)y);
+  else
+    hipLaunchKernelGGL(k_rmsnorm_rows<bf16>, dim3(M), dim3(256), 0, s, (const bf16*)x,
+                       (const bf16*)g, eps, D, (bf16*)y);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const GemmEpiArgs& e,
+          hipStream_t s, bool allow_mfma) {
+  MRT_REQUIRE(M >= 1 && N >= 1 && K >= 1, "gemm: empty problem");
+  if (e.kind == GemmEpi::Geglu) MRT_REQUIRE(N % 64 == 0, "gemm: gated-GELU needs N % 64 == 0");
+  if (e.kind == GemmEpi::CrossKV)
+    MRT_REQUIRE(e.HD == e.H * 64 && N % e.HD == 0 && M == e.nb * e.S, "gemm: bad cross-KV shape");
+  if (dt == DType::BF16 && allow_mfma && N % kBN == 0 && K % kBK == 0) {
+    GemmOut<bf16> out{e, N};
+    hipLaunchKernelGGL(k_gemm_mfma, dim3(N / kBN, (M + kBM - 1) / kBM), dim3(256), 0, s,
+                       (const bf16*)A, (const bf16*)B, M, N, K, out);
+  } else if (dt == DType::BF16) {
+    GemmOut<bf16> out{e, N};
+    hipLaunchKernelGGL(k_gemm_valu<bf16>, dim3((N + 63) / 64, (M + 63) / 64), dim3(256), 0, s,
+                       (const bf16*)A, (const bf16*)B, M, N, K, out);
+  } else {
+    GemmOut<float> out{e, N};
+    hipLaunchKernelGGL(k_gemm_valu<float>, dim3((N + 63) / 64, (M + 63) / 64), dim3(256), 0, s,
+                       (const float*)A, (const float*)B, M, N, K, out);
+  }
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s) {
+  dim3 grid((S + 63) / 64, nb * H);
+  if (dt == DType::F32)
+    hipLaunchKernelGGL(k_enc_attn<float>, grid, dim3(64), 0, s, (const float*)qkv, S, H, (float*)out);
+  else
+    hipLaunchKernelGGL(k_enc_attn<bf16>, grid, dim3(64), 0, s, (const bf16*)qkv, S, H, (bf16*)out);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace mrt

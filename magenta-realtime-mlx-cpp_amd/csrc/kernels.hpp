@@ -1,0 +1,115 @@
+// Host-side launchers for the Depthformer HIP kernels (gfx950).
+//
+// Conventions shared by every launcher:
+//   * ``T`` is the model storage type selected by ``DType`` (fp32 or bf16);
+//     all accumulation is fp32.
+//   * Linear weights are (out, in) row-major, exactly as the bundle stores
+//     them (modules.h:74-76), so a GEMV row is one contiguous dot product.
+//   * ``nb`` is the number of activation rows (2 = one CFG stream).
+//   * Values the reference materialises in the model dtype are rounded to it
+//     at the same points (identity for fp32).
+#pragma once
+
+#include "common.hpp"
+
+namespace mrt {
+
+// RMSNorm prologue applied to X before a GEMV/GEMM when ``g`` is non-null:
+// x_hat = round(round(x * rsqrt(mean(x^2) + eps)) * g)   (modules.cpp:72-84).
+struct NormArg {
+  const void* g = nullptr;
+  float eps = 1e-6f;
+};
+
+// ---- decode GEMVs: Y[b, n] = sum_k W[n, k] * X[b, k] ------------------------
+// Plain store to Y (model dtype).
+void gemv_store(DType dt, int nb, const void* W, int N, int K, const void* X, int ldx,
+                NormArg norm, void* Y, int ldy, hipStream_t s);
+// Store rounded-to-model-dtype values as fp32 (logits).
+void gemv_f32(DType dt, int nb, const void* W, int N, int K, const void* X, int ldx,
+              NormArg norm, float* Y, int ldy, hipStream_t s);
+// Residual: R[b, n] = round(R[b, n] + round(Y[b, n])).
+void gemv_resid(DType dt, int nb, const void* W, int N, int K, const void* X, int ldx,
+                NormArg norm, void* R, int ldr, hipStream_t s);
+// Fused q/k/v projection (W = [Wq; Wk; Wv], 3*HD rows). q goes to Q (nb, HD);
+// k and v are written into ring slot ``pos`` of the caches laid out
+// (nb, H, Lmax, 64).
+void gemv_qkv(DType dt, int nb, const void* W, int HD, int K, const void* X, int ldx,
+              NormArg norm, void* Q, void* Kc, void* Vc, int H, int Lmax, int pos,
+              hipStream_t s);
+// Gated-GELU: W01 packs wi_0/wi_1 in 32-row groups [gate 32 | up 32]; writes
+// H[b, j] = round(gelu(round(gate)) * round(up)) for j < F.
+void gemv_geglu(DType dt, int nb, const void* W01, int F, int K, const void* X, int ldx,
+                NormArg norm, void* Hout, int ldh, hipStream_t s);
+
+// ---- decode attention -------------------------------------------------------
+// Self-attention of the query at ring position qpos over slots 0..len-1,
+// scale 1.0, additive bias table[bucket[qpos - j], h] (modules.cpp:243-295).
+void self_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H,
+               int Lmax, int len, int qpos, const void* bias_tab, const int* buckets,
+               void* out, hipStream_t s);
+// Cross-attention over S encoder keys (no bias/mask), split over key blocks.
+// ``part`` needs nb*H*nsplit*66 floats.
+void cross_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H,
+                int S, void* out, float* part, int nsplit, hipStream_t s);
+int cross_attn_splits(int S);
+
+// out[r, :] = emb[ids[r], :] for r < rows (model dtype copy).
+void embed_rows(DType dt, const void* emb, int D, const int* ids, int rows, void* out,
+                hipStream_t s);
+// out[r, :] = emb[id, :] for every r < rows.
+void embed_fill(DType dt, const void* emb, int D, int id, int rows, void* out, hipStream_t s);
+// Device-to-device copy as a kernel (kept out of memcpy graph nodes).
+void copy_dev(void* dst, const void* src, size_t bytes, hipStream_t s);
+
+// ---- sampling -----------------------------------------------------------------
+struct SampleParams {
+  float guidance_weight;
+  float temperature;
+  int top_k;
+  int codebook;       // C: entries per level
+  int codec_offset;   // first id of level 0
+  int rvq_depth;      // L
+  const uint64_t* seed;  // device pointer to the draw seed
+};
+
+// One CFG stream: rows (0, 1) of ``logits`` (nb=2, C) level slice.
+// CFG-combine -> (temperature, top-k, Gumbel-max) or argmax -> token; the
+// noise of candidate i is keyed by (seed, frame, level, i).
+// Writes tokens[slot] (fed-back id: teacher[slot] if ``teacher`` is non-null),
+// drawn[slot] (the model's own draw) when non-null, the fed-back embedding
+// into ``next_in`` (nb rows), accumulates ``fsum`` and at the last level
+// writes ``frame_mean`` = round(fsum / L).
+void sample_level(DType dt, const float* logits, const SampleParams& p, int frame, int level, int slot,
+                  const int* teacher, int* tokens, int* drawn, const void* emb, int D,
+                  void* next_in, void* fsum, void* frame_mean, hipStream_t s);
+
+// ---- encoder ------------------------------------------------------------------
+// x[r, :] = round(emb[tok[r]] + pe_T[r % S])    (model.cpp:231-236)
+void encoder_embed(DType dt, const void* emb, const void* pe, const int* tok, int M, int S,
+                   int D, void* x, hipStream_t s);
+// y[r, :] = rmsnorm(x[r, :]) * g   (model dtype in and out)
+void rmsnorm_rows(DType dt, const void* x, const void* g, float eps, int M, int D, void* y,
+                  hipStream_t s);
+
+// GEMM C[m, n] = sum_k A[m, k] * B[n, k]; A (M, K) and B (N, K) row-major.
+enum class GemmEpi : int {
+  Store = 0,    // C (M, N) model dtype, ld = N
+  Resid = 1,    // R[m, n] = round(R + round(acc)), ld = N
+  Geglu = 2,    // B packed like gemv_geglu; C (M, N/2)
+  CrossKV = 3,  // n = (layer*2 + kv)*HD + h*64 + d; m = b*S + s ->
+                //   C[(((layer*2+kv)*nb + b)*H + h)*S + s][d]
+};
+struct GemmEpiArgs {
+  GemmEpi kind = GemmEpi::Store;
+  void* C = nullptr;
+  int nb = 2, H = 16, S = 1, HD = 1024;
+};
+void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const GemmEpiArgs& e,
+          hipStream_t s, bool allow_mfma = true);
+
+// Bidirectional encoder self-attention, no mask, no bias, scale 1.0.
+// qkv (nb*S, 3*HD) row-major [q | k | v]; out (nb*S, HD).
+void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s);
+
+}  // namespace mrt

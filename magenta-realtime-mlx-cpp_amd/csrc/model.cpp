@@ -1,0 +1,630 @@
+#include "model.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <thread>
+
+#include "kernels.hpp"
+
+namespace mrt {
+
+// ---------------------------------------------------------------------------
+// Relative position buckets (modules.cpp:139-174, bidirectional = false)
+// ---------------------------------------------------------------------------
+int relative_position_bucket(int n, int num_buckets, int max_distance) {
+  if (n < 0) n = 0;
+  const int eff = num_buckets;
+  const int max_exact = eff / 2;
+  if (n < max_exact) return n;
+  const float log_ratio = std::log(static_cast<float>(max_distance) / static_cast<float>(max_exact));
+  const float v = static_cast<float>(max_exact) +
+                  (std::log(static_cast<float>(n) / static_cast<float>(max_exact)) / log_ratio) *
+                      static_cast<float>(eff - max_exact);
+  const int b = static_cast<int>(v);  // truncation, as astype(int32)
+  return std::min(b, eff - 1);
+}
+
+namespace {
+
+// Sinusoidal table in fp32 (model.cpp:54-80).
+std::vector<float> sinusoid(int max_length, int features) {
+  const int half = features / 2;
+  MRT_REQUIRE(half > 1, "features // 2 must be >= 2 for sinusoidal PE");
+  std::vector<float> data(static_cast<size_t>(max_length) * features, 0.0f);
+  const float min_scale = 1.0f, max_scale = 10000.0f;
+  const float scale_factor = -std::log(max_scale / min_scale) / static_cast<float>(half - 1);
+  std::vector<float> div(half);
+  for (int i = 0; i < half; ++i) div[i] = min_scale * std::exp(static_cast<float>(i) * scale_factor);
+  for (int pos = 0; pos < max_length; ++pos) {
+    float* row = &data[static_cast<size_t>(pos) * features];
+    for (int i = 0; i < half; ++i) {
+      const float angle = static_cast<float>(pos) * div[i];
+      row[i] = std::sin(angle);
+      row[half + i] = std::cos(angle);
+    }
+  }
+  return data;
+}
+
+void expect_shape(const HostTensor& t, std::vector<int64_t> want, const std::string& key) {
+  if (t.shape != want) {
+    std::string got, exp;
+    for (auto d : t.shape) got += std::to_string(d) + ",";
+    for (auto d : want) exp += std::to_string(d) + ",";
+    throw Error(1, "weight shape mismatch for " + key + ": got (" + got + ") expected (" + exp + ")");
+  }
+}
+
+// Parallel fp32 -> storage conversion.
+void convert(DType dt, const float* src, size_t n, void* dst) {
+  if (dt == DType::F32) {
+    std::memcpy(dst, src, n * 4);
+    return;
+  }
+  bf16* d = static_cast<bf16*>(dst);
+  const unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+  if (n < (1u << 20) || nt == 1) {
+    for (size_t i = 0; i < n; ++i) d[i] = f2bf(src[i]);
+    return;
+  }
+  std::vector<std::thread> th;
+  const size_t per = (n + nt - 1) / nt;
+  for (unsigned t = 0; t < nt; ++t) {
+    const size_t a = t * per, b = std::min(n, a + per);
+    if (a >= b) break;
+    th.emplace_back([=] {
+      for (size_t i = a; i < b; ++i) d[i] = f2bf(src[i]);
+    });
+  }
+  for (auto& x : th) x.join();
+}
+
+}  // namespace
+
+// Bundle keys and shapes (model.cpp:177-198, modules.cpp:342-381; Linear
+// weights stored (out, in), modules.h:74-76).
+std::vector<std::pair<std::string, std::vector<int64_t>>> bundle_layout(const Config& c) {
+  const int64_t D = c.d_model, HD = c.hd(), F = c.d_ff, V = c.vocab_size, H = c.num_heads;
+  std::vector<std::pair<std::string, std::vector<int64_t>>> out;
+  out.push_back({"token_embedding.weight", {V, D}});
+  out.push_back({"lm_head.weight", {V, D}});
+  out.push_back({"encoder_norm.weight", {D}});
+  out.push_back({"decoder_norm.weight", {D}});
+  out.push_back({"temporal_rel_pos.relative_attention_bias.weight", {c.temporal_num_buckets, H}});
+  out.push_back({"depth_rel_pos.relative_attention_bias.weight", {c.depth_num_buckets, H}});
+  auto attn = [&](const std::string& p) {
+    out.push_back({p + ".q_proj.weight", {HD, D}});
+    out.push_back({p + ".k_proj.weight", {HD, D}});
+    out.push_back({p + ".v_proj.weight", {HD, D}});
+    out.push_back({p + ".o_proj.weight", {D, HD}});
+  };
+  auto ffn = [&](const std::string& p) {
+    out.push_back({p + ".wi_0.weight", {F, D}});
+    out.push_back({p + ".wi_1.weight", {F, D}});
+    out.push_back({p + ".wo.weight", {D, F}});
+  };
+  for (int i = 0; i < c.num_encoder_layers; ++i) {
+    const std::string p = "encoder_layers." + std::to_string(i);
+    out.push_back({p + ".pre_attn_norm.weight", {D}});
+    attn(p + ".self_attn");
+    out.push_back({p + ".pre_ffn_norm.weight", {D}});
+    ffn(p + ".ffn");
+  }
+  for (int i = 0; i < c.num_temporal_layers; ++i) {
+    const std::string p = "temporal_layers." + std::to_string(i);
+    out.push_back({p + ".pre_self_attn_norm.weight", {D}});
+    attn(p + ".self_attn");
+    out.push_back({p + ".pre_cross_attn_norm.weight", {D}});
+    attn(p + ".cross_attn");
+    out.push_back({p + ".pre_ffn_norm.weight", {D}});
+    ffn(p + ".ffn");
+  }
+  for (int i = 0; i < c.num_depth_layers; ++i) {
+    const std::string p = "depth_layers." + std::to_string(i);
+    out.push_back({p + ".pre_self_attn_norm.weight", {D}});
+    attn(p + ".self_attn");
+    out.push_back({p + ".pre_ffn_norm.weight", {D}});
+    ffn(p + ".ffn");
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Model
+// ---------------------------------------------------------------------------
+
+const void* Model::upload(const std::vector<float>& host) {
+  const size_t bytes = host.size() * esz;
+  void* d = nullptr;
+  MRT_HIP_CHECK(hipMalloc(&d, std::max<size_t>(bytes, 256)));
+  allocs_.push_back(d);
+  std::vector<uint8_t> tmp(bytes);
+  convert(dt, host.data(), host.size(), tmp.data());
+  MRT_HIP_CHECK(hipMemcpy(d, tmp.data(), bytes, hipMemcpyHostToDevice));
+  weight_bytes += bytes;
+  return d;
+}
+
+const void* Model::upload_i32(const std::vector<int>& host) {
+  void* d = nullptr;
+  MRT_HIP_CHECK(hipMalloc(&d, host.size() * 4));
+  allocs_.push_back(d);
+  MRT_HIP_CHECK(hipMemcpy(d, host.data(), host.size() * 4, hipMemcpyHostToDevice));
+  return d;
+}
+
+Model::Model(const TensorSource& src, const Config& c, DType dtype, int dev)
+    : cfg(c), dt(dtype), device(dev), esz(dtype_size(dtype)) {
+  MRT_REQUIRE(cfg.d_kv == 64, "this backend requires d_kv == 64");
+  MRT_REQUIRE(cfg.d_model % 64 == 0 && cfg.d_ff % 64 == 0, "d_model and d_ff must be multiples of 64");
+  MRT_REQUIRE(cfg.num_heads >= 1 && cfg.vocab_size >= 2, "bad config");
+  MRT_REQUIRE(cfg.max_encoder_length >= 1 && cfg.rvq_depth >= 1, "bad config");
+  const int64_t D = cfg.d_model, HD = cfg.hd(), F = cfg.d_ff, V = cfg.vocab_size, H = cfg.num_heads;
+  // Every key and shape is checked before the device is touched.
+  for (const auto& ks : bundle_layout(cfg)) expect_shape(src.tensor(ks.first), ks.second, ks.first);
+  MRT_HIP_CHECK(hipSetDevice(device));
+
+  auto get = [&](const std::string& key, std::vector<int64_t> shape) -> const HostTensor& {
+    const HostTensor& t = src.tensor(key);
+    expect_shape(t, shape, key);
+    return t;
+  };
+  auto vec = [&](const std::string& key, std::vector<int64_t> shape) {
+    const HostTensor& t = get(key, shape);
+    return std::vector<float>(t.data, t.data + t.numel());
+  };
+  // Row-concatenate several (rows_i, D) matrices.
+  auto cat = [&](const std::vector<std::pair<std::string, int64_t>>& parts, int64_t cols) {
+    size_t total = 0;
+    for (auto& p : parts) total += static_cast<size_t>(p.second * cols);
+    std::vector<float> out;
+    out.reserve(total);
+    for (auto& p : parts) {
+      const HostTensor& t = get(p.first, {p.second, cols});
+      out.insert(out.end(), t.data, t.data + t.numel());
+    }
+    return out;
+  };
+  // wi_0 / wi_1 packed in 32-row groups [gate 32 | up 32].
+  auto pack_geglu = [&](const std::string& prefix) {
+    const HostTensor& w0 = get(prefix + ".wi_0.weight", {F, D});
+    const HostTensor& w1 = get(prefix + ".wi_1.weight", {F, D});
+    std::vector<float> out(static_cast<size_t>(2 * F * D));
+    for (int64_t g = 0; g < F / 32; ++g) {
+      std::memcpy(&out[(size_t)(g * 64) * D], w0.data + (size_t)(g * 32) * D, sizeof(float) * 32 * D);
+      std::memcpy(&out[(size_t)(g * 64 + 32) * D], w1.data + (size_t)(g * 32) * D, sizeof(float) * 32 * D);
+    }
+    return out;
+  };
+
+  emb = upload(vec("token_embedding.weight", {V, D}));
+  lm_head = upload(vec("lm_head.weight", {V, D}));
+  {
+    // The fp32 table is cast to the model dtype before the add (model.cpp:232-236).
+    pe = upload(sinusoid(cfg.max_encoder_length, cfg.d_model));
+  }
+  enc_norm = upload(vec("encoder_norm.weight", {D}));
+  dec_norm = upload(vec("decoder_norm.weight", {D}));
+  tbias = upload(vec("temporal_rel_pos.relative_attention_bias.weight", {cfg.temporal_num_buckets, H}));
+  dbias = upload(vec("depth_rel_pos.relative_attention_bias.weight", {cfg.depth_num_buckets, H}));
+  {
+    std::vector<int> tb(kBucketTable), db(kBucketTable);
+    for (int n = 0; n < kBucketTable; ++n) {
+      tb[n] = relative_position_bucket(n, cfg.temporal_num_buckets, cfg.temporal_max_distance);
+      db[n] = relative_position_bucket(n, cfg.depth_num_buckets, cfg.depth_max_distance);
+    }
+    tbuckets = static_cast<const int*>(upload_i32(tb));
+    dbuckets = static_cast<const int*>(upload_i32(db));
+  }
+
+  for (int i = 0; i < cfg.num_encoder_layers; ++i) {
+    const std::string p = "encoder_layers." + std::to_string(i);
+    EncoderLayerW w{};
+    w.norm_attn = upload(vec(p + ".pre_attn_norm.weight", {D}));
+    w.wqkv = upload(cat({{p + ".self_attn.q_proj.weight", HD},
+                         {p + ".self_attn.k_proj.weight", HD},
+                         {p + ".self_attn.v_proj.weight", HD}}, D));
+    w.wo = upload(vec(p + ".self_attn.o_proj.weight", {D, HD}));
+    w.norm_ff = upload(vec(p + ".pre_ffn_norm.weight", {D}));
+    w.w01 = upload(pack_geglu(p + ".ffn"));
+    w.wo2 = upload(vec(p + ".ffn.wo.weight", {D, F}));
+    enc.push_back(w);
+  }
+  std::vector<std::pair<std::string, int64_t>> cross_parts;
+  for (int i = 0; i < cfg.num_temporal_layers; ++i) {
+    const std::string p = "temporal_layers." + std::to_string(i);
+    DecoderLayerW w{};
+    w.norm_sa = upload(vec(p + ".pre_self_attn_norm.weight", {D}));
+    w.wqkv = upload(cat({{p + ".self_attn.q_proj.weight", HD},
+                         {p + ".self_attn.k_proj.weight", HD},
+                         {p + ".self_attn.v_proj.weight", HD}}, D));
+    w.wo = upload(vec(p + ".self_attn.o_proj.weight", {D, HD}));
+    w.norm_ca = upload(vec(p + ".pre_cross_attn_norm.weight", {D}));
+    w.wq_c = upload(vec(p + ".cross_attn.q_proj.weight", {HD, D}));
+    w.wo_c = upload(vec(p + ".cross_attn.o_proj.weight", {D, HD}));
+    w.norm_ff = upload(vec(p + ".pre_ffn_norm.weight", {D}));
+    w.w01 = upload(pack_geglu(p + ".ffn"));
+    w.wo2 = upload(vec(p + ".ffn.wo.weight", {D, F}));
+    tmp.push_back(w);
+    cross_parts.push_back({p + ".cross_attn.k_proj.weight", HD});
+    cross_parts.push_back({p + ".cross_attn.v_proj.weight", HD});
+  }
+  if (!cross_parts.empty()) wkv_cross = upload(cat(cross_parts, D));
+  for (int i = 0; i < cfg.num_depth_layers; ++i) {
+    const std::string p = "depth_layers." + std::to_string(i);
+    DecoderLayerW w{};
+    w.norm_sa = upload(vec(p + ".pre_self_attn_norm.weight", {D}));
+    w.wqkv = upload(cat({{p + ".self_attn.q_proj.weight", HD},
+                         {p + ".self_attn.k_proj.weight", HD},
+                         {p + ".self_attn.v_proj.weight", HD}}, D));
+    w.wo = upload(vec(p + ".self_attn.o_proj.weight", {D, HD}));
+    w.norm_ff = upload(vec(p + ".pre_ffn_norm.weight", {D}));
+    w.w01 = upload(pack_geglu(p + ".ffn"));
+    w.wo2 = upload(vec(p + ".ffn.wo.weight", {D, F}));
+    dep.push_back(w);
+  }
+}
+
+Model::~Model() {
+  (void)hipSetDevice(device);
+  for (void* p : allocs_) (void)hipFree(p);
+}
+
+// ---------------------------------------------------------------------------
+// State
+// ---------------------------------------------------------------------------
+
+void* State::dalloc(size_t bytes) {
+  void* d = nullptr;
+  MRT_HIP_CHECK(hipMalloc(&d, std::max<size_t>(bytes, 256)));
+  allocs_.push_back(d);
+  return d;
+}
+
+State::State(Model& model, int rows_, int max_frames, int enc_len)
+    : m(model), rows(rows_), F(max_frames), S(enc_len) {
+  const Config& c = m.cfg;
+  MRT_REQUIRE(rows == 2, "rows must be 2 (one CFG stream)");
+  MRT_REQUIRE(F >= 1 && F < Model::kBucketTable, "max_frames out of range");
+  MRT_REQUIRE(S >= 1 && S <= c.max_encoder_length, "enc_len must be in [1, max_encoder_length]");
+  MRT_HIP_CHECK(hipSetDevice(m.device));
+  MRT_HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
+  const size_t D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads, L = c.rvq_depth;
+  const size_t M = static_cast<size_t>(rows) * S, e = esz();
+  d_enc_tok = static_cast<int*>(dalloc(M * 4));
+  ex = dalloc(M * D * e);
+  exn = dalloc(M * D * e);
+  eqkv = dalloc(M * 3 * HD * e);
+  eattn = dalloc(M * HD * e);
+  effh = dalloc(M * FF * e);
+  enc_out = dalloc(M * D * e);
+  cross = dalloc(static_cast<size_t>(c.num_temporal_layers) * 2 * rows * H * S * 64 * e);
+  tkv = dalloc(static_cast<size_t>(c.num_temporal_layers) * 2 * rows * H * F * 64 * e);
+  dkv = dalloc(static_cast<size_t>(c.num_depth_layers) * 2 * rows * H * L * 64 * e);
+  x = dalloc(rows * D * e);
+  q = dalloc(rows * HD * e);
+  attn = dalloc(rows * HD * e);
+  ffh = dalloc(rows * FF * e);
+  t_in = dalloc(rows * D * e);
+  t_out = dalloc(rows * D * e);
+  d_in = dalloc(rows * D * e);
+  fsum = dalloc(rows * D * e);
+  max_slice = c.vocab_size;
+  slice = static_cast<float*>(dalloc(static_cast<size_t>(rows) * c.vocab_size * 4));
+  nsplit = cross_attn_splits(S);
+  part = static_cast<float*>(dalloc(static_cast<size_t>(rows) * H * nsplit * 66 * 4));
+  d_tokens = static_cast<int*>(dalloc(static_cast<size_t>(F) * L * 4));
+  d_teacher = static_cast<int*>(dalloc(static_cast<size_t>(F) * L * 4));
+  d_seed = static_cast<uint64_t*>(dalloc(8));
+  h_pinned_n = std::max<size_t>(M, static_cast<size_t>(F) * L) + 2;
+  MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_pinned), h_pinned_n * 4, hipHostMallocDefault));
+}
+
+State::~State() {
+  (void)hipSetDevice(m.device);
+  if (stream) (void)hipStreamSynchronize(stream);
+  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+  if (graph_) (void)hipGraphDestroy(graph_);
+  for (void* p : allocs_) (void)hipFree(p);
+  if (h_pinned) (void)hipHostFree(h_pinned);
+  if (stream) (void)hipStreamDestroy(stream);
+}
+
+char* State::tk(int i) const {
+  const size_t n = static_cast<size_t>(rows) * m.cfg.num_heads * F * 64 * esz();
+  return static_cast<char*>(tkv) + (2 * i) * n;
+}
+char* State::tv(int i) const {
+  const size_t n = static_cast<size_t>(rows) * m.cfg.num_heads * F * 64 * esz();
+  return static_cast<char*>(tkv) + (2 * i + 1) * n;
+}
+char* State::dk(int i) const {
+  const size_t n = static_cast<size_t>(rows) * m.cfg.num_heads * m.cfg.rvq_depth * 64 * esz();
+  return static_cast<char*>(dkv) + (2 * i) * n;
+}
+char* State::dv(int i) const {
+  const size_t n = static_cast<size_t>(rows) * m.cfg.num_heads * m.cfg.rvq_depth * 64 * esz();
+  return static_cast<char*>(dkv) + (2 * i + 1) * n;
+}
+char* State::ck(int i) const {
+  const size_t n = static_cast<size_t>(rows) * m.cfg.num_heads * S * 64 * esz();
+  return static_cast<char*>(cross) + (2 * i) * n;
+}
+char* State::cv(int i) const {
+  const size_t n = static_cast<size_t>(rows) * m.cfg.num_heads * S * 64 * esz();
+  return static_cast<char*>(cross) + (2 * i + 1) * n;
+}
+
+void State::copy(void* dst, const void* src, size_t bytes) { copy_dev(dst, src, bytes, stream); }
+
+void State::sync() { MRT_HIP_CHECK(hipStreamSynchronize(stream)); }
+
+// Depthformer::encode (model.cpp:226-241) followed by the cross K/V projection
+// of every temporal layer (modules.cpp:448-455).
+void State::encode(const int32_t* tokens_host) {
+  const Config& c = m.cfg;
+  const int M = rows * S;
+  for (int i = 0; i < M; ++i)
+    MRT_REQUIRE(tokens_host[i] >= 0 && tokens_host[i] < c.vocab_size, "encode: token id out of range");
+  MRT_HIP_CHECK(hipSetDevice(m.device));
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));  // staging buffer reuse
+  std::memcpy(h_pinned, tokens_host, static_cast<size_t>(M) * 4);
+  MRT_HIP_CHECK(hipMemcpyAsync(d_enc_tok, h_pinned, static_cast<size_t>(M) * 4, hipMemcpyHostToDevice, stream));
+  const DType dt = m.dt;
+  const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads;
+  encoder_embed(dt, m.emb, m.pe, d_enc_tok, M, S, D, ex, stream);
+  for (const auto& L : m.enc) {
+    rmsnorm_rows(dt, ex, L.norm_attn, 1e-6f, M, D, exn, stream);
+    gemm(dt, exn, L.wqkv, M, 3 * HD, D, {GemmEpi::Store, eqkv}, stream);
+    encoder_attn(dt, eqkv, rows, S, H, eattn, stream);
+    gemm(dt, eattn, L.wo, M, D, HD, {GemmEpi::Resid, ex}, stream);
+    rmsnorm_rows(dt, ex, L.norm_ff, 1e-6f, M, D, exn, stream);
+    gemm(dt, exn, L.w01, M, 2 * FF, D, {GemmEpi::Geglu, effh}, stream);
+    gemm(dt, effh, L.wo2, M, D, FF, {GemmEpi::Resid, ex}, stream);
+  }
+  rmsnorm_rows(dt, ex, m.enc_norm, 1e-6f, M, D, enc_out, stream);
+  project_cross(enc_out);
+}
+
+void State::project_cross(const void* src) {
+  const Config& c = m.cfg;
+  if (c.num_temporal_layers == 0) {
+    cross_ready_ = true;
+    return;
+  }
+  GemmEpiArgs e;
+  e.kind = GemmEpi::CrossKV;
+  e.C = cross;
+  e.nb = rows;
+  e.H = c.num_heads;
+  e.S = S;
+  e.HD = c.hd();
+  gemm(m.dt, src, m.wkv_cross, rows * S, c.num_temporal_layers * 2 * c.hd(), c.d_model, e, stream);
+  cross_ready_ = true;
+}
+
+// One temporal step on the device (model.cpp:493-513 eager semantics).
+void State::run_temporal(const void* in, int f, void* out) {
+  const Config& c = m.cfg;
+  const DType dt = m.dt;
+  const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads;
+  copy(out, in, static_cast<size_t>(rows) * D * esz());
+  for (int i = 0; i < c.num_temporal_layers; ++i) {
+    const DecoderLayerW& L = m.tmp[i];
+    gemv_qkv(dt, rows, L.wqkv, HD, D, out, D, {L.norm_sa}, q, tk(i), tv(i), H, F, f, stream);
+    self_attn(dt, rows, q, tk(i), tv(i), H, F, f + 1, f, m.tbias, m.tbuckets, attn, stream);
+    gemv_resid(dt, rows, L.wo, D, HD, attn, HD, {}, out, D, stream);
+    gemv_store(dt, rows, L.wq_c, HD, D, out, D, {L.norm_ca}, q, HD, stream);
+    cross_attn(dt, rows, q, ck(i), cv(i), H, S, attn, part, nsplit, stream);
+    gemv_resid(dt, rows, L.wo_c, D, HD, attn, HD, {}, out, D, stream);
+    gemv_geglu(dt, rows, L.w01, FF, D, out, D, {L.norm_ff}, ffh, FF, stream);
+    gemv_resid(dt, rows, L.wo2, D, FF, ffh, FF, {}, out, D, stream);
+  }
+}
+
+// One depth step on the device (model.cpp:638-658): 4 layers, decoder_norm,
+// lm_head (full vocabulary or one level's rows).
+void State::run_depth(const void* in, int l, int level, int C, int off, float* logits) {
+  const Config& c = m.cfg;
+  const DType dt = m.dt;
+  const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads, L = c.rvq_depth;
+  copy(x, in, static_cast<size_t>(rows) * D * esz());
+  for (int i = 0; i < c.num_depth_layers; ++i) {
+    const DecoderLayerW& W = m.dep[i];
+    gemv_qkv(dt, rows, W.wqkv, HD, D, x, D, {W.norm_sa}, q, dk(i), dv(i), H, L, l, stream);
+    self_attn(dt, rows, q, dk(i), dv(i), H, L, l + 1, l, m.dbias, m.dbuckets, attn, stream);
+    gemv_resid(dt, rows, W.wo, D, HD, attn, HD, {}, x, D, stream);
+    gemv_geglu(dt, rows, W.w01, FF, D, x, D, {W.norm_ff}, ffh, FF, stream);
+    gemv_resid(dt, rows, W.wo2, D, FF, ffh, FF, {}, x, D, stream);
+  }
+  if (level >= 0) {
+    const char* rows0 = static_cast<const char*>(m.lm_head) + static_cast<size_t>(off + C * level) * D * esz();
+    gemv_f32(dt, rows, rows0, C, D, x, D, {m.dec_norm}, logits, C, stream);
+  } else {
+    gemv_f32(dt, rows, m.lm_head, c.vocab_size, D, x, D, {m.dec_norm}, logits, c.vocab_size, stream);
+  }
+}
+
+void State::temporal_step(const void* in, const void* enc, int f, void* out) {
+  MRT_REQUIRE(f >= 0 && f < F, "temporal_step: frame_idx out of range for this state");
+  MRT_HIP_CHECK(hipSetDevice(m.device));
+  if (f == 0) {
+    temporal_len_ = 0;
+    if (enc != nullptr) project_cross(enc);
+  }
+  if (!cross_ready_)
+    throw Error(2, "temporal_step: cross-attention K/V not populated (call encode or pass enc_out at frame 0)");
+  if (temporal_len_ != f)
+    throw Error(1, "temporal_step: cache holds " + std::to_string(temporal_len_) + " entries, frame_idx " +
+                       std::to_string(f));
+  run_temporal(in, f, out);
+  temporal_len_ = f + 1;
+}
+
+void State::depth_step(const void* in, int l, int level, int C, int off, float* logits) {
+  const Config& c = m.cfg;
+  MRT_REQUIRE(l >= 0 && l < c.rvq_depth, "depth_step: depth_idx out of range");
+  if (level >= 0) {
+    MRT_REQUIRE(C >= 1 && off >= 0 && off + C * (level + 1) <= c.vocab_size,
+                "depth_step: level slice outside the vocabulary");
+  }
+  MRT_HIP_CHECK(hipSetDevice(m.device));
+  if (l == 0) depth_len_ = 0;
+  if (depth_len_ != l)
+    throw Error(1, "depth_step: cache holds " + std::to_string(depth_len_) + " entries, depth_idx " +
+                       std::to_string(l));
+  run_depth(in, l, level, C, off, logits);
+  depth_len_ = l + 1;
+}
+
+void State::enqueue_decode(const GenOpts& o) {
+  const Config& c = m.cfg;
+  const DType dt = m.dt;
+  const int D = c.d_model;
+  SampleParams sp{o.guidance_weight, o.temperature, o.top_k, o.codebook, o.codec_offset, o.rvq_depth, d_seed};
+  // Frame 0 feeds emb(PAD = 0) on both rows (decode.cpp:339-341, 366-368).
+  embed_fill(dt, m.emb, D, 0, rows, t_in, stream);
+  const size_t row_bytes = static_cast<size_t>(rows) * D * esz();
+  for (int f = 0; f < o.num_frames; ++f) {
+    run_temporal(t_in, f, t_out);
+    if (o.record_temporal)
+      copy(static_cast<char*>(o.record_temporal) + f * row_bytes, t_out, row_bytes);
+    for (int l = 0; l < o.rvq_depth; ++l) {
+      run_depth(l == 0 ? t_out : d_in, l, l, o.codebook, o.codec_offset, slice);
+      if (o.record_slices)
+        copy(o.record_slices + (static_cast<size_t>(f) * o.rvq_depth + l) * rows * o.codebook, slice,
+             static_cast<size_t>(rows) * o.codebook * 4);
+      sample_level(dt, slice, sp, f, l, f * o.rvq_depth + l, o.teacher ? d_teacher : nullptr, d_tokens,
+                   o.record_drawn, m.emb, D, d_in, fsum, t_in, stream);
+    }
+    if (o.record_frame_mean)
+      copy(static_cast<char*>(o.record_frame_mean) + f * row_bytes, t_in, row_bytes);
+  }
+}
+
+int State::sample(const float* slice_dev, const GenOpts& o, int frame, int level) {
+  const Config& c = m.cfg;
+  MRT_REQUIRE(o.codebook >= 1 && o.codebook <= 1024, "sample: codebook_size must be in [1, 1024]");
+  MRT_REQUIRE(level >= 0 && level < o.rvq_depth && frame >= 0, "sample: frame/level out of range");
+  MRT_REQUIRE(o.codec_offset >= 0 && o.codec_offset + o.codebook * o.rvq_depth <= c.vocab_size,
+              "sample: codec levels exceed the vocabulary");
+  MRT_REQUIRE(o.temperature >= 0.0f, "sample: temperature must be >= 0");
+  MRT_HIP_CHECK(hipSetDevice(m.device));
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  std::memcpy(h_pinned, &o.seed, 8);
+  MRT_HIP_CHECK(hipMemcpyAsync(d_seed, h_pinned, 8, hipMemcpyHostToDevice, stream));
+  SampleParams sp{o.guidance_weight, o.temperature, o.top_k, o.codebook, o.codec_offset, o.rvq_depth, d_seed};
+  // Token goes to slot 0 of the token buffer; the feedback outputs land in
+  // scratch rows that the next decode overwrites.
+  sample_level(m.dt, slice_dev, sp, frame, level, 0, nullptr, d_tokens, nullptr, m.emb, c.d_model, d_in, fsum,
+               x, stream);
+  MRT_HIP_CHECK(hipMemcpyAsync(h_pinned, d_tokens, 4, hipMemcpyDeviceToHost, stream));
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  return h_pinned[0];
+}
+
+void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* out_host) {
+  const Config& c = m.cfg;
+  MRT_REQUIRE(o.num_frames >= 1 && o.num_frames <= F, "generate: num_frames exceeds the state's max_frames");
+  MRT_REQUIRE(o.rvq_depth == c.rvq_depth, "generate: rvq_depth must equal the model's rvq_depth");
+  MRT_REQUIRE(o.codebook >= 1 && o.codebook <= 1024, "generate: codebook_size must be in [1, 1024]");
+  MRT_REQUIRE(o.codec_offset >= 0 && o.codec_offset + o.codebook * o.rvq_depth <= c.vocab_size,
+              "generate: codec levels exceed the vocabulary");
+  MRT_REQUIRE(o.temperature >= 0.0f, "generate: temperature must be >= 0");
+  MRT_HIP_CHECK(hipSetDevice(m.device));
+  if (enc_tokens_host) encode(enc_tokens_host);
+  if (!cross_ready_) throw Error(2, "generate: no encoder output (pass enc_tokens or call encode)");
+  const size_t nt = static_cast<size_t>(o.num_frames) * o.rvq_depth;
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  if (o.teacher) {
+    for (size_t i = 0; i < nt; ++i)
+      MRT_REQUIRE(o.teacher[i] >= 0 && o.teacher[i] < c.vocab_size, "generate: teacher id out of range");
+    std::memcpy(h_pinned, o.teacher, nt * 4);
+    MRT_HIP_CHECK(hipMemcpyAsync(d_teacher, h_pinned, nt * 4, hipMemcpyHostToDevice, stream));
+    MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  }
+  std::memcpy(h_pinned, &o.seed, 8);
+  MRT_HIP_CHECK(hipMemcpyAsync(d_seed, h_pinned, 8, hipMemcpyHostToDevice, stream));
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+
+  if (o.use_graph) {
+    const std::vector<double> key = {
+        (double)o.num_frames, (double)o.rvq_depth, (double)o.temperature, (double)o.top_k,
+        (double)o.guidance_weight, (double)o.codebook, (double)o.codec_offset, o.teacher ? 1.0 : 0.0,
+        (double)reinterpret_cast<uintptr_t>(o.record_slices),
+        (double)reinterpret_cast<uintptr_t>(o.record_temporal),
+        (double)reinterpret_cast<uintptr_t>(o.record_drawn),
+        (double)reinterpret_cast<uintptr_t>(o.record_frame_mean)};
+    if (!graph_exec_ || key != graph_key_) {
+      if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+      if (graph_) (void)hipGraphDestroy(graph_);
+      graph_exec_ = nullptr;
+      graph_ = nullptr;
+      MRT_HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+      try {
+        enqueue_decode(o);
+      } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      MRT_HIP_CHECK(hipStreamEndCapture(stream, &graph_));
+      MRT_HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+      graph_key_ = key;
+    }
+    MRT_HIP_CHECK(hipGraphLaunch(graph_exec_, stream));
+  } else {
+    enqueue_decode(o);
+  }
+  MRT_HIP_CHECK(hipMemcpyAsync(h_pinned, d_tokens, nt * 4, hipMemcpyDeviceToHost, stream));
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  std::memcpy(out_host, h_pinned, nt * 4);
+  temporal_len_ = o.num_frames;
+  depth_len_ = o.rvq_depth;
+}
+
+void* State::buffer(int which, int layer, size_t* bytes) {
+  const Config& c = m.cfg;
+  const size_t H = c.num_heads;
+  auto chk = [&](int n) { MRT_REQUIRE(layer >= 0 && layer < n, "state buffer: layer out of range"); };
+  switch (which) {
+    case 0:
+      *bytes = static_cast<size_t>(rows) * S * c.d_model * esz();
+      return enc_out;
+    case 1:
+    case 2:
+      chk(c.num_temporal_layers);
+      *bytes = static_cast<size_t>(rows) * H * S * 64 * esz();
+      return which == 1 ? ck(layer) : cv(layer);
+    case 3:
+    case 4:
+      chk(c.num_temporal_layers);
+      *bytes = static_cast<size_t>(rows) * H * F * 64 * esz();
+      return which == 3 ? tk(layer) : tv(layer);
+    case 5:
+    case 6:
+      chk(c.num_depth_layers);
+      *bytes = static_cast<size_t>(rows) * H * c.rvq_depth * 64 * esz();
+      return which == 5 ? dk(layer) : dv(layer);
+    default:
+      throw Error(1, "state buffer: unknown buffer id");
+  }
+}
+
+void State::set_cache_length(int kind, int length) {
+  if (kind == 0) {
+    MRT_REQUIRE(length >= 0 && length <= F, "set_cache_length: temporal length out of range");
+    temporal_len_ = length;
+  } else if (kind == 1) {
+    MRT_REQUIRE(length >= 0 && length <= m.cfg.rvq_depth, "set_cache_length: depth length out of range");
+    depth_len_ = length;
+  } else if (kind == 2) {
+    cross_ready_ = length != 0;
+  } else {
+    throw Error(1, "set_cache_length: kind must be 0 (temporal), 1 (depth) or 2 (cross ready)");
+  }
+}
+
+}  // namespace mrt

@@ -1,0 +1,181 @@
+// Host orchestration of the Depthformer HIP backend: device weights (Model)
+// and one decode stream's device state (State).  Mirrors the reference's
+// ``Depthformer`` class (depthformer/model.h:72-239) and ``generate_tokens``
+// (depthformer/decode.cpp:239-573).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "safetensors.hpp"
+
+namespace mrt {
+
+// DepthformerConfig (model.h:47-68).
+struct Config {
+  int vocab_size = 29824;
+  int d_model = 768;
+  int d_kv = 64;
+  int d_ff = 2048;
+  int num_heads = 12;
+  int num_encoder_layers = 12;
+  int num_temporal_layers = 20;
+  int num_depth_layers = 4;
+  int max_encoder_length = 1006;
+  int rvq_depth = 16;
+  int temporal_num_buckets = 128;
+  int temporal_max_distance = 128;
+  int depth_num_buckets = 16;
+  int depth_max_distance = 16;
+
+  static Config base() { return Config{}; }  // model.cpp:34-36
+  static Config large() {                     // model.cpp:38-48
+    Config c;
+    c.d_model = 1024;
+    c.d_kv = 64;
+    c.d_ff = 2816;
+    c.num_heads = 16;
+    c.num_encoder_layers = 24;
+    c.num_temporal_layers = 40;
+    c.num_depth_layers = 8;
+    return c;
+  }
+  int hd() const { return num_heads * d_kv; }
+};
+
+// T5 relative-position bucket for a non-negative query-key distance n
+// (unidirectional branch of modules.cpp:139-174, float32 log branch).
+int relative_position_bucket(int n, int num_buckets, int max_distance);
+
+// Bundle key -> shape for a config (the reference's weight-bundle layout).
+std::vector<std::pair<std::string, std::vector<int64_t>>> bundle_layout(const Config& c);
+
+struct EncoderLayerW {
+  const void *norm_attn, *wqkv, *wo, *norm_ff, *w01, *wo2;
+};
+struct DecoderLayerW {
+  const void *norm_sa, *wqkv, *wo, *norm_ca, *wq_c, *wo_c, *norm_ff, *w01, *wo2;
+};
+
+class Model {
+ public:
+  Model(const TensorSource& src, const Config& cfg, DType dt, int device);
+  ~Model();
+  Model(const Model&) = delete;
+  Model& operator=(const Model&) = delete;
+
+  Config cfg;
+  DType dt;
+  int device;
+  size_t esz;  // bytes per stored element
+
+  const void* emb = nullptr;       // (V, D)
+  const void* lm_head = nullptr;   // (V, D)
+  const void* pe = nullptr;        // (max_enc, D), rounded to the model dtype
+  const void* enc_norm = nullptr;  // (D)
+  const void* dec_norm = nullptr;  // (D)
+  const void* tbias = nullptr;     // (temporal buckets, H)
+  const void* dbias = nullptr;     // (depth buckets, H)
+  const int* tbuckets = nullptr;   // bucket of distance n, n < kBucketTable
+  const int* dbuckets = nullptr;
+  const void* wkv_cross = nullptr; // (Lt * 2 * HD, D): [layer][k|v] rows
+  std::vector<EncoderLayerW> enc;
+  std::vector<DecoderLayerW> tmp, dep;
+  size_t weight_bytes = 0;
+
+  static constexpr int kBucketTable = 4096;
+
+ private:
+  std::vector<void*> allocs_;
+  const void* upload(const std::vector<float>& host);
+  const void* upload_i32(const std::vector<int>& host);
+};
+
+struct GenOpts {
+  int num_frames = 50;
+  int rvq_depth = 16;
+  float temperature = 1.1f;
+  int top_k = 40;
+  float guidance_weight = 4.0f;
+  uint64_t seed = 0;
+  int codebook = 1024;
+  int codec_offset = 2;
+  const int32_t* teacher = nullptr;  // host (F, L)
+  bool use_graph = false;
+  float* record_slices = nullptr;    // device (F, L, rows, C)
+  void* record_temporal = nullptr;   // device (F, rows, D)
+  int* record_drawn = nullptr;       // device (F, L)
+  void* record_frame_mean = nullptr; // device (F, rows, D)
+};
+
+class State {
+ public:
+  State(Model& m, int rows, int max_frames, int enc_len);
+  ~State();
+  State(const State&) = delete;
+  State& operator=(const State&) = delete;
+
+  Model& m;
+  int rows, F, S;
+  hipStream_t stream = nullptr;
+
+  void encode(const int32_t* tokens_host);
+  void project_cross(const void* enc_out_dev);
+  void temporal_step(const void* in, const void* enc_out, int frame_idx, void* out);
+  void depth_step(const void* in, int depth_idx, int level, int codebook, int codec_offset,
+                  float* logits);
+  void generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* out_host);
+  // CFG + temperature/top-k draw over one level slice (rows 0/1, C entries)
+  // held in a device fp32 buffer; returns the LLM id.
+  int sample(const float* slice_dev, const GenOpts& o, int frame, int level);
+
+  // Buffer access for parity checks.
+  void* buffer(int which, int layer, size_t* bytes);
+  void set_cache_length(int kind, int length);
+  void sync();
+
+ private:
+  size_t esz() const { return m.esz; }
+  char* tk(int i) const;
+  char* tv(int i) const;
+  char* dk(int i) const;
+  char* dv(int i) const;
+  char* ck(int i) const;
+  char* cv(int i) const;
+  void run_temporal(const void* in, int f, void* out);
+  void run_depth(const void* in, int l, int level, int codebook, int codec_offset, float* logits);
+  void enqueue_decode(const GenOpts& o);
+  void copy(void* dst, const void* src, size_t bytes);
+
+  std::vector<void*> allocs_;
+  void* dalloc(size_t bytes);
+
+  // device buffers
+  int* d_enc_tok = nullptr;
+  int32_t* h_pinned = nullptr;  // host staging: tokens in/out
+  size_t h_pinned_n = 0;
+  void *ex = nullptr, *exn = nullptr, *eqkv = nullptr, *eattn = nullptr, *effh = nullptr;
+  void* enc_out = nullptr;
+  void *cross = nullptr, *tkv = nullptr, *dkv = nullptr;
+  void *x = nullptr, *q = nullptr, *attn = nullptr, *ffh = nullptr;
+  void *t_in = nullptr, *t_out = nullptr, *d_in = nullptr, *fsum = nullptr;
+  float *slice = nullptr, *part = nullptr;
+  int *d_tokens = nullptr, *d_teacher = nullptr;
+  uint64_t* d_seed = nullptr;
+  int nsplit = 1;
+  int max_slice = 0;
+
+  int temporal_len_ = 0, depth_len_ = 0;
+  bool cross_ready_ = false;
+
+  // captured decode loop
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t graph_exec_ = nullptr;
+  std::vector<double> graph_key_;
+};
+
+}  // namespace mrt

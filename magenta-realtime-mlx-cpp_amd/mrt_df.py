@@ -1,0 +1,386 @@
+"""Python binding of ``libmrt_df.so`` (include/mrt_df.h) over ctypes.
+
+Mirrors the reference's ``Depthformer`` surface (depthformer/model.h:72-239):
+``encode``, ``temporal_step``, ``depth_step``, ``generate_tokens`` and
+``sample_level`` (decode.cpp:124-148).  Device buffers are torch tensors
+(torch is only the allocator here); all compute runs in the HIP library.
+The library must be built (``build.py``); loading fails loudly otherwise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import os
+import pathlib
+import re
+from typing import Dict, Optional, Sequence
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = HERE / "libmrt_df.so"
+HEADER = HERE.parent / "include" / "mrt_df.h"
+
+MRT_OK = 0
+DTYPE_F32, DTYPE_BF16 = 0, 1
+BUF_ENC_OUT, BUF_CROSS_K, BUF_CROSS_V = 0, 1, 2
+BUF_TEMPORAL_K, BUF_TEMPORAL_V, BUF_DEPTH_K, BUF_DEPTH_V = 3, 4, 5, 6
+
+CONFIG_FIELDS = ("vocab_size", "d_model", "d_kv", "d_ff", "num_heads", "num_encoder_layers",
+                 "num_temporal_layers", "num_depth_layers", "max_encoder_length", "rvq_depth",
+                 "temporal_num_buckets", "temporal_max_distance", "depth_num_buckets",
+                 "depth_max_distance")
+
+
+class MrtError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[mrt_df error {code}] {msg}")
+        self.code = code
+
+
+class _Config(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_int32) for f in CONFIG_FIELDS]
+
+
+class _GenOpts(ctypes.Structure):
+    _fields_ = [
+        ("num_frames", ctypes.c_int32),
+        ("rvq_depth", ctypes.c_int32),
+        ("temperature", ctypes.c_float),
+        ("top_k", ctypes.c_int32),
+        ("guidance_weight", ctypes.c_float),
+        ("seed", ctypes.c_uint64),
+        ("codebook_size", ctypes.c_int32),
+        ("codec_offset", ctypes.c_int32),
+        ("teacher", ctypes.POINTER(ctypes.c_int32)),
+        ("use_graph", ctypes.c_int32),
+        ("record_slices", ctypes.c_void_p),
+        ("record_temporal", ctypes.c_void_p),
+        ("record_drawn", ctypes.c_void_p),
+        ("record_frame_mean", ctypes.c_void_p),
+    ]
+
+
+@dataclasses.dataclass(frozen=True)
+class Config:
+    """DepthformerConfig (model.h:47-68)."""
+
+    vocab_size: int = 29824
+    d_model: int = 768
+    d_kv: int = 64
+    d_ff: int = 2048
+    num_heads: int = 12
+    num_encoder_layers: int = 12
+    num_temporal_layers: int = 20
+    num_depth_layers: int = 4
+    max_encoder_length: int = 1006
+    rvq_depth: int = 16
+    temporal_num_buckets: int = 128
+    temporal_max_distance: int = 128
+    depth_num_buckets: int = 16
+    depth_max_distance: int = 16
+
+    @staticmethod
+    def base() -> "Config":
+        return Config()
+
+    @staticmethod
+    def large() -> "Config":
+        return Config(d_model=1024, d_kv=64, d_ff=2816, num_heads=16, num_encoder_layers=24,
+                      num_temporal_layers=40, num_depth_layers=8)
+
+    @staticmethod
+    def bench() -> "Config":
+        """d_model 1024, 16 heads x 64, d_ff 2816, 12/20/4 layers, vocab 29824."""
+        return Config(d_model=1024, d_kv=64, d_ff=2816, num_heads=16, num_encoder_layers=12,
+                      num_temporal_layers=20, num_depth_layers=4)
+
+    @staticmethod
+    def tiny(codebook: int = 8) -> "Config":
+        return Config(vocab_size=2 + 22 * codebook, d_model=128, d_kv=64, d_ff=192, num_heads=2,
+                      num_encoder_layers=2, num_temporal_layers=2, num_depth_layers=2,
+                      max_encoder_length=46)
+
+    def to_c(self) -> _Config:
+        return _Config(*[getattr(self, f) for f in CONFIG_FIELDS])
+
+
+@dataclasses.dataclass
+class GenOptions:
+    """GenerateOptions (decode.h:48-57) + vocab layout (system.h:44-83)."""
+
+    num_frames: int = 50
+    rvq_depth: int = 16
+    temperature: float = 1.1
+    top_k: int = 40
+    guidance_weight: float = 5.0
+    seed: int = 0
+    codebook_size: int = 1024
+    codec_offset: int = 2
+    use_graph: bool = True
+
+
+_lib = None
+
+
+def header_functions(path: pathlib.Path = HEADER) -> list:
+    """Names of the functions include/mrt_df.h declares."""
+    text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mrt_[a-z0-9_]+)\s*\(", text)))
+
+
+def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = pathlib.Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(f"{p} is missing: build it with `python {HERE / 'build.py'}` "
+                           "(there is no CPU fallback)")
+    lib = ctypes.CDLL(str(p))
+    vp, i32, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    sig = {
+        "mrt_last_error": (ctypes.c_char_p, []),
+        "mrt_df_config_base": (None, [ctypes.POINTER(_Config)]),
+        "mrt_df_config_large": (None, [ctypes.POINTER(_Config)]),
+        "mrt_df_create": (i32, [ctypes.c_char_p, ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),
+        "mrt_df_create_from_tensors": (i32, [i32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(vp),
+                                             ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_int32),
+                                             ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),
+        "mrt_df_destroy": (None, [vp]),
+        "mrt_df_get_config": (i32, [vp, ctypes.POINTER(_Config), ctypes.POINTER(i32)]),
+        "mrt_df_state_create": (i32, [vp, i32, i32, i32, ctypes.POINTER(vp)]),
+        "mrt_df_state_destroy": (None, [vp]),
+        "mrt_df_state_stream": (i32, [vp, ctypes.POINTER(vp)]),
+        "mrt_df_sync": (i32, [vp]),
+        "mrt_df_encode": (i32, [vp, ctypes.POINTER(ctypes.c_int32)]),
+        "mrt_df_temporal_step": (i32, [vp, vp, vp, i32, vp]),
+        "mrt_df_depth_step": (i32, [vp, vp, i32, i32, i32, i32, vp]),
+        "mrt_df_generate_tokens": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_GenOpts),
+                                         ctypes.POINTER(ctypes.c_int32)]),
+        "mrt_df_sample_level": (i32, [vp, vp, ctypes.POINTER(_GenOpts), i32, i32,
+                                      ctypes.POINTER(ctypes.c_int32)]),
+        "mrt_df_state_buffer_bytes": (i32, [vp, i32, ctypes.POINTER(sz)]),
+        "mrt_df_state_read": (i32, [vp, i32, i32, vp, sz]),
+        "mrt_df_state_write": (i32, [vp, i32, i32, vp, sz]),
+        "mrt_df_state_set_cache_length": (i32, [vp, i32, i32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(lib, code: int) -> None:
+    if code != MRT_OK:
+        raise MrtError(code, lib.mrt_last_error().decode(errors="replace"))
+
+
+def _i32_ptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+def _torch():
+    import torch  # noqa: PLC0415  (device allocator only)
+    return torch
+
+
+def _dptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(int(t.data_ptr()))
+
+
+class Depthformer:
+    """Device-resident Depthformer (model.h:72-239)."""
+
+    def __init__(self, weights, config: Config, dtype: str = "bf16", device: int = 0):
+        self.lib = load_library()
+        self.config = config
+        self.dtype = dtype
+        self.device = device
+        d = {"fp32": DTYPE_F32, "float32": DTYPE_F32, "bf16": DTYPE_BF16, "bfloat16": DTYPE_BF16}
+        if dtype not in d:
+            raise ValueError(f'unknown dtype "{dtype}"; expected fp32|bf16')
+        h = ctypes.c_void_p()
+        cfg = config.to_c()
+        if isinstance(weights, (str, os.PathLike)):
+            _check(self.lib, self.lib.mrt_df_create(str(weights).encode(), ctypes.byref(cfg), d[dtype],
+                                                    device, ctypes.byref(h)))
+        else:
+            names, arrays = [], []
+            for k, v in weights.items():
+                names.append(k.encode())
+                arrays.append(np.ascontiguousarray(v, dtype=np.float32))
+            n = len(names)
+            c_names = (ctypes.c_char_p * n)(*names)
+            c_data = (ctypes.c_void_p * n)(*[a.ctypes.data for a in arrays])
+            shapes = [np.asarray(a.shape, dtype=np.int64) for a in arrays]
+            c_shapes = (ctypes.c_void_p * n)(*[s.ctypes.data for s in shapes])
+            c_nd = (ctypes.c_int32 * n)(*[a.ndim for a in arrays])
+            _check(self.lib, self.lib.mrt_df_create_from_tensors(
+                n, c_names, c_data, c_shapes, c_nd, ctypes.byref(cfg), d[dtype], device,
+                ctypes.byref(h)))
+        self._h = h
+
+    @property
+    def torch_dtype(self):
+        torch = _torch()
+        return torch.float32 if self.dtype in ("fp32", "float32") else torch.bfloat16
+
+    def new_state(self, rows: int = 2, max_frames: int = 50, enc_len: Optional[int] = None) -> "State":
+        return State(self, rows, max_frames, enc_len or self.config.max_encoder_length)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.mrt_df_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+
+class State:
+    """One decode stream: encoder output, cross K/V, ring KV caches, HIP stream."""
+
+    def __init__(self, model: Depthformer, rows: int, max_frames: int, enc_len: int):
+        self.model = model
+        self.lib = model.lib
+        self.rows, self.max_frames, self.enc_len = rows, max_frames, enc_len
+        h = ctypes.c_void_p()
+        _check(self.lib, self.lib.mrt_df_state_create(model._h, rows, max_frames, enc_len, ctypes.byref(h)))
+        self._h = h
+
+    # -- reference methods ------------------------------------------------
+    def encode(self, tokens: np.ndarray) -> None:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        if t.shape != (self.rows, self.enc_len):
+            raise ValueError(f"tokens must be {(self.rows, self.enc_len)}, got {t.shape}")
+        _check(self.lib, self.lib.mrt_df_encode(self._h, _i32_ptr(t)))
+
+    def temporal_step(self, frame_emb, frame_idx: int, enc_out=None, out=None):
+        torch = _torch()
+        if out is None:
+            out = torch.empty_like(frame_emb)
+        self._sync_torch()
+        _check(self.lib, self.lib.mrt_df_temporal_step(
+            self._h, _dptr(frame_emb), _dptr(enc_out) if enc_out is not None else None, frame_idx,
+            _dptr(out)))
+        self.sync()
+        return out
+
+    def depth_step(self, tok_emb, depth_idx: int, level: Optional[int] = None,
+                   codebook_size: int = 1024, codec_offset: int = 2, out=None):
+        torch = _torch()
+        cfg = self.model.config
+        n = codebook_size if level is not None else cfg.vocab_size
+        if out is None:
+            out = torch.empty((self.rows, n), dtype=torch.float32, device=tok_emb.device)
+        self._sync_torch()
+        _check(self.lib, self.lib.mrt_df_depth_step(
+            self._h, _dptr(tok_emb), depth_idx, -1 if level is None else level, codebook_size,
+            codec_offset, _dptr(out)))
+        self.sync()
+        return out
+
+    def generate_tokens(self, enc_tokens: Optional[np.ndarray], opts: GenOptions,
+                        teacher: Optional[np.ndarray] = None, record: Optional[Dict] = None) -> np.ndarray:
+        o = self._opts(opts)
+        keep = []
+        if teacher is not None:
+            tt = np.ascontiguousarray(teacher, dtype=np.int32)
+            if tt.shape != (opts.num_frames, opts.rvq_depth):
+                raise ValueError("teacher must be (num_frames, rvq_depth)")
+            keep.append(tt)
+            o.teacher = _i32_ptr(tt)
+        if record is not None:
+            for key, field in (("slices", "record_slices"), ("temporal", "record_temporal"),
+                               ("drawn", "record_drawn"), ("frame_mean", "record_frame_mean")):
+                if key in record:
+                    setattr(o, field, int(record[key].data_ptr()))
+            self._sync_torch()
+        enc = None
+        if enc_tokens is not None:
+            enc = np.ascontiguousarray(enc_tokens, dtype=np.int32)
+            if enc.shape != (self.rows, self.enc_len):
+                raise ValueError(f"enc_tokens must be {(self.rows, self.enc_len)}")
+        out = np.zeros((opts.num_frames, opts.rvq_depth), dtype=np.int32)
+        _check(self.lib, self.lib.mrt_df_generate_tokens(
+            self._h, _i32_ptr(enc) if enc is not None else None, ctypes.byref(o), _i32_ptr(out)))
+        return out
+
+    def sample_level(self, slice_logits, opts: GenOptions, frame: int, level: int) -> int:
+        o = self._opts(opts)
+        tok = ctypes.c_int32()
+        self._sync_torch()
+        _check(self.lib, self.lib.mrt_df_sample_level(self._h, _dptr(slice_logits), ctypes.byref(o),
+                                                      frame, level, ctypes.byref(tok)))
+        return int(tok.value)
+
+    # -- buffers ------------------------------------------------------------
+    def buffer_shape(self, which: int):
+        c = self.model.config
+        H = c.num_heads
+        return {
+            BUF_ENC_OUT: (self.rows, self.enc_len, c.d_model),
+            BUF_CROSS_K: (self.rows, H, self.enc_len, 64), BUF_CROSS_V: (self.rows, H, self.enc_len, 64),
+            BUF_TEMPORAL_K: (self.rows, H, self.max_frames, 64),
+            BUF_TEMPORAL_V: (self.rows, H, self.max_frames, 64),
+            BUF_DEPTH_K: (self.rows, H, c.rvq_depth, 64), BUF_DEPTH_V: (self.rows, H, c.rvq_depth, 64),
+        }[which]
+
+    def read(self, which: int, layer: int = 0):
+        torch = _torch()
+        t = torch.empty(self.buffer_shape(which), dtype=self.model.torch_dtype,
+                        device=f"cuda:{self.model.device}")
+        self._sync_torch()
+        _check(self.lib, self.lib.mrt_df_state_read(self._h, which, layer, _dptr(t),
+                                                    t.numel() * t.element_size()))
+        return t
+
+    def write(self, which: int, layer: int, t) -> None:
+        self._sync_torch()
+        _check(self.lib, self.lib.mrt_df_state_write(self._h, which, layer, _dptr(t),
+                                                     t.numel() * t.element_size()))
+
+    def set_cache_length(self, kind: int, length: int) -> None:
+        _check(self.lib, self.lib.mrt_df_state_set_cache_length(self._h, kind, length))
+
+    def stream_handle(self) -> int:
+        s = ctypes.c_void_p()
+        _check(self.lib, self.lib.mrt_df_state_stream(self._h, ctypes.byref(s)))
+        return int(s.value or 0)
+
+    def sync(self) -> None:
+        _check(self.lib, self.lib.mrt_df_sync(self._h))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.mrt_df_state_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+    # -- helpers --------------------------------------------------------------
+    @staticmethod
+    def _opts(opts: GenOptions) -> _GenOpts:
+        return _GenOpts(num_frames=opts.num_frames, rvq_depth=opts.rvq_depth,
+                        temperature=opts.temperature, top_k=opts.top_k,
+                        guidance_weight=opts.guidance_weight, seed=opts.seed & ((1 << 64) - 1),
+                        codebook_size=opts.codebook_size, codec_offset=opts.codec_offset,
+                        teacher=None, use_graph=1 if opts.use_graph else 0)
+
+    @staticmethod
+    def _sync_torch() -> None:
+        torch = _torch()
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()

@@ -1,0 +1,254 @@
+"""HIP path vs the oracle on a tiny seeded model (d_model 128, 2 heads x 64).
+
+Everything is called through the C ABI (libmrt_df.so via mrt_df.py).
+Tolerances (norm-wise relative error ||a-b|| / ||b||):
+  fp32 logits / activations <= 1e-4;  bf16 <= 2e-2;  teacher-forced argmax
+  agreement >= 99 %;  KV ring indexing and token plumbing bit-exact.
+"""
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+def rel(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def env(gpu_available):
+    import torch
+    import mrt_df
+    import synth_bundle
+    from oracle import depthformer_oracle as O
+
+    cfg = mrt_df.Config.tiny()
+    ocfg = O.DepthformerConfig(**dataclasses.asdict(cfg))
+    w = synth_bundle.make_weights(cfg, seed=11, norm_jitter=0.1)
+    rng = np.random.default_rng(42)
+    S = cfg.max_encoder_length
+    C = 8
+    tok = np.zeros((2, S), dtype=np.int32)
+    ctx = rng.integers(0, C, size=(S - 6,))
+    lvl = np.arange(S - 6) % 4
+    tok[0, :S - 6] = 2 + C * lvl + ctx
+    tok[1, :S - 6] = tok[0, :S - 6]
+    tok[0, S - 6:] = 2 + 16 * C + C * np.arange(6) + rng.integers(0, C, 6)
+    tok[1, S - 6:] = 1
+    return dict(torch=torch, mrt_df=mrt_df, O=O, cfg=cfg, ocfg=ocfg, w=w, tok=tok, C=C, rng=rng)
+
+
+def _model(env, dtype):
+    return env["mrt_df"].Depthformer(env["w"], env["cfg"], dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_encode_and_cross_kv(env, dtype, tol):
+    mrt_df, O, torch = env["mrt_df"], env["O"], env["torch"]
+    m = _model(env, dtype)
+    st = m.new_state(max_frames=8)
+    st.encode(env["tok"])
+    om = O.OracleDepthformer(env["w"], env["ocfg"], mode=dtype)
+    enc = om.encode(env["tok"])
+    got = st.read(mrt_df.BUF_ENC_OUT).float().cpu().numpy()
+    assert rel(got, enc) <= tol
+    for i, (k, v) in enumerate(om.precompute_cross_kv(enc)):
+        assert rel(st.read(mrt_df.BUF_CROSS_K, i).float().cpu().numpy(), k) <= tol
+        assert rel(st.read(mrt_df.BUF_CROSS_V, i).float().cpu().numpy(), v) <= tol
+
+
+@pytest.mark.parametrize("dtype,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_temporal_steps_and_ring_indexing(env, dtype, tol):
+    mrt_df, O, torch = env["mrt_df"], env["O"], env["torch"]
+    cfg = env["cfg"]
+    m = _model(env, dtype)
+    F = 6
+    st = m.new_state(max_frames=F)
+    st.encode(env["tok"])
+    om = O.OracleDepthformer(env["w"], env["ocfg"], mode=dtype)
+    enc = om.encode(env["tok"])
+    # Sentinel-fill the rings: slots past the current frame must stay untouched.
+    nan = torch.full(st.buffer_shape(mrt_df.BUF_TEMPORAL_K), float("nan"), dtype=m.torch_dtype, device="cuda")
+    for i in range(cfg.num_temporal_layers):
+        st.write(mrt_df.BUF_TEMPORAL_K, i, nan)
+        st.write(mrt_df.BUF_TEMPORAL_V, i, nan)
+    cache = om.empty_temporal_cache()
+    rng = np.random.default_rng(7)
+    for f in range(F):
+        x = om.P.r(rng.standard_normal((2, 1, cfg.d_model)).astype(np.float32))
+        exp = om.temporal_step(x, enc, cache, f)
+        xin = torch.tensor(x[:, 0], dtype=m.torch_dtype, device="cuda")
+        out = st.temporal_step(xin, f)
+        assert rel(out.float().cpu().numpy(), exp[:, 0]) <= tol, f
+        for i in range(cfg.num_temporal_layers):
+            kr = st.read(mrt_df.BUF_TEMPORAL_K, i).float().cpu().numpy()
+            vr = st.read(mrt_df.BUF_TEMPORAL_V, i).float().cpu().numpy()
+            assert np.isnan(kr[:, :, f + 1:]).all() and np.isnan(vr[:, :, f + 1:]).all()
+            assert not np.isnan(kr[:, :, :f + 1]).any()
+            assert rel(kr[:, :, :f + 1], cache[i]["k"]) <= tol
+            assert rel(vr[:, :, :f + 1], cache[i]["v"]) <= tol
+
+
+def test_temporal_cache_length_errors(env):
+    mrt_df, torch = env["mrt_df"], env["torch"]
+    m = _model(env, "fp32")
+    st = m.new_state(max_frames=4)
+    x = torch.zeros((2, env["cfg"].d_model), device="cuda")
+    with pytest.raises(mrt_df.MrtError) as e:
+        st.temporal_step(x, 0)
+    assert e.value.code == 2  # no encoder output yet
+    st.encode(env["tok"])
+    st.temporal_step(x, 0)
+    with pytest.raises(mrt_df.MrtError) as e:
+        st.temporal_step(x, 2)
+    assert e.value.code == 1 and "cache holds 1" in str(e.value)
+    with pytest.raises(mrt_df.MrtError):
+        st.temporal_step(x, 4)
+
+
+@pytest.mark.parametrize("dtype,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_depth_steps_full_and_slice(env, dtype, tol):
+    mrt_df, O, torch = env["mrt_df"], env["O"], env["torch"]
+    cfg, C = env["cfg"], env["C"]
+    m = _model(env, dtype)
+    st = m.new_state(max_frames=2)
+    om = O.OracleDepthformer(env["w"], env["ocfg"], mode=dtype)
+    cache = om.empty_depth_cache()
+    rng = np.random.default_rng(8)
+    for l in range(cfg.rvq_depth):
+        x = om.P.r(rng.standard_normal((2, 1, cfg.d_model)).astype(np.float32))
+        exp = om.depth_step(x, cache, l)
+        xin = torch.tensor(x[:, 0], dtype=m.torch_dtype, device="cuda")
+        if l % 2 == 0:
+            got = st.depth_step(xin, l).cpu().numpy()
+            assert got.shape == (2, cfg.vocab_size)
+            assert rel(got, exp) <= tol, l
+        else:
+            got = st.depth_step(xin, l, level=l, codebook_size=C, codec_offset=2).cpu().numpy()
+            lo = 2 + C * l
+            assert rel(got, exp[:, lo:lo + C]) <= tol, l
+        for i in range(cfg.num_depth_layers):
+            kr = st.read(mrt_df.BUF_DEPTH_K, i).float().cpu().numpy()
+            assert rel(kr[:, :, :l + 1], cache[i]["k"]) <= tol
+
+
+def _oracle_generate(env, dtype, opts, teacher=None):
+    O = env["O"]
+    om = O.OracleDepthformer(env["w"], env["ocfg"], mode=dtype)
+    rec = {}
+    o = O.GenerateOptions(num_frames=opts.num_frames, rvq_depth=opts.rvq_depth,
+                          temperature=opts.temperature, top_k=opts.top_k,
+                          guidance_weight=opts.guidance_weight, seed=opts.seed,
+                          codebook_size=opts.codebook_size, codec_offset=opts.codec_offset)
+    toks = O.generate_tokens(om, env["tok"], o, teacher=teacher, record=rec)
+    return toks, rec
+
+
+def _gpu_generate(env, dtype, opts, teacher=None, use_graph=True):
+    torch, mrt_df = env["torch"], env["mrt_df"]
+    cfg = env["cfg"]
+    m = _model(env, dtype)
+    st = m.new_state(max_frames=opts.num_frames)
+    F, L, C = opts.num_frames, opts.rvq_depth, opts.codebook_size
+    rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"),
+               temporal=torch.zeros((F, 2, cfg.d_model), dtype=m.torch_dtype, device="cuda"),
+               drawn=torch.zeros((F, L), dtype=torch.int32, device="cuda"),
+               frame_mean=torch.zeros((F, 2, cfg.d_model), dtype=m.torch_dtype, device="cuda"))
+    opts = dataclasses.replace(opts, use_graph=use_graph)
+    toks = st.generate_tokens(env["tok"], opts, teacher=teacher, record=rec)
+    return toks, {k: v.float().cpu().numpy() if v.is_floating_point() else v.cpu().numpy()
+                  for k, v in rec.items()}
+
+
+def _opts(env, **kw):
+    base = dict(num_frames=5, rvq_depth=16, temperature=1.1, top_k=4, guidance_weight=5.0, seed=123,
+                codebook_size=env["C"], codec_offset=2)
+    base.update(kw)
+    return env["mrt_df"].GenOptions(**base)
+
+
+def _teacher(env, F):
+    C = env["C"]
+    rng = np.random.default_rng(99)
+    return (2 + C * np.arange(16)[None, :] + rng.integers(0, C, size=(F, 16))).astype(np.int32)
+
+
+@pytest.mark.parametrize("dtype,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_generate_teacher_forced(env, dtype, tol):
+    opts = _opts(env)
+    teacher = _teacher(env, opts.num_frames)
+    gt, grec = _gpu_generate(env, dtype, opts, teacher)
+    ot, orec = _oracle_generate(env, dtype, opts, teacher)
+    np.testing.assert_array_equal(gt, teacher)        # fed-back tokens: bit-exact plumbing
+    assert rel(grec["temporal"], orec["temporal_out"]) <= tol
+    assert rel(grec["slices"], orec["slices"]) <= tol
+    # teacher-forced argmax agreement of the CFG-combined logits
+    w = opts.guidance_weight
+    ga = np.argmax((1 + w) * grec["slices"][:, :, 0] - w * grec["slices"][:, :, 1], axis=-1)
+    oa = np.argmax((1 + w) * orec["slices"][:, :, 0] - w * orec["slices"][:, :, 1], axis=-1)
+    assert (ga == oa).mean() >= 0.99
+    # frame mean of the teacher embeddings is bit-exact (pure model-dtype adds)
+    np.testing.assert_array_equal(grec["frame_mean"], orec["frame_mean"])
+
+
+def test_generate_free_running_fp32_matches_oracle_draws(env):
+    opts = _opts(env, seed=2024)
+    gt, grec = _gpu_generate(env, "fp32", opts)
+    ot, orec = _oracle_generate(env, "fp32", opts)
+    assert (gt == ot).mean() >= 0.99, (gt, ot)
+    np.testing.assert_array_equal(grec["drawn"], gt)
+    lo = 2 + env["C"] * np.arange(16)[None, :]
+    assert ((gt >= lo) & (gt < lo + env["C"])).all()  # every draw in its level's range
+
+
+def test_generate_argmax_fp32(env):
+    opts = _opts(env, temperature=0.0)
+    gt, _ = _gpu_generate(env, "fp32", opts)
+    ot, _ = _oracle_generate(env, "fp32", opts)
+    np.testing.assert_array_equal(gt, ot)
+
+
+def test_graph_replay_equals_eager(env):
+    mrt_df = env["mrt_df"]
+    opts = _opts(env, seed=77)
+    m = _model(env, "bf16")
+    st = m.new_state(max_frames=opts.num_frames)
+    eager = st.generate_tokens(env["tok"], dataclasses.replace(opts, use_graph=False))
+    for _ in range(3):
+        g = st.generate_tokens(env["tok"], dataclasses.replace(opts, use_graph=True))
+        np.testing.assert_array_equal(g, eager)
+        e2 = st.generate_tokens(None, dataclasses.replace(opts, use_graph=False))
+        np.testing.assert_array_equal(e2, eager)
+
+
+def test_sample_level_matches_oracle(env):
+    torch, O, mrt_df = env["torch"], env["O"], env["mrt_df"]
+    import synth_bundle
+    # vocabulary of the real layout (16 levels x 1024 codes + style block)
+    cfg = dataclasses.replace(env["cfg"], vocab_size=2 + 22 * 1024)
+    m = mrt_df.Depthformer(synth_bundle.make_weights(cfg, seed=3), cfg, dtype="fp32")
+    st = m.new_state(max_frames=2)
+    rng = np.random.default_rng(5)
+    for C, k, T in [(8, 4, 1.1), (1024, 40, 1.1), (1024, 40, 0.0), (1000, 0, 0.7), (300, 40, 2.0),
+                    (1024, 1024, 1.0), (64, 1, 1.0)]:
+        opts = _opts(env, codebook_size=C, top_k=k, temperature=T, seed=int(rng.integers(1 << 40)))
+        agree = 0
+        for trial in range(40):
+            sl = (rng.standard_normal((2, C)) * 3).astype(np.float32)
+            if trial % 7 == 0:
+                sl[:, : C // 2] = sl[:, :1]  # many exact ties
+            level = trial % 16
+            got = st.sample_level(torch.tensor(sl, device="cuda"), opts, frame=trial, level=level)
+            g = O.cfg_combine(sl, opts.guidance_weight)
+            exp = opts.codec_offset + C * level + O.sample_level(
+                g, temperature=T, top_k=k, seed=opts.seed, frame=trial, level=level)
+            agree += got == exp
+        assert agree >= 39, (C, k, T, agree)
