@@ -23,6 +23,7 @@ SOURCES = [
     "decode_kernels.hip",
     "sample_kernels.hip",
     "encoder_kernels.hip",
+    "persist_kernels.hip",
     "safetensors.cpp",
     "model.cpp",
     "api.cpp",

@@ -8,10 +8,24 @@ namespace mrt {
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-// 16-byte streaming load (non-temporal hint: weights are read once per step).
+// 16-byte streaming load (non-temporal hint: weights are read once per step)
+// through a global-address-space pointer (global_load, not flat_load).
 __device__ __forceinline__ uint4 ld_nt16(const void* p) {
-  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  const u32x4_t v =
+      __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t*)(p));
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Plain 16-byte global load.
+__device__ __forceinline__ uint4 ld_g16(const void* p) {
+  const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Plain global load of one element.
+template <typename T>
+__device__ __forceinline__ T ld_g(const T* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -70,6 +84,31 @@ __device__ __forceinline__ uint32_t philox_x0(uint32_t c0, uint32_t c1, uint32_t
     c3 = lo0;
   }
   return c0;
+}
+
+// ---- grid-wide barrier for persistent kernels --------------------------------
+// Monotonic arrival counter: barrier number ``k`` of a launch completes when
+// the counter reaches (k + 1) * gridDim.x.  Every spin is bounded: past
+// ``kSpinLimit`` polls the block records an error in ``*err`` and proceeds, so
+// a barrier can never hang the device (the host reports the error).
+constexpr uint32_t kSpinLimit = 1u << 20;
+
+__device__ __forceinline__ void grid_barrier(uint32_t* bar, uint32_t target, int* err) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();  // release this block's writes device-wide
+    __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t spins = 0;
+    while (__hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __threadfence();  // acquire: later loads see other blocks' writes
+  }
+  __syncthreads();
 }
 
 constexpr uint32_t kSampleStreamTag = 0x4D525444u;

@@ -2,10 +2,12 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <thread>
 
 #include "kernels.hpp"
+#include "persist.hpp"
 
 namespace mrt {
 
@@ -319,6 +321,231 @@ State::State(Model& model, int rows_, int max_frames, int enc_len)
   d_seed = static_cast<uint64_t*>(dalloc(8));
   h_pinned_n = std::max<size_t>(M, static_cast<size_t>(F) * L) + 2;
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_pinned), h_pinned_n * 4, hipHostMallocDefault));
+  MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_err_), 64, hipHostMallocDefault));
+  *h_err_ = 0;
+  const char* path = std::getenv("MRT_DECODE_PATH");
+  if (!(path && std::string(path) == "layers")) setup_persistent();
+}
+
+// The persistent path needs: head dim 64 (checked by Model), every GEMV input
+// <= 1024 wide except d_ff <= 3072, rings of <= 64 slots, and a grid of
+// H * bph workgroups (bph >= 8) that fits on the device.
+void State::setup_persistent() {
+  const Config& c = m.cfg;
+  int num_cu = 0;
+  MRT_HIP_CHECK(hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, m.device));
+  int bph = 0;
+  const int grid = persist_grid(c.num_heads, num_cu, &bph);
+  // Every workgroup must own rows of the d_model and d_ff phases (the launch
+  // epoch advances once data from all workgroups has been seen).
+  const bool ok = grid > 0 && c.d_model <= 1024 && c.hd() <= 1024 && c.d_ff <= kMaxPersistK && c.d_ff % 32 == 0 &&
+                  F <= kMaxPersistLen && c.rvq_depth <= kMaxPersistLen && S <= 128 * bph && c.d_model >= grid &&
+                  c.d_ff >= grid;
+  if (!ok) return;
+  persist_grid_ = grid;
+  bph_ = bph;
+  const size_t D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads;
+  pair_bytes_ = 2 * esz();
+  p_tin = dalloc(D * pair_bytes_);
+  p_tout = dalloc(D * pair_bytes_);
+  p_din = dalloc(D * pair_bytes_);
+  p_fsum = dalloc(D * pair_bytes_);
+  p_in = dalloc(D * pair_bytes_);
+  p_out = dalloc(D * pair_bytes_);
+  (void)HD;
+  (void)FF;
+  // Tagged hand-off words: x, q, k, v, at, h vectors, cross partials, logits,
+  // then the epoch counter and the error flag.
+  const size_t vec = kLLVecWords;
+  const size_t part = static_cast<size_t>(H) * kMaxBph * 2 * 66;
+  const size_t logit = 2 * static_cast<size_t>(c.vocab_size);
+  ll_words_ = 6 * vec + part + logit + 64;
+  ll_block_ = dalloc(ll_words_ * sizeof(uint64_t));
+  reset_handoff();
+  auto table = [&](const std::vector<DecoderLayerW>& ws, bool temporal) {
+    std::vector<LayerDev> t(ws.size());
+    for (size_t i = 0; i < ws.size(); ++i) {
+      const DecoderLayerW& w = ws[i];
+      LayerDev& d = t[i];
+      d.norm_sa = w.norm_sa;
+      d.wqkv = w.wqkv;
+      d.wo = w.wo;
+      d.norm_ca = w.norm_ca;
+      d.wq_c = w.wq_c;
+      d.wo_c = w.wo_c;
+      d.norm_ff = w.norm_ff;
+      d.w01 = w.w01;
+      d.wo2 = w.wo2;
+      d.ck = temporal ? ck(static_cast<int>(i)) : nullptr;
+      d.cv = temporal ? cv(static_cast<int>(i)) : nullptr;
+      d.kc = temporal ? tk(static_cast<int>(i)) : dk(static_cast<int>(i));
+      d.vc = temporal ? tv(static_cast<int>(i)) : dv(static_cast<int>(i));
+    }
+    void* dev = dalloc(std::max<size_t>(t.size(), 1) * sizeof(LayerDev));
+    if (!t.empty()) MRT_HIP_CHECK(hipMemcpy(dev, t.data(), t.size() * sizeof(LayerDev), hipMemcpyHostToDevice));
+    return dev;
+  };
+  tmp_layers_ = table(m.tmp, true);
+  dep_layers_ = table(m.dep, false);
+  if (std::getenv("MRT_TRACE_PHASES")) {
+    d_trace_ = static_cast<uint64_t*>(dalloc(2 * kTraceSlots * sizeof(uint64_t)));
+    MRT_HIP_CHECK(hipMemset(d_trace_, 0, 2 * kTraceSlots * sizeof(uint64_t)));
+  }
+}
+
+// Per-phase timeline of one temporal and one depth step (frame 1, level 1).
+void State::print_trace() {
+  if (!d_trace_) return;
+  std::vector<uint64_t> t(2 * kTraceSlots);
+  MRT_HIP_CHECK(hipMemcpy(t.data(), d_trace_, t.size() * sizeof(uint64_t), hipMemcpyDeviceToHost));
+  const char* names[2] = {"temporal_step", "depth_step"};
+  for (int w = 0; w < 2; ++w) {
+    const uint64_t* r = t.data() + w * kTraceSlots;
+    const uint64_t t0 = r[kTraceStart];
+    if (!t0) continue;
+    // Each activation load records (poll start, poll done, norm done).
+    std::string line;
+    int nb = 0;
+    while (3 * nb + 2 < kTraceStart && r[3 * nb + 2]) ++nb;
+    double wait = 0, norm = 0, work = 0;
+    for (int k = 0; k < nb; ++k) {
+      const uint64_t s0 = r[3 * k], s1 = r[3 * k + 1], s2 = r[3 * k + 2];
+      const uint64_t nx = (k + 1 < nb) ? r[3 * (k + 1)] : r[kTraceEnd];
+      wait += (s1 - s0) * 0.01;
+      norm += (s2 - s1) * 0.01;
+      work += (nx - s2) * 0.01;
+      char buf[64];
+      std::snprintf(buf, sizeof buf, " %.1f/%.1f/%.1f", (s1 - s0) * 0.01, (s2 - s1) * 0.01, (nx - s2) * 0.01);
+      line += buf;
+    }
+    std::fprintf(stderr,
+                 "[mrt] %s: %d loads, total %.2f us (to final arrival %.2f us), first load at %.2f us; "
+                 "sum wait %.1f norm %.1f work %.1f; wait/norm/work us:%s\n",
+                 names[w], nb, (r[kTraceDone] - t0) * 0.01, (r[kTraceEnd] - t0) * 0.01, (r[0] - t0) * 0.01, wait,
+                 norm, work, line.c_str());
+  }
+}
+
+LLBufs State::ll_bufs() const {
+  uint64_t* b = static_cast<uint64_t*>(ll_block_);
+  const size_t vec = kLLVecWords;
+  LLBufs l;
+  l.x = b;
+  l.q = b + vec;
+  l.k = b + 2 * vec;
+  l.v = b + 3 * vec;
+  l.at = b + 4 * vec;
+  l.h = b + 5 * vec;
+  l.part = b + 6 * vec;
+  l.logit = l.part + static_cast<size_t>(m.cfg.num_heads) * kMaxBph * 2 * 66;
+  uint64_t* tail = l.logit + 2 * static_cast<size_t>(m.cfg.vocab_size);
+  l.seq = reinterpret_cast<uint32_t*>(tail);
+  l.err = reinterpret_cast<int*>(tail + 32);
+  return l;
+}
+
+// Zero every hand-off word and start the epoch at 1, so no zeroed word can
+// carry a live tag.
+void State::reset_handoff() {
+  MRT_HIP_CHECK(hipMemsetAsync(ll_block_, 0, ll_words_ * sizeof(uint64_t), stream));
+  const uint32_t one = 1;
+  MRT_HIP_CHECK(hipMemcpyAsync(ll_bufs().seq, &one, sizeof(one), hipMemcpyHostToDevice, stream));
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+}
+
+void State::launch_temporal_p(const void* in_pairs, int f, void* out_pairs) {
+  const Config& c = m.cfg;
+  StepArgs a{};
+  if (d_trace_ && f == 1) a.trace = d_trace_;
+  a.layers = static_cast<const LayerDev*>(tmp_layers_);
+  a.nlayers = c.num_temporal_layers;
+  a.cross = 1;
+  a.D = c.d_model;
+  a.HD = c.hd();
+  a.H = c.num_heads;
+  a.F = c.d_ff;
+  a.bph = bph_;
+  a.pos = f;
+  a.Lmax = F;
+  a.bias_tab = m.tbias;
+  a.buckets = m.tbuckets;
+  a.in = in_pairs;
+  a.out = out_pairs;
+  a.S = S;
+  a.ll = ll_bufs();
+  launch_step(m.dt, a, persist_grid_, stream);
+}
+
+void State::launch_depth_p(const void* in_pairs, int l, const void* head_w, int head_rows, float* logits,
+                           const GenOpts* o, int frame, int level, float* rec_slice) {
+  const Config& c = m.cfg;
+  StepArgs a{};
+  if (d_trace_ && frame == 1 && level == 1) a.trace = d_trace_ + kTraceSlots;
+  a.layers = static_cast<const LayerDev*>(dep_layers_);
+  a.nlayers = c.num_depth_layers;
+  a.cross = 0;
+  a.D = c.d_model;
+  a.HD = c.hd();
+  a.H = c.num_heads;
+  a.F = c.d_ff;
+  a.bph = bph_;
+  a.pos = l;
+  a.Lmax = c.rvq_depth;
+  a.bias_tab = m.dbias;
+  a.buckets = m.dbuckets;
+  a.in = in_pairs;
+  a.S = S;
+  a.dec_norm = m.dec_norm;
+  a.head_w = head_w;
+  a.head_rows = head_rows;
+  a.logits = logits;
+  a.rec_slice = rec_slice;
+  if (o) {
+    a.do_sample = 1;
+    a.sp = SampleParams{o->guidance_weight, o->temperature, o->top_k, o->codebook, o->codec_offset, o->rvq_depth,
+                        d_seed};
+    a.frame = frame;
+    a.level = level;
+    a.slot = frame * o->rvq_depth + level;
+    a.teacher = o->teacher ? d_teacher : nullptr;
+    a.tokens = d_tokens;
+    a.drawn = o->record_drawn;
+    a.emb = m.emb;
+    a.next_in = p_din;
+    a.fsum = p_fsum;
+    a.fmean = p_tin;
+  }
+  a.ll = ll_bufs();
+  launch_step(m.dt, a, persist_grid_, stream);
+}
+
+void State::enqueue_decode_p(const GenOpts& o) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, C = o.codebook;
+  const size_t row_bytes = static_cast<size_t>(rows) * D * esz();
+  embed_pairs(m.dt, m.emb, D, 0, p_tin, stream);  // frame 0 input: emb(PAD = 0)
+  for (int f = 0; f < o.num_frames; ++f) {
+    launch_temporal_p(p_tin, f, p_tout);
+    if (o.record_temporal) pairs_to_rows(m.dt, p_tout, D, static_cast<char*>(o.record_temporal) + f * row_bytes, stream);
+    for (int l = 0; l < o.rvq_depth; ++l) {
+      const char* head = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset + C * l) * D * esz();
+      float* rec = o.record_slices ? o.record_slices + (static_cast<size_t>(f) * o.rvq_depth + l) * rows * C : nullptr;
+      launch_depth_p(l == 0 ? p_tout : p_din, l, head, C, slice, &o, f, l, rec);
+    }
+    if (o.record_frame_mean)
+      pairs_to_rows(m.dt, p_tin, D, static_cast<char*>(o.record_frame_mean) + f * row_bytes, stream);
+  }
+}
+
+void State::check_device_error() {
+  if (!persistent()) return;
+  MRT_HIP_CHECK(hipMemcpyAsync(h_err_, ll_bufs().err, sizeof(int), hipMemcpyDeviceToHost, stream));
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  if (*h_err_ != 0) {
+    *h_err_ = 0;
+    reset_handoff();
+    throw Error(3, "a hand-off poll timed out in a persistent step kernel (results discarded)");
+  }
 }
 
 State::~State() {
@@ -328,6 +555,7 @@ State::~State() {
   if (graph_) (void)hipGraphDestroy(graph_);
   for (void* p : allocs_) (void)hipFree(p);
   if (h_pinned) (void)hipHostFree(h_pinned);
+  if (h_err_) (void)hipHostFree(h_err_);
   if (stream) (void)hipStreamDestroy(stream);
 }
 
@@ -358,7 +586,10 @@ char* State::cv(int i) const {
 
 void State::copy(void* dst, const void* src, size_t bytes) { copy_dev(dst, src, bytes, stream); }
 
-void State::sync() { MRT_HIP_CHECK(hipStreamSynchronize(stream)); }
+void State::sync() {
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  check_device_error();
+}
 
 // Depthformer::encode (model.cpp:226-241) followed by the cross K/V projection
 // of every temporal layer (modules.cpp:448-455).
@@ -458,7 +689,14 @@ void State::temporal_step(const void* in, const void* enc, int f, void* out) {
   if (temporal_len_ != f)
     throw Error(1, "temporal_step: cache holds " + std::to_string(temporal_len_) + " entries, frame_idx " +
                        std::to_string(f));
-  run_temporal(in, f, out);
+  if (persistent()) {
+    const int D = m.cfg.d_model;
+    rows_to_pairs(m.dt, in, D, p_in, stream);
+    launch_temporal_p(p_in, f, p_out);
+    pairs_to_rows(m.dt, p_out, D, out, stream);
+  } else {
+    run_temporal(in, f, out);
+  }
   temporal_len_ = f + 1;
 }
 
@@ -474,7 +712,16 @@ void State::depth_step(const void* in, int l, int level, int C, int off, float* 
   if (depth_len_ != l)
     throw Error(1, "depth_step: cache holds " + std::to_string(depth_len_) + " entries, depth_idx " +
                        std::to_string(l));
-  run_depth(in, l, level, C, off, logits);
+  if (persistent()) {
+    const int D = c.d_model;
+    rows_to_pairs(m.dt, in, D, p_in, stream);
+    const void* head = level >= 0
+                           ? static_cast<const char*>(m.lm_head) + static_cast<size_t>(off + C * level) * D * esz()
+                           : m.lm_head;
+    launch_depth_p(p_in, l, head, level >= 0 ? C : c.vocab_size, logits, nullptr, 0, 0, nullptr);
+  } else {
+    run_depth(in, l, level, C, off, logits);
+  }
   depth_len_ = l + 1;
 }
 
@@ -563,7 +810,10 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
       graph_ = nullptr;
       MRT_HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
       try {
-        enqueue_decode(o);
+        if (persistent())
+          enqueue_decode_p(o);
+        else
+          enqueue_decode(o);
       } catch (...) {
         hipGraph_t g = nullptr;
         (void)hipStreamEndCapture(stream, &g);
@@ -575,11 +825,15 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
       graph_key_ = key;
     }
     MRT_HIP_CHECK(hipGraphLaunch(graph_exec_, stream));
+  } else if (persistent()) {
+    enqueue_decode_p(o);
   } else {
     enqueue_decode(o);
   }
   MRT_HIP_CHECK(hipMemcpyAsync(h_pinned, d_tokens, nt * 4, hipMemcpyDeviceToHost, stream));
   MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  check_device_error();
+  print_trace();
   std::memcpy(out_host, h_pinned, nt * 4);
   temporal_len_ = o.num_frames;
   depth_len_ = o.rvq_depth;

@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "persist.hpp"
 #include "safetensors.hpp"
 
 namespace mrt {
@@ -137,8 +138,30 @@ class State {
   void* buffer(int which, int layer, size_t* bytes);
   void set_cache_length(int kind, int length);
   void sync();
+  bool persistent() const { return persist_grid_ > 0; }
 
  private:
+  // Persistent-kernel decode path (one launch per step).
+  void setup_persistent();
+  void launch_temporal_p(const void* in_pairs, int f, void* out_pairs);
+  void launch_depth_p(const void* in_pairs, int l, const void* head_w, int head_rows, float* logits,
+                      const GenOpts* o, int frame, int level, float* rec_slice);
+  void enqueue_decode_p(const GenOpts& o);
+  void check_device_error();
+  int persist_grid_ = 0, bph_ = 0;
+  size_t pair_bytes_ = 0;
+  void *p_tin = nullptr, *p_tout = nullptr, *p_din = nullptr, *p_fsum = nullptr, *p_in = nullptr,
+       *p_out = nullptr;
+  void* ll_block_ = nullptr;
+  size_t ll_words_ = 0;
+  LLBufs ll_bufs() const;
+  void reset_handoff();
+  void* tmp_layers_ = nullptr;  // LayerDev[num_temporal_layers]
+  void* dep_layers_ = nullptr;  // LayerDev[num_depth_layers]
+  int* h_err_ = nullptr;        // pinned
+  uint64_t* d_trace_ = nullptr; // 2 x kTraceSlots when MRT_TRACE_PHASES is set
+  void print_trace();
+
   size_t esz() const { return m.esz; }
   char* tk(int i) const;
   char* tv(int i) const;
