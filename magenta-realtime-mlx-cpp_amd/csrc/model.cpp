@@ -233,39 +233,55 @@ Model::Model(const TensorSource& src, const Config& c, DType dtype, int dev)
     w.wo2 = upload(vec(p + ".ffn.wo.weight", {D, F}));
     enc.push_back(w);
   }
+  // Decoder stacks are stored per weight kind with layers back to back, so a
+  // layer's weights sit at base + layer * (one layer's elements).
   std::vector<std::pair<std::string, int64_t>> cross_parts;
-  for (int i = 0; i < cfg.num_temporal_layers; ++i) {
-    const std::string p = "temporal_layers." + std::to_string(i);
-    DecoderLayerW w{};
-    w.norm_sa = upload(vec(p + ".pre_self_attn_norm.weight", {D}));
-    w.wqkv = upload(cat({{p + ".self_attn.q_proj.weight", HD},
-                         {p + ".self_attn.k_proj.weight", HD},
-                         {p + ".self_attn.v_proj.weight", HD}}, D));
-    w.wo = upload(vec(p + ".self_attn.o_proj.weight", {D, HD}));
-    w.norm_ca = upload(vec(p + ".pre_cross_attn_norm.weight", {D}));
-    w.wq_c = upload(vec(p + ".cross_attn.q_proj.weight", {HD, D}));
-    w.wo_c = upload(vec(p + ".cross_attn.o_proj.weight", {D, HD}));
-    w.norm_ff = upload(vec(p + ".pre_ffn_norm.weight", {D}));
-    w.w01 = upload(pack_geglu(p + ".ffn"));
-    w.wo2 = upload(vec(p + ".ffn.wo.weight", {D, F}));
-    tmp.push_back(w);
-    cross_parts.push_back({p + ".cross_attn.k_proj.weight", HD});
-    cross_parts.push_back({p + ".cross_attn.v_proj.weight", HD});
-  }
+  auto decoder_stack = [&](const std::string& prefix, int n, bool temporal, std::vector<DecoderLayerW>& out) {
+    std::vector<std::vector<float>> norm_sa, wqkv, wo, norm_ca, wq_c, wo_c, norm_ff, w01, wo2;
+    for (int i = 0; i < n; ++i) {
+      const std::string p = prefix + "." + std::to_string(i);
+      norm_sa.push_back(vec(p + ".pre_self_attn_norm.weight", {D}));
+      wqkv.push_back(cat({{p + ".self_attn.q_proj.weight", HD},
+                          {p + ".self_attn.k_proj.weight", HD},
+                          {p + ".self_attn.v_proj.weight", HD}}, D));
+      wo.push_back(vec(p + ".self_attn.o_proj.weight", {D, HD}));
+      if (temporal) {
+        norm_ca.push_back(vec(p + ".pre_cross_attn_norm.weight", {D}));
+        wq_c.push_back(vec(p + ".cross_attn.q_proj.weight", {HD, D}));
+        wo_c.push_back(vec(p + ".cross_attn.o_proj.weight", {D, HD}));
+        cross_parts.push_back({p + ".cross_attn.k_proj.weight", HD});
+        cross_parts.push_back({p + ".cross_attn.v_proj.weight", HD});
+      }
+      norm_ff.push_back(vec(p + ".pre_ffn_norm.weight", {D}));
+      w01.push_back(pack_geglu(p + ".ffn"));
+      wo2.push_back(vec(p + ".ffn.wo.weight", {D, F}));
+    }
+    out.assign(n, DecoderLayerW{});
+    auto place = [&](std::vector<std::vector<float>>& parts, const void* DecoderLayerW::*field) {
+      if (parts.empty()) return;
+      const size_t per = parts[0].size();
+      std::vector<float> all;
+      all.reserve(per * parts.size());
+      for (auto& v : parts) {
+        all.insert(all.end(), v.begin(), v.end());
+        std::vector<float>().swap(v);
+      }
+      const char* base = static_cast<const char*>(upload(all));
+      for (int i = 0; i < n; ++i) out[i].*field = base + static_cast<size_t>(i) * per * esz;
+    };
+    place(norm_sa, &DecoderLayerW::norm_sa);
+    place(wqkv, &DecoderLayerW::wqkv);
+    place(wo, &DecoderLayerW::wo);
+    place(norm_ca, &DecoderLayerW::norm_ca);
+    place(wq_c, &DecoderLayerW::wq_c);
+    place(wo_c, &DecoderLayerW::wo_c);
+    place(norm_ff, &DecoderLayerW::norm_ff);
+    place(w01, &DecoderLayerW::w01);
+    place(wo2, &DecoderLayerW::wo2);
+  };
+  decoder_stack("temporal_layers", cfg.num_temporal_layers, true, tmp);
   if (!cross_parts.empty()) wkv_cross = upload(cat(cross_parts, D));
-  for (int i = 0; i < cfg.num_depth_layers; ++i) {
-    const std::string p = "depth_layers." + std::to_string(i);
-    DecoderLayerW w{};
-    w.norm_sa = upload(vec(p + ".pre_self_attn_norm.weight", {D}));
-    w.wqkv = upload(cat({{p + ".self_attn.q_proj.weight", HD},
-                         {p + ".self_attn.k_proj.weight", HD},
-                         {p + ".self_attn.v_proj.weight", HD}}, D));
-    w.wo = upload(vec(p + ".self_attn.o_proj.weight", {D, HD}));
-    w.norm_ff = upload(vec(p + ".pre_ffn_norm.weight", {D}));
-    w.w01 = upload(pack_geglu(p + ".ffn"));
-    w.wo2 = upload(vec(p + ".ffn.wo.weight", {D, F}));
-    dep.push_back(w);
-  }
+  decoder_stack("depth_layers", cfg.num_depth_layers, false, dep);
 }
 
 Model::~Model() {
@@ -339,9 +355,12 @@ void State::setup_persistent() {
   // Every workgroup must own rows of the d_model and d_ff phases (the launch
   // epoch advances once data from all workgroups has been seen).
   const bool ok = grid > 0 && c.d_model <= 1024 && c.hd() <= 1024 && c.d_ff <= kMaxPersistK && c.d_ff % 32 == 0 &&
-                  F <= kMaxPersistLen && c.rvq_depth <= kMaxPersistLen && S <= 128 * bph && c.d_model >= grid &&
+                  F <= kMaxPersistLen && c.rvq_depth <= kMaxPersistLen && S <= kMaxCrossChunk * bph && c.d_model >= grid &&
                   c.d_ff >= grid;
   if (!ok) return;
+  lds_t_ = persist_prepare(m.dt, true, m.device);
+  lds_d_ = persist_prepare(m.dt, false, m.device);
+  if (lds_t_ == 0 || lds_d_ == 0) return;
   persist_grid_ = grid;
   bph_ = bph;
   const size_t D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads;
@@ -362,31 +381,25 @@ void State::setup_persistent() {
   ll_words_ = 6 * vec + part + logit + 64;
   ll_block_ = dalloc(ll_words_ * sizeof(uint64_t));
   reset_handoff();
-  auto table = [&](const std::vector<DecoderLayerW>& ws, bool temporal) {
-    std::vector<LayerDev> t(ws.size());
-    for (size_t i = 0; i < ws.size(); ++i) {
-      const DecoderLayerW& w = ws[i];
-      LayerDev& d = t[i];
-      d.norm_sa = w.norm_sa;
-      d.wqkv = w.wqkv;
-      d.wo = w.wo;
-      d.norm_ca = w.norm_ca;
-      d.wq_c = w.wq_c;
-      d.wo_c = w.wo_c;
-      d.norm_ff = w.norm_ff;
-      d.w01 = w.w01;
-      d.wo2 = w.wo2;
-      d.ck = temporal ? ck(static_cast<int>(i)) : nullptr;
-      d.cv = temporal ? cv(static_cast<int>(i)) : nullptr;
-      d.kc = temporal ? tk(static_cast<int>(i)) : dk(static_cast<int>(i));
-      d.vc = temporal ? tv(static_cast<int>(i)) : dv(static_cast<int>(i));
-    }
-    void* dev = dalloc(std::max<size_t>(t.size(), 1) * sizeof(LayerDev));
-    if (!t.empty()) MRT_HIP_CHECK(hipMemcpy(dev, t.data(), t.size() * sizeof(LayerDev), hipMemcpyHostToDevice));
-    return dev;
+  auto stack = [&](const std::vector<DecoderLayerW>& ws, bool temporal) {
+    DecStack d{};
+    if (ws.empty()) return d;
+    const DecoderLayerW& w = ws[0];
+    d.norm_sa = w.norm_sa;
+    d.wqkv = w.wqkv;
+    d.wo = w.wo;
+    d.norm_ca = w.norm_ca;
+    d.wq_c = w.wq_c;
+    d.wo_c = w.wo_c;
+    d.norm_ff = w.norm_ff;
+    d.w01 = w.w01;
+    d.wo2 = w.wo2;
+    d.cross = temporal ? ck(0) : nullptr;
+    d.ring = temporal ? tk(0) : dk(0);
+    return d;
   };
-  tmp_layers_ = table(m.tmp, true);
-  dep_layers_ = table(m.dep, false);
+  tstack_ = stack(m.tmp, true);
+  dstack_ = stack(m.dep, false);
   if (std::getenv("MRT_TRACE_PHASES")) {
     d_trace_ = static_cast<uint64_t*>(dalloc(2 * kTraceSlots * sizeof(uint64_t)));
     MRT_HIP_CHECK(hipMemset(d_trace_, 0, 2 * kTraceSlots * sizeof(uint64_t)));
@@ -403,26 +416,20 @@ void State::print_trace() {
     const uint64_t* r = t.data() + w * kTraceSlots;
     const uint64_t t0 = r[kTraceStart];
     if (!t0) continue;
-    // Each activation load records (poll start, poll done, norm done).
+    // Raw timeline: deltas between consecutive trace points (first 48).
     std::string line;
+    uint64_t prev = t0;
     int nb = 0;
-    while (3 * nb + 2 < kTraceStart && r[3 * nb + 2]) ++nb;
-    double wait = 0, norm = 0, work = 0;
-    for (int k = 0; k < nb; ++k) {
-      const uint64_t s0 = r[3 * k], s1 = r[3 * k + 1], s2 = r[3 * k + 2];
-      const uint64_t nx = (k + 1 < nb) ? r[3 * (k + 1)] : r[kTraceEnd];
-      wait += (s1 - s0) * 0.01;
-      norm += (s2 - s1) * 0.01;
-      work += (nx - s2) * 0.01;
-      char buf[64];
-      std::snprintf(buf, sizeof buf, " %.1f/%.1f/%.1f", (s1 - s0) * 0.01, (s2 - s1) * 0.01, (nx - s2) * 0.01);
-      line += buf;
+    for (int k = 0; k < kTraceStart && r[k]; ++k, ++nb) {
+      if (k < 48) {
+        char buf[32];
+        std::snprintf(buf, sizeof buf, " %.2f", (r[k] - prev) * 0.01);
+        line += buf;
+      }
+      prev = r[k];
     }
-    std::fprintf(stderr,
-                 "[mrt] %s: %d loads, total %.2f us (to final arrival %.2f us), first load at %.2f us; "
-                 "sum wait %.1f norm %.1f work %.1f; wait/norm/work us:%s\n",
-                 names[w], nb, (r[kTraceDone] - t0) * 0.01, (r[kTraceEnd] - t0) * 0.01, (r[0] - t0) * 0.01, wait,
-                 norm, work, line.c_str());
+    std::fprintf(stderr, "[mrt] %s: %d points, total %.2f us (to final arrival %.2f us); deltas us:%s\n", names[w], nb,
+                 (r[kTraceDone] - t0) * 0.01, (r[kTraceEnd] - t0) * 0.01, line.c_str());
   }
 }
 
@@ -457,7 +464,7 @@ void State::launch_temporal_p(const void* in_pairs, int f, void* out_pairs) {
   const Config& c = m.cfg;
   StepArgs a{};
   if (d_trace_ && f == 1) a.trace = d_trace_;
-  a.layers = static_cast<const LayerDev*>(tmp_layers_);
+  a.st = tstack_;
   a.nlayers = c.num_temporal_layers;
   a.cross = 1;
   a.D = c.d_model;
@@ -473,7 +480,7 @@ void State::launch_temporal_p(const void* in_pairs, int f, void* out_pairs) {
   a.out = out_pairs;
   a.S = S;
   a.ll = ll_bufs();
-  launch_step(m.dt, a, persist_grid_, stream);
+  launch_step(m.dt, a, persist_grid_, lds_t_, stream);
 }
 
 void State::launch_depth_p(const void* in_pairs, int l, const void* head_w, int head_rows, float* logits,
@@ -481,7 +488,7 @@ void State::launch_depth_p(const void* in_pairs, int l, const void* head_w, int 
   const Config& c = m.cfg;
   StepArgs a{};
   if (d_trace_ && frame == 1 && level == 1) a.trace = d_trace_ + kTraceSlots;
-  a.layers = static_cast<const LayerDev*>(dep_layers_);
+  a.st = dstack_;
   a.nlayers = c.num_depth_layers;
   a.cross = 0;
   a.D = c.d_model;
@@ -516,7 +523,7 @@ void State::launch_depth_p(const void* in_pairs, int l, const void* head_w, int 
     a.fmean = p_tin;
   }
   a.ll = ll_bufs();
-  launch_step(m.dt, a, persist_grid_, stream);
+  launch_step(m.dt, a, persist_grid_, lds_d_, stream);
 }
 
 void State::enqueue_decode_p(const GenOpts& o) {

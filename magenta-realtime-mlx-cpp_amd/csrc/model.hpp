@@ -156,8 +156,8 @@ class State {
   size_t ll_words_ = 0;
   LLBufs ll_bufs() const;
   void reset_handoff();
-  void* tmp_layers_ = nullptr;  // LayerDev[num_temporal_layers]
-  void* dep_layers_ = nullptr;  // LayerDev[num_depth_layers]
+  DecStack tstack_{}, dstack_{};  // temporal / depth stacks with this state's caches
+  size_t lds_t_ = 0, lds_d_ = 0;   // dynamic LDS of the step kernels
   int* h_err_ = nullptr;        // pinned
   uint64_t* d_trace_ = nullptr; // 2 x kTraceSlots when MRT_TRACE_PHASES is set
   void print_trace();

@@ -10,24 +10,25 @@ namespace mrt {
 
 constexpr int kPersistThreads = 256;
 constexpr int kMaxPersistK = 3072;  // largest GEMV input (d_model, heads*64, d_ff)
-constexpr int kMaxPersistLen = 64;  // self-attention keys handled by the fused path
+constexpr int kMaxPersistLen = 64;  // self-attention ring slots handled by the fused path
 constexpr int kMaxBph = 16;         // workgroups per head
+constexpr int kMaxCrossChunk = 64;  // encoder keys per workgroup in cross attention
 
-// Per-layer device pointers (weights of the model + this state's caches).
-struct LayerDev {
-  const void* norm_sa;
-  const void* wqkv;
-  const void* wo;
-  const void* norm_ca;
-  const void* wq_c;
-  const void* wo_c;
-  const void* norm_ff;
-  const void* w01;
-  const void* wo2;
-  const void* ck;  // cross K (rows, H, S, 64)
-  const void* cv;
-  void* kc;        // self K ring (rows, H, Lmax, 64)
-  void* vc;
+// One decoder stack (temporal or depth) laid out per weight kind: layer i of
+// a kind starts at base + i * (elements of one layer), so every address is a
+// scalar function of kernel arguments.
+struct DecStack {
+  const void* norm_sa;  // (L, D)
+  const void* wqkv;     // (L, 3 HD, D): q | k | v rows
+  const void* wo;       // (L, D, HD)
+  const void* norm_ca;  // (L, D)       temporal only
+  const void* wq_c;     // (L, HD, D)   temporal only
+  const void* wo_c;     // (L, D, HD)   temporal only
+  const void* norm_ff;  // (L, D)
+  const void* w01;      // (L, 2 F, D): 32-row groups [gate 32 | up 32]
+  const void* wo2;      // (L, D, F)
+  const void* cross;    // cross K/V: layer i K at 2i*n, V at (2i+1)*n, n = 2*H*S*64
+  void* ring;           // self K/V ring: layer i K at 2i*m, V at (2i+1)*m, m = 2*H*Lmax*64
 };
 
 // Hand-off buffers of one state: 64-bit words {payload (low 32), tag (high
@@ -48,7 +49,7 @@ struct LLBufs {
 constexpr size_t kLLVecWords = 2 * kMaxPersistK;
 
 struct StepArgs {
-  const LayerDev* layers;
+  DecStack st;
   int nlayers;
   int cross;   // temporal step (has cross attention)
   int D, HD, H, F, bph;
@@ -76,7 +77,7 @@ struct StepArgs {
   void* fmean;     // (D) pairs: frame mean (next temporal input)
   float* rec_slice;  // optional copy of the logits
   LLBufs ll;
-  // Optional phase timeline (100 MHz wall clock) recorded by workgroup 0.
+  // Optional timeline (100 MHz wall clock) recorded by workgroup 0.
   uint64_t* trace;
 };
 constexpr int kTraceSlots = 512;
@@ -88,7 +89,11 @@ constexpr int kTraceDone = kTraceSlots - 1;
 // device (H * blocks-per-head, bph a power of two in [8, 16]); 0 if unsupported.
 int persist_grid(int H, int num_cu, int* bph);
 
-void launch_step(DType dt, const StepArgs& a, int grid, hipStream_t s);
+// Dynamic LDS bytes of a step kernel, after allowing the kernel to use them;
+// 0 if the device cannot give one workgroup that much.
+size_t persist_prepare(DType dt, bool cross, int device);
+
+void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t s);
 
 // (rows=2, D) model-dtype rows <-> (D) pairs.
 void rows_to_pairs(DType dt, const void* rows, int D, void* pairs, hipStream_t s);

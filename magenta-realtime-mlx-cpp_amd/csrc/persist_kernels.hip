@@ -4,26 +4,37 @@
 //
 // Grid = H * bph workgroups (one per CU: 256 on MI355X), 4 waves each.  The
 // phases of a step hand data to each other through 64-bit words {payload,
-// tag} written and read with agent-scope (sc1) atomics, which are coherent
-// across the 8 XCDs without cache maintenance.  A consumer polls the words it
-// needs until each carries the tag of the producing phase of this launch
-// (tag = launch epoch << 10 | phase code), so a hand-off costs one store ->
-// load propagation and needs no counters, barriers or store drains.  The
-// epoch is a device counter that workgroup 0 advances once it has seen data
-// from every workgroup, so graph replays never match stale words.
+// tag} written and read with agent-scope atomics, which are coherent across
+// the 8 XCDs without cache maintenance.  A consumer polls the words it needs
+// until each carries the tag of the producing phase of this launch (tag =
+// launch epoch << 10 | phase code), so a hand-off costs one store -> load
+// propagation and needs no counters, barriers or store drains.  The epoch is
+// a device counter that workgroup 0 advances once it has seen data from every
+// workgroup, so graph replays never match stale words.
 //
 // Every buffer is rewritten only after all of its readers have consumed it:
 // each phase's inputs depend on outputs of every workgroup of the previous
 // phase, which those workgroups produce only after finishing their reads.
 //
-// Weights are read exactly once with 16-byte non-temporal loads issued as
-// soon as the previous phase's outputs are stored, so their HBM latency
-// overlaps the wait for the next phase's inputs.
+// Latency hiding:
+//   * weights of the next phase are loaded into registers (16-byte loads)
+//     as soon as the current phase's outputs are stored, so HBM latency
+//     overlaps the wait for the next phase's inputs;
+//   * every weight, norm and cache address is a scalar function of the kernel
+//     arguments (stacked per-kind layer layout), so no load waits on a
+//     pointer fetched from memory;
+//   * the self-attention ring history and the cross-attention K/V block of a
+//     layer are copied global -> LDS with direct (register-less) 16-byte
+//     loads at the start of the layer, long before they are read;
+//   * cross-lane sums and maxima use DPP row operations, top-k counting uses
+//     wave ballots.
+// Temporal weights (streamed once per frame) use non-temporal loads so that
+// they do not displace the depth stack, which every depth step re-reads,
+// from the last-level cache.
 //
 // Work split per phase (H=16, bph=16, G=256):
-//   QKV:   workgroup (h, j) owns rows 4j..4j+3 of head h's q, k and v
-//          (3 rows per wave); workgroup (h, 0) then runs head h's attention
-//          over the ring (<= 64 keys).
+//   QKV:   workgroup (h, j) owns rows 4j..4j+3 of head h's q, k and v;
+//          workgroup (h, 0) then runs head h's attention over the ring.
 //   O / FFN-down / cross-O / head: ceil(N / G) rows per workgroup.
 //   FFN-up: ceil(d_ff / G) gate/up row pairs per workgroup.
 //   cross:  workgroup (h, j) owns head h's q rows 4j.., then computes the
@@ -35,6 +46,7 @@
 #include "persist.hpp"
 
 #define MRT_GLOBAL __attribute__((address_space(1)))
+#define MRT_LDS __attribute__((address_space(3)))
 
 namespace mrt {
 namespace {
@@ -54,6 +66,22 @@ __device__ __forceinline__ void st_g(T* p, T v) {
   *(MRT_GLOBAL T*)(p) = v;
 }
 
+// 16-byte weight load: non-temporal for the temporal stack.
+template <bool NT>
+__device__ __forceinline__ uint4 ld_w16(const void* p) {
+  if constexpr (NT)
+    return ld_nt16(p);
+  else
+    return ld_g16(p);
+}
+
+// Direct global -> LDS copy: lane l's 16 bytes from `g` land at lds + 16 l.
+__device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)g, (MRT_LDS void*)lds, 16, 0, 0);
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 __device__ __forceinline__ bool spin_failed(uint32_t& spins, int* err) {
   if ((++spins & 255u) == 0) {
     if (aload(err) != 0 || spins > kSpinLimit) {
@@ -62,6 +90,44 @@ __device__ __forceinline__ bool spin_failed(uint32_t& spins, int* err) {
     }
   }
   return false;
+}
+
+// ---- DPP wave reductions (all 64 lanes active; result is wave-uniform) -----------
+
+__device__ __forceinline__ float dpp_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, true));   // quad [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, true));   // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, true));  // row_shr:4
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, true));  // row_shr:8
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x142, 0xa, 0xf, true));  // row_bcast:15
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x143, 0xc, 0xf, true));  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float dpp_max(float v) {
+  const int ninf = __float_as_int(-INFINITY);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0xB1, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x4E, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x114, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x118, 0xf, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x142, 0xa, 0xf, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(ninf, __float_as_int(v), 0x143, 0xc, 0xf, false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ int dpp_min_i(int v) {
+  const int big = 0x7fffffff;
+  v = min(v, __builtin_amdgcn_update_dpp(big, v, 0xB1, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(big, v, 0x4E, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(big, v, 0x114, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(big, v, 0x118, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(big, v, 0x142, 0xa, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(big, v, 0x143, 0xc, 0xf, false));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
 // Plain (rows 0/1) pair of one element: bf16 -> 32 bits, fp32 -> 64 bits.
@@ -126,13 +192,27 @@ struct Side {
   int row;  // -1: nothing for this thread
 };
 
+// Activation rows in LDS, stored in the model dtype (row 1 at +kMaxPersistK
+// elements): bf16 rows feed v_dot2c_f32_bf16 directly.
+template <typename T>
+struct Act {
+  __device__ static void put(float* xs, int k, float v0, float v1) {
+    T* x = reinterpret_cast<T*>(xs);
+    x[k] = St<T>::st(v0);
+    x[kMaxPersistK + k] = St<T>::st(v1);
+  }
+  __device__ static float get(const float* xs, int r, int k) {
+    return St<T>::ld(reinterpret_cast<const T*>(xs)[r * kMaxPersistK + k]);
+  }
+};
+
 // Polls elements k = tid + 256 i (k < K) of a tagged vector until each word
-// carries `tag` and stores both rows to xs[k], xs[kMaxPersistK + k]; the
+// carries `tag` and stores both rows to activation element k; the
 // side element (if any) is returned in r0/r1.  All loads of one round are
 // issued before any is waited for.
 template <typename T>
-__device__ void ll_load_vec(const uint64_t* src, int K, uint32_t tag, float* xs, const Side& sd, float& r0,
-                            float& r1, int* err) {
+__device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t tag, float* xs, const Side& sd,
+                                            float& r0, float& r1, int* err) {
   using PT = PairT<T>;
   constexpr int kPer = kMaxPersistK / kPersistThreads;
   constexpr int NW = LL<T>::kWords;
@@ -166,9 +246,7 @@ __device__ void ll_load_vec(const uint64_t* src, int K, uint32_t tag, float* xs,
 #pragma unroll
         for (int r = 0; r < NW; ++r) ok = ok && ll_tag(w[i][r]) == tag;
         if (ok) {
-          const int k = tid + i * kPersistThreads;
-          xs[k] = LL<T>::get(w[i], 0);
-          xs[kMaxPersistK + k] = LL<T>::get(w[i], 1);
+          Act<T>::put(xs, tid + i * kPersistThreads, LL<T>::get(w[i], 0), LL<T>::get(w[i], 1));
           pend &= ~(1u << i);
         }
       }
@@ -189,85 +267,89 @@ __device__ void ll_load_vec(const uint64_t* src, int K, uint32_t tag, float* xs,
   }
 }
 
-// RMS normalisation of both rows in xs with weight g (modules.cpp:72-84).
-template <typename T>
-__device__ void norm_rows(int K, const T* g, float eps, float* xs, float* red) {
-  using S = St<T>;
-  float s0 = 0.f, s1 = 0.f;
-  for (int k = threadIdx.x; k < K; k += kPersistThreads) {
-    s0 = fmaf(xs[k], xs[k], s0);
-    s1 = fmaf(xs[kMaxPersistK + k], xs[kMaxPersistK + k], s1);
-  }
-  s0 = wave_sum(s0);
-  s1 = wave_sum(s1);
-  const int wid = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    red[wid] = s0;
-    red[4 + wid] = s1;
-  }
-  __syncthreads();
-  const float inv0 = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + eps);
-  const float inv1 = 1.0f / sqrtf((red[4] + red[5] + red[6] + red[7]) / (float)K + eps);
-  for (int k = threadIdx.x; k < K; k += kPersistThreads) {
-    const float gk = S::ld(ld_g(g + k));
-    xs[k] = S::rnd(S::rnd(xs[k] * inv0) * gk);
-    xs[kMaxPersistK + k] = S::rnd(S::rnd(xs[kMaxPersistK + k] * inv1) * gk);
-  }
+__device__ __forceinline__ void trace_point(uint64_t* trace, int slot) {
+  if (trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0 && slot < kTraceStart) trace[slot] = wall_clock64();
 }
 
 // Loads the activation vector of a phase into xs (tagged, or the launch's
-// plain input pairs), with an optional side element and RMS norm.
-__device__ __forceinline__ void trace_point(uint64_t* trace, int slot);
-
+// plain input pairs), with an optional side element and RMS norm with the
+// LDS-staged weight g (modules.cpp:72-84; normed vectors have K <= 1024).
 template <typename T>
-__device__ void load_act(const uint64_t* ll, const void* plain, int K, uint32_t tag, const T* g, float* xs,
-                         float* red, const Side& sd, float& r0, float& r1, int* err, uint64_t* trace = nullptr,
-                         int* tp = nullptr) {
+__device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, int K, uint32_t tag, const T* g,
+                                         float* xs, float* red, const Side& sd, float& r0, float& r1, int* err,
+                                         uint64_t* trace, int& tp) {
   using PT = PairT<T>;
-  if (tp) trace_point(trace, (*tp)++);
+  using S = St<T>;
+  constexpr int kPer = kMaxPersistK / kPersistThreads;
+  constexpr int kG = 1024 / kPersistThreads;
+  const int tid = threadIdx.x;
+  trace_point(trace, tp++);
   if (plain != nullptr) {
-    constexpr int kPer = kMaxPersistK / kPersistThreads;
     typename PT::W w[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int k = threadIdx.x + i * kPersistThreads;
+      const int k = tid + i * kPersistThreads;
       if (k < K) w[i] = ld_g(static_cast<const typename PT::W*>(plain) + k);
     }
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int k = threadIdx.x + i * kPersistThreads;
-      if (k < K) {
-        xs[k] = PT::lo(w[i]);
-        xs[kMaxPersistK + k] = PT::hi(w[i]);
-      }
+      const int k = tid + i * kPersistThreads;
+      if (k < K) Act<T>::put(xs, k, PT::lo(w[i]), PT::hi(w[i]));
     }
     ll_load_vec<T>(nullptr, 0, 0, xs, sd, r0, r1, err);
   } else {
     ll_load_vec<T>(ll, K, tag, xs, sd, r0, r1, err);
   }
-  if (tp) trace_point(trace, (*tp)++);
-  __syncthreads();
+  __builtin_amdgcn_s_waitcnt(0);  // LDS copies issued by this wave (norm weights) have landed
+  trace_point(trace, tp++);
   if (g != nullptr) {
-    norm_rows<T>(K, g, 1e-6f, xs, red);
+    // Each thread squares the elements it wrote itself: no barrier needed yet.
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < kG; ++i) {
+      const int k = tid + i * kPersistThreads;
+      if (k < K) {
+        const float x0 = Act<T>::get(xs, 0, k), x1 = Act<T>::get(xs, 1, k);
+        s0 = fmaf(x0, x0, s0);
+        s1 = fmaf(x1, x1, s1);
+      }
+    }
+    s0 = dpp_sum(s0);
+    s1 = dpp_sum(s1);
+    const int wid = tid >> 6;
+    if ((tid & 63) == 0) {
+      red[wid] = s0;
+      red[4 + wid] = s1;
+    }
     __syncthreads();
+    const float inv0 = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + 1e-6f);
+    const float inv1 = 1.0f / sqrtf((red[4] + red[5] + red[6] + red[7]) / (float)K + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < kG; ++i) {
+      const int k = tid + i * kPersistThreads;
+      if (k < K) {
+        const float gk = S::ld(g[k]);
+        Act<T>::put(xs, k, S::rnd(S::rnd(Act<T>::get(xs, 0, k) * inv0) * gk),
+                    S::rnd(S::rnd(Act<T>::get(xs, 1, k) * inv1) * gk));
+      }
+    }
   }
-  if (tp) trace_point(trace, (*tp)++);
+  __syncthreads();
+  trace_point(trace, tp++);
 }
 
 // ---- GEMV machinery ---------------------------------------------------------------
 
-template <typename T>
-constexpr int nbuf() {
-  return 6 * ((1024 + St<T>::kVec * 64 - 1) / (St<T>::kVec * 64));  // 6 rows of K <= 1024
-}
+constexpr int kNBuf = 12;  // 16-byte weight registers per thread
 
-// Loads the rows of one batch (R rows of P parts) into registers.
-template <typename T, int NV, int P, class RowOf>
-__device__ __forceinline__ void fetch_batch(uint4 (&buf)[nbuf<T>()], const T* W, int K, int b0, int nb,
-                                            RowOf row_of) {
+// Loads the rows of one batch (R rows of P parts; row indices wave-uniform)
+// into registers; 16-byte chunks past the end of a row are zero.
+template <typename T, int NV, int P, bool NT, class RowOf>
+__device__ __forceinline__ void fetch_batch(uint4 (&buf)[kNBuf], const T* W, int K, int b0, int nb, RowOf row_of) {
   constexpr int V = St<T>::kVec;
-  constexpr int R = nbuf<T>() / (P * NV);
+  constexpr int R = kNBuf / (P * NV);
   const int lane = threadIdx.x & 63;
+  const int nch = K / V;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (r < nb) {
@@ -277,21 +359,50 @@ __device__ __forceinline__ void fetch_batch(uint4 (&buf)[nbuf<T>()], const T* W,
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
           const int c = lane + 64 * i;
-          if (c * V < K) buf[(r * P + p) * NV + i] = ld_nt16(row + (size_t)c * V);
+          uint4 v = make_uint4(0u, 0u, 0u, 0u);
+          if (c < nch) v = ld_w16<NT>(row + (size_t)c * V);
+          buf[(r * P + p) * NV + i] = v;
         }
       }
     }
   }
 }
 
-// Dots of a batch against the two activation rows xs[0..K), xs[kMax..kMax+K),
-// reduced across the wave; epi(index, acc[P][2]) runs on every lane.
+// acc += w . x over one 16-byte chunk (8 bf16 or 4 fp32 elements).
+template <typename T>
+struct Dot;
+template <>
+struct Dot<bf16> {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  __device__ static float d2(uint32_t w, uint32_t x, float a) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, w), __builtin_bit_cast(bf2, x), a, false);
+  }
+  __device__ static float acc(float a, const uint4& w, const uint4& x) {
+    a = d2(w.x, x.x, a);
+    a = d2(w.y, x.y, a);
+    a = d2(w.z, x.z, a);
+    return d2(w.w, x.w, a);
+  }
+};
+template <>
+struct Dot<float> {
+  __device__ static float acc(float a, const uint4& w, const uint4& x) {
+    a = fmaf(__uint_as_float(w.x), __uint_as_float(x.x), a);
+    a = fmaf(__uint_as_float(w.y), __uint_as_float(x.y), a);
+    a = fmaf(__uint_as_float(w.z), __uint_as_float(x.z), a);
+    return fmaf(__uint_as_float(w.w), __uint_as_float(x.w), a);
+  }
+};
+
+// Dots of a batch against the two activation rows (model dtype in LDS; the
+// buffer is zero past every row's end, so zero weight chunks meet finite
+// activations); epi(index, sums[P][2]) runs on every lane with wave-uniform sums.
 template <typename T, int NV, int P, class Epi>
-__device__ __forceinline__ void dot_batch(const uint4 (&buf)[nbuf<T>()], int K, int b0, int nb, const float* xs,
-                                          Epi epi) {
+__device__ __forceinline__ void dot_batch(const uint4 (&buf)[kNBuf], int b0, int nb, const float* xs, Epi epi) {
   constexpr int V = St<T>::kVec;
-  constexpr int R = nbuf<T>() / (P * NV);
+  constexpr int R = kNBuf / (P * NV);
   const int lane = threadIdx.x & 63;
+  const T* xt = reinterpret_cast<const T*>(xs);
   float acc[R][P][2];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -300,20 +411,16 @@ __device__ __forceinline__ void dot_batch(const uint4 (&buf)[nbuf<T>()], int K, 
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int c = lane + 64 * i;
-    if (c * V < K) {
+    const uint4 x0 = *reinterpret_cast<const uint4*>(xt + c * V);
+    const uint4 x1 = *reinterpret_cast<const uint4*>(xt + kMaxPersistK + c * V);
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        const float x0 = xs[c * V + e], x1 = xs[kMaxPersistK + c * V + e];
+    for (int r = 0; r < R; ++r) {
+      if (r < nb) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          if (r < nb) {
-#pragma unroll
-            for (int p = 0; p < P; ++p) {
-              const float w = St<T>::ld(reinterpret_cast<const T*>(&buf[(r * P + p) * NV + i])[e]);
-              acc[r][p][0] = fmaf(w, x0, acc[r][p][0]);
-              acc[r][p][1] = fmaf(w, x1, acc[r][p][1]);
-            }
-          }
+        for (int p = 0; p < P; ++p) {
+          const uint4& w = buf[(r * P + p) * NV + i];
+          acc[r][p][0] = Dot<T>::acc(acc[r][p][0], w, x0);
+          acc[r][p][1] = Dot<T>::acc(acc[r][p][1], w, x1);
         }
       }
     }
@@ -321,25 +428,26 @@ __device__ __forceinline__ void dot_batch(const uint4 (&buf)[nbuf<T>()], int K, 
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (r < nb) {
+      float s[P][2];
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        acc[r][p][0] = wave_sum(acc[r][p][0]);
-        acc[r][p][1] = wave_sum(acc[r][p][1]);
+        s[p][0] = dpp_sum(acc[r][p][0]);
+        s[p][1] = dpp_sum(acc[r][p][1]);
       }
-      epi(b0 + r, acc[r]);
+      epi(b0 + r, s);
     }
   }
 }
 
 // Runs a wave's nw rows in batches; the first batch is already in buf.
-template <typename T, int NV, int P, class RowOf, class Epi>
-__device__ __forceinline__ void gemv_rows(uint4 (&buf)[nbuf<T>()], const T* W, int K, int nw, RowOf row_of,
+template <typename T, int NV, int P, bool NT, class RowOf, class Epi>
+__device__ __forceinline__ void gemv_rows(uint4 (&buf)[kNBuf], const T* W, int K, int nw, RowOf row_of,
                                           const float* xs, Epi epi) {
-  constexpr int R = nbuf<T>() / (P * NV);
+  constexpr int R = kNBuf / (P * NV);
   for (int b0 = 0; b0 < nw; b0 += R) {
     const int nb = min(R, nw - b0);
-    if (b0 > 0) fetch_batch<T, NV, P>(buf, W, K, b0, nb, row_of);
-    dot_batch<T, NV, P>(buf, K, b0, nb, xs, epi);
+    if (b0 > 0) fetch_batch<T, NV, P, NT>(buf, W, K, b0, nb, row_of);
+    dot_batch<T, NV, P>(buf, b0, nb, xs, epi);
   }
 }
 
@@ -359,7 +467,8 @@ __device__ __forceinline__ int geglu_row(int j, int p) { return (j >> 5) * 64 + 
 
 // Polls `n` (<= 256) tagged elements src[i] into LDS floats dst0[i], dst1[i].
 template <typename T>
-__device__ void ll_load_small(const uint64_t* src, int n, uint32_t tag, float* dst0, float* dst1, int* err) {
+__device__ __forceinline__ void ll_load_small(const uint64_t* src, int n, uint32_t tag, float* dst0, float* dst1,
+                                              int* err) {
   constexpr int NW = LL<T>::kWords;
   const int tid = threadIdx.x;
   if (tid >= n) return;
@@ -378,21 +487,39 @@ __device__ void ll_load_small(const uint64_t* src, int n, uint32_t tag, float* d
   dst1[tid] = LL<T>::get(w, 1);
 }
 
+// ---- attention ------------------------------------------------------------------
+
+// LDS staging of one layer's attention operands, raw model dtype:
+// region (kind, row) = 64 slots x 64 elements, kind 0 = K, 1 = V.
+constexpr int kRegion = 64 * 64;
+
+// Copies `n` (<= 64) consecutive 64-element slots starting at `src` into an
+// LDS region with the calling wave; `lim` bytes from src are readable.
+template <typename T>
+__device__ __forceinline__ void stage_slots(const T* src, int n, long lim, T* region) {
+  const int lane = threadIdx.x & 63;
+  const int bytes = n * 64 * (int)sizeof(T);
+  for (int off = 0; off < bytes; off += 1024) {
+    const long o = min((long)(off + lane * 16), lim - 16);
+    lds_copy16(reinterpret_cast<const char*>(src) + o, reinterpret_cast<char*>(region) + off);
+  }
+}
+
 // Self attention of head h over ring slots 0..pos (scale 1.0, bias
 // table[bucket[pos - j], h]; modules.cpp:243-295).  Slots before pos were
-// written by earlier launches (plain loads); q and slot pos come as tagged
-// words of this launch.
+// staged into `hist` from earlier launches' ring writes; q and slot pos come
+// as tagged words of this launch.
 template <typename T>
-__device__ void self_attention_head(const StepArgs& a, const LayerDev& L, int h, uint32_t tag, uint32_t out_tag,
-                                    float* sm) {
+__device__ __forceinline__ void self_attention_head(const StepArgs& a, int h, uint32_t tag, uint32_t out_tag,
+                                                    const T* hist, float* sm) {
   using S = St<T>;
   constexpr int V = S::kVec;
   float* qs = sm;        // [2][64]
-  float* ks = sm + 128;  // [2][64]  slot pos, then the output
+  float* ks = sm + 128;  // [2][64]  slot pos
   float* vs = sm + 256;  // [2][64]  slot pos
   float* ps = sm + 384;  // [2][64]
-  __shared__ float sl[2];
-  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  float* os = sm + 512;  // [2][64]
+  const int tid = threadIdx.x, wid = uniform(tid >> 6), lane = tid & 63;
   if (wid < 3) {  // waves 0, 1, 2 fetch q, k, v of head h
     const uint64_t* src = (wid == 0 ? a.ll.q : wid == 1 ? a.ll.k : a.ll.v) + h * 64;
     float* d = sm + wid * 128;
@@ -411,112 +538,89 @@ __device__ void self_attention_head(const StepArgs& a, const LayerDev& L, int h,
     d[lane] = LL<T>::get(w, 0);
     d[64 + lane] = LL<T>::get(w, 1);
   }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's history copies have landed
   __syncthreads();
-  const int len = a.pos + 1;
-  float o = 0.f;
+  const int pos = a.pos, len = pos + 1;
   if (wid < 2) {
     const int b = wid;
-    const T* Kp = static_cast<const T*>(L.kc) + ((size_t)(b * a.H + h) * a.Lmax) * 64;
     float sc = -INFINITY;
-    if (lane < a.pos) {
-      const T* kr = Kp + (size_t)lane * 64;
-      uint4 kv[64 / V];
-#pragma unroll
-      for (int i = 0; i < 64 / V; ++i) kv[i] = ld_g16(kr + i * V);
+    if (lane < pos) {
+      const T* kr = hist + b * kRegion + lane * 64;
       float acc = 0.f;
 #pragma unroll
       for (int i = 0; i < 64 / V; ++i) {
-        const T* ke = reinterpret_cast<const T*>(&kv[i]);
+        const uint4 kv = *reinterpret_cast<const uint4*>(kr + i * V);
+        const T* ke = reinterpret_cast<const T*>(&kv);
 #pragma unroll
         for (int e = 0; e < V; ++e) acc = fmaf(qs[b * 64 + i * V + e], S::ld(ke[e]), acc);
       }
       sc = acc;
-    } else if (lane == a.pos) {
+    } else if (lane == pos) {
       float acc = 0.f;
 #pragma unroll 16
       for (int d = 0; d < 64; ++d) acc = fmaf(qs[b * 64 + d], ks[b * 64 + d], acc);
       sc = acc;
     }
-    if (lane < len) sc += S::ld(ld_g(static_cast<const T*>(a.bias_tab) + ld_g(a.buckets + a.pos - lane) * a.H + h));
-    const float m = wave_max(sc);
+    if (lane < len) sc += S::ld(ld_g(static_cast<const T*>(a.bias_tab) + ld_g(a.buckets + pos - lane) * a.H + h));
+    const float m = dpp_max(sc);
     const float p = lane < len ? expf(sc - m) : 0.f;
-    const float l = wave_sum(p);
+    const float l = dpp_sum(p);
     ps[b * 64 + lane] = p;
-    if (lane == 0) sl[b] = l;
+    // the same wave reads ps back: LDS operations of a wave complete in order
+    const T* vr = hist + (2 + b) * kRegion + lane;
+    float o = ps[b * 64 + pos] * vs[b * 64 + lane];
+    for (int j = 0; j < pos; ++j) o = fmaf(ps[b * 64 + j], S::ld(vr[j * 64]), o);
+    os[b * 64 + lane] = o / l;
   }
   __syncthreads();
-  if (wid < 2) {
-    const int b = wid;
-    const T* Vp = static_cast<const T*>(L.vc) + ((size_t)(b * a.H + h) * a.Lmax) * 64 + lane;
-    float vv[kMaxPersistLen];
-#pragma unroll
-    for (int j = 0; j < kMaxPersistLen; ++j)
-      if (j < a.pos) vv[j] = S::ld(ld_g(Vp + (size_t)j * 64));
-    o = ps[b * 64 + a.pos] * vs[b * 64 + lane];
-#pragma unroll
-    for (int j = 0; j < kMaxPersistLen; ++j)
-      if (j < a.pos) o = fmaf(ps[b * 64 + j], vv[j], o);
-    o = o / sl[b];
-  }
-  __syncthreads();  // every read of ks is done before it is reused
-  if (wid < 2) ks[wid * 64 + lane] = o;
-  __syncthreads();
-  if (tid < 64) LL<T>::put(a.ll.at, h * 64 + tid, ks[tid], ks[64 + tid], out_tag);
+  if (tid < 64) LL<T>::put(a.ll.at, h * 64 + tid, os[tid], os[64 + tid], out_tag);
 }
 
-// Softmax partial of cross attention: head h, key block j, both rows; the
-// cross K/V were written by the encoder launch (plain loads).
+// Softmax partial of cross attention: head h, key block j (staged in `cst`),
+// both rows.  Waves 2b, 2b+1 take the two halves of row b's keys.
 template <typename T>
-__device__ void cross_partial(const StepArgs& a, const LayerDev& L, int h, int j, uint32_t q_tag, uint32_t out_tag,
-                              float* sm) {
+__device__ __forceinline__ void cross_partial(const StepArgs& a, int h, int j, uint32_t q_tag, uint32_t out_tag,
+                                              const T* cst, float* sm) {
   using S = St<T>;
   constexpr int V = S::kVec;
   float* qs = sm;        // [2][64]
   float* ps = sm + 128;  // [4][64]
   float* wo = sm + 384;  // [4][64]
-  __shared__ float wm[4], wl[4];
-  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  float* wm = sm + 640;  // [4]
+  float* wl = sm + 644;  // [4]
+  const int tid = threadIdx.x, wid = uniform(tid >> 6), lane = tid & 63;
   ll_load_small<T>(a.ll.q + h * 64, 64, q_tag, qs, qs + 64, a.ll.err);
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's K/V copies have landed
   __syncthreads();
   const int chunk = (a.S + a.bph - 1) / a.bph;
-  const int half = (chunk + 1) / 2;
-  const int b = wid >> 1;
-  const int kb = j * chunk + (wid & 1) * half;
-  const int ke = min(min(a.S, j * chunk + chunk), kb + half);
-  const int nk = max(0, ke - kb);
-  const T* Kp = static_cast<const T*>(L.ck) + ((size_t)(b * a.H + h) * a.S) * 64;
-  const T* Vp = static_cast<const T*>(L.cv) + ((size_t)(b * a.H + h) * a.S) * 64;
+  const int nk = max(0, min(chunk, a.S - j * chunk));
+  const int h0 = (nk + 1) / 2;
+  const int b = wid >> 1, half = wid & 1;
+  const int klo = half ? h0 : 0;
+  const int nkh = half ? nk - h0 : h0;
   float sc = -INFINITY;
-  if (lane < nk) {
-    const T* kr = Kp + (size_t)(kb + lane) * 64;
-    uint4 kv[64 / V];
-#pragma unroll
-    for (int i = 0; i < 64 / V; ++i) kv[i] = ld_nt16(kr + i * V);
+  if (lane < nkh) {
+    const T* kr = cst + b * kRegion + (klo + lane) * 64;
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 64 / V; ++i) {
-      const T* ke_ = reinterpret_cast<const T*>(&kv[i]);
+      const uint4 kv = *reinterpret_cast<const uint4*>(kr + i * V);
+      const T* ke = reinterpret_cast<const T*>(&kv);
 #pragma unroll
-      for (int e = 0; e < V; ++e) acc = fmaf(qs[b * 64 + i * V + e], S::ld(ke_[e]), acc);
+      for (int e = 0; e < V; ++e) acc = fmaf(qs[b * 64 + i * V + e], S::ld(ke[e]), acc);
     }
     sc = acc;
   }
-  const float m = wave_max(sc);
-  const float p = (lane < nk) ? expf(sc - m) : 0.f;
-  const float l = wave_sum(p);
+  const float m = dpp_max(sc);
+  const float p = (lane < nkh) ? expf(sc - m) : 0.f;
+  const float l = dpp_sum(p);
   ps[wid * 64 + lane] = p;
-  __syncthreads();
-  float vv[64];
-#pragma unroll
-  for (int t = 0; t < 64; ++t)
-    if (t < nk) vv[t] = S::ld(ld_g(Vp + (size_t)(kb + t) * 64 + lane));
+  const T* vr = cst + (2 + b) * kRegion + klo * 64 + lane;
   float o = 0.f;
-#pragma unroll
-  for (int t = 0; t < 64; ++t)
-    if (t < nk) o = fmaf(ps[wid * 64 + t], vv[t], o);
+  for (int t = 0; t < nkh; ++t) o = fmaf(ps[wid * 64 + t], S::ld(vr[t * 64]), o);
   wo[wid * 64 + lane] = o;
   if (lane == 0) {
-    wm[wid] = nk > 0 ? m : -INFINITY;
+    wm[wid] = nkh > 0 ? m : -INFINITY;
     wl[wid] = l;
   }
   __syncthreads();
@@ -538,7 +642,7 @@ __device__ void cross_partial(const StepArgs& a, const LayerDev& L, int h, int j
 
 // Combines the bph partials of head h into its attention output.
 template <typename T>
-__device__ void cross_combine(const StepArgs& a, int h, uint32_t tag, uint32_t out_tag, float* sm) {
+__device__ __forceinline__ void cross_combine(const StepArgs& a, int h, uint32_t tag, uint32_t out_tag, float* sm) {
   float* os = sm;  // [2][64]
   const int tid = threadIdx.x;
   if (tid < 128) {
@@ -585,10 +689,12 @@ __device__ void cross_combine(const StepArgs& a, int h, uint32_t tag, uint32_t o
   if (tid < 64) LL<T>::put(a.ll.at, h * 64 + tid, os[tid], os[64 + tid], out_tag);
 }
 
+// ---- sampling -------------------------------------------------------------------
+
 // CFG + temperature/top-k Gumbel-max draw and token feedback (decode.cpp:
 // 71-148, 458-484), run by wave 0; `lg` holds the two logit rows in LDS.
 template <typename T>
-__device__ void sample_and_feed(const StepArgs& a, const float* lg) {
+__device__ __forceinline__ void sample_and_feed(const StepArgs& a, const float* lg) {
   using PT = PairT<T>;
   using W = typename PT::W;
   using S = St<T>;
@@ -596,6 +702,17 @@ __device__ void sample_and_feed(const StepArgs& a, const float* lg) {
   const int lane = threadIdx.x & 63;
   const SampleParams& p = a.sp;
   const int C = p.codebook;
+  // Loads that do not depend on the draw go first.
+  constexpr int kDPer = 1024 / 64;
+  const W* fs_in = static_cast<const W*>(a.fsum);
+  float fv[kDPer];
+#pragma unroll
+  for (int t = 0; t < kDPer; ++t) {
+    const int d = lane + 64 * t;
+    fv[t] = (a.level != 0 && d < a.D) ? PT::lo(ld_g(fs_in + d)) : 0.f;
+  }
+  const uint64_t seed = ld_g(p.seed);
+  const int teacher_id = a.teacher ? ld_g(a.teacher + a.slot) : 0;
   const float wc = 1.0f + p.guidance_weight, wu = p.guidance_weight;
   float v[kPer];
 #pragma unroll
@@ -608,6 +725,7 @@ __device__ void sample_and_feed(const StepArgs& a, const float* lg) {
     for (int t = 0; t < kPer; ++t)
       if (lane + 64 * t < C) v[t] = __fdiv_rn(v[t], p.temperature);
     if (p.top_k > 0 && p.top_k < C) {
+      // k-th largest key by a most-significant-bit-first search; counts by ballot.
       uint32_t key[kPer];
 #pragma unroll
       for (int t = 0; t < kPer; ++t) key[t] = (lane + 64 * t < C) ? float_key(v[t]) : 0u;
@@ -616,15 +734,14 @@ __device__ void sample_and_feed(const StepArgs& a, const float* lg) {
         const uint32_t cand = prefix | (1u << bit);
         int cnt = 0;
 #pragma unroll
-        for (int t = 0; t < kPer; ++t) cnt += key[t] >= cand ? 1 : 0;
-        if (wave_sum_i(cnt) >= p.top_k) prefix = cand;
+        for (int t = 0; t < kPer; ++t) cnt += __popcll(__ballot(key[t] >= cand));
+        if (cnt >= p.top_k) prefix = cand;
       }
       const float thr = key_float(prefix);
 #pragma unroll
       for (int t = 0; t < kPer; ++t)
         if (v[t] < thr) v[t] = -INFINITY;
     }
-    const uint64_t seed = ld_g(p.seed);
 #pragma unroll
     for (int t = 0; t < kPer; ++t) {
       const int c = lane + 64 * t;
@@ -641,34 +758,23 @@ __device__ void sample_and_feed(const StepArgs& a, const float* lg) {
       bi = c;
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(best, o, 64);
-    const int oi = __shfl_xor(bi, o, 64);
-    if (ov > best || (ov == best && oi < bi)) {
-      best = ov;
-      bi = oi;
-    }
-  }
-  const int drawn_id = p.codec_offset + a.level * C + bi;
-  const int fed = a.teacher ? ld_g(a.teacher + a.slot) : drawn_id;
+  // argmax, ties to the smallest index
+  const float mx = dpp_max(best);
+  const int arg = dpp_min_i(best == mx ? bi : 0x7fffffff);
+  const int drawn_id = p.codec_offset + a.level * C + arg;
+  const int fed = a.teacher ? teacher_id : drawn_id;
   if (lane == 0) {
     st_g(a.tokens + a.slot, fed);
     if (a.drawn) st_g(a.drawn + a.slot, drawn_id);
   }
   // Token feedback: both rows take emb(fed); the frame sum accumulates in the
   // model dtype; the last level's sum / L is the next temporal input.
-  constexpr int kDPer = 1024 / 64;
   const T* e = static_cast<const T*>(a.emb) + (size_t)fed * a.D;
-  const W* fs_in = static_cast<const W*>(a.fsum);
-  float ev[kDPer], fv[kDPer];
+  float ev[kDPer];
 #pragma unroll
   for (int t = 0; t < kDPer; ++t) {
     const int d = lane + 64 * t;
-    if (d < a.D) {
-      ev[t] = S::ld(ld_g(e + d));
-      fv[t] = a.level == 0 ? 0.f : PT::lo(ld_g(fs_in + d));
-    }
+    ev[t] = d < a.D ? S::ld(ld_g(e + d)) : 0.f;
   }
   const float Lf = S::rnd((float)p.rvq_depth);
   W* ni = static_cast<W*>(a.next_in);
@@ -689,36 +795,42 @@ __device__ void sample_and_feed(const StepArgs& a, const float* lg) {
   }
 }
 
-__device__ __forceinline__ void trace_point(uint64_t* trace, int slot) {
-  if (trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0 && slot < kTraceSlots) trace[slot] = wall_clock64();
-}
-
 // Phase codes of the tags (per layer: code = 16 * layer + phase).
 enum : int { kPhQKV = 0, kPhAtt = 1, kPhO = 2, kPhCQ = 3, kPhCP = 4, kPhCC = 5, kPhCO = 6, kPhUp = 7, kPhDn = 8 };
 constexpr int kPhHead = 1000;
 
 template <typename T, bool CROSS>
-__global__ __launch_bounds__(kPersistThreads) void k_step(StepArgs a) {
+__global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_step(StepArgs a) {
   using PT = PairT<T>;
   using W = typename PT::W;
   using S = St<T>;
   constexpr int V = S::kVec;
+  constexpr bool NT = CROSS;
   constexpr int NVD = (1024 + V * 64 - 1) / (V * 64);  // K <= 1024
   constexpr int NVF = 3 * NVD;                         // K <= 3072
   __shared__ float xs[2 * kMaxPersistK];
   __shared__ float red[8];
-  __shared__ float sm[640];
-  __shared__ float kvst[2][2][8];  // [k|v][row][d within this workgroup's slice]
+  __shared__ float sm[704];
+  __shared__ float kvst[2][2][16];  // [k|v][row][d within this workgroup's slice]
+  __shared__ __align__(16) T gam[4][1024];  // norm weights: self-attn, cross-attn, FFN, decoder_norm
+  extern __shared__ __align__(16) unsigned char dyn_lds[];
+  // [K|V][row] regions of 64 x 64: the ring history during self attention,
+  // then the layer's cross K/V block.
+  T* hist = reinterpret_cast<T*>(dyn_lds);
+  T* cst = hist;
 
-  if (aload(a.ll.err) != 0) return;  // a previous launch failed: do nothing
-  const uint32_t ep = aload(a.ll.seq);
-  auto tag = [&](int code) { return (ep << 10) | (uint32_t)code; };
-  const int G = gridDim.x, blk = blockIdx.x, wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int G = gridDim.x, blk = blockIdx.x;
+  const int wid = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int D = a.D, HD = a.HD, H = a.H, F = a.F, bph = a.bph;
   const int h = blk / bph, jpart = blk % bph, rps = 64 / bph;
-  uint4 buf[nbuf<T>()];
+  // Elements of one layer of each stacked kind.
+  const size_t eQKV = (size_t)3 * HD * D, eO = (size_t)D * HD, eQc = (size_t)HD * D, e01 = (size_t)2 * F * D,
+               eO2 = (size_t)D * F;
+  const size_t eRing = (size_t)2 * H * a.Lmax * 64, eCross = (size_t)2 * H * a.S * 64;
+  const T* wqkv0 = static_cast<const T*>(a.st.wqkv);
+  uint4 buf[kNBuf];
   int tp = 0;  // trace slot
-  trace_point(a.trace, kTraceStart);
+#define MRT_TP trace_point(a.trace, tp++)
 
   const RowSplit sD(D, G, blk), sF(F, G, blk);
   // QKV rows of this wave: local t = wid + 4i < 3*rps -> (segment t / rps, row t % rps).
@@ -731,6 +843,18 @@ __global__ __launch_bounds__(kPersistThreads) void k_step(StepArgs a) {
   auto cq_row = [&](int t, int) { return h * 64 + jpart * rps + wid + 4 * t; };
   auto rowD = [&](int t, int) { return sD.row(wid, t); };
   auto rowF = [&](int t, int p) { return geglu_row(sF.row(wid, t), p); };
+
+  // Layer 0's QKV weights first: they take longest to arrive.
+  if (a.nlayers > 0) fetch_batch<T, NVD, 1, NT>(buf, wqkv0, D, 0, min(kNBuf / NVD, nqkv), qkv_row);
+  // Activation elements past a vector's end meet zero weights: keep them finite.
+  for (int k = threadIdx.x; k < 2 * kMaxPersistK; k += kPersistThreads) xs[k] = 0.f;
+  __syncthreads();
+  if (aload(a.ll.err) != 0) return;  // a previous launch failed: do nothing
+  const uint32_t ep = aload(a.ll.seq);
+  auto tag = [&](int code) { return (ep << 10) | (uint32_t)code; };
+  if (a.trace != nullptr && blk == 0 && threadIdx.x == 0) a.trace[kTraceStart] = wall_clock64();
+  if (!CROSS && wid == 3) stage_slots<T>(static_cast<const T*>(a.dec_norm), D / 64, (long)D * sizeof(T), gam[3]);
+
   // residual element of the wave's D-row `lane` (lanes < nw)
   auto side_x = [&](const uint64_t* ll, const void* plain, uint32_t tg) {
     Side s{ll, plain, tg, lane < sD.nw(wid) ? sD.row(wid, lane) : -1};
@@ -738,37 +862,60 @@ __global__ __launch_bounds__(kPersistThreads) void k_step(StepArgs a) {
   };
   const Side no_side{nullptr, nullptr, 0u, -1};
   float r0 = 0.f, r1 = 0.f;
+  auto resid_put = [&](int t, const float (&s)[1][2], uint32_t tg) {
+    const float x0 = lane_value(r0, t), x1 = lane_value(r1, t);
+    if (lane == 0)
+      LL<T>::put(a.ll.x, sD.row(wid, t), S::rnd(x0 + S::rnd(s[0][0])), S::rnd(x1 + S::rnd(s[0][1])), tg);
+  };
 
   uint32_t x_tag = 0;  // tag of the current residual stream (layer >= 1)
-  if (a.nlayers > 0)
-    fetch_batch<T, NVD, 1>(buf, static_cast<const T*>(a.layers[0].wqkv), D, 0, min(nbuf<T>() / NVD, nqkv), qkv_row);
   for (int li = 0; li < a.nlayers; ++li) {
-    const LayerDev& L = a.layers[li];
-    const bool first = li == 0;
+    const bool first = li == 0, last = li + 1 == a.nlayers;
     const int base = 16 * li;
+    T* ring_k = static_cast<T*>(a.st.ring) + 2 * li * eRing;
+    // ---- stage the norm weights, ring history and cross K/V block of this layer in LDS
+    if (wid < 3 && (CROSS || wid != 1)) {
+      const void* g = wid == 0 ? a.st.norm_sa : wid == 1 ? a.st.norm_ca : a.st.norm_ff;
+      stage_slots<T>(static_cast<const T*>(g) + (size_t)li * D, D / 64, (long)D * sizeof(T), gam[wid]);
+    }
+    if (jpart == 0 && a.pos > 0) {
+      const int kind = wid >> 1, b = wid & 1;
+      stage_slots<T>(ring_k + kind * eRing + (size_t)(b * H + h) * a.Lmax * 64, a.pos,
+                     (long)a.Lmax * 64 * sizeof(T), hist + wid * kRegion);
+    }
+    auto stage_cross = [&]() {
+      const int chunk = (a.S + bph - 1) / bph, kb0 = jpart * chunk;
+      const int nk = max(0, min(chunk, a.S - kb0));
+      if (nk > 0) {
+        const int kind = wid >> 1, b = wid & 1;
+        const T* src = static_cast<const T*>(a.st.cross) + (2 * li + kind) * eCross +
+                       ((size_t)(b * H + h) * a.S + kb0) * 64;
+        stage_slots<T>(src, nk, (long)(a.S - kb0) * 64 * sizeof(T), cst + wid * kRegion);
+      }
+    };
+    if (CROSS && jpart != 0) stage_cross();
     // ---- QKV of head h's slice (weights already in flight)
-    load_act<T>(a.ll.x, first ? a.in : nullptr, D, x_tag, static_cast<const T*>(L.norm_sa), xs, red, no_side, r0,
-                r1, a.ll.err, a.trace, &tp);
-    gemv_rows<T, NVD, 1>(buf, static_cast<const T*>(L.wqkv), D, nqkv, qkv_row, xs,
-                         [&](int t, const float (&acc)[1][2]) {
-                           const int lt = wid + 4 * t, seg = lt / rps, r = lt % rps;
-                           const int n = h * 64 + jpart * rps + r;
-                           const float v0 = S::rnd(acc[0][0]), v1 = S::rnd(acc[0][1]);
-                           if (lane == 0) {
-                             uint64_t* dst = seg == 0 ? a.ll.q : seg == 1 ? a.ll.k : a.ll.v;
-                             LL<T>::put(dst, n, v0, v1, tag(base + kPhQKV));
-                             if (seg > 0) {
-                               kvst[seg - 1][0][r] = v0;
-                               kvst[seg - 1][1][r] = v1;
-                             }
-                           }
-                         });
+    load_act<T>(a.ll.x, first ? a.in : nullptr, D, x_tag, gam[0], xs,
+                red, no_side, r0, r1, a.ll.err, a.trace, tp);
+    gemv_rows<T, NVD, 1, NT>(buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs, [&](int t, const float (&s)[1][2]) {
+      const int lt = wid + 4 * t, seg = lt / rps, r = lt % rps;
+      const int n = h * 64 + jpart * rps + r;
+      const float v0 = S::rnd(s[0][0]), v1 = S::rnd(s[0][1]);
+      if (lane == 0) {
+        uint64_t* dst = seg == 0 ? a.ll.q : seg == 1 ? a.ll.k : a.ll.v;
+        LL<T>::put(dst, n, v0, v1, tag(base + kPhQKV));
+        if (seg > 0) {
+          kvst[seg - 1][0][r] = v0;
+          kvst[seg - 1][1][r] = v1;
+        }
+      }
+    });
+    MRT_TP;
     __syncthreads();
-    // plain ring slot (read by later launches): 4 elements per 8-byte store
+    // plain ring slot (read by later launches): 4 elements per thread
     if (threadIdx.x < 2 * 2 * (rps / 4)) {
       const int g4 = threadIdx.x % (rps / 4), rb = (threadIdx.x / (rps / 4)) % 2, kv = threadIdx.x / (rps / 2);
-      T* cache = static_cast<T*>(kv == 0 ? L.kc : L.vc);
-      T* dst = cache + (((size_t)rb * H + h) * a.Lmax + a.pos) * 64 + jpart * rps + 4 * g4;
+      T* dst = ring_k + kv * eRing + (((size_t)rb * H + h) * a.Lmax + a.pos) * 64 + jpart * rps + 4 * g4;
       const float* v = &kvst[kv][rb][4 * g4];
       if constexpr (sizeof(T) == 2) {
         st_g(reinterpret_cast<uint64_t*>(dst), (uint64_t)f2bf(v[0]) | ((uint64_t)f2bf(v[1]) << 16) |
@@ -779,92 +926,102 @@ __global__ __launch_bounds__(kPersistThreads) void k_step(StepArgs a) {
              (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32));
       }
     }
-    // next phase's weights, then head h's attention in workgroup (h, 0)
-    fetch_batch<T, NVD, 1>(buf, static_cast<const T*>(L.wo), HD, 0, min(nbuf<T>() / NVD, sD.nw(wid)), rowD);
-    if (jpart == 0) self_attention_head<T>(a, L, h, tag(base + kPhQKV), tag(base + kPhAtt), sm);
+    // Head h's attention in workgroup (h, 0), then the next phase's weights:
+    // its polls would otherwise also wait for those loads.
+    const T* wo = static_cast<const T*>(a.st.wo) + li * eO;
+    if (jpart == 0) {
+      self_attention_head<T>(a, h, tag(base + kPhQKV), tag(base + kPhAtt), hist, sm);
+      MRT_TP;
+      if (CROSS) stage_cross();  // the history has been read (barrier above)
+    }
+    fetch_batch<T, NVD, 1, NT>(buf, wo, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
     // ---- attention output projection + residual
     load_act<T>(a.ll.at, nullptr, HD, tag(base + kPhAtt), nullptr, xs, red,
-                side_x(a.ll.x, first ? a.in : nullptr, x_tag), r0, r1, a.ll.err, a.trace, &tp);
-    auto resid_put = [&](int t, const float (&acc)[1][2], int code) {
-      const float x0 = __shfl(r0, t, 64), x1 = __shfl(r1, t, 64);
-      if (lane == 0)
-        LL<T>::put(a.ll.x, sD.row(wid, t), S::rnd(x0 + S::rnd(acc[0][0])), S::rnd(x1 + S::rnd(acc[0][1])),
-                   tag(base + code));
-    };
-    gemv_rows<T, NVD, 1>(buf, static_cast<const T*>(L.wo), HD, sD.nw(wid), rowD, xs,
-                         [&](int t, const float (&acc)[1][2]) { resid_put(t, acc, kPhO); });
+                side_x(a.ll.x, first ? a.in : nullptr, x_tag), r0, r1, a.ll.err, a.trace, tp);
+    gemv_rows<T, NVD, 1, NT>(buf, wo, HD, sD.nw(wid), rowD, xs,
+                             [&](int t, const float (&s)[1][2]) { resid_put(t, s, tag(base + kPhO)); });
+    MRT_TP;
     x_tag = tag(base + kPhO);
     if constexpr (CROSS) {
       // ---- cross attention: q rows of head h, key-block partials, combine
-      fetch_batch<T, NVD, 1>(buf, static_cast<const T*>(L.wq_c), D, 0, min(nbuf<T>() / NVD, ncq), cq_row);
-      load_act<T>(a.ll.x, nullptr, D, x_tag, static_cast<const T*>(L.norm_ca), xs, red, no_side, r0, r1, a.ll.err, a.trace, &tp);
-        gemv_rows<T, NVD, 1>(buf, static_cast<const T*>(L.wq_c), D, ncq, cq_row, xs,
-                           [&](int t, const float (&acc)[1][2]) {
-                             if (lane == 0)
-                               LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(acc[0][0]), S::rnd(acc[0][1]),
-                                          tag(base + kPhCQ));
-                           });
-      fetch_batch<T, NVD, 1>(buf, static_cast<const T*>(L.wo_c), HD, 0, min(nbuf<T>() / NVD, sD.nw(wid)), rowD);
-      cross_partial<T>(a, L, h, jpart, tag(base + kPhCQ), tag(base + kPhCP), sm);
-      if (jpart == 0) cross_combine<T>(a, h, tag(base + kPhCP), tag(base + kPhCC), sm);
+      const T* wqc = static_cast<const T*>(a.st.wq_c) + li * eQc;
+      const T* woc = static_cast<const T*>(a.st.wo_c) + li * eO;
+      fetch_batch<T, NVD, 1, NT>(buf, wqc, D, 0, min(kNBuf / NVD, ncq), cq_row);
+      load_act<T>(a.ll.x, nullptr, D, x_tag, gam[1], xs, red, no_side,
+                  r0, r1, a.ll.err, a.trace, tp);
+      gemv_rows<T, NVD, 1, NT>(buf, wqc, D, ncq, cq_row, xs, [&](int t, const float (&s)[1][2]) {
+        if (lane == 0) LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(s[0][0]), S::rnd(s[0][1]), tag(base + kPhCQ));
+      });
+      MRT_TP;
+      fetch_batch<T, NVD, 1, NT>(buf, woc, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
+      cross_partial<T>(a, h, jpart, tag(base + kPhCQ), tag(base + kPhCP), cst, sm);
+      MRT_TP;
+      if (jpart == 0) {
+        cross_combine<T>(a, h, tag(base + kPhCP), tag(base + kPhCC), sm);
+        MRT_TP;
+      }
       load_act<T>(a.ll.at, nullptr, HD, tag(base + kPhCC), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
-                  a.ll.err, a.trace, &tp);
-        gemv_rows<T, NVD, 1>(buf, static_cast<const T*>(L.wo_c), HD, sD.nw(wid), rowD, xs,
-                           [&](int t, const float (&acc)[1][2]) { resid_put(t, acc, kPhCO); });
+                  a.ll.err, a.trace, tp);
+      gemv_rows<T, NVD, 1, NT>(buf, woc, HD, sD.nw(wid), rowD, xs,
+                               [&](int t, const float (&s)[1][2]) { resid_put(t, s, tag(base + kPhCO)); });
+      MRT_TP;
       x_tag = tag(base + kPhCO);
     }
     // ---- gated-GELU up projection
-    fetch_batch<T, NVD, 2>(buf, static_cast<const T*>(L.w01), D, 0, min(nbuf<T>() / (2 * NVD), sF.nw(wid)), rowF);
-    load_act<T>(a.ll.x, nullptr, D, x_tag, static_cast<const T*>(L.norm_ff), xs, red, no_side, r0, r1, a.ll.err, a.trace, &tp);
-    gemv_rows<T, NVD, 2>(buf, static_cast<const T*>(L.w01), D, sF.nw(wid), rowF, xs,
-                         [&](int t, const float (&acc)[2][2]) {
-                           if (lane == 0) {
-                             const float g0 = gelu_t<T>(S::rnd(acc[0][0])), g1 = gelu_t<T>(S::rnd(acc[0][1]));
-                             LL<T>::put(a.ll.h, sF.row(wid, t), S::rnd(g0 * S::rnd(acc[1][0])),
-                                        S::rnd(g1 * S::rnd(acc[1][1])), tag(base + kPhUp));
-                           }
-                         });
+    const T* w01 = static_cast<const T*>(a.st.w01) + li * e01;
+    const T* wo2 = static_cast<const T*>(a.st.wo2) + li * eO2;
+    fetch_batch<T, NVD, 2, NT>(buf, w01, D, 0, min(kNBuf / (2 * NVD), sF.nw(wid)), rowF);
+    load_act<T>(a.ll.x, nullptr, D, x_tag, gam[2], xs, red, no_side, r0,
+                r1, a.ll.err, a.trace, tp);
+    gemv_rows<T, NVD, 2, NT>(buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, const float (&s)[2][2]) {
+      if (lane == 0) {
+        const float g0 = gelu_t<T>(S::rnd(s[0][0])), g1 = gelu_t<T>(S::rnd(s[0][1]));
+        LL<T>::put(a.ll.h, sF.row(wid, t), S::rnd(g0 * S::rnd(s[1][0])), S::rnd(g1 * S::rnd(s[1][1])),
+                   tag(base + kPhUp));
+      }
+    });
+    MRT_TP;
     // ---- down projection + residual
-    fetch_batch<T, NVF, 1>(buf, static_cast<const T*>(L.wo2), F, 0, min(nbuf<T>() / NVF, sD.nw(wid)), rowD);
+    fetch_batch<T, NVF, 1, NT>(buf, wo2, F, 0, min(kNBuf / NVF, sD.nw(wid)), rowD);
     load_act<T>(a.ll.h, nullptr, F, tag(base + kPhUp), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
-                a.ll.err, a.trace, &tp);
-    const bool last = li + 1 == a.nlayers;
+                a.ll.err, a.trace, tp);
     if (CROSS && last) {
       // The temporal step's output leaves as plain pairs (no final norm).
       if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
-      gemv_rows<T, NVF, 1>(buf, static_cast<const T*>(L.wo2), F, sD.nw(wid), rowD, xs,
-                           [&](int t, const float (&acc)[1][2]) {
-                             const float x0 = __shfl(r0, t, 64), x1 = __shfl(r1, t, 64);
-                             if (lane == 0)
-                               st_g(static_cast<W*>(a.out) + sD.row(wid, t),
-                                    PT::pack(S::rnd(x0 + S::rnd(acc[0][0])), S::rnd(x1 + S::rnd(acc[0][1]))));
-                           });
+      gemv_rows<T, NVF, 1, NT>(buf, wo2, F, sD.nw(wid), rowD, xs, [&](int t, const float (&s)[1][2]) {
+        const float x0 = lane_value(r0, t), x1 = lane_value(r1, t);
+        if (lane == 0)
+          st_g(static_cast<W*>(a.out) + sD.row(wid, t),
+               PT::pack(S::rnd(x0 + S::rnd(s[0][0])), S::rnd(x1 + S::rnd(s[0][1]))));
+      });
     } else {
-      gemv_rows<T, NVF, 1>(buf, static_cast<const T*>(L.wo2), F, sD.nw(wid), rowD, xs,
-                           [&](int t, const float (&acc)[1][2]) { resid_put(t, acc, kPhDn); });
+      gemv_rows<T, NVF, 1, NT>(buf, wo2, F, sD.nw(wid), rowD, xs,
+                               [&](int t, const float (&s)[1][2]) { resid_put(t, s, tag(base + kPhDn)); });
     }
+    MRT_TP;
     x_tag = tag(base + kPhDn);
     if (!last)
-      fetch_batch<T, NVD, 1>(buf, static_cast<const T*>(a.layers[li + 1].wqkv), D, 0, min(nbuf<T>() / NVD, nqkv),
-                             qkv_row);
+      fetch_batch<T, NVD, 1, NT>(buf, wqkv0 + (li + 1) * eQKV, D, 0, min(kNBuf / NVD, nqkv), qkv_row);
+    __syncthreads();  // LDS staging regions are rewritten by the next layer
   }
 
   if constexpr (!CROSS) {
     // ---- decoder_norm + lm_head rows (model.cpp:652-653)
     const RowSplit sH(a.head_rows, G, blk);
     auto rowH = [&](int t, int) { return sH.row(wid, t); };
-    fetch_batch<T, NVD, 1>(buf, static_cast<const T*>(a.head_w), D, 0, min(nbuf<T>() / NVD, sH.nw(wid)), rowH);
-    load_act<T>(a.ll.x, nullptr, D, x_tag, static_cast<const T*>(a.dec_norm), xs, red, no_side, r0, r1, a.ll.err, a.trace, &tp);
+    const T* hw = static_cast<const T*>(a.head_w);
+    fetch_batch<T, NVD, 1, NT>(buf, hw, D, 0, min(kNBuf / NVD, sH.nw(wid)), rowH);
+    load_act<T>(a.ll.x, nullptr, D, x_tag, gam[3], xs, red, no_side, r0, r1, a.ll.err,
+                a.trace, tp);
     if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
-    gemv_rows<T, NVD, 1>(buf, static_cast<const T*>(a.head_w), D, sH.nw(wid), rowH, xs,
-                         [&](int t, const float (&acc)[1][2]) {
-                           if (lane == 0) {
-                             const int n = sH.row(wid, t);
-                             astore(a.ll.logit + n, ll_word(__float_as_uint(S::rnd(acc[0][0])), tag(kPhHead)));
-                             astore(a.ll.logit + a.head_rows + n,
-                                    ll_word(__float_as_uint(S::rnd(acc[0][1])), tag(kPhHead)));
-                           }
-                         });
+    gemv_rows<T, NVD, 1, NT>(buf, hw, D, sH.nw(wid), rowH, xs, [&](int t, const float (&s)[1][2]) {
+      if (lane == 0) {
+        const int n = sH.row(wid, t);
+        astore(a.ll.logit + n, ll_word(__float_as_uint(S::rnd(s[0][0])), tag(kPhHead)));
+        astore(a.ll.logit + a.head_rows + n, ll_word(__float_as_uint(S::rnd(s[0][1])), tag(kPhHead)));
+      }
+    });
+    MRT_TP;
     if (blk == 0) {
       // ---- gather the logits, copy them out, sample
       float* lg = xs;  // 2 * head_rows floats when head_rows <= kMaxPersistK
@@ -898,13 +1055,14 @@ __global__ __launch_bounds__(kPersistThreads) void k_step(StepArgs a) {
         }
       }
       __syncthreads();
-      trace_point(a.trace, kTraceEnd);
+      if (a.trace != nullptr && threadIdx.x == 0) a.trace[kTraceEnd] = wall_clock64();
       if (a.do_sample && wid == 0) sample_and_feed<T>(a, lg);
     }
   } else {
-    trace_point(a.trace, kTraceEnd);
+    if (a.trace != nullptr && blk == 0 && threadIdx.x == 0) a.trace[kTraceEnd] = wall_clock64();
   }
-  trace_point(a.trace, kTraceDone);
+#undef MRT_TP
+  if (a.trace != nullptr && blk == 0 && threadIdx.x == 0) a.trace[kTraceDone] = wall_clock64();
 }
 
 template <typename T>
@@ -930,6 +1088,24 @@ __global__ void k_embed_pairs(const T* __restrict__ emb, int D, int id, typename
   }
 }
 
+template <typename T, bool CROSS>
+size_t lds_bytes() {
+  return 4 * static_cast<size_t>(kRegion) * sizeof(T);
+}
+
+template <typename T, bool CROSS>
+bool allow_lds(size_t dyn, int device) {
+  hipFuncAttributes attr{};
+  MRT_HIP_CHECK(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&k_step<T, CROSS>)));
+  int max_lds = 0;
+  MRT_HIP_CHECK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeSharedMemPerBlockOptin, device));
+  if (max_lds <= 0) MRT_HIP_CHECK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
+  if (attr.sharedSizeBytes + dyn > static_cast<size_t>(max_lds)) return false;
+  MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_step<T, CROSS>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(dyn)));
+  return true;
+}
+
 }  // namespace
 
 int persist_grid(int H, int num_cu, int* bph_out) {
@@ -940,17 +1116,30 @@ int persist_grid(int H, int num_cu, int* bph_out) {
   return H * bph;
 }
 
-void launch_step(DType dt, const StepArgs& a, int grid, hipStream_t s) {
+size_t persist_prepare(DType dt, bool cross, int device) {
+  size_t n = 0;
+  bool ok = false;
+  if (dt == DType::F32) {
+    n = cross ? lds_bytes<float, true>() : lds_bytes<float, false>();
+    ok = cross ? allow_lds<float, true>(n, device) : allow_lds<float, false>(n, device);
+  } else {
+    n = cross ? lds_bytes<bf16, true>() : lds_bytes<bf16, false>();
+    ok = cross ? allow_lds<bf16, true>(n, device) : allow_lds<bf16, false>(n, device);
+  }
+  return ok ? n : 0;
+}
+
+void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t s) {
   if (dt == DType::F32) {
     if (a.cross)
-      hipLaunchKernelGGL((k_step<float, true>), dim3(grid), dim3(kPersistThreads), 0, s, a);
+      hipLaunchKernelGGL((k_step<float, true>), dim3(grid), dim3(kPersistThreads), lds, s, a);
     else
-      hipLaunchKernelGGL((k_step<float, false>), dim3(grid), dim3(kPersistThreads), 0, s, a);
+      hipLaunchKernelGGL((k_step<float, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
   } else {
     if (a.cross)
-      hipLaunchKernelGGL((k_step<bf16, true>), dim3(grid), dim3(kPersistThreads), 0, s, a);
+      hipLaunchKernelGGL((k_step<bf16, true>), dim3(grid), dim3(kPersistThreads), lds, s, a);
     else
-      hipLaunchKernelGGL((k_step<bf16, false>), dim3(grid), dim3(kPersistThreads), 0, s, a);
+      hipLaunchKernelGGL((k_step<bf16, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
   }
   MRT_HIP_CHECK(hipGetLastError());
 }
