@@ -380,6 +380,7 @@ void State::setup_persistent() {
   const size_t logit = 2 * static_cast<size_t>(c.vocab_size);
   ll_words_ = 6 * vec + part + logit + 64;
   ll_block_ = dalloc(ll_words_ * sizeof(uint64_t));
+  noise_ = static_cast<float*>(dalloc(static_cast<size_t>(F) * c.rvq_depth * 1024 * sizeof(float)));
   reset_handoff();
   auto stack = [&](const std::vector<DecoderLayerW>& ws, bool temporal) {
     DecStack d{};
@@ -521,6 +522,7 @@ void State::launch_depth_p(const void* in_pairs, int l, const void* head_w, int 
     a.next_in = p_din;
     a.fsum = p_fsum;
     a.fmean = p_tin;
+    a.noise = noise_ + (static_cast<size_t>(frame) * o->rvq_depth + level) * o->codebook;
   }
   a.ll = ll_bufs();
   launch_step(m.dt, a, persist_grid_, lds_d_, stream);
@@ -531,6 +533,7 @@ void State::enqueue_decode_p(const GenOpts& o) {
   const int D = c.d_model, C = o.codebook;
   const size_t row_bytes = static_cast<size_t>(rows) * D * esz();
   embed_pairs(m.dt, m.emb, D, 0, p_tin, stream);  // frame 0 input: emb(PAD = 0)
+  gumbel_table(d_seed, o.num_frames, o.rvq_depth, C, noise_, stream);
   for (int f = 0; f < o.num_frames; ++f) {
     launch_temporal_p(p_tin, f, p_tout);
     if (o.record_temporal) pairs_to_rows(m.dt, p_tout, D, static_cast<char*>(o.record_temporal) + f * row_bytes, stream);

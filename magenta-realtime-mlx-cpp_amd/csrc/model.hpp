@@ -158,6 +158,7 @@ class State {
   void reset_handoff();
   DecStack tstack_{}, dstack_{};  // temporal / depth stacks with this state's caches
   size_t lds_t_ = 0, lds_d_ = 0;   // dynamic LDS of the step kernels
+  float* noise_ = nullptr;         // Gumbel noise of every draw of a decode call
   int* h_err_ = nullptr;        // pinned
   uint64_t* d_trace_ = nullptr; // 2 x kTraceSlots when MRT_TRACE_PHASES is set
   void print_trace();

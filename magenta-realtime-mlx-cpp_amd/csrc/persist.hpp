@@ -76,6 +76,7 @@ struct StepArgs {
   void* fsum;      // (D) pairs
   void* fmean;     // (D) pairs: frame mean (next temporal input)
   float* rec_slice;  // optional copy of the logits
+  const float* noise;  // Gumbel noise of this draw: (codebook) floats
   LLBufs ll;
   // Optional timeline (100 MHz wall clock) recorded by workgroup 0.
   uint64_t* trace;
@@ -94,6 +95,10 @@ int persist_grid(int H, int num_cu, int* bph);
 size_t persist_prepare(DType dt, bool cross, int device);
 
 void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t s);
+
+// Gumbel noise of every draw of a decode call: out[(f * L + l) * C + c] =
+// gumbel(seed, f, l, c) for f < frames, l < L, c < C.
+void gumbel_table(const uint64_t* seed, int frames, int L, int C, float* out, hipStream_t s);
 
 // (rows=2, D) model-dtype rows <-> (D) pairs.
 void rows_to_pairs(DType dt, const void* rows, int D, void* pairs, hipStream_t s);

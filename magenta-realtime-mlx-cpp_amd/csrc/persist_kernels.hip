@@ -40,6 +40,7 @@
 //   cross:  workgroup (h, j) owns head h's q rows 4j.., then computes the
 //          softmax partial of key block j (ceil(S / bph) keys); workgroup
 //          (h, 0) combines the bph partials.
+#include <algorithm>
 #include <cmath>
 
 #include "device_utils.hpp"
@@ -126,8 +127,9 @@ __device__ __forceinline__ int dpp_min_i(int v) {
   return __builtin_amdgcn_readlane(v, 63);
 }
 
-__device__ __forceinline__ float lane_value(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+// Value of `v` held by lane `src` (src - lane is wave-uniform).
+__device__ __forceinline__ float from_lane(float v, int src) {
+  return src == (int)(threadIdx.x & 63) ? v : __shfl(v, src & 63, 64);
 }
 
 // Plain (rows 0/1) pair of one element: bf16 -> 32 bits, fp32 -> 64 bits.
@@ -396,7 +398,9 @@ struct Dot<float> {
 
 // Dots of a batch against the two activation rows (model dtype in LDS; the
 // buffer is zero past every row's end, so zero weight chunks meet finite
-// activations); epi(index, sums[P][2]) runs on every lane with wave-uniform sums.
+// activations).  epi(t, active, sums[P][2]) runs once on every lane: lane r
+// holds the sums of the batch's row r (wave-local row index t = b0 + r) and
+// is active when that row exists.
 template <typename T, int NV, int P, class Epi>
 __device__ __forceinline__ void dot_batch(const uint4 (&buf)[kNBuf], int b0, int nb, const float* xs, Epi epi) {
   constexpr int V = St<T>::kVec;
@@ -425,18 +429,24 @@ __device__ __forceinline__ void dot_batch(const uint4 (&buf)[kNBuf], int b0, int
       }
     }
   }
+  // Row r's sums go to lane r, so the epilogue runs once for all rows.
+  float v[P][2];
+#pragma unroll
+  for (int p = 0; p < P; ++p) v[p][0] = v[p][1] = 0.f;
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     if (r < nb) {
-      float s[P][2];
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        s[p][0] = dpp_sum(acc[r][p][0]);
-        s[p][1] = dpp_sum(acc[r][p][1]);
+        const float s0 = dpp_sum(acc[r][p][0]), s1 = dpp_sum(acc[r][p][1]);
+        if (lane == r) {
+          v[p][0] = s0;
+          v[p][1] = s1;
+        }
       }
-      epi(b0 + r, s);
     }
   }
+  epi(b0 + lane, lane < nb, v);
 }
 
 // Runs a wave's nw rows in batches; the first batch is already in buf.
@@ -691,51 +701,81 @@ __device__ __forceinline__ void cross_combine(const StepArgs& a, int h, uint32_t
 
 // ---- sampling -------------------------------------------------------------------
 
-// CFG + temperature/top-k Gumbel-max draw and token feedback (decode.cpp:
-// 71-148, 458-484), run by wave 0; `lg` holds the two logit rows in LDS.
+// Block-wide CFG + temperature/top-k Gumbel-max draw and token feedback
+// (decode.cpp:71-148, 458-484); `lg` holds the two logit rows in LDS, the
+// Gumbel noise of the draw comes precomputed in a.noise.  The top-k
+// threshold (k-th largest value, ties kept) is found by a most-significant-
+// byte-first radix select over LDS histograms.
 template <typename T>
-__device__ __forceinline__ void sample_and_feed(const StepArgs& a, const float* lg) {
+__device__ __forceinline__ void sample_block(const StepArgs& a, const float* lg, unsigned* hist, int* sel) {
   using PT = PairT<T>;
   using W = typename PT::W;
   using S = St<T>;
-  constexpr int kPer = 16;
-  const int lane = threadIdx.x & 63;
+  constexpr int kPer = 1024 / kPersistThreads;  // candidates and d_model elements per thread
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const SampleParams& p = a.sp;
   const int C = p.codebook;
   // Loads that do not depend on the draw go first.
-  constexpr int kDPer = 1024 / 64;
   const W* fs_in = static_cast<const W*>(a.fsum);
-  float fv[kDPer];
+  float fv[kPer], gn[kPer];
 #pragma unroll
-  for (int t = 0; t < kDPer; ++t) {
-    const int d = lane + 64 * t;
+  for (int t = 0; t < kPer; ++t) {
+    const int d = tid + kPersistThreads * t;
     fv[t] = (a.level != 0 && d < a.D) ? PT::lo(ld_g(fs_in + d)) : 0.f;
+    gn[t] = d < C ? ld_g(a.noise + d) : 0.f;
   }
-  const uint64_t seed = ld_g(p.seed);
   const int teacher_id = a.teacher ? ld_g(a.teacher + a.slot) : 0;
   const float wc = 1.0f + p.guidance_weight, wu = p.guidance_weight;
   float v[kPer];
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {
-    const int c = lane + 64 * t;
+    const int c = tid + kPersistThreads * t;
     v[t] = (c < C) ? __fsub_rn(__fmul_rn(wc, lg[c]), __fmul_rn(wu, lg[C + c])) : -INFINITY;
   }
   if (p.temperature != 0.0f) {
 #pragma unroll
     for (int t = 0; t < kPer; ++t)
-      if (lane + 64 * t < C) v[t] = __fdiv_rn(v[t], p.temperature);
+      if (tid + kPersistThreads * t < C) v[t] = __fdiv_rn(v[t], p.temperature);
     if (p.top_k > 0 && p.top_k < C) {
-      // k-th largest key by a most-significant-bit-first search; counts by ballot.
       uint32_t key[kPer];
 #pragma unroll
-      for (int t = 0; t < kPer; ++t) key[t] = (lane + 64 * t < C) ? float_key(v[t]) : 0u;
-      uint32_t prefix = 0;
-      for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t cand = prefix | (1u << bit);
-        int cnt = 0;
+      for (int t = 0; t < kPer; ++t) key[t] = (tid + kPersistThreads * t < C) ? float_key(v[t]) : 0u;
+      uint32_t prefix = 0, mask = 0;
+      int need = p.top_k;
+      for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        hist[tid] = 0u;
+        __syncthreads();
 #pragma unroll
-        for (int t = 0; t < kPer; ++t) cnt += __popcll(__ballot(key[t] >= cand));
-        if (cnt >= p.top_k) prefix = cand;
+        for (int t = 0; t < kPer; ++t)
+          if (tid + kPersistThreads * t < C && (key[t] & mask) == prefix) atomicAdd(&hist[(key[t] >> shift) & 255u], 1u);
+        __syncthreads();
+        if (wid == 0) {
+          // lane l holds bins 4l..4l+3; suffix counts from the top bin down
+          const unsigned c0 = hist[4 * lane], c1 = hist[4 * lane + 1], c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
+          const unsigned own = c0 + c1 + c2 + c3;
+          unsigned suf = own;  // inclusive suffix sum over lanes >= lane
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) {
+            const unsigned up = __shfl_down(suf, o, 64);
+            if (lane + o < 64) suf += up;
+          }
+          unsigned above = suf - own;  // keys in bins above this lane's
+          const unsigned cs[4] = {c0, c1, c2, c3};
+#pragma unroll
+          for (int i = 3; i >= 0; --i) {
+            if (above < (unsigned)need && above + cs[i] >= (unsigned)need) {
+              sel[0] = 4 * lane + i;
+              sel[1] = (int)above;
+            }
+            above += cs[i];
+          }
+        }
+        __syncthreads();
+        prefix |= (uint32_t)sel[0] << shift;
+        mask |= 255u << shift;
+        need -= sel[1];
+        __syncthreads();  // sel and hist are rewritten by the next pass
       }
       const float thr = key_float(prefix);
 #pragma unroll
@@ -743,37 +783,50 @@ __device__ __forceinline__ void sample_and_feed(const StepArgs& a, const float* 
         if (v[t] < thr) v[t] = -INFINITY;
     }
 #pragma unroll
-    for (int t = 0; t < kPer; ++t) {
-      const int c = lane + 64 * t;
-      if (c < C && v[t] != -INFINITY) v[t] = v[t] + gumbel(seed, a.frame, a.level, c);
-    }
+    for (int t = 0; t < kPer; ++t)
+      if (v[t] != -INFINITY) v[t] = v[t] + gn[t];
   }
+  // argmax, ties to the smallest index
   float best = -INFINITY;
   int bi = 0x7fffffff;
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {
-    const int c = lane + 64 * t;
+    const int c = tid + kPersistThreads * t;
     if (c < C && (v[t] > best || bi == 0x7fffffff)) {
       best = v[t];
       bi = c;
     }
   }
-  // argmax, ties to the smallest index
-  const float mx = dpp_max(best);
-  const int arg = dpp_min_i(best == mx ? bi : 0x7fffffff);
+  const float wmx = dpp_max(best);
+  const int warg = dpp_min_i(best == wmx ? bi : 0x7fffffff);
+  float* wbest = reinterpret_cast<float*>(hist);
+  int* widx = sel + 4;
+  if (lane == 0) {
+    wbest[wid] = wmx;
+    widx[wid] = warg;
+  }
+  __syncthreads();
+  float mx = wbest[0];
+  int arg = widx[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w)
+    if (wbest[w] > mx || (wbest[w] == mx && widx[w] < arg)) {
+      mx = wbest[w];
+      arg = widx[w];
+    }
   const int drawn_id = p.codec_offset + a.level * C + arg;
   const int fed = a.teacher ? teacher_id : drawn_id;
-  if (lane == 0) {
+  if (tid == 0) {
     st_g(a.tokens + a.slot, fed);
     if (a.drawn) st_g(a.drawn + a.slot, drawn_id);
   }
   // Token feedback: both rows take emb(fed); the frame sum accumulates in the
   // model dtype; the last level's sum / L is the next temporal input.
   const T* e = static_cast<const T*>(a.emb) + (size_t)fed * a.D;
-  float ev[kDPer];
+  float ev[kPer];
 #pragma unroll
-  for (int t = 0; t < kDPer; ++t) {
-    const int d = lane + 64 * t;
+  for (int t = 0; t < kPer; ++t) {
+    const int d = tid + kPersistThreads * t;
     ev[t] = d < a.D ? S::ld(ld_g(e + d)) : 0.f;
   }
   const float Lf = S::rnd((float)p.rvq_depth);
@@ -781,8 +834,8 @@ __device__ __forceinline__ void sample_and_feed(const StepArgs& a, const float* 
   W* fs = static_cast<W*>(a.fsum);
   W* fm = static_cast<W*>(a.fmean);
 #pragma unroll
-  for (int t = 0; t < kDPer; ++t) {
-    const int d = lane + 64 * t;
+  for (int t = 0; t < kPer; ++t) {
+    const int d = tid + kPersistThreads * t;
     if (d < a.D) {
       const float sum = (a.level == 0) ? ev[t] : S::rnd(fv[t] + ev[t]);
       st_g(ni + d, PT::pack(ev[t], ev[t]));
@@ -792,6 +845,15 @@ __device__ __forceinline__ void sample_and_feed(const StepArgs& a, const float* 
         st_g(fm + d, PT::pack(m, m));
       }
     }
+  }
+}
+
+__global__ void k_gumbel_table(const uint64_t* __restrict__ seed_p, int frames, int L, int C, float* __restrict__ out) {
+  const uint64_t seed = *seed_p;
+  const int n = frames * L * C;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const int c = i % C, fl = i / C;
+    out[i] = gumbel(seed, fl / L, fl % L, c);
   }
 }
 
@@ -813,6 +875,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   __shared__ float sm[704];
   __shared__ float kvst[2][2][16];  // [k|v][row][d within this workgroup's slice]
   __shared__ __align__(16) T gam[4][1024];  // norm weights: self-attn, cross-attn, FFN, decoder_norm
+  __shared__ unsigned sel_hist[kPersistThreads];
+  __shared__ int sel_res[8];
   extern __shared__ __align__(16) unsigned char dyn_lds[];
   // [K|V][row] regions of 64 x 64: the ring history during self attention,
   // then the layer's cross K/V block.
@@ -862,10 +926,10 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   };
   const Side no_side{nullptr, nullptr, 0u, -1};
   float r0 = 0.f, r1 = 0.f;
-  auto resid_put = [&](int t, const float (&s)[1][2], uint32_t tg) {
-    const float x0 = lane_value(r0, t), x1 = lane_value(r1, t);
-    if (lane == 0)
-      LL<T>::put(a.ll.x, sD.row(wid, t), S::rnd(x0 + S::rnd(s[0][0])), S::rnd(x1 + S::rnd(s[0][1])), tg);
+  // lane t holds the residual element of the wave's row t (side_x)
+  auto resid_put = [&](int t, bool act, const float (&s)[1][2], uint32_t tg) {
+    const float x0 = from_lane(r0, t), x1 = from_lane(r1, t);
+    if (act) LL<T>::put(a.ll.x, sD.row(wid, t), S::rnd(x0 + S::rnd(s[0][0])), S::rnd(x1 + S::rnd(s[0][1])), tg);
   };
 
   uint32_t x_tag = 0;  // tag of the current residual stream (layer >= 1)
@@ -897,11 +961,12 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     // ---- QKV of head h's slice (weights already in flight)
     load_act<T>(a.ll.x, first ? a.in : nullptr, D, x_tag, gam[0], xs,
                 red, no_side, r0, r1, a.ll.err, a.trace, tp);
-    gemv_rows<T, NVD, 1, NT>(buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs, [&](int t, const float (&s)[1][2]) {
+    gemv_rows<T, NVD, 1, NT>(buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs,
+                             [&](int t, bool act, const float (&s)[1][2]) {
       const int lt = wid + 4 * t, seg = lt / rps, r = lt % rps;
       const int n = h * 64 + jpart * rps + r;
       const float v0 = S::rnd(s[0][0]), v1 = S::rnd(s[0][1]);
-      if (lane == 0) {
+      if (act) {
         uint64_t* dst = seg == 0 ? a.ll.q : seg == 1 ? a.ll.k : a.ll.v;
         LL<T>::put(dst, n, v0, v1, tag(base + kPhQKV));
         if (seg > 0) {
@@ -939,7 +1004,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     load_act<T>(a.ll.at, nullptr, HD, tag(base + kPhAtt), nullptr, xs, red,
                 side_x(a.ll.x, first ? a.in : nullptr, x_tag), r0, r1, a.ll.err, a.trace, tp);
     gemv_rows<T, NVD, 1, NT>(buf, wo, HD, sD.nw(wid), rowD, xs,
-                             [&](int t, const float (&s)[1][2]) { resid_put(t, s, tag(base + kPhO)); });
+                             [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhO)); });
     MRT_TP;
     x_tag = tag(base + kPhO);
     if constexpr (CROSS) {
@@ -949,8 +1014,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       fetch_batch<T, NVD, 1, NT>(buf, wqc, D, 0, min(kNBuf / NVD, ncq), cq_row);
       load_act<T>(a.ll.x, nullptr, D, x_tag, gam[1], xs, red, no_side,
                   r0, r1, a.ll.err, a.trace, tp);
-      gemv_rows<T, NVD, 1, NT>(buf, wqc, D, ncq, cq_row, xs, [&](int t, const float (&s)[1][2]) {
-        if (lane == 0) LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(s[0][0]), S::rnd(s[0][1]), tag(base + kPhCQ));
+      gemv_rows<T, NVD, 1, NT>(buf, wqc, D, ncq, cq_row, xs, [&](int t, bool act, const float (&s)[1][2]) {
+        if (act) LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(s[0][0]), S::rnd(s[0][1]), tag(base + kPhCQ));
       });
       MRT_TP;
       fetch_batch<T, NVD, 1, NT>(buf, woc, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
@@ -963,7 +1028,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       load_act<T>(a.ll.at, nullptr, HD, tag(base + kPhCC), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
                   a.ll.err, a.trace, tp);
       gemv_rows<T, NVD, 1, NT>(buf, woc, HD, sD.nw(wid), rowD, xs,
-                               [&](int t, const float (&s)[1][2]) { resid_put(t, s, tag(base + kPhCO)); });
+                               [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhCO)); });
       MRT_TP;
       x_tag = tag(base + kPhCO);
     }
@@ -973,12 +1038,11 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     fetch_batch<T, NVD, 2, NT>(buf, w01, D, 0, min(kNBuf / (2 * NVD), sF.nw(wid)), rowF);
     load_act<T>(a.ll.x, nullptr, D, x_tag, gam[2], xs, red, no_side, r0,
                 r1, a.ll.err, a.trace, tp);
-    gemv_rows<T, NVD, 2, NT>(buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, const float (&s)[2][2]) {
-      if (lane == 0) {
-        const float g0 = gelu_t<T>(S::rnd(s[0][0])), g1 = gelu_t<T>(S::rnd(s[0][1]));
+    gemv_rows<T, NVD, 2, NT>(buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, bool act, const float (&s)[2][2]) {
+      const float g0 = gelu_t<T>(S::rnd(s[0][0])), g1 = gelu_t<T>(S::rnd(s[0][1]));
+      if (act)
         LL<T>::put(a.ll.h, sF.row(wid, t), S::rnd(g0 * S::rnd(s[1][0])), S::rnd(g1 * S::rnd(s[1][1])),
                    tag(base + kPhUp));
-      }
     });
     MRT_TP;
     // ---- down projection + residual
@@ -988,15 +1052,15 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     if (CROSS && last) {
       // The temporal step's output leaves as plain pairs (no final norm).
       if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
-      gemv_rows<T, NVF, 1, NT>(buf, wo2, F, sD.nw(wid), rowD, xs, [&](int t, const float (&s)[1][2]) {
-        const float x0 = lane_value(r0, t), x1 = lane_value(r1, t);
-        if (lane == 0)
+      gemv_rows<T, NVF, 1, NT>(buf, wo2, F, sD.nw(wid), rowD, xs, [&](int t, bool act, const float (&s)[1][2]) {
+        const float x0 = from_lane(r0, t), x1 = from_lane(r1, t);
+        if (act)
           st_g(static_cast<W*>(a.out) + sD.row(wid, t),
                PT::pack(S::rnd(x0 + S::rnd(s[0][0])), S::rnd(x1 + S::rnd(s[0][1]))));
       });
     } else {
       gemv_rows<T, NVF, 1, NT>(buf, wo2, F, sD.nw(wid), rowD, xs,
-                               [&](int t, const float (&s)[1][2]) { resid_put(t, s, tag(base + kPhDn)); });
+                               [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhDn)); });
     }
     MRT_TP;
     x_tag = tag(base + kPhDn);
@@ -1014,8 +1078,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     load_act<T>(a.ll.x, nullptr, D, x_tag, gam[3], xs, red, no_side, r0, r1, a.ll.err,
                 a.trace, tp);
     if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
-    gemv_rows<T, NVD, 1, NT>(buf, hw, D, sH.nw(wid), rowH, xs, [&](int t, const float (&s)[1][2]) {
-      if (lane == 0) {
+    gemv_rows<T, NVD, 1, NT>(buf, hw, D, sH.nw(wid), rowH, xs, [&](int t, bool act, const float (&s)[1][2]) {
+      if (act) {
         const int n = sH.row(wid, t);
         astore(a.ll.logit + n, ll_word(__float_as_uint(S::rnd(s[0][0])), tag(kPhHead)));
         astore(a.ll.logit + a.head_rows + n, ll_word(__float_as_uint(S::rnd(s[0][1])), tag(kPhHead)));
@@ -1056,7 +1120,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       }
       __syncthreads();
       if (a.trace != nullptr && threadIdx.x == 0) a.trace[kTraceEnd] = wall_clock64();
-      if (a.do_sample && wid == 0) sample_and_feed<T>(a, lg);
+      if (a.do_sample) sample_block<T>(a, lg, sel_hist, sel_res);
     }
   } else {
     if (a.trace != nullptr && blk == 0 && threadIdx.x == 0) a.trace[kTraceEnd] = wall_clock64();
@@ -1141,6 +1205,13 @@ void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t 
     else
       hipLaunchKernelGGL((k_step<bf16, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
   }
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void gumbel_table(const uint64_t* seed, int frames, int L, int C, float* out, hipStream_t s) {
+  const int n = frames * L * C;
+  const int blocks = std::min((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(k_gumbel_table, dim3(blocks), dim3(256), 0, s, seed, frames, L, C, out);
   MRT_HIP_CHECK(hipGetLastError());
 }
 
