@@ -283,6 +283,151 @@ __global__ __launch_bounds__(64) void k_enc_attn(const T* __restrict__ qkv, int 
   }
 }
 
+// ---- bf16 encoder self-attention on MFMA --------------------------------------------
+// Flash attention for one (row, head) and 128 queries per workgroup (32 per
+// wave), keys in tiles of 64 staged in LDS.  Scores are computed transposed,
+// S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so lane l owns query l % 32 and
+// the online-softmax rescale is per lane.  The output is also accumulated
+// transposed, O^T += V^T P^T, with P^T taken straight from the score
+// accumulators: lane l's accumulators of a 16-key step hold keys
+// {4h..4h+3, 8+4h..8+4h+3} (h = l / 32), so V^T is staged with the key order
+// inside every 16-key block permuted the same way (swap of key bits 2 and 3).
+// Scores and the softmax are fp32; P enters the second product as the sum of
+// two bf16 parts (hi + lo, ~16 significant bits), as close to the fp32
+// probabilities of the reference's fused attention as bf16 MFMA allows.
+constexpr int kAQ = 128, kAK = 64, kALD = 64 + 8;  // queries, keys per tile, padded LDS row
+
+__global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ qkv, int S, int H,
+                                                       bf16* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) bf16 Ks[2][kAK * kALD];
+  __shared__ __attribute__((aligned(16))) bf16 Vt[2][64 * kALD];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
+  const int HD = H * 64, ld = 3 * HD;
+  const bf16* base = qkv + (size_t)b * S * ld + h * 64;
+  const int lq = lane & 31, hf = lane >> 5;
+  const int q = blockIdx.x * kAQ + wid * 32 + lq;
+
+  // Q^T fragments (B operand): lane l holds Q[q][16 s + 8 hf .. +7].
+  bf16x8_t qf[4];
+  {
+    const bf16* qr = base + (size_t)min(q, S - 1) * ld;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const bf16x8_t*>(qr + 16 * s + 8 * hf);
+  }
+  // Tile staging: thread t moves 16 bytes of K and of V for keys t/8 and
+  // 32 + t/8, dims 8 (t % 8) .. +7.
+  uint4 rk[2], rv[2];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = kb + (tid >> 3) + 32 * i, c = (tid & 7) * 8;
+      if (key < S) {
+        const bf16* row = base + (size_t)key * ld;
+        rk[i] = *reinterpret_cast<const uint4*>(row + HD + c);
+        rv[i] = *reinterpret_cast<const uint4*>(row + 2 * HD + c);
+      } else {
+        rk[i] = make_uint4(0u, 0u, 0u, 0u);
+        rv[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = (tid >> 3) + 32 * i, c = (tid & 7) * 8;
+      *reinterpret_cast<uint4*>(&Ks[buf][key * kALD + c]) = rk[i];
+      const int slot = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+      const bf16* v = reinterpret_cast<const bf16*>(&rv[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Vt[buf][(c + e) * kALD + slot] = v[e];
+    }
+  };
+
+  f32x16_t acc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
+  float m = -INFINITY, lsum = 0.f;
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int ntiles = (S + kAK - 1) / kAK;
+  for (int j = 0; j < ntiles; ++j) {
+    const int cur = j & 1, kb = j * kAK;
+    if (j + 1 < ntiles) gload(kb + kAK);
+    // S^T for keys kb + 32 t + (8 (r/4) + 4 hf + r%4), query q
+    f32x16_t sc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[t][r] = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&Ks[cur][(32 * t + lq) * kALD + 16 * s + 8 * hf]);
+        sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sc[t], 0, 0, 0);
+      }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
+        if (key >= S) sc[t][r] = -INFINITY;
+        mt = fmaxf(mt, sc[t][r]);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m, mt);
+    const float corr = expf(m - mn);
+    float ps = 0.f;
+    bf16x8_t pb[4], pl[4];  // P^T = hi + lo (bf16 each) for the four 16-key steps
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = expf(sc[t][r] - mn);
+        const bf16 hi = f2bf(p);
+        ps += p;
+        reinterpret_cast<bf16*>(&pb[2 * t + (r >> 3)])[r & 7] = hi;
+        reinterpret_cast<bf16*>(&pl[2 * t + (r >> 3)])[r & 7] = f2bf(p - bf2f(hi));
+      }
+    ps += __shfl_xor(ps, 32, 64);
+    lsum = lsum * corr + ps;
+    m = mn;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[t][r] *= corr;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&Vt[cur][(32 * t + lq) * kALD + 16 * s + 8 * hf]);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[s], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pl[s], acc[t], 0, 0, 0);
+      }
+    if (j + 1 < ntiles) sstore(cur ^ 1);
+    __syncthreads();
+  }
+  if (q < S) {
+    bf16* orow = out + ((size_t)b * S + q) * HD + h * 64;
+    const float inv = 1.0f / lsum;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = 32 * t + 8 * g + 4 * hf;
+        uint2 w;
+        w.x = (uint32_t)f2bf(acc[t][4 * g] * inv) | ((uint32_t)f2bf(acc[t][4 * g + 1] * inv) << 16);
+        w.y = (uint32_t)f2bf(acc[t][4 * g + 2] * inv) | ((uint32_t)f2bf(acc[t][4 * g + 3] * inv) << 16);
+        *reinterpret_cast<uint2*>(orow + d) = w;
+      }
+  }
+}
+
 }  // namespace
 
 void encoder_embed(DType dt, const void* emb, const void* pe, const int* tok, int M, int S, int D,
@@ -329,12 +474,17 @@ void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const Gem
   MRT_HIP_CHECK(hipGetLastError());
 }
 
-void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s) {
-  dim3 grid((S + 63) / 64, nb * H);
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_enc_attn<float>, grid, dim3(64), 0, s, (const float*)qkv, S, H, (float*)out);
-  else
-    hipLaunchKernelGGL(k_enc_attn<bf16>, grid, dim3(64), 0, s, (const bf16*)qkv, S, H, (bf16*)out);
+void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s, bool allow_mfma) {
+  if (dt == DType::BF16 && allow_mfma) {
+    hipLaunchKernelGGL(k_enc_attn_mfma, dim3((S + kAQ - 1) / kAQ, nb * H), dim3(256), 0, s, (const bf16*)qkv, S, H,
+                       (bf16*)out);
+  } else {
+    dim3 grid((S + 63) / 64, nb * H);
+    if (dt == DType::F32)
+      hipLaunchKernelGGL(k_enc_attn<float>, grid, dim3(64), 0, s, (const float*)qkv, S, H, (float*)out);
+    else
+      hipLaunchKernelGGL(k_enc_attn<bf16>, grid, dim3(64), 0, s, (const bf16*)qkv, S, H, (bf16*)out);
+  }
   MRT_HIP_CHECK(hipGetLastError());
 }
 

@@ -110,6 +110,7 @@ void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const Gem
 
 // Bidirectional encoder self-attention, no mask, no bias, scale 1.0.
 // qkv (nb*S, 3*HD) row-major [q | k | v]; out (nb*S, HD).
-void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s);
+void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s,
+                  bool allow_mfma = true);
 
 }  // namespace mrt
