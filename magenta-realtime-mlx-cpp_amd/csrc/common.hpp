@@ -51,14 +51,15 @@ __host__ __device__ inline float bf2f(bf16 v) {
 
 __host__ __device__ inline bf16 f2bf(float f) {
 #ifdef __HIP_DEVICE_COMPILE__
-  uint32_t u = __float_as_uint(f);
+  // v_cvt_pk_bf16_f32: round-to-nearest-even in hardware.
+  return __builtin_bit_cast(bf16, static_cast<__bf16>(f));
 #else
   uint32_t u;
   std::memcpy(&u, &f, 4);
-#endif
   if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<bf16>(0x7fc0);  // NaN
   u += 0x7fffu + ((u >> 16) & 1u);
   return static_cast<bf16>(u >> 16);
+#endif
 }
 
 // Per-storage-type traits: load as float, store from float, and round a float

@@ -421,7 +421,7 @@ void State::print_trace() {
     std::string line;
     uint64_t prev = t0;
     int nb = 0;
-    for (int k = 0; k < kTraceStart && r[k]; ++k, ++nb) {
+    for (int k = 0; k < 400 && r[k]; ++k, ++nb) {
       if (k < 48) {
         char buf[32];
         std::snprintf(buf, sizeof buf, " %.2f", (r[k] - prev) * 0.01);
@@ -431,6 +431,19 @@ void State::print_trace() {
     }
     std::fprintf(stderr, "[mrt] %s: %d points, total %.2f us (to final arrival %.2f us); deltas us:%s\n", names[w], nb,
                  (r[kTraceDone] - t0) * 0.01, (r[kTraceEnd] - t0) * 0.01, line.c_str());
+    // per-wave poll completion of the first loads, relative to the load's start
+    std::string pw;
+    for (int k = 0; k < 16 && r[400 + k]; ++k) {
+      pw += " [";
+      for (int wv = 0; wv < 4; ++wv) {
+        const uint64_t v = r[420 + 4 * k + wv];
+        char buf[32];
+        std::snprintf(buf, sizeof buf, "%s%.2f", wv ? " " : "", v ? (double)(int64_t)(v - r[400 + k]) * 0.01 : -1.0);
+        pw += buf;
+      }
+      pw += "]";
+    }
+    std::fprintf(stderr, "[mrt] %s: per-wave poll done (us after load start):%s\n", names[w], pw.c_str());
   }
 }
 

@@ -269,8 +269,11 @@ __device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t
   }
 }
 
+constexpr int kLoadTrace = 400;  // start of the first 16 activation loads
+constexpr int kWaveTrace = 420;  // per-wave poll completion of the first 16 loads
+
 __device__ __forceinline__ void trace_point(uint64_t* trace, int slot) {
-  if (trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0 && slot < kTraceStart) trace[slot] = wall_clock64();
+  if (trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0 && slot < kLoadTrace) trace[slot] = wall_clock64();
 }
 
 // Loads the activation vector of a phase into xs (tagged, or the launch's
@@ -279,12 +282,13 @@ __device__ __forceinline__ void trace_point(uint64_t* trace, int slot) {
 template <typename T>
 __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, int K, uint32_t tag, const T* g,
                                          float* xs, float* red, const Side& sd, float& r0, float& r1, int* err,
-                                         uint64_t* trace, int& tp) {
+                                         uint64_t* trace, int& tp, int& lc) {
   using PT = PairT<T>;
   using S = St<T>;
   constexpr int kPer = kMaxPersistK / kPersistThreads;
   constexpr int kG = 1024 / kPersistThreads;
   const int tid = threadIdx.x;
+  if (trace != nullptr && blockIdx.x == 0 && tid == 0 && lc < 16) trace[kLoadTrace + lc] = wall_clock64();
   trace_point(trace, tp++);
   if (plain != nullptr) {
     typename PT::W w[kPer];
@@ -303,6 +307,8 @@ __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, 
     ll_load_vec<T>(ll, K, tag, xs, sd, r0, r1, err);
   }
   __builtin_amdgcn_s_waitcnt(0);  // LDS copies issued by this wave (norm weights) have landed
+  if (trace != nullptr && blockIdx.x == 0 && (tid & 63) == 0 && lc < 16) trace[kWaveTrace + 4 * lc + (tid >> 6)] = wall_clock64();
+  ++lc;
   trace_point(trace, tp++);
   if (g != nullptr) {
     // Each thread squares the elements it wrote itself: no barrier needed yet.
@@ -893,7 +899,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   const size_t eRing = (size_t)2 * H * a.Lmax * 64, eCross = (size_t)2 * H * a.S * 64;
   const T* wqkv0 = static_cast<const T*>(a.st.wqkv);
   uint4 buf[kNBuf];
-  int tp = 0;  // trace slot
+  int tp = 0;    // trace slot
+  int lcnt = 0;  // activation loads so far (trace only)
 #define MRT_TP trace_point(a.trace, tp++)
 
   const RowSplit sD(D, G, blk), sF(F, G, blk);
@@ -960,7 +967,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     if (CROSS && jpart != 0) stage_cross();
     // ---- QKV of head h's slice (weights already in flight)
     load_act<T>(a.ll.x, first ? a.in : nullptr, D, x_tag, gam[0], xs,
-                red, no_side, r0, r1, a.ll.err, a.trace, tp);
+                red, no_side, r0, r1, a.ll.err, a.trace, tp, lcnt);
     gemv_rows<T, NVD, 1, NT>(buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs,
                              [&](int t, bool act, const float (&s)[1][2]) {
       const int lt = wid + 4 * t, seg = lt / rps, r = lt % rps;
@@ -1002,7 +1009,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     fetch_batch<T, NVD, 1, NT>(buf, wo, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
     // ---- attention output projection + residual
     load_act<T>(a.ll.at, nullptr, HD, tag(base + kPhAtt), nullptr, xs, red,
-                side_x(a.ll.x, first ? a.in : nullptr, x_tag), r0, r1, a.ll.err, a.trace, tp);
+                side_x(a.ll.x, first ? a.in : nullptr, x_tag), r0, r1, a.ll.err, a.trace, tp, lcnt);
     gemv_rows<T, NVD, 1, NT>(buf, wo, HD, sD.nw(wid), rowD, xs,
                              [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhO)); });
     MRT_TP;
@@ -1013,7 +1020,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       const T* woc = static_cast<const T*>(a.st.wo_c) + li * eO;
       fetch_batch<T, NVD, 1, NT>(buf, wqc, D, 0, min(kNBuf / NVD, ncq), cq_row);
       load_act<T>(a.ll.x, nullptr, D, x_tag, gam[1], xs, red, no_side,
-                  r0, r1, a.ll.err, a.trace, tp);
+                  r0, r1, a.ll.err, a.trace, tp, lcnt);
       gemv_rows<T, NVD, 1, NT>(buf, wqc, D, ncq, cq_row, xs, [&](int t, bool act, const float (&s)[1][2]) {
         if (act) LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(s[0][0]), S::rnd(s[0][1]), tag(base + kPhCQ));
       });
@@ -1026,7 +1033,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
         MRT_TP;
       }
       load_act<T>(a.ll.at, nullptr, HD, tag(base + kPhCC), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
-                  a.ll.err, a.trace, tp);
+                  a.ll.err, a.trace, tp, lcnt);
       gemv_rows<T, NVD, 1, NT>(buf, woc, HD, sD.nw(wid), rowD, xs,
                                [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhCO)); });
       MRT_TP;
@@ -1037,7 +1044,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     const T* wo2 = static_cast<const T*>(a.st.wo2) + li * eO2;
     fetch_batch<T, NVD, 2, NT>(buf, w01, D, 0, min(kNBuf / (2 * NVD), sF.nw(wid)), rowF);
     load_act<T>(a.ll.x, nullptr, D, x_tag, gam[2], xs, red, no_side, r0,
-                r1, a.ll.err, a.trace, tp);
+                r1, a.ll.err, a.trace, tp, lcnt);
     gemv_rows<T, NVD, 2, NT>(buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, bool act, const float (&s)[2][2]) {
       const float g0 = gelu_t<T>(S::rnd(s[0][0])), g1 = gelu_t<T>(S::rnd(s[0][1]));
       if (act)
@@ -1048,7 +1055,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     // ---- down projection + residual
     fetch_batch<T, NVF, 1, NT>(buf, wo2, F, 0, min(kNBuf / NVF, sD.nw(wid)), rowD);
     load_act<T>(a.ll.h, nullptr, F, tag(base + kPhUp), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
-                a.ll.err, a.trace, tp);
+                a.ll.err, a.trace, tp, lcnt);
     if (CROSS && last) {
       // The temporal step's output leaves as plain pairs (no final norm).
       if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
@@ -1076,7 +1083,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     const T* hw = static_cast<const T*>(a.head_w);
     fetch_batch<T, NVD, 1, NT>(buf, hw, D, 0, min(kNBuf / NVD, sH.nw(wid)), rowH);
     load_act<T>(a.ll.x, nullptr, D, x_tag, gam[3], xs, red, no_side, r0, r1, a.ll.err,
-                a.trace, tp);
+                a.trace, tp, lcnt);
     if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
     gemv_rows<T, NVD, 1, NT>(buf, hw, D, sH.nw(wid), rowH, xs, [&](int t, bool act, const float (&s)[1][2]) {
       if (act) {
