@@ -60,6 +60,60 @@ def algorithmic_bytes(cfg, esz=2, rows=2, frames=50, enc_len=1006, codebook=1024
     return dict(depth_step=depth_step, temporal_step=temporal_step, chunk=total)
 
 
+def step_bytes(cfg, kind, pos, esz=2, rows=2, codebook=1024, enc_len=1006):
+    """Algorithmic bytes of one step launch at ring position `pos`: every weight
+    once, the level-sliced head (depth), the cross K/V (temporal), and the
+    self K/V slots read or written (pos history slots + the new one)."""
+    ab = algorithmic_bytes(cfg, esz=esz, rows=rows, enc_len=enc_len, codebook=codebook)
+    H = cfg.num_heads
+    layers = cfg.num_depth_layers if kind == "depth" else cfg.num_temporal_layers
+    kv = layers * 2 * rows * H * 64 * esz * (pos + 1)
+    return (ab["depth_step"] if kind == "depth" else ab["temporal_step"]) + kv
+
+
+def time_step_kernels(state, model, cfg, stream, esz, reps_depth=20, reps_temporal=2):
+    """Average launch duration of the persistent depth_step / temporal_step
+    kernels, timed with HIP events on the state's stream over back-to-back
+    launches (each API call is exactly one kernel launch)."""
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(7)
+    x = torch.randn(2, cfg.d_model, generator=g).to(device="cuda", dtype=model.torch_dtype)
+    logits = torch.empty(2, 1024, dtype=torch.float32, device="cuda")
+    out = torch.empty_like(x)
+    L, Fr = cfg.rvq_depth, 50
+    torch.cuda.synchronize()
+    res = {}
+    for kind, reps, n in (("depth", reps_depth, L), ("temporal", reps_temporal, Fr)):
+        def one_pass():
+            for i in range(n):
+                if kind == "depth":
+                    state.depth_step(x, i, level=i, out=logits, sync=False)
+                else:
+                    state.temporal_step(x, i, out=out, sync=False)
+        one_pass()  # warm
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            one_pass()
+        e1.record(stream)
+        e1.synchronize()
+        state.sync()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * n)
+        nbytes = float(np.mean([step_bytes(cfg, kind, p, esz=esz) for p in range(n)]))
+        res[kind] = {"us": us, "bytes": nbytes, "GBs": nbytes / (us * 1e-6) / 1e9, "launches": reps * n}
+    return res
+
+
+def load_traffic():
+    """HBM bytes per depth_step launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE
+    (profiles/depth_step_traffic.json), or None."""
+    p = ROOT / "profiles" / "depth_step_traffic.json"
+    try:
+        return float(json.loads(p.read_text())["bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(weights, cfg, enc_tokens, budget_s=20.0):
     """Time the numpy restatement (fp32) on a bounded sample of the same chunk."""
     import dataclasses
@@ -167,6 +221,12 @@ def main():
     print(f"[bench] chunk ms mean {mean_ms:.2f} p50 {percentile(ms, 50):.2f} p99 {percentile(ms, 99):.2f}; "
           f"gpu {gpu_mean:.2f} ms; {achieved:.0f} GB/s", file=sys.stderr, flush=True)
 
+    esz = 2 if args.dtype == "bf16" else 4
+    kern = time_step_kernels(sess.state, model, cfg, stream, esz)
+    dk = kern["depth"]
+    print(f"[bench] depth_step kernel {dk['us']:.2f} us ({dk['GBs']:.0f} GB/s); temporal_step kernel "
+          f"{kern['temporal']['us']:.2f} us ({kern['temporal']['GBs']:.0f} GB/s)", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu_baseline:
         enc = system.build_encoder_inputs(sess.context, scfg, style)
@@ -192,10 +252,16 @@ def main():
         "chunk_ms_p50": percentile(ms, 50),
         "chunk_ms_p99": percentile(ms, 99),
         "rtf": 2000.0 / mean_ms,
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "unit_of_work": "one chunk (encoder + 50 temporal + 800 depth steps)",
-                     "algorithmic_bytes": ab["chunk"]},
+        "roofline": {"bound": "hbm", "achieved": dk["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dk["GBs"] / HBM_PEAK_GBS, "traffic": load_traffic(),
+                     "kernel": "k_step<bf16, depth> (one depth_step: 4 layers + norm + 1024-row head slice)",
+                     "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
+                     "launches_timed": dk["launches"]},
+        "roofline_chunk": {"achieved": achieved, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                           "algorithmic_bytes": ab["chunk"],
+                           "unit_of_work": "one chunk (encoder + 50 temporal + 800 depth steps)"},
+        "temporal_step_kernel": {"launch_us": kern["temporal"]["us"], "achieved_GBs": kern["temporal"]["GBs"],
+                                 "algorithmic_bytes_per_launch": kern["temporal"]["bytes"]},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -363,16 +363,7 @@ void State::setup_persistent() {
   if (lds_t_ == 0 || lds_d_ == 0) return;
   persist_grid_ = grid;
   bph_ = bph;
-  const size_t D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads;
-  pair_bytes_ = 2 * esz();
-  p_tin = dalloc(D * pair_bytes_);
-  p_tout = dalloc(D * pair_bytes_);
-  p_din = dalloc(D * pair_bytes_);
-  p_fsum = dalloc(D * pair_bytes_);
-  p_in = dalloc(D * pair_bytes_);
-  p_out = dalloc(D * pair_bytes_);
-  (void)HD;
-  (void)FF;
+  const size_t H = c.num_heads;
   // Tagged hand-off words: x, q, k, v, at, h vectors, cross partials, logits,
   // then the epoch counter and the error flag.
   const size_t vec = kLLVecWords;
@@ -474,7 +465,7 @@ void State::reset_handoff() {
   MRT_HIP_CHECK(hipStreamSynchronize(stream));
 }
 
-void State::launch_temporal_p(const void* in_pairs, int f, void* out_pairs) {
+void State::launch_temporal_p(const void* in, int f, void* out) {
   const Config& c = m.cfg;
   StepArgs a{};
   if (d_trace_ && f == 1) a.trace = d_trace_;
@@ -490,14 +481,14 @@ void State::launch_temporal_p(const void* in_pairs, int f, void* out_pairs) {
   a.Lmax = F;
   a.bias_tab = m.tbias;
   a.buckets = m.tbuckets;
-  a.in = in_pairs;
-  a.out = out_pairs;
+  a.in = in;
+  a.out = out;
   a.S = S;
   a.ll = ll_bufs();
   launch_step(m.dt, a, persist_grid_, lds_t_, stream);
 }
 
-void State::launch_depth_p(const void* in_pairs, int l, const void* head_w, int head_rows, float* logits,
+void State::launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits,
                            const GenOpts* o, int frame, int level, float* rec_slice) {
   const Config& c = m.cfg;
   StepArgs a{};
@@ -514,7 +505,7 @@ void State::launch_depth_p(const void* in_pairs, int l, const void* head_w, int 
   a.Lmax = c.rvq_depth;
   a.bias_tab = m.dbias;
   a.buckets = m.dbuckets;
-  a.in = in_pairs;
+  a.in = in;
   a.S = S;
   a.dec_norm = m.dec_norm;
   a.head_w = head_w;
@@ -532,9 +523,9 @@ void State::launch_depth_p(const void* in_pairs, int l, const void* head_w, int 
     a.tokens = d_tokens;
     a.drawn = o->record_drawn;
     a.emb = m.emb;
-    a.next_in = p_din;
-    a.fsum = p_fsum;
-    a.fmean = p_tin;
+    a.next_in = d_in;
+    a.fsum = fsum;
+    a.fmean = t_in;
     a.noise = noise_ + (static_cast<size_t>(frame) * o->rvq_depth + level) * o->codebook;
   }
   a.ll = ll_bufs();
@@ -545,18 +536,17 @@ void State::enqueue_decode_p(const GenOpts& o) {
   const Config& c = m.cfg;
   const int D = c.d_model, C = o.codebook;
   const size_t row_bytes = static_cast<size_t>(rows) * D * esz();
-  embed_pairs(m.dt, m.emb, D, 0, p_tin, stream);  // frame 0 input: emb(PAD = 0)
+  embed_fill(m.dt, m.emb, D, 0, rows, t_in, stream);  // frame 0 input: emb(PAD = 0) on both rows
   gumbel_table(d_seed, o.num_frames, o.rvq_depth, C, noise_, stream);
   for (int f = 0; f < o.num_frames; ++f) {
-    launch_temporal_p(p_tin, f, p_tout);
-    if (o.record_temporal) pairs_to_rows(m.dt, p_tout, D, static_cast<char*>(o.record_temporal) + f * row_bytes, stream);
+    launch_temporal_p(t_in, f, t_out);
+    if (o.record_temporal) copy(static_cast<char*>(o.record_temporal) + f * row_bytes, t_out, row_bytes);
     for (int l = 0; l < o.rvq_depth; ++l) {
       const char* head = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset + C * l) * D * esz();
       float* rec = o.record_slices ? o.record_slices + (static_cast<size_t>(f) * o.rvq_depth + l) * rows * C : nullptr;
-      launch_depth_p(l == 0 ? p_tout : p_din, l, head, C, slice, &o, f, l, rec);
+      launch_depth_p(l == 0 ? t_out : d_in, l, head, C, slice, &o, f, l, rec);
     }
-    if (o.record_frame_mean)
-      pairs_to_rows(m.dt, p_tin, D, static_cast<char*>(o.record_frame_mean) + f * row_bytes, stream);
+    if (o.record_frame_mean) copy(static_cast<char*>(o.record_frame_mean) + f * row_bytes, t_in, row_bytes);
   }
 }
 
@@ -713,10 +703,7 @@ void State::temporal_step(const void* in, const void* enc, int f, void* out) {
     throw Error(1, "temporal_step: cache holds " + std::to_string(temporal_len_) + " entries, frame_idx " +
                        std::to_string(f));
   if (persistent()) {
-    const int D = m.cfg.d_model;
-    rows_to_pairs(m.dt, in, D, p_in, stream);
-    launch_temporal_p(p_in, f, p_out);
-    pairs_to_rows(m.dt, p_out, D, out, stream);
+    launch_temporal_p(in, f, out);
   } else {
     run_temporal(in, f, out);
   }
@@ -737,11 +724,10 @@ void State::depth_step(const void* in, int l, int level, int C, int off, float* 
                        std::to_string(l));
   if (persistent()) {
     const int D = c.d_model;
-    rows_to_pairs(m.dt, in, D, p_in, stream);
     const void* head = level >= 0
                            ? static_cast<const char*>(m.lm_head) + static_cast<size_t>(off + C * level) * D * esz()
                            : m.lm_head;
-    launch_depth_p(p_in, l, head, level >= 0 ? C : c.vocab_size, logits, nullptr, 0, 0, nullptr);
+    launch_depth_p(in, l, head, level >= 0 ? C : c.vocab_size, logits, nullptr, 0, 0, nullptr);
   } else {
     run_depth(in, l, level, C, off, logits);
   }

@@ -143,15 +143,12 @@ class State {
  private:
   // Persistent-kernel decode path (one launch per step).
   void setup_persistent();
-  void launch_temporal_p(const void* in_pairs, int f, void* out_pairs);
-  void launch_depth_p(const void* in_pairs, int l, const void* head_w, int head_rows, float* logits,
+  void launch_temporal_p(const void* in, int f, void* out);
+  void launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits,
                       const GenOpts* o, int frame, int level, float* rec_slice);
   void enqueue_decode_p(const GenOpts& o);
   void check_device_error();
   int persist_grid_ = 0, bph_ = 0;
-  size_t pair_bytes_ = 0;
-  void *p_tin = nullptr, *p_tout = nullptr, *p_din = nullptr, *p_fsum = nullptr, *p_in = nullptr,
-       *p_out = nullptr;
   void* ll_block_ = nullptr;
   size_t ll_words_ = 0;
   LLBufs ll_bufs() const;

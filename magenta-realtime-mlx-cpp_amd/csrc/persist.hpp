@@ -56,8 +56,8 @@ struct StepArgs {
   int pos, Lmax;  // ring slot written this step; ring size
   const void* bias_tab;
   const int* buckets;
-  const void* in;   // (D) row pairs (plain)
-  void* out;        // (D) row pairs (plain): temporal output
+  const void* in;   // (2, D) model-dtype rows (plain)
+  void* out;        // (2, D) rows: temporal output
   int S;            // encoder length
   // depth head
   const void* dec_norm;
@@ -72,9 +72,9 @@ struct StepArgs {
   int* tokens;
   int* drawn;
   const void* emb;
-  void* next_in;   // (D) pairs: embedding of the fed-back token
-  void* fsum;      // (D) pairs
-  void* fmean;     // (D) pairs: frame mean (next temporal input)
+  void* next_in;   // (2, D): embedding of the fed-back token on both rows
+  void* fsum;      // (D): running sum of the frame's token embeddings
+  void* fmean;     // (2, D): frame mean (next temporal input)
   float* rec_slice;  // optional copy of the logits
   const float* noise;  // Gumbel noise of this draw: (codebook) floats
   LLBufs ll;
@@ -100,10 +100,5 @@ void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t 
 // gumbel(seed, f, l, c) for f < frames, l < L, c < C.
 void gumbel_table(const uint64_t* seed, int frames, int L, int C, float* out, hipStream_t s);
 
-// (rows=2, D) model-dtype rows <-> (D) pairs.
-void rows_to_pairs(DType dt, const void* rows, int D, void* pairs, hipStream_t s);
-void pairs_to_rows(DType dt, const void* pairs, int D, void* rows, hipStream_t s);
-// pairs[d] = (emb[id, d], emb[id, d])
-void embed_pairs(DType dt, const void* emb, int D, int id, void* pairs, hipStream_t s);
 
 }  // namespace mrt

@@ -132,26 +132,6 @@ __device__ __forceinline__ float from_lane(float v, int src) {
   return src == (int)(threadIdx.x & 63) ? v : __shfl(v, src & 63, 64);
 }
 
-// Plain (rows 0/1) pair of one element: bf16 -> 32 bits, fp32 -> 64 bits.
-template <typename T>
-struct PairT;
-template <>
-struct PairT<bf16> {
-  using W = uint32_t;
-  __device__ static float lo(W w) { return bf2f(static_cast<bf16>(w & 0xffffu)); }
-  __device__ static float hi(W w) { return bf2f(static_cast<bf16>(w >> 16)); }
-  __device__ static W pack(float a, float b) { return (W)f2bf(a) | ((W)f2bf(b) << 16); }
-};
-template <>
-struct PairT<float> {
-  using W = uint64_t;
-  __device__ static float lo(W w) { return __uint_as_float(static_cast<uint32_t>(w)); }
-  __device__ static float hi(W w) { return __uint_as_float(static_cast<uint32_t>(w >> 32)); }
-  __device__ static W pack(float a, float b) {
-    return (W)__float_as_uint(a) | ((W)__float_as_uint(b) << 32);
-  }
-};
-
 // ---- tagged words -------------------------------------------------------------------
 
 __device__ __forceinline__ uint64_t ll_word(uint32_t payload, uint32_t tag) {
@@ -189,9 +169,10 @@ struct LL<float> {
 // buffer, or from the launch's plain input pairs when `plain` is set.
 struct Side {
   const uint64_t* ll;
-  const void* plain;
+  const void* plain;  // (2, stride) model-dtype rows
   uint32_t tag;
   int row;  // -1: nothing for this thread
+  int stride;
 };
 
 // Activation rows in LDS, stored in the model dtype (row 1 at +kMaxPersistK
@@ -215,7 +196,6 @@ struct Act {
 template <typename T>
 __device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t tag, float* xs, const Side& sd,
                                             float& r0, float& r1, int* err) {
-  using PT = PairT<T>;
   constexpr int kPer = kMaxPersistK / kPersistThreads;
   constexpr int NW = LL<T>::kWords;
   const int tid = threadIdx.x;
@@ -227,9 +207,9 @@ __device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t
     if (src != nullptr && tid + i * kPersistThreads < K) pend |= 1u << i;
   bool side_pend = sd.row >= 0 && sd.plain == nullptr;
   if (sd.row >= 0 && sd.plain != nullptr) {
-    const typename PT::W p = ld_g(static_cast<const typename PT::W*>(sd.plain) + sd.row);
-    r0 = PT::lo(p);
-    r1 = PT::hi(p);
+    const T* p = static_cast<const T*>(sd.plain);
+    r0 = St<T>::ld(ld_g(p + sd.row));
+    r1 = St<T>::ld(ld_g(p + sd.stride + sd.row));
   }
   uint32_t spins = 0;
   while (pend != 0 || side_pend) {
@@ -283,24 +263,27 @@ template <typename T>
 __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, int K, uint32_t tag, const T* g,
                                          float* xs, float* red, const Side& sd, float& r0, float& r1, int* err,
                                          uint64_t* trace, int& tp, int& lc) {
-  using PT = PairT<T>;
   using S = St<T>;
   constexpr int kPer = kMaxPersistK / kPersistThreads;
   constexpr int kG = 1024 / kPersistThreads;
   const int tid = threadIdx.x;
   if (trace != nullptr && blockIdx.x == 0 && tid == 0 && lc < 16) trace[kLoadTrace + lc] = wall_clock64();
   trace_point(trace, tp++);
-  if (plain != nullptr) {
-    typename PT::W w[kPer];
+  if (plain != nullptr) {  // (2, K) model-dtype rows
+    const T* p = static_cast<const T*>(plain);
+    T w0[kPer], w1[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int k = tid + i * kPersistThreads;
-      if (k < K) w[i] = ld_g(static_cast<const typename PT::W*>(plain) + k);
+      if (k < K) {
+        w0[i] = ld_g(p + k);
+        w1[i] = ld_g(p + K + k);
+      }
     }
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int k = tid + i * kPersistThreads;
-      if (k < K) Act<T>::put(xs, k, PT::lo(w[i]), PT::hi(w[i]));
+      if (k < K) Act<T>::put(xs, k, St<T>::ld(w0[i]), St<T>::ld(w1[i]));
     }
     ll_load_vec<T>(nullptr, 0, 0, xs, sd, r0, r1, err);
   } else {
@@ -714,20 +697,18 @@ __device__ __forceinline__ void cross_combine(const StepArgs& a, int h, uint32_t
 // byte-first radix select over LDS histograms.
 template <typename T>
 __device__ __forceinline__ void sample_block(const StepArgs& a, const float* lg, unsigned* hist, int* sel) {
-  using PT = PairT<T>;
-  using W = typename PT::W;
   using S = St<T>;
   constexpr int kPer = 1024 / kPersistThreads;  // candidates and d_model elements per thread
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const SampleParams& p = a.sp;
   const int C = p.codebook;
   // Loads that do not depend on the draw go first.
-  const W* fs_in = static_cast<const W*>(a.fsum);
+  const T* fs_in = static_cast<const T*>(a.fsum);
   float fv[kPer], gn[kPer];
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {
     const int d = tid + kPersistThreads * t;
-    fv[t] = (a.level != 0 && d < a.D) ? PT::lo(ld_g(fs_in + d)) : 0.f;
+    fv[t] = (a.level != 0 && d < a.D) ? S::ld(ld_g(fs_in + d)) : 0.f;
     gn[t] = d < C ? ld_g(a.noise + d) : 0.f;
   }
   const int teacher_id = a.teacher ? ld_g(a.teacher + a.slot) : 0;
@@ -836,19 +817,21 @@ __device__ __forceinline__ void sample_block(const StepArgs& a, const float* lg,
     ev[t] = d < a.D ? S::ld(ld_g(e + d)) : 0.f;
   }
   const float Lf = S::rnd((float)p.rvq_depth);
-  W* ni = static_cast<W*>(a.next_in);
-  W* fs = static_cast<W*>(a.fsum);
-  W* fm = static_cast<W*>(a.fmean);
+  T* ni = static_cast<T*>(a.next_in);
+  T* fs = static_cast<T*>(a.fsum);
+  T* fm = static_cast<T*>(a.fmean);
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {
     const int d = tid + kPersistThreads * t;
     if (d < a.D) {
       const float sum = (a.level == 0) ? ev[t] : S::rnd(fv[t] + ev[t]);
-      st_g(ni + d, PT::pack(ev[t], ev[t]));
-      st_g(fs + d, PT::pack(sum, sum));
+      st_g(ni + d, S::st(ev[t]));
+      st_g(ni + a.D + d, S::st(ev[t]));
+      st_g(fs + d, S::st(sum));
       if (a.level == p.rvq_depth - 1) {
-        const float m = S::rnd(sum / Lf);
-        st_g(fm + d, PT::pack(m, m));
+        const T m = S::st(sum / Lf);
+        st_g(fm + d, m);
+        st_g(fm + a.D + d, m);
       }
     }
   }
@@ -869,8 +852,6 @@ constexpr int kPhHead = 1000;
 
 template <typename T, bool CROSS>
 __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_step(StepArgs a) {
-  using PT = PairT<T>;
-  using W = typename PT::W;
   using S = St<T>;
   constexpr int V = S::kVec;
   constexpr bool NT = CROSS;
@@ -928,10 +909,10 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
 
   // residual element of the wave's D-row `lane` (lanes < nw)
   auto side_x = [&](const uint64_t* ll, const void* plain, uint32_t tg) {
-    Side s{ll, plain, tg, lane < sD.nw(wid) ? sD.row(wid, lane) : -1};
+    Side s{ll, plain, tg, lane < sD.nw(wid) ? sD.row(wid, lane) : -1, D};
     return s;
   };
-  const Side no_side{nullptr, nullptr, 0u, -1};
+  const Side no_side{nullptr, nullptr, 0u, -1, 0};
   float r0 = 0.f, r1 = 0.f;
   // lane t holds the residual element of the wave's row t (side_x)
   auto resid_put = [&](int t, bool act, const float (&s)[1][2], uint32_t tg) {
@@ -1061,9 +1042,11 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
       gemv_rows<T, NVF, 1, NT>(buf, wo2, F, sD.nw(wid), rowD, xs, [&](int t, bool act, const float (&s)[1][2]) {
         const float x0 = from_lane(r0, t), x1 = from_lane(r1, t);
-        if (act)
-          st_g(static_cast<W*>(a.out) + sD.row(wid, t),
-               PT::pack(S::rnd(x0 + S::rnd(s[0][0])), S::rnd(x1 + S::rnd(s[0][1]))));
+        if (act) {
+          T* o = static_cast<T*>(a.out) + sD.row(wid, t);
+          st_g(o, S::st(x0 + S::rnd(s[0][0])));
+          st_g(o + D, S::st(x1 + S::rnd(s[0][1])));
+        }
       });
     } else {
       gemv_rows<T, NVF, 1, NT>(buf, wo2, F, sD.nw(wid), rowD, xs,
@@ -1136,29 +1119,6 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   if (a.trace != nullptr && blk == 0 && threadIdx.x == 0) a.trace[kTraceDone] = wall_clock64();
 }
 
-template <typename T>
-__global__ void k_rows_to_pairs(const T* __restrict__ rows, int D, typename PairT<T>::W* __restrict__ pairs) {
-  for (int d = blockIdx.x * blockDim.x + threadIdx.x; d < D; d += gridDim.x * blockDim.x)
-    pairs[d] = PairT<T>::pack(St<T>::ld(rows[d]), St<T>::ld(rows[D + d]));
-}
-
-template <typename T>
-__global__ void k_pairs_to_rows(const typename PairT<T>::W* __restrict__ pairs, int D, T* __restrict__ rows) {
-  for (int d = blockIdx.x * blockDim.x + threadIdx.x; d < D; d += gridDim.x * blockDim.x) {
-    const auto w = pairs[d];
-    rows[d] = St<T>::st(PairT<T>::lo(w));
-    rows[D + d] = St<T>::st(PairT<T>::hi(w));
-  }
-}
-
-template <typename T>
-__global__ void k_embed_pairs(const T* __restrict__ emb, int D, int id, typename PairT<T>::W* __restrict__ pairs) {
-  for (int d = blockIdx.x * blockDim.x + threadIdx.x; d < D; d += gridDim.x * blockDim.x) {
-    const float e = St<T>::ld(emb[(size_t)id * D + d]);
-    pairs[d] = PairT<T>::pack(e, e);
-  }
-}
-
 template <typename T, bool CROSS>
 size_t lds_bytes() {
   return 4 * static_cast<size_t>(kRegion) * sizeof(T);
@@ -1219,39 +1179,6 @@ void gumbel_table(const uint64_t* seed, int frames, int L, int C, float* out, hi
   const int n = frames * L * C;
   const int blocks = std::min((n + 255) / 256, 1024);
   hipLaunchKernelGGL(k_gumbel_table, dim3(blocks), dim3(256), 0, s, seed, frames, L, C, out);
-  MRT_HIP_CHECK(hipGetLastError());
-}
-
-void rows_to_pairs(DType dt, const void* rows, int D, void* pairs, hipStream_t s) {
-  const int blocks = (D + 255) / 256;
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_rows_to_pairs<float>, dim3(blocks), dim3(256), 0, s, (const float*)rows, D,
-                       (uint64_t*)pairs);
-  else
-    hipLaunchKernelGGL(k_rows_to_pairs<bf16>, dim3(blocks), dim3(256), 0, s, (const bf16*)rows, D,
-                       (uint32_t*)pairs);
-  MRT_HIP_CHECK(hipGetLastError());
-}
-
-void pairs_to_rows(DType dt, const void* pairs, int D, void* rows, hipStream_t s) {
-  const int blocks = (D + 255) / 256;
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_pairs_to_rows<float>, dim3(blocks), dim3(256), 0, s, (const uint64_t*)pairs, D,
-                       (float*)rows);
-  else
-    hipLaunchKernelGGL(k_pairs_to_rows<bf16>, dim3(blocks), dim3(256), 0, s, (const uint32_t*)pairs, D,
-                       (bf16*)rows);
-  MRT_HIP_CHECK(hipGetLastError());
-}
-
-void embed_pairs(DType dt, const void* emb, int D, int id, void* pairs, hipStream_t s) {
-  const int blocks = (D + 255) / 256;
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_embed_pairs<float>, dim3(blocks), dim3(256), 0, s, (const float*)emb, D, id,
-                       (uint64_t*)pairs);
-  else
-    hipLaunchKernelGGL(k_embed_pairs<bf16>, dim3(blocks), dim3(256), 0, s, (const bf16*)emb, D, id,
-                       (uint32_t*)pairs);
   MRT_HIP_CHECK(hipGetLastError());
 }
 

@@ -263,29 +263,38 @@ class State:
             raise ValueError(f"tokens must be {(self.rows, self.enc_len)}, got {t.shape}")
         _check(self.lib, self.lib.mrt_df_encode(self._h, _i32_ptr(t)))
 
-    def temporal_step(self, frame_emb, frame_idx: int, enc_out=None, out=None):
+    def temporal_step(self, frame_emb, frame_idx: int, enc_out=None, out=None, sync: bool = True):
+        """One temporal step on the state's stream.  With sync=False the call only
+        enqueues: the inputs must already be complete and the caller orders later
+        reads of `out` after the state's stream."""
         torch = _torch()
         if out is None:
             out = torch.empty_like(frame_emb)
-        self._sync_torch()
+        if sync:
+            self._sync_torch()
         _check(self.lib, self.lib.mrt_df_temporal_step(
             self._h, _dptr(frame_emb), _dptr(enc_out) if enc_out is not None else None, frame_idx,
             _dptr(out)))
-        self.sync()
+        if sync:
+            self.sync()
         return out
 
     def depth_step(self, tok_emb, depth_idx: int, level: Optional[int] = None,
-                   codebook_size: int = 1024, codec_offset: int = 2, out=None):
+                   codebook_size: int = 1024, codec_offset: int = 2, out=None, sync: bool = True):
+        """One depth step; logits of the level slice (or the full vocabulary when
+        level is None).  sync=False as for temporal_step."""
         torch = _torch()
         cfg = self.model.config
         n = codebook_size if level is not None else cfg.vocab_size
         if out is None:
             out = torch.empty((self.rows, n), dtype=torch.float32, device=tok_emb.device)
-        self._sync_torch()
+        if sync:
+            self._sync_torch()
         _check(self.lib, self.lib.mrt_df_depth_step(
             self._h, _dptr(tok_emb), depth_idx, -1 if level is None else level, codebook_size,
             codec_offset, _dptr(out)))
-        self.sync()
+        if sync:
+            self.sync()
         return out
 
     def generate_tokens(self, enc_tokens: Optional[np.ndarray], opts: GenOptions,
