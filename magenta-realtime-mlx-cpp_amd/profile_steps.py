@@ -1,0 +1,72 @@
+"""Profiling driver: back-to-back depth_step / temporal_step launches at the
+benchmark dims plus a calibration copy of known size, for rocprofv3 counter
+runs (FETCH_SIZE / WRITE_SIZE per dispatch).
+
+    python magenta-realtime-mlx-cpp_amd/profile_steps.py [--reps N] [--copy-mib M]
+
+The copy (torch's device copy of M MiB, M above the 256 MB last-level cache)
+reads and writes exactly M MiB; its counter readings give the scale factor
+between the counters and bytes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import pathlib
+import sys
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+if str(HERE) not in sys.path:
+    sys.path.insert(0, str(HERE))
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--reps", type=int, default=4, help="passes over the 16 depth levels")
+    ap.add_argument("--copy-mib", type=int, default=1024, help="calibration copy size (above the 256 MB MALL)")
+    ap.add_argument("--seed", type=int, default=1234)
+    a = ap.parse_args()
+
+    import torch
+    import mrt_df
+    import synth_bundle
+    import system
+
+    cfg = mrt_df.Config.bench()
+    model = mrt_df.Depthformer(synth_bundle.make_weights(cfg, seed=a.seed, threads=16), cfg, dtype="bf16")
+    scfg = system.SystemConfig()
+    st = model.new_state(rows=2, max_frames=scfg.chunk_frames, enc_len=scfg.encoder_length)
+    rng = np.random.default_rng(42)
+    ctx = np.stack([rng.integers(0, 1024, scfg.context_frames) + 0 for _ in range(16)], axis=1)
+    style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+    st.encode(system.build_encoder_inputs(ctx, scfg, style))
+
+    n = a.copy_mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[profile] calibration copy: {a.copy_mib} MiB read + {a.copy_mib} MiB written", flush=True)
+
+    g = torch.Generator(device="cpu").manual_seed(7)
+    x = torch.randn(2, cfg.d_model, generator=g).to(device="cuda", dtype=torch.bfloat16)
+    logits = torch.empty(2, 1024, dtype=torch.float32, device="cuda")
+    out = torch.empty_like(x)
+    for _ in range(a.reps):
+        for l in range(cfg.rvq_depth):
+            st.depth_step(x, l, level=l, out=logits, sync=False)
+    st.sync()
+    print(f"[profile] {a.reps * cfg.rvq_depth} depth_step launches", flush=True)
+    for f in range(scfg.chunk_frames):
+        st.temporal_step(x, f, out=out, sync=False)
+    st.sync()
+    print(f"[profile] {scfg.chunk_frames} temporal_step launches", flush=True)
+    st.close()
+    model.close()
+
+
+if __name__ == "__main__":
+    main()
