@@ -1,0 +1,196 @@
+"""C-ABI boundary checks that need no GPU.
+
+The library must load and export every function include/mrt_df.h declares;
+the config helpers must return the reference's DepthformerConfig values
+(depthformer/model.cpp:34-48); and bundle / argument errors must come back
+as status codes with a message (the reference throws std::runtime_error /
+std::out_of_range at the same places: weights.cpp:129-130, model.cpp:216-218)
+before any device call is made.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import json
+import struct
+
+import numpy as np
+import pytest
+
+import mrt_df
+import synth_bundle
+
+MRT_ERR_INVALID, MRT_ERR_HIP, MRT_ERR_MISSING_KEY, MRT_ERR_FORMAT = 1, 3, 4, 5
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return mrt_df.load_library()
+
+
+def test_exports_every_header_function(lib):
+    names = mrt_df.header_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_header_functions_all_have_signatures(lib):
+    # every declared entry point is bound with explicit argtypes by the binding
+    for n in mrt_df.header_functions():
+        assert getattr(lib, n).argtypes is not None, n
+
+
+def _cfg(lib, which):
+    c = mrt_df._Config()
+    getattr(lib, f"mrt_df_config_{which}")(ctypes.byref(c))
+    return {f: getattr(c, f) for f in mrt_df.CONFIG_FIELDS}
+
+
+def test_config_base_matches_reference(lib):
+    # DepthformerConfig defaults (model.h:47-68) and base() (model.cpp:34-36)
+    c = _cfg(lib, "base")
+    assert c == dict(vocab_size=29824, d_model=768, d_kv=64, d_ff=2048, num_heads=12, num_encoder_layers=12,
+                     num_temporal_layers=20, num_depth_layers=4, max_encoder_length=1006, rvq_depth=16,
+                     temporal_num_buckets=128, temporal_max_distance=128, depth_num_buckets=16,
+                     depth_max_distance=16)
+
+
+def test_config_large_matches_reference(lib):
+    # large() as the reference defines it (model.cpp:38-48)
+    c = _cfg(lib, "large")
+    assert (c["d_model"], c["num_heads"], c["d_ff"]) == (1024, 16, 2816)
+    assert (c["num_encoder_layers"], c["num_temporal_layers"], c["num_depth_layers"]) == (24, 40, 8)
+    assert c["vocab_size"] == 29824 and c["rvq_depth"] == 16
+
+
+def test_error_message_is_per_call(lib):
+    c = mrt_df._Config()
+    code = lib.mrt_df_get_config(None, ctypes.byref(c), None)
+    assert code == MRT_ERR_INVALID and b"null" in lib.mrt_last_error()
+
+
+def _create_path(lib, path, cfg=None, dtype=mrt_df.DTYPE_BF16):
+    c = cfg.to_c() if cfg is not None else mrt_df.Config.tiny().to_c()
+    h = ctypes.c_void_p()
+    code = lib.mrt_df_create(str(path).encode(), ctypes.byref(c), dtype, 0, ctypes.byref(h))
+    return code, lib.mrt_last_error().decode(), h
+
+
+def test_missing_bundle_file(lib, tmp_path):
+    code, msg, h = _create_path(lib, tmp_path / "nope.safetensors")
+    assert code == MRT_ERR_MISSING_KEY and "not a file" in msg and not h.value
+
+
+def test_malformed_bundle(lib, tmp_path):
+    p = tmp_path / "bad.safetensors"
+    p.write_bytes(b"\x05\x00\x00\x00\x00\x00\x00\x00{oops")
+    code, msg, h = _create_path(lib, p)
+    assert code == MRT_ERR_FORMAT and not h.value, msg
+
+
+def test_bundle_offsets_out_of_range(lib, tmp_path):
+    hdr = json.dumps({"w": {"dtype": "F32", "shape": [4], "data_offsets": [0, 64]}}).encode()
+    p = tmp_path / "short.safetensors"
+    p.write_bytes(struct.pack("<Q", len(hdr)) + hdr + b"\x00" * 16)
+    code, msg, _ = _create_path(lib, p)
+    assert code == MRT_ERR_FORMAT and "out of range" in msg
+
+
+def test_bundle_missing_key(lib, tmp_path):
+    cfg = mrt_df.Config.tiny()
+    w = synth_bundle.make_weights(cfg, seed=1)
+    w.pop("decoder_norm.weight")
+    p = tmp_path / "partial.safetensors"
+    synth_bundle.write_bundle(p, w)
+    code, msg, _ = _create_path(lib, p, cfg)
+    assert code == MRT_ERR_MISSING_KEY and "decoder_norm.weight" in msg
+
+
+def test_bundle_shape_mismatch(lib, tmp_path):
+    cfg = mrt_df.Config.tiny()
+    w = synth_bundle.make_weights(cfg, seed=1)
+    w["lm_head.weight"] = w["lm_head.weight"][:-1]
+    p = tmp_path / "shape.safetensors"
+    synth_bundle.write_bundle(p, w)
+    code, msg, _ = _create_path(lib, p, cfg)
+    assert code == MRT_ERR_INVALID and "lm_head.weight" in msg
+
+
+def test_unsupported_head_dim(lib, tmp_path):
+    cfg = mrt_df.Config.tiny()
+    bad = dataclasses.replace(cfg, d_kv=32)
+    p = tmp_path / "any.safetensors"
+    synth_bundle.write_bundle(p, synth_bundle.make_weights(cfg, seed=1))
+    code, msg, _ = _create_path(lib, p, bad)
+    assert code == MRT_ERR_INVALID and "d_kv" in msg
+
+
+def test_unknown_dtype(lib, tmp_path):
+    cfg = mrt_df.Config.tiny()
+    p = tmp_path / "ok.safetensors"
+    synth_bundle.write_bundle(p, synth_bundle.make_weights(cfg, seed=1))
+    code, msg, _ = _create_path(lib, p, cfg, dtype=7)
+    assert code == MRT_ERR_INVALID and "dtype" in msg
+
+
+def test_valid_bundle_reaches_the_device(lib, tmp_path):
+    """A complete bundle passes every host check; without a GPU the first
+    device call fails with MRT_ERR_HIP, with one it loads."""
+    cfg = mrt_df.Config.tiny()
+    p = tmp_path / "tiny.safetensors"
+    synth_bundle.write_bundle(p, synth_bundle.make_weights(cfg, seed=1))
+    code, msg, h = _create_path(lib, p, cfg)
+    assert code in (0, MRT_ERR_HIP), msg
+    if code == 0:
+        lib.mrt_df_destroy(h)
+
+
+def test_null_arguments(lib):
+    c = mrt_df.Config.tiny().to_c()
+    h = ctypes.c_void_p()
+    assert lib.mrt_df_create(None, ctypes.byref(c), 1, 0, ctypes.byref(h)) == MRT_ERR_INVALID
+    assert lib.mrt_df_state_create(None, 2, 4, 8, ctypes.byref(h)) == MRT_ERR_INVALID
+    assert lib.mrt_df_sync(None) == MRT_ERR_INVALID
+    assert lib.mrt_df_encode(None, None) == MRT_ERR_INVALID
+    assert lib.mrt_df_depth_step(None, None, 0, 0, 8, 2, None) == MRT_ERR_INVALID
+    assert lib.mrt_df_temporal_step(None, None, None, 0, None) == MRT_ERR_INVALID
+    assert lib.mrt_df_generate_tokens(None, None, None, None) == MRT_ERR_INVALID
+    sz = ctypes.c_size_t()
+    assert lib.mrt_df_state_buffer_bytes(None, 0, ctypes.byref(sz)) == MRT_ERR_INVALID
+    assert lib.mrt_df_state_set_cache_length(None, 0, 0) == MRT_ERR_INVALID
+
+
+def test_create_from_tensors_rejects_bad_entries(lib):
+    cfg = mrt_df.Config.tiny().to_c()
+    h = ctypes.c_void_p()
+    names = (ctypes.c_char_p * 1)(None)
+    data = (ctypes.c_void_p * 1)(None)
+    shapes = (ctypes.c_void_p * 1)(None)
+    ndims = (ctypes.c_int32 * 1)(1)
+    code = lib.mrt_df_create_from_tensors(1, names, data, shapes, ndims, ctypes.byref(cfg), 1, 0,
+                                          ctypes.byref(h))
+    assert code == MRT_ERR_INVALID and b"bad tensor entry" in lib.mrt_last_error()
+
+
+def test_bundle_layout_matches_reference_keys():
+    """Key set of the bundle layout (model.cpp:177-198, modules.cpp:342-381) at the tiny dims."""
+    cfg = mrt_df.Config.tiny()
+    layout = dict(synth_bundle.bundle_layout(cfg))
+    keys = set(layout)
+    assert {"token_embedding.weight", "lm_head.weight", "encoder_norm.weight", "decoder_norm.weight",
+            "temporal_rel_pos.relative_attention_bias.weight",
+            "depth_rel_pos.relative_attention_bias.weight"} <= keys
+    for i in range(cfg.num_temporal_layers):
+        for k in ("pre_self_attn_norm", "self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                  "self_attn.o_proj", "pre_cross_attn_norm", "cross_attn.q_proj", "cross_attn.k_proj",
+                  "cross_attn.v_proj", "cross_attn.o_proj", "pre_ffn_norm", "ffn.wi_0", "ffn.wi_1", "ffn.wo"):
+            assert f"temporal_layers.{i}.{k}.weight" in keys
+    for i in range(cfg.num_depth_layers):
+        assert f"depth_layers.{i}.pre_self_attn_norm.weight" in keys
+        assert f"depth_layers.{i}.cross_attn.q_proj.weight" not in keys
+    assert tuple(layout["lm_head.weight"]) == (cfg.vocab_size, cfg.d_model)
+    assert tuple(layout["temporal_layers.0.ffn.wo.weight"]) == (cfg.d_model, cfg.d_ff)
+    assert np.prod(layout["temporal_rel_pos.relative_attention_bias.weight"]) == \
+        cfg.temporal_num_buckets * cfg.num_heads

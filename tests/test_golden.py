@@ -1,0 +1,115 @@
+"""Golden fixtures of the tiny config (tests/golden/tiny_decode.npz, written by
+tests/golden/make_golden.py from the oracle).
+
+CPU: the oracle still reproduces the committed fixture (regression pin of the
+restatement).  GPU: the HIP path, called through the C ABI, matches it to the
+path's tolerances: fp32 <= 1e-4 and bf16 <= 2e-2 norm-wise relative error,
+teacher tokens fed back bit-exactly, >= 99 % of the free-running fp32 draws
+equal; fp32 argmax agreement >= 99 %; bf16 >= 95 % with every disagreement a
+near-tie (top-1/top-2 margin within twice that draw's logit error: 8 codes
+per level leave such ties; >= 99 % is checked at the benchmark dims).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import importlib.util
+import pathlib
+
+import numpy as np
+import pytest
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+
+
+def rel(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def gen():
+    spec = importlib.util.spec_from_file_location("make_golden", GOLDEN / "make_golden.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@pytest.fixture(scope="module")
+def fx():
+    with np.load(GOLDEN / "tiny_decode.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def test_weights_generator_unchanged(gen, fx):
+    _, w, tok, teacher = gen.inputs()
+    np.testing.assert_allclose(gen.checksums(w), fx["weight_checksums"], rtol=1e-12, atol=1e-9)
+    np.testing.assert_array_equal(tok, fx["enc_tokens"])
+    np.testing.assert_array_equal(teacher, fx["teacher"])
+
+
+def test_oracle_reproduces_fixture(gen, fx):
+    new = gen.compute()
+    for k in ("enc_out", "temporal_out", "slices", "frame_mean"):
+        assert rel(new[f"fp32_tf_{k}"], fx[f"fp32_tf_{k}"]) <= 1e-5, k
+        assert rel(new[f"bf16_tf_{k}"], fx[f"bf16_tf_{k}"]) <= 1e-2, k
+    assert (new["fp32_free_tokens"] == fx["fp32_free_tokens"]).mean() >= 0.99
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,tol", [("fp32", 1e-4), ("bf16", 2e-2)])
+def test_hip_matches_fixture_teacher_forced(gpu_available, gen, fx, dtype, tol):
+    import torch
+    import mrt_df
+
+    cfg, w, tok, teacher = gen.inputs()
+    mcfg = mrt_df.Config(**dataclasses.asdict(cfg))
+    m = mrt_df.Depthformer(w, mcfg, dtype=dtype)
+    o = gen.options()
+    F, L, C = o.num_frames, o.rvq_depth, o.codebook_size
+    opts = mrt_df.GenOptions(num_frames=F, rvq_depth=L, temperature=o.temperature, top_k=o.top_k,
+                             guidance_weight=o.guidance_weight, seed=o.seed, codebook_size=C,
+                             codec_offset=o.codec_offset)
+    st = m.new_state(max_frames=F)
+    rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"),
+               temporal=torch.zeros((F, 2, mcfg.d_model), dtype=m.torch_dtype, device="cuda"),
+               frame_mean=torch.zeros((F, 2, mcfg.d_model), dtype=m.torch_dtype, device="cuda"))
+    toks = st.generate_tokens(tok, opts, teacher=teacher, record=rec)
+    np.testing.assert_array_equal(toks, teacher)
+    enc = st.read(mrt_df.BUF_ENC_OUT).float().cpu().numpy()
+    assert rel(enc, fx[f"{dtype}_tf_enc_out"]) <= tol
+    sl = rec["slices"].cpu().numpy()
+    assert rel(rec["temporal"].float().cpu().numpy(), fx[f"{dtype}_tf_temporal_out"]) <= tol
+    assert rel(sl, fx[f"{dtype}_tf_slices"]) <= tol
+    g = 5.0
+    gl = (1 + g) * sl[:, :, 0] - g * sl[:, :, 1]
+    ol = (1 + g) * fx[f"{dtype}_tf_slices"][:, :, 0] - g * fx[f"{dtype}_tf_slices"][:, :, 1]
+    ga, oa = np.argmax(gl, -1), np.argmax(ol, -1)
+    if dtype == "fp32":
+        assert (ga == oa).mean() >= 0.99
+    else:
+        # 8 candidates and guidance 5 leave near-ties at this size: every draw whose
+        # top-1/top-2 margin exceeds the bf16 error of the guided logits must agree
+        # (the >= 99 % criterion itself is checked at the benchmark dims).
+        top2 = np.sort(ol, -1)
+        margin = top2[..., -1] - top2[..., -2]
+        err = np.abs(gl - ol).max(-1)  # per-draw error of the guided logits
+        flips = ga != oa
+        assert (margin[flips] <= 2 * err[flips]).all(), (margin[flips], err[flips])  # near-ties only
+        assert (~flips).mean() >= 0.95
+    np.testing.assert_array_equal(rec["frame_mean"].float().cpu().numpy(), fx[f"{dtype}_tf_frame_mean"])
+
+
+@pytest.mark.gpu
+def test_hip_matches_fixture_free_running_fp32(gpu_available, gen, fx):
+    import mrt_df
+
+    cfg, w, tok, _ = gen.inputs()
+    m = mrt_df.Depthformer(w, mrt_df.Config(**dataclasses.asdict(cfg)), dtype="fp32")
+    o = gen.options(seed=2024)
+    opts = mrt_df.GenOptions(num_frames=o.num_frames, rvq_depth=o.rvq_depth, temperature=o.temperature,
+                             top_k=o.top_k, guidance_weight=o.guidance_weight, seed=o.seed,
+                             codebook_size=o.codebook_size, codec_offset=o.codec_offset)
+    toks = m.new_state(max_frames=o.num_frames).generate_tokens(tok, opts)
+    assert (toks == fx["fp32_free_tokens"]).mean() >= 0.99, (toks, fx["fp32_free_tokens"])

