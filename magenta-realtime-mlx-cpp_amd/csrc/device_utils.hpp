@@ -86,30 +86,9 @@ __device__ __forceinline__ uint32_t philox_x0(uint32_t c0, uint32_t c1, uint32_t
   return c0;
 }
 
-// ---- grid-wide barrier for persistent kernels --------------------------------
-// Monotonic arrival counter: barrier number ``k`` of a launch completes when
-// the counter reaches (k + 1) * gridDim.x.  Every spin is bounded: past
-// ``kSpinLimit`` polls the block records an error in ``*err`` and proceeds, so
-// a barrier can never hang the device (the host reports the error).
+// Polls of the persistent kernels give up (and flag an error for the host)
+// after this many rounds, so no wait can hang the device.
 constexpr uint32_t kSpinLimit = 1u << 20;
-
-__device__ __forceinline__ void grid_barrier(uint32_t* bar, uint32_t target, int* err) {
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();  // release this block's writes device-wide
-    __hip_atomic_fetch_add(bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t spins = 0;
-    while (__hip_atomic_load(bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-    __threadfence();  // acquire: later loads see other blocks' writes
-  }
-  __syncthreads();
-}
 
 constexpr uint32_t kSampleStreamTag = 0x4D525444u;
 
