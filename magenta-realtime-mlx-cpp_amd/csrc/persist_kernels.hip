@@ -127,6 +127,13 @@ __device__ __forceinline__ int dpp_min_i(int v) {
   return __builtin_amdgcn_readlane(v, 63);
 }
 
+// 1/sqrt(x) for x > 0: the hardware estimate refined by one Newton-Raphson
+// step, y (1.5 - x y^2 / 2), to about 1 ulp.
+__device__ __forceinline__ float rsqrt_nr(float x) {
+  const float y = __builtin_amdgcn_rsqf(x);
+  return y * fmaf(-0.5f * x * y, y, 1.5f);
+}
+
 // Value of `v` held by lane `src` (src - lane is wave-uniform).
 __device__ __forceinline__ float from_lane(float v, int src) {
   return src == (int)(threadIdx.x & 63) ? v : __shfl(v, src & 63, 64);
@@ -189,21 +196,22 @@ struct Act {
   }
 };
 
-// Polls elements k = tid + 256 i (k < K) of a tagged vector until each word
-// carries `tag` and stores both rows to activation element k; the
-// side element (if any) is returned in r0/r1.  All loads of one round are
+// Polls elements k = tid + 256 i (i < NPER, k < K) of a tagged vector until
+// each word carries `tag`.  KEEP: both rows of element i go to v0[i] / v1[i];
+// otherwise they are stored to activation element k in LDS as they arrive.
+// The side element (if any) is returned in r0/r1.  All loads of one round are
 // issued before any is waited for.
-template <typename T>
-__device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t tag, float* xs, const Side& sd,
-                                            float& r0, float& r1, int* err) {
-  constexpr int kPer = kMaxPersistK / kPersistThreads;
+template <typename T, int NPER, bool KEEP>
+__device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t tag, float* xs,
+                                            float (&v0)[NPER], float (&v1)[NPER], const Side& sd, float& r0,
+                                            float& r1, int* err) {
   constexpr int NW = LL<T>::kWords;
   const int tid = threadIdx.x;
-  uint64_t w[kPer][NW];
+  uint64_t w[NPER][NW];
   uint64_t sw[NW];
   uint32_t pend = 0;
 #pragma unroll
-  for (int i = 0; i < kPer; ++i)
+  for (int i = 0; i < NPER; ++i)
     if (src != nullptr && tid + i * kPersistThreads < K) pend |= 1u << i;
   bool side_pend = sd.row >= 0 && sd.plain == nullptr;
   if (sd.row >= 0 && sd.plain != nullptr) {
@@ -214,7 +222,7 @@ __device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t
   uint32_t spins = 0;
   while (pend != 0 || side_pend) {
 #pragma unroll
-    for (int i = 0; i < kPer; ++i)
+    for (int i = 0; i < NPER; ++i)
       if ((pend >> i) & 1u)
 #pragma unroll
         for (int r = 0; r < NW; ++r) w[i][r] = aload(src + LL<T>::idx(tid + i * kPersistThreads, r));
@@ -222,13 +230,18 @@ __device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t
 #pragma unroll
       for (int r = 0; r < NW; ++r) sw[r] = aload(sd.ll + LL<T>::idx(sd.row, r));
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
+    for (int i = 0; i < NPER; ++i) {
       if ((pend >> i) & 1u) {
         bool ok = true;
 #pragma unroll
         for (int r = 0; r < NW; ++r) ok = ok && ll_tag(w[i][r]) == tag;
         if (ok) {
-          Act<T>::put(xs, tid + i * kPersistThreads, LL<T>::get(w[i], 0), LL<T>::get(w[i], 1));
+          if constexpr (KEEP) {
+            v0[i] = LL<T>::get(w[i], 0);
+            v1[i] = LL<T>::get(w[i], 1);
+          } else {
+            Act<T>::put(xs, tid + i * kPersistThreads, LL<T>::get(w[i], 0), LL<T>::get(w[i], 1));
+          }
           pend &= ~(1u << i);
         }
       }
@@ -256,24 +269,25 @@ __device__ __forceinline__ void trace_point(uint64_t* trace, int slot) {
   if (trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0 && slot < kLoadTrace) trace[slot] = wall_clock64();
 }
 
-// Loads the activation vector of a phase into xs (tagged, or the launch's
-// plain input pairs), with an optional side element and RMS norm with the
-// LDS-staged weight g (modules.cpp:72-84; normed vectors have K <= 1024).
-template <typename T>
+// Loads the activation vector of a phase (K <= 256 * NPER elements; tagged,
+// or the launch's plain input rows) into LDS, with an optional side element.
+// NORM: RMS norm with the LDS-staged weight g (modules.cpp:72-84): the sum of
+// squares is taken from the polled values in registers, and each element is
+// written to LDS once, normalised.
+template <typename T, int NPER, bool NORM>
 __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, int K, uint32_t tag, const T* g,
                                          float* xs, float* red, const Side& sd, float& r0, float& r1, int* err,
                                          uint64_t* trace, int& tp, int& lc) {
   using S = St<T>;
-  constexpr int kPer = kMaxPersistK / kPersistThreads;
-  constexpr int kG = 1024 / kPersistThreads;
   const int tid = threadIdx.x;
   if (trace != nullptr && blockIdx.x == 0 && tid == 0 && lc < 16) trace[kLoadTrace + lc] = wall_clock64();
   trace_point(trace, tp++);
+  float v0[NPER], v1[NPER];
   if (plain != nullptr) {  // (2, K) model-dtype rows
     const T* p = static_cast<const T*>(plain);
-    T w0[kPer], w1[kPer];
+    T w0[NPER], w1[NPER];
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
+    for (int i = 0; i < NPER; ++i) {
       const int k = tid + i * kPersistThreads;
       if (k < K) {
         w0[i] = ld_g(p + k);
@@ -281,28 +295,30 @@ __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, 
       }
     }
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
+    for (int i = 0; i < NPER; ++i) {
       const int k = tid + i * kPersistThreads;
-      if (k < K) Act<T>::put(xs, k, St<T>::ld(w0[i]), St<T>::ld(w1[i]));
+      if (k < K) {
+        v0[i] = S::ld(w0[i]);
+        v1[i] = S::ld(w1[i]);
+        if constexpr (!NORM) Act<T>::put(xs, k, v0[i], v1[i]);
+      }
     }
-    ll_load_vec<T>(nullptr, 0, 0, xs, sd, r0, r1, err);
+    ll_load_vec<T, NPER, NORM>(nullptr, 0, 0, xs, v0, v1, sd, r0, r1, err);
   } else {
-    ll_load_vec<T>(ll, K, tag, xs, sd, r0, r1, err);
+    ll_load_vec<T, NPER, NORM>(ll, K, tag, xs, v0, v1, sd, r0, r1, err);
   }
   __builtin_amdgcn_s_waitcnt(0);  // LDS copies issued by this wave (norm weights) have landed
   if (trace != nullptr && blockIdx.x == 0 && (tid & 63) == 0 && lc < 16) trace[kWaveTrace + 4 * lc + (tid >> 6)] = wall_clock64();
   ++lc;
   trace_point(trace, tp++);
-  if (g != nullptr) {
-    // Each thread squares the elements it wrote itself: no barrier needed yet.
+  if constexpr (NORM) {
+    const float inv_k = 1.0f / (float)K;
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < kG; ++i) {
-      const int k = tid + i * kPersistThreads;
-      if (k < K) {
-        const float x0 = Act<T>::get(xs, 0, k), x1 = Act<T>::get(xs, 1, k);
-        s0 = fmaf(x0, x0, s0);
-        s1 = fmaf(x1, x1, s1);
+    for (int i = 0; i < NPER; ++i) {
+      if (tid + i * kPersistThreads < K) {
+        s0 = fmaf(v0[i], v0[i], s0);
+        s1 = fmaf(v1[i], v1[i], s1);
       }
     }
     s0 = dpp_sum(s0);
@@ -313,16 +329,18 @@ __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, 
       red[4 + wid] = s1;
     }
     __syncthreads();
-    const float inv0 = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)K + 1e-6f);
-    const float inv1 = 1.0f / sqrtf((red[4] + red[5] + red[6] + red[7]) / (float)K + 1e-6f);
+    float gk[NPER];
 #pragma unroll
-    for (int i = 0; i < kG; ++i) {
+    for (int i = 0; i < NPER; ++i) {
       const int k = tid + i * kPersistThreads;
-      if (k < K) {
-        const float gk = S::ld(g[k]);
-        Act<T>::put(xs, k, S::rnd(S::rnd(Act<T>::get(xs, 0, k) * inv0) * gk),
-                    S::rnd(S::rnd(Act<T>::get(xs, 1, k) * inv1) * gk));
-      }
+      gk[i] = k < K ? S::ld(g[k]) : 0.f;
+    }
+    const float inv0 = rsqrt_nr((red[0] + red[1] + red[2] + red[3]) * inv_k + 1e-6f);
+    const float inv1 = rsqrt_nr((red[4] + red[5] + red[6] + red[7]) * inv_k + 1e-6f);
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+      const int k = tid + i * kPersistThreads;
+      if (k < K) Act<T>::put(xs, k, S::rnd(S::rnd(v0[i] * inv0) * gk[i]), S::rnd(S::rnd(v1[i] * inv1) * gk[i]));
     }
   }
   __syncthreads();
@@ -857,7 +875,11 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   constexpr bool NT = CROSS;
   constexpr int NVD = (1024 + V * 64 - 1) / (V * 64);  // K <= 1024
   constexpr int NVF = 3 * NVD;                         // K <= 3072
-  __shared__ float xs[2 * kMaxPersistK];
+  // Activation rows, double-buffered by phase: a wave that starts polling the
+  // next phase writes the other buffer while slower waves still read this one.
+  __shared__ float xsb[2][2 * kMaxPersistK];
+  float* xs = xsb[0];
+  int xsel = 0;
   __shared__ float red[8];
   __shared__ float sm[704];
   __shared__ float kvst[2][2][16];  // [k|v][row][d within this workgroup's slice]
@@ -899,7 +921,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   // Layer 0's QKV weights first: they take longest to arrive.
   if (a.nlayers > 0) fetch_batch<T, NVD, 1, NT>(buf, wqkv0, D, 0, min(kNBuf / NVD, nqkv), qkv_row);
   // Activation elements past a vector's end meet zero weights: keep them finite.
-  for (int k = threadIdx.x; k < 2 * kMaxPersistK; k += kPersistThreads) xs[k] = 0.f;
+  for (int k = threadIdx.x; k < 2 * kMaxPersistK; k += kPersistThreads) xsb[0][k] = xsb[1][k] = 0.f;
   __syncthreads();
   if (aload(a.ll.err) != 0) return;  // a previous launch failed: do nothing
   const uint32_t ep = aload(a.ll.seq);
@@ -947,7 +969,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     };
     if (CROSS && jpart != 0) stage_cross();
     // ---- QKV of head h's slice (weights already in flight)
-    load_act<T>(a.ll.x, first ? a.in : nullptr, D, x_tag, gam[0], xs,
+    xs = xsb[++xsel & 1];
+    load_act<T, 4, true>(a.ll.x, first ? a.in : nullptr, D, x_tag, gam[0], xs,
                 red, no_side, r0, r1, a.ll.err, a.trace, tp, lcnt);
     gemv_rows<T, NVD, 1, NT>(buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs,
                              [&](int t, bool act, const float (&s)[1][2]) {
@@ -989,7 +1012,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     }
     fetch_batch<T, NVD, 1, NT>(buf, wo, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
     // ---- attention output projection + residual
-    load_act<T>(a.ll.at, nullptr, HD, tag(base + kPhAtt), nullptr, xs, red,
+    xs = xsb[++xsel & 1];
+    load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhAtt), nullptr, xs, red,
                 side_x(a.ll.x, first ? a.in : nullptr, x_tag), r0, r1, a.ll.err, a.trace, tp, lcnt);
     gemv_rows<T, NVD, 1, NT>(buf, wo, HD, sD.nw(wid), rowD, xs,
                              [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhO)); });
@@ -1000,7 +1024,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       const T* wqc = static_cast<const T*>(a.st.wq_c) + li * eQc;
       const T* woc = static_cast<const T*>(a.st.wo_c) + li * eO;
       fetch_batch<T, NVD, 1, NT>(buf, wqc, D, 0, min(kNBuf / NVD, ncq), cq_row);
-      load_act<T>(a.ll.x, nullptr, D, x_tag, gam[1], xs, red, no_side,
+      xs = xsb[++xsel & 1];
+      load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gam[1], xs, red, no_side,
                   r0, r1, a.ll.err, a.trace, tp, lcnt);
       gemv_rows<T, NVD, 1, NT>(buf, wqc, D, ncq, cq_row, xs, [&](int t, bool act, const float (&s)[1][2]) {
         if (act) LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(s[0][0]), S::rnd(s[0][1]), tag(base + kPhCQ));
@@ -1013,7 +1038,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
         cross_combine<T>(a, h, tag(base + kPhCP), tag(base + kPhCC), sm);
         MRT_TP;
       }
-      load_act<T>(a.ll.at, nullptr, HD, tag(base + kPhCC), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
+      xs = xsb[++xsel & 1];
+      load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhCC), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
                   a.ll.err, a.trace, tp, lcnt);
       gemv_rows<T, NVD, 1, NT>(buf, woc, HD, sD.nw(wid), rowD, xs,
                                [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhCO)); });
@@ -1024,7 +1050,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     const T* w01 = static_cast<const T*>(a.st.w01) + li * e01;
     const T* wo2 = static_cast<const T*>(a.st.wo2) + li * eO2;
     fetch_batch<T, NVD, 2, NT>(buf, w01, D, 0, min(kNBuf / (2 * NVD), sF.nw(wid)), rowF);
-    load_act<T>(a.ll.x, nullptr, D, x_tag, gam[2], xs, red, no_side, r0,
+    xs = xsb[++xsel & 1];
+    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gam[2], xs, red, no_side, r0,
                 r1, a.ll.err, a.trace, tp, lcnt);
     gemv_rows<T, NVD, 2, NT>(buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, bool act, const float (&s)[2][2]) {
       const float g0 = gelu_t<T>(S::rnd(s[0][0])), g1 = gelu_t<T>(S::rnd(s[0][1]));
@@ -1035,7 +1062,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     MRT_TP;
     // ---- down projection + residual
     fetch_batch<T, NVF, 1, NT>(buf, wo2, F, 0, min(kNBuf / NVF, sD.nw(wid)), rowD);
-    load_act<T>(a.ll.h, nullptr, F, tag(base + kPhUp), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
+    xs = xsb[++xsel & 1];
+    load_act<T, kMaxPersistK / kPersistThreads, false>(a.ll.h, nullptr, F, tag(base + kPhUp), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
                 a.ll.err, a.trace, tp, lcnt);
     if (CROSS && last) {
       // The temporal step's output leaves as plain pairs (no final norm).
@@ -1065,7 +1093,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     auto rowH = [&](int t, int) { return sH.row(wid, t); };
     const T* hw = static_cast<const T*>(a.head_w);
     fetch_batch<T, NVD, 1, NT>(buf, hw, D, 0, min(kNBuf / NVD, sH.nw(wid)), rowH);
-    load_act<T>(a.ll.x, nullptr, D, x_tag, gam[3], xs, red, no_side, r0, r1, a.ll.err,
+    xs = xsb[++xsel & 1];
+    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gam[3], xs, red, no_side, r0, r1, a.ll.err,
                 a.trace, tp, lcnt);
     if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
     gemv_rows<T, NVD, 1, NT>(buf, hw, D, sH.nw(wid), rowH, xs, [&](int t, bool act, const float (&s)[1][2]) {
