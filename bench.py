@@ -71,6 +71,17 @@ def step_bytes(cfg, kind, pos, esz=2, rows=2, codebook=1024, enc_len=1006):
     return (ab["depth_step"] if kind == "depth" else ab["temporal_step"]) + kv
 
 
+def frame_bytes(cfg, f, esz=2, rows=2, codebook=1024, enc_len=1006):
+    """Algorithmic bytes of one frame launch (frame f of the chunk): the
+    temporal step at ring position f, the rvq_depth depth steps at positions
+    0..L-1, the Gumbel noise of the frame's draws (L x codebook fp32) and the
+    L - 1 fed-back embedding rows."""
+    L = cfg.rvq_depth
+    b = step_bytes(cfg, "temporal", f, esz=esz, rows=rows, codebook=codebook, enc_len=enc_len)
+    b += sum(step_bytes(cfg, "depth", l, esz=esz, rows=rows, codebook=codebook, enc_len=enc_len) for l in range(L))
+    return b + L * codebook * 4 + (L - 1) * cfg.d_model * esz
+
+
 def time_step_kernels(state, model, cfg, stream, esz, reps_depth=20, reps_temporal=2):
     """Average launch duration of the persistent depth_step / temporal_step
     kernels, timed with HIP events on the state's stream over back-to-back
@@ -104,10 +115,10 @@ def time_step_kernels(state, model, cfg, stream, esz, reps_depth=20, reps_tempor
     return res
 
 
-def load_traffic():
-    """HBM bytes per depth_step launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE
-    (profiles/depth_step_traffic.json), or None."""
-    p = ROOT / "profiles" / "depth_step_traffic.json"
+def load_traffic(name):
+    """HBM bytes per launch of a kernel measured with rocprofv3 FETCH_SIZE /
+    WRITE_SIZE, scaled by a copy of known size (profiles/<name>.json), or None."""
+    p = ROOT / "profiles" / f"{name}.json"
     try:
         return float(json.loads(p.read_text())["bytes_per_launch"])
     except (OSError, KeyError, ValueError):
@@ -200,7 +211,8 @@ def main():
         print(f"[bench] warmup chunk {i}: {(time.perf_counter() - t0) * 1e3:.1f} ms", file=sys.stderr, flush=True)
 
     torch.cuda.synchronize()
-    wall, gpu = [], []
+    wall, gpu, dec = [], [], []
+    launches = 0
     t_all = time.perf_counter()
     for i in range(args.steps):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -211,6 +223,8 @@ def main():
         e1.synchronize()
         wall.append((time.perf_counter() - t0) * 1e3)
         gpu.append(e0.elapsed_time(e1))
+        d_ms, launches = sess.state.decode_time()  # HIP events on the state's stream (library side)
+        dec.append(d_ms)
     torch.cuda.synchronize()
     total_s = time.perf_counter() - t_all
     ms = sorted(wall)
@@ -222,10 +236,32 @@ def main():
           f"gpu {gpu_mean:.2f} ms; {achieved:.0f} GB/s", file=sys.stderr, flush=True)
 
     esz = 2 if args.dtype == "bf16" else 4
+    frames = sess.opts.num_frames
+    if launches == frames:  # one persistent launch per frame
+        fb = float(np.mean([frame_bytes(cfg, f, esz=esz) for f in range(frames)]))
+        f_us = float(np.mean(dec)) * 1e3 / frames
+        roof = {"bound": "hbm", "achieved": fb / (f_us * 1e-6) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "traffic": load_traffic("frame_kernel_traffic"),
+                "kernel": f"k_frame<{args.dtype}> (one frame: temporal step 20L + 16 x (depth step 4L + "
+                          "norm + 1024-row head slice + draw))",
+                "algorithmic_bytes_per_launch": fb, "launch_us": f_us, "launches_timed": frames * args.steps,
+                "timing": "HIP events around the decode section of each timed chunk (frame launches + one "
+                          "Gumbel-table kernel per chunk) / frames"}
+        roof["frac"] = roof["achieved"] / HBM_PEAK_GBS
+        print(f"[bench] frame kernel {f_us:.1f} us/launch ({roof['achieved']:.0f} GB/s); decode "
+              f"{np.mean(dec):.2f} ms/chunk", file=sys.stderr, flush=True)
+    else:
+        roof = None
     kern = time_step_kernels(sess.state, model, cfg, stream, esz)
     dk = kern["depth"]
     print(f"[bench] depth_step kernel {dk['us']:.2f} us ({dk['GBs']:.0f} GB/s); temporal_step kernel "
           f"{kern['temporal']['us']:.2f} us ({kern['temporal']['GBs']:.0f} GB/s)", file=sys.stderr, flush=True)
+    if roof is None:  # one launch per step: the depth step kernel dominates
+        roof = {"bound": "hbm", "achieved": dk["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": dk["GBs"] / HBM_PEAK_GBS, "traffic": load_traffic("depth_step_traffic"),
+                "kernel": f"k_step<{args.dtype}, depth> (one depth_step: 4 layers + norm + 1024-row head slice)",
+                "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
+                "launches_timed": dk["launches"]}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -252,14 +288,14 @@ def main():
         "chunk_ms_p50": percentile(ms, 50),
         "chunk_ms_p99": percentile(ms, 99),
         "rtf": 2000.0 / mean_ms,
-        "roofline": {"bound": "hbm", "achieved": dk["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": dk["GBs"] / HBM_PEAK_GBS, "traffic": load_traffic(),
-                     "kernel": "k_step<bf16, depth> (one depth_step: 4 layers + norm + 1024-row head slice)",
-                     "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
-                     "launches_timed": dk["launches"]},
+        "roofline": roof,
         "roofline_chunk": {"achieved": achieved, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                            "algorithmic_bytes": ab["chunk"],
                            "unit_of_work": "one chunk (encoder + 50 temporal + 800 depth steps)"},
+        "decode_ms_per_chunk": float(np.mean(dec)),
+        "depth_step_kernel": {"launch_us": dk["us"], "achieved_GBs": dk["GBs"],
+                              "algorithmic_bytes_per_launch": dk["bytes"],
+                              "traffic": load_traffic("depth_step_traffic")},
         "temporal_step_kernel": {"launch_us": kern["temporal"]["us"], "achieved_GBs": kern["temporal"]["GBs"],
                                  "algorithmic_bytes_per_launch": kern["temporal"]["bytes"]},
         "cpu_baseline": cpu,

@@ -154,6 +154,16 @@ int mrt_df_generate_tokens(mrt_df_state* st, const int32_t* enc_tokens, const mr
 int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts* opts, int frame,
                         int level, int32_t* token);
 
+/* Instrumentation, no counterpart in the reference (its CLI times whole
+ * chunks on the host, cli/main.cpp:459-505): GPU time in ms of the decode
+ * section of the last mrt_df_generate_tokens call on this state -- the
+ * Gumbel noise table and the decode launches after the encoder -- from HIP
+ * events recorded on the state's stream.  *launches (may be NULL) receives
+ * the number of persistent-kernel launches in it: num_frames with the frame
+ * kernel, num_frames * (1 + rvq_depth) with one launch per step, 0 on the
+ * per-layer path.  Waits for the section to finish. */
+int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches);
+
 /* State buffers exposed for parity checks (device-to-device copies). */
 #define MRT_BUF_ENC_OUT 0     /* (rows, enc_len, d_model)                       */
 #define MRT_BUF_CROSS_K 1     /* layer: (rows, heads, enc_len, d_kv)            */

@@ -221,6 +221,13 @@ int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts
   });
 }
 
+int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches) {
+  return guarded([&] {
+    if (!ms) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *ms = S(st).last_decode_ms(launches);
+  });
+}
+
 int mrt_df_state_buffer_bytes(mrt_df_state* st, int which, size_t* bytes) {
   return guarded([&] {
     if (!bytes) throw mrt::Error(MRT_ERR_INVALID, "null argument");

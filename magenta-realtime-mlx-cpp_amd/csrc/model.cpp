@@ -358,11 +358,20 @@ void State::setup_persistent() {
                   F <= kMaxPersistLen && c.rvq_depth <= kMaxPersistLen && S <= kMaxCrossChunk * bph && c.d_model >= grid &&
                   c.d_ff >= grid;
   if (!ok) return;
-  lds_t_ = persist_prepare(m.dt, true, m.device);
-  lds_d_ = persist_prepare(m.dt, false, m.device);
+  lds_t_ = persist_prepare(m.dt, PersistKernel::Temporal, m.device);
+  lds_d_ = persist_prepare(m.dt, PersistKernel::Depth, m.device);
   if (lds_t_ == 0 || lds_d_ == 0) return;
   persist_grid_ = grid;
   bph_ = bph;
+  // The frame kernel keeps the depth history in LDS and numbers the phases of
+  // a whole frame in one tag space.
+  const int codes = 16 * (c.num_temporal_layers + 1) + 16 * c.rvq_depth * (c.num_depth_layers + 1);
+  const char* fk = std::getenv("MRT_FRAME_KERNEL");
+  if (!(fk && std::string(fk) == "0") && c.num_depth_layers * c.rvq_depth <= kMaxResidentSlots &&
+      codes <= (1 << kTagShift)) {
+    lds_f_ = persist_prepare(m.dt, PersistKernel::Frame, m.device);
+    frame_kernel_ = lds_f_ > 0;
+  }
   const size_t H = c.num_heads;
   // Tagged hand-off words: x, q, k, v, at, h vectors, cross partials, logits,
   // then the epoch counter and the error flag.
@@ -452,6 +461,7 @@ LLBufs State::ll_bufs() const {
   l.logit = l.part + static_cast<size_t>(m.cfg.num_heads) * kMaxBph * 2 * 66;
   uint64_t* tail = l.logit + 2 * static_cast<size_t>(m.cfg.vocab_size);
   l.seq = reinterpret_cast<uint32_t*>(tail);
+  l.tok = tail + 16;
   l.err = reinterpret_cast<int*>(tail + 32);
   return l;
 }
@@ -463,9 +473,22 @@ void State::reset_handoff() {
   const uint32_t one = 1;
   MRT_HIP_CHECK(hipMemcpyAsync(ll_bufs().seq, &one, sizeof(one), hipMemcpyHostToDevice, stream));
   MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  epochs_used_ = 0;
 }
 
-void State::launch_temporal_p(const void* in, int f, void* out) {
+// Each persistent launch advances the epoch by one; tags keep its low 20
+// bits.  Before those wrap, every hand-off word is zeroed and the epoch
+// restarts (outside any capture: callers reserve before enqueueing).
+void State::reserve_epochs(uint32_t n) {
+  if (epochs_used_ + n + 2 >= kEpochPeriod) reset_handoff();
+  epochs_used_ += n;
+}
+
+int State::decode_launches(const GenOpts& o) const {
+  return frame_kernel_ ? o.num_frames : o.num_frames * (1 + o.rvq_depth);
+}
+
+StepArgs State::temporal_args(const void* in, int f, void* out) const {
   const Config& c = m.cfg;
   StepArgs a{};
   if (d_trace_ && f == 1) a.trace = d_trace_;
@@ -485,14 +508,13 @@ void State::launch_temporal_p(const void* in, int f, void* out) {
   a.out = out;
   a.S = S;
   a.ll = ll_bufs();
-  launch_step(m.dt, a, persist_grid_, lds_t_, stream);
+  return a;
 }
 
-void State::launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits,
-                           const GenOpts* o, int frame, int level, float* rec_slice) {
+StepArgs State::depth_args(const void* in, int l, const void* head_w, int head_rows, float* logits,
+                           float* rec_slice) const {
   const Config& c = m.cfg;
   StepArgs a{};
-  if (d_trace_ && frame == 1 && level == 1) a.trace = d_trace_ + kTraceSlots;
   a.st = dstack_;
   a.nlayers = c.num_depth_layers;
   a.cross = 0;
@@ -512,39 +534,73 @@ void State::launch_depth_p(const void* in, int l, const void* head_w, int head_r
   a.head_rows = head_rows;
   a.logits = logits;
   a.rec_slice = rec_slice;
-  if (o) {
-    a.do_sample = 1;
-    a.sp = SampleParams{o->guidance_weight, o->temperature, o->top_k, o->codebook, o->codec_offset, o->rvq_depth,
-                        d_seed};
-    a.frame = frame;
-    a.level = level;
-    a.slot = frame * o->rvq_depth + level;
-    a.teacher = o->teacher ? d_teacher : nullptr;
-    a.tokens = d_tokens;
-    a.drawn = o->record_drawn;
-    a.emb = m.emb;
-    a.next_in = d_in;
-    a.fsum = fsum;
-    a.fmean = t_in;
-    a.noise = noise_ + (static_cast<size_t>(frame) * o->rvq_depth + level) * o->codebook;
-  }
   a.ll = ll_bufs();
+  return a;
+}
+
+void State::launch_temporal_p(const void* in, int f, void* out) {
+  StepArgs a = temporal_args(in, f, out);
+  if (d_trace_ && f == 1) a.trace = d_trace_;
+  launch_step(m.dt, a, persist_grid_, lds_t_, stream);
+}
+
+void State::launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits,
+                           float* rec_slice) {
+  StepArgs a = depth_args(in, l, head_w, head_rows, logits, rec_slice);
   launch_step(m.dt, a, persist_grid_, lds_d_, stream);
 }
 
+// Frame f of the decode loop as one launch: temporal step on t_in, 16 depth
+// steps with on-device draws; the frame mean lands in t_in.
+void State::launch_frame_p(const GenOpts& o, int f) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, C = o.codebook, L = o.rvq_depth;
+  const size_t row_bytes = static_cast<size_t>(rows) * D * esz();
+  FrameArgs fa{};
+  fa.t = temporal_args(t_in, f, nullptr);
+  if (d_trace_ && f == 1) fa.t.trace = d_trace_;
+  const void* head = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset) * D * esz();
+  fa.d = depth_args(nullptr, 0, head, C, nullptr, nullptr);
+  if (d_trace_ && f == 1) fa.d.trace = d_trace_ + kTraceSlots;
+  fa.d.sp = SampleParams{o.guidance_weight, o.temperature, o.top_k, C, o.codec_offset, L, d_seed};
+  fa.d.frame = f;
+  fa.d.teacher = o.teacher ? d_teacher : nullptr;
+  fa.d.tokens = d_tokens;
+  fa.d.drawn = o.record_drawn;
+  fa.d.emb = m.emb;
+  fa.d.fmean = t_in;
+  fa.d.noise = noise_ + static_cast<size_t>(f) * L * C;
+  fa.codebook = C;
+  fa.levels = L;
+  fa.rec_slices = o.record_slices ? o.record_slices + static_cast<size_t>(f) * L * rows * C : nullptr;
+  fa.rec_temporal = o.record_temporal ? static_cast<char*>(o.record_temporal) + f * row_bytes : nullptr;
+  launch_frame(m.dt, fa, persist_grid_, lds_f_, stream);
+}
+
+// Decode loop on the persistent kernels (decode.cpp:339-486).  Frame 0 feeds
+// emb(PAD = 0) on both rows; the Gumbel noise of every draw is tabulated
+// first.  Without the frame kernel each step is one launch and each draw
+// runs in the sampling kernel.
 void State::enqueue_decode_p(const GenOpts& o) {
   const Config& c = m.cfg;
-  const int D = c.d_model, C = o.codebook;
+  const int D = c.d_model, C = o.codebook, L = o.rvq_depth;
   const size_t row_bytes = static_cast<size_t>(rows) * D * esz();
-  embed_fill(m.dt, m.emb, D, 0, rows, t_in, stream);  // frame 0 input: emb(PAD = 0) on both rows
-  gumbel_table(d_seed, o.num_frames, o.rvq_depth, C, noise_, stream);
+  embed_fill(m.dt, m.emb, D, 0, rows, t_in, stream);
+  gumbel_table(d_seed, o.num_frames, L, C, noise_, stream);
+  SampleParams sp{o.guidance_weight, o.temperature, o.top_k, C, o.codec_offset, L, d_seed};
   for (int f = 0; f < o.num_frames; ++f) {
-    launch_temporal_p(t_in, f, t_out);
-    if (o.record_temporal) copy(static_cast<char*>(o.record_temporal) + f * row_bytes, t_out, row_bytes);
-    for (int l = 0; l < o.rvq_depth; ++l) {
-      const char* head = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset + C * l) * D * esz();
-      float* rec = o.record_slices ? o.record_slices + (static_cast<size_t>(f) * o.rvq_depth + l) * rows * C : nullptr;
-      launch_depth_p(l == 0 ? t_out : d_in, l, head, C, slice, &o, f, l, rec);
+    if (frame_kernel_) {
+      launch_frame_p(o, f);
+    } else {
+      launch_temporal_p(t_in, f, t_out);
+      if (o.record_temporal) copy(static_cast<char*>(o.record_temporal) + f * row_bytes, t_out, row_bytes);
+      for (int l = 0; l < L; ++l) {
+        const char* head = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset + C * l) * D * esz();
+        float* rec = o.record_slices ? o.record_slices + (static_cast<size_t>(f) * L + l) * rows * C : nullptr;
+        launch_depth_p(l == 0 ? t_out : d_in, l, head, C, slice, rec);
+        sample_level(m.dt, slice, sp, f, l, f * L + l, o.teacher ? d_teacher : nullptr, d_tokens, o.record_drawn,
+                     m.emb, D, d_in, fsum, t_in, stream);
+      }
     }
     if (o.record_frame_mean) copy(static_cast<char*>(o.record_frame_mean) + f * row_bytes, t_in, row_bytes);
   }
@@ -566,6 +622,8 @@ State::~State() {
   if (stream) (void)hipStreamSynchronize(stream);
   if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
   if (graph_) (void)hipGraphDestroy(graph_);
+  for (hipEvent_t e : ev_dec_)
+    if (e) (void)hipEventDestroy(e);
   for (void* p : allocs_) (void)hipFree(p);
   if (h_pinned) (void)hipHostFree(h_pinned);
   if (h_err_) (void)hipHostFree(h_err_);
@@ -703,6 +761,7 @@ void State::temporal_step(const void* in, const void* enc, int f, void* out) {
     throw Error(1, "temporal_step: cache holds " + std::to_string(temporal_len_) + " entries, frame_idx " +
                        std::to_string(f));
   if (persistent()) {
+    reserve_epochs(1);
     launch_temporal_p(in, f, out);
   } else {
     run_temporal(in, f, out);
@@ -727,7 +786,8 @@ void State::depth_step(const void* in, int l, int level, int C, int off, float* 
     const void* head = level >= 0
                            ? static_cast<const char*>(m.lm_head) + static_cast<size_t>(off + C * level) * D * esz()
                            : m.lm_head;
-    launch_depth_p(in, l, head, level >= 0 ? C : c.vocab_size, logits, nullptr, 0, 0, nullptr);
+    reserve_epochs(1);
+    launch_depth_p(in, l, head, level >= 0 ? C : c.vocab_size, logits, nullptr);
   } else {
     run_depth(in, l, level, C, off, logits);
   }
@@ -804,6 +864,12 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
   MRT_HIP_CHECK(hipMemcpyAsync(d_seed, h_pinned, 8, hipMemcpyHostToDevice, stream));
   MRT_HIP_CHECK(hipStreamSynchronize(stream));
 
+  if (persistent()) reserve_epochs(decode_launches(o));
+  if (!ev_dec_[0]) {
+    MRT_HIP_CHECK(hipEventCreate(&ev_dec_[0]));
+    MRT_HIP_CHECK(hipEventCreate(&ev_dec_[1]));
+  }
+  dec_launches_ = persistent() ? decode_launches(o) : 0;
   if (o.use_graph) {
     const std::vector<double> key = {
         (double)o.num_frames, (double)o.rvq_depth, (double)o.temperature, (double)o.top_k,
@@ -833,12 +899,17 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
       MRT_HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
       graph_key_ = key;
     }
+    MRT_HIP_CHECK(hipEventRecord(ev_dec_[0], stream));
     MRT_HIP_CHECK(hipGraphLaunch(graph_exec_, stream));
-  } else if (persistent()) {
-    enqueue_decode_p(o);
   } else {
-    enqueue_decode(o);
+    MRT_HIP_CHECK(hipEventRecord(ev_dec_[0], stream));
+    if (persistent())
+      enqueue_decode_p(o);
+    else
+      enqueue_decode(o);
   }
+  MRT_HIP_CHECK(hipEventRecord(ev_dec_[1], stream));
+  dec_timed_ = true;
   MRT_HIP_CHECK(hipMemcpyAsync(h_pinned, d_tokens, nt * 4, hipMemcpyDeviceToHost, stream));
   MRT_HIP_CHECK(hipStreamSynchronize(stream));
   check_device_error();
@@ -846,6 +917,15 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
   std::memcpy(out_host, h_pinned, nt * 4);
   temporal_len_ = o.num_frames;
   depth_len_ = o.rvq_depth;
+}
+
+float State::last_decode_ms(int* launches) {
+  if (!dec_timed_) throw Error(1, "decode time: no generate call on this state yet");
+  MRT_HIP_CHECK(hipEventSynchronize(ev_dec_[1]));
+  float ms = 0.f;
+  MRT_HIP_CHECK(hipEventElapsedTime(&ms, ev_dec_[0], ev_dec_[1]));
+  if (launches) *launches = dec_launches_;
+  return ms;
 }
 
 void* State::buffer(int which, int layer, size_t* bytes) {

@@ -139,25 +139,40 @@ class State {
   void set_cache_length(int kind, int length);
   void sync();
   bool persistent() const { return persist_grid_ > 0; }
+  // GPU ms of the decode section (after the encoder) of the last generate
+  // call, from HIP events on the state's stream; launches = persistent
+  // kernel launches in it (0 on the per-layer path).
+  float last_decode_ms(int* launches);
 
  private:
-  // Persistent-kernel decode path (one launch per step).
+  // Persistent-kernel decode path: one launch per step (API steps) or per
+  // frame (decode loop).
   void setup_persistent();
+  StepArgs temporal_args(const void* in, int f, void* out) const;
+  StepArgs depth_args(const void* in, int l, const void* head_w, int head_rows, float* logits,
+                      float* rec_slice) const;
   void launch_temporal_p(const void* in, int f, void* out);
-  void launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits,
-                      const GenOpts* o, int frame, int level, float* rec_slice);
+  void launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits, float* rec_slice);
+  void launch_frame_p(const GenOpts& o, int f);
   void enqueue_decode_p(const GenOpts& o);
+  int decode_launches(const GenOpts& o) const;
+  void reserve_epochs(uint32_t n);
   void check_device_error();
   int persist_grid_ = 0, bph_ = 0;
+  bool frame_kernel_ = false;  // the decode loop runs one launch per frame
   void* ll_block_ = nullptr;
   size_t ll_words_ = 0;
+  uint32_t epochs_used_ = 0;   // launches since the hand-off words were zeroed
   LLBufs ll_bufs() const;
   void reset_handoff();
   DecStack tstack_{}, dstack_{};  // temporal / depth stacks with this state's caches
-  size_t lds_t_ = 0, lds_d_ = 0;   // dynamic LDS of the step kernels
+  size_t lds_t_ = 0, lds_d_ = 0, lds_f_ = 0;  // dynamic LDS of the persistent kernels
   float* noise_ = nullptr;         // Gumbel noise of every draw of a decode call
   int* h_err_ = nullptr;        // pinned
   uint64_t* d_trace_ = nullptr; // 2 x kTraceSlots when MRT_TRACE_PHASES is set
+  hipEvent_t ev_dec_[2] = {nullptr, nullptr};  // around the decode section of generate
+  int dec_launches_ = 0;
+  bool dec_timed_ = false;
   void print_trace();
 
   size_t esz() const { return m.esz; }

@@ -43,9 +43,15 @@ struct LLBufs {
   uint64_t* h;      // gated-GELU output
   uint64_t* part;   // cross-attention partials: H * kMaxBph * 2 * 66 words
   uint64_t* logit;  // head logits: 2 * head_rows words
+  uint64_t* tok;    // token drawn by workgroup 0 (frame kernel)
   uint32_t* seq;    // launch counter (tag epoch), advanced by each launch
   int* err;         // set when a poll exceeds its spin limit
 };
+// tag = (epoch << kTagShift) | phase code: codes stay below 1 << kTagShift,
+// and the host zeroes every word and restarts the epoch at 1 before the
+// epoch's low 20 bits wrap.
+constexpr int kTagShift = 12;
+constexpr uint32_t kEpochPeriod = 1u << (32 - kTagShift);
 constexpr size_t kLLVecWords = 2 * kMaxPersistK;
 
 struct StepArgs {
@@ -64,19 +70,16 @@ struct StepArgs {
   const void* head_w;  // first lm_head row of the head
   int head_rows;       // rows of the head (codebook, or vocab)
   float* logits;       // (2, head_rows) plain copy
-  // sampling after the head (depth step of the decode loop)
-  int do_sample;
+  // sampling after the head (frame kernel)
   SampleParams sp;
-  int frame, level, slot;
-  const int* teacher;
-  int* tokens;
-  int* drawn;
-  const void* emb;
-  void* next_in;   // (2, D): embedding of the fed-back token on both rows
-  void* fsum;      // (D): running sum of the frame's token embeddings
-  void* fmean;     // (2, D): frame mean (next temporal input)
-  float* rec_slice;  // optional copy of the logits
-  const float* noise;  // Gumbel noise of this draw: (codebook) floats
+  int frame;
+  const int* teacher;  // (frames * levels) ids fed back instead of the draws, or nullptr
+  int* tokens;         // (frames * levels) fed-back ids
+  int* drawn;          // (frames * levels) drawn ids, or nullptr
+  const void* emb;     // (vocab, D) token embeddings
+  void* fmean;         // (2, D): frame mean (next temporal input)
+  float* rec_slice;    // optional copy of the logits
+  const float* noise;  // Gumbel noise of the frame's draws: (levels, codebook) floats
   LLBufs ll;
   // Optional timeline (100 MHz wall clock) recorded by workgroup 0.
   uint64_t* trace;
@@ -90,11 +93,28 @@ constexpr int kTraceDone = kTraceSlots - 1;
 // device (H * blocks-per-head, bph a power of two in [8, 16]); 0 if unsupported.
 int persist_grid(int H, int num_cu, int* bph);
 
-// Dynamic LDS bytes of a step kernel, after allowing the kernel to use them;
-// 0 if the device cannot give one workgroup that much.
-size_t persist_prepare(DType dt, bool cross, int device);
+enum class PersistKernel { Temporal, Depth, Frame };
+// Dynamic LDS bytes of a persistent kernel, after allowing the kernel to use
+// them; 0 if the device cannot give one workgroup that much.
+size_t persist_prepare(DType dt, PersistKernel kind, int device);
 
 void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t s);
+
+// One frame of the decode loop in one launch: the temporal step (t), then
+// `levels` depth steps (d, d.pos ignored), each followed by a draw whose
+// token is fed back on the device.  d.head_w is the first lm_head row of
+// level 0's slice (level l at + l * codebook rows).
+struct FrameArgs {
+  StepArgs t;
+  StepArgs d;
+  int codebook, levels;
+  float* rec_slices;   // (levels, 2, codebook) copies of the logits, or nullptr
+  void* rec_temporal;  // (2, D) copy of the temporal output, or nullptr
+};
+// The frame kernel keeps the depth K/V history in LDS: it needs
+// depth layers * levels <= kMaxResidentSlots.
+constexpr int kMaxResidentSlots = 64;
+void launch_frame(DType dt, const FrameArgs& a, int grid, size_t lds, hipStream_t s);
 
 // Gumbel noise of every draw of a decode call: out[(f * L + l) * C + c] =
 // gumbel(seed, f, l, c) for f < frames, l < L, c < C.

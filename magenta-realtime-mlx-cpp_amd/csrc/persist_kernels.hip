@@ -7,7 +7,7 @@
 // tag} written and read with agent-scope atomics, which are coherent across
 // the 8 XCDs without cache maintenance.  A consumer polls the words it needs
 // until each carries the tag of the producing phase of this launch (tag =
-// launch epoch << 10 | phase code), so a hand-off costs one store -> load
+// launch epoch << 12 | phase code), so a hand-off costs one store -> load
 // propagation and needs no counters, barriers or store drains.  The epoch is
 // a device counter that workgroup 0 advances once it has seen data from every
 // workgroup, so graph replays never match stale words.
@@ -82,6 +82,14 @@ __device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Selects one of three values.  Taking the operands by value keeps the
+// selection off member addresses of the kernel arguments, which would force
+// a private-memory copy of the argument block.
+template <typename P>
+__device__ __forceinline__ P pick3(int i, P p0, P p1, P p2) {
+  return i == 0 ? p0 : i == 1 ? p1 : p2;
+}
 
 __device__ __forceinline__ bool spin_failed(uint32_t& spins, int* err) {
   if ((++spins & 255u) == 0) {
@@ -270,20 +278,20 @@ __device__ __forceinline__ void trace_point(uint64_t* trace, int slot) {
 }
 
 // Loads the activation vector of a phase (K <= 256 * NPER elements; tagged,
-// or the launch's plain input rows) into LDS, with an optional side element.
+// or plain input rows) into LDS, with an optional side element.
 // NORM: RMS norm with the LDS-staged weight g (modules.cpp:72-84): the sum of
 // squares is taken from the polled values in registers, and each element is
 // written to LDS once, normalised.
 template <typename T, int NPER, bool NORM>
 __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, int K, uint32_t tag, const T* g,
                                          float* xs, float* red, const Side& sd, float& r0, float& r1, int* err,
-                                         uint64_t* trace, int& tp, int& lc) {
+                                         uint64_t* trace, int& tp, int& lc, int stride) {
   using S = St<T>;
   const int tid = threadIdx.x;
   if (trace != nullptr && blockIdx.x == 0 && tid == 0 && lc < 16) trace[kLoadTrace + lc] = wall_clock64();
   trace_point(trace, tp++);
   float v0[NPER], v1[NPER];
-  if (plain != nullptr) {  // (2, K) model-dtype rows
+  if (plain != nullptr) {  // two model-dtype rows, row 1 at +stride (0: the same row twice)
     const T* p = static_cast<const T*>(plain);
     T w0[NPER], w1[NPER];
 #pragma unroll
@@ -291,7 +299,7 @@ __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, 
       const int k = tid + i * kPersistThreads;
       if (k < K) {
         w0[i] = ld_g(p + k);
-        w1[i] = ld_g(p + K + k);
+        w1[i] = ld_g(p + stride + k);
       }
     }
 #pragma unroll
@@ -523,12 +531,15 @@ __device__ __forceinline__ void stage_slots(const T* src, int n, long lim, T* re
 }
 
 // Self attention of head h over ring slots 0..pos (scale 1.0, bias
-// table[bucket[pos - j], h]; modules.cpp:243-295).  Slots before pos were
-// staged into `hist` from earlier launches' ring writes; q and slot pos come
-// as tagged words of this launch.
+// table[bucket[pos - j], h]; modules.cpp:243-295).  q and slot pos come as
+// tagged words of this launch; slots before pos are in LDS, region
+// (kind, row) = `cap` slots x 64 at hist + (kind * 2 + row) * cap * 64 (kind
+// 0 = K, 1 = V).  They were staged there from the global ring (slots written
+// by earlier launches) or, `resident`, written by this function at earlier
+// steps of the same launch: it then also stores slot pos for the next step.
 template <typename T>
-__device__ __forceinline__ void self_attention_head(const StepArgs& a, int h, uint32_t tag, uint32_t out_tag,
-                                                    const T* hist, float* sm) {
+__device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, int h, uint32_t tag, uint32_t out_tag,
+                                                    T* hist, int cap, bool resident, float* sm) {
   using S = St<T>;
   constexpr int V = S::kVec;
   float* qs = sm;        // [2][64]
@@ -537,8 +548,9 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int h, ui
   float* ps = sm + 384;  // [2][64]
   float* os = sm + 512;  // [2][64]
   const int tid = threadIdx.x, wid = uniform(tid >> 6), lane = tid & 63;
+  const int len = pos + 1, rs = cap * 64;
   if (wid < 3) {  // waves 0, 1, 2 fetch q, k, v of head h
-    const uint64_t* src = (wid == 0 ? a.ll.q : wid == 1 ? a.ll.k : a.ll.v) + h * 64;
+    const uint64_t* src = pick3<const uint64_t*>(wid, a.ll.q, a.ll.k, a.ll.v) + h * 64;
     float* d = sm + wid * 128;
     constexpr int NW = LL<T>::kWords;
     uint64_t w[NW];
@@ -552,17 +564,22 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int h, ui
       if (ok || spin_failed(spins, a.ll.err)) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    d[lane] = LL<T>::get(w, 0);
-    d[64 + lane] = LL<T>::get(w, 1);
+    const float v0 = LL<T>::get(w, 0), v1 = LL<T>::get(w, 1);
+    d[lane] = v0;
+    d[64 + lane] = v1;
+    if (resident && wid > 0) {  // keep slot pos of K (wave 1) / V (wave 2) for later steps
+      T* slot = hist + ((wid - 1) * 2) * rs + pos * 64 + lane;
+      slot[0] = S::st(v0);
+      slot[rs] = S::st(v1);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wave's history copies have landed
   __syncthreads();
-  const int pos = a.pos, len = pos + 1;
   if (wid < 2) {
     const int b = wid;
     float sc = -INFINITY;
     if (lane < pos) {
-      const T* kr = hist + b * kRegion + lane * 64;
+      const T* kr = hist + b * rs + lane * 64;
       float acc = 0.f;
 #pragma unroll
       for (int i = 0; i < 64 / V; ++i) {
@@ -584,7 +601,7 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int h, ui
     const float l = dpp_sum(p);
     ps[b * 64 + lane] = p;
     // the same wave reads ps back: LDS operations of a wave complete in order
-    const T* vr = hist + (2 + b) * kRegion + lane;
+    const T* vr = hist + (2 + b) * rs + lane;
     float o = ps[b * 64 + pos] * vs[b * 64 + lane];
     for (int j = 0; j < pos; ++j) o = fmaf(ps[b * 64 + j], S::ld(vr[j * 64]), o);
     os[b * 64 + lane] = o / l;
@@ -709,27 +726,30 @@ __device__ __forceinline__ void cross_combine(const StepArgs& a, int h, uint32_t
 // ---- sampling -------------------------------------------------------------------
 
 // Block-wide CFG + temperature/top-k Gumbel-max draw and token feedback
-// (decode.cpp:71-148, 458-484); `lg` holds the two logit rows in LDS, the
-// Gumbel noise of the draw comes precomputed in a.noise.  The top-k
-// threshold (k-th largest value, ties kept) is found by a most-significant-
-// byte-first radix select over LDS histograms.
+// (decode.cpp:71-148, 458-484) for one level: `lg` holds the two logit rows
+// of the level slice in LDS, `noise` the precomputed Gumbel noise of the draw.
+// The top-k threshold (k-th largest value, ties kept) is found by a
+// most-significant-byte-first radix select over LDS histograms.  The running
+// frame sum of the fed-back embeddings stays in registers (`fs`, 4 elements
+// per thread, model dtype); the last level writes the frame mean (both rows)
+// to `fmean`.  Returns the fed-back token (the same in every thread).
 template <typename T>
-__device__ __forceinline__ void sample_block(const StepArgs& a, const float* lg, unsigned* hist, int* sel) {
+__device__ __forceinline__ int sample_block(const SampleParams& p, int frame, int level, int slot,
+                                            const float* noise, const int* teacher, int* tokens, int* drawn,
+                                            const T* emb, int D, float (&fs)[4], T* fmean, const float* lg,
+                                            unsigned* hist, int* sel) {
   using S = St<T>;
   constexpr int kPer = 1024 / kPersistThreads;  // candidates and d_model elements per thread
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const SampleParams& p = a.sp;
   const int C = p.codebook;
   // Loads that do not depend on the draw go first.
-  const T* fs_in = static_cast<const T*>(a.fsum);
-  float fv[kPer], gn[kPer];
+  float gn[kPer];
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {
-    const int d = tid + kPersistThreads * t;
-    fv[t] = (a.level != 0 && d < a.D) ? S::ld(ld_g(fs_in + d)) : 0.f;
-    gn[t] = d < C ? ld_g(a.noise + d) : 0.f;
+    const int c = tid + kPersistThreads * t;
+    gn[t] = c < C ? ld_g(noise + c) : 0.f;
   }
-  const int teacher_id = a.teacher ? ld_g(a.teacher + a.slot) : 0;
+  const int teacher_id = teacher ? ld_g(teacher + slot) : 0;
   const float wc = 1.0f + p.guidance_weight, wu = p.guidance_weight;
   float v[kPer];
 #pragma unroll
@@ -819,40 +839,37 @@ __device__ __forceinline__ void sample_block(const StepArgs& a, const float* lg,
       mx = wbest[w];
       arg = widx[w];
     }
-  const int drawn_id = p.codec_offset + a.level * C + arg;
-  const int fed = a.teacher ? teacher_id : drawn_id;
+  const int drawn_id = p.codec_offset + level * C + arg;
+  const int fed = teacher ? teacher_id : drawn_id;
   if (tid == 0) {
-    st_g(a.tokens + a.slot, fed);
-    if (a.drawn) st_g(a.drawn + a.slot, drawn_id);
+    st_g(tokens + slot, fed);
+    if (drawn) st_g(drawn + slot, drawn_id);
   }
-  // Token feedback: both rows take emb(fed); the frame sum accumulates in the
-  // model dtype; the last level's sum / L is the next temporal input.
-  const T* e = static_cast<const T*>(a.emb) + (size_t)fed * a.D;
+  // Frame sum in the model dtype; the last level's sum / L is the next
+  // temporal input (decode.cpp:263-273, 476-484).
+  const T* e = emb + (size_t)fed * D;
   float ev[kPer];
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {
     const int d = tid + kPersistThreads * t;
-    ev[t] = d < a.D ? S::ld(ld_g(e + d)) : 0.f;
+    ev[t] = d < D ? S::ld(ld_g(e + d)) : 0.f;
   }
-  const float Lf = S::rnd((float)p.rvq_depth);
-  T* ni = static_cast<T*>(a.next_in);
-  T* fs = static_cast<T*>(a.fsum);
-  T* fm = static_cast<T*>(a.fmean);
 #pragma unroll
-  for (int t = 0; t < kPer; ++t) {
-    const int d = tid + kPersistThreads * t;
-    if (d < a.D) {
-      const float sum = (a.level == 0) ? ev[t] : S::rnd(fv[t] + ev[t]);
-      st_g(ni + d, S::st(ev[t]));
-      st_g(ni + a.D + d, S::st(ev[t]));
-      st_g(fs + d, S::st(sum));
-      if (a.level == p.rvq_depth - 1) {
-        const T m = S::st(sum / Lf);
-        st_g(fm + d, m);
-        st_g(fm + a.D + d, m);
+  for (int t = 0; t < kPer; ++t) fs[t] = level == 0 ? ev[t] : S::rnd(fs[t] + ev[t]);
+  if (level == p.rvq_depth - 1) {
+    const float Lf = S::rnd((float)p.rvq_depth);
+#pragma unroll
+    for (int t = 0; t < kPer; ++t) {
+      const int d = tid + kPersistThreads * t;
+      if (d < D) {
+        const T m = S::st(fs[t] / Lf);
+        st_g(fmean + d, m);
+        st_g(fmean + D + d, m);
       }
     }
   }
+  __syncthreads();  // hist / sel are reused by the next draw
+  return fed;
 }
 
 __global__ void k_gumbel_table(const uint64_t* __restrict__ seed_p, int frames, int L, int C, float* __restrict__ out) {
@@ -864,51 +881,96 @@ __global__ void k_gumbel_table(const uint64_t* __restrict__ seed_p, int frames, 
   }
 }
 
-// Phase codes of the tags (per layer: code = 16 * layer + phase).
+// Phase codes of the tags: code = stack base + 16 * layer + phase.
 enum : int { kPhQKV = 0, kPhAtt = 1, kPhO = 2, kPhCQ = 3, kPhCP = 4, kPhCC = 5, kPhCO = 6, kPhUp = 7, kPhDn = 8 };
-constexpr int kPhHead = 1000;
+enum : int { kPhLogit = 0, kPhToken = 1 };  // after a depth stack: base + 16 * nlayers + ...
 
+// LDS and per-thread state of one persistent workgroup.
+template <typename T>
+struct Ctx {
+  // Activation rows, double-buffered by phase: a wave that starts polling the
+  // next phase writes the other buffer while slower waves still read this one.
+  float (*xsb)[2 * kMaxPersistK];
+  int xsel;
+  float* red;
+  float* sm;
+  float (*kvst)[2][16];  // [k|v][row][d within this workgroup's slice]
+  T (*gam)[1024];        // norm weights: self-attn, cross-attn, FFN, decoder_norm
+  unsigned* sel_hist;
+  int* sel_res;
+  T* dyn;                // attention staging (4 regions of kRegion)
+  uint4 buf[kNBuf];      // weights of the next phase
+  uint32_t ep;
+  int tp, lcnt;
+  int G, blk, wid, lane, h, jpart, rps;
+  __device__ float* next_xs() {
+    xsel ^= 1;
+    return xsb[xsel];
+  }
+  __device__ uint32_t tag(int code) const { return (ep << kTagShift) | (uint32_t)code; }
+};
+
+// Input and output of a decoder stack.
+struct StackIO {
+  const void* in_plain;  // layer-0 input as plain rows (nullptr: tagged x words)
+  int in_stride;         // row stride of in_plain (0: both rows are the same row)
+  uint32_t in_tag;       // tag of the tagged layer-0 input
+  void* out_plain;       // optional plain (2, D) copy of the output
+  bool out_tagged;       // leave the output as tagged x words
+  int code_base;
+  bool resident;         // self-attention history kept in LDS across the steps of one launch
+  int cap;               // LDS slots per (K|V, row) region
+  int pos;               // ring slot written by this step
+  uint64_t* trace;       // timeline of workgroup 0, or nullptr
+};
+
+// Rows of wave `wid` for the QKV phase: local t = wid + 4i < 3*rps ->
+// (segment t / rps, row t % rps) of head h's rows owned by workgroup (h, j).
+template <typename T>
+__device__ __forceinline__ int qkv_rows(const Ctx<T>& c) {
+  return (3 * c.rps > c.wid) ? (3 * c.rps - c.wid + 3) / 4 : 0;
+}
+
+// Prefetches the first QKV batch of layer `li` of a stack into c.buf.
+template <typename T, bool NT>
+__device__ __forceinline__ void prefetch_qkv(Ctx<T>& c, const StepArgs& a, int li) {
+  constexpr int V = St<T>::kVec;
+  constexpr int NVD = (1024 + V * 64 - 1) / (V * 64);
+  const int HD = a.HD, D = a.D, h = c.h, jpart = c.jpart, rps = c.rps, wid = c.wid;
+  auto qkv_row = [&](int t, int) {
+    const int lt = wid + 4 * t;
+    return (lt / rps) * HD + h * 64 + jpart * rps + (lt % rps);
+  };
+  const T* w = static_cast<const T*>(a.st.wqkv) + (size_t)li * 3 * HD * D;
+  fetch_batch<T, NVD, 1, NT>(c.buf, w, D, 0, min(kNBuf / NVD, qkv_rows(c)), qkv_row);
+}
+
+// Decoder stack of a.nlayers layers at ring position io.pos (modules.cpp:384-408):
+// pre-norm self attention (+ cross attention) + gated-GELU FFN, residuals.
+// On entry c.buf holds layer 0's first QKV batch.  Returns the tag of the
+// output x words (when io.out_tagged).
 template <typename T, bool CROSS>
-__global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_step(StepArgs a) {
+__device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, const StackIO& io) {
   using S = St<T>;
   constexpr int V = S::kVec;
   constexpr bool NT = CROSS;
   constexpr int NVD = (1024 + V * 64 - 1) / (V * 64);  // K <= 1024
   constexpr int NVF = 3 * NVD;                         // K <= 3072
-  // Activation rows, double-buffered by phase: a wave that starts polling the
-  // next phase writes the other buffer while slower waves still read this one.
-  __shared__ float xsb[2][2 * kMaxPersistK];
-  float* xs = xsb[0];
-  int xsel = 0;
-  __shared__ float red[8];
-  __shared__ float sm[704];
-  __shared__ float kvst[2][2][16];  // [k|v][row][d within this workgroup's slice]
-  __shared__ __align__(16) T gam[4][1024];  // norm weights: self-attn, cross-attn, FFN, decoder_norm
-  __shared__ unsigned sel_hist[kPersistThreads];
-  __shared__ int sel_res[8];
-  extern __shared__ __align__(16) unsigned char dyn_lds[];
-  // [K|V][row] regions of 64 x 64: the ring history during self attention,
-  // then the layer's cross K/V block.
-  T* hist = reinterpret_cast<T*>(dyn_lds);
-  T* cst = hist;
-
-  const int G = gridDim.x, blk = blockIdx.x;
-  const int wid = uniform(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int G = c.G, blk = c.blk, wid = c.wid, lane = c.lane, h = c.h, jpart = c.jpart, rps = c.rps;
   const int D = a.D, HD = a.HD, H = a.H, F = a.F, bph = a.bph;
-  const int h = blk / bph, jpart = blk % bph, rps = 64 / bph;
-  // Elements of one layer of each stacked kind.
   const size_t eQKV = (size_t)3 * HD * D, eO = (size_t)D * HD, eQc = (size_t)HD * D, e01 = (size_t)2 * F * D,
                eO2 = (size_t)D * F;
   const size_t eRing = (size_t)2 * H * a.Lmax * 64, eCross = (size_t)2 * H * a.S * 64;
   const T* wqkv0 = static_cast<const T*>(a.st.wqkv);
-  uint4 buf[kNBuf];
-  int tp = 0;    // trace slot
-  int lcnt = 0;  // activation loads so far (trace only)
-#define MRT_TP trace_point(a.trace, tp++)
+  float* xs = c.xsb[c.xsel];
+  float* red = c.red;
+  float* sm = c.sm;
+  T* hist = c.dyn;
+  T* cst = c.dyn;
+#define MRT_TP trace_point(io.trace, c.tp++)
 
   const RowSplit sD(D, G, blk), sF(F, G, blk);
-  // QKV rows of this wave: local t = wid + 4i < 3*rps -> (segment t / rps, row t % rps).
-  const int nqkv = (3 * rps > wid) ? (3 * rps - wid + 3) / 4 : 0;
+  const int nqkv = qkv_rows(c);
   auto qkv_row = [&](int t, int) {
     const int lt = wid + 4 * t;
     return (lt / rps) * HD + h * 64 + jpart * rps + (lt % rps);
@@ -917,21 +979,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   auto cq_row = [&](int t, int) { return h * 64 + jpart * rps + wid + 4 * t; };
   auto rowD = [&](int t, int) { return sD.row(wid, t); };
   auto rowF = [&](int t, int p) { return geglu_row(sF.row(wid, t), p); };
-
-  // Layer 0's QKV weights first: they take longest to arrive.
-  if (a.nlayers > 0) fetch_batch<T, NVD, 1, NT>(buf, wqkv0, D, 0, min(kNBuf / NVD, nqkv), qkv_row);
-  // Activation elements past a vector's end meet zero weights: keep them finite.
-  for (int k = threadIdx.x; k < 2 * kMaxPersistK; k += kPersistThreads) xsb[0][k] = xsb[1][k] = 0.f;
-  __syncthreads();
-  if (aload(a.ll.err) != 0) return;  // a previous launch failed: do nothing
-  const uint32_t ep = aload(a.ll.seq);
-  auto tag = [&](int code) { return (ep << 10) | (uint32_t)code; };
-  if (a.trace != nullptr && blk == 0 && threadIdx.x == 0) a.trace[kTraceStart] = wall_clock64();
-  if (!CROSS && wid == 3) stage_slots<T>(static_cast<const T*>(a.dec_norm), D / 64, (long)D * sizeof(T), gam[3]);
-
-  // residual element of the wave's D-row `lane` (lanes < nw)
-  auto side_x = [&](const uint64_t* ll, const void* plain, uint32_t tg) {
-    Side s{ll, plain, tg, lane < sD.nw(wid) ? sD.row(wid, lane) : -1, D};
+  auto side_x = [&](const uint64_t* ll, const void* plain, uint32_t tg, int stride) {
+    Side s{ll, plain, tg, lane < sD.nw(wid) ? sD.row(wid, lane) : -1, stride};
     return s;
   };
   const Side no_side{nullptr, nullptr, 0u, -1, 0};
@@ -942,19 +991,23 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     if (act) LL<T>::put(a.ll.x, sD.row(wid, t), S::rnd(x0 + S::rnd(s[0][0])), S::rnd(x1 + S::rnd(s[0][1])), tg);
   };
 
-  uint32_t x_tag = 0;  // tag of the current residual stream (layer >= 1)
+  uint32_t x_tag = io.in_tag;
   for (int li = 0; li < a.nlayers; ++li) {
     const bool first = li == 0, last = li + 1 == a.nlayers;
-    const int base = 16 * li;
+    const int base = io.code_base + 16 * li;
+    auto tag = [&](int code) { return c.tag(code); };
     T* ring_k = static_cast<T*>(a.st.ring) + 2 * li * eRing;
+    const void* in_plain = first ? io.in_plain : nullptr;
+    const int in_stride = io.in_stride;
     // ---- stage the norm weights, ring history and cross K/V block of this layer in LDS
     if (wid < 3 && (CROSS || wid != 1)) {
-      const void* g = wid == 0 ? a.st.norm_sa : wid == 1 ? a.st.norm_ca : a.st.norm_ff;
-      stage_slots<T>(static_cast<const T*>(g) + (size_t)li * D, D / 64, (long)D * sizeof(T), gam[wid]);
+      const void* g = pick3<const void*>(wid, a.st.norm_sa, a.st.norm_ca, a.st.norm_ff);
+      stage_slots<T>(static_cast<const T*>(g) + (size_t)li * D, D / 64, (long)D * sizeof(T), c.gam[wid]);
     }
-    if (jpart == 0 && a.pos > 0) {
+    T* lhist = io.resident ? hist + (size_t)li * 4 * io.cap * 64 : hist;
+    if (!io.resident && jpart == 0 && io.pos > 0) {
       const int kind = wid >> 1, b = wid & 1;
-      stage_slots<T>(ring_k + kind * eRing + (size_t)(b * H + h) * a.Lmax * 64, a.pos,
+      stage_slots<T>(ring_k + kind * eRing + (size_t)(b * H + h) * a.Lmax * 64, io.pos,
                      (long)a.Lmax * 64 * sizeof(T), hist + wid * kRegion);
     }
     auto stage_cross = [&]() {
@@ -969,20 +1022,20 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     };
     if (CROSS && jpart != 0) stage_cross();
     // ---- QKV of head h's slice (weights already in flight)
-    xs = xsb[++xsel & 1];
-    load_act<T, 4, true>(a.ll.x, first ? a.in : nullptr, D, x_tag, gam[0], xs,
-                red, no_side, r0, r1, a.ll.err, a.trace, tp, lcnt);
-    gemv_rows<T, NVD, 1, NT>(buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs,
+    xs = c.next_xs();
+    load_act<T, 4, true>(a.ll.x, in_plain, D, x_tag, c.gam[0], xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
+                         c.lcnt, in_stride);
+    gemv_rows<T, NVD, 1, NT>(c.buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs,
                              [&](int t, bool act, const float (&s)[1][2]) {
       const int lt = wid + 4 * t, seg = lt / rps, r = lt % rps;
       const int n = h * 64 + jpart * rps + r;
       const float v0 = S::rnd(s[0][0]), v1 = S::rnd(s[0][1]);
       if (act) {
-        uint64_t* dst = seg == 0 ? a.ll.q : seg == 1 ? a.ll.k : a.ll.v;
+        uint64_t* dst = pick3<uint64_t*>(seg, a.ll.q, a.ll.k, a.ll.v);
         LL<T>::put(dst, n, v0, v1, tag(base + kPhQKV));
         if (seg > 0) {
-          kvst[seg - 1][0][r] = v0;
-          kvst[seg - 1][1][r] = v1;
+          c.kvst[seg - 1][0][r] = v0;
+          c.kvst[seg - 1][1][r] = v1;
         }
       }
     });
@@ -991,8 +1044,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     // plain ring slot (read by later launches): 4 elements per thread
     if (threadIdx.x < 2 * 2 * (rps / 4)) {
       const int g4 = threadIdx.x % (rps / 4), rb = (threadIdx.x / (rps / 4)) % 2, kv = threadIdx.x / (rps / 2);
-      T* dst = ring_k + kv * eRing + (((size_t)rb * H + h) * a.Lmax + a.pos) * 64 + jpart * rps + 4 * g4;
-      const float* v = &kvst[kv][rb][4 * g4];
+      T* dst = ring_k + kv * eRing + (((size_t)rb * H + h) * a.Lmax + io.pos) * 64 + jpart * rps + 4 * g4;
+      const float* v = &c.kvst[kv][rb][4 * g4];
       if constexpr (sizeof(T) == 2) {
         st_g(reinterpret_cast<uint64_t*>(dst), (uint64_t)f2bf(v[0]) | ((uint64_t)f2bf(v[1]) << 16) |
                                                    ((uint64_t)f2bf(v[2]) << 32) | ((uint64_t)f2bf(v[3]) << 48));
@@ -1006,16 +1059,17 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     // its polls would otherwise also wait for those loads.
     const T* wo = static_cast<const T*>(a.st.wo) + li * eO;
     if (jpart == 0) {
-      self_attention_head<T>(a, h, tag(base + kPhQKV), tag(base + kPhAtt), hist, sm);
+      self_attention_head<T>(a, io.pos, h, tag(base + kPhQKV), tag(base + kPhAtt), lhist, io.resident ? io.cap : 64,
+                             io.resident, sm);
       MRT_TP;
       if (CROSS) stage_cross();  // the history has been read (barrier above)
     }
-    fetch_batch<T, NVD, 1, NT>(buf, wo, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
+    fetch_batch<T, NVD, 1, NT>(c.buf, wo, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
     // ---- attention output projection + residual
-    xs = xsb[++xsel & 1];
+    xs = c.next_xs();
     load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhAtt), nullptr, xs, red,
-                side_x(a.ll.x, first ? a.in : nullptr, x_tag), r0, r1, a.ll.err, a.trace, tp, lcnt);
-    gemv_rows<T, NVD, 1, NT>(buf, wo, HD, sD.nw(wid), rowD, xs,
+                          side_x(a.ll.x, in_plain, x_tag, in_stride), r0, r1, a.ll.err, io.trace, c.tp, c.lcnt, 0);
+    gemv_rows<T, NVD, 1, NT>(c.buf, wo, HD, sD.nw(wid), rowD, xs,
                              [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhO)); });
     MRT_TP;
     x_tag = tag(base + kPhO);
@@ -1023,25 +1077,25 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       // ---- cross attention: q rows of head h, key-block partials, combine
       const T* wqc = static_cast<const T*>(a.st.wq_c) + li * eQc;
       const T* woc = static_cast<const T*>(a.st.wo_c) + li * eO;
-      fetch_batch<T, NVD, 1, NT>(buf, wqc, D, 0, min(kNBuf / NVD, ncq), cq_row);
-      xs = xsb[++xsel & 1];
-      load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gam[1], xs, red, no_side,
-                  r0, r1, a.ll.err, a.trace, tp, lcnt);
-      gemv_rows<T, NVD, 1, NT>(buf, wqc, D, ncq, cq_row, xs, [&](int t, bool act, const float (&s)[1][2]) {
+      fetch_batch<T, NVD, 1, NT>(c.buf, wqc, D, 0, min(kNBuf / NVD, ncq), cq_row);
+      xs = c.next_xs();
+      load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, c.gam[1], xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
+                           c.lcnt, 0);
+      gemv_rows<T, NVD, 1, NT>(c.buf, wqc, D, ncq, cq_row, xs, [&](int t, bool act, const float (&s)[1][2]) {
         if (act) LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(s[0][0]), S::rnd(s[0][1]), tag(base + kPhCQ));
       });
       MRT_TP;
-      fetch_batch<T, NVD, 1, NT>(buf, woc, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
+      fetch_batch<T, NVD, 1, NT>(c.buf, woc, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
       cross_partial<T>(a, h, jpart, tag(base + kPhCQ), tag(base + kPhCP), cst, sm);
       MRT_TP;
       if (jpart == 0) {
         cross_combine<T>(a, h, tag(base + kPhCP), tag(base + kPhCC), sm);
         MRT_TP;
       }
-      xs = xsb[++xsel & 1];
-      load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhCC), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
-                  a.ll.err, a.trace, tp, lcnt);
-      gemv_rows<T, NVD, 1, NT>(buf, woc, HD, sD.nw(wid), rowD, xs,
+      xs = c.next_xs();
+      load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhCC), nullptr, xs, red,
+                            side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, io.trace, c.tp, c.lcnt, 0);
+      gemv_rows<T, NVD, 1, NT>(c.buf, woc, HD, sD.nw(wid), rowD, xs,
                                [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhCO)); });
       MRT_TP;
       x_tag = tag(base + kPhCO);
@@ -1049,11 +1103,11 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     // ---- gated-GELU up projection
     const T* w01 = static_cast<const T*>(a.st.w01) + li * e01;
     const T* wo2 = static_cast<const T*>(a.st.wo2) + li * eO2;
-    fetch_batch<T, NVD, 2, NT>(buf, w01, D, 0, min(kNBuf / (2 * NVD), sF.nw(wid)), rowF);
-    xs = xsb[++xsel & 1];
-    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gam[2], xs, red, no_side, r0,
-                r1, a.ll.err, a.trace, tp, lcnt);
-    gemv_rows<T, NVD, 2, NT>(buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, bool act, const float (&s)[2][2]) {
+    fetch_batch<T, NVD, 2, NT>(c.buf, w01, D, 0, min(kNBuf / (2 * NVD), sF.nw(wid)), rowF);
+    xs = c.next_xs();
+    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, c.gam[2], xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
+                         c.lcnt, 0);
+    gemv_rows<T, NVD, 2, NT>(c.buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, bool act, const float (&s)[2][2]) {
       const float g0 = gelu_t<T>(S::rnd(s[0][0])), g1 = gelu_t<T>(S::rnd(s[0][1]));
       if (act)
         LL<T>::put(a.ll.h, sF.row(wid, t), S::rnd(g0 * S::rnd(s[1][0])), S::rnd(g1 * S::rnd(s[1][1])),
@@ -1061,109 +1115,275 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     });
     MRT_TP;
     // ---- down projection + residual
-    fetch_batch<T, NVF, 1, NT>(buf, wo2, F, 0, min(kNBuf / NVF, sD.nw(wid)), rowD);
-    xs = xsb[++xsel & 1];
-    load_act<T, kMaxPersistK / kPersistThreads, false>(a.ll.h, nullptr, F, tag(base + kPhUp), nullptr, xs, red, side_x(a.ll.x, nullptr, x_tag), r0, r1,
-                a.ll.err, a.trace, tp, lcnt);
-    if (CROSS && last) {
-      // The temporal step's output leaves as plain pairs (no final norm).
-      if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
-      gemv_rows<T, NVF, 1, NT>(buf, wo2, F, sD.nw(wid), rowD, xs, [&](int t, bool act, const float (&s)[1][2]) {
-        const float x0 = from_lane(r0, t), x1 = from_lane(r1, t);
-        if (act) {
-          T* o = static_cast<T*>(a.out) + sD.row(wid, t);
-          st_g(o, S::st(x0 + S::rnd(s[0][0])));
-          st_g(o + D, S::st(x1 + S::rnd(s[0][1])));
-        }
-      });
-    } else {
-      gemv_rows<T, NVF, 1, NT>(buf, wo2, F, sD.nw(wid), rowD, xs,
-                               [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhDn)); });
-    }
-    MRT_TP;
-    x_tag = tag(base + kPhDn);
-    if (!last)
-      fetch_batch<T, NVD, 1, NT>(buf, wqkv0 + (li + 1) * eQKV, D, 0, min(kNBuf / NVD, nqkv), qkv_row);
-    __syncthreads();  // LDS staging regions are rewritten by the next layer
-  }
-
-  if constexpr (!CROSS) {
-    // ---- decoder_norm + lm_head rows (model.cpp:652-653)
-    const RowSplit sH(a.head_rows, G, blk);
-    auto rowH = [&](int t, int) { return sH.row(wid, t); };
-    const T* hw = static_cast<const T*>(a.head_w);
-    fetch_batch<T, NVD, 1, NT>(buf, hw, D, 0, min(kNBuf / NVD, sH.nw(wid)), rowH);
-    xs = xsb[++xsel & 1];
-    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gam[3], xs, red, no_side, r0, r1, a.ll.err,
-                a.trace, tp, lcnt);
-    if (blk == 0 && threadIdx.x == 0) astore(a.ll.seq, ep + 1u);  // every workgroup has started
-    gemv_rows<T, NVD, 1, NT>(buf, hw, D, sH.nw(wid), rowH, xs, [&](int t, bool act, const float (&s)[1][2]) {
+    fetch_batch<T, NVF, 1, NT>(c.buf, wo2, F, 0, min(kNBuf / NVF, sD.nw(wid)), rowD);
+    xs = c.next_xs();
+    load_act<T, kMaxPersistK / kPersistThreads, false>(a.ll.h, nullptr, F, tag(base + kPhUp), nullptr, xs, red,
+                                                       side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, io.trace,
+                                                       c.tp, c.lcnt, 0);
+    const bool tagged_out = !last || io.out_tagged;
+    gemv_rows<T, NVF, 1, NT>(c.buf, wo2, F, sD.nw(wid), rowD, xs, [&](int t, bool act, const float (&s)[1][2]) {
+      const float x0 = from_lane(r0, t), x1 = from_lane(r1, t);
+      const float y0 = S::rnd(x0 + S::rnd(s[0][0])), y1 = S::rnd(x1 + S::rnd(s[0][1]));
       if (act) {
-        const int n = sH.row(wid, t);
-        astore(a.ll.logit + n, ll_word(__float_as_uint(S::rnd(s[0][0])), tag(kPhHead)));
-        astore(a.ll.logit + a.head_rows + n, ll_word(__float_as_uint(S::rnd(s[0][1])), tag(kPhHead)));
+        const int n = sD.row(wid, t);
+        if (tagged_out) LL<T>::put(a.ll.x, n, y0, y1, tag(base + kPhDn));
+        if (last && io.out_plain != nullptr) {
+          T* o = static_cast<T*>(io.out_plain) + n;
+          st_g(o, S::st(y0));
+          st_g(o + D, S::st(y1));
+        }
       }
     });
     MRT_TP;
-    if (blk == 0) {
-      // ---- gather the logits, copy them out, sample
-      float* lg = xs;  // 2 * head_rows floats when head_rows <= kMaxPersistK
-      const int n2 = 2 * a.head_rows;
-      const uint32_t tg = tag(kPhHead);
-      uint32_t spins = 0;
-      __syncthreads();  // xs is no longer read by the head GEMV
-      for (int base_i = 0; base_i < n2; base_i += kPersistThreads * 8) {
-        uint64_t w[8];
-        uint32_t pend = 0;
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-          if (base_i + (int)threadIdx.x + u * kPersistThreads < n2) pend |= 1u << u;
-        while (pend != 0) {
-#pragma unroll
-          for (int u = 0; u < 8; ++u)
-            if ((pend >> u) & 1u) w[u] = aload(a.ll.logit + base_i + threadIdx.x + u * kPersistThreads);
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            if (((pend >> u) & 1u) && ll_tag(w[u]) == tg) {
-              const int i = base_i + threadIdx.x + u * kPersistThreads;
-              const float v = __uint_as_float(static_cast<uint32_t>(w[u]));
-              if (i < 2 * kMaxPersistK) lg[i] = v;
-              if (a.logits) st_g(a.logits + i, v);
-              if (a.rec_slice) st_g(a.rec_slice + i, v);
-              pend &= ~(1u << u);
-            }
-          }
-          if (pend == 0 || spin_failed(spins, a.ll.err)) break;
-          __builtin_amdgcn_s_sleep(1);
-        }
-      }
-      __syncthreads();
-      if (a.trace != nullptr && threadIdx.x == 0) a.trace[kTraceEnd] = wall_clock64();
-      if (a.do_sample) sample_block<T>(a, lg, sel_hist, sel_res);
-    }
-  } else {
-    if (a.trace != nullptr && blk == 0 && threadIdx.x == 0) a.trace[kTraceEnd] = wall_clock64();
+    x_tag = tag(base + kPhDn);
+    if (!last) prefetch_qkv<T, NT>(c, a, li + 1);
+    __syncthreads();  // LDS staging regions are rewritten by the next layer
   }
 #undef MRT_TP
-  if (a.trace != nullptr && blk == 0 && threadIdx.x == 0) a.trace[kTraceDone] = wall_clock64();
+  return x_tag;
 }
 
+// decoder_norm + lm_head rows of one level (model.cpp:652-653): every
+// workgroup computes ceil(head_rows / G) rows and publishes them as tagged
+// fp32 words; c.buf holds the first head batch on entry.
+template <typename T>
+__device__ __forceinline__ void run_head(Ctx<T>& c, const StepArgs& a, const T* hw, uint32_t x_tag, uint32_t out_tag,
+                                         uint64_t* trace) {
+  using S = St<T>;
+  constexpr int V = S::kVec;
+  constexpr int NVD = (1024 + V * 64 - 1) / (V * 64);
+  const int wid = c.wid;
+  const RowSplit sH(a.head_rows, c.G, c.blk);
+  auto rowH = [&](int t, int) { return sH.row(wid, t); };
+  const Side no_side{nullptr, nullptr, 0u, -1, 0};
+  float r0 = 0.f, r1 = 0.f;
+  float* xs = c.next_xs();
+  load_act<T, 4, true>(a.ll.x, nullptr, a.D, x_tag, c.gam[3], xs, c.red, no_side, r0, r1, a.ll.err, trace, c.tp,
+                       c.lcnt, 0);
+  gemv_rows<T, NVD, 1, false>(c.buf, hw, a.D, sH.nw(wid), rowH, xs, [&](int t, bool act, const float (&s)[1][2]) {
+    if (act) {
+      const int n = sH.row(wid, t);
+      astore(a.ll.logit + n, ll_word(__float_as_uint(S::rnd(s[0][0])), out_tag));
+      astore(a.ll.logit + a.head_rows + n, ll_word(__float_as_uint(S::rnd(s[0][1])), out_tag));
+    }
+  });
+}
+
+template <typename T>
+__device__ __forceinline__ void prefetch_head(Ctx<T>& c, const StepArgs& a, const T* hw) {
+  constexpr int V = St<T>::kVec;
+  constexpr int NVD = (1024 + V * 64 - 1) / (V * 64);
+  const RowSplit sH(a.head_rows, c.G, c.blk);
+  const int wid = c.wid;
+  fetch_batch<T, NVD, 1, false>(c.buf, hw, a.D, 0, min(kNBuf / NVD, sH.nw(wid)), [&](int t, int) { return sH.row(wid, t); });
+}
+
+// Workgroup 0 gathers the 2 x head_rows tagged logits into LDS (and copies
+// them to `logits` / `rec`, when set).
+template <typename T>
+__device__ __forceinline__ void gather_logits(const StepArgs& a, uint32_t tg, float* lg, float* logits, float* rec) {
+  const int n2 = 2 * a.head_rows;
+  uint32_t spins = 0;
+  for (int base_i = 0; base_i < n2; base_i += kPersistThreads * 8) {
+    uint64_t w[8];
+    uint32_t pend = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (base_i + (int)threadIdx.x + u * kPersistThreads < n2) pend |= 1u << u;
+    while (pend != 0) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if ((pend >> u) & 1u) w[u] = aload(a.ll.logit + base_i + threadIdx.x + u * kPersistThreads);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (((pend >> u) & 1u) && ll_tag(w[u]) == tg) {
+          const int i = base_i + threadIdx.x + u * kPersistThreads;
+          const float v = __uint_as_float(static_cast<uint32_t>(w[u]));
+          if (i < 2 * kMaxPersistK) lg[i] = v;
+          if (logits) st_g(logits + i, v);
+          if (rec) st_g(rec + i, v);
+          pend &= ~(1u << u);
+        }
+      }
+      if (pend == 0 || spin_failed(spins, a.ll.err)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __syncthreads();
+}
+
+#define MRT_DECLARE_LDS(T)                                                                    \
+  __shared__ float xsb[2][2 * kMaxPersistK];                                                  \
+  __shared__ float red[8];                                                                    \
+  __shared__ float sm[704];                                                                   \
+  __shared__ float kvst[2][2][16];                                                            \
+  __shared__ __align__(16) T gam[4][1024];                                                    \
+  __shared__ unsigned sel_hist[kPersistThreads];                                              \
+  __shared__ int sel_res[8];                                                                  \
+  extern __shared__ __align__(16) unsigned char dyn_lds[];                                    \
+  Ctx<T> c;                                                                                   \
+  c.xsb = xsb;                                                                                \
+  c.xsel = 0;                                                                                 \
+  c.red = red;                                                                                \
+  c.sm = sm;                                                                                  \
+  c.kvst = kvst;                                                                              \
+  c.gam = gam;                                                                                \
+  c.sel_hist = sel_hist;                                                                      \
+  c.sel_res = sel_res;                                                                        \
+  c.dyn = reinterpret_cast<T*>(dyn_lds);                                                      \
+  c.tp = 0;                                                                                   \
+  c.lcnt = 0;                                                                                 \
+  c.G = gridDim.x;                                                                            \
+  c.blk = blockIdx.x;                                                                         \
+  c.wid = uniform(threadIdx.x >> 6);                                                          \
+  c.lane = threadIdx.x & 63
+
+// Per-launch start of a persistent kernel: reads the error flag and the
+// epoch first (their loads must not queue behind the weight prefetch), zeroes
+// the activation buffers (elements past a vector's end meet zero weights).
+// Returns false if a previous launch failed.
+template <typename T>
+__device__ __forceinline__ bool start(Ctx<T>& c, const LLBufs& ll, int bph) {
+  c.h = c.blk / bph;
+  c.jpart = c.blk % bph;
+  c.rps = 64 / bph;
+  const int err = aload(ll.err);
+  c.ep = aload(ll.seq);
+  float4* z = reinterpret_cast<float4*>(&c.xsb[0][0]);
+  for (int k = threadIdx.x; k < 2 * 2 * kMaxPersistK / 4; k += kPersistThreads) z[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+  return err == 0;
+}
+
+// One step launch (the temporal_step / depth_step API): a decoder stack, then
+// for depth the level-sliced head with the logits copied to a.logits.
 template <typename T, bool CROSS>
+__global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_step(StepArgs a) {
+  MRT_DECLARE_LDS(T);
+  const bool ok = start<T>(c, a.ll, a.bph);
+  if (a.nlayers > 0) prefetch_qkv<T, CROSS>(c, a, 0);
+  __syncthreads();
+  if (!ok) return;  // a previous launch failed: do nothing
+  if (a.trace != nullptr && c.blk == 0 && threadIdx.x == 0) a.trace[kTraceStart] = wall_clock64();
+  if (!CROSS && c.wid == 3) stage_slots<T>(static_cast<const T*>(a.dec_norm), a.D / 64, (long)a.D * sizeof(T), gam[3]);
+  StackIO io{a.in, a.D, 0u, CROSS ? a.out : nullptr, !CROSS, 0, false, 64, a.pos, a.trace};
+  const uint32_t x_tag = run_stack<T, CROSS>(c, a, io);
+  if constexpr (!CROSS) {
+    const T* hw = static_cast<const T*>(a.head_w);
+    prefetch_head<T>(c, a, hw);
+    const uint32_t tg = c.tag(16 * a.nlayers + kPhLogit);
+    run_head<T>(c, a, hw, x_tag, tg, a.trace);
+    if (c.blk == 0 && threadIdx.x == 0) astore(a.ll.seq, c.ep + 1u);  // every workgroup has started
+    if (c.blk == 0) {
+      __syncthreads();
+      gather_logits<T>(a, tg, c.xsb[c.xsel ^ 1], a.logits, a.rec_slice);
+    }
+  } else {
+    if (c.blk == 0 && threadIdx.x == 0) astore(a.ll.seq, c.ep + 1u);  // every workgroup has read the epoch
+  }
+  if (a.trace != nullptr && c.blk == 0 && threadIdx.x == 0) a.trace[kTraceEnd] = a.trace[kTraceDone] = wall_clock64();
+}
+
+// One frame of the decode loop in one launch (decode.cpp:339-486): the
+// temporal step (input a.t.in, the previous frame's mean), then `levels`
+// depth steps each ending in a draw by workgroup 0, which publishes the fed
+// token as a tagged word; every workgroup then reads that token's embedding
+// row as the next depth input.  The depth K/V history stays in the LDS of the
+// attention workgroups; ring slots are still written to memory.
+template <typename T>
+__global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_frame(FrameArgs fa) {
+  MRT_DECLARE_LDS(T);
+  const StepArgs& at = fa.t;
+  const StepArgs& ad = fa.d;
+  const bool ok = start<T>(c, at.ll, at.bph);
+  prefetch_qkv<T, true>(c, at, 0);
+  __syncthreads();
+  if (!ok) return;
+  if (at.trace != nullptr && c.blk == 0 && threadIdx.x == 0) at.trace[kTraceStart] = wall_clock64();
+  if (c.wid == 3) stage_slots<T>(static_cast<const T*>(ad.dec_norm), ad.D / 64, (long)ad.D * sizeof(T), gam[3]);
+  // ---- temporal step
+  StackIO tio{at.in, at.D, 0u, fa.rec_temporal, true, 0, false, 64, at.pos, at.trace};
+  uint32_t x_tag = run_stack<T, true>(c, at, tio);
+  if (at.trace != nullptr && c.blk == 0 && threadIdx.x == 0) at.trace[kTraceEnd] = at.trace[kTraceDone] = wall_clock64();
+  // ---- depth steps
+  const int L = fa.levels, C = fa.codebook, D = ad.D;
+  const int code0 = 16 * (at.nlayers + 1), per_step = 16 * (ad.nlayers + 1);
+  float fs[4] = {0.f, 0.f, 0.f, 0.f};  // frame sum (workgroup 0)
+  int tok = 0;
+  prefetch_qkv<T, false>(c, ad, 0);
+  for (int l = 0; l < L; ++l) {
+    uint64_t* trace = l == 1 ? ad.trace : nullptr;  // timeline of level 1
+    if (l == 1) {
+      c.tp = 0;
+      c.lcnt = 0;
+      if (trace != nullptr && c.blk == 0 && threadIdx.x == 0) trace[kTraceStart] = wall_clock64();
+    }
+    const int base = code0 + l * per_step;
+    StackIO io{nullptr, 0, x_tag, nullptr, true, base, true, L, l, trace};
+    if (l > 0) {
+      io.in_plain = static_cast<const T*>(ad.emb) + (size_t)tok * D;  // both rows: emb(token)
+      io.in_stride = 0;
+    }
+    x_tag = run_stack<T, false>(c, ad, io);
+    const T* hw = static_cast<const T*>(ad.head_w) + (size_t)l * C * D;
+    prefetch_head<T>(c, ad, hw);
+    const uint32_t tg_logit = c.tag(base + 16 * ad.nlayers + kPhLogit);
+    const uint32_t tg_tok = c.tag(base + 16 * ad.nlayers + kPhToken);
+    run_head<T>(c, ad, hw, x_tag, tg_logit, trace);
+    if (l + 1 < L) prefetch_qkv<T, false>(c, ad, 0);
+    if (c.blk == 0) {
+      if (l + 1 == L && threadIdx.x == 0) astore(ad.ll.seq, c.ep + 1u);  // every workgroup has started
+      __syncthreads();
+      float* lg = c.xsb[c.xsel ^ 1];
+      gather_logits<T>(ad, tg_logit, lg, nullptr, fa.rec_slices ? fa.rec_slices + (size_t)l * 2 * C : nullptr);
+      if (trace != nullptr && threadIdx.x == 0) trace[kTraceEnd] = wall_clock64();
+      tok = sample_block<T>(ad.sp, ad.frame, l, ad.frame * L + l, ad.noise + (size_t)l * C, ad.teacher, ad.tokens,
+                            ad.drawn, static_cast<const T*>(ad.emb), D, fs, static_cast<T*>(ad.fmean), lg, c.sel_hist,
+                            c.sel_res);
+      if (l + 1 < L && threadIdx.x == 0) astore(ad.ll.tok, ll_word((uint32_t)tok, tg_tok));
+      if (trace != nullptr && threadIdx.x == 0) trace[kTraceDone] = wall_clock64();
+    } else if (l + 1 < L) {
+      // every workgroup waits for the draw (one word, polled by one lane)
+      __shared__ int tok_s;
+      if (threadIdx.x == 0) {
+        uint32_t spins = 0;
+        uint64_t w;
+        for (;;) {
+          w = aload(ad.ll.tok);
+          if (ll_tag(w) == tg_tok || spin_failed(spins, ad.ll.err)) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+        // after a failed poll (error flagged) any in-range row keeps the reads in bounds
+        tok_s = ll_tag(w) == tg_tok ? (int)static_cast<uint32_t>(w) : 0;
+      }
+      __syncthreads();
+      tok = tok_s;
+    }
+  }
+}
+
+template <typename T>
 size_t lds_bytes() {
   return 4 * static_cast<size_t>(kRegion) * sizeof(T);
 }
 
-template <typename T, bool CROSS>
-bool allow_lds(size_t dyn, int device) {
+bool allow_lds(const void* fn, size_t dyn, int device) {
   hipFuncAttributes attr{};
-  MRT_HIP_CHECK(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&k_step<T, CROSS>)));
+  MRT_HIP_CHECK(hipFuncGetAttributes(&attr, fn));
   int max_lds = 0;
   MRT_HIP_CHECK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeSharedMemPerBlockOptin, device));
   if (max_lds <= 0) MRT_HIP_CHECK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
   if (attr.sharedSizeBytes + dyn > static_cast<size_t>(max_lds)) return false;
-  MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_step<T, CROSS>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(dyn)));
+  MRT_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(dyn)));
   return true;
+}
+
+template <typename T>
+size_t prepare(PersistKernel kind, int device) {
+  const void* fn = kind == PersistKernel::Temporal ? reinterpret_cast<const void*>(&k_step<T, true>)
+                   : kind == PersistKernel::Depth  ? reinterpret_cast<const void*>(&k_step<T, false>)
+                                                   : reinterpret_cast<const void*>(&k_frame<T>);
+  const size_t n = lds_bytes<T>();
+  return allow_lds(fn, n, device) ? n : 0;
 }
 
 }  // namespace
@@ -1176,17 +1396,8 @@ int persist_grid(int H, int num_cu, int* bph_out) {
   return H * bph;
 }
 
-size_t persist_prepare(DType dt, bool cross, int device) {
-  size_t n = 0;
-  bool ok = false;
-  if (dt == DType::F32) {
-    n = cross ? lds_bytes<float, true>() : lds_bytes<float, false>();
-    ok = cross ? allow_lds<float, true>(n, device) : allow_lds<float, false>(n, device);
-  } else {
-    n = cross ? lds_bytes<bf16, true>() : lds_bytes<bf16, false>();
-    ok = cross ? allow_lds<bf16, true>(n, device) : allow_lds<bf16, false>(n, device);
-  }
-  return ok ? n : 0;
+size_t persist_prepare(DType dt, PersistKernel kind, int device) {
+  return dt == DType::F32 ? prepare<float>(kind, device) : prepare<bf16>(kind, device);
 }
 
 void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t s) {
@@ -1201,6 +1412,14 @@ void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t 
     else
       hipLaunchKernelGGL((k_step<bf16, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
   }
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void launch_frame(DType dt, const FrameArgs& a, int grid, size_t lds, hipStream_t s) {
+  if (dt == DType::F32)
+    hipLaunchKernelGGL((k_frame<float>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+  else
+    hipLaunchKernelGGL((k_frame<bf16>), dim3(grid), dim3(kPersistThreads), lds, s, a);
   MRT_HIP_CHECK(hipGetLastError());
 }
 

@@ -165,6 +165,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_state_read": (i32, [vp, i32, i32, vp, sz]),
         "mrt_df_state_write": (i32, [vp, i32, i32, vp, sz]),
         "mrt_df_state_set_cache_length": (i32, [vp, i32, i32]),
+        "mrt_df_state_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(i32)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -359,6 +360,13 @@ class State:
 
     def set_cache_length(self, kind: int, length: int) -> None:
         _check(self.lib, self.lib.mrt_df_state_set_cache_length(self._h, kind, length))
+
+    def decode_time(self):
+        """(GPU ms, persistent launches) of the decode section of the last
+        generate_tokens call, timed with HIP events on the state's stream."""
+        ms, n = ctypes.c_float(), ctypes.c_int()
+        _check(self.lib, self.lib.mrt_df_state_decode_time(self._h, ctypes.byref(ms), ctypes.byref(n)))
+        return float(ms.value), int(n.value)
 
     def stream_handle(self) -> int:
         s = ctypes.c_void_p()

@@ -1,6 +1,7 @@
-"""Profiling driver: back-to-back depth_step / temporal_step launches at the
-benchmark dims plus a calibration copy of known size, for rocprofv3 counter
-runs (FETCH_SIZE / WRITE_SIZE per dispatch).
+"""Profiling driver: back-to-back depth_step / temporal_step launches and one
+decode of a 50-frame chunk (one frame-kernel launch per frame, no graph) at
+the benchmark dims, plus a calibration copy of known size, for rocprofv3
+counter runs (FETCH_SIZE / WRITE_SIZE per dispatch) and kernel traces.
 
     python magenta-realtime-mlx-cpp_amd/profile_steps.py [--reps N] [--copy-mib M]
 
@@ -64,6 +65,11 @@ def main() -> None:
         st.temporal_step(x, f, out=out, sync=False)
     st.sync()
     print(f"[profile] {scfg.chunk_frames} temporal_step launches", flush=True)
+    opts = mrt_df.GenOptions(num_frames=scfg.chunk_frames, rvq_depth=cfg.rvq_depth, temperature=1.1, top_k=40,
+                             guidance_weight=5.0, seed=a.seed, use_graph=False)
+    st.generate_tokens(None, opts)
+    ms, launches = st.decode_time()
+    print(f"[profile] decode of {scfg.chunk_frames} frames: {launches} persistent launches, {ms:.2f} ms", flush=True)
     st.close()
     model.close()
 

@@ -7,8 +7,11 @@ steps) per dtype.
 Tolerances (norm-wise relative error): fp32 <= 1e-4, bf16 <= 2e-2; fp32
 teacher-forced argmax agreement >= 99 %; bf16 agreement no lower than the
 bf16-vs-fp32 agreement of the oracle itself (bf16 rounding noise bounds it);
-teacher tokens fed back and frame means bit-exact.  The persistent step kernels run at these dims (grid 256, one
-workgroup per CU), so this is the parity check of the benchmarked kernels.
+teacher tokens fed back and frame means bit-exact.  The persistent kernels run
+at these dims (grid 256, one workgroup per CU), so this is the parity check of
+the benchmarked kernels: the decode loop as one launch per frame (default) and
+as one launch per step plus the sampling kernel (MRT_FRAME_KERNEL=0), and the
+temporal_step / depth_step entry points, each one launch.
 """
 
 from __future__ import annotations
@@ -58,11 +61,20 @@ def _oracle(env, dtype):
     return rec
 
 
-def _hip(env, dtype):
+def _hip(env, dtype, path="frame"):
+    import os
     import torch
     mrt_df = env["mrt_df"]
     m = mrt_df.Depthformer(env["w"], env["cfg"], dtype=dtype)
-    st = m.new_state(max_frames=FRAMES)
+    old = os.environ.get("MRT_FRAME_KERNEL")
+    os.environ["MRT_FRAME_KERNEL"] = "1" if path == "frame" else "0"  # read when the state is created
+    try:
+        st = m.new_state(max_frames=FRAMES)
+    finally:
+        if old is None:
+            del os.environ["MRT_FRAME_KERNEL"]
+        else:
+            os.environ["MRT_FRAME_KERNEL"] = old
     F, L, C, D = FRAMES, 16, 1024, env["cfg"].d_model
     rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"),
                temporal=torch.zeros((F, 2, D), dtype=m.torch_dtype, device="cuda"),
@@ -94,9 +106,10 @@ def _guided_argmax(slices, w=5.0):
     return np.argmax((1 + w) * slices[:, :, 0] - w * slices[:, :, 1], -1)
 
 
-@pytest.mark.parametrize("dtype,tol", [("fp32", 1e-4), ("bf16", 2e-2)])
-def test_full_size_teacher_forced(env, dtype, tol):
-    g = _hip(env, dtype)
+@pytest.mark.parametrize("dtype,tol,path", [("fp32", 1e-4, "frame"), ("bf16", 2e-2, "frame"),
+                                            ("fp32", 1e-4, "steps"), ("bf16", 2e-2, "steps")])
+def test_full_size_teacher_forced(env, dtype, tol, path):
+    g = _hip(env, dtype, path)
     o = _oracle_cached(env, dtype)
     np.testing.assert_array_equal(g["tokens"], env["teacher"])
     assert rel(g["enc_out"], o["enc_out"]) <= tol
@@ -122,3 +135,43 @@ def test_full_size_teacher_forced(env, dtype, tol):
     # every draw falls in its level's 1024-id range
     lo = 2 + 1024 * np.arange(16)[None, :]
     assert ((g["drawn"] >= lo) & (g["drawn"] < lo + 1024)).all()
+
+
+@pytest.mark.parametrize("dtype,tol", [("fp32", 1e-4), ("bf16", 2e-2)])
+def test_full_size_step_entry_points(env, dtype, tol):
+    """temporal_step and depth_step (one persistent launch each) on the
+    oracle's own inputs of the teacher-forced decode: frame f's temporal input
+    is emb(PAD) / the previous frame mean, depth step l's input is the temporal
+    output / emb(teacher[f, l-1]) on both rows.  Depth steps alternate between
+    the full vocabulary (checked against the oracle's depth_step) and the
+    level slice (checked against the recorded slice)."""
+    import torch
+    mrt_df, O = env["mrt_df"], env["O"]
+    o = _oracle_cached(env, dtype)
+    om = O.OracleDepthformer(env["w"], O.DepthformerConfig(**dataclasses.asdict(env["cfg"])), mode=dtype)
+    m = mrt_df.Depthformer(env["w"], env["cfg"], dtype=dtype)
+    st = m.new_state(max_frames=FRAMES)
+    st.encode(env["tok"])
+    D, C = env["cfg"].d_model, 1024
+    dev = lambda a: torch.tensor(np.asarray(a, dtype=np.float32), dtype=m.torch_dtype, device="cuda")
+    for f in range(FRAMES):
+        t_in = om.embed(np.zeros((2,), dtype=np.int64)) if f == 0 else o["frame_mean"][f - 1]
+        out = st.temporal_step(dev(t_in), f).float().cpu().numpy()
+        assert rel(out, o["temporal_out"][f]) <= tol, f
+        cache = om.empty_depth_cache()
+        for l in range(16):
+            x = o["temporal_out"][f] if l == 0 else om.embed(np.full((2,), env["teacher"][f, l - 1], dtype=np.int64))
+            lo = 2 + C * l
+            if f == 0 and l % 4 == 0:
+                exp = om.depth_step(np.asarray(x, dtype=np.float32)[:, None], cache, l)
+                got = st.depth_step(dev(x), l).cpu().numpy()
+                assert got.shape == (2, env["cfg"].vocab_size)
+                assert rel(got, exp) <= tol, (f, l)
+                assert rel(got[:, lo:lo + C], o["slices"][f, l]) <= tol, (f, l)
+            else:
+                if f == 0:
+                    om.depth_step(np.asarray(x, dtype=np.float32)[:, None], cache, l)
+                got = st.depth_step(dev(x), l, level=l, codebook_size=C, codec_offset=2).cpu().numpy()
+                assert rel(got, o["slices"][f, l]) <= tol, (f, l)
+    st.close()
+    m.close()
