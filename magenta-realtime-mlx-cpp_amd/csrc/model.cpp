@@ -344,7 +344,8 @@ State::State(Model& model, int rows_, int max_frames, int enc_len)
 }
 
 // The persistent path needs: head dim 64 (checked by Model), every GEMV input
-// <= 1024 wide except d_ff <= 3072, rings of <= 64 slots, and a grid of
+// <= 1024 wide except d_ff <= 3072, GEMV inputs in whole 16-byte chunks
+// (d_model % 8 == 0), rings of <= 64 slots, and a grid of
 // H * bph workgroups (bph >= 8) that fits on the device.
 void State::setup_persistent() {
   const Config& c = m.cfg;
@@ -354,7 +355,8 @@ void State::setup_persistent() {
   const int grid = persist_grid(c.num_heads, num_cu, &bph);
   // Every workgroup must own rows of the d_model and d_ff phases (the launch
   // epoch advances once data from all workgroups has been seen).
-  const bool ok = grid > 0 && c.d_model <= 1024 && c.hd() <= 1024 && c.d_ff <= kMaxPersistK && c.d_ff % 32 == 0 &&
+  const bool ok = grid > 0 && c.d_model <= 1024 && c.d_model % 8 == 0 && c.hd() <= 1024 && c.d_ff <= kMaxPersistK &&
+                  c.d_ff % 32 == 0 &&
                   F <= kMaxPersistLen && c.rvq_depth <= kMaxPersistLen && S <= kMaxCrossChunk * bph && c.d_model >= grid &&
                   c.d_ff >= grid;
   if (!ok) return;
@@ -422,7 +424,7 @@ void State::print_trace() {
     uint64_t prev = t0;
     int nb = 0;
     for (int k = 0; k < 400 && r[k]; ++k, ++nb) {
-      if (k < 48) {
+      if (k < (w == 0 ? 48 : 100)) {
         char buf[32];
         std::snprintf(buf, sizeof buf, " %.2f", (r[k] - prev) * 0.01);
         line += buf;
@@ -444,6 +446,17 @@ void State::print_trace() {
       pw += "]";
     }
     std::fprintf(stderr, "[mrt] %s: per-wave poll done (us after load start):%s\n", names[w], pw.c_str());
+    if (r[490]) {  // inside the draw: after v, 4 radix passes, argmax, end
+      std::string dl;
+      uint64_t pv = r[kTraceEnd];
+      for (int k = 490; k < 497 && r[k]; ++k) {
+        char buf[32];
+        std::snprintf(buf, sizeof buf, " %.2f", (r[k] - pv) * 0.01);
+        dl += buf;
+        pv = r[k];
+      }
+      std::fprintf(stderr, "[mrt] %s: draw deltas us (from gather end):%s\n", names[w], dl.c_str());
+    }
   }
 }
 

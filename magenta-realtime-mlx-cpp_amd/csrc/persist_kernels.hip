@@ -272,50 +272,66 @@ __device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t
 
 constexpr int kLoadTrace = 400;  // start of the first 16 activation loads
 constexpr int kWaveTrace = 420;  // per-wave poll completion of the first 16 loads
+constexpr int kDrawTrace = 490;  // 7 points inside a draw
 
 __device__ __forceinline__ void trace_point(uint64_t* trace, int slot) {
   if (trace != nullptr && blockIdx.x == 0 && threadIdx.x == 0 && slot < kLoadTrace) trace[slot] = wall_clock64();
 }
 
+// Norm weights of the elements a thread owns in load_act (k = tid + 256 i),
+// loaded into registers ahead of the weight prefetch of the phase that uses
+// them and kept raw (model dtype) so that nothing waits for the load before
+// the norm; elements past K are masked there.
+template <typename T, int NPER>
+struct Gamma {
+  T g[NPER];
+  __device__ float get(int i, int K) const {
+    return threadIdx.x + i * kPersistThreads < K ? St<T>::ld(g[i]) : 0.f;
+  }
+};
+
+template <typename T, int NPER>
+__device__ __forceinline__ void load_gamma(const T* g, int K, Gamma<T, NPER>& out) {
+#pragma unroll
+  for (int i = 0; i < NPER; ++i) out.g[i] = ld_g(g + min((int)threadIdx.x + i * kPersistThreads, K - 1));
+}
+
 // Loads the activation vector of a phase (K <= 256 * NPER elements; tagged,
 // or plain input rows) into LDS, with an optional side element.
-// NORM: RMS norm with the LDS-staged weight g (modules.cpp:72-84): the sum of
-// squares is taken from the polled values in registers, and each element is
-// written to LDS once, normalised.
+// NORM: RMS norm with the weights gk (modules.cpp:72-84): the sum of squares
+// is taken from the polled values in registers, and each element is written
+// to LDS once, normalised (zero past K, where the GEMV meets zero weights).
 template <typename T, int NPER, bool NORM>
-__device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, int K, uint32_t tag, const T* g,
-                                         float* xs, float* red, const Side& sd, float& r0, float& r1, int* err,
-                                         uint64_t* trace, int& tp, int& lc, int stride) {
+__device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, int K, uint32_t tag,
+                                         const Gamma<T, NPER>& gk, float* xs, float* red, const Side& sd, float& r0,
+                                         float& r1, int* err, uint64_t* trace, int& tp, int& lc, int stride) {
   using S = St<T>;
   const int tid = threadIdx.x;
   if (trace != nullptr && blockIdx.x == 0 && tid == 0 && lc < 16) trace[kLoadTrace + lc] = wall_clock64();
   trace_point(trace, tp++);
   float v0[NPER], v1[NPER];
+#pragma unroll
+  for (int i = 0; i < NPER; ++i) v0[i] = v1[i] = 0.f;
   if (plain != nullptr) {  // two model-dtype rows, row 1 at +stride (0: the same row twice)
     const T* p = static_cast<const T*>(plain);
     T w0[NPER], w1[NPER];
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
-      const int k = tid + i * kPersistThreads;
-      if (k < K) {
-        w0[i] = ld_g(p + k);
-        w1[i] = ld_g(p + stride + k);
-      }
+      const int k = min(tid + i * kPersistThreads, K - 1);
+      w0[i] = ld_g(p + k);
+      w1[i] = ld_g(p + stride + k);
     }
 #pragma unroll
     for (int i = 0; i < NPER; ++i) {
-      const int k = tid + i * kPersistThreads;
-      if (k < K) {
-        v0[i] = S::ld(w0[i]);
-        v1[i] = S::ld(w1[i]);
-        if constexpr (!NORM) Act<T>::put(xs, k, v0[i], v1[i]);
-      }
+      const bool in = tid + i * kPersistThreads < K;
+      v0[i] = in ? S::ld(w0[i]) : 0.f;
+      v1[i] = in ? S::ld(w1[i]) : 0.f;
+      if constexpr (!NORM) Act<T>::put(xs, tid + i * kPersistThreads, v0[i], v1[i]);
     }
     ll_load_vec<T, NPER, NORM>(nullptr, 0, 0, xs, v0, v1, sd, r0, r1, err);
   } else {
     ll_load_vec<T, NPER, NORM>(ll, K, tag, xs, v0, v1, sd, r0, r1, err);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // LDS copies issued by this wave (norm weights) have landed
   if (trace != nullptr && blockIdx.x == 0 && (tid & 63) == 0 && lc < 16) trace[kWaveTrace + 4 * lc + (tid >> 6)] = wall_clock64();
   ++lc;
   trace_point(trace, tp++);
@@ -323,11 +339,9 @@ __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, 
     const float inv_k = 1.0f / (float)K;
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int i = 0; i < NPER; ++i) {
-      if (tid + i * kPersistThreads < K) {
-        s0 = fmaf(v0[i], v0[i], s0);
-        s1 = fmaf(v1[i], v1[i], s1);
-      }
+    for (int i = 0; i < NPER; ++i) {  // zero past K
+      s0 = fmaf(v0[i], v0[i], s0);
+      s1 = fmaf(v1[i], v1[i], s1);
     }
     s0 = dpp_sum(s0);
     s1 = dpp_sum(s1);
@@ -337,18 +351,14 @@ __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, 
       red[4 + wid] = s1;
     }
     __syncthreads();
-    float gk[NPER];
+    const float4 ra = *reinterpret_cast<const float4*>(red);
+    const float4 rb = *reinterpret_cast<const float4*>(red + 4);
+    const float inv0 = rsqrt_nr((ra.x + ra.y + ra.z + ra.w) * inv_k + 1e-6f);
+    const float inv1 = rsqrt_nr((rb.x + rb.y + rb.z + rb.w) * inv_k + 1e-6f);
 #pragma unroll
-    for (int i = 0; i < NPER; ++i) {
-      const int k = tid + i * kPersistThreads;
-      gk[i] = k < K ? S::ld(g[k]) : 0.f;
-    }
-    const float inv0 = rsqrt_nr((red[0] + red[1] + red[2] + red[3]) * inv_k + 1e-6f);
-    const float inv1 = rsqrt_nr((red[4] + red[5] + red[6] + red[7]) * inv_k + 1e-6f);
-#pragma unroll
-    for (int i = 0; i < NPER; ++i) {
-      const int k = tid + i * kPersistThreads;
-      if (k < K) Act<T>::put(xs, k, S::rnd(S::rnd(v0[i] * inv0) * gk[i]), S::rnd(S::rnd(v1[i] * inv1) * gk[i]));
+    for (int i = 0; i < NPER; ++i) {  // gamma is zero past K
+      const float g = gk.get(i, K);
+      Act<T>::put(xs, tid + i * kPersistThreads, S::rnd(S::rnd(v0[i] * inv0) * g), S::rnd(S::rnd(v1[i] * inv1) * g));
     }
   }
   __syncthreads();
@@ -360,7 +370,10 @@ __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, 
 constexpr int kNBuf = 12;  // 16-byte weight registers per thread
 
 // Loads the rows of one batch (R rows of P parts; row indices wave-uniform)
-// into registers; 16-byte chunks past the end of a row are zero.
+// into registers; 16-byte chunks past the end of a row are zero.  (The zero
+// fill makes the compiler wait for older loads of the wave before each row;
+// with vmcnt in order, that staggering keeps the next poll from queueing
+// behind a whole batch, which measured faster than issuing every load at once.)
 template <typename T, int NV, int P, bool NT, class RowOf>
 __device__ __forceinline__ void fetch_batch(uint4 (&buf)[kNBuf], const T* W, int K, int b0, int nb, RowOf row_of) {
   constexpr int V = St<T>::kVec;
@@ -412,7 +425,7 @@ struct Dot<float> {
 };
 
 // Dots of a batch against the two activation rows (model dtype in LDS; the
-// buffer is zero past every row's end, so zero weight chunks meet finite
+// weight chunks are zero past every row's end, where they meet finite
 // activations).  epi(t, active, sums[P][2]) runs once on every lane: lane r
 // holds the sums of the batch's row r (wave-local row index t = b0 + r) and
 // is active when that row exists.
@@ -725,151 +738,233 @@ __device__ __forceinline__ void cross_combine(const StepArgs& a, int h, uint32_t
 
 // ---- sampling -------------------------------------------------------------------
 
-// Block-wide CFG + temperature/top-k Gumbel-max draw and token feedback
-// (decode.cpp:71-148, 458-484) for one level: `lg` holds the two logit rows
-// of the level slice in LDS, `noise` the precomputed Gumbel noise of the draw.
-// The top-k threshold (k-th largest value, ties kept) is found by a
-// most-significant-byte-first radix select over LDS histograms.  The running
-// frame sum of the fed-back embeddings stays in registers (`fs`, 4 elements
-// per thread, model dtype); the last level writes the frame mean (both rows)
-// to `fmean`.  Returns the fed-back token (the same in every thread).
-template <typename T>
-__device__ __forceinline__ int sample_block(const SampleParams& p, int frame, int level, int slot,
-                                            const float* noise, const int* teacher, int* tokens, int* drawn,
-                                            const T* emb, int D, float (&fs)[4], T* fmean, const float* lg,
-                                            unsigned* hist, int* sel) {
-  using S = St<T>;
-  constexpr int kPer = 1024 / kPersistThreads;  // candidates and d_model elements per thread
+constexpr int kDrawPer = 1024 / kPersistThreads;  // candidates and d_model elements per thread
+constexpr int kHistWords = 3 * 4 * 256;           // 3 rotating buffers x 4 per-wave 256-bin histograms
+
+// Loads of a draw that do not depend on the logits (issued before the gather).
+struct DrawPrefetch {
+  float gn[kDrawPer];  // Gumbel noise of this thread's candidates
+  int teacher_id;
+};
+
+__device__ __forceinline__ void draw_prefetch(int C, const float* noise, const int* teacher, int slot,
+                                              DrawPrefetch& d) {
+#pragma unroll
+  for (int t = 0; t < kDrawPer; ++t) {
+    const int c = threadIdx.x + kPersistThreads * t;
+    d.gn[t] = c < C ? ld_g(noise + c) : 0.f;
+  }
+  d.teacher_id = teacher ? ld_g(teacher + slot) : 0;
+}
+
+// Zeroes the histogram buffers of the first two radix passes of the next draw
+// (the caller orders this before the draw with a barrier).
+__device__ __forceinline__ void draw_clear(unsigned* hist) {
+  for (int i = threadIdx.x; i < 2 * 4 * 256; i += kPersistThreads) hist[i] = 0u;
+}
+
+// Block argmax of w (ties to the smallest candidate index), candidate c =
+// tid + 256 t.  One barrier; wres[0..7] is written.
+__device__ __forceinline__ int block_argmax(const float (&w)[kDrawPer], int C, int* wres) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int C = p.codebook;
-  // Loads that do not depend on the draw go first.
-  float gn[kPer];
-#pragma unroll
-  for (int t = 0; t < kPer; ++t) {
-    const int c = tid + kPersistThreads * t;
-    gn[t] = c < C ? ld_g(noise + c) : 0.f;
-  }
-  const int teacher_id = teacher ? ld_g(teacher + slot) : 0;
-  const float wc = 1.0f + p.guidance_weight, wu = p.guidance_weight;
-  float v[kPer];
-#pragma unroll
-  for (int t = 0; t < kPer; ++t) {
-    const int c = tid + kPersistThreads * t;
-    v[t] = (c < C) ? __fsub_rn(__fmul_rn(wc, lg[c]), __fmul_rn(wu, lg[C + c])) : -INFINITY;
-  }
-  if (p.temperature != 0.0f) {
-#pragma unroll
-    for (int t = 0; t < kPer; ++t)
-      if (tid + kPersistThreads * t < C) v[t] = __fdiv_rn(v[t], p.temperature);
-    if (p.top_k > 0 && p.top_k < C) {
-      uint32_t key[kPer];
-#pragma unroll
-      for (int t = 0; t < kPer; ++t) key[t] = (tid + kPersistThreads * t < C) ? float_key(v[t]) : 0u;
-      uint32_t prefix = 0, mask = 0;
-      int need = p.top_k;
-      for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 24 - 8 * pass;
-        hist[tid] = 0u;
-        __syncthreads();
-#pragma unroll
-        for (int t = 0; t < kPer; ++t)
-          if (tid + kPersistThreads * t < C && (key[t] & mask) == prefix) atomicAdd(&hist[(key[t] >> shift) & 255u], 1u);
-        __syncthreads();
-        if (wid == 0) {
-          // lane l holds bins 4l..4l+3; suffix counts from the top bin down
-          const unsigned c0 = hist[4 * lane], c1 = hist[4 * lane + 1], c2 = hist[4 * lane + 2], c3 = hist[4 * lane + 3];
-          const unsigned own = c0 + c1 + c2 + c3;
-          unsigned suf = own;  // inclusive suffix sum over lanes >= lane
-#pragma unroll
-          for (int o = 1; o < 64; o <<= 1) {
-            const unsigned up = __shfl_down(suf, o, 64);
-            if (lane + o < 64) suf += up;
-          }
-          unsigned above = suf - own;  // keys in bins above this lane's
-          const unsigned cs[4] = {c0, c1, c2, c3};
-#pragma unroll
-          for (int i = 3; i >= 0; --i) {
-            if (above < (unsigned)need && above + cs[i] >= (unsigned)need) {
-              sel[0] = 4 * lane + i;
-              sel[1] = (int)above;
-            }
-            above += cs[i];
-          }
-        }
-        __syncthreads();
-        prefix |= (uint32_t)sel[0] << shift;
-        mask |= 255u << shift;
-        need -= sel[1];
-        __syncthreads();  // sel and hist are rewritten by the next pass
-      }
-      const float thr = key_float(prefix);
-#pragma unroll
-      for (int t = 0; t < kPer; ++t)
-        if (v[t] < thr) v[t] = -INFINITY;
-    }
-#pragma unroll
-    for (int t = 0; t < kPer; ++t)
-      if (v[t] != -INFINITY) v[t] = v[t] + gn[t];
-  }
-  // argmax, ties to the smallest index
   float best = -INFINITY;
   int bi = 0x7fffffff;
 #pragma unroll
-  for (int t = 0; t < kPer; ++t) {
+  for (int t = 0; t < kDrawPer; ++t) {
     const int c = tid + kPersistThreads * t;
-    if (c < C && (v[t] > best || bi == 0x7fffffff)) {
-      best = v[t];
+    if (c < C && (w[t] > best || bi == 0x7fffffff)) {
+      best = w[t];
       bi = c;
     }
   }
   const float wmx = dpp_max(best);
   const int warg = dpp_min_i(best == wmx ? bi : 0x7fffffff);
-  float* wbest = reinterpret_cast<float*>(hist);
-  int* widx = sel + 4;
   if (lane == 0) {
-    wbest[wid] = wmx;
-    widx[wid] = warg;
+    wres[wid] = __float_as_int(wmx);
+    wres[4 + wid] = warg;
   }
   __syncthreads();
-  float mx = wbest[0];
-  int arg = widx[0];
+  float mx = __int_as_float(wres[0]);
+  int arg = wres[4];
 #pragma unroll
-  for (int w = 1; w < 4; ++w)
-    if (wbest[w] > mx || (wbest[w] == mx && widx[w] < arg)) {
-      mx = wbest[w];
-      arg = widx[w];
+  for (int q = 1; q < 4; ++q) {
+    const float m = __int_as_float(wres[q]);
+    const int ix = wres[4 + q];
+    if (m > mx || (m == mx && ix < arg)) {
+      mx = m;
+      arg = ix;
     }
-  const int drawn_id = p.codec_offset + level * C + arg;
-  const int fed = teacher ? teacher_id : drawn_id;
-  if (tid == 0) {
-    st_g(tokens + slot, fed);
-    if (drawn) st_g(drawn + slot, drawn_id);
   }
-  // Frame sum in the model dtype; the last level's sum / L is the next
-  // temporal input (decode.cpp:263-273, 476-484).
-  const T* e = emb + (size_t)fed * D;
-  float ev[kPer];
+  return arg;
+}
+
+// k-th largest key of the candidates (ties counted), by a most-significant-
+// byte-first radix select: each pass counts the candidates into per-wave
+// 256-bin LDS histograms, and after one barrier every wave scans the four
+// histograms itself, so the selected digit needs no broadcast.  Pass p uses
+// buffer p % 3; buffer (p + 2) % 3, last read before this pass's barrier, is
+// cleared for pass p + 2.  Buffers 0 and 1 must be zero on entry.
+__device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[kDrawPer], int C, int k, unsigned* hist) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  uint32_t prefix = 0, mask = 0;
+  int need = k;
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    unsigned* hb = hist + (pass % 3) * 1024;
+#pragma unroll
+    for (int t = 0; t < kDrawPer; ++t)
+      if (tid + kPersistThreads * t < C && (key[t] & mask) == prefix)
+        atomicAdd(&hb[wid * 256 + ((key[t] >> shift) & 255u)], 1u);
+    __syncthreads();
+    if (pass < 2) {  // buffer of pass + 2 (pass 2: buffer 2, pass 3: buffer 0)
+      unsigned* hc = hist + ((pass + 2) % 3) * 1024;
+      for (int i = tid; i < 1024; i += kPersistThreads) hc[i] = 0u;
+    }
+    // lane l holds bins 4l..4l+3 summed over the waves; suffix counts from the top bin down
+    unsigned cs[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint4 h4 = *reinterpret_cast<const uint4*>(hb + q * 256 + 4 * lane);
+      cs[0] += h4.x;
+      cs[1] += h4.y;
+      cs[2] += h4.z;
+      cs[3] += h4.w;
+    }
+    const unsigned own = cs[0] + cs[1] + cs[2] + cs[3];
+    unsigned suf = own;  // inclusive suffix sum over lanes >= lane
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const unsigned up = __shfl_down(suf, o, 64);
+      if (lane + o < 64) suf += up;
+    }
+    unsigned above = suf - own;  // keys in bins above this lane's
+    int bin = -1, before = 0;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) {
+      if (bin < 0 && above < (unsigned)need && above + cs[i] >= (unsigned)need) {
+        bin = 4 * lane + i;
+        before = (int)above;
+      }
+      above += cs[i];
+    }
+    // exactly one lane finds the bin (the counts sum to >= need)
+    const uint64_t hit = __ballot(bin >= 0);
+    const int src = hit ? (int)__builtin_ctzll(hit) : 0;
+    prefix |= (uint32_t)uniform(__shfl(bin, src, 64)) << shift;
+    mask |= 255u << shift;
+    need -= uniform(__shfl(before, src, 64));
+  }
+  return prefix;
+}
+
+// Block-wide CFG + temperature/top-k Gumbel-max draw (decode.cpp:71-148,
+// 465-474) for one level: `lg` holds the two logit rows of the level slice in
+// LDS.  The reference masks every logit below the k-th largest (ties kept) and
+// takes the argmax of logit + Gumbel noise, ties to the smallest index.  Fast
+// path: A = argmax of v + g over all candidates is that answer whenever A is
+// in the top-k set, i.e. fewer than k values are strictly greater than v_A
+// (every candidate of the set is a candidate of the full argmax, and A is the
+// smallest index attaining its maximum).  Otherwise the k-th largest value is
+// found by radix select and the masked argmax is taken.  The fed token is
+// published (`tok_word`, tagged, when non-null) as soon as it is known.
+// Returns the fed token (the same in every thread).
+template <typename T>
+__device__ __forceinline__ int sample_block(const SampleParams& p, int level, int slot, const DrawPrefetch& pf,
+                                            bool teacher, int* tokens, int* drawn, uint64_t* tok_word,
+                                            uint32_t tok_tag, const float* lg, unsigned* hist, int* wres,
+                                            uint64_t* trace) {
+  constexpr int kPer = kDrawPer;
+  const int tid = threadIdx.x, wid = tid >> 6;
+  const int C = p.codebook;
+  const float wc = 1.0f + p.guidance_weight, wu = p.guidance_weight;
+  auto tpoint = [&](int i) {
+    if (trace != nullptr && tid == 0) trace[kDrawTrace + i] = wall_clock64();
+  };
+  auto guided = [&](int c) { return __fsub_rn(__fmul_rn(wc, lg[c]), __fmul_rn(wu, lg[C + c])); };
+  float v[kPer];
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {
-    const int d = tid + kPersistThreads * t;
-    ev[t] = d < D ? S::ld(ld_g(e + d)) : 0.f;
+    const int c = tid + kPersistThreads * t;
+    v[t] = (c < C) ? guided(c) : -INFINITY;
   }
+  tpoint(0);
+  int arg;
+  if (p.temperature == 0.0f) {
+    arg = block_argmax(v, C, wres);
+  } else {
 #pragma unroll
-  for (int t = 0; t < kPer; ++t) fs[t] = level == 0 ? ev[t] : S::rnd(fs[t] + ev[t]);
-  if (level == p.rvq_depth - 1) {
-    const float Lf = S::rnd((float)p.rvq_depth);
+    for (int t = 0; t < kPer; ++t)
+      if (tid + kPersistThreads * t < C) v[t] = __fdiv_rn(v[t], p.temperature);
+    float w[kPer];
 #pragma unroll
-    for (int t = 0; t < kPer; ++t) {
-      const int d = tid + kPersistThreads * t;
-      if (d < D) {
-        const T m = S::st(fs[t] / Lf);
-        st_g(fmean + d, m);
-        st_g(fmean + D + d, m);
+    for (int t = 0; t < kPer; ++t) w[t] = v[t] != -INFINITY ? v[t] + pf.gn[t] : -INFINITY;
+    arg = block_argmax(w, C, wres);
+    tpoint(1);
+    if (p.top_k > 0 && p.top_k < C) {
+      const float va = __fdiv_rn(guided(arg), p.temperature);
+      int n = 0;
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) n += __popcll(__ballot(tid + kPersistThreads * t < C && v[t] > va));
+      if ((tid & 63) == 0) wres[8 + wid] = n;
+      __syncthreads();
+      const int greater = wres[8] + wres[9] + wres[10] + wres[11];
+      tpoint(2);
+      if (greater >= p.top_k) {  // the unmasked winner is outside the top-k set
+        uint32_t key[kPer];
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) key[t] = (tid + kPersistThreads * t < C) ? float_key(v[t]) : 0u;
+        const float thr = key_float(radix_select(key, C, p.top_k, hist));
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) w[t] = (v[t] >= thr && v[t] != -INFINITY) ? v[t] + pf.gn[t] : -INFINITY;
+        arg = block_argmax(w, C, wres);
+        for (int i = tid; i < 2 * 4 * 256; i += kPersistThreads) hist[i] = 0u;  // buffers 0 / 1 for the next draw
+        tpoint(3);
       }
     }
   }
-  __syncthreads();  // hist / sel are reused by the next draw
+  const int drawn_id = p.codec_offset + level * C + arg;
+  const int fed = teacher ? pf.teacher_id : drawn_id;
+  if (tid == 0) {
+    if (tok_word != nullptr) astore(tok_word, ll_word((uint32_t)fed, tok_tag));
+    st_g(tokens + slot, fed);
+    if (drawn) st_g(drawn + slot, drawn_id);
+  }
+  tpoint(4);
   return fed;
+}
+
+// Running frame sum of the fed embeddings in the model dtype (decode.cpp:263-273,
+// 476-484): fs = emb(tok) at level 0, else rnd(fs + emb(tok)); thread tid owns
+// elements tid + 256 t.
+template <typename T>
+__device__ __forceinline__ void frame_sum_add(float (&fs)[kDrawPer], const T* emb, int tok, int D, bool first) {
+  using S = St<T>;
+  const T* e = emb + (size_t)tok * D;
+  float ev[kDrawPer];
+#pragma unroll
+  for (int t = 0; t < kDrawPer; ++t) {
+    const int d = threadIdx.x + kPersistThreads * t;
+    ev[t] = d < D ? S::ld(ld_g(e + d)) : 0.f;
+  }
+#pragma unroll
+  for (int t = 0; t < kDrawPer; ++t) fs[t] = first ? ev[t] : S::rnd(fs[t] + ev[t]);
+}
+
+// Frame mean fs / L on both rows: the next temporal input (decode.cpp:484).
+template <typename T>
+__device__ __forceinline__ void frame_mean_store(const float (&fs)[kDrawPer], int L, T* fmean, int D) {
+  using S = St<T>;
+  const float Lf = S::rnd((float)L);
+#pragma unroll
+  for (int t = 0; t < kDrawPer; ++t) {
+    const int d = threadIdx.x + kPersistThreads * t;
+    if (d < D) {
+      const T m = S::st(fs[t] / Lf);
+      st_g(fmean + d, m);
+      st_g(fmean + D + d, m);
+    }
+  }
 }
 
 __global__ void k_gumbel_table(const uint64_t* __restrict__ seed_p, int frames, int L, int C, float* __restrict__ out) {
@@ -895,7 +990,7 @@ struct Ctx {
   float* red;
   float* sm;
   float (*kvst)[2][16];  // [k|v][row][d within this workgroup's slice]
-  T (*gam)[1024];        // norm weights: self-attn, cross-attn, FFN, decoder_norm
+  Gamma<T, 4> gq;        // norm weights of the next QKV / head input
   unsigned* sel_hist;
   int* sel_res;
   T* dyn;                // attention staging (4 regions of kRegion)
@@ -931,12 +1026,14 @@ __device__ __forceinline__ int qkv_rows(const Ctx<T>& c) {
   return (3 * c.rps > c.wid) ? (3 * c.rps - c.wid + 3) / 4 : 0;
 }
 
-// Prefetches the first QKV batch of layer `li` of a stack into c.buf.
+// Prefetches the self-attention norm weights (c.gq) and the first QKV batch
+// (c.buf) of layer `li` of a stack.
 template <typename T, bool NT>
 __device__ __forceinline__ void prefetch_qkv(Ctx<T>& c, const StepArgs& a, int li) {
   constexpr int V = St<T>::kVec;
   constexpr int NVD = (1024 + V * 64 - 1) / (V * 64);
   const int HD = a.HD, D = a.D, h = c.h, jpart = c.jpart, rps = c.rps, wid = c.wid;
+  load_gamma<T, 4>(static_cast<const T*>(a.st.norm_sa) + (size_t)li * D, D, c.gq);
   auto qkv_row = [&](int t, int) {
     const int lt = wid + 4 * t;
     return (lt / rps) * HD + h * 64 + jpart * rps + (lt % rps);
@@ -999,11 +1096,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     T* ring_k = static_cast<T*>(a.st.ring) + 2 * li * eRing;
     const void* in_plain = first ? io.in_plain : nullptr;
     const int in_stride = io.in_stride;
-    // ---- stage the norm weights, ring history and cross K/V block of this layer in LDS
-    if (wid < 3 && (CROSS || wid != 1)) {
-      const void* g = pick3<const void*>(wid, a.st.norm_sa, a.st.norm_ca, a.st.norm_ff);
-      stage_slots<T>(static_cast<const T*>(g) + (size_t)li * D, D / 64, (long)D * sizeof(T), c.gam[wid]);
-    }
+    // ---- stage the ring history and cross K/V block of this layer in LDS
     T* lhist = io.resident ? hist + (size_t)li * 4 * io.cap * 64 : hist;
     if (!io.resident && jpart == 0 && io.pos > 0) {
       const int kind = wid >> 1, b = wid & 1;
@@ -1023,7 +1116,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     if (CROSS && jpart != 0) stage_cross();
     // ---- QKV of head h's slice (weights already in flight)
     xs = c.next_xs();
-    load_act<T, 4, true>(a.ll.x, in_plain, D, x_tag, c.gam[0], xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
+    load_act<T, 4, true>(a.ll.x, in_plain, D, x_tag, c.gq, xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
                          c.lcnt, in_stride);
     gemv_rows<T, NVD, 1, NT>(c.buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs,
                              [&](int t, bool act, const float (&s)[1][2]) {
@@ -1067,7 +1160,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     fetch_batch<T, NVD, 1, NT>(c.buf, wo, HD, 0, min(kNBuf / NVD, sD.nw(wid)), rowD);
     // ---- attention output projection + residual
     xs = c.next_xs();
-    load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhAtt), nullptr, xs, red,
+    load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhAtt), c.gq, xs, red,
                           side_x(a.ll.x, in_plain, x_tag, in_stride), r0, r1, a.ll.err, io.trace, c.tp, c.lcnt, 0);
     gemv_rows<T, NVD, 1, NT>(c.buf, wo, HD, sD.nw(wid), rowD, xs,
                              [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhO)); });
@@ -1077,9 +1170,11 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
       // ---- cross attention: q rows of head h, key-block partials, combine
       const T* wqc = static_cast<const T*>(a.st.wq_c) + li * eQc;
       const T* woc = static_cast<const T*>(a.st.wo_c) + li * eO;
+      Gamma<T, 4> gc;
+      load_gamma<T, 4>(static_cast<const T*>(a.st.norm_ca) + (size_t)li * D, D, gc);
       fetch_batch<T, NVD, 1, NT>(c.buf, wqc, D, 0, min(kNBuf / NVD, ncq), cq_row);
       xs = c.next_xs();
-      load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, c.gam[1], xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
+      load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gc, xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
                            c.lcnt, 0);
       gemv_rows<T, NVD, 1, NT>(c.buf, wqc, D, ncq, cq_row, xs, [&](int t, bool act, const float (&s)[1][2]) {
         if (act) LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(s[0][0]), S::rnd(s[0][1]), tag(base + kPhCQ));
@@ -1093,7 +1188,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
         MRT_TP;
       }
       xs = c.next_xs();
-      load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhCC), nullptr, xs, red,
+      load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhCC), c.gq, xs, red,
                             side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, io.trace, c.tp, c.lcnt, 0);
       gemv_rows<T, NVD, 1, NT>(c.buf, woc, HD, sD.nw(wid), rowD, xs,
                                [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhCO)); });
@@ -1103,9 +1198,11 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     // ---- gated-GELU up projection
     const T* w01 = static_cast<const T*>(a.st.w01) + li * e01;
     const T* wo2 = static_cast<const T*>(a.st.wo2) + li * eO2;
+    Gamma<T, 4> gf;
+    load_gamma<T, 4>(static_cast<const T*>(a.st.norm_ff) + (size_t)li * D, D, gf);
     fetch_batch<T, NVD, 2, NT>(c.buf, w01, D, 0, min(kNBuf / (2 * NVD), sF.nw(wid)), rowF);
     xs = c.next_xs();
-    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, c.gam[2], xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
+    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gf, xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
                          c.lcnt, 0);
     gemv_rows<T, NVD, 2, NT>(c.buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, bool act, const float (&s)[2][2]) {
       const float g0 = gelu_t<T>(S::rnd(s[0][0])), g1 = gelu_t<T>(S::rnd(s[0][1]));
@@ -1117,7 +1214,8 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     // ---- down projection + residual
     fetch_batch<T, NVF, 1, NT>(c.buf, wo2, F, 0, min(kNBuf / NVF, sD.nw(wid)), rowD);
     xs = c.next_xs();
-    load_act<T, kMaxPersistK / kPersistThreads, false>(a.ll.h, nullptr, F, tag(base + kPhUp), nullptr, xs, red,
+    const Gamma<T, kMaxPersistK / kPersistThreads> nog{};  // no norm
+    load_act<T, kMaxPersistK / kPersistThreads, false>(a.ll.h, nullptr, F, tag(base + kPhUp), nog, xs, red,
                                                        side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, io.trace,
                                                        c.tp, c.lcnt, 0);
     const bool tagged_out = !last || io.out_tagged;
@@ -1137,7 +1235,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     MRT_TP;
     x_tag = tag(base + kPhDn);
     if (!last) prefetch_qkv<T, NT>(c, a, li + 1);
-    __syncthreads();  // LDS staging regions are rewritten by the next layer
+    if (!io.resident) __syncthreads();  // LDS staging regions are rewritten by the next layer
   }
 #undef MRT_TP
   return x_tag;
@@ -1158,7 +1256,7 @@ __device__ __forceinline__ void run_head(Ctx<T>& c, const StepArgs& a, const T* 
   const Side no_side{nullptr, nullptr, 0u, -1, 0};
   float r0 = 0.f, r1 = 0.f;
   float* xs = c.next_xs();
-  load_act<T, 4, true>(a.ll.x, nullptr, a.D, x_tag, c.gam[3], xs, c.red, no_side, r0, r1, a.ll.err, trace, c.tp,
+  load_act<T, 4, true>(a.ll.x, nullptr, a.D, x_tag, c.gq, xs, c.red, no_side, r0, r1, a.ll.err, trace, c.tp,
                        c.lcnt, 0);
   gemv_rows<T, NVD, 1, false>(c.buf, hw, a.D, sH.nw(wid), rowH, xs, [&](int t, bool act, const float (&s)[1][2]) {
     if (act) {
@@ -1175,6 +1273,7 @@ __device__ __forceinline__ void prefetch_head(Ctx<T>& c, const StepArgs& a, cons
   constexpr int NVD = (1024 + V * 64 - 1) / (V * 64);
   const RowSplit sH(a.head_rows, c.G, c.blk);
   const int wid = c.wid;
+  load_gamma<T, 4>(static_cast<const T*>(a.dec_norm), a.D, c.gq);
   fetch_batch<T, NVD, 1, false>(c.buf, hw, a.D, 0, min(kNBuf / NVD, sH.nw(wid)), [&](int t, int) { return sH.row(wid, t); });
 }
 
@@ -1214,12 +1313,11 @@ __device__ __forceinline__ void gather_logits(const StepArgs& a, uint32_t tg, fl
 
 #define MRT_DECLARE_LDS(T)                                                                    \
   __shared__ float xsb[2][2 * kMaxPersistK];                                                  \
-  __shared__ float red[8];                                                                    \
+  __shared__ __align__(16) float red[8];                                                      \
   __shared__ float sm[704];                                                                   \
   __shared__ float kvst[2][2][16];                                                            \
-  __shared__ __align__(16) T gam[4][1024];                                                    \
-  __shared__ unsigned sel_hist[kPersistThreads];                                              \
-  __shared__ int sel_res[8];                                                                  \
+  __shared__ __align__(16) unsigned sel_hist[kHistWords];                                     \
+  __shared__ int sel_res[16];                                                                 \
   extern __shared__ __align__(16) unsigned char dyn_lds[];                                    \
   Ctx<T> c;                                                                                   \
   c.xsb = xsb;                                                                                \
@@ -1227,7 +1325,6 @@ __device__ __forceinline__ void gather_logits(const StepArgs& a, uint32_t tg, fl
   c.red = red;                                                                                \
   c.sm = sm;                                                                                  \
   c.kvst = kvst;                                                                              \
-  c.gam = gam;                                                                                \
   c.sel_hist = sel_hist;                                                                      \
   c.sel_res = sel_res;                                                                        \
   c.dyn = reinterpret_cast<T*>(dyn_lds);                                                      \
@@ -1264,7 +1361,6 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   __syncthreads();
   if (!ok) return;  // a previous launch failed: do nothing
   if (a.trace != nullptr && c.blk == 0 && threadIdx.x == 0) a.trace[kTraceStart] = wall_clock64();
-  if (!CROSS && c.wid == 3) stage_slots<T>(static_cast<const T*>(a.dec_norm), a.D / 64, (long)a.D * sizeof(T), gam[3]);
   StackIO io{a.in, a.D, 0u, CROSS ? a.out : nullptr, !CROSS, 0, false, 64, a.pos, a.trace};
   const uint32_t x_tag = run_stack<T, CROSS>(c, a, io);
   if constexpr (!CROSS) {
@@ -1299,7 +1395,6 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   __syncthreads();
   if (!ok) return;
   if (at.trace != nullptr && c.blk == 0 && threadIdx.x == 0) at.trace[kTraceStart] = wall_clock64();
-  if (c.wid == 3) stage_slots<T>(static_cast<const T*>(ad.dec_norm), ad.D / 64, (long)ad.D * sizeof(T), gam[3]);
   // ---- temporal step
   StackIO tio{at.in, at.D, 0u, fa.rec_temporal, true, 0, false, 64, at.pos, at.trace};
   uint32_t x_tag = run_stack<T, true>(c, at, tio);
@@ -1307,7 +1402,8 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   // ---- depth steps
   const int L = fa.levels, C = fa.codebook, D = ad.D;
   const int code0 = 16 * (at.nlayers + 1), per_step = 16 * (ad.nlayers + 1);
-  float fs[4] = {0.f, 0.f, 0.f, 0.f};  // frame sum (workgroup 0)
+  float fs[kDrawPer] = {};  // frame sum (workgroup 0)
+  if (c.blk == 0) draw_clear(c.sel_hist);  // ordered before the first draw by the gather's barriers
   int tok = 0;
   prefetch_qkv<T, false>(c, ad, 0);
   for (int l = 0; l < L; ++l) {
@@ -1332,15 +1428,22 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     if (l + 1 < L) prefetch_qkv<T, false>(c, ad, 0);
     if (c.blk == 0) {
       if (l + 1 == L && threadIdx.x == 0) astore(ad.ll.seq, c.ep + 1u);  // every workgroup has started
+      const int slot = ad.frame * L + l;
+      DrawPrefetch pf;
+      draw_prefetch(C, ad.noise + (size_t)l * C, ad.teacher, slot, pf);
+      // the previous level's token joins the frame sum while the logits arrive
+      if (l > 0) frame_sum_add<T>(fs, static_cast<const T*>(ad.emb), tok, D, l == 1);
       __syncthreads();
       float* lg = c.xsb[c.xsel ^ 1];
       gather_logits<T>(ad, tg_logit, lg, nullptr, fa.rec_slices ? fa.rec_slices + (size_t)l * 2 * C : nullptr);
       if (trace != nullptr && threadIdx.x == 0) trace[kTraceEnd] = wall_clock64();
-      tok = sample_block<T>(ad.sp, ad.frame, l, ad.frame * L + l, ad.noise + (size_t)l * C, ad.teacher, ad.tokens,
-                            ad.drawn, static_cast<const T*>(ad.emb), D, fs, static_cast<T*>(ad.fmean), lg, c.sel_hist,
-                            c.sel_res);
-      if (l + 1 < L && threadIdx.x == 0) astore(ad.ll.tok, ll_word((uint32_t)tok, tg_tok));
+      tok = sample_block<T>(ad.sp, l, slot, pf, ad.teacher != nullptr, ad.tokens, ad.drawn,
+                            l + 1 < L ? ad.ll.tok : nullptr, tg_tok, lg, c.sel_hist, c.sel_res, trace);
       if (trace != nullptr && threadIdx.x == 0) trace[kTraceDone] = wall_clock64();
+      if (l + 1 == L) {
+        frame_sum_add<T>(fs, static_cast<const T*>(ad.emb), tok, D, L == 1);
+        frame_mean_store<T>(fs, L, static_cast<T*>(ad.fmean), D);
+      }
     } else if (l + 1 < L) {
       // every workgroup waits for the draw (one word, polled by one lane)
       __shared__ int tok_s;

@@ -132,6 +132,14 @@ def test_full_size_teacher_forced(env, dtype, tol, path):
         assert agree >= floor - 2 / 32, (agree, floor)
         assert rel(g["slices"], o32["slices"]) <= tol
     np.testing.assert_array_equal(g["frame_mean"], o["frame_mean"])
+    # The device draw given its own logits: the oracle's sampler (CFG, top-k 40,
+    # T 1.1, Philox Gumbel noise) on the recorded slices; one near-tie flip of
+    # the 32 draws is tolerated (noise evaluated by different log routines).
+    O = env["O"]
+    exp = np.array([[2 + 1024 * l + O.sample_level(O.cfg_combine(g["slices"][f, l], 5.0), temperature=1.1, top_k=40,
+                                                   seed=5, frame=f, level=l)
+                     for l in range(16)] for f in range(FRAMES)])
+    assert (g["drawn"] == exp).mean() >= 31 / 32, (g["drawn"], exp)
     # every draw falls in its level's 1024-id range
     lo = 2 + 1024 * np.arange(16)[None, :]
     assert ((g["drawn"] >= lo) & (g["drawn"] < lo + 1024)).all()
@@ -175,3 +183,37 @@ def test_full_size_step_entry_points(env, dtype, tol):
                 assert rel(got, o["slices"][f, l]) <= tol, (f, l)
     st.close()
     m.close()
+
+
+@pytest.fixture(scope="module")
+def fp32_model(env):
+    m = env["mrt_df"].Depthformer(env["w"], env["cfg"], dtype="fp32")
+    yield m
+    m.close()
+
+
+@pytest.mark.parametrize("temperature,top_k", [(1.1, 40), (40.0, 40), (1.1, 1), (0.0, 40), (1.1, 0), (1.1, 1024)])
+def test_full_size_device_draws(env, fp32_model, temperature, top_k):
+    """Free-running decode, frame kernel: every draw equals the oracle's sampler
+    (CFG w 5, temperature, top-k with ties kept, Philox Gumbel-max) applied to
+    the logits the device recorded for it, and the drawn ids are the fed ids.
+    T 40 and top-k 1 make the Gumbel winner fall outside the top-k set, so the
+    radix-select path runs; T 1.1 / top-k 40 mostly takes the unmasked-winner
+    path; T 0 is argmax; top-k 0 and 1024 (= codebook) disable the mask."""
+    import torch
+    mrt_df, O = env["mrt_df"], env["O"]
+    F, L, C = FRAMES, 16, 1024
+    st = fp32_model.new_state(max_frames=F)
+    rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"),
+               drawn=torch.zeros((F, L), dtype=torch.int32, device="cuda"))
+    opts = mrt_df.GenOptions(num_frames=F, rvq_depth=L, temperature=temperature, top_k=top_k, guidance_weight=5.0,
+                             seed=11, codebook_size=C, codec_offset=2)
+    toks = st.generate_tokens(env["tok"], opts, record=rec)
+    sl = rec["slices"].cpu().numpy()
+    drawn = rec["drawn"].cpu().numpy()
+    st.close()
+    np.testing.assert_array_equal(toks, drawn)
+    exp = np.array([[2 + C * l + O.sample_level(O.cfg_combine(sl[f, l], 5.0), temperature=temperature, top_k=top_k,
+                                                seed=11, frame=f, level=l)
+                     for l in range(L)] for f in range(F)])
+    assert (drawn == exp).mean() >= 31 / 32, (drawn, exp)
