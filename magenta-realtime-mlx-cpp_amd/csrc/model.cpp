@@ -446,10 +446,11 @@ void State::print_trace() {
       pw += "]";
     }
     std::fprintf(stderr, "[mrt] %s: per-wave poll done (us after load start):%s\n", names[w], pw.c_str());
-    if (r[490]) {  // inside the draw: after v, 4 radix passes, argmax, end
+    if (r[490]) {  // inside the draw: v, argmax, count, [fallback], publish, then radix passes 1-4
       std::string dl;
       uint64_t pv = r[kTraceEnd];
-      for (int k = 490; k < 497 && r[k]; ++k) {
+      for (int k = 490; k < 499 && r[k]; ++k) {
+        if (k == 495) pv = r[492];  // radix passes start after the count
         char buf[32];
         std::snprintf(buf, sizeof buf, " %.2f", (r[k] - pv) * 0.01);
         dl += buf;

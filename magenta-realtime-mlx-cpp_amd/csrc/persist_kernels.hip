@@ -124,6 +124,18 @@ __device__ __forceinline__ float dpp_max(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Inclusive prefix sum over the 64 lanes (lane 0 first): Hillis-Steele
+// within each 16-lane row, then row 0 -> 1, 2 -> 3 and rows 0-1 -> 2-3.
+__device__ __forceinline__ unsigned dpp_prefix_sum(unsigned v) {
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0u, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+
 __device__ __forceinline__ int dpp_min_i(int v) {
   const int big = 0x7fffffff;
   v = min(v, __builtin_amdgcn_update_dpp(big, v, 0xB1, 0xf, 0xf, false));
@@ -531,16 +543,60 @@ __device__ __forceinline__ void ll_load_small(const uint64_t* src, int n, uint32
 // region (kind, row) = 64 slots x 64 elements, kind 0 = K, 1 = V.
 constexpr int kRegion = 64 * 64;
 
-// Copies `n` (<= 64) consecutive 64-element slots starting at `src` into an
-// LDS region with the calling wave; `lim` bytes from src are readable.
+// K slots are kept in LDS rotated by 16-byte chunk: chunk c of slot j sits at
+// chunk (c + j) mod kChunks<T>, so the lanes of a score loop (lane = slot)
+// reading their chunk i at the same step hit different banks.
 template <typename T>
+constexpr int kChunks = 64 * (int)sizeof(T) / 16;  // 16-byte chunks per slot
+template <typename T>
+__device__ __forceinline__ int krot(int slot, int chunk) {
+  return (chunk + slot) & (kChunks<T> - 1);
+}
+
+// Copies `n` (<= 64) consecutive 64-element slots starting at `src` into an
+// LDS region with the calling wave; `lim` bytes from src are readable.  ROT:
+// store the slots rotated (K).  The LDS destination of a lane is fixed by the
+// instruction (16 bytes per lane), so the rotation picks the source chunk.
+template <typename T, bool ROT>
 __device__ __forceinline__ void stage_slots(const T* src, int n, long lim, T* region) {
+  constexpr int kRow = 64 * (int)sizeof(T);
   const int lane = threadIdx.x & 63;
-  const int bytes = n * 64 * (int)sizeof(T);
+  const int bytes = n * kRow;
   for (int off = 0; off < bytes; off += 1024) {
-    const long o = min((long)(off + lane * 16), lim - 16);
+    long o = off + lane * 16;
+    if constexpr (ROT) {
+      const int j = (int)(o / kRow), pch = (int)(o % kRow) / 16;  // slot, stored chunk
+      o = (long)j * kRow + ((pch - j) & (kChunks<T> - 1)) * 16;
+    }
+    o = min(o, lim - 16);
     lds_copy16(reinterpret_cast<const char*>(src) + o, reinterpret_cast<char*>(region) + off);
   }
+}
+
+// sum_{j < n} p[j] * v[64 j] + init: four independent partial sums over
+// float4 reads of p, so eight LDS loads are in flight per step.
+template <typename T>
+__device__ __forceinline__ float pv_sum(const float* p, const T* v, int n, float init) {
+  using S = St<T>;
+  float o0 = init, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+  int j = 0;
+  for (; j + 8 <= n; j += 8) {
+    const float4 pa = *reinterpret_cast<const float4*>(p + j);
+    const float4 pb = *reinterpret_cast<const float4*>(p + j + 4);
+    float w[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) w[u] = S::ld(v[(j + u) * 64]);
+    o0 = fmaf(pa.x, w[0], o0);
+    o1 = fmaf(pa.y, w[1], o1);
+    o2 = fmaf(pa.z, w[2], o2);
+    o3 = fmaf(pa.w, w[3], o3);
+    o0 = fmaf(pb.x, w[4], o0);
+    o1 = fmaf(pb.y, w[5], o1);
+    o2 = fmaf(pb.z, w[6], o2);
+    o3 = fmaf(pb.w, w[7], o3);
+  }
+  for (; j < n; ++j) o0 = fmaf(p[j], S::ld(v[j * 64]), o0);
+  return (o0 + o1) + (o2 + o3);
 }
 
 // Self attention of head h over ring slots 0..pos (scale 1.0, bias
@@ -580,8 +636,9 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
     const float v0 = LL<T>::get(w, 0), v1 = LL<T>::get(w, 1);
     d[lane] = v0;
     d[64 + lane] = v1;
-    if (resident && wid > 0) {  // keep slot pos of K (wave 1) / V (wave 2) for later steps
-      T* slot = hist + ((wid - 1) * 2) * rs + pos * 64 + lane;
+    if (resident && wid > 0) {  // keep slot pos of K (wave 1, rotated) / V (wave 2) for later steps
+      const int e = wid == 1 ? krot<T>(pos, lane / V) * V + lane % V : lane;
+      T* slot = hist + ((wid - 1) * 2) * rs + pos * 64 + e;
       slot[0] = S::st(v0);
       slot[rs] = S::st(v1);
     }
@@ -596,7 +653,7 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
       float acc = 0.f;
 #pragma unroll
       for (int i = 0; i < 64 / V; ++i) {
-        const uint4 kv = *reinterpret_cast<const uint4*>(kr + i * V);
+        const uint4 kv = *reinterpret_cast<const uint4*>(kr + krot<T>(lane, i) * V);
         const T* ke = reinterpret_cast<const T*>(&kv);
 #pragma unroll
         for (int e = 0; e < V; ++e) acc = fmaf(qs[b * 64 + i * V + e], S::ld(ke[e]), acc);
@@ -614,9 +671,7 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
     const float l = dpp_sum(p);
     ps[b * 64 + lane] = p;
     // the same wave reads ps back: LDS operations of a wave complete in order
-    const T* vr = hist + (2 + b) * rs + lane;
-    float o = ps[b * 64 + pos] * vs[b * 64 + lane];
-    for (int j = 0; j < pos; ++j) o = fmaf(ps[b * 64 + j], S::ld(vr[j * 64]), o);
+    const float o = pv_sum<T>(ps + b * 64, hist + (2 + b) * rs + lane, pos, ps[b * 64 + pos] * vs[b * 64 + lane]);
     os[b * 64 + lane] = o / l;
   }
   __syncthreads();
@@ -651,7 +706,7 @@ __device__ __forceinline__ void cross_partial(const StepArgs& a, int h, int j, u
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 64 / V; ++i) {
-      const uint4 kv = *reinterpret_cast<const uint4*>(kr + i * V);
+      const uint4 kv = *reinterpret_cast<const uint4*>(kr + krot<T>(klo + lane, i) * V);
       const T* ke = reinterpret_cast<const T*>(&kv);
 #pragma unroll
       for (int e = 0; e < V; ++e) acc = fmaf(qs[b * 64 + i * V + e], S::ld(ke[e]), acc);
@@ -662,10 +717,7 @@ __device__ __forceinline__ void cross_partial(const StepArgs& a, int h, int j, u
   const float p = (lane < nkh) ? expf(sc - m) : 0.f;
   const float l = dpp_sum(p);
   ps[wid * 64 + lane] = p;
-  const T* vr = cst + (2 + b) * kRegion + klo * 64 + lane;
-  float o = 0.f;
-  for (int t = 0; t < nkh; ++t) o = fmaf(ps[wid * 64 + t], S::ld(vr[t * 64]), o);
-  wo[wid * 64 + lane] = o;
+  wo[wid * 64 + lane] = pv_sum<T>(ps + wid * 64, cst + (2 + b) * kRegion + klo * 64 + lane, nkh, 0.f);
   if (lane == 0) {
     wm[wid] = nkh > 0 ? m : -INFINITY;
     wl[wid] = l;
@@ -804,7 +856,8 @@ __device__ __forceinline__ int block_argmax(const float (&w)[kDrawPer], int C, i
 // histograms itself, so the selected digit needs no broadcast.  Pass p uses
 // buffer p % 3; buffer (p + 2) % 3, last read before this pass's barrier, is
 // cleared for pass p + 2.  Buffers 0 and 1 must be zero on entry.
-__device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[kDrawPer], int C, int k, unsigned* hist) {
+__device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[kDrawPer], int C, int k, unsigned* hist,
+                                                 uint64_t* trace) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   uint32_t prefix = 0, mask = 0;
   int need = k;
@@ -821,29 +874,26 @@ __device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[kDrawPer]
       unsigned* hc = hist + ((pass + 2) % 3) * 1024;
       for (int i = tid; i < 1024; i += kPersistThreads) hc[i] = 0u;
     }
-    // lane l holds bins 4l..4l+3 summed over the waves; suffix counts from the top bin down
+    // lane l holds the bins of group g = 63 - l (bins 4g..4g+3, top group in
+    // lane 0), summed over the waves; a prefix sum over lanes then counts the
+    // keys in this group and every group above it.
+    const int g = 63 - lane;
     unsigned cs[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const uint4 h4 = *reinterpret_cast<const uint4*>(hb + q * 256 + 4 * lane);
+      const uint4 h4 = *reinterpret_cast<const uint4*>(hb + q * 256 + 4 * g);
       cs[0] += h4.x;
       cs[1] += h4.y;
       cs[2] += h4.z;
       cs[3] += h4.w;
     }
     const unsigned own = cs[0] + cs[1] + cs[2] + cs[3];
-    unsigned suf = own;  // inclusive suffix sum over lanes >= lane
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const unsigned up = __shfl_down(suf, o, 64);
-      if (lane + o < 64) suf += up;
-    }
-    unsigned above = suf - own;  // keys in bins above this lane's
+    unsigned above = dpp_prefix_sum(own) - own;  // keys in the groups above
     int bin = -1, before = 0;
 #pragma unroll
     for (int i = 3; i >= 0; --i) {
       if (bin < 0 && above < (unsigned)need && above + cs[i] >= (unsigned)need) {
-        bin = 4 * lane + i;
+        bin = 4 * g + i;
         before = (int)above;
       }
       above += cs[i];
@@ -851,9 +901,10 @@ __device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[kDrawPer]
     // exactly one lane finds the bin (the counts sum to >= need)
     const uint64_t hit = __ballot(bin >= 0);
     const int src = hit ? (int)__builtin_ctzll(hit) : 0;
-    prefix |= (uint32_t)uniform(__shfl(bin, src, 64)) << shift;
+    prefix |= (uint32_t)__builtin_amdgcn_readlane(bin, src) << shift;
     mask |= 255u << shift;
-    need -= uniform(__shfl(before, src, 64));
+    need -= __builtin_amdgcn_readlane(before, src);
+    if (trace != nullptr && tid == 0) trace[kDrawTrace + 5 + pass] = wall_clock64();
   }
   return prefix;
 }
@@ -914,7 +965,7 @@ __device__ __forceinline__ int sample_block(const SampleParams& p, int level, in
         uint32_t key[kPer];
 #pragma unroll
         for (int t = 0; t < kPer; ++t) key[t] = (tid + kPersistThreads * t < C) ? float_key(v[t]) : 0u;
-        const float thr = key_float(radix_select(key, C, p.top_k, hist));
+        const float thr = key_float(radix_select(key, C, p.top_k, hist, trace));
 #pragma unroll
         for (int t = 0; t < kPer; ++t) w[t] = (v[t] >= thr && v[t] != -INFINITY) ? v[t] + pf.gn[t] : -INFINITY;
         arg = block_argmax(w, C, wres);
@@ -1100,8 +1151,12 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     T* lhist = io.resident ? hist + (size_t)li * 4 * io.cap * 64 : hist;
     if (!io.resident && jpart == 0 && io.pos > 0) {
       const int kind = wid >> 1, b = wid & 1;
-      stage_slots<T>(ring_k + kind * eRing + (size_t)(b * H + h) * a.Lmax * 64, io.pos,
-                     (long)a.Lmax * 64 * sizeof(T), hist + wid * kRegion);
+      const T* src = ring_k + kind * eRing + (size_t)(b * H + h) * a.Lmax * 64;
+      const long lim = (long)a.Lmax * 64 * sizeof(T);
+      if (kind == 0)
+        stage_slots<T, true>(src, io.pos, lim, hist + wid * kRegion);
+      else
+        stage_slots<T, false>(src, io.pos, lim, hist + wid * kRegion);
     }
     auto stage_cross = [&]() {
       const int chunk = (a.S + bph - 1) / bph, kb0 = jpart * chunk;
@@ -1110,7 +1165,11 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
         const int kind = wid >> 1, b = wid & 1;
         const T* src = static_cast<const T*>(a.st.cross) + (2 * li + kind) * eCross +
                        ((size_t)(b * H + h) * a.S + kb0) * 64;
-        stage_slots<T>(src, nk, (long)(a.S - kb0) * 64 * sizeof(T), cst + wid * kRegion);
+        const long lim = (long)(a.S - kb0) * 64 * sizeof(T);
+        if (kind == 0)
+          stage_slots<T, true>(src, nk, lim, cst + wid * kRegion);
+        else
+          stage_slots<T, false>(src, nk, lim, cst + wid * kRegion);
       }
     };
     if (CROSS && jpart != 0) stage_cross();
@@ -1314,7 +1373,7 @@ __device__ __forceinline__ void gather_logits(const StepArgs& a, uint32_t tg, fl
 #define MRT_DECLARE_LDS(T)                                                                    \
   __shared__ float xsb[2][2 * kMaxPersistK];                                                  \
   __shared__ __align__(16) float red[8];                                                      \
-  __shared__ float sm[704];                                                                   \
+  __shared__ __align__(16) float sm[704];                                                     \
   __shared__ float kvst[2][2][16];                                                            \
   __shared__ __align__(16) unsigned sel_hist[kHistWords];                                     \
   __shared__ int sel_res[16];                                                                 \
