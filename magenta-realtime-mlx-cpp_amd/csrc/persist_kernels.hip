@@ -643,7 +643,7 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
       slot[rs] = S::st(v1);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's history copies have landed
+  if (!resident) __builtin_amdgcn_s_waitcnt(0);  // this wave's history copies have landed
   __syncthreads();
   if (wid < 2) {
     const int b = wid;
