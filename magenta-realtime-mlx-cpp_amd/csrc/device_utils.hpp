@@ -4,6 +4,10 @@
 
 #include "common.hpp"
 
+// Address-space qualifiers: global memory and LDS.
+#define MRT_GLOBAL __attribute__((address_space(1)))
+#define MRT_LDS __attribute__((address_space(3)))
+
 namespace mrt {
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));

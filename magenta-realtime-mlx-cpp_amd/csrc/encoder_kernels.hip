@@ -131,95 +131,133 @@ __global__ __launch_bounds__(256) void k_gemm_valu(const T* __restrict__ A, cons
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 64, kLDK = kBK + 8;  // padded LDS row (bf16)
+constexpr int kBN = 128, kBK = 64, kStages = 3;
 
-// 4 waves in a 2x2 grid, each owning a 64x64 sub-tile = 2x2 32x32 MFMA tiles.
+// LDS rows of a tile are 64 bf16 = 8 chunks of 16 bytes; chunk c of row r is
+// stored at chunk c ^ swz(r), so the 32 rows x 2 chunks of an MFMA fragment
+// read (and 16 consecutive lanes of any ds_read_b128) fall in distinct banks.
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+// s_waitcnt immediate waiting for vmcnt <= n (expcnt and lgkmcnt left alone).
+constexpr int vm_wait_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// C = A B^T (A (M, K), B (N, K) bf16, fp32 accumulation) with the GemmOut
+// epilogue.  Tile BM x 128 x 64, 4 waves in a 2x2 grid (wave tile BM/2 x 64 =
+// (BM/64) x 2 MFMA 32x32x16 tiles).  Tiles stream global -> LDS with direct
+// 16-byte loads (global_load_lds) through a 3-stage ring: tile j + 2 is
+// requested while tile j is multiplied, and a wave waits only for its own
+// loads of tile j (vmcnt counts in order) before the barrier.  Rows past M
+// read row M - 1 (their results are not stored).
 // Operand fragments of v_mfma_f32_32x32x16_bf16: lane l holds row (l % 32)
 // and k = 8*(l / 32) .. +7 of both A (32x16) and B^T (32x16); the 16
 // accumulators of lane l hold column l % 32, rows 8*(r/4) + 4*(l/32) + r%4.
+template <int BM>
 __global__ __launch_bounds__(256) void k_gemm_mfma(const bf16* __restrict__ A, const bf16* __restrict__ B,
                                                    int M, int N, int K, GemmOut<bf16> out) {
-  __shared__ __attribute__((aligned(16))) bf16 As[2][kBM * kLDK];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2][kBN * kLDK];
+  constexpr int MI = BM / 64;                        // MFMA tiles per wave in M
+  constexpr int kStageBytes = (BM + kBN) * 128;      // A rows then B rows, 128 bytes each
+  constexpr int LA = BM / 32 + kBN / 32;             // load instructions per wave per tile
+  extern __shared__ __align__(16) unsigned char lds[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid >> 1, wn = wid & 1;
-  const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
+  const int nk = K / kBK;
 
-  uint4 ra[4], rb[4];
-  auto gload = [&](int k0) {
+  // tile kt -> stage kt % kStages; wave w loads rows [w*BM/4, +BM/4) of A and
+  // [w*32, +32) of B, 8 rows (1 KB) per instruction
+  auto issue = [&](int kt) {
+    const int ktc = min(kt, nk - 1);  // past the end: reload the last tile into a free stage
+    unsigned char* st = lds + (kt % kStages) * kStageBytes;
+    const int r8 = lane >> 3, p = lane & 7;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int id = tid + 256 * i, r = id >> 3, c = (id & 7) * 8;
-      const int gm = m0 + r;
-      ra[i] = gm < M ? *reinterpret_cast<const uint4*>(A + (size_t)gm * K + k0 + c) : make_uint4(0, 0, 0, 0);
-      rb[i] = *reinterpret_cast<const uint4*>(B + (size_t)(n0 + r) * K + k0 + c);
+    for (int q = 0; q < BM / 32; ++q) {
+      const int r = wid * (BM / 4) + q * 8 + r8;
+      const int gm = min(m0 + r, M - 1);
+      const bf16* src = A + (size_t)gm * K + ktc * kBK + ((p ^ swz(r)) << 3);
+      __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)src,
+                                       (MRT_LDS void*)(st + (wid * (BM / 4) + q * 8) * 128), 16, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < kBN / 32; ++q) {
+      const int r = wid * (kBN / 4) + q * 8 + r8;
+      const bf16* src = B + (size_t)(n0 + r) * K + ktc * kBK + ((p ^ swz(r)) << 3);
+      __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)src,
+                                       (MRT_LDS void*)(st + BM * 128 + (wid * (kBN / 4) + q * 8) * 128), 16, 0, 0);
     }
   };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int id = tid + 256 * i, r = id >> 3, c = (id & 7) * 8;
-      *reinterpret_cast<uint4*>(&As[buf][r * kLDK + c]) = ra[i];
-      *reinterpret_cast<uint4*>(&Bs[buf][r * kLDK + c]) = rb[i];
-    }
-  };
 
-  f32x16_t acc[2][2];
+  f32x16_t acc[MI][2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  const int nk = K / kBK;
-  const int lr = lane & 31, lk = (lane >> 5) * 8;
+#pragma unroll
+  for (int kt = 0; kt < kStages - 1; ++kt) issue(kt);
+  const int lr = lane & 31, lh = lane >> 5;
   for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * kBK);
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm((kStages - 2) * LA));  // this wave's loads of tile kt have landed
+    __syncthreads();  // every wave's loads of tile kt; every wave is done with tile kt - 1
+    issue(kt + kStages - 1);
+    const unsigned char* st = lds + (kt % kStages) * kStageBytes;
 #pragma unroll
-    for (int ks = 0; ks < kBK; ks += 16) {
-      bf16x8_t a[2], b[2];
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      const int c = 2 * ks + lh;
+      bf16x8_t a[MI], b[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t*>(&As[cur][(wm * 64 + i * 32 + lr) * kLDK + ks + lk]);
+      for (int i = 0; i < MI; ++i) {
+        const int r = wm * (BM / 2) + i * 32 + lr;
+        a[i] = *reinterpret_cast<const bf16x8_t*>(st + r * 128 + ((c ^ swz(r)) << 4));
+      }
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
-        b[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[cur][(wn * 64 + j * 32 + lr) * kLDK + ks + lk]);
+      for (int j = 0; j < 2; ++j) {
+        const int r = wn * 64 + j * 32 + lr;
+        b[j] = *reinterpret_cast<const bf16x8_t*>(st + BM * 128 + r * 128 + ((c ^ swz(r)) << 4));
+      }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) sstore(cur ^ 1);
-    __syncthreads();
   }
+  __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));  // no copy into LDS outlives the block
 
   const int col_l = lane & 31, row_l = 4 * (lane >> 5);
   if (out.a.kind == GemmEpi::Geglu) {
     const int n = n0 + wn * 64 + col_l;  // gate column; up is n + 32
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
+        const int m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
         if (m < M) out.put_geglu(m, n, acc[i][0][r], acc[i][1][r]);
       }
   } else {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
+          const int m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
           if (m < M) out.put(m, n0 + wn * 64 + j * 32 + col_l, acc[i][j][r]);
         }
   }
+}
+
+template <int BM>
+void launch_gemm_mfma(const bf16* A, const bf16* B, int M, int N, int K, const GemmOut<bf16>& out, hipStream_t s) {
+  constexpr size_t lds = (size_t)kStages * (BM + kBN) * 128;
+  static bool allowed = false;  // dynamic LDS above 64 KB needs an explicit allowance
+  if (!allowed) {
+    MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mfma<BM>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    allowed = true;
+  }
+  hipLaunchKernelGGL((k_gemm_mfma<BM>), dim3(N / kBN, (M + BM - 1) / BM), dim3(256), lds, s, A, B, M, N, K, out);
 }
 
 // ---- encoder self-attention (bidirectional, no mask, no bias, scale 1.0) -------------
@@ -460,8 +498,11 @@ void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const Gem
     MRT_REQUIRE(e.HD == e.H * 64 && N % e.HD == 0 && M == e.nb * e.S, "gemm: bad cross-KV shape");
   if (dt == DType::BF16 && allow_mfma && N % kBN == 0 && K % kBK == 0) {
     GemmOut<bf16> out{e, N};
-    hipLaunchKernelGGL(k_gemm_mfma, dim3(N / kBN, (M + kBM - 1) / kBM), dim3(256), 0, s,
-                       (const bf16*)A, (const bf16*)B, M, N, K, out);
+    // 128-row tiles when they give >= 1.5 tiles per CU of a 256-CU part, else 64-row tiles
+    if ((long)((M + 127) / 128) * (N / kBN) >= 384)
+      launch_gemm_mfma<128>((const bf16*)A, (const bf16*)B, M, N, K, out, s);
+    else
+      launch_gemm_mfma<64>((const bf16*)A, (const bf16*)B, M, N, K, out, s);
   } else if (dt == DType::BF16) {
     GemmOut<bf16> out{e, N};
     hipLaunchKernelGGL(k_gemm_valu<bf16>, dim3((N + 63) / 64, (M + 63) / 64), dim3(256), 0, s,

@@ -46,8 +46,6 @@
 #include "device_utils.hpp"
 #include "persist.hpp"
 
-#define MRT_GLOBAL __attribute__((address_space(1)))
-#define MRT_LDS __attribute__((address_space(3)))
 
 namespace mrt {
 namespace {
