@@ -131,7 +131,7 @@ __global__ __launch_bounds__(256) void k_gemm_valu(const T* __restrict__ A, cons
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-constexpr int kBN = 128, kBK = 64, kStages = 3;
+constexpr int kBN = 128, kBK = 64, kStages = 2;
 
 // LDS rows of a tile are 64 bf16 = 8 chunks of 16 bytes; chunk c of row r is
 // stored at chunk c ^ swz(r), so the 32 rows x 2 chunks of an MFMA fragment
@@ -144,10 +144,12 @@ constexpr int vm_wait_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 <<
 // C = A B^T (A (M, K), B (N, K) bf16, fp32 accumulation) with the GemmOut
 // epilogue.  Tile BM x 128 x 64, 4 waves in a 2x2 grid (wave tile BM/2 x 64 =
 // (BM/64) x 2 MFMA 32x32x16 tiles).  Tiles stream global -> LDS with direct
-// 16-byte loads (global_load_lds) through a 3-stage ring: tile j + 2 is
-// requested while tile j is multiplied, and a wave waits only for its own
-// loads of tile j (vmcnt counts in order) before the barrier.  Rows past M
-// read row M - 1 (their results are not stored).
+// 16-byte loads (global_load_lds) through a kStages-deep ring: tile
+// j + kStages - 1 is requested while tile j is multiplied, and a wave waits
+// only for its own loads of tile j (vmcnt counts in order) before the
+// barrier.  Two stages (64 / 48 KB of LDS) leave room for 2-3 blocks per CU,
+// which hides more latency than a deeper ring in one block (measured).  Rows
+// past M read row M - 1 (their results are not stored).
 // Operand fragments of v_mfma_f32_32x32x16_bf16: lane l holds row (l % 32)
 // and k = 8*(l / 32) .. +7 of both A (32x16) and B^T (32x16); the 16
 // accumulators of lane l hold column l % 32, rows 8*(r/4) + 4*(l/32) + r%4.
