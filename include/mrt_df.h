@@ -172,12 +172,84 @@ int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches);
 #define MRT_BUF_TEMPORAL_V 4
 #define MRT_BUF_DEPTH_K 5     /* layer: (rows, heads, rvq_depth, d_kv) ring     */
 #define MRT_BUF_DEPTH_V 6
+#define MRT_BUF_ENC_TOKENS 7  /* (rows, enc_len) int32 ids of the last encode; read-only */
 int mrt_df_state_buffer_bytes(mrt_df_state* st, int which, size_t* bytes);
 int mrt_df_state_read(mrt_df_state* st, int which, int layer, void* dst, size_t bytes);
 int mrt_df_state_write(mrt_df_state* st, int which, int layer, const void* src, size_t bytes);
 /* Declare how many ring slots hold valid K/V (kind 0: temporal, 1: depth), e.g.
  * after mrt_df_state_write for a step micro-benchmark at a given cache length. */
 int mrt_df_state_set_cache_length(mrt_df_state* st, int kind, int length);
+
+/* ---- Streaming: the token half of System::generate_chunk on the device ----
+ *
+ * System::generate_chunk (system.cpp:177-370) without the codec: the RVQ
+ * context (SystemState::context_tokens, system.h:124-130) stays in device
+ * memory.  Per chunk, on the stream's HIP stream: the encoder inputs are
+ * built from the context and the style (build_encoder_inputs_host,
+ * system.cpp:62-95), the encoder and the 50x16 decode run, the LLM ids are
+ * turned into RVQ codes (llm_to_rvq safe mode, rvq.cpp:112-132) and rolled
+ * into the context (system.cpp:315-333).  Only the chunk's ids leave the
+ * device. */
+
+/* The SystemConfig fields the token half reads (system.h:44-83). */
+typedef struct mrt_stream_config {
+  int32_t chunk_frames;            /* 50  chunk_length_frames */
+  int32_t context_frames;          /* 250 context_length_frames */
+  int32_t codebook_size;           /* 1024 codec_rvq_codebook_size */
+  int32_t encoder_codec_rvq_depth; /* 4 */
+  int32_t encoder_style_rvq_depth; /* 6 */
+  int32_t decoder_codec_rvq_depth; /* 16 (= the model's rvq_depth) */
+  int32_t mask_token;              /* 1  vocab_mask_token */
+  int32_t codec_offset;            /* 2  vocab_codec_offset */
+} mrt_stream_config;
+
+/* GenerateChunkOptions (system.h:86-121); `speculative` is not supported. */
+typedef struct mrt_chunk_opts {
+  float temperature;        /* 1.1 */
+  int32_t top_k;            /* 40 */
+  float guidance_weight;    /* 5.0 */
+  int32_t has_seed;         /* 0: the stream picks base + chunk_index from a random base */
+  uint64_t seed;
+  int32_t pipeline_encoder; /* enqueue the next chunk's encoder before returning */
+  int32_t use_graph;        /* replay the decode loop from a captured hipGraph */
+  const int32_t* teacher;   /* optional host (chunk_frames, levels) ids fed back instead of draws */
+} mrt_chunk_opts;
+
+typedef struct mrt_df_stream mrt_df_stream;
+
+/* SystemConfig defaults (system.h:44-83) / GenerateChunkOptions defaults. */
+void mrt_stream_config_default(mrt_stream_config* cfg);
+void mrt_chunk_opts_default(mrt_chunk_opts* opts);
+
+/* System::empty_state (system.cpp:165-176): every context slot empty (-1),
+ * chunk index 0.  Owns a state with rows = 2, max_frames = chunk_frames and
+ * enc_len = context_frames * encoder_codec_rvq_depth + encoder_style_rvq_depth. */
+int mrt_df_stream_create(mrt_df* h, const mrt_stream_config* cfg, mrt_df_stream** out);
+void mrt_df_stream_destroy(mrt_df_stream* s);
+
+/* System::generate_chunk (system.cpp:177-370), token half.  style: host
+ * (encoder_style_rvq_depth) style-vocab ids or NULL (masked), as
+ * style_tokens_lm.  llm_out / rvq_out: host (chunk_frames, levels) or NULL:
+ * the chunk's LLM ids (SystemState::last_frame_tokens_llm) and RVQ codes.
+ * A decoded id at the wrong level fails with MRT_ERR_INVALID and
+ * "llm_to_rvq: token levels do not match expected RVQ structure" (the
+ * reference's std::invalid_argument); the context and chunk index are then
+ * unchanged.  With pipeline_encoder the next chunk's encoder is enqueued
+ * before returning and reused by the next call if its style is the same
+ * (system.cpp:218-232, 334-370). */
+int mrt_df_stream_generate_chunk(mrt_df_stream* s, const int32_t* style, const mrt_chunk_opts* opts,
+                                 int32_t* llm_out, int32_t* rvq_out);
+
+/* SystemState::context_tokens and chunk_index in and out: host
+ * (context_frames, levels) int32, -1 = empty.  set_context drops a
+ * pipelined encoder output. */
+int mrt_df_stream_set_context(mrt_df_stream* s, const int32_t* context, int64_t chunk_index);
+int mrt_df_stream_get_context(mrt_df_stream* s, int32_t* context, int64_t* chunk_index);
+
+/* The stream's decode state, for the instrumentation and buffer calls above
+ * (mrt_df_state_decode_time, mrt_df_state_read).  Owned by the stream:
+ * valid until mrt_df_stream_destroy; mrt_df_state_destroy ignores it. */
+int mrt_df_stream_state(mrt_df_stream* s, mrt_df_state** st);
 
 #ifdef __cplusplus
 }

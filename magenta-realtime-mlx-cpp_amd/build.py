@@ -24,8 +24,10 @@ SOURCES = [
     "sample_kernels.hip",
     "encoder_kernels.hip",
     "persist_kernels.hip",
+    "stream_kernels.hip",
     "safetensors.cpp",
     "model.cpp",
+    "stream.cpp",
     "api.cpp",
 ]
 

@@ -7,14 +7,22 @@
 #include <string>
 
 #include "model.hpp"
+#include "stream.hpp"
 
 struct mrt_df {
   std::unique_ptr<mrt::Model> model;
 };
 
 struct mrt_df_state {
-  mrt_df* owner;
-  std::unique_ptr<mrt::State> state;
+  mrt_df* owner = nullptr;
+  std::unique_ptr<mrt::State> owned;
+  mrt::State* state = nullptr;  // owned.get(), or a stream's state
+};
+
+struct mrt_df_stream {
+  mrt_df* owner = nullptr;
+  std::unique_ptr<mrt::Stream> stream;
+  mrt_df_state view;  // borrowed handle on stream->st
 };
 
 namespace {
@@ -105,6 +113,24 @@ mrt::State& S(mrt_df_state* st) {
   return *st->state;
 }
 
+mrt::Stream& SS(mrt_df_stream* s) {
+  if (!s || !s->stream) throw mrt::Error(MRT_ERR_INVALID, "null stream handle");
+  return *s->stream;
+}
+
+mrt::StreamConfig to_stream_config(const mrt_stream_config* c) {
+  mrt::StreamConfig k;
+  k.chunk_frames = c->chunk_frames;
+  k.context_frames = c->context_frames;
+  k.codebook = c->codebook_size;
+  k.enc_depth = c->encoder_codec_rvq_depth;
+  k.style_depth = c->encoder_style_rvq_depth;
+  k.levels = c->decoder_codec_rvq_depth;
+  k.mask = c->mask_token;
+  k.codec_offset = c->codec_offset;
+  return k;
+}
+
 }  // namespace
 
 extern "C" {
@@ -164,12 +190,15 @@ int mrt_df_state_create(mrt_df* h, int rows, int max_frames, int enc_len, mrt_df
     *out = nullptr;
     auto st = std::make_unique<mrt_df_state>();
     st->owner = h;
-    st->state = std::make_unique<mrt::State>(*h->model, rows, max_frames, enc_len);
+    st->owned = std::make_unique<mrt::State>(*h->model, rows, max_frames, enc_len);
+    st->state = st->owned.get();
     *out = st.release();
   });
 }
 
-void mrt_df_state_destroy(mrt_df_state* st) { delete st; }
+void mrt_df_state_destroy(mrt_df_state* st) {
+  if (st && st->owned) delete st;  // a stream's borrowed handle is freed with the stream
+}
 
 int mrt_df_state_stream(mrt_df_state* st, void** hip_stream) {
   return guarded([&] {
@@ -251,6 +280,7 @@ int mrt_df_state_write(mrt_df_state* st, int which, int layer, const void* src, 
     if (!src) throw mrt::Error(MRT_ERR_INVALID, "null argument");
     size_t n = 0;
     void* dst = S(st).buffer(which, layer, &n);
+    if (which == MRT_BUF_ENC_TOKENS) throw mrt::Error(MRT_ERR_INVALID, "state_write: the encoder ids are read-only");
     if (bytes != n) throw mrt::Error(MRT_ERR_INVALID, "state_write: size mismatch (" + std::to_string(n) + " bytes)");
     MRT_HIP_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, S(st).stream));
     S(st).sync();
@@ -260,6 +290,83 @@ int mrt_df_state_write(mrt_df_state* st, int which, int layer, const void* src, 
 
 int mrt_df_state_set_cache_length(mrt_df_state* st, int kind, int length) {
   return guarded([&] { S(st).set_cache_length(kind, length); });
+}
+
+void mrt_stream_config_default(mrt_stream_config* cfg) {
+  if (!cfg) return;
+  const mrt::StreamConfig k;
+  cfg->chunk_frames = k.chunk_frames;
+  cfg->context_frames = k.context_frames;
+  cfg->codebook_size = k.codebook;
+  cfg->encoder_codec_rvq_depth = k.enc_depth;
+  cfg->encoder_style_rvq_depth = k.style_depth;
+  cfg->decoder_codec_rvq_depth = k.levels;
+  cfg->mask_token = k.mask;
+  cfg->codec_offset = k.codec_offset;
+}
+
+void mrt_chunk_opts_default(mrt_chunk_opts* opts) {
+  if (!opts) return;
+  const mrt::ChunkOpts k;
+  opts->temperature = k.temperature;
+  opts->top_k = k.top_k;
+  opts->guidance_weight = k.guidance_weight;
+  opts->has_seed = 0;
+  opts->seed = 0;
+  opts->pipeline_encoder = 0;
+  opts->use_graph = 1;
+  opts->teacher = nullptr;
+}
+
+int mrt_df_stream_create(mrt_df* h, const mrt_stream_config* cfg, mrt_df_stream** out) {
+  return guarded([&] {
+    if (!h || !h->model || !cfg || !out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *out = nullptr;
+    auto s = std::make_unique<mrt_df_stream>();
+    s->owner = h;
+    s->stream = std::make_unique<mrt::Stream>(*h->model, to_stream_config(cfg));
+    s->view.owner = h;
+    s->view.state = &s->stream->st;
+    *out = s.release();
+  });
+}
+
+void mrt_df_stream_destroy(mrt_df_stream* s) { delete s; }
+
+int mrt_df_stream_generate_chunk(mrt_df_stream* s, const int32_t* style, const mrt_chunk_opts* opts,
+                                 int32_t* llm_out, int32_t* rvq_out) {
+  return guarded([&] {
+    if (!opts) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    mrt::ChunkOpts o;
+    o.temperature = opts->temperature;
+    o.top_k = opts->top_k;
+    o.guidance_weight = opts->guidance_weight;
+    o.has_seed = opts->has_seed != 0;
+    o.seed = opts->seed;
+    o.pipeline_encoder = opts->pipeline_encoder != 0;
+    o.use_graph = opts->use_graph != 0;
+    o.teacher = opts->teacher;
+    SS(s).generate_chunk(style, o, llm_out, rvq_out);
+  });
+}
+
+int mrt_df_stream_set_context(mrt_df_stream* s, const int32_t* context, int64_t chunk_index) {
+  return guarded([&] {
+    if (!context) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    SS(s).set_context(context, chunk_index);
+  });
+}
+
+int mrt_df_stream_get_context(mrt_df_stream* s, int32_t* context, int64_t* chunk_index) {
+  return guarded([&] { SS(s).get_context(context, chunk_index); });
+}
+
+int mrt_df_stream_state(mrt_df_stream* s, mrt_df_state** st) {
+  return guarded([&] {
+    if (!st) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    SS(s);
+    *st = &s->view;
+  });
 }
 
 }  // extern "C"

@@ -687,6 +687,15 @@ void State::encode(const int32_t* tokens_host) {
   MRT_HIP_CHECK(hipStreamSynchronize(stream));  // staging buffer reuse
   std::memcpy(h_pinned, tokens_host, static_cast<size_t>(M) * 4);
   MRT_HIP_CHECK(hipMemcpyAsync(d_enc_tok, h_pinned, static_cast<size_t>(M) * 4, hipMemcpyHostToDevice, stream));
+  encode_device();
+}
+
+// The encoder on the token ids already in d_enc_tok (range-checked by whoever
+// wrote them), then the cross K/V of every temporal layer.
+void State::encode_device() {
+  const Config& c = m.cfg;
+  const int M = rows * S;
+  MRT_HIP_CHECK(hipSetDevice(m.device));
   const DType dt = m.dt;
   const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads;
   encoder_embed(dt, m.emb, m.pe, d_enc_tok, M, S, D, ex, stream);
@@ -965,6 +974,9 @@ void* State::buffer(int which, int layer, size_t* bytes) {
       chk(c.num_depth_layers);
       *bytes = static_cast<size_t>(rows) * H * c.rvq_depth * 64 * esz();
       return which == 5 ? dk(layer) : dv(layer);
+    case 7:
+      *bytes = static_cast<size_t>(rows) * S * 4;
+      return d_enc_tok;
     default:
       throw Error(1, "state buffer: unknown buffer id");
   }

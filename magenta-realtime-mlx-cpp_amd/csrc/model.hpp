@@ -125,6 +125,9 @@ class State {
   hipStream_t stream = nullptr;
 
   void encode(const int32_t* tokens_host);
+  void encode_device();  // encoder on the ids in enc_tokens_dev()
+  int* enc_tokens_dev() const { return d_enc_tok; }
+  int* tokens_dev() const { return d_tokens; }
   void project_cross(const void* enc_out_dev);
   void temporal_step(const void* in, const void* enc_out, int frame_idx, void* out);
   void depth_step(const void* in, int depth_idx, int level, int codebook, int codec_offset,

@@ -1,0 +1,91 @@
+// A stream's token context on the device: System::generate_chunk's LLM half
+// (system.cpp:177-333) without host round trips between chunks.
+#pragma once
+
+#include <cstdint>
+#include <vector>
+
+#include "common.hpp"
+#include "model.hpp"
+
+namespace mrt {
+
+// Encoder inputs (2, frames * e + s) int32 from the context (frames, levels)
+// (system.cpp:62-95); style may be null (every style slot MASK).
+void encoder_inputs(const int* ctx, int frames, int levels, int e, const int* style, int s, int C, int offset,
+                    int mask, int* out, hipStream_t st);
+
+// LLM ids (n, levels) -> RVQ codes (rvq.cpp:112-132, safe: *err = 1 on a
+// level mismatch, context untouched), rolled into the context
+// (frames, levels) in place (system.cpp:320-333).
+bool llm_to_rvq_roll_fits(int frames, int levels);
+void llm_to_rvq_roll(const int* llm, int n, int levels, int C, int offset, int* ctx, int frames, int* err,
+                     hipStream_t st);
+
+// The SystemConfig fields the token half reads (system.h:44-83).
+struct StreamConfig {
+  int chunk_frames = 50;       // chunk_length_frames
+  int context_frames = 250;    // context_length_frames
+  int codebook = 1024;         // codec_rvq_codebook_size
+  int enc_depth = 4;           // encoder_codec_rvq_depth
+  int style_depth = 6;         // encoder_style_rvq_depth
+  int levels = 16;             // decoder_codec_rvq_depth
+  int mask = 1;                // vocab_mask_token
+  int codec_offset = 2;        // vocab_codec_offset
+  int enc_len() const { return context_frames * enc_depth + style_depth; }
+};
+
+// GenerateChunkOptions (system.h:86-121) without the speculative path.
+struct ChunkOpts {
+  float temperature = 1.1f;
+  int top_k = 40;
+  float guidance_weight = 5.0f;
+  bool has_seed = false;
+  uint64_t seed = 0;
+  bool pipeline_encoder = false;
+  bool use_graph = true;
+  const int32_t* teacher = nullptr;  // host (chunk_frames, levels) ids fed in place of the draws
+};
+
+// SystemState's token context (system.h:124-160) resident in device memory,
+// with the decode state it feeds.  Each chunk: encoder inputs built on the
+// device from the context and style, encoder, decode, LLM ids -> RVQ codes
+// rolled into the context; with pipeline_encoder the next chunk's encoder is
+// enqueued before returning (system.cpp:334-370) and reused when the next
+// call's style matches.
+class Stream {
+ public:
+  Stream(Model& m, const StreamConfig& cfg);
+  ~Stream();
+  Stream(const Stream&) = delete;
+  Stream& operator=(const Stream&) = delete;
+
+  StreamConfig cfg;
+  State st;
+  int64_t chunk_index = 0;
+
+  // style: host (style_depth) ids or null (masked).  llm_out / rvq_out: host
+  // (chunk_frames, levels) or null.
+  void generate_chunk(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out);
+  void set_context(const int32_t* ctx_host, int64_t index);  // (context_frames, levels), -1 = empty
+  void get_context(int32_t* ctx_host, int64_t* index);
+  bool pre_encoded() const { return pre_valid_; }
+
+ private:
+  void upload_style(const int32_t* style);
+  void build_and_encode(const int32_t* style);
+  int* d_ctx_ = nullptr;
+  int* d_style_ = nullptr;
+  int* d_err_ = nullptr;
+  int32_t* h_stage_ = nullptr;  // pinned: style in, codes and flag out
+  size_t h_stage_n_ = 0;
+  bool style_set_ = false;            // d_style_ holds dev_style_
+  std::vector<int32_t> dev_style_;
+  bool pre_valid_ = false;            // st holds the encoder output of the context + pre_style_
+  bool pre_masked_ = true;
+  std::vector<int32_t> pre_style_;
+  std::vector<int32_t> llm_tmp_;
+  uint64_t seed_base_ = 0;
+};
+
+}  // namespace mrt

@@ -26,6 +26,7 @@ MRT_OK = 0
 DTYPE_F32, DTYPE_BF16 = 0, 1
 BUF_ENC_OUT, BUF_CROSS_K, BUF_CROSS_V = 0, 1, 2
 BUF_TEMPORAL_K, BUF_TEMPORAL_V, BUF_DEPTH_K, BUF_DEPTH_V = 3, 4, 5, 6
+BUF_ENC_TOKENS = 7
 
 CONFIG_FIELDS = ("vocab_size", "d_model", "d_kv", "d_ff", "num_heads", "num_encoder_layers",
                  "num_temporal_layers", "num_depth_layers", "max_encoder_length", "rvq_depth",
@@ -59,6 +60,25 @@ class _GenOpts(ctypes.Structure):
         ("record_temporal", ctypes.c_void_p),
         ("record_drawn", ctypes.c_void_p),
         ("record_frame_mean", ctypes.c_void_p),
+    ]
+
+
+class _StreamConfig(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_int32) for f in (
+        "chunk_frames", "context_frames", "codebook_size", "encoder_codec_rvq_depth",
+        "encoder_style_rvq_depth", "decoder_codec_rvq_depth", "mask_token", "codec_offset")]
+
+
+class _ChunkOpts(ctypes.Structure):
+    _fields_ = [
+        ("temperature", ctypes.c_float),
+        ("top_k", ctypes.c_int32),
+        ("guidance_weight", ctypes.c_float),
+        ("has_seed", ctypes.c_int32),
+        ("seed", ctypes.c_uint64),
+        ("pipeline_encoder", ctypes.c_int32),
+        ("use_graph", ctypes.c_int32),
+        ("teacher", ctypes.POINTER(ctypes.c_int32)),
     ]
 
 
@@ -166,6 +186,15 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_state_write": (i32, [vp, i32, i32, vp, sz]),
         "mrt_df_state_set_cache_length": (i32, [vp, i32, i32]),
         "mrt_df_state_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(i32)]),
+        "mrt_stream_config_default": (None, [ctypes.POINTER(_StreamConfig)]),
+        "mrt_chunk_opts_default": (None, [ctypes.POINTER(_ChunkOpts)]),
+        "mrt_df_stream_create": (i32, [vp, ctypes.POINTER(_StreamConfig), ctypes.POINTER(vp)]),
+        "mrt_df_stream_destroy": (None, [vp]),
+        "mrt_df_stream_generate_chunk": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_ChunkOpts),
+                                               ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)]),
+        "mrt_df_stream_set_context": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.c_int64]),
+        "mrt_df_stream_get_context": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64)]),
+        "mrt_df_stream_state": (i32, [vp, ctypes.POINTER(vp)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -342,12 +371,13 @@ class State:
             BUF_TEMPORAL_K: (self.rows, H, self.max_frames, 64),
             BUF_TEMPORAL_V: (self.rows, H, self.max_frames, 64),
             BUF_DEPTH_K: (self.rows, H, c.rvq_depth, 64), BUF_DEPTH_V: (self.rows, H, c.rvq_depth, 64),
+            BUF_ENC_TOKENS: (self.rows, self.enc_len),
         }[which]
 
     def read(self, which: int, layer: int = 0):
         torch = _torch()
-        t = torch.empty(self.buffer_shape(which), dtype=self.model.torch_dtype,
-                        device=f"cuda:{self.model.device}")
+        dt = torch.int32 if which == BUF_ENC_TOKENS else self.model.torch_dtype
+        t = torch.empty(self.buffer_shape(which), dtype=dt, device=f"cuda:{self.model.device}")
         self._sync_torch()
         _check(self.lib, self.lib.mrt_df_state_read(self._h, which, layer, _dptr(t),
                                                     t.numel() * t.element_size()))
@@ -378,7 +408,8 @@ class State:
 
     def close(self) -> None:
         if getattr(self, "_h", None):
-            self.lib.mrt_df_state_destroy(self._h)
+            if not getattr(self, "_borrowed", False):
+                self.lib.mrt_df_state_destroy(self._h)
             self._h = None
 
     def __del__(self):
@@ -386,6 +417,16 @@ class State:
             self.close()
         except Exception:  # noqa: BLE001
             pass
+
+    @classmethod
+    def _view(cls, model: Depthformer, handle: ctypes.c_void_p, rows: int, max_frames: int,
+              enc_len: int) -> "State":
+        """A handle owned elsewhere (a stream's state); close() leaves it alone."""
+        st = cls.__new__(cls)
+        st.model, st.lib = model, model.lib
+        st.rows, st.max_frames, st.enc_len = rows, max_frames, enc_len
+        st._h, st._borrowed = handle, True
+        return st
 
     # -- helpers --------------------------------------------------------------
     @staticmethod
@@ -401,3 +442,111 @@ class State:
         torch = _torch()
         if torch.cuda.is_available():
             torch.cuda.synchronize()
+
+
+@dataclasses.dataclass(frozen=True)
+class StreamConfig:
+    """The SystemConfig fields of the token half (system.h:44-83)."""
+
+    chunk_frames: int = 50
+    context_frames: int = 250
+    codebook_size: int = 1024
+    encoder_codec_rvq_depth: int = 4
+    encoder_style_rvq_depth: int = 6
+    decoder_codec_rvq_depth: int = 16
+    mask_token: int = 1
+    codec_offset: int = 2
+
+    @property
+    def encoder_length(self) -> int:
+        return self.context_frames * self.encoder_codec_rvq_depth + self.encoder_style_rvq_depth
+
+    def to_c(self) -> _StreamConfig:
+        return _StreamConfig(*[getattr(self, f) for f, _ in _StreamConfig._fields_])
+
+
+@dataclasses.dataclass
+class ChunkOptions:
+    """GenerateChunkOptions (system.h:86-121) without the speculative path."""
+
+    temperature: float = 1.1
+    top_k: int = 40
+    guidance_weight: float = 5.0
+    seed: Optional[int] = None
+    pipeline_encoder: bool = False
+    use_graph: bool = True
+
+
+class Stream:
+    """System::generate_chunk's token half with the RVQ context on the device
+    (system.cpp:177-370): encoder inputs, encoder, decode, llm_to_rvq and the
+    context roll all run on the stream's HIP stream."""
+
+    def __init__(self, model: Depthformer, cfg: StreamConfig = StreamConfig()):
+        self.model, self.lib, self.cfg = model, model.lib, cfg
+        h = ctypes.c_void_p()
+        c = cfg.to_c()
+        _check(self.lib, self.lib.mrt_df_stream_create(model._h, ctypes.byref(c), ctypes.byref(h)))
+        self._h = h
+        sh = ctypes.c_void_p()
+        _check(self.lib, self.lib.mrt_df_stream_state(h, ctypes.byref(sh)))
+        self.state = State._view(model, sh, 2, cfg.chunk_frames, cfg.encoder_length)
+
+    def generate_chunk(self, style: Optional[Sequence[int]], opts: ChunkOptions,
+                       teacher: Optional[np.ndarray] = None):
+        """Returns (llm ids, rvq codes), both (chunk_frames, levels) int32."""
+        cfg = self.cfg
+        shape = (cfg.chunk_frames, cfg.decoder_codec_rvq_depth)
+        o = _ChunkOpts(temperature=opts.temperature, top_k=opts.top_k, guidance_weight=opts.guidance_weight,
+                       has_seed=0 if opts.seed is None else 1,
+                       seed=0 if opts.seed is None else opts.seed & ((1 << 64) - 1),
+                       pipeline_encoder=1 if opts.pipeline_encoder else 0,
+                       use_graph=1 if opts.use_graph else 0, teacher=None)
+        keep = []
+        if teacher is not None:
+            tt = np.ascontiguousarray(teacher, dtype=np.int32)
+            if tt.shape != shape:
+                raise ValueError(f"teacher must be {shape}")
+            keep.append(tt)
+            o.teacher = _i32_ptr(tt)
+        st = None
+        if style is not None:
+            st = np.ascontiguousarray(style, dtype=np.int32)
+            if st.shape != (cfg.encoder_style_rvq_depth,):
+                raise ValueError("style_tokens_lm size != encoder_style_rvq_depth")
+        llm = np.zeros(shape, dtype=np.int32)
+        rvq = np.zeros(shape, dtype=np.int32)
+        _check(self.lib, self.lib.mrt_df_stream_generate_chunk(
+            self._h, _i32_ptr(st) if st is not None else None, ctypes.byref(o), _i32_ptr(llm), _i32_ptr(rvq)))
+        return llm, rvq
+
+    def set_context(self, context: np.ndarray, chunk_index: int = 0) -> None:
+        c = np.ascontiguousarray(context, dtype=np.int32)
+        if c.shape != (self.cfg.context_frames, self.cfg.decoder_codec_rvq_depth):
+            raise ValueError("context must be (context_frames, decoder_codec_rvq_depth)")
+        _check(self.lib, self.lib.mrt_df_stream_set_context(self._h, _i32_ptr(c), chunk_index))
+
+    def get_context(self):
+        """(context (context_frames, levels) int32, chunk index)."""
+        c = np.zeros((self.cfg.context_frames, self.cfg.decoder_codec_rvq_depth), dtype=np.int32)
+        idx = ctypes.c_int64()
+        _check(self.lib, self.lib.mrt_df_stream_get_context(self._h, _i32_ptr(c), ctypes.byref(idx)))
+        return c, int(idx.value)
+
+    @property
+    def chunk_index(self) -> int:
+        idx = ctypes.c_int64()
+        _check(self.lib, self.lib.mrt_df_stream_get_context(self._h, None, ctypes.byref(idx)))
+        return int(idx.value)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.state._h = None
+            self.lib.mrt_df_stream_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass

@@ -1,11 +1,15 @@
 """Host-side token plumbing around the decode path (the LLM half of System::generate_chunk).
 
 * ``build_encoder_inputs``  -- system.cpp:62-95
-* ``llm_to_rvq``            -- rvq.cpp:169-191 (safe mode raises on a level mismatch)
+* ``llm_to_rvq``            -- rvq.cpp:112-132 (safe mode raises on a level mismatch)
 * ``roll_context``          -- system.cpp:320-333
 * ``StreamingSession``      -- system.cpp:177-333 without the codec: per-chunk
   seed = base seed + chunk index (cli/main.cpp:459,599), encoder re-run on the
-  sliding 10 s context, tokens decoded on the device.
+  sliding 10 s context, tokens decoded on the device, context kept on the host.
+* ``DeviceStreamingSession`` -- the same with the context on the device
+  (``mrt_df.Stream``): encoder inputs, llm_to_rvq and the roll run as HIP
+  kernels, and ``pipeline_encoder`` enqueues the next chunk's encoder early
+  (system.cpp:334-370).
 """
 
 from __future__ import annotations
@@ -93,6 +97,7 @@ class StreamingSession:
         self.state = model.new_state(rows=2, max_frames=cfg.chunk_frames, enc_len=cfg.encoder_length)
         self.context = np.full((cfg.context_frames, cfg.decoder_codec_rvq_depth), -1, dtype=np.int32)
         self.chunk_index = 0
+        self.last_llm: Optional[np.ndarray] = None
         self.base_seed = seed
         self.opts = mrt_df.GenOptions(num_frames=cfg.chunk_frames, rvq_depth=cfg.decoder_codec_rvq_depth,
                                       temperature=temperature, top_k=top_k,
@@ -104,7 +109,44 @@ class StreamingSession:
         enc = build_encoder_inputs(self.context, self.cfg, self.style)
         self.opts.seed = self.base_seed + self.chunk_index
         llm = self.state.generate_tokens(enc, self.opts)
+        self.last_llm = llm
         rvq = llm_to_rvq(llm, self.cfg.codebook_size, self.cfg.codec_offset)
         self.context = roll_context(self.context, rvq)
         self.chunk_index += 1
+        return rvq
+
+
+class DeviceStreamingSession:
+    """StreamingSession with the RVQ context resident on the device."""
+
+    def __init__(self, model: "mrt_df.Depthformer", cfg: SystemConfig = SystemConfig(),
+                 style: Optional[Sequence[int]] = None, seed: int = 0, temperature: float = 1.1,
+                 top_k: int = 40, guidance_weight: float = 5.0, use_graph: bool = True,
+                 pipeline_encoder: bool = True):
+        self.model, self.cfg, self.style = model, cfg, style
+        self.stream = mrt_df.Stream(model, mrt_df.StreamConfig(
+            chunk_frames=cfg.chunk_frames, context_frames=cfg.context_frames,
+            codebook_size=cfg.codebook_size, encoder_codec_rvq_depth=cfg.encoder_codec_rvq_depth,
+            encoder_style_rvq_depth=cfg.encoder_style_rvq_depth,
+            decoder_codec_rvq_depth=cfg.decoder_codec_rvq_depth, mask_token=cfg.mask_token,
+            codec_offset=cfg.codec_offset))
+        self.state = self.stream.state
+        self.base_seed = seed
+        self.opts = mrt_df.ChunkOptions(temperature=temperature, top_k=top_k,
+                                        guidance_weight=guidance_weight,
+                                        pipeline_encoder=pipeline_encoder, use_graph=use_graph)
+        self.last_llm: Optional[np.ndarray] = None
+
+    @property
+    def chunk_index(self) -> int:
+        return self.stream.chunk_index
+
+    @property
+    def context(self) -> np.ndarray:
+        return self.stream.get_context()[0]
+
+    def generate_chunk(self) -> np.ndarray:
+        """Returns the chunk's (50, 16) RVQ ids and advances the device context."""
+        self.opts.seed = self.base_seed + self.chunk_index
+        self.last_llm, rvq = self.stream.generate_chunk(self.style, self.opts)
         return rvq

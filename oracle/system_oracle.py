@@ -6,7 +6,7 @@ Restates:
   * vocabulary layout constants        -- system.h:44-83
   * build_encoder_inputs_host          -- system.cpp:62-95
   * build_vocab_masks (level ranges)   -- system.cpp:135-157
-  * rvq_to_llm / llm_to_rvq            -- rvq.cpp:162-191 (upstream utils.py:106-147)
+  * rvq_to_llm / llm_to_rvq            -- rvq.cpp:105-132 (upstream utils.py:106-147)
   * context roll after a chunk         -- system.cpp:320-333
 Pinned by the upstream known answers (system_test.py:29-41, decode_test.py:26-71,
 utils_test.py:99-149) restated in tests/test_oracle_system.py.
@@ -101,7 +101,7 @@ def build_vocab_masks(cfg: SystemConfig) -> np.ndarray:
 
 
 def rvq_to_llm(tokens: np.ndarray, codebook_size: int, offset: int = 0) -> np.ndarray:
-    """rvq.cpp:162-167 (range checks of upstream utils.py:110-113)."""
+    """rvq.cpp:105-110 (range checks of upstream utils.py:110-113)."""
     t = np.asarray(tokens)
     if t.ndim == 0:
         raise ValueError(f"Invalid array shape: {t.shape}")
@@ -114,7 +114,8 @@ def rvq_to_llm(tokens: np.ndarray, codebook_size: int, offset: int = 0) -> np.nd
 
 def llm_to_rvq(tokens: np.ndarray, codebook_size: int, offset: int = 0,
                safe: bool = True) -> np.ndarray:
-    """rvq.cpp:169-191 / upstream utils.py:123-147 (safe -> IndexError)."""
+    """rvq.cpp:112-132 / upstream utils.py:123-147 (safe -> IndexError; the C++ raises
+    std::invalid_argument on exactly the same ids: floor((t - offset) / C) != level)."""
     t = np.asarray(tokens)
     if t.ndim == 0:
         raise ValueError(f"Invalid array shape: {t.shape}")
