@@ -178,6 +178,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--session", default="device", choices=["device", "host"],
+                    help="device: RVQ context on the device, next chunk's encoder enqueued early; "
+                         "host: context on the host, encoder ids uploaded per chunk")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; multi-GPU runs are not part of it "
@@ -201,8 +204,13 @@ def main():
     scfg = system.SystemConfig()
     rng = np.random.default_rng(42)
     style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
-    sess = system.StreamingSession(model, scfg, style=style, seed=args.seed, temperature=1.1, top_k=40,
-                                   guidance_weight=5.0, use_graph=not args.no_graph)
+    if args.session == "device":
+        sess = system.DeviceStreamingSession(model, scfg, style=style, seed=args.seed, temperature=1.1,
+                                             top_k=40, guidance_weight=5.0, use_graph=not args.no_graph,
+                                             pipeline_encoder=True)
+    else:
+        sess = system.StreamingSession(model, scfg, style=style, seed=args.seed, temperature=1.1, top_k=40,
+                                       guidance_weight=5.0, use_graph=not args.no_graph)
     stream = torch.cuda.ExternalStream(sess.state.stream_handle())
 
     for i in range(args.warmup):
@@ -236,7 +244,7 @@ def main():
           f"gpu {gpu_mean:.2f} ms; {achieved:.0f} GB/s", file=sys.stderr, flush=True)
 
     esz = 2 if args.dtype == "bf16" else 4
-    frames = sess.opts.num_frames
+    frames = scfg.chunk_frames
     if launches == frames:  # one persistent launch per frame
         fb = float(np.mean([frame_bytes(cfg, f, esz=esz) for f in range(frames)]))
         f_us = float(np.mean(dec)) * 1e3 / frames
@@ -284,7 +292,9 @@ def main():
         "config": {"workload": "streaming chunks: encoder 12L over 1006 ctx tokens + 50 frames x "
                                "(temporal 20L + 16 x depth 4L) decode, top-k 40, T 1.1, CFG w 5",
                    "d_model": 1024, "heads": 16, "d_ff": 2816, "vocab": 29824, "rows": 2,
-                   "graph": not args.no_graph},
+                   "graph": not args.no_graph,
+                   "session": ("device-resident context, next chunk's encoder enqueued before returning"
+                               if args.session == "device" else "host context, encoder ids uploaded per chunk")},
         "chunk_ms_p50": percentile(ms, 50),
         "chunk_ms_p99": percentile(ms, 99),
         "rtf": 2000.0 / mean_ms,

@@ -339,6 +339,7 @@ State::State(Model& model, int rows_, int max_frames, int enc_len)
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_pinned), h_pinned_n * 4, hipHostMallocDefault));
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_err_), 64, hipHostMallocDefault));
   *h_err_ = 0;
+  MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_seed_), 64, hipHostMallocDefault));
   const char* path = std::getenv("MRT_DECODE_PATH");
   if (!(path && std::string(path) == "layers")) setup_persistent();
 }
@@ -641,6 +642,7 @@ State::~State() {
   for (void* p : allocs_) (void)hipFree(p);
   if (h_pinned) (void)hipHostFree(h_pinned);
   if (h_err_) (void)hipHostFree(h_err_);
+  if (h_seed_) (void)hipHostFree(h_seed_);
   if (stream) (void)hipStreamDestroy(stream);
 }
 
@@ -850,9 +852,8 @@ int State::sample(const float* slice_dev, const GenOpts& o, int frame, int level
               "sample: codec levels exceed the vocabulary");
   MRT_REQUIRE(o.temperature >= 0.0f, "sample: temperature must be >= 0");
   MRT_HIP_CHECK(hipSetDevice(m.device));
-  MRT_HIP_CHECK(hipStreamSynchronize(stream));
-  std::memcpy(h_pinned, &o.seed, 8);
-  MRT_HIP_CHECK(hipMemcpyAsync(d_seed, h_pinned, 8, hipMemcpyHostToDevice, stream));
+  *h_seed_ = o.seed;  // its previous copy ended before the last call returned
+  MRT_HIP_CHECK(hipMemcpyAsync(d_seed, h_seed_, 8, hipMemcpyHostToDevice, stream));
   SampleParams sp{o.guidance_weight, o.temperature, o.top_k, o.codebook, o.codec_offset, o.rvq_depth, d_seed};
   // Token goes to slot 0 of the token buffer; the feedback outputs land in
   // scratch rows that the next decode overwrites.
@@ -875,17 +876,17 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
   if (enc_tokens_host) encode(enc_tokens_host);
   if (!cross_ready_) throw Error(2, "generate: no encoder output (pass enc_tokens or call encode)");
   const size_t nt = static_cast<size_t>(o.num_frames) * o.rvq_depth;
-  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  // No wait on the stream here unless the staging buffer is needed: work
+  // already enqueued (an encoder) runs on while the decode is enqueued.
   if (o.teacher) {
     for (size_t i = 0; i < nt; ++i)
       MRT_REQUIRE(o.teacher[i] >= 0 && o.teacher[i] < c.vocab_size, "generate: teacher id out of range");
+    MRT_HIP_CHECK(hipStreamSynchronize(stream));  // staging reuse (an encode may be reading it)
     std::memcpy(h_pinned, o.teacher, nt * 4);
     MRT_HIP_CHECK(hipMemcpyAsync(d_teacher, h_pinned, nt * 4, hipMemcpyHostToDevice, stream));
-    MRT_HIP_CHECK(hipStreamSynchronize(stream));
   }
-  std::memcpy(h_pinned, &o.seed, 8);
-  MRT_HIP_CHECK(hipMemcpyAsync(d_seed, h_pinned, 8, hipMemcpyHostToDevice, stream));
-  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  *h_seed_ = o.seed;  // its previous copy ended before the last call returned
+  MRT_HIP_CHECK(hipMemcpyAsync(d_seed, h_seed_, 8, hipMemcpyHostToDevice, stream));
 
   if (persistent()) reserve_epochs(decode_launches(o));
   if (!ev_dec_[0]) {
@@ -906,6 +907,7 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
       if (graph_) (void)hipGraphDestroy(graph_);
       graph_exec_ = nullptr;
       graph_ = nullptr;
+      MRT_HIP_CHECK(hipStreamSynchronize(stream));  // capture starts on an idle stream
       MRT_HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
       try {
         if (persistent())

@@ -172,6 +172,7 @@ class State {
   size_t lds_t_ = 0, lds_d_ = 0, lds_f_ = 0;  // dynamic LDS of the persistent kernels
   float* noise_ = nullptr;         // Gumbel noise of every draw of a decode call
   int* h_err_ = nullptr;        // pinned
+  uint64_t* h_seed_ = nullptr;  // pinned: the draw seed of a generate / sample call
   uint64_t* d_trace_ = nullptr; // 2 x kTraceSlots when MRT_TRACE_PHASES is set
   hipEvent_t ev_dec_[2] = {nullptr, nullptr};  // around the decode section of generate
   int dec_launches_ = 0;
