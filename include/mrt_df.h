@@ -251,6 +251,40 @@ int mrt_df_stream_get_context(mrt_df_stream* s, int32_t* context, int64_t* chunk
  * valid until mrt_df_stream_destroy; mrt_df_state_destroy ignores it. */
 int mrt_df_stream_state(mrt_df_stream* s, mrt_df_state** st);
 
+/* ---- Batched independent streams ----------------------------------------------
+ *
+ * No counterpart in the reference, whose generate_tokens decodes one stream
+ * (decode.cpp:239-573); this is the same loop for `streams` independent
+ * streams (each its own encoder tokens, seed and KV caches) run together as
+ * 2 * streams activation rows, so the projections become skinny GEMMs on the
+ * matrix cores.  Per stream the semantics are those of
+ * mrt_df_generate_tokens.  bf16 models only; streams <= 32. */
+typedef struct mrt_df_batch mrt_df_batch;
+
+/* KV rings for `max_frames` temporal steps and rvq_depth depth steps per
+ * stream; encoder length enc_len (<= max_encoder_length). */
+int mrt_df_batch_create(mrt_df* h, int streams, int max_frames, int enc_len, mrt_df_batch** out);
+void mrt_df_batch_destroy(mrt_df_batch* b);
+/* Depthformer::encode (model.cpp:226-241) of every stream: tokens
+ * (2 * streams, enc_len) host int32, rows 2s and 2s + 1 = stream s's CFG
+ * pair; then the cross K/V of every temporal layer. */
+int mrt_df_batch_encode(mrt_df_batch* b, const int32_t* tokens);
+/* One chunk of every stream: enc_tokens as mrt_df_batch_encode (NULL: reuse
+ * the last encode); seeds (streams) host, stream s draws with seeds[s];
+ * opts->teacher, when set, is host (streams, num_frames, rvq_depth);
+ * opts->record_slices (device (F, L, 2 * streams, codebook)) and
+ * opts->record_temporal (device (F, 2 * streams, d_model)) are honoured,
+ * record_drawn / record_frame_mean must be NULL.  out_tokens: host
+ * (streams, num_frames, rvq_depth) LLM ids. */
+int mrt_df_batch_generate_tokens(mrt_df_batch* b, const int32_t* enc_tokens, const mrt_gen_opts* opts,
+                                 const uint64_t* seeds, int32_t* out_tokens);
+/* GPU ms of the last generate call's decode section (HIP events on the
+ * batch's stream); instrumentation, as mrt_df_state_decode_time. */
+int mrt_df_batch_decode_time(mrt_df_batch* b, float* ms);
+/* Device copy of the encoder output (2 * streams, enc_len, d_model) (model
+ * dtype) into dst, for parity checks. */
+int mrt_df_batch_read_enc_out(mrt_df_batch* b, void* dst, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

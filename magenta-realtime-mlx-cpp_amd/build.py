@@ -25,9 +25,11 @@ SOURCES = [
     "encoder_kernels.hip",
     "persist_kernels.hip",
     "stream_kernels.hip",
+    "batch_kernels.hip",
     "safetensors.cpp",
     "model.cpp",
     "stream.cpp",
+    "batch.cpp",
     "api.cpp",
 ]
 

@@ -6,6 +6,7 @@
 #include <memory>
 #include <string>
 
+#include "batch.hpp"
 #include "model.hpp"
 #include "stream.hpp"
 
@@ -17,6 +18,10 @@ struct mrt_df_state {
   mrt_df* owner = nullptr;
   std::unique_ptr<mrt::State> owned;
   mrt::State* state = nullptr;  // owned.get(), or a stream's state
+};
+
+struct mrt_df_batch {
+  std::unique_ptr<mrt::Batch> batch;
 };
 
 struct mrt_df_stream {
@@ -111,6 +116,11 @@ mrt::GenOpts to_opts(const mrt_gen_opts* opts) {
 mrt::State& S(mrt_df_state* st) {
   if (!st || !st->state) throw mrt::Error(MRT_ERR_INVALID, "null state handle");
   return *st->state;
+}
+
+mrt::Batch& BB(mrt_df_batch* b) {
+  if (!b || !b->batch) throw mrt::Error(MRT_ERR_INVALID, "null batch handle");
+  return *b->batch;
 }
 
 mrt::Stream& SS(mrt_df_stream* s) {
@@ -366,6 +376,53 @@ int mrt_df_stream_state(mrt_df_stream* s, mrt_df_state** st) {
     if (!st) throw mrt::Error(MRT_ERR_INVALID, "null argument");
     SS(s);
     *st = &s->view;
+  });
+}
+
+int mrt_df_batch_create(mrt_df* h, int streams, int max_frames, int enc_len, mrt_df_batch** out) {
+  return guarded([&] {
+    if (!h || !h->model || !out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *out = nullptr;
+    auto b = std::make_unique<mrt_df_batch>();
+    b->batch = std::make_unique<mrt::Batch>(*h->model, streams, max_frames, enc_len);
+    *out = b.release();
+  });
+}
+
+void mrt_df_batch_destroy(mrt_df_batch* b) { delete b; }
+
+int mrt_df_batch_encode(mrt_df_batch* b, const int32_t* tokens) {
+  return guarded([&] {
+    if (!tokens) throw mrt::Error(MRT_ERR_INVALID, "null tokens");
+    BB(b).encode(tokens);
+  });
+}
+
+int mrt_df_batch_generate_tokens(mrt_df_batch* b, const int32_t* enc_tokens, const mrt_gen_opts* opts,
+                                 const uint64_t* seeds, int32_t* out_tokens) {
+  return guarded([&] {
+    if (!opts || !seeds || !out_tokens) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    if (opts->record_drawn || opts->record_frame_mean)
+      throw mrt::Error(MRT_ERR_INVALID, "batch generate: record_drawn / record_frame_mean are not supported");
+    BB(b).generate(enc_tokens, to_opts(opts), seeds, out_tokens);
+  });
+}
+
+int mrt_df_batch_decode_time(mrt_df_batch* b, float* ms) {
+  return guarded([&] {
+    if (!ms) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *ms = BB(b).last_decode_ms();
+  });
+}
+
+int mrt_df_batch_read_enc_out(mrt_df_batch* b, void* dst, size_t bytes) {
+  return guarded([&] {
+    if (!dst) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    mrt::Batch& bt = BB(b);
+    const size_t n = static_cast<size_t>(bt.R) * bt.S * bt.m.cfg.d_model * 2;
+    if (bytes != n) throw mrt::Error(MRT_ERR_INVALID, "batch_read_enc_out: size mismatch (" + std::to_string(n) + " bytes)");
+    MRT_HIP_CHECK(hipMemcpyAsync(dst, bt.enc_out(), n, hipMemcpyDeviceToDevice, bt.stream));
+    MRT_HIP_CHECK(hipStreamSynchronize(bt.stream));
   });
 }
 

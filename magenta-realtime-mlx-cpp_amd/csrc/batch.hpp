@@ -1,0 +1,84 @@
+// Batched independent streams: B streams (each its own encoder tokens, seed,
+// KV caches) decoded together as R = 2B activation rows, so every projection
+// is one skinny GEMM on the matrix cores and the weights stream once per step
+// for all streams.  Per stream the semantics are those of generate_tokens
+// (depthformer/decode.cpp:239-573) at batch 1.
+#pragma once
+
+#include <cstdint>
+#include <vector>
+
+#include "common.hpp"
+#include "model.hpp"
+
+namespace mrt {
+
+constexpr int kBatchRows = 64;  // activation rows of one batched step (32 streams)
+
+// Skinny GEMMs Y (M x N) = X (M x K) . W^T, bf16 in, fp32 accumulation, M <= 64,
+// K % 32 == 0 (batch_kernels.hip).  Epilogues as the batch-1 GEMVs.
+void bgemm_store(const void* X, int M, int K, const void* W, int N, void* Y, int ldy, hipStream_t s);
+void bgemm_f32(const void* X, int M, int K, const void* W, int N, float* Y, int ldy, hipStream_t s);
+void bgemm_resid(const void* X, int M, int K, const void* W, int N, void* R, int ldr, hipStream_t s);
+// W = [Wq; Wk; Wv] (3 HD rows): q -> Q (M, HD); k, v -> ring slot pos (or
+// *pos_ptr when non-null) of caches laid out (M, H, Lmax, 64).
+void bgemm_qkv(const void* X, int M, int K, const void* W, int HD, void* Q, void* Kc, void* Vc, int H, int Lmax, int pos,
+               const int* pos_ptr, hipStream_t s);
+// Gated GELU over the 32-row packed wi_0 / wi_1 matrix (2F rows) -> (M, F).
+void bgemm_geglu(const void* X, int M, int K, const void* W01, int F, void* Hout, int ldh, hipStream_t s);
+
+// Device frame counter of a replayed frame graph.
+void set_counter(int* p, int v, hipStream_t s);
+void advance_counter(int* p, hipStream_t s);
+
+class Batch {
+ public:
+  Batch(Model& m, int streams, int max_frames, int enc_len);
+  ~Batch();
+  Batch(const Batch&) = delete;
+  Batch& operator=(const Batch&) = delete;
+
+  Model& m;
+  int B, R, F, S;
+  hipStream_t stream = nullptr;
+
+  // tokens: host (R, S); rows 2b and 2b + 1 are stream b's CFG pair.
+  void encode(const int32_t* tokens_host);
+  void encode_device();
+  int* enc_tokens_dev() const { return enc_.tok; }
+  // One chunk of every stream.  seeds: host (B); o.teacher: host (B, F, L)
+  // or null; out: host (B, num_frames, L) LLM ids.  o.record_slices (device
+  // (F, L, R, C)) and o.record_temporal (device (F, R, D)) run the loop
+  // without the frame graph.
+  void generate(const int32_t* enc_tokens_host, const GenOpts& o, const uint64_t* seeds, int32_t* out_host);
+  // GPU ms of the last generate call's decode section.
+  float last_decode_ms() const;
+  void* enc_out() const { return enc_.enc_out; }
+
+ private:
+  void enqueue_frame(const GenOpts& o, int f, bool dynamic);
+  void temporal_stack(int f, const int* fptr);
+  void depth_stack(void* x, int l);
+  void* dalloc(size_t bytes);
+  char* ring(void* base, int layer, int kv, int len) const;
+
+  std::vector<void*> allocs_;
+  EncoderBufs enc_;
+  bool encoded_ = false;
+  void *tkv_ = nullptr, *dkv_ = nullptr;
+  void *t_in_ = nullptr, *d_in_ = nullptr, *xn_ = nullptr, *q_ = nullptr, *att_ = nullptr, *ffh_ = nullptr;
+  void* fsum_ = nullptr;
+  float *logits_ = nullptr, *part_ = nullptr;
+  int nsplit_ = 1;
+  int *d_tokens_ = nullptr, *d_teacher_ = nullptr, *d_frame_ = nullptr;
+  uint64_t* d_seeds_ = nullptr;
+  int32_t* h_pinned_ = nullptr;
+  size_t h_pinned_n_ = 0;
+  hipEvent_t ev_[2] = {nullptr, nullptr};
+  bool timed_ = false;
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t graph_exec_ = nullptr;
+  std::vector<double> graph_key_;
+};
+
+}  // namespace mrt

@@ -293,14 +293,20 @@ void gemv_geglu(DType dt, int nb, const void* W01, int F, int K, const void* X, 
 // ---- self-attention over the ring KV ----------------------------------------------
 namespace {
 
+// qpos_ptr non-null: the query position is read from it and len = qpos + 1.
 template <typename T>
 __global__ __launch_bounds__(64) void k_self_attn(const T* __restrict__ Q, const T* __restrict__ Kc,
                                                   const T* __restrict__ Vc, int H, int Lmax, int len,
-                                                  int qpos, const T* __restrict__ bias_tab,
+                                                  int qpos, const int* __restrict__ qpos_ptr,
+                                                  const T* __restrict__ bias_tab,
                                                   const int* __restrict__ buckets, T* __restrict__ out) {
   using S = St<T>;
   constexpr int V = S::kVec;
   const int bh = blockIdx.x, b = bh / H, h = bh - b * H, lane = threadIdx.x;
+  if (qpos_ptr != nullptr) {
+    qpos = *qpos_ptr;
+    len = qpos + 1;
+  }
   const int HD = H * 64;
   __shared__ float qs[64];
   __shared__ float ps[kMaxSelfLen];
@@ -438,13 +444,20 @@ void self_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, 
                hipStream_t s) {
   MRT_REQUIRE(len >= 1 && len <= kMaxSelfLen && len <= Lmax, "self_attn: bad cache length");
   MRT_REQUIRE(qpos >= len - 1, "self_attn: query precedes keys");
+  self_attn_at(dt, nb, Q, Kc, Vc, H, Lmax, len, qpos, nullptr, bias_tab, buckets, out, s);
+}
+
+void self_attn_at(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H, int Lmax, int len,
+                  int qpos, const int* qpos_ptr, const void* bias_tab, const int* buckets, void* out,
+                  hipStream_t s) {
+  MRT_REQUIRE(qpos_ptr == nullptr || Lmax <= kMaxSelfLen, "self_attn: ring longer than the kernel's score buffer");
   if (dt == DType::F32)
     hipLaunchKernelGGL(k_self_attn<float>, dim3(nb * H), dim3(64), 0, s, (const float*)Q,
-                       (const float*)Kc, (const float*)Vc, H, Lmax, len, qpos,
+                       (const float*)Kc, (const float*)Vc, H, Lmax, len, qpos, qpos_ptr,
                        (const float*)bias_tab, buckets, (float*)out);
   else
     hipLaunchKernelGGL(k_self_attn<bf16>, dim3(nb * H), dim3(64), 0, s, (const bf16*)Q,
-                       (const bf16*)Kc, (const bf16*)Vc, H, Lmax, len, qpos,
+                       (const bf16*)Kc, (const bf16*)Vc, H, Lmax, len, qpos, qpos_ptr,
                        (const bf16*)bias_tab, buckets, (bf16*)out);
   MRT_HIP_CHECK(hipGetLastError());
 }

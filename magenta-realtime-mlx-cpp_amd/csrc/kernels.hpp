@@ -48,6 +48,11 @@ void gemv_geglu(DType dt, int nb, const void* W01, int F, int K, const void* X, 
 void self_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H,
                int Lmax, int len, int qpos, const void* bias_tab, const int* buckets,
                void* out, hipStream_t s);
+// The same with the query position read on the device from *qpos_ptr when it
+// is non-null (len = qpos + 1; the caller keeps it below Lmax).
+void self_attn_at(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H, int Lmax, int len,
+                  int qpos, const int* qpos_ptr, const void* bias_tab, const int* buckets, void* out,
+                  hipStream_t s);
 // Cross-attention over S encoder keys (no bias/mask), split over key blocks.
 // ``part`` needs nb*H*nsplit*66 floats.
 void cross_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H,
@@ -83,6 +88,15 @@ struct SampleParams {
 void sample_level(DType dt, const float* logits, const SampleParams& p, int frame, int level, int slot,
                   const int* teacher, int* tokens, int* drawn, const void* emb, int D,
                   void* next_in, void* fsum, void* frame_mean, hipStream_t s);
+
+// The same for `streams` independent streams in one launch (block b: logits
+// rows 2b and 2b + 1, seed p.seed[b], token slots slot + b * tstride, the
+// feedback rows 2b and 2b + 1 of next_in / fsum / frame_mean).  frame_ptr
+// non-null: the frame index is read from it on the device and the slot
+// advances by frame * rvq_depth.
+void sample_levels(DType dt, int streams, const float* logits, const SampleParams& p, int frame,
+                   const int* frame_ptr, int level, int slot, int tstride, const int* teacher, int* tokens,
+                   int* drawn, const void* emb, int D, void* next_in, void* fsum, void* frame_mean, hipStream_t s);
 
 // ---- encoder ------------------------------------------------------------------
 // x[r, :] = round(emb[tok[r]] + pe_T[r % S])    (model.cpp:231-236)

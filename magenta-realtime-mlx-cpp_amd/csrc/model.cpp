@@ -692,34 +692,28 @@ void State::encode(const int32_t* tokens_host) {
   encode_device();
 }
 
-// The encoder on the token ids already in d_enc_tok (range-checked by whoever
-// wrote them), then the cross K/V of every temporal layer.
-void State::encode_device() {
+void run_encoder(const Model& m, const EncoderBufs& b, hipStream_t s) {
   const Config& c = m.cfg;
-  const int M = rows * S;
-  MRT_HIP_CHECK(hipSetDevice(m.device));
+  const int M = b.rows * b.S;
   const DType dt = m.dt;
   const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads;
-  encoder_embed(dt, m.emb, m.pe, d_enc_tok, M, S, D, ex, stream);
+  encoder_embed(dt, m.emb, m.pe, b.tok, M, b.S, D, b.ex, s);
   for (const auto& L : m.enc) {
-    rmsnorm_rows(dt, ex, L.norm_attn, 1e-6f, M, D, exn, stream);
-    gemm(dt, exn, L.wqkv, M, 3 * HD, D, {GemmEpi::Store, eqkv}, stream);
-    encoder_attn(dt, eqkv, rows, S, H, eattn, stream);
-    gemm(dt, eattn, L.wo, M, D, HD, {GemmEpi::Resid, ex}, stream);
-    rmsnorm_rows(dt, ex, L.norm_ff, 1e-6f, M, D, exn, stream);
-    gemm(dt, exn, L.w01, M, 2 * FF, D, {GemmEpi::Geglu, effh}, stream);
-    gemm(dt, effh, L.wo2, M, D, FF, {GemmEpi::Resid, ex}, stream);
+    rmsnorm_rows(dt, b.ex, L.norm_attn, 1e-6f, M, D, b.exn, s);
+    gemm(dt, b.exn, L.wqkv, M, 3 * HD, D, {GemmEpi::Store, b.eqkv}, s);
+    encoder_attn(dt, b.eqkv, b.rows, b.S, H, b.eattn, s);
+    gemm(dt, b.eattn, L.wo, M, D, HD, {GemmEpi::Resid, b.ex}, s);
+    rmsnorm_rows(dt, b.ex, L.norm_ff, 1e-6f, M, D, b.exn, s);
+    gemm(dt, b.exn, L.w01, M, 2 * FF, D, {GemmEpi::Geglu, b.effh}, s);
+    gemm(dt, b.effh, L.wo2, M, D, FF, {GemmEpi::Resid, b.ex}, s);
   }
-  rmsnorm_rows(dt, ex, m.enc_norm, 1e-6f, M, D, enc_out, stream);
-  project_cross(enc_out);
+  rmsnorm_rows(dt, b.ex, m.enc_norm, 1e-6f, M, D, b.enc_out, s);
+  project_cross_kv(m, b.enc_out, b.rows, b.S, b.cross, s);
 }
 
-void State::project_cross(const void* src) {
+void project_cross_kv(const Model& m, const void* enc_out, int rows, int S, void* cross, hipStream_t s) {
   const Config& c = m.cfg;
-  if (c.num_temporal_layers == 0) {
-    cross_ready_ = true;
-    return;
-  }
+  if (c.num_temporal_layers == 0) return;
   GemmEpiArgs e;
   e.kind = GemmEpi::CrossKV;
   e.C = cross;
@@ -727,7 +721,30 @@ void State::project_cross(const void* src) {
   e.H = c.num_heads;
   e.S = S;
   e.HD = c.hd();
-  gemm(m.dt, src, m.wkv_cross, rows * S, c.num_temporal_layers * 2 * c.hd(), c.d_model, e, stream);
+  gemm(m.dt, enc_out, m.wkv_cross, rows * S, c.num_temporal_layers * 2 * c.hd(), c.d_model, e, s);
+}
+
+// The encoder on the token ids already in d_enc_tok (range-checked by whoever
+// wrote them), then the cross K/V of every temporal layer.
+void State::encode_device() {
+  MRT_HIP_CHECK(hipSetDevice(m.device));
+  EncoderBufs b;
+  b.rows = rows;
+  b.S = S;
+  b.tok = d_enc_tok;
+  b.ex = ex;
+  b.exn = exn;
+  b.eqkv = eqkv;
+  b.eattn = eattn;
+  b.effh = effh;
+  b.enc_out = enc_out;
+  b.cross = cross;
+  run_encoder(m, b, stream);
+  cross_ready_ = true;
+}
+
+void State::project_cross(const void* src) {
+  project_cross_kv(m, src, rows, S, cross, stream);
   cross_ready_ = true;
 }
 

@@ -96,6 +96,19 @@ class Model {
   const void* upload_i32(const std::vector<int>& host);
 };
 
+// Encoder workspace for `rows` rows of S token ids (2 rows per stream).
+struct EncoderBufs {
+  int rows = 0, S = 0;
+  int* tok = nullptr;  // (rows, S) ids, range-checked by whoever wrote them
+  void *ex = nullptr, *exn = nullptr, *eqkv = nullptr, *eattn = nullptr, *effh = nullptr;
+  void* enc_out = nullptr;  // (rows, S, d_model)
+  void* cross = nullptr;    // (Lt, k|v, rows, H, S, 64)
+};
+// Depthformer::encode (model.cpp:226-241) over every row, then the cross K/V
+// of every temporal layer (modules.cpp:448-455).
+void run_encoder(const Model& m, const EncoderBufs& b, hipStream_t s);
+void project_cross_kv(const Model& m, const void* enc_out, int rows, int S, void* cross, hipStream_t s);
+
 struct GenOpts {
   int num_frames = 50;
   int rvq_depth = 16;

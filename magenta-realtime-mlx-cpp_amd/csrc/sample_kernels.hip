@@ -29,10 +29,12 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   }
 }
 
+// Block b draws for stream b: logits rows (2b, 2b + 1), seed p.seed[b], token
+// slots slot + b * tstride; frame < 0 reads the frame index from *frame_ptr.
 template <typename T>
 __global__ __launch_bounds__(64) void k_sample(const float* __restrict__ logits, SampleParams p,
-                                               int frame, int level, int slot,
-                                               const int* __restrict__ teacher,
+                                               int frame, const int* __restrict__ frame_ptr, int level, int slot,
+                                               int tstride, const int* __restrict__ teacher,
                                                int* __restrict__ tokens, int* __restrict__ drawn,
                                                const T* __restrict__ emb, int D, T* __restrict__ next_in,
                                                T* __restrict__ fsum, T* __restrict__ fmean) {
@@ -40,6 +42,11 @@ __global__ __launch_bounds__(64) void k_sample(const float* __restrict__ logits,
   const int lane = threadIdx.x;
   const int stream = blockIdx.x;
   const int C = p.codebook;
+  if (frame_ptr != nullptr) {
+    frame = *frame_ptr;
+    slot += frame * p.rvq_depth;
+  }
+  slot += stream * tstride;
   const float* l0 = logits + (size_t)(2 * stream) * C;
   const float* l1 = l0 + C;
   const float wc = 1.0f + p.guidance_weight;  // decode.cpp:255-256
@@ -75,7 +82,7 @@ __global__ __launch_bounds__(64) void k_sample(const float* __restrict__ logits,
       for (int t = 0; t < kMaxPerLane; ++t)
         if (v[t] < thr) v[t] = -INFINITY;  // decode.cpp:121
     }
-    const uint64_t seed = *p.seed;
+    const uint64_t seed = p.seed[stream];
 #pragma unroll
     for (int t = 0; t < kMaxPerLane; ++t) {
       const int c = lane + 64 * t;
@@ -129,14 +136,22 @@ __global__ __launch_bounds__(64) void k_sample(const float* __restrict__ logits,
 void sample_level(DType dt, const float* logits, const SampleParams& p, int frame, int level, int slot,
                   const int* teacher, int* tokens, int* drawn, const void* emb, int D,
                   void* next_in, void* fsum, void* frame_mean, hipStream_t s) {
+  sample_levels(dt, 1, logits, p, frame, nullptr, level, slot, 0, teacher, tokens, drawn, emb, D, next_in, fsum,
+                frame_mean, s);
+}
+
+void sample_levels(DType dt, int streams, const float* logits, const SampleParams& p, int frame,
+                   const int* frame_ptr, int level, int slot, int tstride, const int* teacher, int* tokens,
+                   int* drawn, const void* emb, int D, void* next_in, void* fsum, void* frame_mean, hipStream_t s) {
   MRT_REQUIRE(p.codebook >= 1 && p.codebook <= 64 * kMaxPerLane, "sample: codebook must be <= 1024");
+  MRT_REQUIRE(streams >= 1, "sample: no streams");
   if (dt == DType::F32)
-    hipLaunchKernelGGL(k_sample<float>, dim3(1), dim3(64), 0, s, logits, p, frame, level, slot, teacher,
-                       tokens, drawn, (const float*)emb, D, (float*)next_in, (float*)fsum,
+    hipLaunchKernelGGL(k_sample<float>, dim3(streams), dim3(64), 0, s, logits, p, frame, frame_ptr, level, slot,
+                       tstride, teacher, tokens, drawn, (const float*)emb, D, (float*)next_in, (float*)fsum,
                        (float*)frame_mean);
   else
-    hipLaunchKernelGGL(k_sample<bf16>, dim3(1), dim3(64), 0, s, logits, p, frame, level, slot, teacher,
-                       tokens, drawn, (const bf16*)emb, D, (bf16*)next_in, (bf16*)fsum,
+    hipLaunchKernelGGL(k_sample<bf16>, dim3(streams), dim3(64), 0, s, logits, p, frame, frame_ptr, level, slot,
+                       tstride, teacher, tokens, drawn, (const bf16*)emb, D, (bf16*)next_in, (bf16*)fsum,
                        (bf16*)frame_mean);
   MRT_HIP_CHECK(hipGetLastError());
 }

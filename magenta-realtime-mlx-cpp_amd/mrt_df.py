@@ -195,6 +195,13 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_stream_set_context": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.c_int64]),
         "mrt_df_stream_get_context": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64)]),
         "mrt_df_stream_state": (i32, [vp, ctypes.POINTER(vp)]),
+        "mrt_df_batch_create": (i32, [vp, i32, i32, i32, ctypes.POINTER(vp)]),
+        "mrt_df_batch_destroy": (None, [vp]),
+        "mrt_df_batch_encode": (i32, [vp, ctypes.POINTER(ctypes.c_int32)]),
+        "mrt_df_batch_generate_tokens": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_GenOpts),
+                                               ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_int32)]),
+        "mrt_df_batch_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
+        "mrt_df_batch_read_enc_out": (i32, [vp, vp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -543,6 +550,79 @@ class Stream:
         if getattr(self, "_h", None):
             self.state._h = None
             self.lib.mrt_df_stream_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+
+class Batch:
+    """Independent streams decoded together (2 rows per stream, <= 32 streams,
+    bf16): per stream the semantics of State.generate_tokens."""
+
+    def __init__(self, model: Depthformer, streams: int, max_frames: int = 50, enc_len: Optional[int] = None):
+        self.model, self.lib = model, model.lib
+        self.streams, self.max_frames = streams, max_frames
+        self.enc_len = enc_len or model.config.max_encoder_length
+        h = ctypes.c_void_p()
+        _check(self.lib, self.lib.mrt_df_batch_create(model._h, streams, max_frames, self.enc_len, ctypes.byref(h)))
+        self._h = h
+
+    def encode(self, tokens: np.ndarray) -> None:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        if t.shape != (2 * self.streams, self.enc_len):
+            raise ValueError(f"tokens must be {(2 * self.streams, self.enc_len)}")
+        _check(self.lib, self.lib.mrt_df_batch_encode(self._h, _i32_ptr(t)))
+
+    def generate_tokens(self, enc_tokens: Optional[np.ndarray], opts: GenOptions, seeds: Sequence[int],
+                        teacher: Optional[np.ndarray] = None, record: Optional[Dict] = None) -> np.ndarray:
+        """(streams, num_frames, rvq_depth) LLM ids; stream s draws with seeds[s]."""
+        o = State._opts(opts)
+        keep = []
+        sd = np.ascontiguousarray([int(x) & ((1 << 64) - 1) for x in seeds], dtype=np.uint64)
+        if sd.shape != (self.streams,):
+            raise ValueError("one seed per stream")
+        if teacher is not None:
+            tt = np.ascontiguousarray(teacher, dtype=np.int32)
+            if tt.shape != (self.streams, opts.num_frames, opts.rvq_depth):
+                raise ValueError("teacher must be (streams, num_frames, rvq_depth)")
+            keep.append(tt)
+            o.teacher = _i32_ptr(tt)
+        if record is not None:
+            for key, field in (("slices", "record_slices"), ("temporal", "record_temporal")):
+                if key in record:
+                    setattr(o, field, int(record[key].data_ptr()))
+            State._sync_torch()
+        enc = None
+        if enc_tokens is not None:
+            enc = np.ascontiguousarray(enc_tokens, dtype=np.int32)
+            if enc.shape != (2 * self.streams, self.enc_len):
+                raise ValueError(f"enc_tokens must be {(2 * self.streams, self.enc_len)}")
+        out = np.zeros((self.streams, opts.num_frames, opts.rvq_depth), dtype=np.int32)
+        _check(self.lib, self.lib.mrt_df_batch_generate_tokens(
+            self._h, _i32_ptr(enc) if enc is not None else None, ctypes.byref(o),
+            sd.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), _i32_ptr(out)))
+        return out
+
+    def decode_time(self) -> float:
+        ms = ctypes.c_float()
+        _check(self.lib, self.lib.mrt_df_batch_decode_time(self._h, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def read_enc_out(self):
+        torch = _torch()
+        t = torch.empty((2 * self.streams, self.enc_len, self.model.config.d_model), dtype=torch.bfloat16,
+                        device=f"cuda:{self.model.device}")
+        State._sync_torch()
+        _check(self.lib, self.lib.mrt_df_batch_read_enc_out(self._h, _dptr(t), t.numel() * 2))
+        return t
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.mrt_df_batch_destroy(self._h)
             self._h = None
 
     def __del__(self):
