@@ -31,6 +31,7 @@ for p in (ROOT, PKG):
         sys.path.insert(0, str(p))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 matrix-core peak of MI355X
 
 
 def percentile(sorted_vals, p):
@@ -115,6 +116,117 @@ def time_step_kernels(state, model, cfg, stream, esz, reps_depth=20, reps_tempor
     return res
 
 
+def encoder_flops(cfg, rows, enc_len=1006):
+    """FLOPs of one encoder pass over `rows` token rows: the 12 layers' projections,
+    bidirectional attention, and the cross K/V projection of every temporal layer."""
+    D, HD, F = cfg.d_model, cfg.num_heads * cfg.d_kv, cfg.d_ff
+    linear = 2 * (3 * HD * D + HD * D + 2 * F * D + F * D) * cfg.num_encoder_layers * rows * enc_len
+    attn = 4 * enc_len * enc_len * HD * cfg.num_encoder_layers * rows
+    cross = 2 * D * cfg.num_temporal_layers * 2 * HD * rows * enc_len
+    return linear + attn + cross
+
+
+def decode_flops(cfg, rows, frames=50, codebook=1024):
+    """Projection FLOPs of one chunk's decode (2 per weight element per row)."""
+    D, HD, F = cfg.d_model, cfg.num_heads * cfg.d_kv, cfg.d_ff
+    self_layer = 3 * HD * D + HD * D + 3 * F * D
+    temporal = cfg.num_temporal_layers * (self_layer + 2 * HD * D)
+    depth = cfg.num_depth_layers * self_layer + codebook * D
+    return 2 * rows * frames * (temporal + cfg.rvq_depth * depth)
+
+
+def synthetic_stream_tokens(n, seed):
+    """Encoder ids of n streams: a random full 10 s context and style each (rows 2s, 2s + 1)."""
+    import system
+    scfg = system.SystemConfig()
+    rng = np.random.default_rng(seed)
+    toks = []
+    for _ in range(n):
+        ctx = rng.integers(0, 1024, size=(scfg.context_frames, 16)).astype(np.int32)
+        style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+        toks.append(system.build_encoder_inputs(ctx, scfg, style))
+    return np.concatenate(toks, axis=0)
+
+
+def bench_batched(model, cfg, streams=32, chunks=3, seed=1234):
+    """Batched independent streams: `streams` streams (own encoder ids, seed and
+    caches), each chunk = encoder over 2 * streams x 1006 rows + 50 frames x 16
+    levels for every stream.  Aggregate RVQ tokens/s and per-stream RTF."""
+    import torch
+    import mrt_df
+    enc = synthetic_stream_tokens(streams, seed=7)
+    b = mrt_df.Batch(model, streams, max_frames=50)
+    st = torch.cuda.ExternalStream(b.stream_handle())
+    opts = mrt_df.GenOptions(num_frames=50, rvq_depth=16, temperature=1.1, top_k=40, guidance_weight=5.0,
+                             codebook_size=1024, codec_offset=2, use_graph=True)
+    t0 = time.perf_counter()
+    b.generate_tokens(enc, opts, seeds=[seed + s for s in range(streams)])  # frame graph capture
+    print(f"[bench] batched {streams} streams: warmup chunk {(time.perf_counter() - t0) * 1e3:.1f} ms",
+          file=sys.stderr, flush=True)
+    wall, gpu, dec = [], [], []
+    for c in range(chunks):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(st)
+        out = b.generate_tokens(enc, opts, seeds=[seed + 1000 * (c + 1) + s for s in range(streams)])
+        e1.record(st)
+        e1.synchronize()
+        wall.append((time.perf_counter() - t0) * 1e3)
+        gpu.append(e0.elapsed_time(e1))
+        dec.append(b.decode_time())
+    lo = 2 + 1024 * np.arange(16)
+    assert ((out >= lo) & (out < lo + 1024)).all()
+    b.close()
+    chunk_ms = float(np.mean(wall))
+    dec_ms = float(np.mean(dec))
+    ab = algorithmic_bytes(cfg, rows=2 * streams)
+    fl = decode_flops(cfg, 2 * streams)
+    res = {"streams": streams, "rows": 2 * streams, "chunk_ms": chunk_ms, "gpu_ms": float(np.mean(gpu)),
+           "decode_ms": dec_ms, "encode_ms": float(np.mean(gpu)) - dec_ms,
+           "rvq_tokens_per_s": 800.0 * streams / (chunk_ms * 1e-3), "per_stream_rtf": 2000.0 / chunk_ms,
+           "decode_roofline": {"bound": "hbm", "algorithmic_bytes": ab["chunk"],
+                               "achieved": ab["chunk"] / (dec_ms * 1e-3) / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s"},
+           "decode_mfma": {"flops": fl, "achieved": fl / (dec_ms * 1e-3) / 1e12, "peak": MFMA_BF16_PEAK_TFLOPS,
+                           "unit": "TFLOP/s"},
+           "chunks_timed": chunks,
+           "data": "synthetic: random 10 s contexts and styles per stream, encoder re-run per chunk"}
+    res["decode_roofline"]["frac"] = res["decode_roofline"]["achieved"] / HBM_PEAK_GBS
+    res["decode_mfma"]["frac"] = res["decode_mfma"]["achieved"] / MFMA_BF16_PEAK_TFLOPS
+    print(f"[bench] batched {streams} streams: chunk {chunk_ms:.1f} ms (decode {dec_ms:.1f} ms), "
+          f"{res['rvq_tokens_per_s']:.0f} RVQ tok/s aggregate, per-stream RTF {res['per_stream_rtf']:.1f}",
+          file=sys.stderr, flush=True)
+    return res
+
+
+def bench_encoder(model, cfg, batches=(1, 8, 32), reps=3):
+    """Encoder prefill alone over 2 x batch x 1006 token rows (CFG pairs): ms and
+    matrix-core utilisation against the dense bf16 peak."""
+    import torch
+    import mrt_df
+    res = {}
+    for nb in batches:
+        b = mrt_df.Batch(model, nb, max_frames=1)
+        st = torch.cuda.ExternalStream(b.stream_handle())
+        b.encode(synthetic_stream_tokens(nb, seed=11))
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            b.encode(synthetic_stream_tokens(nb, seed=11))
+            e1.record(st)
+            e1.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        b.close()
+        t = float(np.median(ms))
+        fl = encoder_flops(cfg, 2 * nb)
+        res[str(nb)] = {"rows": 2 * nb * 1006, "ms": t, "tflops": fl / (t * 1e-3) / 1e12,
+                        "mfma_frac": fl / (t * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS}
+        print(f"[bench] encoder batch {nb}: {t:.2f} ms, {res[str(nb)]['tflops']:.0f} TFLOP/s", file=sys.stderr,
+              flush=True)
+    return res
+
+
 def load_traffic(name):
     """HBM bytes per launch of a kernel measured with rocprofv3 FETCH_SIZE /
     WRITE_SIZE, scaled by a copy of known size (profiles/<name>.json), or None."""
@@ -178,6 +290,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-batched", action="store_true", help="skip the 32-stream and encoder-prefill figures")
     ap.add_argument("--session", default="device", choices=["device", "host"],
                     help="device: RVQ context on the device, next chunk's encoder enqueued early; "
                          "host: context on the host, encoder ids uploaded per chunk")
@@ -271,6 +384,11 @@ def main():
                 "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
                 "launches_timed": dk["launches"]}
 
+    batched = encoder = None
+    if not args.no_batched and args.dtype == "bf16":
+        batched = bench_batched(model, cfg)
+        encoder = bench_encoder(model, cfg)
+
     cpu = None
     if not args.no_cpu_baseline:
         enc = system.build_encoder_inputs(sess.context, scfg, style)
@@ -308,6 +426,8 @@ def main():
                               "traffic": load_traffic("depth_step_traffic")},
         "temporal_step_kernel": {"launch_us": kern["temporal"]["us"], "achieved_GBs": kern["temporal"]["GBs"],
                                  "algorithmic_bytes_per_launch": kern["temporal"]["bytes"]},
+        "batched_streams": batched,
+        "encoder_prefill": encoder,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

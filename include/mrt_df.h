@@ -278,6 +278,8 @@ int mrt_df_batch_encode(mrt_df_batch* b, const int32_t* tokens);
  * (streams, num_frames, rvq_depth) LLM ids. */
 int mrt_df_batch_generate_tokens(mrt_df_batch* b, const int32_t* enc_tokens, const mrt_gen_opts* opts,
                                  const uint64_t* seeds, int32_t* out_tokens);
+/* The batch's hipStream_t (all its work is ordered on it). */
+int mrt_df_batch_stream(mrt_df_batch* b, void** hip_stream);
 /* GPU ms of the last generate call's decode section (HIP events on the
  * batch's stream); instrumentation, as mrt_df_state_decode_time. */
 int mrt_df_batch_decode_time(mrt_df_batch* b, float* ms);

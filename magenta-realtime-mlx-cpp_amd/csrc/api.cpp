@@ -408,6 +408,13 @@ int mrt_df_batch_generate_tokens(mrt_df_batch* b, const int32_t* enc_tokens, con
   });
 }
 
+int mrt_df_batch_stream(mrt_df_batch* b, void** hip_stream) {
+  return guarded([&] {
+    if (!hip_stream) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *hip_stream = BB(b).stream;
+  });
+}
+
 int mrt_df_batch_decode_time(mrt_df_batch* b, float* ms) {
   return guarded([&] {
     if (!ms) throw mrt::Error(MRT_ERR_INVALID, "null argument");

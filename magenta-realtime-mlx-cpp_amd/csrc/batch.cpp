@@ -54,8 +54,7 @@ Batch::Batch(Model& model, int streams, int max_frames, int enc_len)
   ffh_ = dalloc(R * FF * e);
   fsum_ = dalloc(R * D * e);
   logits_ = static_cast<float*>(dalloc(static_cast<size_t>(R) * 1024 * 4));
-  nsplit_ = cross_attn_splits(S);
-  part_ = static_cast<float*>(dalloc(static_cast<size_t>(R) * H * nsplit_ * 66 * 4));
+  noise_ = static_cast<float*>(dalloc(static_cast<size_t>(B) * F * L * 1024 * 4));
   d_tokens_ = static_cast<int*>(dalloc(static_cast<size_t>(B) * F * L * 4));
   d_teacher_ = static_cast<int*>(dalloc(static_cast<size_t>(B) * F * L * 4));
   d_frame_ = static_cast<int*>(dalloc(4));
@@ -114,8 +113,7 @@ void Batch::temporal_stack(int f, const int* fptr) {
     bgemm_resid(att_, R, HD, W.wo, D, t_in_, D, stream);
     rmsnorm_rows(DType::BF16, t_in_, W.norm_ca, 1e-6f, R, D, xn_, stream);
     bgemm_store(xn_, R, D, W.wq_c, HD, q_, HD, stream);
-    cross_attn(DType::BF16, R, q_, ring(enc_.cross, i, 0, S), ring(enc_.cross, i, 1, S), H, S, att_, part_, nsplit_,
-               stream);
+    cross_attn_rows(q_, ring(enc_.cross, i, 0, S), ring(enc_.cross, i, 1, S), R, H, S, att_, stream);
     bgemm_resid(att_, R, HD, W.wo_c, D, t_in_, D, stream);
     rmsnorm_rows(DType::BF16, t_in_, W.norm_ff, 1e-6f, R, D, xn_, stream);
     bgemm_geglu(xn_, R, D, W.w01, FF, ffh_, FF, stream);
@@ -150,7 +148,7 @@ void Batch::enqueue_frame(const GenOpts& o, int f, bool dynamic) {
   const int D = c.d_model, L = o.rvq_depth, C = o.codebook;
   const int* fptr = dynamic ? d_frame_ : nullptr;
   const size_t row_bytes = static_cast<size_t>(R) * D * 2;
-  SampleParams sp{o.guidance_weight, o.temperature, o.top_k, C, o.codec_offset, L, d_seeds_};
+  SampleParams sp{o.guidance_weight, o.temperature, o.top_k, C, o.codec_offset, L, d_seeds_, noise_, F};
   temporal_stack(f, fptr);
   if (o.record_temporal) copy_dev(static_cast<char*>(o.record_temporal) + f * row_bytes, t_in_, row_bytes, stream);
   for (int l = 0; l < L; ++l) {
@@ -199,7 +197,10 @@ void Batch::generate(const int32_t* enc_tokens_host, const GenOpts& o, const uin
 
   const bool graph = o.use_graph && !o.record_slices && !o.record_temporal;
   MRT_HIP_CHECK(hipEventRecord(ev_[0], stream));
-  // Frame 0 feeds emb(PAD = 0) on every row (decode.cpp:339-341, 366-368).
+  // The noise of every draw, tabulated once (the sampler reads it instead of
+  // running Philox per candidate); then frame 0 feeds emb(PAD = 0) on every
+  // row (decode.cpp:339-341, 366-368).
+  if (o.temperature != 0.0f) gumbel_tables(d_seeds_, B, F, L, o.codebook, noise_, stream);
   embed_fill(DType::BF16, m.emb, c.d_model, 0, R, t_in_, stream);
   if (graph) {
     const std::vector<double> key = {(double)L, (double)o.temperature, (double)o.top_k, (double)o.guidance_weight,

@@ -27,6 +27,13 @@ void bgemm_qkv(const void* X, int M, int K, const void* W, int HD, void* Q, void
 // Gated GELU over the 32-row packed wi_0 / wi_1 matrix (2F rows) -> (M, F).
 void bgemm_geglu(const void* X, int M, int K, const void* W01, int F, void* Hout, int ldh, hipStream_t s);
 
+// Cross attention (no bias, no mask, scale 1) of every (row, head) over S <=
+// 1024 encoder keys, caches laid out (rows, H, S, 64); out (rows, H * 64).
+void cross_attn_rows(const void* Q, const void* Kc, const void* Vc, int rows, int H, int S, void* out, hipStream_t s);
+
+// Gumbel noise of every draw for every stream: out (streams, frames, L, C).
+void gumbel_tables(const uint64_t* seeds, int streams, int frames, int L, int C, float* out, hipStream_t s);
+
 // Device frame counter of a replayed frame graph.
 void set_counter(int* p, int v, hipStream_t s);
 void advance_counter(int* p, hipStream_t s);
@@ -68,8 +75,8 @@ class Batch {
   void *tkv_ = nullptr, *dkv_ = nullptr;
   void *t_in_ = nullptr, *d_in_ = nullptr, *xn_ = nullptr, *q_ = nullptr, *att_ = nullptr, *ffh_ = nullptr;
   void* fsum_ = nullptr;
-  float *logits_ = nullptr, *part_ = nullptr;
-  int nsplit_ = 1;
+  float* logits_ = nullptr;
+  float* noise_ = nullptr;  // (B, F, L, 1024) Gumbel noise of the current call
   int *d_tokens_ = nullptr, *d_teacher_ = nullptr, *d_frame_ = nullptr;
   uint64_t* d_seeds_ = nullptr;
   int32_t* h_pinned_ = nullptr;

@@ -25,6 +25,36 @@ __global__ void k_encoder_embed(const T* __restrict__ emb, const T* __restrict__
     x[(size_t)r * D + d] = St<T>::st(St<T>::ld(e[d]) + St<T>::ld(p[d]));
 }
 
+// Rows of up to 256 * kNormPer elements: each thread keeps its elements in
+// registers between the sum of squares and the scaling (one read of x).
+constexpr int kNormPer = 8;
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_reg(const T* __restrict__ x, const T* __restrict__ g,
+                                                          float eps, int D, T* __restrict__ y) {
+  using S = St<T>;
+  __shared__ float red[4];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const T* xr = x + (size_t)r * D;
+  float v[kNormPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormPer; ++i) {
+    const int d = tid + 256 * i;
+    v[i] = d < D ? S::ld(xr[d]) : 0.f;
+    ss += v[i] * v[i];
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)D + eps);
+#pragma unroll
+  for (int i = 0; i < kNormPer; ++i) {
+    const int d = tid + 256 * i;
+    if (d < D) y[(size_t)r * D + d] = S::st(S::rnd(v[i] * inv) * S::ld(g[d]));
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, const T* __restrict__ g,
                                                       float eps, int D, T* __restrict__ y) {
@@ -483,12 +513,13 @@ void encoder_embed(DType dt, const void* emb, const void* pe, const int* tok, in
 
 void rmsnorm_rows(DType dt, const void* x, const void* g, float eps, int M, int D, void* y,
                   hipStream_t s) {
+  const bool reg = D <= 256 * kNormPer;
   if (dt == DType::F32)
-    hipLaunchKernelGGL(k_rmsnorm_rows<float>, dim3(M), dim3(256), 0, s, (const float*)x,
-                       (const float*)g, eps, D, (float*)y);
+    hipLaunchKernelGGL(reg ? k_rmsnorm_rows_reg<float> : k_rmsnorm_rows<float>, dim3(M), dim3(256), 0, s,
+                       (const float*)x, (const float*)g, eps, D, (float*)y);
   else
-    hipLaunchKernelGGL(k_rmsnorm_rows<bf16>, dim3(M), dim3(256), 0, s, (const bf16*)x,
-                       (const bf16*)g, eps, D, (bf16*)y);
+    hipLaunchKernelGGL(reg ? k_rmsnorm_rows_reg<bf16> : k_rmsnorm_rows<bf16>, dim3(M), dim3(256), 0, s,
+                       (const bf16*)x, (const bf16*)g, eps, D, (bf16*)y);
   MRT_HIP_CHECK(hipGetLastError());
 }
 

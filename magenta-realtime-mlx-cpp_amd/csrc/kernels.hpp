@@ -75,7 +75,11 @@ struct SampleParams {
   int codebook;       // C: entries per level
   int codec_offset;   // first id of level 0
   int rvq_depth;      // L
-  const uint64_t* seed;  // device pointer to the draw seed
+  const uint64_t* seed;  // device pointer to the draw seed (one per stream)
+  // Optional tabulated noise: noise[((stream * noise_frames + frame) * rvq_depth
+  // + level) * codebook + i] = gumbel(seed[stream], frame, level, i).
+  const float* noise = nullptr;
+  int noise_frames = 0;
 };
 
 // One CFG stream: rows (0, 1) of ``logits`` (nb=2, C) level slice.

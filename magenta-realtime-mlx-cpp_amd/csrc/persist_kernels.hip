@@ -930,7 +930,12 @@ __device__ __forceinline__ int sample_block(const SampleParams& p, int level, in
   auto tpoint = [&](int i) {
     if (trace != nullptr && tid == 0) trace[kDrawTrace + i] = wall_clock64();
   };
-  auto guided = [&](int c) { return __fsub_rn(__fmul_rn(wc, lg[c]), __fmul_rn(wu, lg[C + c])); };
+  // (1+w)*cond - w*uncond with both products rounded (decode.cpp:83-84): no
+  // fused multiply-add.
+  auto guided = [&](int c) {
+#pragma clang fp contract(off)
+    return wc * lg[c] - wu * lg[C + c];
+  };
   float v[kPer];
 #pragma unroll
   for (int t = 0; t < kPer; ++t) {

@@ -1,11 +1,13 @@
 // On-device CFG + level-masked top-k temperature sampling and token feedback
 // for one RVQ level (decode.cpp:71-148, 458-484).
 //
-// One 64-lane wave per stream; the level's C logits (C <= 1024) live in
-// registers, 16 per lane.  The top-k threshold (the k-th largest value,
-// counting ties, i.e. min(topk(x, k)) of decode.cpp:119-120) is found by a
-// 32-step bitwise radix select over order-preserving float keys; the draw is
-// Gumbel-max over the kept entries with Philox-4x32-10 noise.
+// One workgroup per stream; its first wave draws, with the level's C logits
+// (C <= 1024) in registers, 16 per lane.  The draw is Gumbel-max over the kept entries with
+// Philox-4x32-10 noise.  When the winner over every candidate is itself in the
+// top-k set it is the answer; otherwise the top-k threshold (the k-th largest
+// value, counting ties, i.e. min(topk(x, k)) of decode.cpp:119-120) is found
+// by a 32-step bitwise radix select over order-preserving float keys, each
+// step counting with a DPP wave sum.
 #include <cmath>
 
 #include "device_utils.hpp"
@@ -15,6 +17,19 @@ namespace mrt {
 namespace {
 
 constexpr int kMaxPerLane = 16;  // C <= 1024
+constexpr int kFeedPer = 8;      // d_model elements per thread in the feedback (d_model <= 2048)
+
+// Sum over the 64 lanes with DPP (row shifts and broadcasts, no LDS
+// crossbar); every lane active; the result is wave-uniform.
+__device__ __forceinline__ int dpp_sum_i(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true);   // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true);   // quad_perm [2,3,0,1]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, true);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, true);  // row_bcast:31
+  return __builtin_amdgcn_readlane(v, 63);
+}
 
 // argmax with the first index winning ties (mx::argmax semantics).
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
@@ -29,42 +44,81 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   }
 }
 
-// Block b draws for stream b: logits rows (2b, 2b + 1), seed p.seed[b], token
-// slots slot + b * tstride; frame < 0 reads the frame index from *frame_ptr.
-template <typename T>
-__global__ __launch_bounds__(64) void k_sample(const float* __restrict__ logits, SampleParams p,
-                                               int frame, const int* __restrict__ frame_ptr, int level, int slot,
-                                               int tstride, const int* __restrict__ teacher,
-                                               int* __restrict__ tokens, int* __restrict__ drawn,
-                                               const T* __restrict__ emb, int D, T* __restrict__ next_in,
-                                               T* __restrict__ fsum, T* __restrict__ fmean) {
-  using S = St<T>;
+// The draw of one stream by one wave (lane = threadIdx.x < 64): returns the
+// winning index within the level's C entries.
+__device__ __forceinline__ int wave_draw(const float* __restrict__ logits, const SampleParams& p, int stream,
+                                         int frame, int level) {
   const int lane = threadIdx.x;
-  const int stream = blockIdx.x;
   const int C = p.codebook;
-  if (frame_ptr != nullptr) {
-    frame = *frame_ptr;
-    slot += frame * p.rvq_depth;
-  }
-  slot += stream * tstride;
   const float* l0 = logits + (size_t)(2 * stream) * C;
   const float* l1 = l0 + C;
   const float wc = 1.0f + p.guidance_weight;  // decode.cpp:255-256
   const float wu = p.guidance_weight;
 
-  float v[kMaxPerLane];
+  // Loads are unconditional (indices clamped into range) and all issued
+  // before the first use; entries past C are masked afterwards.
+  float a0[kMaxPerLane], a1[kMaxPerLane], gn[kMaxPerLane];
 #pragma unroll
   for (int t = 0; t < kMaxPerLane; ++t) {
-    const int c = lane + 64 * t;
-    // (1+w)*cond - w*uncond, each product rounded separately (decode.cpp:83-84).
-    v[t] = (c < C) ? __fsub_rn(__fmul_rn(wc, l0[c]), __fmul_rn(wu, l1[c])) : -INFINITY;
+    const int c = min(lane + 64 * t, C - 1);
+    a0[t] = l0[c];
+    a1[t] = l1[c];
+  }
+  if (p.temperature != 0.0f && p.noise != nullptr) {
+    const float* nz = p.noise + (((size_t)stream * p.noise_frames + frame) * p.rvq_depth + level) * C;
+#pragma unroll
+    for (int t = 0; t < kMaxPerLane; ++t) gn[t] = nz[min(lane + 64 * t, C - 1)];
+  }
+  float v[kMaxPerLane];
+  {
+    // (1+w)*cond - w*uncond, each product rounded separately (decode.cpp:83-84):
+    // no fused multiply-add here.
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int t = 0; t < kMaxPerLane; ++t) v[t] = lane + 64 * t < C ? wc * a0[t] - wu * a1[t] : -INFINITY;
   }
 
+  bool done = false;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
   if (p.temperature != 0.0f) {
 #pragma unroll
     for (int t = 0; t < kMaxPerLane; ++t)
       if (lane + 64 * t < C) v[t] = __fdiv_rn(v[t], p.temperature);
+    if (p.noise == nullptr) {
+      const uint64_t seed0 = p.seed[stream];
+#pragma unroll
+      for (int t = 0; t < kMaxPerLane; ++t) {
+        const int c = lane + 64 * t;
+        gn[t] = c < C ? gumbel(seed0, frame, level, c) : 0.f;
+      }
+    }
     if (p.top_k > 0 && p.top_k < C) {
+      // The Gumbel-max winner A over every candidate is the winner over the
+      // top-k set whenever A is in it, i.e. when fewer than k scaled logits
+      // exceed v_A (ties at the k-th value are kept); only otherwise is the
+      // threshold needed.
+#pragma unroll
+      for (int t = 0; t < kMaxPerLane; ++t) {
+        const int c = lane + 64 * t;
+        const float w = v[t] + gn[t];
+        if (c < C && (w > best || bi == 0x7fffffff)) {
+          best = w;
+          bi = c;
+        }
+      }
+      wave_argmax(best, bi);
+      float va = 0.f;
+#pragma unroll
+      for (int t = 0; t < kMaxPerLane; ++t)
+        if (lane + 64 * t == bi) va = v[t];
+      va = __shfl(va, bi & 63, 64);
+      int above = 0;
+#pragma unroll
+      for (int t = 0; t < kMaxPerLane; ++t) above += (lane + 64 * t < C && v[t] > va) ? 1 : 0;
+      done = dpp_sum_i(above) < p.top_k;
+    }
+    if (!done && p.top_k > 0 && p.top_k < C) {
       uint32_t key[kMaxPerLane];
 #pragma unroll
       for (int t = 0; t < kMaxPerLane; ++t) key[t] = (lane + 64 * t < C) ? float_key(v[t]) : 0u;
@@ -74,53 +128,90 @@ __global__ __launch_bounds__(64) void k_sample(const float* __restrict__ logits,
         int cnt = 0;
 #pragma unroll
         for (int t = 0; t < kMaxPerLane; ++t) cnt += key[t] >= cand ? 1 : 0;
-        cnt = wave_sum_i(cnt);
-        if (cnt >= p.top_k) prefix = cand;
+        if (dpp_sum_i(cnt) >= p.top_k) prefix = cand;
       }
       const float thr = key_float(prefix);
 #pragma unroll
       for (int t = 0; t < kMaxPerLane; ++t)
         if (v[t] < thr) v[t] = -INFINITY;  // decode.cpp:121
     }
-    const uint64_t seed = p.seed[stream];
+    if (!done) {
+#pragma unroll
+      for (int t = 0; t < kMaxPerLane; ++t) {
+        const int c = lane + 64 * t;
+        if (c < C && v[t] != -INFINITY) v[t] = v[t] + gn[t];
+      }
+    }
+  }
+  if (!done) {
+    best = -INFINITY;
+    bi = 0x7fffffff;
 #pragma unroll
     for (int t = 0; t < kMaxPerLane; ++t) {
       const int c = lane + 64 * t;
-      if (c < C && v[t] != -INFINITY) v[t] = v[t] + gumbel(seed, frame, level, c);
+      if (c < C && (v[t] > best || bi == 0x7fffffff)) {  // c ascends: first max wins
+        best = v[t];
+        bi = c;
+      }
     }
+    wave_argmax(best, bi);
   }
-  float best = -INFINITY;
-  int bi = 0x7fffffff;
-#pragma unroll
-  for (int t = 0; t < kMaxPerLane; ++t) {
-    const int c = lane + 64 * t;
-    if (c < C && (v[t] > best || bi == 0x7fffffff)) {  // c ascends: first max wins
-      best = v[t];
-      bi = c;
-    }
-  }
-  wave_argmax(best, bi);
 
-  const int L = p.rvq_depth;
-  const int drawn_id = p.codec_offset + level * C + bi;
-  const int fed = teacher ? teacher[slot] : drawn_id;
-  if (lane == 0) {
-    tokens[slot] = fed;
-    if (drawn) drawn[slot] = drawn_id;
+  return bi;
+}
+
+// Block b draws for stream b: logits rows (2b, 2b + 1), seed p.seed[b], token
+// slots slot + b * tstride; a non-null frame_ptr supplies the frame index.
+// Wave 0 draws; all four waves then write the token's embedding to both rows
+// of next_in and update the frame sum (whose rows they load while the draw
+// runs).
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_sample(
+    const float* __restrict__ logits, SampleParams p, int frame, const int* __restrict__ frame_ptr, int level,
+    int slot, int tstride, const int* __restrict__ teacher, int* __restrict__ tokens, int* __restrict__ drawn,
+    const T* __restrict__ emb, int D, T* __restrict__ next_in, T* __restrict__ fsum, T* __restrict__ fmean) {
+  using S = St<T>;
+  __shared__ int fed_s;
+  const int tid = threadIdx.x;
+  const int stream = blockIdx.x;
+  const int C = p.codebook, L = p.rvq_depth;
+  if (frame_ptr != nullptr) {
+    frame = *frame_ptr;
+    slot += frame * L;
   }
-  // Token feedback (decode.cpp:476-484): both CFG rows take emb(fed); the
-  // frame sum accumulates in the model dtype; at the last level the mean is
-  // the sum divided by L in the model dtype.
-  const T* e = emb + (size_t)fed * D;
-  const float Lf = S::rnd((float)L);
+  slot += stream * tstride;
   T* ni = next_in + (size_t)(2 * stream) * D;
   T* fs = fsum + (size_t)(2 * stream) * D;
   T* fm = fmean + (size_t)(2 * stream) * D;
-  for (int d = lane; d < D; d += 64) {
-    const T ev = e[d];
-    const float sum = (level == 0) ? S::ld(ev) : S::rnd(S::ld(fs[d]) + S::ld(ev));
-    ni[d] = ev;
-    ni[D + d] = ev;
+  T fv[kFeedPer];
+#pragma unroll
+  for (int i = 0; i < kFeedPer; ++i) fv[i] = fs[min(tid + 256 * i, D - 1)];  // unused at level 0
+  if (tid < 64) {
+    const int bi = wave_draw(logits, p, stream, frame, level);
+    if (tid == 0) {
+      const int drawn_id = p.codec_offset + level * C + bi;
+      const int fed = teacher ? teacher[slot] : drawn_id;
+      tokens[slot] = fed;
+      if (drawn) drawn[slot] = drawn_id;
+      fed_s = fed;
+    }
+  }
+  __syncthreads();
+  // Token feedback (decode.cpp:476-484): both CFG rows take emb(fed); the
+  // frame sum accumulates in the model dtype; at the last level the mean is
+  // the sum divided by L in the model dtype.
+  const T* e = emb + (size_t)fed_s * D;
+  const float Lf = S::rnd((float)L);
+  T ev[kFeedPer];
+#pragma unroll
+  for (int i = 0; i < kFeedPer; ++i) ev[i] = e[min(tid + 256 * i, D - 1)];
+#pragma unroll
+  for (int i = 0; i < kFeedPer; ++i) {
+    const int d = tid + 256 * i;
+    if (d >= D) continue;
+    const float sum = (level == 0) ? S::ld(ev[i]) : S::rnd(S::ld(fv[i]) + S::ld(ev[i]));
+    ni[d] = ev[i];
+    ni[D + d] = ev[i];
     fs[d] = S::st(sum);
     fs[D + d] = S::st(sum);
     if (level == L - 1) {
@@ -145,12 +236,13 @@ void sample_levels(DType dt, int streams, const float* logits, const SampleParam
                    int* drawn, const void* emb, int D, void* next_in, void* fsum, void* frame_mean, hipStream_t s) {
   MRT_REQUIRE(p.codebook >= 1 && p.codebook <= 64 * kMaxPerLane, "sample: codebook must be <= 1024");
   MRT_REQUIRE(streams >= 1, "sample: no streams");
+  MRT_REQUIRE(D >= 1 && D <= 256 * kFeedPer, "sample: d_model must be in [1, 2048]");
   if (dt == DType::F32)
-    hipLaunchKernelGGL(k_sample<float>, dim3(streams), dim3(64), 0, s, logits, p, frame, frame_ptr, level, slot,
+    hipLaunchKernelGGL(k_sample<float>, dim3(streams), dim3(256), 0, s, logits, p, frame, frame_ptr, level, slot,
                        tstride, teacher, tokens, drawn, (const float*)emb, D, (float*)next_in, (float*)fsum,
                        (float*)frame_mean);
   else
-    hipLaunchKernelGGL(k_sample<bf16>, dim3(streams), dim3(64), 0, s, logits, p, frame, frame_ptr, level, slot,
+    hipLaunchKernelGGL(k_sample<bf16>, dim3(streams), dim3(256), 0, s, logits, p, frame, frame_ptr, level, slot,
                        tstride, teacher, tokens, drawn, (const bf16*)emb, D, (bf16*)next_in, (bf16*)fsum,
                        (bf16*)frame_mean);
   MRT_HIP_CHECK(hipGetLastError());

@@ -200,6 +200,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_batch_encode": (i32, [vp, ctypes.POINTER(ctypes.c_int32)]),
         "mrt_df_batch_generate_tokens": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_GenOpts),
                                                ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_int32)]),
+        "mrt_df_batch_stream": (i32, [vp, ctypes.POINTER(vp)]),
         "mrt_df_batch_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
         "mrt_df_batch_read_enc_out": (i32, [vp, vp, sz]),
     }
@@ -611,6 +612,11 @@ class Batch:
         ms = ctypes.c_float()
         _check(self.lib, self.lib.mrt_df_batch_decode_time(self._h, ctypes.byref(ms)))
         return float(ms.value)
+
+    def stream_handle(self) -> int:
+        s = ctypes.c_void_p()
+        _check(self.lib, self.lib.mrt_df_batch_stream(self._h, ctypes.byref(s)))
+        return int(s.value or 0)
 
     def read_enc_out(self):
         torch = _torch()

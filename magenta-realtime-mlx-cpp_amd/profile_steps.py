@@ -4,6 +4,10 @@ the benchmark dims, plus a calibration copy of known size, for rocprofv3
 counter runs (FETCH_SIZE / WRITE_SIZE per dispatch) and kernel traces.
 
     python magenta-realtime-mlx-cpp_amd/profile_steps.py [--reps N] [--copy-mib M]
+    python magenta-realtime-mlx-cpp_amd/profile_steps.py --batched 32 [--frames F]
+
+--batched N instead runs N independent streams together: one encode of
+2N x 1006 rows and one decode of F frames through the replayed frame graph.
 
 The copy (torch's device copy of M MiB, M above the 256 MB last-level cache)
 reads and writes exactly M MiB; its counter readings give the scale factor
@@ -28,6 +32,8 @@ def main() -> None:
     ap.add_argument("--reps", type=int, default=4, help="passes over the 16 depth levels")
     ap.add_argument("--copy-mib", type=int, default=1024, help="calibration copy size (above the 256 MB MALL)")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--batched", type=int, default=0, help="streams of a batched decode (0: single stream)")
+    ap.add_argument("--frames", type=int, default=50, help="frames of the batched decode")
     a = ap.parse_args()
 
     import torch
@@ -38,6 +44,22 @@ def main() -> None:
     cfg = mrt_df.Config.bench()
     model = mrt_df.Depthformer(synth_bundle.make_weights(cfg, seed=a.seed, threads=16), cfg, dtype="bf16")
     scfg = system.SystemConfig()
+    if a.batched:
+        rng = np.random.default_rng(7)
+        toks = []
+        for _ in range(a.batched):
+            ctx = rng.integers(0, 1024, size=(scfg.context_frames, 16)).astype(np.int32)
+            style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+            toks.append(system.build_encoder_inputs(ctx, scfg, style))
+        b = mrt_df.Batch(model, a.batched, max_frames=a.frames)
+        opts = mrt_df.GenOptions(num_frames=a.frames, rvq_depth=cfg.rvq_depth, temperature=1.1, top_k=40,
+                                 guidance_weight=5.0, use_graph=True)
+        seeds = [a.seed + s for s in range(a.batched)]
+        b.generate_tokens(np.concatenate(toks, axis=0), opts, seeds=seeds)
+        print(f"[profile] batched {a.batched} streams, {a.frames} frames: decode {b.decode_time():.2f} ms", flush=True)
+        b.close()
+        model.close()
+        return
     st = model.new_state(rows=2, max_frames=scfg.chunk_frames, enc_len=scfg.encoder_length)
     rng = np.random.default_rng(42)
     ctx = np.stack([rng.integers(0, 1024, scfg.context_frames) + 0 for _ in range(16)], axis=1)
