@@ -11,6 +11,9 @@ is base + chunk index.
 Prints one JSON line: value = RVQ tokens/s (800 tokens per chunk / chunk
 seconds), plus chunk ms p50/p99, RTF, the HBM roofline of the decode and the
 CPU baseline (the numpy restatement timed on a bounded sample on this host).
+Beside it (not the headline value): 32 independent streams decoded as one
+batch (aggregate RVQ tokens/s, per-stream RTF) and the encoder prefill alone
+at 1 / 8 / 32 streams (matrix-core utilisation); --no-batched skips them.
 """
 
 from __future__ import annotations
