@@ -366,6 +366,7 @@ __global__ __launch_bounds__(64) void k_enc_attn(const T* __restrict__ qkv, int 
 // two bf16 parts (hi + lo, ~16 significant bits), as close to the fp32
 // probabilities of the reference's fused attention as bf16 MFMA allows.
 constexpr int kAQ = 128, kAK = 64, kALD = 64 + 8;  // queries, keys per tile, padded LDS row
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
 
 __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ qkv, int S, int H,
                                                        bf16* __restrict__ out) {
@@ -446,7 +447,7 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kb + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
-        if (key >= S) sc[t][r] = -INFINITY;
+        sc[t][r] = key < S ? sc[t][r] : -INFINITY;
         mt = fmaxf(mt, sc[t][r]);
       }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
@@ -455,15 +456,16 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
     float ps = 0.f;
     bf16x8_t pb[4], pl[4];  // P^T = hi + lo (bf16 each) for the four 16-key steps
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int g = 0; g < 4; ++g) {
+      f32x8_t pv;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = expf(sc[t][r] - mn);
-        const bf16 hi = f2bf(p);
-        ps += p;
-        reinterpret_cast<bf16*>(&pb[2 * t + (r >> 3)])[r & 7] = hi;
-        reinterpret_cast<bf16*>(&pl[2 * t + (r >> 3)])[r & 7] = f2bf(p - bf2f(hi));
+      for (int i = 0; i < 8; ++i) {
+        pv[i] = expf(sc[g >> 1][8 * (g & 1) + i] - mn);
+        ps += pv[i];
       }
+      pb[g] = __builtin_convertvector(pv, bf16x8_t);  // packed round-to-nearest-even conversions
+      pl[g] = __builtin_convertvector(pv - __builtin_convertvector(pb[g], f32x8_t), bf16x8_t);
+    }
     ps += __shfl_xor(ps, 32, 64);
     lsum = lsum * corr + ps;
     m = mn;
