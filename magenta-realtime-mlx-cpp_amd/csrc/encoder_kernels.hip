@@ -292,6 +292,120 @@ void launch_gemm_mfma(const bf16* A, const bf16* B, int M, int N, int K, const G
   hipLaunchKernelGGL((k_gemm_mfma<BM>), dim3(N / kBN, (M + BM - 1) / BM), dim3(256), lds, s, A, B, M, N, K, out);
 }
 
+// Large-M GEMM (the encoder of several streams): 256 x 256 x 64 tiles, 16
+// waves in a 4 x 4 grid (wave tile 64 x 64 = 2 x 2 MFMA 32x32x16 tiles, the
+// accumulators of k_gemm_mfma's waves), the same swizzled two-stage global ->
+// LDS ring.  Against 128 x 128 tiles it halves the operand bytes read from L2
+// per FLOP, which is what bounds the smaller tiles at these sizes.  Rows past
+// M read row M - 1 (not stored); N % 256 == 0.
+constexpr int kGB = 256;                 // block tile, M and N
+constexpr int kGBWaves = 16;
+constexpr int kGBStage = 2 * kGB * 128;  // A rows then B rows, 128 bytes (64 bf16) each
+
+__global__ __launch_bounds__(64 * kGBWaves) void k_gemm_big(const bf16* __restrict__ A, const bf16* __restrict__ B,
+                                                            int M, int N, int K, GemmOut<bf16> out) {
+  constexpr int RW = kGB / kGBWaves;  // rows of A (and of B) each wave loads per stage
+  constexpr int LA = 2 * RW / 8;      // load instructions per wave per stage (8 rows each)
+  extern __shared__ __align__(16) unsigned char lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int wm = wid >> 2, wn = wid & 3;
+  const int m0 = blockIdx.y * kGB, n0 = blockIdx.x * kGB;
+  const int nk = K / kBK;
+
+  auto issue = [&](int kt) {
+    const int ktc = min(kt, nk - 1);
+    unsigned char* st = lds + (kt % kStages) * kGBStage;
+    const int r8 = lane >> 3, p = lane & 7;
+#pragma unroll
+    for (int q = 0; q < RW / 8; ++q) {
+      const int r = wid * RW + q * 8 + r8;
+      const int gm = min(m0 + r, M - 1);
+      const bf16* src = A + (size_t)gm * K + ktc * kBK + ((p ^ swz(r)) << 3);
+      __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)src, (MRT_LDS void*)(st + (wid * RW + q * 8) * 128),
+                                       16, 0, 0);
+    }
+#pragma unroll
+    for (int q = 0; q < RW / 8; ++q) {
+      const int r = wid * RW + q * 8 + r8;
+      const bf16* src = B + (size_t)(n0 + r) * K + ktc * kBK + ((p ^ swz(r)) << 3);
+      __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)src,
+                                       (MRT_LDS void*)(st + kGB * 128 + (wid * RW + q * 8) * 128), 16, 0, 0);
+    }
+  };
+
+  f32x16_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+#pragma unroll
+  for (int kt = 0; kt < kStages - 1; ++kt) issue(kt);
+  const int lr = lane & 31, lh = lane >> 5;
+  for (int kt = 0; kt < nk; ++kt) {
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm((kStages - 2) * LA));  // this wave's loads of tile kt have landed
+    __syncthreads();  // every wave's loads of tile kt; every wave is done with tile kt - 1
+    issue(kt + kStages - 1);
+    const unsigned char* st = lds + (kt % kStages) * kGBStage;
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      const int c = 2 * ks + lh;
+      bf16x8_t a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r = wm * 64 + i * 32 + lr;
+        a[i] = *reinterpret_cast<const bf16x8_t*>(st + r * 128 + ((c ^ swz(r)) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = wn * 64 + j * 32 + lr;
+        b[j] = *reinterpret_cast<const bf16x8_t*>(st + kGB * 128 + r * 128 + ((c ^ swz(r)) << 4));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));  // no copy into LDS outlives the block
+
+  const int col_l = lane & 31, row_l = 4 * (lane >> 5);
+  if (out.a.kind == GemmEpi::Geglu) {
+    const int n = n0 + wn * 64 + col_l;  // gate column; up is n + 32
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
+        if (m < M) out.put_geglu(m, n, acc[i][0][r], acc[i][1][r]);
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
+          if (m < M) out.put(m, n0 + wn * 64 + j * 32 + col_l, acc[i][j][r]);
+        }
+  }
+}
+
+void launch_gemm_big(const bf16* A, const bf16* B, int M, int N, int K, const GemmOut<bf16>& out, hipStream_t s) {
+  constexpr size_t lds = (size_t)kStages * kGBStage;
+  static bool allowed = false;  // dynamic LDS above 64 KB needs an explicit allowance
+  if (!allowed) {
+    MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_big),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    allowed = true;
+  }
+  hipLaunchKernelGGL(k_gemm_big, dim3(N / kGB, (M + kGB - 1) / kGB), dim3(64 * kGBWaves), lds, s, A, B, M, N, K, out);
+}
+
 // ---- encoder self-attention (bidirectional, no mask, no bias, scale 1.0) -------------
 // One lane per query row, 64 rows per block; K/V tiles of 64 keys staged in
 // LDS; online softmax per 64-key tile.
@@ -533,8 +647,13 @@ void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const Gem
     MRT_REQUIRE(e.HD == e.H * 64 && N % e.HD == 0 && M == e.nb * e.S, "gemm: bad cross-KV shape");
   if (dt == DType::BF16 && allow_mfma && N % kBN == 0 && K % kBK == 0) {
     GemmOut<bf16> out{e, N};
-    // 128-row tiles when they give >= 1.5 tiles per CU of a 256-CU part, else 64-row tiles
-    if ((long)((M + 127) / 128) * (N / kBN) >= 384)
+    // 256 x 256 tiles for outputs up to 4096 wide when they still give >= 2
+    // tiles per CU of a 256-CU part (measured: faster there, slower for the
+    // 5632- and 40960-wide outputs, where 2-3 smaller blocks per CU hide more
+    // latency); 128-row tiles when those give >= 1.5 tiles per CU, else 64-row
+    if (N % kGB == 0 && N <= 4096 && (long)((M + kGB - 1) / kGB) * (N / kGB) >= 512)
+      launch_gemm_big((const bf16*)A, (const bf16*)B, M, N, K, out, s);
+    else if ((long)((M + 127) / 128) * (N / kBN) >= 384)
       launch_gemm_mfma<128>((const bf16*)A, (const bf16*)B, M, N, K, out, s);
     else
       launch_gemm_mfma<64>((const bf16*)A, (const bf16*)B, M, N, K, out, s);
