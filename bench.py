@@ -119,6 +119,39 @@ def time_step_kernels(state, model, cfg, stream, esz, reps_depth=20, reps_tempor
     return res
 
 
+def step_length_table(state, model, cfg, stream, esz, reps=10):
+    """depth_step at every cache length 0..15 and temporal_step at lengths 0, 10,
+    .., 40, 49: the cache is declared to hold `pos` entries before each launch,
+    so one launch is timed at one length (HIP events over `reps` launches).
+    Back-to-back depth steps find their 105 MB of weights in the 256 MB MALL."""
+    import torch
+    g = torch.Generator(device="cpu").manual_seed(7)
+    x = torch.randn(2, cfg.d_model, generator=g).to(device="cuda", dtype=model.torch_dtype)
+    logits = torch.empty(2, 1024, dtype=torch.float32, device="cuda")
+    out = torch.empty_like(x)
+    table = {"depth": [], "temporal": []}
+    for kind, positions in (("depth", range(cfg.rvq_depth)), ("temporal", (0, 10, 20, 30, 40, 49))):
+        for pos in positions:
+            def launch():
+                state.set_cache_length(1 if kind == "depth" else 0, pos)
+                if kind == "depth":
+                    state.depth_step(x, pos, level=pos, out=logits, sync=False)
+                else:
+                    state.temporal_step(x, pos, out=out, sync=False)
+            launch()  # warm
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                launch()
+            e1.record(stream)
+            e1.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / reps
+            nb = step_bytes(cfg, kind, pos, esz=esz)
+            table[kind].append({"cache_len": pos, "us": round(us, 2), "GBs": round(nb / (us * 1e-6) / 1e9, 1)})
+    state.sync()
+    return table
+
+
 def encoder_flops(cfg, rows, enc_len=1006):
     """FLOPs of one encoder pass over `rows` token rows: the 12 layers' projections,
     bidirectional attention, and the cross K/V projection of every temporal layer."""
@@ -377,6 +410,7 @@ def main():
     else:
         roof = None
     kern = time_step_kernels(sess.state, model, cfg, stream, esz)
+    lens = step_length_table(sess.state, model, cfg, stream, esz)
     dk = kern["depth"]
     print(f"[bench] depth_step kernel {dk['us']:.2f} us ({dk['GBs']:.0f} GB/s); temporal_step kernel "
           f"{kern['temporal']['us']:.2f} us ({kern['temporal']['GBs']:.0f} GB/s)", file=sys.stderr, flush=True)
@@ -426,9 +460,10 @@ def main():
         "decode_ms_per_chunk": float(np.mean(dec)),
         "depth_step_kernel": {"launch_us": dk["us"], "achieved_GBs": dk["GBs"],
                               "algorithmic_bytes_per_launch": dk["bytes"],
-                              "traffic": load_traffic("depth_step_traffic")},
+                              "traffic": load_traffic("depth_step_traffic"), "by_cache_len": lens["depth"]},
         "temporal_step_kernel": {"launch_us": kern["temporal"]["us"], "achieved_GBs": kern["temporal"]["GBs"],
-                                 "algorithmic_bytes_per_launch": kern["temporal"]["bytes"]},
+                                 "algorithmic_bytes_per_launch": kern["temporal"]["bytes"],
+                                 "by_cache_len": lens["temporal"]},
         "batched_streams": batched,
         "encoder_prefill": encoder,
         "cpu_baseline": cpu,
