@@ -569,7 +569,9 @@ def generate_tokens(model: OracleDepthformer, enc_tokens: np.ndarray,
     ``teacher`` (F, L) LLM ids: teacher forcing (the fed-back token is the
     teacher token, the model's draw is still recorded).  ``record`` collects
     per-step data: 'slices' (F, L, 2, C) level-slice logits in model dtype,
-    'temporal_out' (F, 2, D), 'frame_mean' (F, 2, D), 'drawn' (F, L) ids.
+    'temporal_out' (F, 2, D), 'frame_mean' (F, 2, D), 'drawn' (F, L) ids, and
+    at the end 'temporal_cache' (every temporal layer's K/V over all frames)
+    and 'depth_cache' (the last frame's depth K/V).
     Returns (F, L) int32 LLM ids (the fed-back tokens).
     """
     P = model.P
@@ -616,4 +618,7 @@ def generate_tokens(model: OracleDepthformer, enc_tokens: np.ndarray,
         prev_mean = P.r(fsum / rvq_div)  # decode.cpp:484
         if record is not None:
             record["frame_mean"][f] = prev_mean[:, 0]
+            record["depth_cache"] = dcache
+    if record is not None:
+        record["temporal_cache"] = tcache
     return out

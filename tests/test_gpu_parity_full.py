@@ -217,3 +217,46 @@ def test_full_size_device_draws(env, fp32_model, temperature, top_k):
                                                 seed=11, frame=f, level=l)
                      for l in range(L)] for f in range(F)])
     assert (drawn == exp).mean() >= 31 / 32, (drawn, exp)
+
+
+def test_full_chunk_fp32_teacher_forced(env, fp32_model):
+    """The whole 2 s chunk in fp32 (50 frames x 16 levels through the frame
+    kernel), teacher-forced on uniform-random tokens: every level's logits, every
+    temporal output, the temporal K/V rings of the first and last layer after
+    the chunk and the depth K/V rings of the last frame against the oracle
+    (norm-wise rel-err <= 1e-4), CFG argmax agreement >= 99 %."""
+    import torch
+    mrt_df, O = env["mrt_df"], env["O"]
+    F, L, C, D = 50, 16, 1024, env["cfg"].d_model
+    rng = np.random.default_rng(42)
+    teacher = (2 + C * np.arange(L)[None, :] + rng.integers(0, C, (F, L))).astype(np.int32)
+    st = fp32_model.new_state(max_frames=F)
+    rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"),
+               temporal=torch.zeros((F, 2, D), dtype=torch.float32, device="cuda"))
+    opts = mrt_df.GenOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40, guidance_weight=5.0,
+                             seed=5, codebook_size=C, codec_offset=2)
+    toks = st.generate_tokens(env["tok"], opts, teacher=teacher, record=rec)
+    np.testing.assert_array_equal(toks, teacher)
+    sl = rec["slices"].cpu().numpy()
+    tp = rec["temporal"].cpu().numpy()
+    nt = env["cfg"].num_temporal_layers
+    tk = {i: (st.read(mrt_df.BUF_TEMPORAL_K, i).cpu().numpy(), st.read(mrt_df.BUF_TEMPORAL_V, i).cpu().numpy())
+          for i in (0, nt - 1)}
+    dk = {i: (st.read(mrt_df.BUF_DEPTH_K, i).cpu().numpy(), st.read(mrt_df.BUF_DEPTH_V, i).cpu().numpy())
+          for i in (0, env["cfg"].num_depth_layers - 1)}
+    st.close()
+    om = O.OracleDepthformer(env["w"], O.DepthformerConfig(**dataclasses.asdict(env["cfg"])), mode="fp32")
+    orec = {}
+    o = O.GenerateOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40, guidance_weight=5.0, seed=5,
+                          codebook_size=C, codec_offset=2)
+    O.generate_tokens(om, env["tok"], o, teacher=teacher, record=orec, enc_out=_oracle_cached(env, "fp32")["enc_out"])
+    errs = [rel(sl[f, l], orec["slices"][f, l]) for f in range(F) for l in range(L)]
+    assert max(errs) <= 1e-4, max(errs)
+    assert rel(tp, orec["temporal_out"]) <= 1e-4
+    assert (_guided_argmax(sl) == _guided_argmax(orec["slices"])).mean() >= 0.99
+    for i, (k, v) in tk.items():
+        assert rel(k, orec["temporal_cache"][i]["k"]) <= 1e-4, i
+        assert rel(v, orec["temporal_cache"][i]["v"]) <= 1e-4, i
+    for i, (k, v) in dk.items():
+        assert rel(k, orec["depth_cache"][i]["k"]) <= 1e-4, i
+        assert rel(v, orec["depth_cache"][i]["v"]) <= 1e-4, i
