@@ -77,6 +77,14 @@ typedef struct mrt_gen_opts {
   void* record_temporal;   /* (F, rows, d_model) temporal_step outputs (model dtype) */
   int32_t* record_drawn;   /* (F, L) the model's own draws (device) */
   void* record_frame_mean; /* (F, rows, d_model) mean of each frame's 16 level embeddings */
+  /* GenerateOptions speculative path (decode.cpp:150-237, 380-446): frame f's
+   * levels are drafted with the previous call's tokens of frame f, verified in
+   * one causal pass over the frame's 16 positions, accepted up to the first
+   * disagreement (whose draw is the token), the rest decoded as usual.  The
+   * tokens are those of the same draws from the same logits.  bf16 models on
+   * the persistent path; ignored on a state's first call, with a teacher, or
+   * with record_drawn / record_frame_mean. */
+  int32_t speculative;
 } mrt_gen_opts;
 
 typedef struct mrt_df mrt_df;
@@ -203,7 +211,7 @@ typedef struct mrt_stream_config {
   int32_t codec_offset;            /* 2  vocab_codec_offset */
 } mrt_stream_config;
 
-/* GenerateChunkOptions (system.h:86-121); `speculative` is not supported. */
+/* GenerateChunkOptions (system.h:86-121). */
 typedef struct mrt_chunk_opts {
   float temperature;        /* 1.1 */
   int32_t top_k;            /* 40 */
@@ -213,6 +221,7 @@ typedef struct mrt_chunk_opts {
   int32_t pipeline_encoder; /* enqueue the next chunk's encoder before returning */
   int32_t use_graph;        /* replay the decode loop from a captured hipGraph */
   const int32_t* teacher;   /* optional host (chunk_frames, levels) ids fed back instead of draws */
+  int32_t speculative;      /* speculative depth decoding, drafts = the previous chunk's tokens */
 } mrt_chunk_opts;
 
 typedef struct mrt_df_stream mrt_df_stream;

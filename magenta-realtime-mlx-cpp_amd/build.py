@@ -26,6 +26,7 @@ SOURCES = [
     "persist_kernels.hip",
     "stream_kernels.hip",
     "batch_kernels.hip",
+    "spec_kernels.hip",
     "safetensors.cpp",
     "model.cpp",
     "stream.cpp",

@@ -110,6 +110,7 @@ mrt::GenOpts to_opts(const mrt_gen_opts* opts) {
   o.record_temporal = opts->record_temporal;
   o.record_drawn = opts->record_drawn;
   o.record_frame_mean = opts->record_frame_mean;
+  o.speculative = opts->speculative != 0;
   return o;
 }
 
@@ -326,6 +327,7 @@ void mrt_chunk_opts_default(mrt_chunk_opts* opts) {
   opts->pipeline_encoder = 0;
   opts->use_graph = 1;
   opts->teacher = nullptr;
+  opts->speculative = 0;
 }
 
 int mrt_df_stream_create(mrt_df* h, const mrt_stream_config* cfg, mrt_df_stream** out) {
@@ -356,6 +358,7 @@ int mrt_df_stream_generate_chunk(mrt_df_stream* s, const int32_t* style, const m
     o.pipeline_encoder = opts->pipeline_encoder != 0;
     o.use_graph = opts->use_graph != 0;
     o.teacher = opts->teacher;
+    o.speculative = opts->speculative != 0;
     SS(s).generate_chunk(style, o, llm_out, rvq_out);
   });
 }

@@ -24,6 +24,14 @@ void bgemm_resid(const void* X, int M, int K, const void* W, int N, void* R, int
 // *pos_ptr when non-null) of caches laid out (M, H, Lmax, 64).
 void bgemm_qkv(const void* X, int M, int K, const void* W, int HD, void* Q, void* Kc, void* Vc, int H, int Lmax, int pos,
                const int* pos_ptr, hipStream_t s);
+// The same for rows m = P * pos + r (positions of one stream's frame, P CFG
+// rows each): k / v -> slot pos of ring row r (P, H, Lmax, 64).
+void bgemm_qkv_pos(const void* X, int M, int K, const void* W, int HD, void* Q, void* Kc, void* Vc, int H, int Lmax,
+                   int P, hipStream_t s);
+// groups independent products: rows [g rows, +rows) of X against
+// W + g * w_group_stride, logits rounded to bf16 into Y rows g rows + m.
+void bgemm_f32_grouped(const void* X, int rows, int K, const void* W, long w_group_stride, int N, float* Y, int ldy,
+                       int groups, hipStream_t s);
 // Gated GELU over the 32-row packed wi_0 / wi_1 matrix (2F rows) -> (M, F).
 void bgemm_geglu(const void* X, int M, int K, const void* W01, int F, void* Hout, int ldh, hipStream_t s);
 

@@ -71,6 +71,26 @@ struct BQKV {
   }
 };
 
+// Rows m = P * pos + r (the positions of one frame, rows r = 0..P-1 each):
+// q -> Q row m; k / v -> ring slot pos of ring row r, caches (P, H, Lmax, 64).
+struct BQKVPos {
+  bf16* q;
+  bf16* kc;
+  bf16* vc;
+  int HD, H, Lmax, P;
+  __device__ void operator()(int m, int n, const float (&v)[1]) const {
+    const bf16 o = St<bf16>::st(v[0]);
+    const int which = n / HD, nn = n - which * HD;
+    if (which == 0) {
+      q[(size_t)m * HD + nn] = o;
+    } else {
+      const int r = m % P, pos = m / P;
+      bf16* c = which == 1 ? kc : vc;
+      c[(((size_t)r * H + (nn >> 6)) * Lmax + pos) * 64 + (nn & 63)] = o;
+    }
+  }
+};
+
 struct BGeglu {
   bf16* h;
   int ldh;
@@ -106,7 +126,13 @@ struct HasPre<Epi, decltype((void)Epi::kPre)> {
 // XCD's L2 for the others.
 template <int P, int MT, class Epi>
 __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X, int M, int K,
-                                                      const bf16* __restrict__ W, int nout, int ntiles, Epi epi) {
+                                                      const bf16* __restrict__ W, int nout, int ntiles, Epi epi,
+                                                      long w_group_stride) {
+  // blockIdx.y = group g (grouped launch): rows [g M, g M + M) of X against
+  // W + g * w_group_stride, outputs at rows g M + m
+  const int grow = blockIdx.y * M;
+  X += (size_t)grow * K;
+  W += blockIdx.y * w_group_stride;
   constexpr int kRows = 16 * MT;
   constexpr int kOut = kRows * kBgCols;                        // outputs of the block
   constexpr int kPer = (kOut + kBgThreads - 1) / kBgThreads;  // epilogue outputs per thread
@@ -134,7 +160,7 @@ __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int idx = tid + kBgThreads * i, m = m0 + idx / kBgCols, n = j0 + idx % kBgCols;
-      pre[i] = (idx < kOut && m < M && n < nout) ? epi.pre(m, n) : 0.f;
+      pre[i] = (idx < kOut && m < M && n < nout) ? epi.pre(grow + m, n) : 0.f;
     }
   }
   f32x4_t acc[P][MT];
@@ -191,9 +217,9 @@ __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X
     const int idx = tid + kBgThreads * i, m = m0 + idx / kBgCols, n = idx % kBgCols;
     if (idx >= kOut || m >= M || j0 + n >= nout) continue;
     if constexpr (HasPre<Epi>::value)
-      epi(m, j0 + n, v[i], pre[i]);
+      epi(grow + m, j0 + n, v[i], pre[i]);
     else
-      epi(m, j0 + n, v[i]);
+      epi(grow + m, j0 + n, v[i]);
   }
 }
 
@@ -202,20 +228,21 @@ __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X
 // outputs keep all rows in a block (measured faster: each block then reads the
 // activations once for twice the columns' work).
 template <int P, class Epi>
-void launch_bgemm(const bf16* X, int M, int K, const bf16* W, int nout, const Epi& epi, hipStream_t s) {
+void launch_bgemm(const bf16* X, int M, int K, const bf16* W, int nout, const Epi& epi, hipStream_t s, int groups = 1,
+                  long w_group_stride = 0) {
   MRT_REQUIRE(M >= 1 && M <= kBatchRows, "batched GEMM: rows must be in [1, 64]");
   MRT_REQUIRE(K % 32 == 0 && K >= 32, "batched GEMM: K must be a multiple of 32");
-  MRT_REQUIRE(nout >= 1, "batched GEMM: no outputs");
+  MRT_REQUIRE(nout >= 1 && groups >= 1, "batched GEMM: no outputs");
   const int ntiles = (nout + kBgCols - 1) / kBgCols, mtiles = (M + 15) / 16;
   int ms = 1;
   while (ntiles < 128 && ms < 4 && ms < mtiles && ntiles * ms < 256) ms *= 2;
-  const dim3 grid(ntiles * ms), block(kBgThreads);
+  const dim3 grid(ntiles * ms, groups), block(kBgThreads);
   if (ms == 1)
-    hipLaunchKernelGGL((k_bgemm<P, 4, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi);
+    hipLaunchKernelGGL((k_bgemm<P, 4, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi, w_group_stride);
   else if (ms == 2)
-    hipLaunchKernelGGL((k_bgemm<P, 2, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi);
+    hipLaunchKernelGGL((k_bgemm<P, 2, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi, w_group_stride);
   else
-    hipLaunchKernelGGL((k_bgemm<P, 1, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi);
+    hipLaunchKernelGGL((k_bgemm<P, 1, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi, w_group_stride);
   MRT_HIP_CHECK(hipGetLastError());
 }
 
@@ -368,6 +395,19 @@ void bgemm_qkv(const void* X, int M, int K, const void* W, int HD, void* Q, void
                const int* pos_ptr, hipStream_t s) {
   BQKV e{static_cast<bf16*>(Q), static_cast<bf16*>(Kc), static_cast<bf16*>(Vc), HD, H, Lmax, pos, pos_ptr};
   launch_bgemm<1>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W), 3 * HD, e, s);
+}
+
+void bgemm_qkv_pos(const void* X, int M, int K, const void* W, int HD, void* Q, void* Kc, void* Vc, int H, int Lmax,
+                   int P, hipStream_t s) {
+  MRT_REQUIRE(P >= 1 && M % P == 0 && M / P <= Lmax, "batched GEMM: positions exceed the ring");
+  BQKVPos e{static_cast<bf16*>(Q), static_cast<bf16*>(Kc), static_cast<bf16*>(Vc), HD, H, Lmax, P};
+  launch_bgemm<1>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W), 3 * HD, e, s);
+}
+
+void bgemm_f32_grouped(const void* X, int rows, int K, const void* W, long w_group_stride, int N, float* Y, int ldy,
+                       int groups, hipStream_t s) {
+  launch_bgemm<1>(static_cast<const bf16*>(X), rows, K, static_cast<const bf16*>(W), N, BF32{Y, ldy}, s, groups,
+                  w_group_stride);
 }
 
 void bgemm_geglu(const void* X, int M, int K, const void* W01, int F, void* Hout, int ldh, hipStream_t s) {

@@ -294,10 +294,12 @@ void gemv_geglu(DType dt, int nb, const void* W01, int F, int K, const void* X, 
 namespace {
 
 // qpos_ptr non-null: the query position is read from it and len = qpos + 1.
+// pos_rows > 0: query row b is position b / pos_rows of ring row b % pos_rows
+// (all positions of one frame at once, causal: len = position + 1).
 template <typename T>
 __global__ __launch_bounds__(64) void k_self_attn(const T* __restrict__ Q, const T* __restrict__ Kc,
                                                   const T* __restrict__ Vc, int H, int Lmax, int len,
-                                                  int qpos, const int* __restrict__ qpos_ptr,
+                                                  int qpos, const int* __restrict__ qpos_ptr, int pos_rows,
                                                   const T* __restrict__ bias_tab,
                                                   const int* __restrict__ buckets, T* __restrict__ out) {
   using S = St<T>;
@@ -307,13 +309,19 @@ __global__ __launch_bounds__(64) void k_self_attn(const T* __restrict__ Q, const
     qpos = *qpos_ptr;
     len = qpos + 1;
   }
+  int rb = b;  // ring row
+  if (pos_rows > 0) {
+    rb = b % pos_rows;
+    qpos = b / pos_rows;
+    len = qpos + 1;
+  }
   const int HD = H * 64;
   __shared__ float qs[64];
   __shared__ float ps[kMaxSelfLen];
   qs[lane] = S::ld(Q[(size_t)b * HD + h * 64 + lane]);
   __syncthreads();
-  const T* Kp = Kc + (size_t)bh * Lmax * 64;
-  const T* Vp = Vc + (size_t)bh * Lmax * 64;
+  const T* Kp = Kc + ((size_t)rb * H + h) * Lmax * 64;
+  const T* Vp = Vc + ((size_t)rb * H + h) * Lmax * 64;
   float mx = -INFINITY;
   for (int j = lane; j < len; j += 64) {
     const T* kr = Kp + (size_t)j * 64;
@@ -449,15 +457,17 @@ void self_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, 
 
 void self_attn_at(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H, int Lmax, int len,
                   int qpos, const int* qpos_ptr, const void* bias_tab, const int* buckets, void* out,
-                  hipStream_t s) {
+                  hipStream_t s, int pos_rows) {
   MRT_REQUIRE(qpos_ptr == nullptr || Lmax <= kMaxSelfLen, "self_attn: ring longer than the kernel's score buffer");
+  MRT_REQUIRE(pos_rows == 0 || (nb % pos_rows == 0 && nb / pos_rows <= Lmax && Lmax <= kMaxSelfLen),
+              "self_attn: positions exceed the ring");
   if (dt == DType::F32)
     hipLaunchKernelGGL(k_self_attn<float>, dim3(nb * H), dim3(64), 0, s, (const float*)Q,
-                       (const float*)Kc, (const float*)Vc, H, Lmax, len, qpos, qpos_ptr,
+                       (const float*)Kc, (const float*)Vc, H, Lmax, len, qpos, qpos_ptr, pos_rows,
                        (const float*)bias_tab, buckets, (float*)out);
   else
     hipLaunchKernelGGL(k_self_attn<bf16>, dim3(nb * H), dim3(64), 0, s, (const bf16*)Q,
-                       (const bf16*)Kc, (const bf16*)Vc, H, Lmax, len, qpos, qpos_ptr,
+                       (const bf16*)Kc, (const bf16*)Vc, H, Lmax, len, qpos, qpos_ptr, pos_rows,
                        (const bf16*)bias_tab, buckets, (bf16*)out);
   MRT_HIP_CHECK(hipGetLastError());
 }

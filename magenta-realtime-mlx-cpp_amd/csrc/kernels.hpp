@@ -50,9 +50,11 @@ void self_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, 
                void* out, hipStream_t s);
 // The same with the query position read on the device from *qpos_ptr when it
 // is non-null (len = qpos + 1; the caller keeps it below Lmax).
+// pos_rows > 0 instead attends all positions of one frame at once: query row
+// b is position b / pos_rows of ring row b % pos_rows, causal (len = pos + 1).
 void self_attn_at(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H, int Lmax, int len,
                   int qpos, const int* qpos_ptr, const void* bias_tab, const int* buckets, void* out,
-                  hipStream_t s);
+                  hipStream_t s, int pos_rows = 0);
 // Cross-attention over S encoder keys (no bias/mask), split over key blocks.
 // ``part`` needs nb*H*nsplit*66 floats.
 void cross_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H,
@@ -80,6 +82,9 @@ struct SampleParams {
   // + level) * codebook + i] = gumbel(seed[stream], frame, level, i).
   const float* noise = nullptr;
   int noise_frames = 0;
+  // Optional: levels <= *decided already have their token (speculative
+  // decoding); the sampler then does nothing for them.
+  const int* decided = nullptr;
 };
 
 // One CFG stream: rows (0, 1) of ``logits`` (nb=2, C) level slice.
@@ -101,6 +106,11 @@ void sample_level(DType dt, const float* logits, const SampleParams& p, int fram
 void sample_levels(DType dt, int streams, const float* logits, const SampleParams& p, int frame,
                    const int* frame_ptr, int level, int slot, int tstride, const int* teacher, int* tokens,
                    int* drawn, const void* emb, int D, void* next_in, void* fsum, void* frame_mean, hipStream_t s);
+
+// Every level of one frame drawn at once from logits (levels, 2, C) (one
+// stream, noise (F, L, C) tabulated or computed from p.seed[0]):
+// drawn[l] = codec_offset + C * l + winner.
+void draw_levels(const float* logits, const SampleParams& p, int frame, int levels, int* drawn, hipStream_t s);
 
 // ---- encoder ------------------------------------------------------------------
 // x[r, :] = round(emb[tok[r]] + pe_T[r % S])    (model.cpp:231-236)

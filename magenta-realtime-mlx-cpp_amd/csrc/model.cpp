@@ -6,8 +6,10 @@
 #include <cstring>
 #include <thread>
 
+#include "batch.hpp"
 #include "kernels.hpp"
 #include "persist.hpp"
+#include "spec.hpp"
 
 namespace mrt {
 
@@ -340,6 +342,19 @@ State::State(Model& model, int rows_, int max_frames, int enc_len)
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_err_), 64, hipHostMallocDefault));
   *h_err_ = 0;
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_seed_), 64, hipHostMallocDefault));
+  if (m.dt == DType::BF16) {  // speculative decoding (verification pass over 2 L rows)
+    const size_t R2 = 2 * L;
+    d_drafts_ = static_cast<int*>(dalloc(static_cast<size_t>(F) * L * 4));
+    sx_ = dalloc(R2 * D * e);
+    sxn_ = dalloc(R2 * std::max(D, FF) * e);
+    sq_ = dalloc(R2 * HD * e);
+    satt_ = dalloc(R2 * HD * e);
+    sffh_ = dalloc(R2 * FF * e);
+    slog_ = static_cast<float*>(dalloc(R2 * 1024 * 4));
+    sdrawn_ = static_cast<int*>(dalloc(L * 4));
+    sdecided_ = static_cast<int*>(dalloc(4));
+    sfm_ = dalloc(rows * D * e);
+  }
   const char* path = std::getenv("MRT_DECODE_PATH");
   if (!(path && std::string(path) == "layers")) setup_persistent();
 }
@@ -500,6 +515,7 @@ void State::reserve_epochs(uint32_t n) {
 }
 
 int State::decode_launches(const GenOpts& o) const {
+  if (spec_drafts_) return o.num_frames * o.rvq_depth;  // temporal + L - 1 depth steps per frame
   return frame_kernel_ ? o.num_frames : o.num_frames * (1 + o.rvq_depth);
 }
 
@@ -618,6 +634,73 @@ void State::enqueue_decode_p(const GenOpts& o) {
       }
     }
     if (o.record_frame_mean) copy(static_cast<char*>(o.record_frame_mean) + f * row_bytes, t_in, row_bytes);
+  }
+}
+
+// Speculation runs when asked for, on the bf16 persistent path, with drafts
+// from a previous call of the same frame count and no teacher or per-draw
+// records (the reference also speculates only once a chunk exists,
+// system.cpp:244-256).
+bool State::speculating(const GenOpts& o) const {
+  return o.speculative && m.dt == DType::BF16 && persistent() && o.teacher == nullptr && o.record_drawn == nullptr &&
+         o.record_frame_mean == nullptr && 2 * o.rvq_depth <= kBatchRows && o.rvq_depth == m.cfg.rvq_depth;
+}
+
+// The decode loop with speculative depth decoding (decode.cpp:380-446).  Per
+// frame: the temporal step; one causal pass over [temporal_out, emb(draft
+// 0..L-2)] (depth_forward_full, model.cpp:243-268) writing the depth K/V of
+// every position and every level's logits; every level drawn with its own
+// noise; the drafts accepted up to the first disagreement (whose draw is the
+// token); then the remaining levels as depth steps with draws (each skips
+// itself when its level is already decided); the frame mean of the L tokens.
+void State::enqueue_decode_spec(const GenOpts& o) {
+  const Config& c = m.cfg;
+  const DType dt = m.dt;
+  const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads, C = o.codebook, L = o.rvq_depth;
+  const int R2 = 2 * L;
+  const size_t row_bytes = static_cast<size_t>(rows) * D * esz();
+  embed_fill(dt, m.emb, D, 0, rows, t_in, stream);
+  gumbel_table(d_seed, o.num_frames, L, C, noise_, stream);
+  SampleParams sp{o.guidance_weight, o.temperature, o.top_k, C, o.codec_offset, L, d_seed};
+  SampleParams sp_all = sp;
+  sp_all.noise = noise_;
+  SampleParams sp_rest = sp_all;
+  sp_rest.noise_frames = o.num_frames;  // one stream: noise row (frame * L + level)
+  sp_rest.decided = sdecided_;
+  const char* head0 = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset) * D * esz();
+  for (int f = 0; f < o.num_frames; ++f) {
+    int* tok = d_tokens + static_cast<size_t>(f) * L;
+    launch_temporal_p(t_in, f, t_out);
+    if (o.record_temporal) copy(static_cast<char*>(o.record_temporal) + f * row_bytes, t_out, row_bytes);
+    // verification pass: rows 2i + r
+    spec_inputs(dt, t_out, m.emb, d_drafts_ + static_cast<size_t>(f) * L, L, D, sx_, stream);
+    for (int i = 0; i < c.num_depth_layers; ++i) {
+      const DecoderLayerW& W = m.dep[i];
+      rmsnorm_rows(dt, sx_, W.norm_sa, 1e-6f, R2, D, sxn_, stream);
+      bgemm_qkv_pos(sxn_, R2, D, W.wqkv, HD, sq_, dk(i), dv(i), H, L, rows, stream);
+      self_attn_at(dt, R2, sq_, dk(i), dv(i), H, L, 0, 0, nullptr, m.dbias, m.dbuckets, satt_, stream, rows);
+      bgemm_resid(satt_, R2, HD, W.wo, D, sx_, D, stream);
+      rmsnorm_rows(dt, sx_, W.norm_ff, 1e-6f, R2, D, sxn_, stream);
+      bgemm_geglu(sxn_, R2, D, W.w01, FF, sffh_, FF, stream);
+      bgemm_resid(sffh_, R2, FF, W.wo2, D, sx_, D, stream);
+    }
+    rmsnorm_rows(dt, sx_, m.dec_norm, 1e-6f, R2, D, sxn_, stream);
+    bgemm_f32_grouped(sxn_, rows, D, head0, static_cast<long>(C) * D, C, slog_, C, L, stream);
+    draw_levels(slog_, sp_all, f, L, sdrawn_, stream);
+    spec_accept(sdrawn_, d_drafts_ + static_cast<size_t>(f) * L, L, tok, sdecided_, stream);
+    float* rec = o.record_slices ? o.record_slices + static_cast<size_t>(f) * L * rows * C : nullptr;
+    if (rec) spec_record(slog_, slice, sdecided_, 0, C, rec, stream);
+    // the levels after the first disagreement
+    for (int l = 1; l < L; ++l) {
+      spec_feed(dt, tok, l, m.emb, D, d_in, stream);
+      const char* head = head0 + static_cast<size_t>(C) * l * D * esz();
+      StepArgs a = depth_args(d_in, l, head, C, slice, nullptr);
+      a.sp = sp_rest;
+      launch_step(dt, a, persist_grid_, lds_d_, stream);
+      sample_level(dt, slice, sp_rest, f, l, f * L + l, nullptr, d_tokens, nullptr, m.emb, D, x, fsum, sfm_, stream);
+      if (rec) spec_record(slog_, slice, sdecided_, l, C, rec + static_cast<size_t>(l) * rows * C, stream);
+    }
+    frame_mean_tokens(dt, tok, L, m.emb, D, t_in, stream);
   }
 }
 
@@ -874,6 +957,7 @@ int State::sample(const float* slice_dev, const GenOpts& o, int frame, int level
   SampleParams sp{o.guidance_weight, o.temperature, o.top_k, o.codebook, o.codec_offset, o.rvq_depth, d_seed};
   // Token goes to slot 0 of the token buffer; the feedback outputs land in
   // scratch rows that the next decode overwrites.
+  prev_frames_ = 0;  // slot 0 of the token buffer is no longer the last call's
   sample_level(m.dt, slice_dev, sp, frame, level, 0, nullptr, d_tokens, nullptr, m.emb, c.d_model, d_in, fsum,
                x, stream);
   MRT_HIP_CHECK(hipMemcpyAsync(h_pinned, d_tokens, 4, hipMemcpyDeviceToHost, stream));
@@ -904,6 +988,12 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
   }
   *h_seed_ = o.seed;  // its previous copy ended before the last call returned
   MRT_HIP_CHECK(hipMemcpyAsync(d_seed, h_seed_, 8, hipMemcpyHostToDevice, stream));
+  // Speculative decoding drafts frame f with the previous call's tokens of
+  // frame f (build_depth_draft, decode.cpp:150-166): copied before this call
+  // overwrites them.  Without a previous call of the same length it does not
+  // speculate (as the reference's first chunk).
+  spec_drafts_ = speculating(o) && prev_frames_ == o.num_frames;
+  if (spec_drafts_) copy(d_drafts_, d_tokens, nt * 4);
 
   if (persistent()) reserve_epochs(decode_launches(o));
   if (!ev_dec_[0]) {
@@ -915,6 +1005,7 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
     const std::vector<double> key = {
         (double)o.num_frames, (double)o.rvq_depth, (double)o.temperature, (double)o.top_k,
         (double)o.guidance_weight, (double)o.codebook, (double)o.codec_offset, o.teacher ? 1.0 : 0.0,
+        spec_drafts_ ? 1.0 : 0.0,
         (double)reinterpret_cast<uintptr_t>(o.record_slices),
         (double)reinterpret_cast<uintptr_t>(o.record_temporal),
         (double)reinterpret_cast<uintptr_t>(o.record_drawn),
@@ -927,7 +1018,9 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
       MRT_HIP_CHECK(hipStreamSynchronize(stream));  // capture starts on an idle stream
       MRT_HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
       try {
-        if (persistent())
+        if (spec_drafts_)
+          enqueue_decode_spec(o);
+        else if (persistent())
           enqueue_decode_p(o);
         else
           enqueue_decode(o);
@@ -945,7 +1038,9 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
     MRT_HIP_CHECK(hipGraphLaunch(graph_exec_, stream));
   } else {
     MRT_HIP_CHECK(hipEventRecord(ev_dec_[0], stream));
-    if (persistent())
+    if (spec_drafts_)
+      enqueue_decode_spec(o);
+    else if (persistent())
       enqueue_decode_p(o);
     else
       enqueue_decode(o);
@@ -959,6 +1054,7 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
   std::memcpy(out_host, h_pinned, nt * 4);
   temporal_len_ = o.num_frames;
   depth_len_ = o.rvq_depth;
+  prev_frames_ = o.num_frames;
 }
 
 float State::last_decode_ms(int* launches) {

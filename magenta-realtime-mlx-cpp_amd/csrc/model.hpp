@@ -120,6 +120,9 @@ struct GenOpts {
   int codec_offset = 2;
   const int32_t* teacher = nullptr;  // host (F, L)
   bool use_graph = false;
+  // Speculative depth decoding (decode.cpp:150-237, 380-446) with the previous
+  // call's tokens as the drafts: bf16 persistent path, no teacher.
+  bool speculative = false;
   float* record_slices = nullptr;    // device (F, L, rows, C)
   void* record_temporal = nullptr;   // device (F, rows, D)
   int* record_drawn = nullptr;       // device (F, L)
@@ -171,6 +174,8 @@ class State {
   void launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits, float* rec_slice);
   void launch_frame_p(const GenOpts& o, int f);
   void enqueue_decode_p(const GenOpts& o);
+  void enqueue_decode_spec(const GenOpts& o);
+  bool speculating(const GenOpts& o) const;
   int decode_launches(const GenOpts& o) const;
   void reserve_epochs(uint32_t n);
   void check_device_error();
@@ -190,6 +195,15 @@ class State {
   hipEvent_t ev_dec_[2] = {nullptr, nullptr};  // around the decode section of generate
   int dec_launches_ = 0;
   bool dec_timed_ = false;
+  // speculative decoding: drafts (the previous call's tokens), the
+  // verification pass's rows (2 L) and its per-level draws / accepted count
+  int* d_drafts_ = nullptr;
+  int prev_frames_ = 0;  // frames of the tokens left by the last generate (0: none)
+  bool spec_drafts_ = false;  // this call speculates with d_drafts_
+  void *sx_ = nullptr, *sxn_ = nullptr, *sq_ = nullptr, *satt_ = nullptr, *sffh_ = nullptr;
+  float* slog_ = nullptr;
+  int *sdrawn_ = nullptr, *sdecided_ = nullptr;
+  void* sfm_ = nullptr;  // scratch frame-mean rows of the sampler (the spec path writes its own)
   void print_trace();
 
   size_t esz() const { return m.esz; }

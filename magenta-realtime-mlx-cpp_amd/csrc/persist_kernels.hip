@@ -1422,6 +1422,12 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   if (a.nlayers > 0) prefetch_qkv<T, CROSS>(c, a, 0);
   __syncthreads();
   if (!ok) return;  // a previous launch failed: do nothing
+  if (!CROSS && a.sp.decided != nullptr && *a.sp.decided >= a.pos) {
+    // speculative decoding already has this level's token: only the epoch advances
+    __builtin_amdgcn_s_waitcnt(0);
+    if (c.blk == 0 && threadIdx.x == 0) astore(a.ll.seq, c.ep + 1u);
+    return;
+  }
   if (a.trace != nullptr && c.blk == 0 && threadIdx.x == 0) a.trace[kTraceStart] = wall_clock64();
   StackIO io{a.in, a.D, 0u, CROSS ? a.out : nullptr, !CROSS, 0, false, 64, a.pos, a.trace};
   const uint32_t x_tag = run_stack<T, CROSS>(c, a, io);

@@ -44,14 +44,15 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   }
 }
 
-// The draw of one stream by one wave (lane = threadIdx.x < 64): returns the
-// winning index within the level's C entries.
-__device__ __forceinline__ int wave_draw(const float* __restrict__ logits, const SampleParams& p, int stream,
-                                         int frame, int level) {
+// One draw by one wave (lane = threadIdx.x < 64) over the level's C entries
+// of the CFG rows l0 (conditioned) / l1 (unconditioned); nz: the draw's
+// tabulated noise row, or null to compute gumbel(seed, frame, level, i).
+// Returns the winning index.
+__device__ __forceinline__ int wave_draw_rows(const float* __restrict__ l0, const float* __restrict__ l1,
+                                              const float* __restrict__ nz, uint64_t seed, const SampleParams& p,
+                                              int frame, int level) {
   const int lane = threadIdx.x;
   const int C = p.codebook;
-  const float* l0 = logits + (size_t)(2 * stream) * C;
-  const float* l1 = l0 + C;
   const float wc = 1.0f + p.guidance_weight;  // decode.cpp:255-256
   const float wu = p.guidance_weight;
 
@@ -64,8 +65,7 @@ __device__ __forceinline__ int wave_draw(const float* __restrict__ logits, const
     a0[t] = l0[c];
     a1[t] = l1[c];
   }
-  if (p.temperature != 0.0f && p.noise != nullptr) {
-    const float* nz = p.noise + (((size_t)stream * p.noise_frames + frame) * p.rvq_depth + level) * C;
+  if (p.temperature != 0.0f && nz != nullptr) {
 #pragma unroll
     for (int t = 0; t < kMaxPerLane; ++t) gn[t] = nz[min(lane + 64 * t, C - 1)];
   }
@@ -85,8 +85,8 @@ __device__ __forceinline__ int wave_draw(const float* __restrict__ logits, const
 #pragma unroll
     for (int t = 0; t < kMaxPerLane; ++t)
       if (lane + 64 * t < C) v[t] = __fdiv_rn(v[t], p.temperature);
-    if (p.noise == nullptr) {
-      const uint64_t seed0 = p.seed[stream];
+    if (nz == nullptr) {
+      const uint64_t seed0 = seed;
 #pragma unroll
       for (int t = 0; t < kMaxPerLane; ++t) {
         const int c = lane + 64 * t;
@@ -160,6 +160,27 @@ __device__ __forceinline__ int wave_draw(const float* __restrict__ logits, const
   return bi;
 }
 
+__device__ __forceinline__ int wave_draw(const float* __restrict__ logits, const SampleParams& p, int stream,
+                                         int frame, int level) {
+  const int C = p.codebook;
+  const float* l0 = logits + (size_t)(2 * stream) * C;
+  const float* nz = p.noise != nullptr
+                        ? p.noise + (((size_t)stream * p.noise_frames + frame) * p.rvq_depth + level) * C
+                        : nullptr;
+  return wave_draw_rows(l0, l0 + C, nz, p.temperature != 0.0f ? p.seed[stream] : 0, p, frame, level);
+}
+
+// Every level of one frame drawn at once (block l draws level l from logit
+// rows 2l, 2l + 1; the speculative verification pass): drawn[l] = the LLM id.
+__global__ __launch_bounds__(64) void k_draw_levels(const float* __restrict__ logits, SampleParams p, int frame,
+                                                    int* __restrict__ drawn) {
+  const int l = blockIdx.x, C = p.codebook;
+  const float* l0 = logits + (size_t)(2 * l) * C;
+  const float* nz = p.noise != nullptr ? p.noise + ((size_t)frame * p.rvq_depth + l) * C : nullptr;
+  const int bi = wave_draw_rows(l0, l0 + C, nz, p.temperature != 0.0f ? p.seed[0] : 0, p, frame, l);
+  if (threadIdx.x == 0) drawn[l] = p.codec_offset + l * C + bi;
+}
+
 // Block b draws for stream b: logits rows (2b, 2b + 1), seed p.seed[b], token
 // slots slot + b * tstride; a non-null frame_ptr supplies the frame index.
 // Wave 0 draws; all four waves then write the token's embedding to both rows
@@ -175,6 +196,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int tid = threadIdx.x;
   const int stream = blockIdx.x;
   const int C = p.codebook, L = p.rvq_depth;
+  if (p.decided != nullptr && *p.decided >= level) return;  // the level's token is already known
   if (frame_ptr != nullptr) {
     frame = *frame_ptr;
     slot += frame * L;
@@ -229,6 +251,12 @@ void sample_level(DType dt, const float* logits, const SampleParams& p, int fram
                   void* next_in, void* fsum, void* frame_mean, hipStream_t s) {
   sample_levels(dt, 1, logits, p, frame, nullptr, level, slot, 0, teacher, tokens, drawn, emb, D, next_in, fsum,
                 frame_mean, s);
+}
+
+void draw_levels(const float* logits, const SampleParams& p, int frame, int levels, int* drawn, hipStream_t s) {
+  MRT_REQUIRE(p.codebook >= 1 && p.codebook <= 64 * kMaxPerLane, "draw: codebook must be <= 1024");
+  hipLaunchKernelGGL(k_draw_levels, dim3(levels), dim3(64), 0, s, logits, p, frame, drawn);
+  MRT_HIP_CHECK(hipGetLastError());
 }
 
 void sample_levels(DType dt, int streams, const float* logits, const SampleParams& p, int frame,

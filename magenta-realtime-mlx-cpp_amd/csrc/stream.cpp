@@ -104,6 +104,7 @@ void Stream::generate_chunk(const int32_t* style, const ChunkOpts& o, int32_t* l
   g.codec_offset = c.codec_offset;
   g.teacher = o.teacher;
   g.use_graph = o.use_graph;
+  g.speculative = o.speculative;
   const size_t n = static_cast<size_t>(c.chunk_frames) * c.levels;
   llm_tmp_.resize(n);
   st.generate(nullptr, g, llm_tmp_.data());  // waits for the chunk's ids

@@ -35,7 +35,7 @@ struct StreamConfig {
   int enc_len() const { return context_frames * enc_depth + style_depth; }
 };
 
-// GenerateChunkOptions (system.h:86-121) without the speculative path.
+// GenerateChunkOptions (system.h:86-121).
 struct ChunkOpts {
   float temperature = 1.1f;
   int top_k = 40;
@@ -45,6 +45,7 @@ struct ChunkOpts {
   bool pipeline_encoder = false;
   bool use_graph = true;
   const int32_t* teacher = nullptr;  // host (chunk_frames, levels) ids fed in place of the draws
+  bool speculative = false;          // drafts: the previous chunk's tokens of the same frame
 };
 
 // SystemState's token context (system.h:124-160) resident in device memory,

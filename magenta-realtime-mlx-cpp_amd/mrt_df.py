@@ -60,6 +60,7 @@ class _GenOpts(ctypes.Structure):
         ("record_temporal", ctypes.c_void_p),
         ("record_drawn", ctypes.c_void_p),
         ("record_frame_mean", ctypes.c_void_p),
+        ("speculative", ctypes.c_int32),
     ]
 
 
@@ -79,6 +80,7 @@ class _ChunkOpts(ctypes.Structure):
         ("pipeline_encoder", ctypes.c_int32),
         ("use_graph", ctypes.c_int32),
         ("teacher", ctypes.POINTER(ctypes.c_int32)),
+        ("speculative", ctypes.c_int32),
     ]
 
 
@@ -139,6 +141,7 @@ class GenOptions:
     codebook_size: int = 1024
     codec_offset: int = 2
     use_graph: bool = True
+    speculative: bool = False
 
 
 _lib = None
@@ -443,7 +446,8 @@ class State:
                         temperature=opts.temperature, top_k=opts.top_k,
                         guidance_weight=opts.guidance_weight, seed=opts.seed & ((1 << 64) - 1),
                         codebook_size=opts.codebook_size, codec_offset=opts.codec_offset,
-                        teacher=None, use_graph=1 if opts.use_graph else 0)
+                        teacher=None, use_graph=1 if opts.use_graph else 0,
+                        speculative=1 if getattr(opts, "speculative", False) else 0)
 
     @staticmethod
     def _sync_torch() -> None:
@@ -483,6 +487,7 @@ class ChunkOptions:
     seed: Optional[int] = None
     pipeline_encoder: bool = False
     use_graph: bool = True
+    speculative: bool = False
 
 
 class Stream:
@@ -509,7 +514,8 @@ class Stream:
                        has_seed=0 if opts.seed is None else 1,
                        seed=0 if opts.seed is None else opts.seed & ((1 << 64) - 1),
                        pipeline_encoder=1 if opts.pipeline_encoder else 0,
-                       use_graph=1 if opts.use_graph else 0, teacher=None)
+                       use_graph=1 if opts.use_graph else 0, teacher=None,
+                       speculative=1 if opts.speculative else 0)
         keep = []
         if teacher is not None:
             tt = np.ascontiguousarray(teacher, dtype=np.int32)

@@ -1,0 +1,191 @@
+"""Speculative depth decoding (decode.cpp:150-237, 380-446) through the C ABI.
+
+The drafts of frame f are the previous call's tokens of frame f; one causal
+pass over the frame's 16 positions gives every level's logits, the drafts are
+accepted up to the first level whose draw differs, and the rest is decoded
+step by step.  Checks (bf16):
+  * every token is the oracle sampler's draw from the logits recorded for it
+    (per-(frame, level) noise, CFG, temperature, top-k);
+  * those logits match the oracle's decode teacher-forced with the same tokens
+    (norm-wise rel-err over all recorded logits <= 2e-2; single 1024-entry
+    slices carry bf16 rounding noise of the same size, up to ~2.1e-2 at the
+    benchmark dims): the verification pass, the depth K/V it leaves for the
+    continuation and the frame mean are right whatever was accepted;
+  * with drafts equal to a decode of the same chunk and seed, nearly every
+    draft is accepted and the tokens agree with it;
+  * the first call of a state (no drafts) and an fp32 model decode as usual.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+
+
+def rel(a, b):
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def tiny(gpu_available):
+    import mrt_df
+    import synth_bundle
+    from oracle import depthformer_oracle as O
+
+    cfg = mrt_df.Config.tiny()
+    w = synth_bundle.make_weights(cfg, seed=11, norm_jitter=0.1)
+    rng = np.random.default_rng(42)
+    S, C = cfg.max_encoder_length, 8
+    tok = np.zeros((2, S), dtype=np.int32)
+    tok[0, :S - 6] = 2 + C * (np.arange(S - 6) % 4) + rng.integers(0, C, S - 6)
+    tok[1, :S - 6] = tok[0, :S - 6]
+    tok[0, S - 6:] = 2 + 16 * C + C * np.arange(6) + rng.integers(0, C, 6)
+    tok[1, S - 6:] = 1
+    model = mrt_df.Depthformer(w, cfg, dtype="bf16")
+    yield dict(mrt_df=mrt_df, O=O, cfg=cfg, w=w, tok=tok, C=C, model=model,
+               ocfg=O.DepthformerConfig(**dataclasses.asdict(cfg)))
+    model.close()
+
+
+def _opts(mrt_df, F, C, seed, spec, **kw):
+    return mrt_df.GenOptions(num_frames=F, rvq_depth=16, temperature=kw.get("temperature", 1.1),
+                             top_k=kw.get("top_k", 4), guidance_weight=5.0, seed=seed, codebook_size=C,
+                             codec_offset=2, speculative=spec, use_graph=kw.get("use_graph", True))
+
+
+def _check_against_oracle(env, model_w, ocfg, enc_tokens, toks, sl, opts, mode="bf16"):
+    O = env["O"]
+    F, L, C = toks.shape[0], toks.shape[1], opts.codebook_size
+    exp = np.array([[2 + C * l + O.sample_level(O.cfg_combine(sl[f, l], opts.guidance_weight),
+                                                temperature=opts.temperature, top_k=opts.top_k, seed=opts.seed,
+                                                frame=f, level=l)
+                     for l in range(L)] for f in range(F)])
+    assert (toks == exp).mean() >= 0.99, (toks, exp)
+    om = O.OracleDepthformer(model_w, ocfg, mode=mode)
+    orec = {}
+    o = O.GenerateOptions(num_frames=F, rvq_depth=L, temperature=opts.temperature, top_k=opts.top_k,
+                          guidance_weight=opts.guidance_weight, seed=opts.seed, codebook_size=C, codec_offset=2)
+    O.generate_tokens(om, enc_tokens, o, teacher=toks, record=orec)
+    assert rel(sl, orec["slices"]) <= BF16_TOL
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_speculative_tiny(tiny, use_graph):
+    import torch
+    mrt_df = tiny["mrt_df"]
+    F, L, C = 4, 16, tiny["C"]
+    st = tiny["model"].new_state(max_frames=F)
+    # first call: no drafts, ordinary decode (one frame launch per frame)
+    first = st.generate_tokens(tiny["tok"], _opts(mrt_df, F, C, 7, True, use_graph=use_graph))
+    assert st.decode_time()[1] == F
+    # speculating with unrelated drafts (another seed): tokens from their own logits
+    rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"))
+    o2 = _opts(mrt_df, F, C, 8, True, use_graph=use_graph)
+    second = st.generate_tokens(None, o2, record=rec)
+    assert st.decode_time()[1] == F * L  # temporal step + 15 depth steps per frame
+    _check_against_oracle(tiny, tiny["w"], tiny["ocfg"], tiny["tok"], second, rec["slices"].cpu().numpy(), o2)
+    # drafts = a decode of the same chunk and seed: nearly all accepted
+    rec3 = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"))
+    third = st.generate_tokens(None, o2, record=rec3)
+    assert (third == second).mean() >= 0.9, (third, second)
+    _check_against_oracle(tiny, tiny["w"], tiny["ocfg"], tiny["tok"], third, rec3["slices"].cpu().numpy(), o2)
+    lo = 2 + C * np.arange(L)
+    for t in (first, second, third):
+        assert ((t >= lo) & (t < lo + C)).all()
+    st.close()
+
+
+def test_speculative_matches_plain_decode(tiny):
+    """Plain decode, then the same chunk and seed with speculation (drafts = the
+    plain tokens): the draws come from logits within bf16 rounding of the
+    plain ones, so the tokens agree almost everywhere."""
+    mrt_df = tiny["mrt_df"]
+    F, C = 4, tiny["C"]
+    st = tiny["model"].new_state(max_frames=F)
+    plain = st.generate_tokens(tiny["tok"], _opts(mrt_df, F, C, 21, False))
+    spec = st.generate_tokens(None, _opts(mrt_df, F, C, 21, True))
+    assert (spec == plain).mean() >= 0.9, (spec, plain)
+    st.close()
+
+
+def test_speculative_ignored_for_fp32(tiny):
+    import synth_bundle
+    mrt_df = tiny["mrt_df"]
+    m32 = mrt_df.Depthformer(synth_bundle.make_weights(tiny["cfg"], seed=11, norm_jitter=0.1), tiny["cfg"],
+                             dtype="fp32")
+    st = m32.new_state(max_frames=3)
+    a = st.generate_tokens(tiny["tok"], _opts(mrt_df, 3, tiny["C"], 5, False))
+    b = st.generate_tokens(None, _opts(mrt_df, 3, tiny["C"], 5, True))
+    np.testing.assert_array_equal(a, b)  # the same decode: no speculation on fp32
+    assert st.decode_time()[1] == 3
+    st.close()
+    m32.close()
+
+
+def _prefix(a, b):
+    """Per frame, the number of leading levels on which a and b agree."""
+    eq = a == b
+    return np.where(eq.all(axis=1), eq.shape[1], np.argmin(eq, axis=1))
+
+
+def test_speculative_full_size(gpu_available):
+    """Benchmark dims, two frames, bf16.
+
+    Call k + 1 (same seed, drafts = call k's tokens) verifies levels 0..n_k of
+    frame 0 from the same inputs as call k did (n_k = levels call k accepted),
+    on bit-identical verification rows, so it draws the same tokens there and
+    accepts at least n_k + 1 levels: the accepted prefix of frame 0 grows every
+    call until the whole chunk is a fixed point whose every level is accepted.
+    This holds exactly, whatever bf16 rounding does to single draws between
+    the verification pass and the depth steps.  The first call with unrelated
+    drafts and the fixed point are checked against the oracle sampler and the
+    oracle's teacher-forced logits."""
+    import torch
+    import mrt_df
+    import synth_bundle
+    import system
+    from oracle import depthformer_oracle as O
+
+    cfg = mrt_df.Config.bench()
+    w = synth_bundle.make_weights(cfg, seed=1234, threads=16)
+    model = mrt_df.Depthformer(w, cfg, dtype="bf16")
+    scfg = system.SystemConfig()
+    rng = np.random.default_rng(42)
+    ctx = rng.integers(0, 1024, size=(scfg.context_frames, 16)).astype(np.int32)
+    style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+    tok = system.build_encoder_inputs(ctx, scfg, style)
+    F, L, C = 2, 16, 1024
+    st = model.new_state(max_frames=F)
+    mk = lambda seed: mrt_df.GenOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40, guidance_weight=5.0,
+                                        seed=seed, codebook_size=C, codec_offset=2, speculative=True)
+    st.generate_tokens(tok, mk(3))
+    env = dict(O=O)
+    ocfg = O.DepthformerConfig(**dataclasses.asdict(cfg))
+    rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"))
+    prev = st.generate_tokens(None, mk(4), record=rec)  # drafts from seed 3
+    _check_against_oracle(env, w, ocfg, tok, prev, rec["slices"].cpu().numpy(), mk(4))
+    n_prev, fixed = -1, False
+    for k in range(2 * (L + 2)):
+        rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"))
+        toks = st.generate_tokens(None, mk(4), record=rec)
+        n = _prefix(toks, prev)
+        print(f"call {k}: accepted prefix per frame {n.tolist()}", flush=True)
+        if n_prev < L:
+            assert n[0] >= min(n_prev + 1, L), (k, n, n_prev)
+        n_prev = int(n[0])
+        if (toks == prev).all():
+            fixed = True
+            break
+        prev = toks
+    assert fixed, "repeated speculative calls reached no fixed point"
+    _check_against_oracle(env, w, ocfg, tok, toks, rec["slices"].cpu().numpy(), mk(4))
+    st.close()
+    model.close()
