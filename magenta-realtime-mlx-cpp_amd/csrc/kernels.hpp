@@ -83,7 +83,8 @@ struct SampleParams {
   const float* noise = nullptr;
   int noise_frames = 0;
   // Optional: levels <= *decided already have their token (speculative
-  // decoding); the sampler then does nothing for them.
+  // decoding); the sampler then only feeds emb(token) to next_in (no draw, no
+  // frame sum) and the depth step returns at once.
   const int* decided = nullptr;
 };
 

@@ -687,17 +687,18 @@ void State::enqueue_decode_spec(const GenOpts& o) {
     rmsnorm_rows(dt, sx_, m.dec_norm, 1e-6f, R2, D, sxn_, stream);
     bgemm_f32_grouped(sxn_, rows, D, head0, static_cast<long>(C) * D, C, slog_, C, L, stream);
     draw_levels(slog_, sp_all, f, L, sdrawn_, stream);
-    spec_accept(sdrawn_, d_drafts_ + static_cast<size_t>(f) * L, L, tok, sdecided_, stream);
+    spec_accept(dt, sdrawn_, d_drafts_ + static_cast<size_t>(f) * L, L, tok, sdecided_, m.emb, D, d_in, stream);
     float* rec = o.record_slices ? o.record_slices + static_cast<size_t>(f) * L * rows * C : nullptr;
     if (rec) spec_record(slog_, slice, sdecided_, 0, C, rec, stream);
-    // the levels after the first disagreement
+    // the levels after the first disagreement; a decided level's step and
+    // draw return at once, its draw feeding the known token on
     for (int l = 1; l < L; ++l) {
-      spec_feed(dt, tok, l, m.emb, D, d_in, stream);
       const char* head = head0 + static_cast<size_t>(C) * l * D * esz();
       StepArgs a = depth_args(d_in, l, head, C, slice, nullptr);
       a.sp = sp_rest;
       launch_step(dt, a, persist_grid_, lds_d_, stream);
-      sample_level(dt, slice, sp_rest, f, l, f * L + l, nullptr, d_tokens, nullptr, m.emb, D, x, fsum, sfm_, stream);
+      sample_level(dt, slice, sp_rest, f, l, f * L + l, nullptr, d_tokens, nullptr, m.emb, D, d_in, fsum, sfm_,
+                   stream);
       if (rec) spec_record(slog_, slice, sdecided_, l, C, rec + static_cast<size_t>(l) * rows * C, stream);
     }
     frame_mean_tokens(dt, tok, L, m.emb, D, t_in, stream);

@@ -196,13 +196,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int tid = threadIdx.x;
   const int stream = blockIdx.x;
   const int C = p.codebook, L = p.rvq_depth;
-  if (p.decided != nullptr && *p.decided >= level) return;  // the level's token is already known
   if (frame_ptr != nullptr) {
     frame = *frame_ptr;
     slot += frame * L;
   }
   slot += stream * tstride;
   T* ni = next_in + (size_t)(2 * stream) * D;
+  if (p.decided != nullptr && *p.decided >= level) {
+    // the level's token is already known: only feed it to the next depth step
+    // (the frame sum is not kept on this path)
+    const T* e = emb + (size_t)tokens[slot] * D;
+    for (int d = tid; d < D; d += 256) {
+      ni[d] = e[d];
+      ni[D + d] = e[d];
+    }
+    return;
+  }
   T* fs = fsum + (size_t)(2 * stream) * D;
   T* fm = fmean + (size_t)(2 * stream) * D;
   T fv[kFeedPer];

@@ -10,10 +10,10 @@ namespace mrt {
 void spec_inputs(DType dt, const void* t_out, const void* emb, const int* draft, int L, int D, void* out,
                  hipStream_t s);
 // Accept the drafts up to the first level whose draw differs (decode.cpp:
-// 225-236): tokens[0..n] = drawn[0..n], *decided = n (L: all accepted).
-void spec_accept(const int* drawn, const int* draft, int L, int* tokens, int* decided, hipStream_t s);
-// Both rows of out = emb(tokens[l - 1]).
-void spec_feed(DType dt, const int* tokens, int l, const void* emb, int D, void* out, hipStream_t s);
+// 225-236): tokens[0..n] = drawn[0..n], *decided = n (L: all accepted); both
+// rows of next_in = emb(drawn[0]), the input of depth step 1.
+void spec_accept(DType dt, const int* drawn, const int* draft, int L, int* tokens, int* decided, const void* emb,
+                 int D, void* next_in, hipStream_t s);
 // Frame mean of the L tokens' embeddings in the model dtype (decode.cpp:476-484), both rows.
 void frame_mean_tokens(DType dt, const int* tokens, int L, const void* emb, int D, void* out, hipStream_t s);
 // dst (2, C) = the logits level l was drawn from (the pass's rows 2l, 2l+1

@@ -26,28 +26,26 @@ __global__ void k_spec_inputs(const T* __restrict__ t_out, const T* __restrict__
 
 // decode.cpp:225-236: the first level whose draw differs from its draft ends
 // the accepted run and takes the draw; tokens[0..n] = drawn[0..n], *decided =
-// n (L when every draft was accepted).
-__global__ void k_spec_accept(const int* __restrict__ drawn, const int* __restrict__ draft, int L,
-                              int* __restrict__ tokens, int* __restrict__ decided) {
-  if (threadIdx.x != 0) return;
-  int n = L;
-  for (int i = 0; i < L; ++i)
-    if (drawn[i] != draft[i]) {
-      n = i;
-      break;
-    }
-  for (int i = 0; i <= n && i < L; ++i) tokens[i] = drawn[i];
-  *decided = n;
-}
-
-// Both rows of out = emb(tokens[l - 1]), the input of depth step l.
+// n (L when every draft was accepted).  Level 0's token is always decided:
+// both rows of next_in = emb(drawn[0]), the input of depth step 1.
 template <typename T>
-__global__ void k_spec_feed(const int* __restrict__ tokens, int l, const T* __restrict__ emb, int D,
-                            T* __restrict__ out) {
-  const T* src = emb + (size_t)tokens[l - 1] * D;
+__global__ void k_spec_accept(const int* __restrict__ drawn, const int* __restrict__ draft, int L,
+                              int* __restrict__ tokens, int* __restrict__ decided, const T* __restrict__ emb, int D,
+                              T* __restrict__ next_in) {
+  if (threadIdx.x == 0) {
+    int n = L;
+    for (int i = 0; i < L; ++i)
+      if (drawn[i] != draft[i]) {
+        n = i;
+        break;
+      }
+    for (int i = 0; i <= n && i < L; ++i) tokens[i] = drawn[i];
+    *decided = n;
+  }
+  const T* src = emb + (size_t)drawn[0] * D;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    out[d] = src[d];
-    out[D + d] = src[d];
+    next_in[d] = src[d];
+    next_in[D + d] = src[d];
   }
 }
 
@@ -88,16 +86,14 @@ void spec_inputs(DType dt, const void* t_out, const void* emb, const int* draft,
   MRT_HIP_CHECK(hipGetLastError());
 }
 
-void spec_accept(const int* drawn, const int* draft, int L, int* tokens, int* decided, hipStream_t s) {
-  hipLaunchKernelGGL(k_spec_accept, dim3(1), dim3(64), 0, s, drawn, draft, L, tokens, decided);
-  MRT_HIP_CHECK(hipGetLastError());
-}
-
-void spec_feed(DType dt, const int* tokens, int l, const void* emb, int D, void* out, hipStream_t s) {
+void spec_accept(DType dt, const int* drawn, const int* draft, int L, int* tokens, int* decided, const void* emb,
+                 int D, void* next_in, hipStream_t s) {
   if (dt == DType::F32)
-    hipLaunchKernelGGL(k_spec_feed<float>, dim3(1), dim3(256), 0, s, tokens, l, (const float*)emb, D, (float*)out);
+    hipLaunchKernelGGL(k_spec_accept<float>, dim3(1), dim3(256), 0, s, drawn, draft, L, tokens, decided,
+                       (const float*)emb, D, (float*)next_in);
   else
-    hipLaunchKernelGGL(k_spec_feed<bf16>, dim3(1), dim3(256), 0, s, tokens, l, (const bf16*)emb, D, (bf16*)out);
+    hipLaunchKernelGGL(k_spec_accept<bf16>, dim3(1), dim3(256), 0, s, drawn, draft, L, tokens, decided,
+                       (const bf16*)emb, D, (bf16*)next_in);
   MRT_HIP_CHECK(hipGetLastError());
 }
 
