@@ -12,8 +12,10 @@ Prints one JSON line: value = RVQ tokens/s (800 tokens per chunk / chunk
 seconds), plus chunk ms p50/p99, RTF, the HBM roofline of the decode and the
 CPU baseline (the numpy restatement timed on a bounded sample on this host).
 Beside it (not the headline value): 32 independent streams decoded as one
-batch (aggregate RVQ tokens/s, per-stream RTF) and the encoder prefill alone
-at 1 / 8 / 32 streams (matrix-core utilisation); --no-batched skips them.
+batch (aggregate RVQ tokens/s, per-stream RTF), the encoder prefill alone
+at 1 / 8 / 32 streams (matrix-core utilisation) and the decode section with
+speculative depth decoding at rejected and at accepted drafts; --no-batched
+skips them.
 """
 
 from __future__ import annotations
@@ -234,6 +236,60 @@ def bench_batched(model, cfg, streams=32, chunks=3, seed=1234):
     return res
 
 
+def bench_speculative(model, cfg, enc, reps=3, seed=1234):
+    """Speculative depth decoding (opt-in): the decode section of one 50-frame
+    chunk, plain against speculative with drafts that are rejected (each call a
+    new seed: the drafts are an unrelated chunk's tokens) and with drafts that
+    are all accepted (the same seed repeated until the tokens reach a fixed
+    point).  GPU ms from the state's own HIP events."""
+    import mrt_df
+    F, L = 50, 16
+    st = model.new_state(max_frames=F)
+    mk = lambda s, spec: mrt_df.GenOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40,
+                                           guidance_weight=5.0, seed=s, codebook_size=1024, codec_offset=2,
+                                           speculative=spec, use_graph=True)
+    prev = st.generate_tokens(enc, mk(seed, False))
+
+    def prefix(a, b):
+        eq = a == b
+        return np.where(eq.all(axis=1), L, np.argmin(eq, axis=1))
+
+    plain = []
+    for _ in range(reps):
+        st.generate_tokens(None, mk(seed, False))
+        plain.append(st.decode_time()[0])
+    rej, acc = [], []
+    for r in range(reps + 1):
+        t = st.generate_tokens(None, mk(seed + 1 + r, True))
+        if r > 0:  # the first call of a new graph key captures
+            rej.append(st.decode_time()[0])
+            acc.append(float(np.minimum(prefix(t, prev) + 1, L).mean()) / L)
+        prev = t
+    calls = 0
+    while calls < 4 * L:
+        t = st.generate_tokens(None, mk(seed, True))
+        calls += 1
+        if (t == prev).all():
+            break
+        prev = t
+    fixed = bool((t == prev).all())
+    full = []
+    for _ in range(reps):
+        st.generate_tokens(None, mk(seed, True))
+        full.append(st.decode_time()[0])
+    st.close()
+    res = {"plain_decode_ms": float(np.mean(plain)),
+           "rejected_drafts": {"decode_ms": float(np.mean(rej)), "levels_from_verification": float(np.mean(acc))},
+           "accepted_drafts": {"decode_ms": float(np.mean(full)), "fixed_point": fixed,
+                               "calls_to_fixed_point": calls},
+           "note": "decode section only (encoder excluded); levels_from_verification = share of levels whose "
+                   "token came from the verification pass (accepted drafts + the first disagreement)"}
+    print(f"[bench] speculative: plain {res['plain_decode_ms']:.1f} ms, rejected drafts "
+          f"{res['rejected_drafts']['decode_ms']:.1f} ms, accepted drafts {res['accepted_drafts']['decode_ms']:.1f} ms "
+          f"(fixed point after {calls} calls)", file=sys.stderr, flush=True)
+    return res
+
+
 def bench_encoder(model, cfg, batches=(1, 8, 32), reps=3):
     """Encoder prefill alone over 2 x batch x 1006 token rows (CFG pairs): ms and
     matrix-core utilisation against the dense bf16 peak."""
@@ -326,7 +382,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--no-batched", action="store_true", help="skip the 32-stream and encoder-prefill figures")
+    ap.add_argument("--no-batched", action="store_true", help="skip the 32-stream, encoder-prefill and speculative figures")
     ap.add_argument("--session", default="device", choices=["device", "host"],
                     help="device: RVQ context on the device, next chunk's encoder enqueued early; "
                          "host: context on the host, encoder ids uploaded per chunk")
@@ -421,10 +477,11 @@ def main():
                 "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
                 "launches_timed": dk["launches"]}
 
-    batched = encoder = None
+    batched = encoder = spec = None
     if not args.no_batched and args.dtype == "bf16":
         batched = bench_batched(model, cfg)
         encoder = bench_encoder(model, cfg)
+        spec = bench_speculative(model, cfg, system.build_encoder_inputs(sess.context, scfg, style))
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -466,6 +523,7 @@ def main():
                                  "by_cache_len": lens["temporal"]},
         "batched_streams": batched,
         "encoder_prefill": encoder,
+        "speculative": spec,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -82,8 +82,9 @@ typedef struct mrt_gen_opts {
    * one causal pass over the frame's 16 positions, accepted up to the first
    * disagreement (whose draw is the token), the rest decoded as usual.  The
    * tokens are those of the same draws from the same logits.  bf16 models on
-   * the persistent path; ignored on a state's first call, with a teacher, or
-   * with record_drawn / record_frame_mean. */
+   * the persistent path; ignored (plain decode) on a state's
+   * first call, when num_frames differs from the previous call's, with a
+   * teacher, or with record_drawn / record_frame_mean. */
   int32_t speculative;
 } mrt_gen_opts;
 
@@ -143,7 +144,8 @@ int mrt_df_temporal_step(mrt_df_state* st, const void* frame_emb, const void* en
 int mrt_df_depth_step(mrt_df_state* st, const void* tok_emb, int depth_idx, int level,
                       int codebook_size, int codec_offset, float* logits);
 
-/* generate_tokens (depthformer/decode.cpp:239-573), non-speculative path:
+/* generate_tokens (depthformer/decode.cpp:239-573), with the speculative
+ * path of decode.cpp:380-446 when opts->speculative applies:
  * enc_tokens (rows, enc_len) host int32 (NULL: reuse the last encode) ->
  * out_tokens (num_frames, rvq_depth) host int32 LLM ids.  CFG, level mask,
  * temperature/top-k sampling, token feedback and the frame mean all run on
