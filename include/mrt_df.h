@@ -298,6 +298,65 @@ int mrt_df_batch_decode_time(mrt_df_batch* b, float* ms);
  * dtype) into dst, for parity checks. */
 int mrt_df_batch_read_enc_out(mrt_df_batch* b, void* dst, size_t bytes);
 
+/* ------------------------------------------------------------------------
+ * Codec decode: the audio half of System::generate_chunk (system.cpp:
+ * 373-390): rvq_dequantization (rvq.cpp:68-88) with the SpectroStream
+ * codebooks, SpectroStreamDecoder::operator() (spectrostream.cpp:365-432)
+ * and istft_postprocess (spectrostream.cpp:593-681), all in fp32 as the
+ * reference runs them (system.cpp:118-119).
+ * ------------------------------------------------------------------------ */
+typedef struct mrt_codec mrt_codec;
+
+typedef struct {
+  int32_t embedding_dim;   /* 256: SpectroStreamDecoder::kEmbeddingDim */
+  int32_t proj_channels;   /* 2560: input_proj 256 -> 2560 -> 2560 (spectrostream.cpp:356-362) */
+  int32_t unfold;          /* 5: unfold_width factor (2560 = 5 x 512) */
+  int32_t block_in[7];     /* decoder block channels (spectrostream.cpp:328-338); the */
+  int32_t block_out[7];    /*   strides, kernels and crops are the reference's */
+  int32_t rvq_levels;      /* 16: codebooks summed per frame */
+  int32_t codebook_size;   /* 1024 */
+  int32_t max_frames;      /* largest decode the handle serves (51 = 1 crossfade + 50) */
+} mrt_codec_config;
+
+#define MRT_CODEC_BUF_EMB 0         /* (frames + 1, 256) dequantised embeddings + the zero pad frame */
+#define MRT_CODEC_BUF_INPUT_CONV 1  /* (1, frames + 1, 5, 512) after input_proj + input_conv */
+#define MRT_CODEC_BUF_BLOCK0 2      /* 2..8: decoder block i output, (2, H, W, C) after block 0's stereo split */
+#define MRT_CODEC_BUF_SPEC 9        /* (2, 4 frames, 480, 2): stereo half s, (real, imag) -- the decoder
+                                       output before the (B, H, 480, 4) interleave */
+#define MRT_CODEC_BUF_FRAMES 10     /* (2 x 4 frames, 960) windowed iSTFT frames */
+
+/* The reference's decoder configuration (SpectroStreamDecoder, the decoder
+ * block table and SystemConfig's 1 crossfade frame + 50 chunk frames). */
+void mrt_codec_config_default(mrt_codec_config* cfg);
+/* SpectroStreamDecoder(bundle, float32) (spectrostream.cpp:356-362) from
+ * spectrostream_decoder.safetensors plus the "codebooks" tensor (K, C, 256)
+ * of spectrostream_codebooks.safetensors (weights.cpp:80-83; system.cpp:
+ * 105-119).  Conv weights (out, in, kH, kW), transposed-conv weights (in,
+ * out, kH, kW), as stored. */
+int mrt_codec_create(const char* decoder_path, const char* codebooks_path, const mrt_codec_config* cfg, int device,
+                     mrt_codec** out);
+/* The same from caller-owned fp32 host arrays (decoder keys and "codebooks"). */
+int mrt_codec_create_from_tensors(int n, const char* const* names, const float* const* data,
+                                  const int64_t* const* shapes, const int32_t* ndims, const mrt_codec_config* cfg,
+                                  int device, mrt_codec** out);
+void mrt_codec_destroy(mrt_codec* c);
+/* system.cpp:373-390: rvq_tokens host (frames, rvq_levels) int32 in [0,
+ * codebook_size) -> audio host (frames * 1920, 2) float32, L/R interleaved
+ * (istft_postprocess with target length frames * 48000 / 25).  Ids outside
+ * the codebook return MRT_ERR_INVALID before any device work. */
+int mrt_codec_decode(mrt_codec* c, const int32_t* rvq_tokens, int frames, float* audio);
+/* The same on device pointers, enqueued on the codec's stream without a host
+ * sync (ids outside the codebook are read as 0). */
+int mrt_codec_decode_device(mrt_codec* c, const int32_t* rvq_tokens_dev, int frames, float* audio_dev);
+/* The codec's hipStream_t, a wait for its work, and the GPU ms of the last
+ * decode (HIP events on its stream). */
+int mrt_codec_stream(mrt_codec* c, void** hip_stream);
+int mrt_codec_sync(mrt_codec* c);
+int mrt_codec_decode_time(mrt_codec* c, float* ms);
+/* Copy of an intermediate of the last decode (MRT_CODEC_BUF_*); bytes must
+ * equal its size at that decode's frame count. */
+int mrt_codec_read(mrt_codec* c, int which, void* dst, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,10 +27,12 @@ SOURCES = [
     "stream_kernels.hip",
     "batch_kernels.hip",
     "spec_kernels.hip",
+    "codec_kernels.hip",
     "safetensors.cpp",
     "model.cpp",
     "stream.cpp",
     "batch.cpp",
+    "codec.cpp",
     "api.cpp",
 ]
 

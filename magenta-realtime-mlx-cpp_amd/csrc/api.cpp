@@ -7,6 +7,7 @@
 #include <string>
 
 #include "batch.hpp"
+#include "codec.hpp"
 #include "model.hpp"
 #include "stream.hpp"
 
@@ -22,6 +23,10 @@ struct mrt_df_state {
 
 struct mrt_df_batch {
   std::unique_ptr<mrt::Batch> batch;
+};
+
+struct mrt_codec {
+  std::unique_ptr<mrt::Codec> codec;
 };
 
 struct mrt_df_stream {
@@ -127,6 +132,27 @@ mrt::Batch& BB(mrt_df_batch* b) {
 mrt::Stream& SS(mrt_df_stream* s) {
   if (!s || !s->stream) throw mrt::Error(MRT_ERR_INVALID, "null stream handle");
   return *s->stream;
+}
+
+mrt::Codec& CC(mrt_codec* c) {
+  if (!c || !c->codec) throw mrt::Error(MRT_ERR_INVALID, "null codec handle");
+  return *c->codec;
+}
+
+mrt::CodecConfig to_codec_config(const mrt_codec_config* c, int* max_frames) {
+  mrt::CodecConfig k;
+  k.embedding_dim = c->embedding_dim;
+  k.proj_ch = c->proj_channels;
+  k.unfold = c->unfold;
+  for (int i = 0; i < 7; ++i) {
+    k.blocks[i].in_ch = c->block_in[i];
+    k.blocks[i].out_ch = c->block_out[i];
+  }
+  k.levels = c->rvq_levels;
+  k.codebook = c->codebook_size;
+  if (k.levels < 1 || k.codebook < 1) throw mrt::Error(MRT_ERR_INVALID, "codec: rvq_levels and codebook_size must be >= 1");
+  *max_frames = c->max_frames;
+  return k;
 }
 
 mrt::StreamConfig to_stream_config(const mrt_stream_config* c) {
@@ -433,6 +459,93 @@ int mrt_df_batch_read_enc_out(mrt_df_batch* b, void* dst, size_t bytes) {
     if (bytes != n) throw mrt::Error(MRT_ERR_INVALID, "batch_read_enc_out: size mismatch (" + std::to_string(n) + " bytes)");
     MRT_HIP_CHECK(hipMemcpyAsync(dst, bt.enc_out(), n, hipMemcpyDeviceToDevice, bt.stream));
     MRT_HIP_CHECK(hipStreamSynchronize(bt.stream));
+  });
+}
+
+void mrt_codec_config_default(mrt_codec_config* cfg) {
+  if (!cfg) return;
+  const mrt::CodecConfig k;
+  cfg->embedding_dim = k.embedding_dim;
+  cfg->proj_channels = k.proj_ch;
+  cfg->unfold = k.unfold;
+  for (int i = 0; i < 7; ++i) {
+    cfg->block_in[i] = k.blocks[i].in_ch;
+    cfg->block_out[i] = k.blocks[i].out_ch;
+  }
+  cfg->rvq_levels = k.levels;
+  cfg->codebook_size = k.codebook;
+  cfg->max_frames = 51;
+}
+
+int mrt_codec_create(const char* decoder_path, const char* codebooks_path, const mrt_codec_config* cfg, int device,
+                     mrt_codec** out) {
+  return guarded([&] {
+    if (!decoder_path || !codebooks_path || !cfg || !out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *out = nullptr;
+    int maxf = 0;
+    const mrt::CodecConfig k = to_codec_config(cfg, &maxf);
+    mrt::SafetensorsFile dec(decoder_path), cbs(codebooks_path);
+    auto h = std::make_unique<mrt_codec>();
+    h->codec = std::make_unique<mrt::Codec>(dec, cbs, k, device, maxf);
+    *out = h.release();
+  });
+}
+
+int mrt_codec_create_from_tensors(int n, const char* const* names, const float* const* data,
+                                  const int64_t* const* shapes, const int32_t* ndims, const mrt_codec_config* cfg,
+                                  int device, mrt_codec** out) {
+  return guarded([&] {
+    if (!names || !data || !shapes || !ndims || !cfg || !out || n < 0)
+      throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *out = nullptr;
+    int maxf = 0;
+    const mrt::CodecConfig k = to_codec_config(cfg, &maxf);
+    mrt::TensorList src;
+    for (int i = 0; i < n; ++i) {
+      if (!names[i] || !data[i] || ndims[i] < 0) throw mrt::Error(MRT_ERR_INVALID, "bad tensor entry");
+      src.add(names[i], data[i], std::vector<int64_t>(shapes[i], shapes[i] + ndims[i]));
+    }
+    auto h = std::make_unique<mrt_codec>();
+    h->codec = std::make_unique<mrt::Codec>(src, src, k, device, maxf);
+    *out = h.release();
+  });
+}
+
+void mrt_codec_destroy(mrt_codec* c) { delete c; }
+
+int mrt_codec_decode(mrt_codec* c, const int32_t* rvq_tokens, int frames, float* audio) {
+  return guarded([&] { CC(c).decode(rvq_tokens, frames, audio); });
+}
+
+int mrt_codec_decode_device(mrt_codec* c, const int32_t* rvq_tokens_dev, int frames, float* audio_dev) {
+  return guarded([&] { CC(c).decode_device(rvq_tokens_dev, frames, audio_dev); });
+}
+
+int mrt_codec_stream(mrt_codec* c, void** hip_stream) {
+  return guarded([&] {
+    if (!hip_stream) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *hip_stream = CC(c).stream;
+  });
+}
+
+int mrt_codec_sync(mrt_codec* c) {
+  return guarded([&] { MRT_HIP_CHECK(hipStreamSynchronize(CC(c).stream)); });
+}
+
+int mrt_codec_decode_time(mrt_codec* c, float* ms) {
+  return guarded([&] {
+    if (!ms) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *ms = CC(c).last_ms();
+  });
+}
+
+int mrt_codec_read(mrt_codec* c, int which, void* dst, size_t bytes) {
+  return guarded([&] {
+    if (!dst) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    auto [src, n] = CC(c).buffer(which);
+    if (bytes != n) throw mrt::Error(MRT_ERR_INVALID, "codec_read: size mismatch (" + std::to_string(n) + " bytes)");
+    MRT_HIP_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDefault, CC(c).stream));
+    MRT_HIP_CHECK(hipStreamSynchronize(CC(c).stream));
   });
 }
 

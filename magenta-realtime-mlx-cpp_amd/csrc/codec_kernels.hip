@@ -1,0 +1,211 @@
+// Codec decode kernels (fp32): the implicit-GEMM convolution on the matrix
+// cores, RVQ dequantisation and the iSTFT overlap-add.
+//
+// k_conv: a 64 x 64 output tile (pixels x channels) per 256-thread
+// workgroup, 4 waves in a 2 x 2 grid, each wave 2 x 2 tiles of
+// v_mfma_f32_16x16x4_f32.  The K loop runs over (tap, KC-channel chunk);
+// each chunk's A rows (the tap's input pixel for every output pixel of the
+// tile, zero outside the input, ELU applied on load when asked) and B rows
+// (packed weights) are staged through a double-buffered LDS with one barrier
+// per chunk, the next chunk's global loads in flight while the current one
+// is multiplied.  LDS strides: A rows KC + 4 floats (the 16 rows x 4 k lanes of
+// an A fragment hit 64 distinct banks), B rows 80 floats (the same for B).
+#include "codec.hpp"
+
+namespace mrt {
+namespace {
+
+constexpr int kBM = 64, kBN = 64, kThreads = 256;
+
+__device__ __forceinline__ float elu1(float v) { return v > 0.f ? v : expf(v) - 1.f; }
+
+template <int KC>
+__global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
+  constexpr int AS = KC + 4;
+  constexpr int BS = kBN + 16;
+  constexpr int CPR = KC / 4;            // float4 chunks per A row
+  constexpr int RPP = kThreads / CPR;    // A rows per load pass
+  constexpr int APASS = kBM / RPP;       // A loads per thread
+  constexpr int BPASS = KC * (kBN / 4) / kThreads;  // B loads per thread
+  static_assert(kBM % RPP == 0 && BPASS >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) float As[2][kBM * AS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][KC * BS];
+
+  int si = 0;
+  while (si + 1 < a.nsub && (int)blockIdx.x >= a.subs[si + 1].tile0) ++si;
+  const ConvSub* sub = a.subs + si;
+  const int gy = sub->gy, gx = sub->gx, ntaps = sub->ntaps;
+  const int M = a.n * gy * gx;
+  const int m0 = ((int)blockIdx.x - sub->tile0) * kBM;
+  const int n0 = (int)blockIdx.y * kBN;
+  const float* __restrict__ W = sub->w;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+
+  // this thread's A rows: image offset and grid coordinates
+  int a_img[APASS], a_y[APASS], a_x[APASS];
+  const int a_chunk = tid % CPR;
+#pragma unroll
+  for (int p = 0; p < APASS; ++p) {
+    const int m = min(m0 + tid / CPR + p * RPP, M - 1);
+    const int img = m / (gy * gx), r = m - img * gy * gx;
+    a_img[p] = img * a.hin;
+    a_y[p] = r / gx;
+    a_x[p] = r - (r / gx) * gx;
+  }
+  const int b_col = (tid % (kBN / 4)) * 4;
+  const int b_row = tid / (kBN / 4);
+
+  const int cpt = a.cin / KC;
+  const int nk = ntaps * cpt;
+  float ra[APASS][4], rb[BPASS][4];
+
+  auto load = [&](int kc) {
+    const int t = kc / cpt, c0 = (kc - t * cpt) * KC + a_chunk * 4;
+    const int dy = sub->dy[t], dx = sub->dx[t];
+#pragma unroll
+    for (int p = 0; p < APASS; ++p) {
+      const int iy = a_y[p] + dy, ix = a_x[p] + dx;
+      const bool ok = iy >= 0 && iy < a.hin && ix >= 0 && ix < a.win;
+      const int cy = ok ? iy : 0, cx = ok ? ix : 0;
+      const float4 v = *reinterpret_cast<const float4*>(a.x + ((size_t)(a_img[p] + cy) * a.win + cx) * a.cin + c0);
+      ra[p][0] = ok ? v.x : 0.f;
+      ra[p][1] = ok ? v.y : 0.f;
+      ra[p][2] = ok ? v.z : 0.f;
+      ra[p][3] = ok ? v.w : 0.f;
+    }
+    const float* wb = W + ((size_t)t * a.cin + (kc - t * cpt) * KC) * a.cout_pad + n0 + b_col;
+#pragma unroll
+    for (int p = 0; p < BPASS; ++p) {
+      const float4 v = *reinterpret_cast<const float4*>(wb + (size_t)(b_row + p * (kThreads / (kBN / 4))) * a.cout_pad);
+      rb[p][0] = v.x;
+      rb[p][1] = v.y;
+      rb[p][2] = v.z;
+      rb[p][3] = v.w;
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < APASS; ++p) {
+      float4 v = make_float4(ra[p][0], ra[p][1], ra[p][2], ra[p][3]);
+      if (a.elu_in) {  // zero padding stays 0 (elu(0) = 0)
+        v.x = elu1(v.x);
+        v.y = elu1(v.y);
+        v.z = elu1(v.z);
+        v.w = elu1(v.w);
+      }
+      *reinterpret_cast<float4*>(&As[buf][(tid / CPR + p * RPP) * AS + a_chunk * 4]) = v;
+    }
+#pragma unroll
+    for (int p = 0; p < BPASS; ++p)
+      *reinterpret_cast<float4*>(&Bs[buf][(b_row + p * (kThreads / (kBN / 4))) * BS + b_col]) =
+          make_float4(rb[p][0], rb[p][1], rb[p][2], rb[p][3]);
+  };
+
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  f4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  load(0);
+  store(0);
+  __syncthreads();
+  const int lr = lane & 15, lk = lane >> 4;
+  for (int kc = 0; kc < nk; ++kc) {
+    const int buf = kc & 1;
+    if (kc + 1 < nk) load(kc + 1);
+    const float* Ab = As[buf] + (wm * 32 + lr) * AS + lk;
+    const float* Bb = Bs[buf] + lk * BS + wn * 32 + lr;
+#pragma unroll
+    for (int ks = 0; ks < KC / 4; ++ks) {
+      const float a0 = Ab[ks * 4], a1 = Ab[16 * AS + ks * 4];
+      const float b0 = Bb[ks * 4 * BS], b1 = Bb[ks * 4 * BS + 16];
+      acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
+      acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
+      acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
+      acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+    }
+    if (kc + 1 < nk) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows 4 * (lane / 16) + v, column lane % 16 of each tile
+#pragma unroll
+  for (int tm = 0; tm < 2; ++tm) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = m0 + wm * 32 + tm * 16 + 4 * lk + v;
+      if (m >= M) continue;
+      const int img = m / (gy * gx), r = m - img * gy * gx;
+      const int yy = r / gx, xx = r - (r / gx) * gx;
+      const int oy = yy * sub->oys + sub->oyo, ox = xx * sub->oxs + sub->oxo;
+#pragma unroll
+      for (int tn = 0; tn < 2; ++tn) {
+        const int o = n0 + wn * 32 + tn * 16 + lr;
+        if (o >= a.cout) continue;
+        float val = acc[tm][tn][v];
+        if (a.bias) val += a.bias[o];
+        if (a.res)
+          val += a.res[((size_t)(img * a.res_h + oy / a.rh) * a.res_w + ox / a.rw) * a.cout + o];
+        if (a.elu_out) val = elu1(val);
+        const int oi = (o / a.split) * a.n + img, oc = o - (o / a.split) * a.split;
+        a.y[((size_t)(oi * a.hout + oy) * a.wout + ox) * a.split + oc] = val;
+      }
+    }
+  }
+}
+
+__global__ void k_rvq_dequant(const int* __restrict__ tokens, int frames, int levels,
+                              const float* __restrict__ cb, int codebook, int dim, float* __restrict__ emb) {
+  const int f = blockIdx.x;
+  for (int d = threadIdx.x; d < dim; d += blockDim.x) {
+    float s = 0.f;
+    if (f < frames) {
+      for (int k = 0; k < levels; ++k) {
+        int id = tokens[f * levels + k];
+        if (id < 0 || id >= codebook) id = 0;
+        s = s + cb[((size_t)k * codebook + id) * dim + d];
+      }
+    }
+    emb[(size_t)f * dim + d] = s;
+  }
+}
+
+__global__ void k_overlap_add(const float* __restrict__ wf, int H, int n_fft, int T, float* __restrict__ audio) {
+  const int hop = n_fft / 2;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 2 * T) return;
+  const int t = i >> 1, s = i & 1;
+  const int f = t / hop, j = t - f * hop;
+  float v = 0.f;
+  if (f < H) v = wf[(size_t)(s * H + f) * n_fft + j];
+  if (f >= 1 && f - 1 < H) v += wf[(size_t)(s * H + f - 1) * n_fft + hop + j];
+  audio[i] = v;
+}
+
+}  // namespace
+
+void conv_launch(const ConvLaunch& a, int tiles_m, int tiles_n, hipStream_t s) {
+  if (a.cin % 32 == 0)
+    hipLaunchKernelGGL(k_conv<32>, dim3(tiles_m, tiles_n), dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(k_conv<16>, dim3(tiles_m, tiles_n), dim3(kThreads), 0, s, a);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void rvq_dequant(const int* tokens, int frames, int levels, const float* codebooks, int codebook, int dim, int pad,
+                 float* emb, hipStream_t s) {
+  hipLaunchKernelGGL(k_rvq_dequant, dim3(frames + pad), dim3(256), 0, s, tokens, frames, levels, codebooks, codebook,
+                     dim, emb);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void overlap_add(const float* wf, int H, int n_fft, int T, float* audio, hipStream_t s) {
+  const int n = 2 * T;
+  hipLaunchKernelGGL(k_overlap_add, dim3((n + 255) / 256), dim3(256), 0, s, wf, H, n_fft, T, audio);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace mrt

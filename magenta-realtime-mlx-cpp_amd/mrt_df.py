@@ -84,6 +84,22 @@ class _ChunkOpts(ctypes.Structure):
     ]
 
 
+class _CodecConfig(ctypes.Structure):
+    _fields_ = [
+        ("embedding_dim", ctypes.c_int32),
+        ("proj_channels", ctypes.c_int32),
+        ("unfold", ctypes.c_int32),
+        ("block_in", ctypes.c_int32 * 7),
+        ("block_out", ctypes.c_int32 * 7),
+        ("rvq_levels", ctypes.c_int32),
+        ("codebook_size", ctypes.c_int32),
+        ("max_frames", ctypes.c_int32),
+    ]
+
+
+CODEC_BUF_EMB, CODEC_BUF_INPUT_CONV, CODEC_BUF_BLOCK0, CODEC_BUF_SPEC, CODEC_BUF_FRAMES = 0, 1, 2, 9, 10
+
+
 @dataclasses.dataclass(frozen=True)
 class Config:
     """DepthformerConfig (model.h:47-68)."""
@@ -206,6 +222,19 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_batch_stream": (i32, [vp, ctypes.POINTER(vp)]),
         "mrt_df_batch_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
         "mrt_df_batch_read_enc_out": (i32, [vp, vp, sz]),
+        "mrt_codec_config_default": (None, [ctypes.POINTER(_CodecConfig)]),
+        "mrt_codec_create": (i32, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_CodecConfig), i32,
+                                   ctypes.POINTER(vp)]),
+        "mrt_codec_create_from_tensors": (i32, [i32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(vp),
+                                                ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_int32),
+                                                ctypes.POINTER(_CodecConfig), i32, ctypes.POINTER(vp)]),
+        "mrt_codec_destroy": (None, [vp]),
+        "mrt_codec_decode": (i32, [vp, ctypes.POINTER(ctypes.c_int32), i32, ctypes.POINTER(ctypes.c_float)]),
+        "mrt_codec_decode_device": (i32, [vp, vp, i32, vp]),
+        "mrt_codec_stream": (i32, [vp, ctypes.POINTER(vp)]),
+        "mrt_codec_sync": (i32, [vp]),
+        "mrt_codec_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
+        "mrt_codec_read": (i32, [vp, i32, vp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -635,6 +664,95 @@ class Batch:
     def close(self) -> None:
         if getattr(self, "_h", None):
             self.lib.mrt_df_batch_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+
+def _tensor_list(weights):
+    names, arrays = [], []
+    for k, v in weights.items():
+        names.append(k.encode())
+        arrays.append(np.ascontiguousarray(v, dtype=np.float32))
+    n = len(names)
+    shapes = [np.asarray(a.shape, dtype=np.int64) for a in arrays]
+    keep = (arrays, shapes)
+    return (n, (ctypes.c_char_p * n)(*names), (ctypes.c_void_p * n)(*[a.ctypes.data for a in arrays]),
+            (ctypes.c_void_p * n)(*[x.ctypes.data for x in shapes]), (ctypes.c_int32 * n)(*[a.ndim for a in arrays]),
+            keep)
+
+
+class Codec:
+    """Codec decode on the device (system.cpp:373-390): RVQ ids (frames, 16)
+    -> rvq_dequantization -> SpectroStreamDecoder -> istft_postprocess ->
+    stereo audio (frames * 1920, 2) float32 at 48 kHz.
+
+    ``weights``: a dict holding the decoder keys and "codebooks", or a pair of
+    paths (spectrostream_decoder.safetensors, spectrostream_codebooks.safetensors).
+    ``channels``: optional (embedding_dim, proj_channels, block_in, block_out)
+    for a reduced test decoder; the default is the reference's."""
+
+    def __init__(self, weights, max_frames: int = 51, device: int = 0, channels=None, rvq_levels: int = 16,
+                 codebook_size: int = 1024):
+        self.lib = load_library()
+        cfg = _CodecConfig()
+        self.lib.mrt_codec_config_default(ctypes.byref(cfg))
+        if channels is not None:
+            e, p, bi, bo = channels
+            cfg.embedding_dim, cfg.proj_channels = e, p
+            for i in range(7):
+                cfg.block_in[i], cfg.block_out[i] = bi[i], bo[i]
+        cfg.rvq_levels, cfg.codebook_size, cfg.max_frames = rvq_levels, codebook_size, max_frames
+        self.max_frames, self.levels = max_frames, rvq_levels
+        h = ctypes.c_void_p()
+        if isinstance(weights, (tuple, list)):
+            _check(self.lib, self.lib.mrt_codec_create(str(weights[0]).encode(), str(weights[1]).encode(),
+                                                       ctypes.byref(cfg), device, ctypes.byref(h)))
+        else:
+            n, c_names, c_data, c_shapes, c_nd, _keep = _tensor_list(weights)
+            _check(self.lib, self.lib.mrt_codec_create_from_tensors(n, c_names, c_data, c_shapes, c_nd,
+                                                                    ctypes.byref(cfg), device, ctypes.byref(h)))
+        self._h = h
+
+    def decode(self, rvq_tokens: np.ndarray) -> np.ndarray:
+        tok = np.ascontiguousarray(rvq_tokens, dtype=np.int32)
+        if tok.ndim != 2 or tok.shape[1] != self.levels:
+            raise ValueError(f"rvq_tokens must be (frames, {self.levels})")
+        out = np.empty((tok.shape[0] * 1920, 2), dtype=np.float32)
+        _check(self.lib, self.lib.mrt_codec_decode(self._h, _i32_ptr(tok), tok.shape[0],
+                                                   out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return out
+
+    def decode_device(self, tokens_dev, audio_dev) -> None:
+        """Device tensors: tokens (frames, levels) int32, audio (frames * 1920, 2) float32."""
+        _check(self.lib, self.lib.mrt_codec_decode_device(self._h, _dptr(tokens_dev), int(tokens_dev.shape[0]),
+                                                          _dptr(audio_dev)))
+
+    def sync(self) -> None:
+        _check(self.lib, self.lib.mrt_codec_sync(self._h))
+
+    def stream_handle(self) -> int:
+        s = ctypes.c_void_p()
+        _check(self.lib, self.lib.mrt_codec_stream(self._h, ctypes.byref(s)))
+        return int(s.value or 0)
+
+    def decode_time(self) -> float:
+        ms = ctypes.c_float()
+        _check(self.lib, self.lib.mrt_codec_decode_time(self._h, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def read(self, which: int, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=np.float32)
+        _check(self.lib, self.lib.mrt_codec_read(self._h, which, ctypes.c_void_p(out.ctypes.data), out.nbytes))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.mrt_codec_destroy(self._h)
             self._h = None
 
     def __del__(self):
