@@ -13,9 +13,10 @@ seconds), plus chunk ms p50/p99, RTF, the HBM roofline of the decode and the
 CPU baseline (the numpy restatement timed on a bounded sample on this host).
 Beside it (not the headline value): 32 independent streams decoded as one
 batch (aggregate RVQ tokens/s, per-stream RTF), the encoder prefill alone
-at 1 / 8 / 32 streams (matrix-core utilisation) and the decode section with
-speculative depth decoding at rejected and at accepted drafts; --no-batched
-skips them.
+at 1 / 8 / 32 streams (matrix-core utilisation), the decode section with
+speculative depth decoding at rejected and at accepted drafts, and the codec
+decode of one chunk (RVQ ids -> audio, fp32 matrix-core utilisation);
+--no-batched skips them.
 """
 
 from __future__ import annotations
@@ -37,6 +38,7 @@ for p in (ROOT, PKG):
 
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 matrix-core peak of MI355X
+MFMA_FP32_PEAK_TFLOPS = 157.3   # dense fp32 matrix-core peak of MI355X
 
 
 def percentile(sorted_vals, p):
@@ -290,6 +292,46 @@ def bench_speculative(model, cfg, enc, reps=3, seed=1234):
     return res
 
 
+def bench_codec(reps=10, frames=51, cpu=True):
+    """Codec decode of one chunk (system.cpp:373-390): 1 crossfade frame + 50
+    frames of RVQ ids -> dequantisation -> SpectroStream decoder -> iSTFT ->
+    97920 stereo samples, fp32 with seeded synthetic codec weights.  GPU ms by
+    the codec's HIP events; FLOPs of every conv at the sizes the reference
+    evaluates, against the dense fp32 matrix-core peak; the numpy oracle timed
+    once on the host for comparison."""
+    import mrt_df
+    import synth_bundle
+    shape = synth_bundle.CodecShape.reference()
+    w = synth_bundle.make_codec_weights(shape)
+    codec = mrt_df.Codec(w, max_frames=frames)
+    tok = np.random.default_rng(3).integers(0, 1024, size=(frames, 16)).astype(np.int32)
+    for _ in range(3):
+        codec.decode(tok)
+    ms = []
+    for _ in range(reps):
+        codec.decode(tok)
+        ms.append(codec.decode_time())
+    codec.close()
+    fl = synth_bundle.codec_flops(shape, frames)["total"]
+    gpu_ms = float(np.median(ms))
+    res = {"frames": frames, "samples": frames * 1920, "gpu_ms": gpu_ms, "rtf": frames * 40.0 / gpu_ms,
+           "flops": fl, "mfma": {"bound": "mfma", "achieved": fl / (gpu_ms * 1e-3) / 1e12,
+                                 "peak": MFMA_FP32_PEAK_TFLOPS, "unit": "TFLOP/s"},
+           "dtype": "f32", "reps": reps,
+           "data": "synthetic: seeded codec weights (reference key layout), random RVQ ids"}
+    res["mfma"]["frac"] = res["mfma"]["achieved"] / MFMA_FP32_PEAK_TFLOPS
+    if cpu:  # CPU baseline leg: the numpy restatement, timed once
+        from oracle import codec_oracle as C
+        t0 = time.perf_counter()
+        C.OracleCodec(w, C.CodecConfig.reference(), "fp32").decode(tok)
+        res["cpu_oracle_ms"] = (time.perf_counter() - t0) * 1e3
+        res["cpu_cores"] = len(os.sched_getaffinity(0))
+    print(f"[bench] codec decode {frames} frames: {gpu_ms:.2f} ms GPU ({res['mfma']['achieved']:.1f} TFLOP/s fp32, "
+          f"{100 * res['mfma']['frac']:.0f}% of peak)" +
+          (f"; numpy oracle {res['cpu_oracle_ms']:.0f} ms" if cpu else ""), file=sys.stderr, flush=True)
+    return res
+
+
 def bench_encoder(model, cfg, batches=(1, 8, 32), reps=3):
     """Encoder prefill alone over 2 x batch x 1006 token rows (CFG pairs): ms and
     matrix-core utilisation against the dense bf16 peak."""
@@ -382,7 +424,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--no-batched", action="store_true", help="skip the 32-stream, encoder-prefill and speculative figures")
+    ap.add_argument("--no-batched", action="store_true", help="skip the 32-stream, encoder-prefill, speculative and codec figures")
     ap.add_argument("--session", default="device", choices=["device", "host"],
                     help="device: RVQ context on the device, next chunk's encoder enqueued early; "
                          "host: context on the host, encoder ids uploaded per chunk")
@@ -477,11 +519,12 @@ def main():
                 "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
                 "launches_timed": dk["launches"]}
 
-    batched = encoder = spec = None
+    batched = encoder = spec = codec = None
     if not args.no_batched and args.dtype == "bf16":
         batched = bench_batched(model, cfg)
         encoder = bench_encoder(model, cfg)
         spec = bench_speculative(model, cfg, system.build_encoder_inputs(sess.context, scfg, style))
+        codec = bench_codec(cpu=not args.no_cpu_baseline)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -524,6 +567,7 @@ def main():
         "batched_streams": batched,
         "encoder_prefill": encoder,
         "speculative": spec,
+        "codec_decode": codec,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -163,7 +163,21 @@ Codec::Codec(const TensorSource& w, const TensorSource& cbs, const CodecConfig& 
     blk_c_.push_back(pack_conv(w, p + ".conv", b.out_ch, b.out_ch, b.kph, b.kpw));
     blk_sc_.push_back(b.in_ch != b.out_ch ? pack_conv(w, p + ".shortcut", b.out_ch, b.in_ch, 1, 1) : Conv{});
   }
-  out_conv_ = pack_conv(w, "output_conv", cfg.out_ch, cfg.blocks.back().out_ch, cfg.out_k, cfg.out_k);
+  {  // output conv: compact (kh, kw, cin, 2) for the vector-ALU kernel
+    const int ci = cfg.blocks.back().out_ch, k = cfg.out_k;
+    MRT_REQUIRE(k == 7 && ci % 8 == 0, "codec: output conv shape");
+    const HostTensor& t = w.tensor("output_conv.weight");
+    std::vector<float> h(static_cast<size_t>(k) * k * ci * 2);
+    for (int o = 0; o < 2; ++o)
+      for (int c = 0; c < ci; ++c)
+        for (int y = 0; y < k; ++y)
+          for (int x = 0; x < k; ++x)
+            h[((static_cast<size_t>(y) * k + x) * ci + c) * 2 + o] = t.data[((static_cast<size_t>(o) * ci + c) * k + y) * k + x];
+    out_w_ = dalloc(h.size());
+    MRT_HIP_CHECK(hipMemcpy(out_w_, h.data(), h.size() * 4, hipMemcpyHostToDevice));
+    out_b_ = dalloc(2);
+    MRT_HIP_CHECK(hipMemcpy(out_b_, w.tensor("output_conv.bias").data, 8, hipMemcpyHostToDevice));
+  }
 
   // iSTFT basis (spectrostream.cpp:616-646): frame row [re_0, im_0, .., re_479,
   // im_479] (bin 480, the restored Nyquist bin, is 0) -> windowed samples:
@@ -247,6 +261,7 @@ const Codec::Plan& Codec::plan(int frames) {
   auto pl = std::make_unique<Plan>();
   pl->frames = frames;
   std::vector<std::vector<ConvSub>> subs;
+  size_t need_partial = 0;
 
   auto add = [&](ConvLaunch L, std::vector<ConvSub> s) {
     int tiles = 0;
@@ -265,6 +280,17 @@ const Codec::Plan& Codec::plan(int frames) {
         }
     }
     MRT_REQUIRE(L.cin % 16 == 0 && L.cout % L.split == 0, "codec plan: channel layout");
+    // split-K when the tiles alone give fewer than 2 workgroups per CU:
+    // ~512 workgroups, >= 2 K chunks per slice
+    L.ksplit = 1;
+    L.rows = tiles * 64;
+    const int blocks = tiles * (L.cout_pad / 64);
+    if (blocks < 512) {
+      int min_nk = 1 << 30;
+      for (auto& q : s) min_nk = std::min(min_nk, q.ntaps * (L.cin / (L.cin % 32 == 0 ? 32 : 16)));
+      L.ksplit = std::max(1, std::min({(512 + blocks - 1) / blocks, min_nk / 2, 16}));
+    }
+    if (L.ksplit > 1) need_partial = std::max(need_partial, static_cast<size_t>(L.ksplit) * L.rows * L.cout_pad);
     pl->launches.push_back(L);
     pl->tiles_m.push_back(tiles);
     pl->tiles_n.push_back(L.cout_pad / 64);
@@ -388,16 +414,22 @@ const Codec::Plan& Codec::plan(int frames) {
     H = Ho;
     W = Wo;
   }
-  // elu -> output conv 7x7 causal, first temporal_crop rows dropped
+  // elu -> output conv 7x7 causal, first temporal_crop rows dropped (out_conv)
   const int Hs = H - cfg.temporal_crop;
-  {
-    ConvLaunch L = base(out_conv_, x, 2, H, W, spec_, Hs, W);
-    L.elu_in = 1;
-    add(L, regular(out_conv_, Hs, W, cfg.out_k, cfg.out_k, cfg.out_k - 1, (cfg.out_k - 1) / 2, cfg.temporal_crop));
-  }
+  MRT_REQUIRE(x == blk_out_.back() && Hs >= 1, "codec plan: output conv input");
+  pl->out_at = static_cast<int>(pl->launches.size());
+  pl->out_h = H;
+  pl->out_w = W;
+  pl->out_hs = Hs;
   // iSTFT frames: spec (2 Hs rows of 2 hop) x basis (2 hop, n_fft)
   add(base(istft_, spec_, 1, 2 * Hs, 1, wf_, 2 * Hs, 1), regular(istft_, 2 * Hs, 1, 1, 1, 0, 0, 0));
 
+  if (need_partial > partial_n_) {
+    MRT_HIP_CHECK(hipStreamSynchronize(stream));  // an older, smaller buffer may still be in use
+    partial_ = dalloc(need_partial);
+    partial_n_ = need_partial;
+  }
+  for (auto& L : pl->launches) L.partial = partial_;
   // upload every launch's sub-problems into one device array
   size_t total = 0;
   for (auto& s : subs) total += s.size();
@@ -420,7 +452,12 @@ void Codec::enqueue(const int* tokens_dev, int frames, float* audio_dev) {
   MRT_HIP_CHECK(hipEventRecord(ev_[0], stream));
   rvq_dequant(tokens_dev, frames, cfg.levels, codebooks_, cfg.codebook, cfg.embedding_dim, cfg.temporal_pad, emb_,
               stream);
-  for (size_t l = 0; l < pl.launches.size(); ++l) conv_launch(pl.launches[l], pl.tiles_m[l], pl.tiles_n[l], stream);
+  for (size_t l = 0; l < pl.launches.size(); ++l) {
+    if (static_cast<int>(l) == pl.out_at)
+      out_conv(blk_out_.back(), 2, pl.out_h, pl.out_w, cfg.blocks.back().out_ch, cfg.temporal_crop, out_w_, out_b_,
+               spec_, pl.out_hs, stream);
+    conv_launch(pl.launches[l], pl.tiles_m[l], pl.tiles_n[l], stream);
+  }
   const int Hs = spec_frames(frames);
   overlap_add(wf_, Hs, cfg.n_fft, frames * cfg.samples_per_frame, audio_dev, stream);
   MRT_HIP_CHECK(hipEventRecord(ev_[1], stream));

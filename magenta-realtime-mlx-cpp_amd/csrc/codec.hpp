@@ -52,14 +52,26 @@ struct ConvLaunch {
   int elu_in, elu_out;  // ELU on the loaded input (zero padding stays 0) / on the result
   int nsub;
   const ConvSub* subs;  // device array of nsub
+  // split-K: ksplit > 1 splits each tile's K loop over blockIdx.z; the slices
+  // write raw sums to partial[(z * rows + tile row) * cout_pad + o] (rows =
+  // 64 x the launch's M tiles) and conv_finish adds them in slice order
+  // before the epilogue.
+  int ksplit, rows;
+  float* partial;
 };
 
+// One convolution launch (plus its split-K finish when a.ksplit > 1).
 void conv_launch(const ConvLaunch& a, int tiles_m, int tiles_n, hipStream_t s);
 // emb (frames + pad, dim): rows < frames = sum over levels k < levels of
 // codebooks[k][tokens[f * levels + k]] (fp32, level order); the pad rows 0.
 // Ids outside [0, codebook) are read as 0.
 void rvq_dequant(const int* tokens, int frames, int levels, const float* codebooks, int codebook, int dim, int pad,
                  float* emb, hipStream_t s);
+// The output conv: x (n, H, W, cin) -> out (n, Hs, W, 2) = conv7x7(elu(x))
+// with causal padding (top 6, left 3, right 3) over input rows from `crop`
+// on, plus bias; w packed (kh, kw, cin, 2); cin a multiple of 8.
+void out_conv(const float* x, int n, int H, int W, int cin, int crop, const float* w, const float* bias, float* out,
+              int Hs, hipStream_t s);
 // audio (T, 2) from windowed frames wf (2 * H, n_fft): overlap-add at hop
 // n_fft / 2 (spectrostream.cpp:649-667), trimmed to T, channels interleaved.
 void overlap_add(const float* wf, int H, int n_fft, int T, float* audio, hipStream_t s);
@@ -121,6 +133,8 @@ class Codec {
     std::vector<int> tiles_m, tiles_n;
     ConvSub* subs_dev = nullptr;
     int frames = 0;
+    int out_at = 0;  // the output conv runs before launches[out_at]
+    int out_h = 0, out_w = 0, out_hs = 0;
   };
   const Plan& plan(int frames);
   void enqueue(const int* tokens_dev, int frames, float* audio_dev);
@@ -130,7 +144,8 @@ class Codec {
 
   std::vector<void*> allocs_;
   float* codebooks_ = nullptr;
-  Conv proj_sc_, proj_c1_, proj_c2_, in_c1_, in_c2_, out_conv_, istft_;
+  Conv proj_sc_, proj_c1_, proj_c2_, in_c1_, in_c2_, istft_;
+  float *out_w_ = nullptr, *out_b_ = nullptr;  // output conv (kh, kw, cin, 2), bias (2)
   std::vector<Conv> blk_t_, blk_c_, blk_sc_;
   float *emb_ = nullptr, *skip_ = nullptr, *p1_ = nullptr, *x0_ = nullptr, *t0_ = nullptr, *x1_ = nullptr;
   std::vector<float*> blk_out_;
@@ -139,6 +154,8 @@ class Codec {
   int* tok_ = nullptr;
   int last_frames_ = 0;
   std::map<int, std::unique_ptr<Plan>> plans_;
+  float* partial_ = nullptr;  // split-K partial sums (grown by plan())
+  size_t partial_n_ = 0;
   hipEvent_t ev_[2] = {nullptr, nullptr};
   bool timed_ = false;
 };

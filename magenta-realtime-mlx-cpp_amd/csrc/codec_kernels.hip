@@ -19,6 +19,21 @@ constexpr int kBM = 64, kBN = 64, kThreads = 256;
 
 __device__ __forceinline__ float elu1(float v) { return v > 0.f ? v : expf(v) - 1.f; }
 
+// The epilogue of output (sub-local row m, channel o): bias, residual (at the
+// output pixel divided by the repeat factors), ELU, store (with the stereo
+// split of the output channels).
+__device__ __forceinline__ void conv_store(const ConvLaunch& a, const ConvSub* sub, int m, int o, float val) {
+  const int gy = sub->gy, gx = sub->gx;
+  const int img = m / (gy * gx), r = m - img * gy * gx;
+  const int yy = r / gx, xx = r - (r / gx) * gx;
+  const int oy = yy * sub->oys + sub->oyo, ox = xx * sub->oxs + sub->oxo;
+  if (a.bias) val += a.bias[o];
+  if (a.res) val += a.res[((size_t)(img * a.res_h + oy / a.rh) * a.res_w + ox / a.rw) * a.cout + o];
+  if (a.elu_out) val = elu1(val);
+  const int oi = (o / a.split) * a.n + img, oc = o - (o / a.split) * a.split;
+  a.y[((size_t)(oi * a.hout + oy) * a.wout + ox) * a.split + oc] = val;
+}
+
 template <int KC>
 __global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
   constexpr int AS = KC + 4;
@@ -57,10 +72,13 @@ __global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
   const int b_row = tid / (kBN / 4);
 
   const int cpt = a.cin / KC;
-  const int nk = ntaps * cpt;
+  const int nk_all = ntaps * cpt;
+  const int kb = (int)blockIdx.z * nk_all / a.ksplit, ke = ((int)blockIdx.z + 1) * nk_all / a.ksplit;
+  const int nk = ke - kb;
   float ra[APASS][4], rb[BPASS][4];
 
   auto load = [&](int kc) {
+    kc += kb;
     const int t = kc / cpt, c0 = (kc - t * cpt) * KC + a_chunk * 4;
     const int dy = sub->dy[t], dx = sub->dx[t];
 #pragma unroll
@@ -109,10 +127,12 @@ __global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  load(0);
-  store(0);
-  __syncthreads();
   const int lr = lane & 15, lk = lane >> 4;
+  if (nk > 0) {
+    load(0);
+    store(0);
+  }
+  __syncthreads();
   for (int kc = 0; kc < nk; ++kc) {
     const int buf = kc & 1;
     if (kc + 1 < nk) load(kc + 1);
@@ -132,28 +152,142 @@ __global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
   }
 
   // epilogue: lane holds rows 4 * (lane / 16) + v, column lane % 16 of each tile
+  if (a.ksplit > 1) {
+    float* part = a.partial + ((size_t)blockIdx.z * a.rows + (size_t)blockIdx.x * kBM) * a.cout_pad;
+#pragma unroll
+    for (int tm = 0; tm < 2; ++tm)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+          part[(size_t)(wm * 32 + tm * 16 + 4 * lk + v) * a.cout_pad + n0 + wn * 32 + tn * 16 + lr] = acc[tm][tn][v];
+    return;
+  }
 #pragma unroll
   for (int tm = 0; tm < 2; ++tm) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int m = m0 + wm * 32 + tm * 16 + 4 * lk + v;
       if (m >= M) continue;
-      const int img = m / (gy * gx), r = m - img * gy * gx;
-      const int yy = r / gx, xx = r - (r / gx) * gx;
-      const int oy = yy * sub->oys + sub->oyo, ox = xx * sub->oxs + sub->oxo;
 #pragma unroll
       for (int tn = 0; tn < 2; ++tn) {
         const int o = n0 + wn * 32 + tn * 16 + lr;
-        if (o >= a.cout) continue;
-        float val = acc[tm][tn][v];
-        if (a.bias) val += a.bias[o];
-        if (a.res)
-          val += a.res[((size_t)(img * a.res_h + oy / a.rh) * a.res_w + ox / a.rw) * a.cout + o];
-        if (a.elu_out) val = elu1(val);
-        const int oi = (o / a.split) * a.n + img, oc = o - (o / a.split) * a.split;
-        a.y[((size_t)(oi * a.hout + oy) * a.wout + ox) * a.split + oc] = val;
+        if (o < a.cout) conv_store(a, sub, m, o, acc[tm][tn][v]);
       }
     }
+  }
+}
+
+// Split-K finish: thread (tile row, channel) sums the slices in order, then
+// the epilogue.
+__global__ __launch_bounds__(256) void k_conv_finish(ConvLaunch a) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (size_t)a.rows * a.cout) return;
+  const int row = (int)(i / a.cout), o = (int)(i - (size_t)row * a.cout);
+  const int tile = row / kBM;
+  int si = 0;
+  while (si + 1 < a.nsub && tile >= a.subs[si + 1].tile0) ++si;
+  const ConvSub* sub = a.subs + si;
+  const int m = (tile - sub->tile0) * kBM + (row - tile * kBM);
+  if (m >= a.n * sub->gy * sub->gx) return;
+  float v = 0.f;
+  for (int z = 0; z < a.ksplit; ++z) v += a.partial[((size_t)z * a.rows + row) * a.cout_pad + o];
+  conv_store(a, sub, m, o, v);
+}
+
+// The output convolution (Cout = 2, a 7 x 7 kernel, causal padding, the
+// first `crop` rows dropped; spectrostream.cpp:420-427) on the vector ALUs:
+// a matrix-core tile would be 2 of 16 columns.  Workgroup: 4 output rows x
+// 128 columns of one image and 256 threads, two halves over the input
+// channels (waves 0-1 and 2-3, so the weights a wave needs are uniform and
+// come through scalar loads); a thread owns a 4-pixel strip x 2 outputs.
+// The input halo (4 + 6 rows x 128 + 6 columns) is staged through LDS 8
+// channels at a time (4 per half) with the ELU applied; the halves' sums
+// meet in LDS at the end.
+constexpr int kOcRows = 4, kOcCols = 128, kOcStrip = 4, kOcThreads = 256;
+constexpr int kOcCh = 8, kOcK = 7;
+constexpr int kOcHaloR = kOcRows + kOcK - 1, kOcHaloC = kOcCols + kOcK - 1;
+constexpr int kOcPlane = kOcHaloR * kOcHaloC;
+
+__global__ __launch_bounds__(kOcThreads) void k_out_conv(const float* __restrict__ x, int H, int W, int cin, int crop,
+                                                         const float* __restrict__ w, const float* __restrict__ bias,
+                                                         float* __restrict__ out, int Hs) {
+  __shared__ float hl[kOcCh * kOcPlane];  // (channel, halo row, halo column)
+  const int tid = threadIdx.x;
+  const int img = blockIdx.z;
+  const int y0 = blockIdx.y * kOcRows, x0 = blockIdx.x * kOcCols;
+  const int half = __builtin_amdgcn_readfirstlane(tid >> 7);  // wave-uniform
+  const int st = tid & 127;
+  const int ty = st / (kOcCols / kOcStrip), tx = (st % (kOcCols / kOcStrip)) * kOcStrip;
+  float acc[kOcStrip][2];
+#pragma unroll
+  for (int p = 0; p < kOcStrip; ++p) acc[p][0] = acc[p][1] = 0.f;
+  // input row of halo row r: y0 + crop + r - (k - 1); column of halo column q: x0 + q - (k - 1) / 2
+  const int iy0 = y0 + crop - (kOcK - 1), ix0 = x0 - (kOcK - 1) / 2;
+  for (int c0 = 0; c0 < cin; c0 += kOcCh) {
+    __syncthreads();  // the previous chunk's reads are done
+    for (int i = tid; i < kOcPlane * 2; i += kOcThreads) {
+      const int hh = i & 1, pix = i >> 1;
+      const int r = pix / kOcHaloC, q = pix - r * kOcHaloC;
+      const int iy = iy0 + r, ix = ix0 + q;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (iy >= 0 && iy < H && ix >= 0 && ix < W) {
+        v = *reinterpret_cast<const float4*>(x + ((size_t)(img * H + iy) * W + ix) * cin + c0 + hh * 4);
+        v.x = elu1(v.x);
+        v.y = elu1(v.y);
+        v.z = elu1(v.z);
+        v.w = elu1(v.w);
+      }
+      float* d = hl + (hh * 4) * kOcPlane + pix;
+      d[0] = v.x;
+      d[kOcPlane] = v.y;
+      d[2 * kOcPlane] = v.z;
+      d[3 * kOcPlane] = v.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int ch = c0 + half * 4 + c;
+      const float* hc = hl + (half * 4 + c) * kOcPlane;
+#pragma unroll
+      for (int kh = 0; kh < kOcK; ++kh) {
+        float in[kOcStrip + kOcK - 1];
+#pragma unroll
+        for (int q = 0; q < kOcStrip + kOcK - 1; ++q) in[q] = hc[(ty + kh) * kOcHaloC + tx + q];
+#pragma unroll
+        for (int kw = 0; kw < kOcK; ++kw) {
+          const float* wk = w + ((size_t)(kh * kOcK + kw) * cin + ch) * 2;
+          const float w0 = wk[0], w1 = wk[1];
+#pragma unroll
+          for (int p = 0; p < kOcStrip; ++p) {
+            acc[p][0] = fmaf(in[p + kw], w0, acc[p][0]);
+            acc[p][1] = fmaf(in[p + kw], w1, acc[p][1]);
+          }
+        }
+      }
+    }
+  }
+  // the upper half's sums join the lower half's through LDS
+  __syncthreads();
+  float* red = hl;
+  if (half == 1) {
+#pragma unroll
+    for (int p = 0; p < kOcStrip; ++p) {
+      red[(p * 2) * 128 + st] = acc[p][0];
+      red[(p * 2 + 1) * 128 + st] = acc[p][1];
+    }
+  }
+  __syncthreads();
+  if (half == 1) return;
+  const int oy = y0 + ty;
+  if (oy >= Hs) return;
+#pragma unroll
+  for (int p = 0; p < kOcStrip; ++p) {
+    const int ox = x0 + tx + p;
+    if (ox >= W) continue;
+    float* o = out + ((size_t)(img * Hs + oy) * W + ox) * 2;
+    o[0] = acc[p][0] + red[(p * 2) * 128 + st] + bias[0];
+    o[1] = acc[p][1] + red[(p * 2 + 1) * 128 + st] + bias[1];
   }
 }
 
@@ -188,10 +322,24 @@ __global__ void k_overlap_add(const float* __restrict__ wf, int H, int n_fft, in
 }  // namespace
 
 void conv_launch(const ConvLaunch& a, int tiles_m, int tiles_n, hipStream_t s) {
+  const dim3 grid(tiles_m, tiles_n, a.ksplit);
   if (a.cin % 32 == 0)
-    hipLaunchKernelGGL(k_conv<32>, dim3(tiles_m, tiles_n), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(k_conv<32>, grid, dim3(kThreads), 0, s, a);
   else
-    hipLaunchKernelGGL(k_conv<16>, dim3(tiles_m, tiles_n), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(k_conv<16>, grid, dim3(kThreads), 0, s, a);
+  MRT_HIP_CHECK(hipGetLastError());
+  if (a.ksplit > 1) {
+    const size_t n = static_cast<size_t>(a.rows) * a.cout;
+    hipLaunchKernelGGL(k_conv_finish, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, a);
+    MRT_HIP_CHECK(hipGetLastError());
+  }
+}
+
+void out_conv(const float* x, int n, int H, int W, int cin, int crop, const float* w, const float* bias, float* out,
+              int Hs, hipStream_t s) {
+  MRT_REQUIRE(cin % kOcCh == 0, "codec: output conv input channels must be a multiple of 8");
+  const dim3 grid((W + kOcCols - 1) / kOcCols, (Hs + kOcRows - 1) / kOcRows, n);
+  hipLaunchKernelGGL(k_out_conv, grid, dim3(kOcThreads), 0, s, x, H, W, cin, crop, w, bias, out, Hs);
   MRT_HIP_CHECK(hipGetLastError());
 }
 

@@ -9,6 +9,11 @@ counter runs (FETCH_SIZE / WRITE_SIZE per dispatch) and kernel traces.
 --batched N instead runs N independent streams together: one encode of
 2N x 1006 rows and one decode of F frames through the replayed frame graph.
 
+    python magenta-realtime-mlx-cpp_amd/profile_steps.py --codec 51 [--reps N]
+
+--codec F instead runs N codec decodes of F frames (RVQ ids -> audio, fp32,
+seeded synthetic codec weights) after 2 untimed ones.
+
 The copy (torch's device copy of M MiB, M above the 256 MB last-level cache)
 reads and writes exactly M MiB; its counter readings give the scale factor
 between the counters and bytes.
@@ -34,12 +39,27 @@ def main() -> None:
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--batched", type=int, default=0, help="streams of a batched decode (0: single stream)")
     ap.add_argument("--frames", type=int, default=50, help="frames of the batched decode")
+    ap.add_argument("--codec", type=int, default=0, help="frames of codec decodes (0: Depthformer steps)")
     a = ap.parse_args()
 
     import torch
     import mrt_df
     import synth_bundle
     import system
+
+    if a.codec:
+        shape = synth_bundle.CodecShape.reference()
+        codec = mrt_df.Codec(synth_bundle.make_codec_weights(shape), max_frames=a.codec)
+        tok = np.random.default_rng(3).integers(0, 1024, size=(a.codec, 16)).astype(np.int32)
+        for _ in range(2):
+            codec.decode(tok)
+        ms = []
+        for _ in range(a.reps):
+            codec.decode(tok)
+            ms.append(codec.decode_time())
+        print(f"[profile] codec {a.codec} frames: {np.mean(ms):.3f} ms per decode over {a.reps}", flush=True)
+        codec.close()
+        return
 
     cfg = mrt_df.Config.bench()
     model = mrt_df.Depthformer(synth_bundle.make_weights(cfg, seed=a.seed, threads=16), cfg, dtype="bf16")

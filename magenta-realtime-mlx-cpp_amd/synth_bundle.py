@@ -15,6 +15,8 @@ values do not depend on generation order.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import dataclasses
+import math
 import zlib
 from typing import Dict, List, Tuple
 
@@ -95,3 +97,136 @@ def write_bundle(path, weights: Dict[str, np.ndarray]) -> None:
     """Write an fp32 ``.safetensors`` bundle."""
     from safetensors.numpy import save_file  # noqa: PLC0415
     save_file({k: np.ascontiguousarray(v, dtype=np.float32) for k, v in weights.items()}, str(path))
+
+
+# ---------------------------------------------------------------------------
+# SpectroStream codec bundles (decoder + codebooks)
+
+
+@dataclasses.dataclass(frozen=True)
+class CodecBlock:
+    in_ch: int
+    out_ch: int
+    stride: Tuple[int, int]
+    transpose_kernel: Tuple[int, int]
+    post_kernel: Tuple[int, int]
+
+
+@dataclasses.dataclass(frozen=True)
+class CodecShape:
+    """The SpectroStream decoder's shape (spectrostream.cpp:328-362): input
+    projection E -> P -> P, unfold 5, seven transposed-conv blocks, a 7x7
+    output conv to (real, imag).  ``tiny()`` divides the channels by 4 and
+    keeps every stride, kernel and crop (test-only)."""
+
+    embedding_dim: int = 256
+    proj_ch: int = 2560
+    unfold: int = 5
+    blocks: Tuple[CodecBlock, ...] = (
+        CodecBlock(512, 1024, (2, 1), (4, 3), (3, 3)),
+        CodecBlock(512, 256, (2, 2), (4, 4), (3, 3)),
+        CodecBlock(256, 256, (1, 2), (3, 4), (3, 3)),
+        CodecBlock(256, 256, (1, 2), (3, 4), (3, 3)),
+        CodecBlock(256, 128, (1, 3), (3, 6), (3, 3)),
+        CodecBlock(128, 128, (1, 2), (3, 4), (3, 3)),
+        CodecBlock(128, 64, (1, 2), (3, 4), (3, 3)),
+    )
+    out_ch: int = 2
+    out_kernel: Tuple[int, int] = (7, 7)
+    temporal_pad: int = 1
+    temporal_crop: int = 4
+    n_fft: int = 960
+
+    @property
+    def input_conv_ch(self) -> int:
+        return self.proj_ch // self.unfold
+
+    @staticmethod
+    def reference() -> "CodecShape":
+        return CodecShape()
+
+    @staticmethod
+    def tiny() -> "CodecShape":
+        r = CodecShape()
+        return dataclasses.replace(r, embedding_dim=64, proj_ch=640,
+                                   blocks=tuple(dataclasses.replace(b, in_ch=b.in_ch // 4, out_ch=b.out_ch // 4)
+                                                for b in r.blocks))
+
+    def channels(self):
+        """The ``channels`` argument of ``mrt_df.Codec``."""
+        return (self.embedding_dim, self.proj_ch, [b.in_ch for b in self.blocks], [b.out_ch for b in self.blocks])
+
+
+def codec_layout(shape) -> List[Tuple[str, Tuple[int, ...]]]:
+    """Decoder bundle keys and stored shapes (spectrostream.cpp:125-158,
+    163-262, 356-362): conv (out, in, kH, kW), transposed conv (in, out, kH,
+    kW), biases (out,)."""
+    E, P, C0 = shape.embedding_dim, shape.proj_ch, shape.proj_ch // shape.unfold
+    out: List[Tuple[str, Tuple[int, ...]]] = []
+
+    def conv(name, o, i, kh, kw):
+        out.append((name + ".weight", (o, i, kh, kw)))
+        out.append((name + ".bias", (o,)))
+
+    conv("input_proj.conv1", P, E, 1, 1)
+    conv("input_proj.conv2", P, P, 1, 1)
+    conv("input_proj.shortcut", P, E, 1, 1)
+    conv("input_conv.conv1", C0, C0, 3, 3)
+    conv("input_conv.conv2", C0, C0, 3, 3)
+    for i, b in enumerate(shape.blocks):
+        p = f"decoder_blocks.{i}"
+        out.append((p + ".conv_transpose.weight", (b.in_ch, b.out_ch) + tuple(b.transpose_kernel)))
+        out.append((p + ".conv_transpose.bias", (b.out_ch,)))
+        conv(p + ".conv", b.out_ch, b.out_ch, *b.post_kernel)
+        if b.in_ch != b.out_ch:
+            conv(p + ".shortcut", b.out_ch, b.in_ch, 1, 1)
+    conv("output_conv", shape.out_ch, shape.blocks[-1].out_ch, *shape.out_kernel)
+    return out
+
+
+def make_codec_weights(shape, seed: int = 5, levels: int = 16, codebook: int = 1024,
+                       cb_std: float = 0.25) -> Dict[str, np.ndarray]:
+    """Seeded fp32 decoder weights in the stored layouts plus "codebooks"
+    (levels, codebook, E): conv weights N(0, 1/fan_in) (fan_in = in * kH *
+    kW), biases N(0, 0.02^2), codebooks N(0, cb_std^2); each tensor from its
+    own (seed, crc32(name)) stream."""
+    out = {}
+    for name, shp in codec_layout(shape):
+        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
+        if name.endswith(".bias"):
+            out[name] = (0.02 * rng.standard_normal(shp)).astype(np.float32)
+        else:
+            fan_in = (shp[0] if ".conv_transpose." in name else shp[1]) * shp[2] * shp[3]
+            out[name] = (rng.standard_normal(shp) / math.sqrt(fan_in)).astype(np.float32)
+    rng = np.random.default_rng([seed, zlib.crc32(b"codebooks")])
+    out["codebooks"] = (cb_std * rng.standard_normal((levels, codebook, shape.embedding_dim))).astype(np.float32)
+    return out
+
+
+def codec_flops(shape, frames: int) -> Dict[str, float]:
+    """FLOPs (2 per multiply-add) one decode of ``frames`` RVQ frames needs:
+    transposed convs over their input pixels and taps (cropped outputs
+    included), block shortcuts on their input grid (a 1x1 conv commutes with
+    the residual's repeat), the output conv on the rows kept after the crop,
+    the iSTFT as a real DFT product."""
+    fl = {}
+    H, E, P = frames + shape.temporal_pad, shape.embedding_dim, shape.proj_ch
+    fl["input_proj"] = 2.0 * H * (E * P + P * P + E * P)
+    W, C = shape.unfold, shape.proj_ch // shape.unfold
+    fl["input_conv"] = 2.0 * 2 * H * W * 9 * C * C
+    n = 1
+    for i, b in enumerate(shape.blocks):
+        if i == 1:
+            n = 2
+        kh, kw = b.transpose_kernel
+        sh, sw = b.stride
+        t = 2.0 * n * H * W * kh * kw * b.in_ch * b.out_ch
+        Ho, Wo = H * sh, W * sw
+        c = 2.0 * n * Ho * Wo * b.post_kernel[0] * b.post_kernel[1] * b.out_ch * b.out_ch
+        s = 2.0 * n * H * W * b.in_ch * b.out_ch if b.in_ch != b.out_ch else 0.0  # on the input grid
+        fl[f"block{i}"] = t + c + s
+        H, W = Ho, Wo
+    fl["output_conv"] = 2.0 * n * (H - shape.temporal_crop) * W * 49 * shape.blocks[-1].out_ch * shape.out_ch
+    fl["istft"] = 2.0 * 2 * (H - shape.temporal_crop) * shape.n_fft * shape.n_fft
+    fl["total"] = sum(fl.values())
+    return fl

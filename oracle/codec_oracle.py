@@ -33,6 +33,8 @@ How each part is pinned (tests/test_oracle_codec.py):
   * pads                         -- closed forms at the shapes the decoder uses;
   * decoder shape arithmetic     -- the header's (B, H, 480, 4) output and
                                     H = 4 * (S + 1) - 4;
+Bundle layout, synthetic weights and FLOP counts are the package's
+(synth_bundle.codec_layout / make_codec_weights / codec_flops).
   * istft_postprocess            -- a brute-force DFT + overlap-add loop, and
                                     the round trip istft(stft_hann(x)) == x
                                     (Hann analysis window, the reference's
@@ -106,63 +108,6 @@ class CodecConfig:
             r, embedding_dim=64, proj_ch=640,
             blocks=tuple(DecBlock(b.in_ch // 4, b.out_ch // 4, b.stride, b.transpose_kernel, b.post_kernel)
                          for b in r.blocks))
-
-
-def decoder_layout(cfg: CodecConfig) -> List[Tuple[str, Tuple[int, ...]]]:
-    """Bundle keys and stored shapes (spectrostream.cpp:125-158, 163-262, 356-362)."""
-    E, P, C0 = cfg.embedding_dim, cfg.proj_ch, cfg.input_conv_ch
-    out: List[Tuple[str, Tuple[int, ...]]] = []
-
-    def conv(name, o, i, kh, kw):
-        out.append((name + ".weight", (o, i, kh, kw)))
-        out.append((name + ".bias", (o,)))
-
-    conv("input_proj.conv1", P, E, 1, 1)
-    conv("input_proj.conv2", P, P, 1, 1)
-    conv("input_proj.shortcut", P, E, 1, 1)
-    conv("input_conv.conv1", C0, C0, 3, 3)
-    conv("input_conv.conv2", C0, C0, 3, 3)
-    for i, b in enumerate(cfg.blocks):
-        p = f"decoder_blocks.{i}"
-        out.append((p + ".conv_transpose.weight", (b.in_ch, b.out_ch) + tuple(b.transpose_kernel)))
-        out.append((p + ".conv_transpose.bias", (b.out_ch,)))
-        conv(p + ".conv", b.out_ch, b.out_ch, *b.post_kernel)
-        if b.in_ch != b.out_ch:
-            conv(p + ".shortcut", b.out_ch, b.in_ch, 1, 1)
-    conv("output_conv", cfg.out_ch, cfg.blocks[-1].out_ch, *cfg.out_kernel)
-    return out
-
-
-def decoder_flops(cfg: CodecConfig, frames: int) -> Dict[str, float]:
-    """Multiply-add FLOPs (2 per MAC) of one decode of ``frames`` RVQ frames,
-    counting every conv at the sizes the reference evaluates (transposed
-    convs over their input pixels and taps, cropped outputs included), and the
-    iSTFT as a real DFT product."""
-    fl = {}
-    H, W = frames + cfg.temporal_pad, 1
-    E, P = cfg.embedding_dim, cfg.proj_ch
-    fl["input_proj"] = 2.0 * H * (E * P + P * P + E * P)
-    W = cfg.unfold
-    C = cfg.input_conv_ch
-    fl["input_conv"] = 2.0 * 2 * H * W * 9 * C * C
-    n = 1
-    for i, b in enumerate(cfg.blocks):
-        if i == 1:
-            n = 2
-        kh, kw = b.transpose_kernel
-        sh, sw = b.stride
-        t = 2.0 * n * H * W * kh * kw * b.in_ch * b.out_ch
-        Ho = (H - 1) * sh + kh - (kh - sh)
-        Wo = (W - 1) * sw + kw - (kw - sw)
-        c = 2.0 * n * Ho * Wo * b.post_kernel[0] * b.post_kernel[1] * b.out_ch * b.out_ch
-        s = 2.0 * n * Ho * Wo * b.in_ch * b.out_ch if b.in_ch != b.out_ch else 0.0
-        fl[f"block{i}"] = t + c + s
-        H, W = Ho, Wo
-    fl["output_conv"] = 2.0 * n * H * W * 49 * cfg.blocks[-1].out_ch * cfg.out_ch
-    frames_out = H - cfg.temporal_crop
-    fl["istft"] = 2.0 * 2 * frames_out * (2 * (cfg.n_fft // 2)) * cfg.n_fft
-    fl["total"] = sum(fl.values())
-    return fl
 
 
 # ---------------------------------------------------------------------------
@@ -397,29 +342,3 @@ def istft_postprocess(spec: np.ndarray, B: int, target_length: int, cfg: CodecCo
     audio = np.concatenate([body.reshape(B * 2, frames * hop), right[:, -1]], axis=-1)
     audio = audio[:, :target_length].reshape(B, 2, target_length).transpose(0, 2, 1)
     return np.ascontiguousarray(audio)
-
-
-# ---------------------------------------------------------------------------
-# Synthetic weights (test-only; the reference's checkpoints are not available)
-
-
-def synthetic_codec_weights(cfg: CodecConfig, seed: int = 5, levels: int = 16, codebook: int = 1024,
-                            cb_std: float = 0.25) -> Dict[str, np.ndarray]:
-    """Seeded fp32 weights in the stored layouts: conv weights N(0, 1/fan_in)
-    (fan_in = in * kH * kW), biases N(0, 0.02^2), codebooks N(0, cb_std^2);
-    each tensor from its own (seed, crc32(name)) stream."""
-    import zlib
-    out = {}
-    for name, shape in decoder_layout(cfg):
-        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
-        if name.endswith(".bias"):
-            out[name] = (0.02 * rng.standard_normal(shape)).astype(np.float32)
-        else:
-            if ".conv_transpose." in name:
-                fan_in = shape[0] * shape[2] * shape[3]
-            else:
-                fan_in = shape[1] * shape[2] * shape[3]
-            out[name] = (rng.standard_normal(shape) / math.sqrt(fan_in)).astype(np.float32)
-    rng = np.random.default_rng([seed, zlib.crc32(b"codebooks")])
-    out["codebooks"] = (cb_std * rng.standard_normal((levels, codebook, cfg.embedding_dim))).astype(np.float32)
-    return out

@@ -11,26 +11,26 @@ import ctypes
 import pytest
 
 import mrt_df
-from oracle import codec_oracle as C
+import synth_bundle
 
 MRT_ERR_INVALID, MRT_ERR_MISSING_KEY = 1, 4
 
 
 @pytest.fixture(scope="module")
 def tiny_weights():
-    cfg = C.CodecConfig.tiny()
-    return cfg, C.synthetic_codec_weights(cfg, levels=16, codebook=64)
+    shape = synth_bundle.CodecShape.tiny()
+    return shape, synth_bundle.make_codec_weights(shape, levels=16, codebook=64)
 
 
-def _channels(cfg):
-    return (cfg.embedding_dim, cfg.proj_ch, [b.in_ch for b in cfg.blocks], [b.out_ch for b in cfg.blocks])
+def _channels(shape):
+    return shape.channels()
 
 
 def test_codec_config_default_is_the_reference_decoder():
     lib = mrt_df.load_library()
     c = mrt_df._CodecConfig()
     lib.mrt_codec_config_default(ctypes.byref(c))
-    ref = C.CodecConfig.reference()
+    ref = synth_bundle.CodecShape.reference()
     assert (c.embedding_dim, c.proj_channels, c.unfold) == (256, 2560, 5)
     assert list(c.block_in) == [b.in_ch for b in ref.blocks]
     assert list(c.block_out) == [b.out_ch for b in ref.blocks]

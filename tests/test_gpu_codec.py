@@ -9,6 +9,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+import synth_bundle
 from oracle import codec_oracle as C
 
 pytestmark = pytest.mark.gpu
@@ -56,7 +57,7 @@ def _check(codec, cfg, w, tok):
 def test_codec_tiny_every_stage(gpu_available):
     import mrt_df
     cfg = C.CodecConfig.tiny()
-    w = C.synthetic_codec_weights(cfg, levels=16, codebook=64)
+    w = synth_bundle.make_codec_weights(synth_bundle.CodecShape.tiny(), levels=16, codebook=64)
     codec = mrt_df.Codec(w, max_frames=6, channels=_channels(cfg), codebook_size=64)
     rng = np.random.default_rng(0)
     _check(codec, cfg, w, rng.integers(0, 64, size=(5, 16)).astype(np.int32))
@@ -70,7 +71,7 @@ def test_codec_tiny_every_stage(gpu_available):
 def test_codec_errors(gpu_available):
     import mrt_df
     cfg = C.CodecConfig.tiny()
-    w = C.synthetic_codec_weights(cfg, levels=16, codebook=64)
+    w = synth_bundle.make_codec_weights(synth_bundle.CodecShape.tiny(), levels=16, codebook=64)
     codec = mrt_df.Codec(w, max_frames=4, channels=_channels(cfg), codebook_size=64)
     tok = np.zeros((3, 16), np.int32)
     tok[1, 5] = 64
@@ -91,7 +92,7 @@ def test_codec_errors(gpu_available):
 def full():
     import mrt_df
     cfg = C.CodecConfig.reference()
-    w = C.synthetic_codec_weights(cfg)
+    w = synth_bundle.make_codec_weights(synth_bundle.CodecShape.reference())
     codec = mrt_df.Codec(w, max_frames=51)
     yield cfg, w, codec
     codec.close()

@@ -10,6 +10,7 @@ import math
 import numpy as np
 import pytest
 
+import synth_bundle
 from oracle import codec_oracle as C
 
 
@@ -154,7 +155,10 @@ def test_istft_round_trip():
 
 def test_decoder_shapes_and_finite():
     cfg = C.CodecConfig.tiny()
-    w = C.synthetic_codec_weights(cfg, levels=16, codebook=64)
+    shape = synth_bundle.CodecShape.tiny()
+    assert shape.channels() == (cfg.embedding_dim, cfg.proj_ch, [b.in_ch for b in cfg.blocks],
+                                [b.out_ch for b in cfg.blocks])
+    w = synth_bundle.make_codec_weights(shape, levels=16, codebook=64)
     o = C.OracleCodec(w, cfg, "fp64")
     S = 3
     tok = np.random.default_rng(6).integers(0, 64, size=(S, 16))
@@ -163,13 +167,21 @@ def test_decoder_shapes_and_finite():
     assert rec["spec_planar"].shape == (2, 4 * S, 480, 2)  # H = 4 (S + 1) - 4
     assert rec["block0"].shape == (2, 2 * (S + 1), 5, cfg.blocks[0].out_ch // 2)
     assert audio.shape == (S * 1920, 2) and np.isfinite(audio).all()
-    for name, shape in C.decoder_layout(cfg):
-        assert w[name].shape == shape
+    for name, shp in synth_bundle.codec_layout(shape):
+        assert w[name].shape == shp
+
+
+def test_package_codec_shape_is_the_oracle_config():
+    ref, sh = C.CodecConfig.reference(), synth_bundle.CodecShape.reference()
+    for a, b in zip(ref.blocks, sh.blocks):
+        assert (a.in_ch, a.out_ch, a.stride, a.transpose_kernel, a.post_kernel) == \
+            (b.in_ch, b.out_ch, b.stride, b.transpose_kernel, b.post_kernel)
+    assert (ref.embedding_dim, ref.proj_ch, ref.unfold) == (sh.embedding_dim, sh.proj_ch, sh.unfold)
 
 
 def test_flops_table():
-    fl = C.decoder_flops(C.CodecConfig.reference(), 51)
-    assert 195e9 < fl["total"] < 215e9
+    fl = synth_bundle.codec_flops(synth_bundle.CodecShape.reference(), 51)
+    assert 195e9 < fl["total"] < 205e9
 
 
 def test_design_identity_shortcut_commutes_with_repeat():
