@@ -1,21 +1,24 @@
 // Codec decode kernels (fp32): the implicit-GEMM convolution on the matrix
 // cores, RVQ dequantisation and the iSTFT overlap-add.
 //
-// k_conv: a 64 x 64 output tile (pixels x channels) per 256-thread
-// workgroup, 4 waves in a 2 x 2 grid, each wave 2 x 2 tiles of
-// v_mfma_f32_16x16x4_f32.  The K loop runs over (tap, KC-channel chunk);
+// k_conv<BM, BN, KC>: a BM x BN output tile (pixels x channels) per
+// 256-thread workgroup (64 x 64: larger tiles measured slower, fewer
+// workgroups per CU hide less load latency), 4 waves in a 2 x 2 grid, each
+// wave BM/32 x BN/32 tiles of v_mfma_f32_16x16x4_f32.  The K loop runs over (tap, KC-channel chunk);
 // each chunk's A rows (the tap's input pixel for every output pixel of the
 // tile, zero outside the input, ELU applied on load when asked) and B rows
 // (packed weights) are staged through a double-buffered LDS with one barrier
-// per chunk, the next chunk's global loads in flight while the current one
-// is multiplied.  LDS strides: A rows KC + 4 floats (the 16 rows x 4 k lanes of
+// per chunk; the global loads run two chunks ahead of the multiplies (two
+// register sets).  LDS strides: A rows KC + 4 floats (the 16 rows x 4 k lanes of
 // an A fragment hit 64 distinct banks), B rows 80 floats (the same for B).
 #include "codec.hpp"
+
+#include <type_traits>
 
 namespace mrt {
 namespace {
 
-constexpr int kBM = 64, kBN = 64, kThreads = 256;
+constexpr int kThreads = 256;
 
 __device__ __forceinline__ float elu1(float v) { return v > 0.f ? v : expf(v) - 1.f; }
 
@@ -34,16 +37,17 @@ __device__ __forceinline__ void conv_store(const ConvLaunch& a, const ConvSub* s
   a.y[((size_t)(oi * a.hout + oy) * a.wout + ox) * a.split + oc] = val;
 }
 
-template <int KC>
+template <int BM, int BN, int KC>
 __global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
-  constexpr int AS = KC + 4;
-  constexpr int BS = kBN + 16;
-  constexpr int CPR = KC / 4;            // float4 chunks per A row
-  constexpr int RPP = kThreads / CPR;    // A rows per load pass
-  constexpr int APASS = kBM / RPP;       // A loads per thread
-  constexpr int BPASS = KC * (kBN / 4) / kThreads;  // B loads per thread
-  static_assert(kBM % RPP == 0 && BPASS >= 1, "tile shape");
-  __shared__ __attribute__((aligned(16))) float As[2][kBM * AS];
+  constexpr int AS = KC + 4;  // the 16 rows x 4 k lanes of an A fragment hit 64 distinct banks
+  constexpr int BS = BN + 16;  // the 4 k rows x 16 columns of a B fragment hit 64 distinct banks
+  constexpr int CPR = KC / 4;             // float4 chunks per A row
+  constexpr int RPP = kThreads / CPR;     // A rows per load pass
+  constexpr int APASS = BM / RPP;         // A loads per thread
+  constexpr int BCPR = BN / 4, BRPP = kThreads / BCPR, BPASS = KC / BRPP;  // B loads per thread
+  constexpr int TM = BM / 32, TN = BN / 32;  // 16 x 16 tiles per wave (2 x 2 waves)
+  static_assert(BM % RPP == 0 && KC % BRPP == 0 && BPASS >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
   __shared__ __attribute__((aligned(16))) float Bs[2][KC * BS];
 
   int si = 0;
@@ -51,8 +55,8 @@ __global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
   const ConvSub* sub = a.subs + si;
   const int gy = sub->gy, gx = sub->gx, ntaps = sub->ntaps;
   const int M = a.n * gy * gx;
-  const int m0 = ((int)blockIdx.x - sub->tile0) * kBM;
-  const int n0 = (int)blockIdx.y * kBN;
+  const int m0 = ((int)blockIdx.x - sub->tile0) * BM;
+  const int n0 = (int)blockIdx.y * BN;
   const float* __restrict__ W = sub->w;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -68,16 +72,21 @@ __global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
     a_y[p] = r / gx;
     a_x[p] = r - (r / gx) * gx;
   }
-  const int b_col = (tid % (kBN / 4)) * 4;
-  const int b_row = tid / (kBN / 4);
+  const int b_col = (tid % BCPR) * 4;
+  const int b_row = tid / BCPR;
 
   const int cpt = a.cin / KC;
   const int nk_all = ntaps * cpt;
   const int kb = (int)blockIdx.z * nk_all / a.ksplit, ke = ((int)blockIdx.z + 1) * nk_all / a.ksplit;
   const int nk = ke - kb;
-  float ra[APASS][4], rb[BPASS][4];
+  // two register sets: chunk kc + 2 is loaded while chunk kc is multiplied
+  // and chunk kc + 1 (loaded a whole chunk earlier) goes to the LDS
+  float ra[2][APASS][4], rb[2][BPASS][4];
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
 
-  auto load = [&](int kc) {
+  auto load = [&](int kc, auto S) {
+    constexpr int q = decltype(S)::value;
     kc += kb;
     const int t = kc / cpt, c0 = (kc - t * cpt) * KC + a_chunk * 4;
     const int dy = sub->dy[t], dx = sub->dx[t];
@@ -87,92 +96,102 @@ __global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
       const bool ok = iy >= 0 && iy < a.hin && ix >= 0 && ix < a.win;
       const int cy = ok ? iy : 0, cx = ok ? ix : 0;
       const float4 v = *reinterpret_cast<const float4*>(a.x + ((size_t)(a_img[p] + cy) * a.win + cx) * a.cin + c0);
-      ra[p][0] = ok ? v.x : 0.f;
-      ra[p][1] = ok ? v.y : 0.f;
-      ra[p][2] = ok ? v.z : 0.f;
-      ra[p][3] = ok ? v.w : 0.f;
+      ra[q][p][0] = ok ? v.x : 0.f;
+      ra[q][p][1] = ok ? v.y : 0.f;
+      ra[q][p][2] = ok ? v.z : 0.f;
+      ra[q][p][3] = ok ? v.w : 0.f;
     }
     const float* wb = W + ((size_t)t * a.cin + (kc - t * cpt) * KC) * a.cout_pad + n0 + b_col;
 #pragma unroll
     for (int p = 0; p < BPASS; ++p) {
-      const float4 v = *reinterpret_cast<const float4*>(wb + (size_t)(b_row + p * (kThreads / (kBN / 4))) * a.cout_pad);
-      rb[p][0] = v.x;
-      rb[p][1] = v.y;
-      rb[p][2] = v.z;
-      rb[p][3] = v.w;
+      const float4 v = *reinterpret_cast<const float4*>(wb + (size_t)(b_row + p * BRPP) * a.cout_pad);
+      rb[q][p][0] = v.x;
+      rb[q][p][1] = v.y;
+      rb[q][p][2] = v.z;
+      rb[q][p][3] = v.w;
     }
   };
-  auto store = [&](int buf) {
+  auto store = [&](auto S) {  // register set q -> LDS buffer q
+    constexpr int q = decltype(S)::value;
 #pragma unroll
     for (int p = 0; p < APASS; ++p) {
-      float4 v = make_float4(ra[p][0], ra[p][1], ra[p][2], ra[p][3]);
+      float4 v = make_float4(ra[q][p][0], ra[q][p][1], ra[q][p][2], ra[q][p][3]);
       if (a.elu_in) {  // zero padding stays 0 (elu(0) = 0)
         v.x = elu1(v.x);
         v.y = elu1(v.y);
         v.z = elu1(v.z);
         v.w = elu1(v.w);
       }
-      *reinterpret_cast<float4*>(&As[buf][(tid / CPR + p * RPP) * AS + a_chunk * 4]) = v;
+      *reinterpret_cast<float4*>(&As[q][(tid / CPR + p * RPP) * AS + a_chunk * 4]) = v;
     }
 #pragma unroll
     for (int p = 0; p < BPASS; ++p)
-      *reinterpret_cast<float4*>(&Bs[buf][(b_row + p * (kThreads / (kBN / 4))) * BS + b_col]) =
-          make_float4(rb[p][0], rb[p][1], rb[p][2], rb[p][3]);
+      *reinterpret_cast<float4*>(&Bs[q][(b_row + p * BRPP) * BS + b_col]) =
+          make_float4(rb[q][p][0], rb[q][p][1], rb[q][p][2], rb[q][p][3]);
   };
 
   typedef float f4 __attribute__((ext_vector_type(4)));
-  f4 acc[2][2];
+  f4 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int lr = lane & 15, lk = lane >> 4;
-  if (nk > 0) {
-    load(0);
-    store(0);
-  }
-  __syncthreads();
-  for (int kc = 0; kc < nk; ++kc) {
-    const int buf = kc & 1;
-    if (kc + 1 < nk) load(kc + 1);
-    const float* Ab = As[buf] + (wm * 32 + lr) * AS + lk;
-    const float* Bb = Bs[buf] + lk * BS + wn * 32 + lr;
+  auto step = [&](int kc, auto S) {  // chunk kc, held in LDS buffer q = kc & 1
+    constexpr int q = decltype(S)::value;
+    if (kc + 2 < nk) load(kc + 2, S);
+    const float* Ab = As[q] + (wm * (BM / 2) + lr) * AS + lk;
+    const float* Bb = Bs[q] + lk * BS + wn * (BN / 2) + lr;
 #pragma unroll
     for (int ks = 0; ks < KC / 4; ++ks) {
-      const float a0 = Ab[ks * 4], a1 = Ab[16 * AS + ks * 4];
-      const float b0 = Bb[ks * 4 * BS], b1 = Bb[ks * 4 * BS + 16];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+      float av[TM], bv[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) av[i] = Ab[i * 16 * AS + ks * 4];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bv[j] = Bb[ks * 4 * BS + j * 16];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
     }
-    if (kc + 1 < nk) store(buf ^ 1);
+    if (kc + 1 < nk) store(std::integral_constant<int, 1 - q>{});
     __syncthreads();
+  };
+  if (nk > 0) {
+    load(0, I0{});
+    if (nk > 1) load(1, I1{});
+    store(I0{});
+  }
+  __syncthreads();
+  for (int kc = 0; kc < nk; kc += 2) {
+    step(kc, I0{});
+    if (kc + 1 < nk) step(kc + 1, I1{});
   }
 
   // epilogue: lane holds rows 4 * (lane / 16) + v, column lane % 16 of each tile
   if (a.ksplit > 1) {
-    float* part = a.partial + ((size_t)blockIdx.z * a.rows + (size_t)blockIdx.x * kBM) * a.cout_pad;
+    float* part = a.partial + ((size_t)blockIdx.z * a.rows + (size_t)blockIdx.x * BM) * a.cout_pad;
 #pragma unroll
-    for (int tm = 0; tm < 2; ++tm)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int v = 0; v < 4; ++v)
 #pragma unroll
-        for (int tn = 0; tn < 2; ++tn)
-          part[(size_t)(wm * 32 + tm * 16 + 4 * lk + v) * a.cout_pad + n0 + wn * 32 + tn * 16 + lr] = acc[tm][tn][v];
+        for (int j = 0; j < TN; ++j)
+          part[(size_t)(wm * (BM / 2) + i * 16 + 4 * lk + v) * a.cout_pad + n0 + wn * (BN / 2) + j * 16 + lr] =
+              acc[i][j][v];
     return;
   }
 #pragma unroll
-  for (int tm = 0; tm < 2; ++tm) {
+  for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int m = m0 + wm * 32 + tm * 16 + 4 * lk + v;
+      const int m = m0 + wm * (BM / 2) + i * 16 + 4 * lk + v;
       if (m >= M) continue;
 #pragma unroll
-      for (int tn = 0; tn < 2; ++tn) {
-        const int o = n0 + wn * 32 + tn * 16 + lr;
-        if (o < a.cout) conv_store(a, sub, m, o, acc[tm][tn][v]);
+      for (int j = 0; j < TN; ++j) {
+        const int o = n0 + wn * (BN / 2) + j * 16 + lr;
+        if (o < a.cout) conv_store(a, sub, m, o, acc[i][j][v]);
       }
     }
   }
@@ -184,11 +203,11 @@ __global__ __launch_bounds__(256) void k_conv_finish(ConvLaunch a) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (size_t)a.rows * a.cout) return;
   const int row = (int)(i / a.cout), o = (int)(i - (size_t)row * a.cout);
-  const int tile = row / kBM;
+  const int tile = row / 64;
   int si = 0;
   while (si + 1 < a.nsub && tile >= a.subs[si + 1].tile0) ++si;
   const ConvSub* sub = a.subs + si;
-  const int m = (tile - sub->tile0) * kBM + (row - tile * kBM);
+  const int m = (tile - sub->tile0) * 64 + (row - tile * 64);
   if (m >= a.n * sub->gy * sub->gx) return;
   float v = 0.f;
   for (int z = 0; z < a.ksplit; ++z) v += a.partial[((size_t)z * a.rows + row) * a.cout_pad + o];
@@ -324,9 +343,9 @@ __global__ void k_overlap_add(const float* __restrict__ wf, int H, int n_fft, in
 void conv_launch(const ConvLaunch& a, int tiles_m, int tiles_n, hipStream_t s) {
   const dim3 grid(tiles_m, tiles_n, a.ksplit);
   if (a.cin % 32 == 0)
-    hipLaunchKernelGGL(k_conv<32>, grid, dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((k_conv<64, 64, 32>), grid, dim3(kThreads), 0, s, a);
   else
-    hipLaunchKernelGGL(k_conv<16>, grid, dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((k_conv<64, 64, 16>), grid, dim3(kThreads), 0, s, a);
   MRT_HIP_CHECK(hipGetLastError());
   if (a.ksplit > 1) {
     const size_t n = static_cast<size_t>(a.rows) * a.cout;
