@@ -15,8 +15,9 @@ Beside it (not the headline value): 32 independent streams decoded as one
 batch (aggregate RVQ tokens/s, per-stream RTF), the encoder prefill alone
 at 1 / 8 / 32 streams (matrix-core utilisation), the decode section with
 speculative depth decoding at rejected and at accepted drafts, and the codec
-decode of one chunk (RVQ ids -> audio, fp32 matrix-core utilisation);
---no-batched skips them.
+decode of one chunk (RVQ ids -> audio, fp32 matrix-core utilisation), and the
+whole generate_chunk with audio (tokens + codec + crossfade); --no-batched
+skips them.
 """
 
 from __future__ import annotations
@@ -332,6 +333,41 @@ def bench_codec(reps=10, frames=51, cpu=True):
     return res
 
 
+def bench_full_chunk(model, cfg, chunks=10, warmup=2, seed=1234):
+    """The whole generate_chunk with audio (system.cpp:177-440) on the device
+    stream: encoder (pipelined), 50 x 16 decode, llm_to_rvq + roll, then the
+    codec decode of 51 frames and the crossfade on the codec's stream while
+    the next chunk's encoder runs.  Wall ms per chunk, host waits included."""
+    import mrt_df
+    import synth_bundle
+    import system
+    scfg = system.SystemConfig()
+    rng = np.random.default_rng(42)
+    style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+    sess = system.DeviceStreamingSession(model, scfg, style=style, seed=seed, temperature=1.1, top_k=40,
+                                         guidance_weight=5.0, pipeline_encoder=True)
+    codec = mrt_df.Codec(synth_bundle.make_codec_weights(synth_bundle.CodecShape.reference()), max_frames=51)
+    sess.attach_codec(codec)
+    for _ in range(warmup):
+        sess.generate_chunk()
+    wall = []
+    for _ in range(chunks):
+        t0 = time.perf_counter()
+        sess.generate_chunk()
+        wall.append((time.perf_counter() - t0) * 1e3)
+    assert sess.last_audio.shape == (96000, 2) and np.isfinite(sess.last_audio).all()
+    sess.stream.close()
+    codec.close()
+    ms = sorted(wall)
+    res = {"chunks_timed": chunks, "chunk_ms_mean": float(np.mean(wall)), "chunk_ms_p50": percentile(ms, 50),
+           "chunk_ms_p99": percentile(ms, 99), "rtf": 2000.0 / float(np.mean(wall)),
+           "audio": "96000 stereo samples per chunk at 48 kHz, fp32",
+           "data": "synthetic: seeded Depthformer and codec weights, free-running tokens"}
+    print(f"[bench] full chunk with audio: {res['chunk_ms_mean']:.1f} ms mean (p99 {res['chunk_ms_p99']:.1f}), "
+          f"RTF {res['rtf']:.1f}", file=sys.stderr, flush=True)
+    return res
+
+
 def bench_encoder(model, cfg, batches=(1, 8, 32), reps=3):
     """Encoder prefill alone over 2 x batch x 1006 token rows (CFG pairs): ms and
     matrix-core utilisation against the dense bf16 peak."""
@@ -519,8 +555,9 @@ def main():
                 "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
                 "launches_timed": dk["launches"]}
 
-    batched = encoder = spec = codec = None
+    batched = encoder = spec = codec = full = None
     if not args.no_batched and args.dtype == "bf16":
+        full = bench_full_chunk(model, cfg)
         batched = bench_batched(model, cfg)
         encoder = bench_encoder(model, cfg)
         spec = bench_speculative(model, cfg, system.build_encoder_inputs(sess.context, scfg, style))
@@ -568,6 +605,7 @@ def main():
         "encoder_prefill": encoder,
         "speculative": spec,
         "codec_decode": codec,
+        "full_chunk_with_audio": full,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

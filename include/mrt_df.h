@@ -211,6 +211,8 @@ typedef struct mrt_stream_config {
   int32_t decoder_codec_rvq_depth; /* 16 (= the model's rvq_depth) */
   int32_t mask_token;              /* 1  vocab_mask_token */
   int32_t codec_offset;            /* 2  vocab_codec_offset */
+  int32_t crossfade_frames;        /* 1  crossfade_length_frames (0.04 s x 25 Hz) */
+  int32_t samples_per_frame;       /* 1920 codec_sample_rate / codec_frame_rate */
 } mrt_stream_config;
 
 /* GenerateChunkOptions (system.h:86-121). */
@@ -227,6 +229,7 @@ typedef struct mrt_chunk_opts {
 } mrt_chunk_opts;
 
 typedef struct mrt_df_stream mrt_df_stream;
+typedef struct mrt_codec mrt_codec; /* the codec decode handle (declared below) */
 
 /* SystemConfig defaults (system.h:44-83) / GenerateChunkOptions defaults. */
 void mrt_stream_config_default(mrt_stream_config* cfg);
@@ -250,6 +253,22 @@ void mrt_df_stream_destroy(mrt_df_stream* s);
  * (system.cpp:218-232, 334-370). */
 int mrt_df_stream_generate_chunk(mrt_df_stream* s, const int32_t* style, const mrt_chunk_opts* opts,
                                  int32_t* llm_out, int32_t* rvq_out);
+
+/* The whole System::generate_chunk (system.cpp:177-440) on the device: the
+ * token half as mrt_df_stream_generate_chunk, then the codec decode of
+ * [crossfade_frames context frames before the chunk (ids clamped at 0; zeros
+ * on chunk 0), the chunk's codes] (system.cpp:294-313, 373-390) on the
+ * attached codec's stream -- overlapping the pipelined encoder of the next
+ * chunk -- and the equal-power crossfade against the previous chunk's tail
+ * (system.cpp:395-440).  audio_out: host (chunk_frames * samples_per_frame,
+ * 2) float32, L/R interleaved (GenerateResult::waveform).  The crossfade
+ * applies when the previous call of the stream also produced audio. */
+int mrt_df_stream_generate_chunk_audio(mrt_df_stream* s, const int32_t* style, const mrt_chunk_opts* opts,
+                                       int32_t* llm_out, int32_t* rvq_out, float* audio_out);
+/* Attach a codec (not owned; NULL detaches) to a stream.  Its rvq_levels and
+ * codebook_size must equal the stream's and its max_frames must be at least
+ * chunk_frames + crossfade_frames. */
+int mrt_df_stream_attach_codec(mrt_df_stream* s, mrt_codec* c);
 
 /* SystemState::context_tokens and chunk_index in and out: host
  * (context_frames, levels) int32, -1 = empty.  set_context drops a
@@ -305,8 +324,6 @@ int mrt_df_batch_read_enc_out(mrt_df_batch* b, void* dst, size_t bytes);
  * and istft_postprocess (spectrostream.cpp:593-681), all in fp32 as the
  * reference runs them (system.cpp:118-119).
  * ------------------------------------------------------------------------ */
-typedef struct mrt_codec mrt_codec;
-
 typedef struct {
   int32_t embedding_dim;   /* 256: SpectroStreamDecoder::kEmbeddingDim */
   int32_t proj_channels;   /* 2560: input_proj 256 -> 2560 -> 2560 (spectrostream.cpp:356-362) */

@@ -155,6 +155,20 @@ mrt::CodecConfig to_codec_config(const mrt_codec_config* c, int* max_frames) {
   return k;
 }
 
+mrt::ChunkOpts to_chunk_opts(const mrt_chunk_opts* opts) {
+  mrt::ChunkOpts o;
+  o.temperature = opts->temperature;
+  o.top_k = opts->top_k;
+  o.guidance_weight = opts->guidance_weight;
+  o.has_seed = opts->has_seed != 0;
+  o.seed = opts->seed;
+  o.pipeline_encoder = opts->pipeline_encoder != 0;
+  o.use_graph = opts->use_graph != 0;
+  o.teacher = opts->teacher;
+  o.speculative = opts->speculative != 0;
+  return o;
+}
+
 mrt::StreamConfig to_stream_config(const mrt_stream_config* c) {
   mrt::StreamConfig k;
   k.chunk_frames = c->chunk_frames;
@@ -165,6 +179,8 @@ mrt::StreamConfig to_stream_config(const mrt_stream_config* c) {
   k.levels = c->decoder_codec_rvq_depth;
   k.mask = c->mask_token;
   k.codec_offset = c->codec_offset;
+  k.crossfade_frames = c->crossfade_frames;
+  k.samples_per_frame = c->samples_per_frame;
   return k;
 }
 
@@ -340,6 +356,8 @@ void mrt_stream_config_default(mrt_stream_config* cfg) {
   cfg->decoder_codec_rvq_depth = k.levels;
   cfg->mask_token = k.mask;
   cfg->codec_offset = k.codec_offset;
+  cfg->crossfade_frames = k.crossfade_frames;
+  cfg->samples_per_frame = k.samples_per_frame;
 }
 
 void mrt_chunk_opts_default(mrt_chunk_opts* opts) {
@@ -375,18 +393,20 @@ int mrt_df_stream_generate_chunk(mrt_df_stream* s, const int32_t* style, const m
                                  int32_t* llm_out, int32_t* rvq_out) {
   return guarded([&] {
     if (!opts) throw mrt::Error(MRT_ERR_INVALID, "null argument");
-    mrt::ChunkOpts o;
-    o.temperature = opts->temperature;
-    o.top_k = opts->top_k;
-    o.guidance_weight = opts->guidance_weight;
-    o.has_seed = opts->has_seed != 0;
-    o.seed = opts->seed;
-    o.pipeline_encoder = opts->pipeline_encoder != 0;
-    o.use_graph = opts->use_graph != 0;
-    o.teacher = opts->teacher;
-    o.speculative = opts->speculative != 0;
-    SS(s).generate_chunk(style, o, llm_out, rvq_out);
+    SS(s).generate_chunk(style, to_chunk_opts(opts), llm_out, rvq_out);
   });
+}
+
+int mrt_df_stream_generate_chunk_audio(mrt_df_stream* s, const int32_t* style, const mrt_chunk_opts* opts,
+                                       int32_t* llm_out, int32_t* rvq_out, float* audio_out) {
+  return guarded([&] {
+    if (!opts || !audio_out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    SS(s).generate_chunk_audio(style, to_chunk_opts(opts), llm_out, rvq_out, audio_out);
+  });
+}
+
+int mrt_df_stream_attach_codec(mrt_df_stream* s, mrt_codec* c) {
+  return guarded([&] { SS(s).attach_codec(c ? &CC(c) : nullptr); });
 }
 
 int mrt_df_stream_set_context(mrt_df_stream* s, const int32_t* context, int64_t chunk_index) {

@@ -53,6 +53,42 @@ Stream::~Stream() {
   if (d_style_) (void)hipFree(d_style_);
   if (d_err_) (void)hipFree(d_err_);
   if (h_stage_) (void)hipHostFree(h_stage_);
+  if (codec_ && codec_->stream) (void)hipStreamSynchronize(codec_->stream);
+  for (void* q : {static_cast<void*>(d_codec_tok_), static_cast<void*>(d_audio_), static_cast<void*>(d_audio_out_),
+                  static_cast<void*>(d_tail_)})
+    if (q) (void)hipFree(q);
+  if (h_audio_) (void)hipHostFree(h_audio_);
+  if (ev_ctx_) (void)hipEventDestroy(ev_ctx_);
+}
+
+void Stream::attach_codec(Codec* c) {
+  MRT_HIP_CHECK(hipSetDevice(st.m.device));
+  if (codec_ && codec_->stream) MRT_HIP_CHECK(hipStreamSynchronize(codec_->stream));
+  codec_ = nullptr;
+  tail_valid_ = false;
+  if (!c) return;
+  const StreamConfig& k = cfg;
+  MRT_REQUIRE(c->device == st.m.device, "attach_codec: the codec is on another device");
+  MRT_REQUIRE(c->cfg.levels == k.levels && c->cfg.codebook == k.codebook,
+              "attach_codec: the codec's rvq_levels / codebook_size differ from the stream's");
+  MRT_REQUIRE(c->max_frames >= k.chunk_frames + k.crossfade_frames,
+              "attach_codec: the codec's max_frames is below chunk_frames + crossfade_frames");
+  MRT_REQUIRE(k.crossfade_frames >= 0 && k.crossfade_frames <= k.context_frames - k.chunk_frames,
+              "attach_codec: crossfade_frames must fit in the context before the chunk");
+  MRT_REQUIRE(k.samples_per_frame == c->cfg.samples_per_frame, "attach_codec: samples per frame differ");
+  const size_t nf = static_cast<size_t>(k.chunk_frames + k.crossfade_frames);
+  const size_t T = nf * k.samples_per_frame;
+  const size_t xf = static_cast<size_t>(k.crossfade_frames) * k.samples_per_frame;
+  if (!d_codec_tok_) {
+    MRT_HIP_CHECK(hipMalloc(&d_codec_tok_, nf * k.levels * 4));
+    MRT_HIP_CHECK(hipMalloc(&d_audio_, T * 2 * 4));
+    MRT_HIP_CHECK(hipMalloc(&d_audio_out_, std::max<size_t>(T - xf, 1) * 2 * 4));
+    MRT_HIP_CHECK(hipMalloc(&d_tail_, std::max<size_t>(xf, 1) * 2 * 4));
+    MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_audio_), std::max<size_t>(T - xf, 1) * 2 * 4,
+                                hipHostMallocDefault));
+    MRT_HIP_CHECK(hipEventCreateWithFlags(&ev_ctx_, hipEventDisableTiming));
+  }
+  codec_ = c;
 }
 
 // d_style_ <- style (only when it differs from what the device holds).
@@ -77,7 +113,9 @@ void Stream::build_and_encode(const int32_t* style) {
   st.encode_device();
 }
 
-void Stream::generate_chunk(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out) {
+// Encoder (or the pipelined one), decode, llm_to_rvq and the roll; returns
+// with the state's stream idle.
+void Stream::token_half(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out) {
   const StreamConfig& c = cfg;
   const int vocab = st.m.cfg.vocab_size;
   MRT_HIP_CHECK(hipSetDevice(st.m.device));
@@ -124,16 +162,50 @@ void Stream::generate_chunk(const int32_t* style, const ChunkOpts& o, int32_t* l
     throw Error(1, "llm_to_rvq: token levels do not match expected RVQ structure");
   }
   if (rvq_out) std::copy(h_stage_, h_stage_ + n, rvq_out);
+}
 
-  // Next chunk's encoder kicked off before returning (system.cpp:334-370).
-  if (o.pipeline_encoder) {
-    build_and_encode(style);
-    pre_valid_ = true;
-    pre_masked_ = style == nullptr;
-    if (style) pre_style_.assign(style, style + c.style_depth);
-  }
+// Next chunk's encoder kicked off before returning (system.cpp:334-370).
+void Stream::kick_pipeline(const int32_t* style) {
+  build_and_encode(style);
+  pre_valid_ = true;
+  pre_masked_ = style == nullptr;
+  if (style) pre_style_.assign(style, style + cfg.style_depth);
+}
+
+void Stream::generate_chunk(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out) {
+  token_half(style, o, llm_out, rvq_out);
+  if (o.pipeline_encoder) kick_pipeline(style);
+  tail_valid_ = false;  // this chunk's audio was not made: no tail for the next crossfade
   ++chunk_index;
 }
+
+void Stream::generate_chunk_audio(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out,
+                                  float* audio_out) {
+  MRT_REQUIRE(codec_ != nullptr, "generate_chunk_audio: no codec attached");
+  MRT_REQUIRE(audio_out != nullptr, "generate_chunk_audio: null audio buffer");
+  const StreamConfig& c = cfg;
+  const bool first = chunk_index == 0;
+  token_half(style, o, llm_out, rvq_out);
+  // decoder input from the rolled context, then the codec on its own stream
+  const int nf = c.chunk_frames + c.crossfade_frames;
+  codec_frames(d_ctx_, c.context_frames, c.levels, c.chunk_frames, c.crossfade_frames, first, d_codec_tok_,
+               st.stream);
+  MRT_HIP_CHECK(hipEventRecord(ev_ctx_, st.stream));
+  MRT_HIP_CHECK(hipStreamWaitEvent(codec_->stream, ev_ctx_, 0));
+  codec_->decode_device(d_codec_tok_, nf, d_audio_);
+  const int T = nf * c.samples_per_frame, xf = c.crossfade_frames * c.samples_per_frame;
+  // system.cpp:423-425: the ramp needs a previous tail of the same length
+  crossfade(d_audio_, T, xf, !first && tail_valid_ && xf > 0 && T - xf >= xf, d_tail_, d_audio_out_, codec_->stream);
+  const size_t na = static_cast<size_t>(T - xf) * 2;
+  MRT_HIP_CHECK(hipMemcpyAsync(h_audio_, d_audio_out_, na * 4, hipMemcpyDeviceToHost, codec_->stream));
+  // the next chunk's encoder runs on the state's stream while the codec runs
+  if (o.pipeline_encoder) kick_pipeline(style);
+  MRT_HIP_CHECK(hipStreamSynchronize(codec_->stream));
+  std::copy(h_audio_, h_audio_ + na, audio_out);
+  tail_valid_ = xf > 0;
+  ++chunk_index;
+}
+
 
 void Stream::set_context(const int32_t* ctx_host, int64_t index) {
   const StreamConfig& c = cfg;
@@ -148,6 +220,7 @@ void Stream::set_context(const int32_t* ctx_host, int64_t index) {
   MRT_HIP_CHECK(hipStreamSynchronize(st.stream));
   chunk_index = index;
   pre_valid_ = false;
+  tail_valid_ = false;
 }
 
 void Stream::get_context(int32_t* ctx_host, int64_t* index) {

@@ -5,6 +5,7 @@
 #include <cstdint>
 #include <vector>
 
+#include "codec.hpp"
 #include "common.hpp"
 #include "model.hpp"
 
@@ -22,6 +23,13 @@ bool llm_to_rvq_roll_fits(int frames, int levels);
 void llm_to_rvq_roll(const int* llm, int n, int levels, int C, int offset, int* ctx, int frames, int* err,
                      hipStream_t st);
 
+// The codec input (n + xf, levels) of a chunk from the rolled context
+// (system.cpp:294-313); first: the crossfade rows are zeros.
+void codec_frames(const int* ctx, int frames, int levels, int n, int xf, bool first, int* out, hipStream_t st);
+// Crossfade (system.cpp:410-437) of audio (T, 2) against tail (xf, 2) into
+// out (T - xf, 2); tail <- audio's last xf samples.
+void crossfade(const float* audio, int T, int xf, bool fade, float* tail, float* out, hipStream_t st);
+
 // The SystemConfig fields the token half reads (system.h:44-83).
 struct StreamConfig {
   int chunk_frames = 50;       // chunk_length_frames
@@ -32,6 +40,8 @@ struct StreamConfig {
   int levels = 16;             // decoder_codec_rvq_depth
   int mask = 1;                // vocab_mask_token
   int codec_offset = 2;        // vocab_codec_offset
+  int crossfade_frames = 1;    // crossfade_length_frames (0.04 s at 25 Hz)
+  int samples_per_frame = 1920;  // codec_sample_rate / codec_frame_rate
   int enc_len() const { return context_frames * enc_depth + style_depth; }
 };
 
@@ -68,6 +78,15 @@ class Stream {
   // style: host (style_depth) ids or null (masked).  llm_out / rvq_out: host
   // (chunk_frames, levels) or null.
   void generate_chunk(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out);
+  // The whole System::generate_chunk (system.cpp:177-440): the token half,
+  // then the codec decode of [the crossfade frame, the chunk] on the attached
+  // codec's stream (overlapping the pipelined encoder of the next chunk) and
+  // the crossfade.  audio_out: host (chunk_frames * samples_per_frame, 2).
+  void generate_chunk_audio(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out,
+                            float* audio_out);
+  // Not owned; null detaches.  Its levels / codebook must be the stream's and
+  // its max_frames >= chunk_frames + crossfade_frames.
+  void attach_codec(Codec* c);
   void set_context(const int32_t* ctx_host, int64_t index);  // (context_frames, levels), -1 = empty
   void get_context(int32_t* ctx_host, int64_t* index);
   bool pre_encoded() const { return pre_valid_; }
@@ -75,6 +94,13 @@ class Stream {
  private:
   void upload_style(const int32_t* style);
   void build_and_encode(const int32_t* style);
+  void token_half(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out);
+  void kick_pipeline(const int32_t* style);
+  Codec* codec_ = nullptr;
+  int* d_codec_tok_ = nullptr;
+  float *d_audio_ = nullptr, *d_audio_out_ = nullptr, *d_tail_ = nullptr, *h_audio_ = nullptr;
+  bool tail_valid_ = false;  // d_tail_ holds the previous chunk's tail (crossfade applies)
+  hipEvent_t ev_ctx_ = nullptr;
   int* d_ctx_ = nullptr;
   int* d_style_ = nullptr;
   int* d_err_ = nullptr;

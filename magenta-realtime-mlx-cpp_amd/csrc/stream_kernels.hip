@@ -77,6 +77,42 @@ __global__ __launch_bounds__(kRollThreads) void k_llm_to_rvq_roll(const int* __r
   }
 }
 
+// The codec input of a chunk (system.cpp:294-313) from the rolled context
+// (frames, levels): xf rows = the context's rows before the chunk's (the last
+// rows before the roll), negative ids clamped to 0, zeros on the first chunk;
+// then the chunk's n rows.
+__global__ void k_codec_frames(const int* __restrict__ ctx, int frames, int levels, int n, int xf, int first,
+                               int* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (n + xf) * levels) return;
+  const int f = i / levels;
+  const int v = ctx[(size_t)(frames - n - xf) * levels + i];
+  out[i] = f < xf ? (first ? 0 : max(v, 0)) : v;
+}
+
+// system.cpp:410-437: out = audio[0, T - xf) with its first xf samples ramped
+// in (sin(t pi/2)) against the previous tail ramped out (sin((1 - t) pi/2)),
+// t = i / (xf - 1), unless `fade` is 0; the tail becomes audio[T - xf, T).
+// Thread i reads tail[i] before it writes it (i < 2 xf), so the update is
+// race-free.
+__global__ void k_crossfade(const float* __restrict__ audio, int T, int xf, int fade, float* __restrict__ tail,
+                            float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 2 * T) return;
+  const int j = i >> 1;
+  if (j < T - xf) {
+    float v = audio[i];
+    if (fade && j < xf) {
+      const float t = (float)j / (float)(xf - 1 == 0 ? 1 : xf - 1);
+      const float fin = sinf(t * 1.5707963267948966f);
+      const float fout = sinf((1.0f - t) * 1.5707963267948966f);
+      v = v * fin + tail[i] * fout;
+    }
+    out[i] = v;
+  }
+  if (i < 2 * xf) tail[i] = audio[2 * (T - xf) + i];
+}
+
 }  // namespace
 
 void encoder_inputs(const int* ctx, int frames, int levels, int e, const int* style, int s, int C, int offset,
@@ -93,6 +129,18 @@ void llm_to_rvq_roll(const int* llm, int n, int levels, int C, int offset, int* 
                      hipStream_t st) {
   hipLaunchKernelGGL(k_llm_to_rvq_roll, dim3(1), dim3(kRollThreads), 0, st, llm, n, levels, C, offset, ctx, frames,
                      err);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void codec_frames(const int* ctx, int frames, int levels, int n, int xf, bool first, int* out, hipStream_t st) {
+  const int m = (n + xf) * levels;
+  hipLaunchKernelGGL(k_codec_frames, dim3((m + 255) / 256), dim3(256), 0, st, ctx, frames, levels, n, xf, first ? 1 : 0,
+                     out);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void crossfade(const float* audio, int T, int xf, bool fade, float* tail, float* out, hipStream_t st) {
+  hipLaunchKernelGGL(k_crossfade, dim3((2 * T + 255) / 256), dim3(256), 0, st, audio, T, xf, fade ? 1 : 0, tail, out);
   MRT_HIP_CHECK(hipGetLastError());
 }
 

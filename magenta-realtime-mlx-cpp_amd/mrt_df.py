@@ -67,7 +67,8 @@ class _GenOpts(ctypes.Structure):
 class _StreamConfig(ctypes.Structure):
     _fields_ = [(f, ctypes.c_int32) for f in (
         "chunk_frames", "context_frames", "codebook_size", "encoder_codec_rvq_depth",
-        "encoder_style_rvq_depth", "decoder_codec_rvq_depth", "mask_token", "codec_offset")]
+        "encoder_style_rvq_depth", "decoder_codec_rvq_depth", "mask_token", "codec_offset",
+        "crossfade_frames", "samples_per_frame")]
 
 
 class _ChunkOpts(ctypes.Structure):
@@ -214,6 +215,10 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_stream_set_context": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.c_int64]),
         "mrt_df_stream_get_context": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int64)]),
         "mrt_df_stream_state": (i32, [vp, ctypes.POINTER(vp)]),
+        "mrt_df_stream_generate_chunk_audio": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(_ChunkOpts),
+                                                     ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+                                                     ctypes.POINTER(ctypes.c_float)]),
+        "mrt_df_stream_attach_codec": (i32, [vp, vp]),
         "mrt_df_batch_create": (i32, [vp, i32, i32, i32, ctypes.POINTER(vp)]),
         "mrt_df_batch_destroy": (None, [vp]),
         "mrt_df_batch_encode": (i32, [vp, ctypes.POINTER(ctypes.c_int32)]),
@@ -497,6 +502,8 @@ class StreamConfig:
     decoder_codec_rvq_depth: int = 16
     mask_token: int = 1
     codec_offset: int = 2
+    crossfade_frames: int = 1
+    samples_per_frame: int = 1920
 
     @property
     def encoder_length(self) -> int:
@@ -534,9 +541,21 @@ class Stream:
         _check(self.lib, self.lib.mrt_df_stream_state(h, ctypes.byref(sh)))
         self.state = State._view(model, sh, 2, cfg.chunk_frames, cfg.encoder_length)
 
+    def attach_codec(self, codec: Optional["Codec"]) -> None:
+        """Decode each chunk's codes to audio with ``codec`` (None detaches)."""
+        _check(self.lib, self.lib.mrt_df_stream_attach_codec(self._h, codec._h if codec is not None else None))
+        self._codec = codec  # kept alive while attached
+
+    def generate_chunk_audio(self, style: Optional[Sequence[int]], opts: ChunkOptions,
+                             teacher: Optional[np.ndarray] = None):
+        """The whole System::generate_chunk: (llm ids, rvq codes, audio
+        (chunk_frames * samples_per_frame, 2) float32)."""
+        return self.generate_chunk(style, opts, teacher, audio=True)
+
     def generate_chunk(self, style: Optional[Sequence[int]], opts: ChunkOptions,
-                       teacher: Optional[np.ndarray] = None):
-        """Returns (llm ids, rvq codes), both (chunk_frames, levels) int32."""
+                       teacher: Optional[np.ndarray] = None, audio: bool = False):
+        """Returns (llm ids, rvq codes), both (chunk_frames, levels) int32
+        (and the chunk's audio with ``audio``)."""
         cfg = self.cfg
         shape = (cfg.chunk_frames, cfg.decoder_codec_rvq_depth)
         o = _ChunkOpts(temperature=opts.temperature, top_k=opts.top_k, guidance_weight=opts.guidance_weight,
@@ -559,6 +578,12 @@ class Stream:
                 raise ValueError("style_tokens_lm size != encoder_style_rvq_depth")
         llm = np.zeros(shape, dtype=np.int32)
         rvq = np.zeros(shape, dtype=np.int32)
+        if audio:
+            wav = np.zeros((cfg.chunk_frames * cfg.samples_per_frame, 2), dtype=np.float32)
+            _check(self.lib, self.lib.mrt_df_stream_generate_chunk_audio(
+                self._h, _i32_ptr(st) if st is not None else None, ctypes.byref(o), _i32_ptr(llm), _i32_ptr(rvq),
+                wav.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+            return llm, rvq, wav
         _check(self.lib, self.lib.mrt_df_stream_generate_chunk(
             self._h, _i32_ptr(st) if st is not None else None, ctypes.byref(o), _i32_ptr(llm), _i32_ptr(rvq)))
         return llm, rvq

@@ -136,6 +136,13 @@ class DeviceStreamingSession:
                                         guidance_weight=guidance_weight,
                                         pipeline_encoder=pipeline_encoder, use_graph=use_graph)
         self.last_llm: Optional[np.ndarray] = None
+        self.last_audio: Optional[np.ndarray] = None
+        self.codec = None
+
+    def attach_codec(self, codec: "mrt_df.Codec") -> None:
+        """From now on each chunk also returns audio (the whole generate_chunk)."""
+        self.stream.attach_codec(codec)
+        self.codec = codec
 
     @property
     def chunk_index(self) -> int:
@@ -148,5 +155,8 @@ class DeviceStreamingSession:
     def generate_chunk(self) -> np.ndarray:
         """Returns the chunk's (50, 16) RVQ ids and advances the device context."""
         self.opts.seed = self.base_seed + self.chunk_index
-        self.last_llm, rvq = self.stream.generate_chunk(self.style, self.opts)
+        if self.codec is not None:
+            self.last_llm, rvq, self.last_audio = self.stream.generate_chunk_audio(self.style, self.opts)
+        else:
+            self.last_llm, rvq = self.stream.generate_chunk(self.style, self.opts)
         return rvq

@@ -8,8 +8,10 @@ Restates:
   * build_vocab_masks (level ranges)   -- system.cpp:135-157
   * rvq_to_llm / llm_to_rvq            -- rvq.cpp:105-132 (upstream utils.py:106-147)
   * context roll after a chunk         -- system.cpp:320-333
+  * codec input + crossfade of a chunk -- system.cpp:294-313, 395-440
 Pinned by the upstream known answers (system_test.py:29-41, decode_test.py:26-71,
-utils_test.py:99-149) restated in tests/test_oracle_system.py.
+utils_test.py:99-149) restated in tests/test_oracle_system.py; the crossfade
+by its closed form (equal-power sine ramp) in the same file.
 """
 
 from __future__ import annotations
@@ -140,3 +142,33 @@ def roll_context(context_tokens: np.ndarray, new_rvq: np.ndarray) -> np.ndarray:
     out[:] = ctx[src]
     out[frames - n:] = new
     return out
+
+
+def codec_input_frames(context_before: np.ndarray, chunk_rvq: np.ndarray, chunk_index: int,
+                       xf_frames: int = 1) -> np.ndarray:
+    """system.cpp:294-313: the decoder input of a chunk: the context's last
+    xf_frames rows before the roll (negative ids clamped to 0; zeros on chunk
+    0), then the chunk's RVQ ids."""
+    ctx = np.asarray(context_before, dtype=np.int32)
+    levels = ctx.shape[1]
+    xf = np.zeros((xf_frames, levels), np.int32)
+    if chunk_index > 0:
+        xf = np.maximum(ctx[ctx.shape[0] - xf_frames:], 0).astype(np.int32)
+    return np.concatenate([xf, np.asarray(chunk_rvq, dtype=np.int32)], axis=0)
+
+
+def crossfade_chunk(wave: np.ndarray, prev_tail: Optional[np.ndarray], chunk_index: int, xf_samples: int = 1920):
+    """system.cpp:395-440: (decoded, next_tail) from the chunk's waveform (T, C):
+    the last xf_samples samples become the next tail; the rest is the chunk's
+    audio, its first xf_samples ramped in (sin) against the previous tail
+    ramped out (sin of the complement), t = i / (xf_samples - 1), in float32."""
+    wave = np.asarray(wave, dtype=np.float32)
+    T = wave.shape[0]
+    nxt = wave[T - xf_samples:].copy()
+    dec = wave[:T - xf_samples].copy()
+    if chunk_index > 0 and prev_tail is not None and prev_tail.shape[0] == xf_samples and dec.shape[0] >= xf_samples:
+        t = np.arange(xf_samples, dtype=np.float32) / np.float32(max(xf_samples - 1, 1))
+        fin = np.sin(t * np.float32(1.5707963267948966)).astype(np.float32)
+        fout = np.sin((np.float32(1.0) - t) * np.float32(1.5707963267948966)).astype(np.float32)
+        dec[:xf_samples] = dec[:xf_samples] * fin[:, None] + prev_tail * fout[:, None]
+    return dec, nxt

@@ -191,3 +191,54 @@ def test_stream_full_size_matches_host_session(gpu_available):
     dev.stream.close()
     host.state.close()
     model.close()
+
+
+@pytest.mark.parametrize("pipeline", [False, True])
+def test_stream_audio_matches_oracle(tiny, pipeline):
+    """The whole System::generate_chunk (system.cpp:177-440) on the device: the
+    decoder input of each chunk is [the context frame before it (clamped; zeros
+    on chunk 0), the chunk's codes] (bit-exact through the oracle's
+    codec_input_frames), the codec output within 1e-4 of the oracle's fp32
+    decode, the crossfade against the previous chunk's tail as the oracle's
+    crossfade_chunk.  A token-only chunk in between drops the tail (no
+    crossfade on the next audio chunk)."""
+    import synth_bundle
+    from oracle import codec_oracle as CO
+    mrt_df = tiny["mrt_df"]
+    shape = synth_bundle.CodecShape.tiny()
+    w = synth_bundle.make_codec_weights(shape, levels=16, codebook=TINY_C)
+    codec = mrt_df.Codec(w, max_frames=5, channels=shape.channels(), codebook_size=TINY_C)
+    oc = CO.OracleCodec(w, CO.CodecConfig.tiny(), "fp32")
+    s = _stream(tiny)
+    s.attach_codec(codec)
+    ctx = np.full((10, 16), -1, np.int32)
+    ctx[3:6] = np.random.default_rng(3).integers(0, TINY_C, size=(3, 16))  # a mix of empty and set slots
+    s.set_context(ctx, 0)
+    tail = None
+    plan = ["audio", "audio", "audio", "tokens", "audio"]
+    for i, kind in enumerate(plan):
+        before, idx = s.get_context()
+        if kind == "tokens":
+            s.generate_chunk(tiny["style_a"], _chunk_opts(tiny, seed=300 + i, pipeline=pipeline))
+            tail = None
+            continue
+        llm, rvq, audio = s.generate_chunk_audio(tiny["style_a"], _chunk_opts(tiny, seed=300 + i, pipeline=pipeline))
+        frames = so.codec_input_frames(before, rvq, idx)
+        wave = oc.decode(frames)
+        exp, tail = so.crossfade_chunk(wave, tail, idx)
+        assert audio.shape == (4 * 1920, 2)
+        err = float(np.linalg.norm(audio - exp) / np.linalg.norm(exp))
+        print(f"chunk {i}: index {idx}, rel err {err:.2e}", flush=True)
+        assert err <= 1e-4, (i, err)
+        after, _ = s.get_context()
+        np.testing.assert_array_equal(after, so.roll_context(before, rvq))
+    s.attach_codec(None)
+    with pytest.raises(mrt_df.MrtError):
+        s.generate_chunk_audio(None, _chunk_opts(tiny, seed=9))
+    big = mrt_df.Codec(w, max_frames=4, channels=shape.channels(), codebook_size=TINY_C)
+    with pytest.raises(mrt_df.MrtError) as e:  # 4 frames + 1 crossfade frame do not fit
+        s.attach_codec(big)
+    assert "max_frames" in str(e.value)
+    s.close()
+    codec.close()
+    big.close()

@@ -104,3 +104,34 @@ def test_context_roll():
     got = so.roll_context(ctx, new)
     np.testing.assert_array_equal(got[:200], ctx[50:])
     np.testing.assert_array_equal(got[200:], new)
+
+
+def test_codec_input_frames():
+    """system.cpp:294-313: [clamped last context row | chunk ids]; zeros on chunk 0."""
+    from oracle import system_oracle as SO
+    ctx = np.arange(5 * 3).reshape(5, 3).astype(np.int32) - 2  # last row 10..12, first row has -2, -1
+    ctx[-1, 0] = -1
+    new = np.full((2, 3), 7, np.int32)
+    a = SO.codec_input_frames(ctx, new, chunk_index=3)
+    np.testing.assert_array_equal(a, [[0, 11, 12], [7, 7, 7], [7, 7, 7]])
+    b = SO.codec_input_frames(ctx, new, chunk_index=0)
+    np.testing.assert_array_equal(b[0], [0, 0, 0])
+
+
+def test_crossfade_equal_power():
+    """Ramp sin(t pi/2) in, sin((1-t) pi/2) out: at t = 0 the old tail alone,
+    at t = 1 the new audio alone, and fin^2 + fout^2 = 1 (equal power), so a
+    constant signal faded against itself keeps its power profile."""
+    from oracle import system_oracle as SO
+    xf = 5
+    wave = np.ones((12, 2), np.float32) * 2.0
+    tail = np.full((xf, 2), 3.0, np.float32)
+    dec, nxt = SO.crossfade_chunk(wave, tail, chunk_index=1, xf_samples=xf)
+    assert dec.shape == (7, 2) and nxt.shape == (xf, 2)
+    np.testing.assert_allclose(dec[0], [3.0, 3.0], rtol=1e-6)
+    np.testing.assert_allclose(dec[xf - 1], [2.0, 2.0], rtol=1e-6)
+    t = np.arange(xf) / (xf - 1)
+    np.testing.assert_allclose(dec[:xf, 0], 2 * np.sin(t * np.pi / 2) + 3 * np.cos(t * np.pi / 2), rtol=1e-5)
+    np.testing.assert_array_equal(dec[xf:], wave[xf:7])
+    dec0, _ = SO.crossfade_chunk(wave, tail, chunk_index=0, xf_samples=xf)
+    np.testing.assert_array_equal(dec0, wave[:7])
