@@ -16,8 +16,9 @@ batch (aggregate RVQ tokens/s, per-stream RTF), the encoder prefill alone
 at 1 / 8 / 32 streams (matrix-core utilisation), the decode section with
 speculative depth decoding at rejected and at accepted drafts, and the codec
 decode of one chunk (RVQ ids -> audio, fp32 matrix-core utilisation), and the
-whole generate_chunk with audio (tokens + codec + crossfade); --no-batched
-skips them.
+whole generate_chunk with audio (tokens + codec + crossfade), and the style
+model's text path (prompt ids -> MusicCoCa embedding -> style ids);
+--no-batched skips them.
 """
 
 from __future__ import annotations
@@ -368,6 +369,48 @@ def bench_full_chunk(model, cfg, chunks=10, warmup=2, seed=1234):
     return res
 
 
+def bench_style(reps=10, cpu=True):
+    """StyleModel text path (style_model.cpp:76-121): one 128-slot prompt
+    through the 12-layer MusicCoCa text encoder, the pooler and the RVQ
+    quantisation, fp32 with seeded synthetic weights.  GPU ms of embed_text
+    by HIP events, FLOPs against the dense fp32 matrix peak, the numpy oracle
+    timed once on the host."""
+    import mrt_df
+    import synth_bundle
+    cfg = mrt_df.CocaConfig()
+    w = synth_bundle.make_coca_weights(cfg)
+    sm = mrt_df.StyleModel(w, cfg)
+    rng = np.random.default_rng(5)
+    L = cfg.max_text_len
+    ids = np.zeros(L, np.int32)
+    pad = np.ones(L, np.float32)
+    ids[0], pad[0] = 1, 0
+    ids[1:13], pad[1:13] = rng.integers(2, cfg.vocab_size, 12), 0
+    for _ in range(3):
+        sm.style_tokens_lm(ids, padding=pad)
+    ms = []
+    for _ in range(reps):
+        sm.embed_text(ids, pad)
+        ms.append(sm.embed_time())
+    sm.close()
+    fl = synth_bundle.coca_flops(cfg)
+    gpu_ms = float(np.median(ms))
+    res = {"gpu_ms": gpu_ms, "flops": fl, "text_slots": L,
+           "mfma": {"bound": "mfma", "achieved": fl / (gpu_ms * 1e-3) / 1e12, "peak": MFMA_FP32_PEAK_TFLOPS,
+                    "unit": "TFLOP/s"}, "dtype": "f32", "reps": reps,
+           "data": "synthetic: seeded MusicCoCa text weights and codebooks, a random 12-id prompt"}
+    res["mfma"]["frac"] = res["mfma"]["achieved"] / MFMA_FP32_PEAK_TFLOPS
+    if cpu:  # CPU baseline leg: the numpy restatement, timed once
+        from oracle import musiccoca_oracle as M
+        t0 = time.perf_counter()
+        M.OracleCoca(w, M.CocaConfig(), "fp32").embed_text(ids, pad)
+        res["cpu_oracle_ms"] = (time.perf_counter() - t0) * 1e3
+        res["cpu_cores"] = len(os.sched_getaffinity(0))
+    print(f"[bench] style model embed_text: {gpu_ms:.3f} ms GPU ({res['mfma']['achieved']:.1f} TFLOP/s fp32)" +
+          (f"; numpy oracle {res['cpu_oracle_ms']:.0f} ms" if cpu else ""), file=sys.stderr, flush=True)
+    return res
+
+
 def bench_encoder(model, cfg, batches=(1, 8, 32), reps=3):
     """Encoder prefill alone over 2 x batch x 1006 token rows (CFG pairs): ms and
     matrix-core utilisation against the dense bf16 peak."""
@@ -460,7 +503,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--seed", type=int, default=1234)
-    ap.add_argument("--no-batched", action="store_true", help="skip the 32-stream, encoder-prefill, speculative and codec figures")
+    ap.add_argument("--no-batched", action="store_true", help="skip the 32-stream, encoder-prefill, speculative, codec and style-model figures")
     ap.add_argument("--session", default="device", choices=["device", "host"],
                     help="device: RVQ context on the device, next chunk's encoder enqueued early; "
                          "host: context on the host, encoder ids uploaded per chunk")
@@ -555,13 +598,14 @@ def main():
                 "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
                 "launches_timed": dk["launches"]}
 
-    batched = encoder = spec = codec = full = None
+    batched = encoder = spec = codec = full = style = None
     if not args.no_batched and args.dtype == "bf16":
         full = bench_full_chunk(model, cfg)
         batched = bench_batched(model, cfg)
         encoder = bench_encoder(model, cfg)
         spec = bench_speculative(model, cfg, system.build_encoder_inputs(sess.context, scfg, style))
         codec = bench_codec(cpu=not args.no_cpu_baseline)
+        style = bench_style(cpu=not args.no_cpu_baseline)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -606,6 +650,7 @@ def main():
         "speculative": spec,
         "codec_decode": codec,
         "full_chunk_with_audio": full,
+        "style_model": style,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -374,6 +374,56 @@ int mrt_codec_decode_time(mrt_codec* c, float* ms);
  * equal its size at that decode's frame count. */
 int mrt_codec_read(mrt_codec* c, int which, void* dst, size_t bytes);
 
+/* ------------------------------------------------------------------------
+ * MusicCoCa text path and style tokens (StyleModel, style_model.cpp:76-121;
+ * MusicCoCaEncoder::embed_text, musiccoca.cpp:272-294; rvq_quantization,
+ * rvq.cpp:24-62), fp32 as the reference's StyleModel default.  The
+ * SentencePiece tokenizer stays with the caller: ids come in laid out as
+ * StyleModel::tokenize_text_ids (style_model.cpp:52-74) does -- BOS (1),
+ * the lower-cased prompt's ids, zeros; padding 1.0 on the padded slots.
+ * ------------------------------------------------------------------------ */
+typedef struct mrt_coca mrt_coca;
+
+typedef struct {
+  int32_t d_model;       /* 768  MusicCoCaConfig (musiccoca.h:151-162) */
+  int32_t num_heads;     /* 12 */
+  int32_t d_head;        /* 64 */
+  int32_t d_ff;          /* 3072 */
+  int32_t num_layers;    /* 12 */
+  int32_t pooler_d_head; /* 256 */
+  int32_t vocab_size;    /* 64000 */
+  int32_t max_text_len;  /* 128  StyleModel::kMaxTextLength */
+  int32_t rvq_depth;     /* 12   StyleModel::kRVQDepth */
+  int32_t codebook_size; /* 1024 StyleModel::kRVQCodebookSize */
+} mrt_coca_config;
+
+#define MRT_COCA_BUF_EMBEDDING 0 /* (d_model) the last embedding; 1 + i: text layer i's output (max_text_len, d_model) */
+
+void mrt_coca_config_default(mrt_coca_config* cfg);
+/* StyleModel(encoder_bundle, codebooks_bundle) (style_model.cpp:37-50): the
+ * text-path keys of the MusicCoCa bundle (Linear weights (out, in)) and the
+ * "codebooks" tensor (K >= rvq_depth, codebook_size, d_model). */
+int mrt_coca_create(const char* encoder_path, const char* codebooks_path, const mrt_coca_config* cfg, int device,
+                    mrt_coca** out);
+int mrt_coca_create_from_tensors(int n, const char* const* names, const float* const* data,
+                                 const int64_t* const* shapes, const int32_t* ndims, const mrt_coca_config* cfg,
+                                 int device, mrt_coca** out);
+void mrt_coca_destroy(mrt_coca* h);
+/* MusicCoCaEncoder::embed_text of one prompt: ids (max_text_len) int32 and
+ * padding (max_text_len) float, host -> embedding (d_model) float, host. */
+int mrt_coca_embed_text(mrt_coca* h, const int32_t* ids, const float* padding, float* embedding);
+/* StyleModel::tokenize: embedding host (d_model), or NULL for the last
+ * mrt_coca_embed_text result -> tokens (rvq_depth) int32, host. */
+int mrt_coca_tokenize(mrt_coca* h, const float* embedding, int32_t* tokens);
+/* StyleModel::style_tokens_lm: embed, tokenize, keep the first style_depth
+ * levels, then offset + level * codebook + token (rvq_to_llm, rvq.cpp:98-103). */
+int mrt_coca_style_tokens_lm(mrt_coca* h, const int32_t* ids, const float* padding, int style_depth,
+                             int style_codebook_size, int vocab_style_offset, int32_t* out);
+/* GPU ms of the last embed_text (HIP events on the handle's stream). */
+int mrt_coca_embed_time(mrt_coca* h, float* ms);
+/* Copy of an intermediate of the last embed_text (MRT_COCA_BUF_*); bytes must match. */
+int mrt_coca_read(mrt_coca* h, int which, void* dst, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,11 +28,13 @@ SOURCES = [
     "batch_kernels.hip",
     "spec_kernels.hip",
     "codec_kernels.hip",
+    "coca_kernels.hip",
     "safetensors.cpp",
     "model.cpp",
     "stream.cpp",
     "batch.cpp",
     "codec.cpp",
+    "coca.cpp",
     "api.cpp",
 ]
 

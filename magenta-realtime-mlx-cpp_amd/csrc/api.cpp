@@ -7,6 +7,7 @@
 #include <string>
 
 #include "batch.hpp"
+#include "coca.hpp"
 #include "codec.hpp"
 #include "model.hpp"
 #include "stream.hpp"
@@ -27,6 +28,10 @@ struct mrt_df_batch {
 
 struct mrt_codec {
   std::unique_ptr<mrt::Codec> codec;
+};
+
+struct mrt_coca {
+  std::unique_ptr<mrt::Coca> coca;
 };
 
 struct mrt_df_stream {
@@ -132,6 +137,28 @@ mrt::Batch& BB(mrt_df_batch* b) {
 mrt::Stream& SS(mrt_df_stream* s) {
   if (!s || !s->stream) throw mrt::Error(MRT_ERR_INVALID, "null stream handle");
   return *s->stream;
+}
+
+mrt::Coca& CO(mrt_coca* h) {
+  if (!h || !h->coca) throw mrt::Error(MRT_ERR_INVALID, "null style-model handle");
+  return *h->coca;
+}
+
+mrt::CocaConfig to_coca_config(const mrt_coca_config* c) {
+  mrt::CocaConfig k;
+  k.d_model = c->d_model;
+  k.num_heads = c->num_heads;
+  k.d_head = c->d_head;
+  k.d_ff = c->d_ff;
+  k.num_layers = c->num_layers;
+  k.pooler_d_head = c->pooler_d_head;
+  k.vocab_size = c->vocab_size;
+  k.max_text_len = c->max_text_len;
+  k.rvq_depth = c->rvq_depth;
+  k.codebook = c->codebook_size;
+  if (k.num_layers < 1 || k.num_heads < 1 || k.vocab_size < 1)
+    throw mrt::Error(MRT_ERR_INVALID, "musiccoca: layers, heads and vocabulary must be >= 1");
+  return k;
 }
 
 mrt::Codec& CC(mrt_codec* c) {
@@ -566,6 +593,100 @@ int mrt_codec_read(mrt_codec* c, int which, void* dst, size_t bytes) {
     if (bytes != n) throw mrt::Error(MRT_ERR_INVALID, "codec_read: size mismatch (" + std::to_string(n) + " bytes)");
     MRT_HIP_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDefault, CC(c).stream));
     MRT_HIP_CHECK(hipStreamSynchronize(CC(c).stream));
+  });
+}
+
+void mrt_coca_config_default(mrt_coca_config* cfg) {
+  if (!cfg) return;
+  const mrt::CocaConfig k;
+  cfg->d_model = k.d_model;
+  cfg->num_heads = k.num_heads;
+  cfg->d_head = k.d_head;
+  cfg->d_ff = k.d_ff;
+  cfg->num_layers = k.num_layers;
+  cfg->pooler_d_head = k.pooler_d_head;
+  cfg->vocab_size = k.vocab_size;
+  cfg->max_text_len = k.max_text_len;
+  cfg->rvq_depth = k.rvq_depth;
+  cfg->codebook_size = k.codebook;
+}
+
+int mrt_coca_create(const char* encoder_path, const char* codebooks_path, const mrt_coca_config* cfg, int device,
+                    mrt_coca** out) {
+  return guarded([&] {
+    if (!encoder_path || !codebooks_path || !cfg || !out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *out = nullptr;
+    const mrt::CocaConfig k = to_coca_config(cfg);
+    mrt::SafetensorsFile enc(encoder_path), cbs(codebooks_path);
+    auto h = std::make_unique<mrt_coca>();
+    h->coca = std::make_unique<mrt::Coca>(enc, cbs, k, device);
+    *out = h.release();
+  });
+}
+
+int mrt_coca_create_from_tensors(int n, const char* const* names, const float* const* data,
+                                 const int64_t* const* shapes, const int32_t* ndims, const mrt_coca_config* cfg,
+                                 int device, mrt_coca** out) {
+  return guarded([&] {
+    if (!names || !data || !shapes || !ndims || !cfg || !out || n < 0)
+      throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *out = nullptr;
+    const mrt::CocaConfig k = to_coca_config(cfg);
+    mrt::TensorList src;
+    for (int i = 0; i < n; ++i) {
+      if (!names[i] || !data[i] || ndims[i] < 0) throw mrt::Error(MRT_ERR_INVALID, "bad tensor entry");
+      src.add(names[i], data[i], std::vector<int64_t>(shapes[i], shapes[i] + ndims[i]));
+    }
+    auto h = std::make_unique<mrt_coca>();
+    h->coca = std::make_unique<mrt::Coca>(src, src, k, device);
+    *out = h.release();
+  });
+}
+
+void mrt_coca_destroy(mrt_coca* h) { delete h; }
+
+int mrt_coca_embed_text(mrt_coca* h, const int32_t* ids, const float* padding, float* embedding) {
+  return guarded([&] {
+    if (!ids || !padding || !embedding) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    CO(h).embed_text(ids, padding, embedding);
+  });
+}
+
+int mrt_coca_tokenize(mrt_coca* h, const float* embedding, int32_t* tokens) {
+  return guarded([&] {
+    if (!tokens) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    CO(h).tokenize(embedding, tokens);
+  });
+}
+
+int mrt_coca_style_tokens_lm(mrt_coca* h, const int32_t* ids, const float* padding, int style_depth,
+                             int style_codebook_size, int vocab_style_offset, int32_t* out) {
+  return guarded([&] {
+    if (!ids || !padding || !out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    mrt::Coca& c = CO(h);
+    if (style_depth < 0 || style_depth > c.cfg.rvq_depth)
+      throw mrt::Error(MRT_ERR_INVALID, "style_tokens_lm: style_depth must be in [0, rvq_depth]");
+    c.embed_text(ids, padding, nullptr);
+    std::vector<int32_t> tok(c.cfg.rvq_depth);
+    c.tokenize(nullptr, tok.data());
+    for (int l = 0; l < style_depth; ++l) out[l] = vocab_style_offset + l * style_codebook_size + tok[l];
+  });
+}
+
+int mrt_coca_embed_time(mrt_coca* h, float* ms) {
+  return guarded([&] {
+    if (!ms) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *ms = CO(h).last_ms();
+  });
+}
+
+int mrt_coca_read(mrt_coca* h, int which, void* dst, size_t bytes) {
+  return guarded([&] {
+    if (!dst) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    auto [src, n] = CO(h).buffer(which);
+    if (bytes != n) throw mrt::Error(MRT_ERR_INVALID, "coca_read: size mismatch (" + std::to_string(n) + " bytes)");
+    MRT_HIP_CHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDefault, CO(h).stream));
+    MRT_HIP_CHECK(hipStreamSynchronize(CO(h).stream));
   });
 }
 

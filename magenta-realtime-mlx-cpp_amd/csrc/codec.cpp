@@ -334,7 +334,7 @@ const Codec::Plan& Codec::plan(int frames) {
   add(base(proj_sc_, emb_, 1, Hn, 1, skip_, Hn, 1), regular(proj_sc_, Hn, 1, 1, 1, 0, 0, 0));
   {
     ConvLaunch L = base(proj_c1_, emb_, 1, Hn, 1, p1_, Hn, 1);
-    L.elu_out = 1;
+    L.act_out = kActElu;
     add(L, regular(proj_c1_, Hn, 1, 1, 1, 0, 0, 0));
     ConvLaunch L2 = base(proj_c2_, p1_, 1, Hn, 1, x0_, Hn, 1);
     L2.res = skip_;
@@ -348,7 +348,7 @@ const Codec::Plan& Codec::plan(int frames) {
   {
     ConvLaunch L = base(in_c1_, x0_, 1, Hn, W0, t0_, Hn, W0);
     L.elu_in = 1;
-    L.elu_out = 1;
+    L.act_out = kActElu;
     add(L, regular(in_c1_, Hn, W0, 3, 3, 2, 1, 0));
     ConvLaunch L2 = base(in_c2_, t0_, 1, Hn, W0, x1_, Hn, W0);
     L2.res = x0_;
@@ -372,7 +372,7 @@ const Codec::Plan& Codec::plan(int frames) {
     {
       ConvLaunch L = base(blk_t_[i], x, n, H, W, tbuf_, Ho, Wo);
       L.elu_in = 1;
-      L.elu_out = 1;
+      L.act_out = kActElu;
       std::vector<ConvSub> ph_subs;
       int wi = 0;
       for (int ph = 0; ph < b.sh; ++ph)

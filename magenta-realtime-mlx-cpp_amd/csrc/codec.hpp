@@ -25,6 +25,8 @@
 namespace mrt {
 
 constexpr int kConvMaxTaps = 49;
+// Epilogue activations: ELU (nn_ops.h:31-39), exact GELU x/2 (1 + erf(x/sqrt 2)) (nn_ops.h:41-53).
+constexpr int kActNone = 0, kActElu = 1, kActGelu = 2;
 
 // One stride-1 sub-problem of a convolution launch.  GEMM row m = (n, y, x)
 // over an n x gy x gx grid; output pixel (y * oys + oyo, x * oxs + oxo); tap t
@@ -49,7 +51,8 @@ struct ConvLaunch {
   const float* bias;  // (cout)
   const float* res;   // (n, res_h, res_w, cout) added at (oy / rh, ox / rw), or null
   int res_h, res_w, rh, rw;
-  int elu_in, elu_out;  // ELU on the loaded input (zero padding stays 0) / on the result
+  int elu_in;   // ELU on the loaded input (zero padding stays 0)
+  int act_out;  // on the result: kActNone, kActElu or kActGelu
   int nsub;
   const ConvSub* subs;  // device array of nsub
   // split-K: ksplit > 1 splits each tile's K loop over blockIdx.z; the slices

@@ -32,7 +32,8 @@ __device__ __forceinline__ void conv_store(const ConvLaunch& a, const ConvSub* s
   const int oy = yy * sub->oys + sub->oyo, ox = xx * sub->oxs + sub->oxo;
   if (a.bias) val += a.bias[o];
   if (a.res) val += a.res[((size_t)(img * a.res_h + oy / a.rh) * a.res_w + ox / a.rw) * a.cout + o];
-  if (a.elu_out) val = elu1(val);
+  if (a.act_out == kActElu) val = elu1(val);
+  else if (a.act_out == kActGelu) val = val * 0.5f * (1.0f + erff(val * 0.7071067811865475f));
   const int oi = (o / a.split) * a.n + img, oc = o - (o / a.split) * a.split;
   a.y[((size_t)(oi * a.hout + oy) * a.wout + ox) * a.split + oc] = val;
 }

@@ -98,7 +98,14 @@ class _CodecConfig(ctypes.Structure):
     ]
 
 
+class _CocaConfig(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_int32) for f in (
+        "d_model", "num_heads", "d_head", "d_ff", "num_layers", "pooler_d_head", "vocab_size", "max_text_len",
+        "rvq_depth", "codebook_size")]
+
+
 CODEC_BUF_EMB, CODEC_BUF_INPUT_CONV, CODEC_BUF_BLOCK0, CODEC_BUF_SPEC, CODEC_BUF_FRAMES = 0, 1, 2, 9, 10
+COCA_BUF_EMBEDDING = 0
 
 
 @dataclasses.dataclass(frozen=True)
@@ -240,6 +247,20 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_codec_sync": (i32, [vp]),
         "mrt_codec_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
         "mrt_codec_read": (i32, [vp, i32, vp, sz]),
+        "mrt_coca_config_default": (None, [ctypes.POINTER(_CocaConfig)]),
+        "mrt_coca_create": (i32, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_CocaConfig), i32,
+                                  ctypes.POINTER(vp)]),
+        "mrt_coca_create_from_tensors": (i32, [i32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(vp),
+                                               ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_int32),
+                                               ctypes.POINTER(_CocaConfig), i32, ctypes.POINTER(vp)]),
+        "mrt_coca_destroy": (None, [vp]),
+        "mrt_coca_embed_text": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_float),
+                                      ctypes.POINTER(ctypes.c_float)]),
+        "mrt_coca_tokenize": (i32, [vp, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_int32)]),
+        "mrt_coca_style_tokens_lm": (i32, [vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_float), i32,
+                                           i32, i32, ctypes.POINTER(ctypes.c_int32)]),
+        "mrt_coca_embed_time": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
+        "mrt_coca_read": (i32, [vp, i32, vp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -778,6 +799,126 @@ class Codec:
     def close(self) -> None:
         if getattr(self, "_h", None):
             self.lib.mrt_codec_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001
+            pass
+
+
+@dataclasses.dataclass(frozen=True)
+class CocaConfig:
+    """MusicCoCaConfig (musiccoca.h:151-162) + the StyleModel constants."""
+
+    d_model: int = 768
+    num_heads: int = 12
+    d_head: int = 64
+    d_ff: int = 3072
+    num_layers: int = 12
+    pooler_d_head: int = 256
+    vocab_size: int = 64000
+    max_text_len: int = 128
+    rvq_depth: int = 12
+    codebook_size: int = 1024
+
+    @staticmethod
+    def tiny() -> "CocaConfig":
+        return CocaConfig(d_model=128, num_heads=4, d_head=32, d_ff=256, num_layers=2, pooler_d_head=64,
+                          vocab_size=500, max_text_len=32, rvq_depth=12, codebook_size=64)
+
+    def to_c(self) -> _CocaConfig:
+        return _CocaConfig(*[getattr(self, f) for f, _ in _CocaConfig._fields_])
+
+
+class StyleModel:
+    """StyleModel (style_model.h:22-79) on the device: text prompt -> MusicCoCa
+    embedding -> RVQ tokens -> LLM-vocabulary style ids.  ``weights``: a dict
+    with the text-path keys and "codebooks", or (encoder_path,
+    codebooks_path).  ``vocab_path``: a SentencePiece model for string
+    prompts (``style_tokens_lm(prompt)``); id arrays work without one."""
+
+    def __init__(self, weights, cfg: CocaConfig = CocaConfig(), device: int = 0, vocab_path=None):
+        self.lib, self.cfg = load_library(), cfg
+        c = cfg.to_c()
+        h = ctypes.c_void_p()
+        if isinstance(weights, (tuple, list)):
+            _check(self.lib, self.lib.mrt_coca_create(str(weights[0]).encode(), str(weights[1]).encode(),
+                                                      ctypes.byref(c), device, ctypes.byref(h)))
+        else:
+            n, c_names, c_data, c_shapes, c_nd, _keep = _tensor_list(weights)
+            _check(self.lib, self.lib.mrt_coca_create_from_tensors(n, c_names, c_data, c_shapes, c_nd,
+                                                                   ctypes.byref(c), device, ctypes.byref(h)))
+        self._h = h
+        self._spm = None
+        if vocab_path is not None:
+            import sentencepiece  # noqa: PLC0415  (host tokenizer, as the reference links it)
+            self._spm = sentencepiece.SentencePieceProcessor(model_file=str(vocab_path))
+
+    def text_ids(self, prompt: str):
+        """StyleModel::tokenize_text_ids (style_model.cpp:52-74)."""
+        if self._spm is None:
+            raise RuntimeError("no SentencePiece vocabulary: pass vocab_path or use ids")
+        raw = self._spm.encode(prompt.lower())
+        L = self.cfg.max_text_len
+        keep = min(len(raw), L - 1)
+        ids = np.zeros(L, np.int32)
+        pad = np.ones(L, np.float32)
+        ids[0], pad[0] = 1, 0
+        ids[1:keep + 1], pad[1:keep + 1] = raw[:keep], 0
+        return ids, pad
+
+    def embed_text(self, ids: np.ndarray, padding: np.ndarray) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        pad = np.ascontiguousarray(padding, dtype=np.float32)
+        if ids.shape != (self.cfg.max_text_len,) or pad.shape != ids.shape:
+            raise ValueError(f"ids / padding must be ({self.cfg.max_text_len},)")
+        out = np.empty(self.cfg.d_model, np.float32)
+        _check(self.lib, self.lib.mrt_coca_embed_text(self._h, _i32_ptr(ids),
+                                                      pad.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                                      out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return out
+
+    def tokenize(self, embedding: Optional[np.ndarray] = None) -> np.ndarray:
+        tok = np.empty(self.cfg.rvq_depth, np.int32)
+        e = None
+        if embedding is not None:
+            e = np.ascontiguousarray(embedding, dtype=np.float32)
+            if e.shape != (self.cfg.d_model,):
+                raise ValueError(f"embedding must be ({self.cfg.d_model},)")
+        _check(self.lib, self.lib.mrt_coca_tokenize(
+            self._h, e.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if e is not None else None, _i32_ptr(tok)))
+        return tok
+
+    def style_tokens_lm(self, prompt, style_depth: int = 6, codebook: int = 1024, offset: int = 17410,
+                        padding: Optional[np.ndarray] = None) -> np.ndarray:
+        """``prompt``: a string (needs the vocabulary) or an ids array with ``padding``."""
+        if isinstance(prompt, str):
+            ids, padding = self.text_ids(prompt)
+        else:
+            ids = prompt
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        pad = np.ascontiguousarray(padding, dtype=np.float32)
+        out = np.empty(style_depth, np.int32)
+        _check(self.lib, self.lib.mrt_coca_style_tokens_lm(self._h, _i32_ptr(ids),
+                                                           pad.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                                           style_depth, codebook, offset, _i32_ptr(out)))
+        return out
+
+    def embed_time(self) -> float:
+        ms = ctypes.c_float()
+        _check(self.lib, self.lib.mrt_coca_embed_time(self._h, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def read(self, which: int, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=np.float32)
+        _check(self.lib, self.lib.mrt_coca_read(self._h, which, ctypes.c_void_p(out.ctypes.data), out.nbytes))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.lib.mrt_coca_destroy(self._h)
             self._h = None
 
     def __del__(self):

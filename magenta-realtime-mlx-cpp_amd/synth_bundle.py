@@ -230,3 +230,80 @@ def codec_flops(shape, frames: int) -> Dict[str, float]:
     fl["istft"] = 2.0 * 2 * (H - shape.temporal_crop) * shape.n_fft * shape.n_fft
     fl["total"] = sum(fl.values())
     return fl
+
+
+# ---------------------------------------------------------------------------
+# MusicCoCa text encoder bundles (text path + pooler + RVQ codebooks)
+
+
+def coca_layout(cfg) -> List[Tuple[str, Tuple[int, ...]]]:
+    """Text-path keys and stored shapes of the MusicCoCa bundle
+    (musiccoca.cpp:183-193, 212-218, 251-266): Linear weights (out, in)."""
+    D, F, HD, PD = cfg.d_model, cfg.d_ff, cfg.num_heads * cfg.d_head, cfg.num_heads * cfg.pooler_d_head
+    out: List[Tuple[str, Tuple[int, ...]]] = [("token_embedding.weight", (cfg.vocab_size, D))]
+
+    def lin(name, o, i):
+        out.append((name + ".weight", (o, i)))
+        out.append((name + ".bias", (o,)))
+
+    def ln(name):
+        out.append((name + ".weight", (D,)))
+        out.append((name + ".bias", (D,)))
+
+    for i in range(cfg.num_layers):
+        p = f"text_layers.{i}"
+        ln(p + ".attn_ln")
+        lin(p + ".attn.q_proj", HD, D)
+        lin(p + ".attn.k_proj", HD, D)
+        lin(p + ".attn.v_proj", HD, D)
+        lin(p + ".attn.o_proj", D, HD)
+        ln(p + ".ffn_ln")
+        lin(p + ".ffn_w1", F, D)
+        lin(p + ".ffn_w2", D, F)
+    ln("text_exit_ln")
+    out.append(("text_pooler.query", (1, 1, D)))
+    ln("text_pooler.ln")
+    lin("text_pooler.attn.q_proj", PD, D)
+    lin("text_pooler.attn.k_proj", PD, D)
+    lin("text_pooler.attn.v_proj", PD, D)
+    lin("text_pooler.attn.o_proj", D, PD)
+    out.append(("text_pooler.attn._per_dim_scale", (cfg.pooler_d_head,)))
+    return out
+
+
+def make_coca_weights(cfg, seed: int = 9, cb_std: float = 0.05) -> Dict[str, np.ndarray]:
+    """Seeded fp32 MusicCoCa text weights plus "codebooks" (rvq_depth,
+    codebook_size, d_model): embeddings N(0, 1/d_model) (the encoder scales
+    them by sqrt(d_model)), Linear weights N(0, 1/fan_in), biases N(0, 0.02^2),
+    LayerNorm weights 1 + N(0, 0.1^2), the pooler query N(0, 1), the per-dim
+    scale N(0, 0.1^2), codebooks N(0, cb_std^2)."""
+    out = {}
+    for name, shp in coca_layout(cfg):
+        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
+        if name == "token_embedding.weight":
+            w = rng.standard_normal(shp, dtype=np.float32) / np.float32(math.sqrt(cfg.d_model))
+        elif name.endswith("_ln.weight") or name.endswith(".ln.weight"):
+            w = 1.0 + 0.1 * rng.standard_normal(shp)
+        elif name.endswith(".bias"):
+            w = 0.02 * rng.standard_normal(shp)
+        elif name == "text_pooler.query":
+            w = rng.standard_normal(shp)
+        elif name.endswith("_per_dim_scale"):
+            w = 0.1 * rng.standard_normal(shp)
+        else:
+            w = rng.standard_normal(shp) / math.sqrt(shp[1])
+        out[name] = np.asarray(w, dtype=np.float32)
+    rng = np.random.default_rng([seed, zlib.crc32(b"codebooks")])
+    out["codebooks"] = (cb_std * rng.standard_normal((cfg.rvq_depth, cfg.codebook_size, cfg.d_model))).astype(
+        np.float32)
+    return out
+
+
+def coca_flops(cfg) -> float:
+    """FLOPs (2 per multiply-add) of one MusicCoCa embed_text (max_text_len
+    rows): the text layers' projections and attention, the pooler."""
+    L, D, F = cfg.max_text_len, cfg.d_model, cfg.d_ff
+    HD, PD = cfg.num_heads * cfg.d_head, cfg.num_heads * cfg.pooler_d_head
+    per_layer = 2.0 * L * (3 * D * HD + HD * D + 2 * D * F) + 2.0 * 2 * L * L * HD
+    pooler = 2.0 * (D * PD + L * 2 * D * PD + PD * D) + 2.0 * 2 * L * PD
+    return cfg.num_layers * per_layer + pooler
