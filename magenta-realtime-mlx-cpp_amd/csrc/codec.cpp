@@ -216,8 +216,10 @@ Codec::Codec(const TensorSource& w, const TensorSource& cbs, const CodecConfig& 
   skip_ = dalloc(static_cast<size_t>(Hn) * P);
   p1_ = dalloc(static_cast<size_t>(Hn) * P);
   x0_ = dalloc(static_cast<size_t>(Hn) * P);
+  x0e_ = dalloc(static_cast<size_t>(Hn) * P);
   t0_ = dalloc(static_cast<size_t>(Hn) * P);
   x1_ = dalloc(static_cast<size_t>(Hn) * P);
+  x1e_ = dalloc(static_cast<size_t>(Hn) * P);
   size_t tmax = 0, rmax = 0;
   int n = 1, H = Hn, W = cfg.unfold;
   for (size_t i = 0; i < cfg.blocks.size(); ++i) {
@@ -228,6 +230,7 @@ Codec::Codec(const TensorSource& w, const TensorSource& cbs, const CodecConfig& 
     const size_t outn = static_cast<size_t>(n) * H * W * b.out_ch;
     tmax = std::max(tmax, outn);
     blk_out_.push_back(dalloc(outn));
+    blk_oute_.push_back(dalloc(outn));
     blk_out_n_.push_back(outn);
     if (i == 0) n = 2;
   }
@@ -337,6 +340,7 @@ const Codec::Plan& Codec::plan(int frames) {
     L.act_out = kActElu;
     add(L, regular(proj_c1_, Hn, 1, 1, 1, 0, 0, 0));
     ConvLaunch L2 = base(proj_c2_, p1_, 1, Hn, 1, x0_, Hn, 1);
+    L2.y_elu = x0e_;  // elu(x0): input_conv's first conv reads it as is
     L2.res = skip_;
     L2.res_h = Hn;
     L2.res_w = 1;
@@ -346,18 +350,19 @@ const Codec::Plan& Codec::plan(int frames) {
   const int W0 = cfg.unfold;
   // Res3x3Block input_conv, causal (spectrostream.cpp:191-200): pads top 2, left 1
   {
-    ConvLaunch L = base(in_c1_, x0_, 1, Hn, W0, t0_, Hn, W0);
-    L.elu_in = 1;
+    ConvLaunch L = base(in_c1_, x0e_, 1, Hn, W0, t0_, Hn, W0);
     L.act_out = kActElu;
     add(L, regular(in_c1_, Hn, W0, 3, 3, 2, 1, 0));
     ConvLaunch L2 = base(in_c2_, t0_, 1, Hn, W0, x1_, Hn, W0);
+    L2.y_elu = x1e_;
     L2.res = x0_;
     L2.res_h = Hn;
     L2.res_w = W0;
     add(L2, regular(in_c2_, Hn, W0, 3, 3, 2, 1, 0));
   }
   // DecoderResBlocks (spectrostream.cpp:224-262)
-  const float* x = x1_;
+  const float* x = x1_;   // raw: the residual / shortcut input
+  const float* xe = x1e_;  // elu(x): the transposed conv's input
   int n = 1, H = Hn, W = W0;
   for (size_t i = 0; i < cfg.blocks.size(); ++i) {
     const CodecBlockCfg& b = cfg.blocks[i];
@@ -370,8 +375,7 @@ const Codec::Plan& Codec::plan(int frames) {
     }
     // conv_transpose(elu(x)) + bias, cropped, then elu: one sub-problem per phase
     {
-      ConvLaunch L = base(blk_t_[i], x, n, H, W, tbuf_, Ho, Wo);
-      L.elu_in = 1;
+      ConvLaunch L = base(blk_t_[i], xe, n, H, W, tbuf_, Ho, Wo);
       L.act_out = kActElu;
       std::vector<ConvSub> ph_subs;
       int wi = 0;
@@ -401,6 +405,7 @@ const Codec::Plan& Codec::plan(int frames) {
     {
       const int top = b.kph - 1, left = (b.kpw - 1) / 2;
       ConvLaunch L = base(blk_c_[i], tbuf_, n, Ho, Wo, blk_out_[i], Ho, Wo);
+      L.y_elu = blk_oute_[i];
       L.res = res;
       L.res_h = H;
       L.res_w = W;
@@ -410,6 +415,7 @@ const Codec::Plan& Codec::plan(int frames) {
       add(L, regular(blk_c_[i], Ho, Wo, b.kph, b.kpw, top, left, 0));
     }
     x = blk_out_[i];
+    xe = blk_oute_[i];
     if (i == 0) n = 2;
     H = Ho;
     W = Wo;
@@ -454,7 +460,8 @@ void Codec::enqueue(const int* tokens_dev, int frames, float* audio_dev) {
               stream);
   for (size_t l = 0; l < pl.launches.size(); ++l) {
     if (static_cast<int>(l) == pl.out_at)
-      out_conv(blk_out_.back(), 2, pl.out_h, pl.out_w, cfg.blocks.back().out_ch, cfg.temporal_crop, out_w_, out_b_,
+      out_conv(blk_oute_.back(), 2, pl.out_h, pl.out_w, cfg.blocks.back().out_ch, cfg.temporal_crop, false, out_w_,
+               out_b_,
                spec_, pl.out_hs, stream);
     conv_launch(pl.launches[l], pl.tiles_m[l], pl.tiles_n[l], stream);
   }

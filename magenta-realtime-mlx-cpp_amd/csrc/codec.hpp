@@ -61,6 +61,7 @@ struct ConvLaunch {
   // before the epilogue.
   int ksplit, rows;
   float* partial;
+  float* y_elu;  // when non-null, also elu(result) here (same layout): the next ELU'd input
 };
 
 // One convolution launch (plus its split-K finish when a.ksplit > 1).
@@ -71,10 +72,11 @@ void conv_launch(const ConvLaunch& a, int tiles_m, int tiles_n, hipStream_t s);
 void rvq_dequant(const int* tokens, int frames, int levels, const float* codebooks, int codebook, int dim, int pad,
                  float* emb, hipStream_t s);
 // The output conv: x (n, H, W, cin) -> out (n, Hs, W, 2) = conv7x7(elu(x))
-// with causal padding (top 6, left 3, right 3) over input rows from `crop`
-// on, plus bias; w packed (kh, kw, cin, 2); cin a multiple of 8.
-void out_conv(const float* x, int n, int H, int W, int cin, int crop, const float* w, const float* bias, float* out,
-              int Hs, hipStream_t s);
+// (x already ELU'd when !elu_in) with causal padding (top 6, left 3, right 3)
+// over input rows from `crop` on, plus bias; w packed (kh, kw, cin, 2); cin a
+// multiple of 8.
+void out_conv(const float* x, int n, int H, int W, int cin, int crop, bool elu_in, const float* w, const float* bias,
+              float* out, int Hs, hipStream_t s);
 // audio (T, 2) from windowed frames wf (2 * H, n_fft): overlap-add at hop
 // n_fft / 2 (spectrostream.cpp:649-667), trimmed to T, channels interleaved.
 void overlap_add(const float* wf, int H, int n_fft, int T, float* audio, hipStream_t s);
@@ -151,7 +153,8 @@ class Codec {
   float *out_w_ = nullptr, *out_b_ = nullptr;  // output conv (kh, kw, cin, 2), bias (2)
   std::vector<Conv> blk_t_, blk_c_, blk_sc_;
   float *emb_ = nullptr, *skip_ = nullptr, *p1_ = nullptr, *x0_ = nullptr, *t0_ = nullptr, *x1_ = nullptr;
-  std::vector<float*> blk_out_;
+  float *x0e_ = nullptr, *x1e_ = nullptr;  // elu(x0), elu(x1)
+  std::vector<float*> blk_out_, blk_oute_;  // block outputs and their ELU'd copies
   std::vector<size_t> blk_out_n_;
   float *tbuf_ = nullptr, *rbuf_ = nullptr, *spec_ = nullptr, *wf_ = nullptr, *audio_ = nullptr;
   int* tok_ = nullptr;

@@ -35,7 +35,9 @@ __device__ __forceinline__ void conv_store(const ConvLaunch& a, const ConvSub* s
   if (a.act_out == kActElu) val = elu1(val);
   else if (a.act_out == kActGelu) val = val * 0.5f * (1.0f + erff(val * 0.7071067811865475f));
   const int oi = (o / a.split) * a.n + img, oc = o - (o / a.split) * a.split;
-  a.y[((size_t)(oi * a.hout + oy) * a.wout + ox) * a.split + oc] = val;
+  const size_t idx = ((size_t)(oi * a.hout + oy) * a.wout + ox) * a.split + oc;
+  a.y[idx] = val;
+  if (a.y_elu) a.y_elu[idx] = elu1(val);
 }
 
 template <int BM, int BN, int KC>
@@ -86,17 +88,28 @@ __global__ __launch_bounds__(kThreads) void k_conv(ConvLaunch a) {
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
 
+  // the A rows' input pixels depend on the tap only: recomputed when it changes
+  int cur_t = -1;
+  bool a_ok[APASS];
+  const float* a_src[APASS];
   auto load = [&](int kc, auto S) {
     constexpr int q = decltype(S)::value;
     kc += kb;
     const int t = kc / cpt, c0 = (kc - t * cpt) * KC + a_chunk * 4;
-    const int dy = sub->dy[t], dx = sub->dx[t];
+    if (t != cur_t) {
+      cur_t = t;
+      const int dy = sub->dy[t], dx = sub->dx[t];
+#pragma unroll
+      for (int p = 0; p < APASS; ++p) {
+        const int iy = a_y[p] + dy, ix = a_x[p] + dx;
+        a_ok[p] = iy >= 0 && iy < a.hin && ix >= 0 && ix < a.win;
+        a_src[p] = a.x + ((size_t)(a_img[p] + (a_ok[p] ? iy : 0)) * a.win + (a_ok[p] ? ix : 0)) * a.cin;
+      }
+    }
 #pragma unroll
     for (int p = 0; p < APASS; ++p) {
-      const int iy = a_y[p] + dy, ix = a_x[p] + dx;
-      const bool ok = iy >= 0 && iy < a.hin && ix >= 0 && ix < a.win;
-      const int cy = ok ? iy : 0, cx = ok ? ix : 0;
-      const float4 v = *reinterpret_cast<const float4*>(a.x + ((size_t)(a_img[p] + cy) * a.win + cx) * a.cin + c0);
+      const bool ok = a_ok[p];
+      const float4 v = *reinterpret_cast<const float4*>(a_src[p] + c0);
       ra[q][p][0] = ok ? v.x : 0.f;
       ra[q][p][1] = ok ? v.y : 0.f;
       ra[q][p][2] = ok ? v.z : 0.f;
@@ -230,8 +243,9 @@ constexpr int kOcHaloR = kOcRows + kOcK - 1, kOcHaloC = kOcCols + kOcK - 1;
 constexpr int kOcPlane = kOcHaloR * kOcHaloC;
 
 __global__ __launch_bounds__(kOcThreads) void k_out_conv(const float* __restrict__ x, int H, int W, int cin, int crop,
-                                                         const float* __restrict__ w, const float* __restrict__ bias,
-                                                         float* __restrict__ out, int Hs) {
+                                                         int elu_in, const float* __restrict__ w,
+                                                         const float* __restrict__ bias, float* __restrict__ out,
+                                                         int Hs) {
   __shared__ float hl[kOcCh * kOcPlane];  // (channel, halo row, halo column)
   const int tid = threadIdx.x;
   const int img = blockIdx.z;
@@ -253,10 +267,12 @@ __global__ __launch_bounds__(kOcThreads) void k_out_conv(const float* __restrict
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (iy >= 0 && iy < H && ix >= 0 && ix < W) {
         v = *reinterpret_cast<const float4*>(x + ((size_t)(img * H + iy) * W + ix) * cin + c0 + hh * 4);
-        v.x = elu1(v.x);
-        v.y = elu1(v.y);
-        v.z = elu1(v.z);
-        v.w = elu1(v.w);
+        if (elu_in) {
+          v.x = elu1(v.x);
+          v.y = elu1(v.y);
+          v.z = elu1(v.z);
+          v.w = elu1(v.w);
+        }
       }
       float* d = hl + (hh * 4) * kOcPlane + pix;
       d[0] = v.x;
@@ -355,11 +371,11 @@ void conv_launch(const ConvLaunch& a, int tiles_m, int tiles_n, hipStream_t s) {
   }
 }
 
-void out_conv(const float* x, int n, int H, int W, int cin, int crop, const float* w, const float* bias, float* out,
-              int Hs, hipStream_t s) {
+void out_conv(const float* x, int n, int H, int W, int cin, int crop, bool elu_in, const float* w, const float* bias,
+              float* out, int Hs, hipStream_t s) {
   MRT_REQUIRE(cin % kOcCh == 0, "codec: output conv input channels must be a multiple of 8");
   const dim3 grid((W + kOcCols - 1) / kOcCols, (Hs + kOcRows - 1) / kOcRows, n);
-  hipLaunchKernelGGL(k_out_conv, grid, dim3(kOcThreads), 0, s, x, H, W, cin, crop, w, bias, out, Hs);
+  hipLaunchKernelGGL(k_out_conv, grid, dim3(kOcThreads), 0, s, x, H, W, cin, crop, elu_in ? 1 : 0, w, bias, out, Hs);
   MRT_HIP_CHECK(hipGetLastError());
 }
 
