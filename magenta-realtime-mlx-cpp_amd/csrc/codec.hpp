@@ -122,6 +122,13 @@ class Codec {
   void decode(const int32_t* tokens_host, int frames, float* audio_host);
   // Device pointers; enqueued on `stream`, no host sync.
   void decode_device(const int* tokens_dev, int frames, float* audio_dev);
+  // Builds (and checks) the launch plan of a decode of `frames` frames now,
+  // so that a later decode of that size cannot fail on its geometry.
+  void prepare(int frames) {
+    MRT_REQUIRE(frames >= 1 && frames <= max_frames, "codec: frames must be in [1, max_frames]");
+    MRT_HIP_CHECK(hipSetDevice(device));
+    plan(frames);
+  }
   float last_ms() const;
   // (pointer, bytes) of an intermediate of the last decode.
   std::pair<const void*, size_t> buffer(int which) const;

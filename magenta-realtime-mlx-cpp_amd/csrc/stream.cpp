@@ -76,6 +76,7 @@ void Stream::attach_codec(Codec* c) {
   MRT_REQUIRE(k.crossfade_frames >= 0 && k.crossfade_frames <= k.context_frames - k.chunk_frames,
               "attach_codec: crossfade_frames must fit in the context before the chunk");
   MRT_REQUIRE(k.samples_per_frame == c->cfg.samples_per_frame, "attach_codec: samples per frame differ");
+  c->prepare(k.chunk_frames + k.crossfade_frames);  // geometry errors surface here, not mid-chunk
   const size_t nf = static_cast<size_t>(k.chunk_frames + k.crossfade_frames);
   const size_t T = nf * k.samples_per_frame;
   const size_t xf = static_cast<size_t>(k.crossfade_frames) * k.samples_per_frame;
