@@ -294,6 +294,51 @@ def bench_speculative(model, cfg, enc, reps=3, seed=1234):
     return res
 
 
+def bench_concurrent_batches(model, batches=2, streams=32, chunks=3, seed=1234):
+    """Serving capacity: `batches` independent Batch objects of `streams`
+    streams each, every one on its own HIP stream, driven from one host
+    thread each (the library releases the GIL).  The 32-stream decode is
+    latency-bound, so concurrent batches share the GPU.  Wall ms per round
+    (every batch one chunk), aggregate RVQ tokens/s and per-stream RTF."""
+    import threading
+    import mrt_df
+    opts = mrt_df.GenOptions(num_frames=50, rvq_depth=16, temperature=1.1, top_k=40, guidance_weight=5.0,
+                             codebook_size=1024, codec_offset=2, use_graph=True)
+    bs = [mrt_df.Batch(model, streams, max_frames=50) for _ in range(batches)]
+    encs = [synthetic_stream_tokens(streams, seed=7 + i) for i in range(batches)]
+    for i, b in enumerate(bs):
+        b.generate_tokens(encs[i], opts, seeds=[seed + s for s in range(streams)])  # frame-graph capture
+    errors = []
+
+    def run(i, c):
+        try:
+            bs[i].generate_tokens(encs[i], opts, seeds=[seed + 1000 * (c + 1) + 97 * i + s for s in range(streams)])
+        except Exception as e:  # noqa: BLE001  (re-raised below)
+            errors.append(e)
+
+    wall = []
+    for c in range(chunks):
+        th = [threading.Thread(target=run, args=(i, c)) for i in range(batches)]
+        t0 = time.perf_counter()
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        wall.append((time.perf_counter() - t0) * 1e3)
+    for b in bs:
+        b.close()
+    if errors:
+        raise errors[0]
+    ms = float(np.mean(wall))
+    res = {"batches": batches, "streams": batches * streams, "round_ms": ms,
+           "rvq_tokens_per_s": batches * streams * 800.0 / (ms * 1e-3), "per_stream_rtf": 2000.0 / ms,
+           "chunks_timed": chunks}
+    print(f"[bench] {batches} concurrent batches of {streams} streams: {ms:.1f} ms per round, "
+          f"{res['rvq_tokens_per_s']:.0f} RVQ tok/s aggregate, per-stream RTF {res['per_stream_rtf']:.1f}",
+          file=sys.stderr, flush=True)
+    return res
+
+
 def bench_codec(reps=10, frames=51, cpu=True):
     """Codec decode of one chunk (system.cpp:373-390): 1 crossfade frame + 50
     frames of RVQ ids -> dequantisation -> SpectroStream decoder -> iSTFT ->
@@ -602,6 +647,7 @@ def main():
     if not args.no_batched and args.dtype == "bf16":
         full = bench_full_chunk(model, cfg)
         batched = bench_batched(model, cfg)
+        batched["concurrent"] = bench_concurrent_batches(model)
         encoder = bench_encoder(model, cfg)
         spec = bench_speculative(model, cfg, system.build_encoder_inputs(sess.context, scfg, style))
         codec = bench_codec(cpu=not args.no_cpu_baseline)
