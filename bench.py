@@ -643,7 +643,7 @@ def main():
                 "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
                 "launches_timed": dk["launches"]}
 
-    batched = encoder = spec = codec = full = style = None
+    batched = encoder = spec = codec = full = style_res = None
     if not args.no_batched and args.dtype == "bf16":
         full = bench_full_chunk(model, cfg)
         batched = bench_batched(model, cfg)
@@ -651,7 +651,7 @@ def main():
         encoder = bench_encoder(model, cfg)
         spec = bench_speculative(model, cfg, system.build_encoder_inputs(sess.context, scfg, style))
         codec = bench_codec(cpu=not args.no_cpu_baseline)
-        style = bench_style(cpu=not args.no_cpu_baseline)
+        style_res = bench_style(cpu=not args.no_cpu_baseline)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -696,7 +696,7 @@ def main():
         "speculative": spec,
         "codec_decode": codec,
         "full_chunk_with_audio": full,
-        "style_model": style,
+        "style_model": style_res,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
