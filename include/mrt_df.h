@@ -267,7 +267,8 @@ int mrt_df_stream_generate_chunk_audio(mrt_df_stream* s, const int32_t* style, c
                                        int32_t* llm_out, int32_t* rvq_out, float* audio_out);
 /* Attach a codec (not owned; NULL detaches) to a stream.  Its rvq_levels and
  * codebook_size must equal the stream's and its max_frames must be at least
- * chunk_frames + crossfade_frames. */
+ * chunk_frames + crossfade_frames.  The codec must outlive the stream or be
+ * detached first; its launch plan for the chunk size is built here. */
 int mrt_df_stream_attach_codec(mrt_df_stream* s, mrt_codec* c);
 
 /* SystemState::context_tokens and chunk_index in and out: host
