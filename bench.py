@@ -282,7 +282,25 @@ def bench_speculative(model, cfg, enc, reps=3, seed=1234):
         st.generate_tokens(None, mk(seed, True))
         full.append(st.decode_time()[0])
     st.close()
+    # streaming (drafts = the previous chunk's tokens, a new seed and context
+    # each chunk): speculation off against the adaptive mode
+    import system
+    scfg = system.SystemConfig()
+    stream_ms = {}
+    for mode in (0, 2):
+        strm = mrt_df.Stream(model, mrt_df.StreamConfig())
+        style = scfg.style_offset + 1024 * np.arange(6)
+        ms, spec_chunks = [], 0
+        for c in range(12):
+            strm.generate_chunk(style, mrt_df.ChunkOptions(seed=seed + c, speculative=mode))
+            if c >= 2:
+                ms.append(strm.state.decode_time()[0])
+                spec_chunks += strm.state.spec_acceptance() >= 0
+        strm.close()
+        stream_ms[mode] = (float(np.mean(ms)), spec_chunks)
     res = {"plain_decode_ms": float(np.mean(plain)),
+           "streaming_adaptive": {"plain_decode_ms": stream_ms[0][0], "adaptive_decode_ms": stream_ms[2][0],
+                                  "chunks": 10, "speculative_chunks": stream_ms[2][1]},
            "rejected_drafts": {"decode_ms": float(np.mean(rej)), "levels_from_verification": float(np.mean(acc))},
            "accepted_drafts": {"decode_ms": float(np.mean(full)), "fixed_point": fixed,
                                "calls_to_fixed_point": calls},
@@ -290,7 +308,8 @@ def bench_speculative(model, cfg, enc, reps=3, seed=1234):
                    "token came from the verification pass (accepted drafts + the first disagreement)"}
     print(f"[bench] speculative: plain {res['plain_decode_ms']:.1f} ms, rejected drafts "
           f"{res['rejected_drafts']['decode_ms']:.1f} ms, accepted drafts {res['accepted_drafts']['decode_ms']:.1f} ms "
-          f"(fixed point after {calls} calls)", file=sys.stderr, flush=True)
+          f"(fixed point after {calls} calls); streaming adaptive {stream_ms[2][0]:.1f} ms vs plain "
+          f"{stream_ms[0][0]:.1f} ms ({stream_ms[2][1]} of 10 chunks speculated)", file=sys.stderr, flush=True)
     return res
 
 

@@ -84,7 +84,8 @@ typedef struct mrt_gen_opts {
    * tokens are those of the same draws from the same logits.  bf16 models on
    * the persistent path; ignored (plain decode) on a state's
    * first call, when num_frames differs from the previous call's, with a
-   * teacher, or with record_drawn / record_frame_mean. */
+   * teacher, or with record_drawn / record_frame_mean.  Any nonzero value
+   * turns it on (the adaptive mode 2 is a policy of the stream entry points). */
   int32_t speculative;
 } mrt_gen_opts;
 
@@ -173,6 +174,11 @@ int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts
  * kernel, num_frames * (1 + rvq_depth) with one launch per step, 0 on the
  * per-layer path.  Waits for the section to finish. */
 int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches);
+/* Share of the last mrt_df_generate_tokens call's RVQ levels whose token came
+ * from the speculative verification pass (accepted drafts plus each frame's
+ * first disagreement); -1 when that call did not speculate.  No counterpart
+ * in the reference. */
+int mrt_df_state_spec_acceptance(mrt_df_state* st, float* acceptance);
 
 /* State buffers exposed for parity checks (device-to-device copies). */
 #define MRT_BUF_ENC_OUT 0     /* (rows, enc_len, d_model)                       */
@@ -225,7 +231,10 @@ typedef struct mrt_chunk_opts {
   int32_t pipeline_encoder; /* enqueue the next chunk's encoder before returning */
   int32_t use_graph;        /* replay the decode loop from a captured hipGraph */
   const int32_t* teacher;   /* optional host (chunk_frames, levels) ids fed back instead of draws */
-  int32_t speculative;      /* speculative depth decoding, drafts = the previous chunk's tokens */
+  int32_t speculative;      /* speculative depth decoding, drafts = the previous chunk's tokens:
+                               0 off, 1 on, 2 adaptive (speculate while the last speculative chunk
+                               took >= 1/4 of its levels from the verification pass; after one below,
+                               4 chunks plain, then try again) */
 } mrt_chunk_opts;
 
 typedef struct mrt_df_stream mrt_df_stream;

@@ -192,7 +192,7 @@ mrt::ChunkOpts to_chunk_opts(const mrt_chunk_opts* opts) {
   o.pipeline_encoder = opts->pipeline_encoder != 0;
   o.use_graph = opts->use_graph != 0;
   o.teacher = opts->teacher;
-  o.speculative = opts->speculative != 0;
+  o.speculative = opts->speculative;
   return o;
 }
 
@@ -334,6 +334,13 @@ int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches) {
   return guarded([&] {
     if (!ms) throw mrt::Error(MRT_ERR_INVALID, "null argument");
     *ms = S(st).last_decode_ms(launches);
+  });
+}
+
+int mrt_df_state_spec_acceptance(mrt_df_state* st, float* acceptance) {
+  return guarded([&] {
+    if (!acceptance) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *acceptance = S(st).spec_acceptance();
   });
 }
 

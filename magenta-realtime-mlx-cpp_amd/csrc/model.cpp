@@ -337,7 +337,7 @@ State::State(Model& model, int rows_, int max_frames, int enc_len)
   d_tokens = static_cast<int*>(dalloc(static_cast<size_t>(F) * L * 4));
   d_teacher = static_cast<int*>(dalloc(static_cast<size_t>(F) * L * 4));
   d_seed = static_cast<uint64_t*>(dalloc(8));
-  h_pinned_n = std::max<size_t>(M, static_cast<size_t>(F) * L) + 2;
+  h_pinned_n = std::max<size_t>(M, static_cast<size_t>(F) * L + F) + 2;  // tokens + per-frame accepted counts
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_pinned), h_pinned_n * 4, hipHostMallocDefault));
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_err_), 64, hipHostMallocDefault));
   *h_err_ = 0;
@@ -352,7 +352,7 @@ State::State(Model& model, int rows_, int max_frames, int enc_len)
     sffh_ = dalloc(R2 * FF * e);
     slog_ = static_cast<float*>(dalloc(R2 * 1024 * 4));
     sdrawn_ = static_cast<int*>(dalloc(L * 4));
-    sdecided_ = static_cast<int*>(dalloc(4));
+    sdecided_ = static_cast<int*>(dalloc(static_cast<size_t>(F) * 4));
     sfm_ = dalloc(rows * D * e);
   }
   const char* path = std::getenv("MRT_DECODE_PATH");
@@ -666,7 +666,6 @@ void State::enqueue_decode_spec(const GenOpts& o) {
   sp_all.noise = noise_;
   SampleParams sp_rest = sp_all;
   sp_rest.noise_frames = o.num_frames;  // one stream: noise row (frame * L + level)
-  sp_rest.decided = sdecided_;
   const char* head0 = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset) * D * esz();
   for (int f = 0; f < o.num_frames; ++f) {
     int* tok = d_tokens + static_cast<size_t>(f) * L;
@@ -687,9 +686,11 @@ void State::enqueue_decode_spec(const GenOpts& o) {
     rmsnorm_rows(dt, sx_, m.dec_norm, 1e-6f, R2, D, sxn_, stream);
     bgemm_f32_grouped(sxn_, rows, D, head0, static_cast<long>(C) * D, C, slog_, C, L, stream);
     draw_levels(slog_, sp_all, f, L, sdrawn_, stream);
-    spec_accept(dt, sdrawn_, d_drafts_ + static_cast<size_t>(f) * L, L, tok, sdecided_, m.emb, D, d_in, stream);
+    int* decided = sdecided_ + f;
+    sp_rest.decided = decided;
+    spec_accept(dt, sdrawn_, d_drafts_ + static_cast<size_t>(f) * L, L, tok, decided, m.emb, D, d_in, stream);
     float* rec = o.record_slices ? o.record_slices + static_cast<size_t>(f) * L * rows * C : nullptr;
-    if (rec) spec_record(slog_, slice, sdecided_, 0, C, rec, stream);
+    if (rec) spec_record(slog_, slice, decided, 0, C, rec, stream);
     // the levels after the first disagreement; a decided level's step and
     // draw return at once, its draw feeding the known token on
     for (int l = 1; l < L; ++l) {
@@ -699,7 +700,7 @@ void State::enqueue_decode_spec(const GenOpts& o) {
       launch_step(dt, a, persist_grid_, lds_d_, stream);
       sample_level(dt, slice, sp_rest, f, l, f * L + l, nullptr, d_tokens, nullptr, m.emb, D, d_in, fsum, sfm_,
                    stream);
-      if (rec) spec_record(slog_, slice, sdecided_, l, C, rec + static_cast<size_t>(l) * rows * C, stream);
+      if (rec) spec_record(slog_, slice, decided, l, C, rec + static_cast<size_t>(l) * rows * C, stream);
     }
     frame_mean_tokens(dt, tok, L, m.emb, D, t_in, stream);
   }
@@ -1049,10 +1050,19 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
   MRT_HIP_CHECK(hipEventRecord(ev_dec_[1], stream));
   dec_timed_ = true;
   MRT_HIP_CHECK(hipMemcpyAsync(h_pinned, d_tokens, nt * 4, hipMemcpyDeviceToHost, stream));
+  if (spec_drafts_)
+    MRT_HIP_CHECK(hipMemcpyAsync(h_pinned + nt, sdecided_, static_cast<size_t>(o.num_frames) * 4,
+                                 hipMemcpyDeviceToHost, stream));
   MRT_HIP_CHECK(hipStreamSynchronize(stream));
   check_device_error();
   print_trace();
   std::memcpy(out_host, h_pinned, nt * 4);
+  spec_acc_ = -1.f;
+  if (spec_drafts_) {  // levels 0..n of frame f came from the verification pass (n = L: all)
+    long from_pass = 0;
+    for (int f = 0; f < o.num_frames; ++f) from_pass += std::min(h_pinned[nt + f] + 1, o.rvq_depth);
+    spec_acc_ = static_cast<float>(from_pass) / static_cast<float>(nt);
+  }
   temporal_len_ = o.num_frames;
   depth_len_ = o.rvq_depth;
   prev_frames_ = o.num_frames;

@@ -161,6 +161,9 @@ class State {
   // GPU ms of the decode section (after the encoder) of the last generate
   // call, from HIP events on the state's stream; launches = persistent
   // kernel launches in it (0 on the per-layer path).
+  // Share of the last generate's levels whose token came from the verification
+  // pass (accepted drafts and the first disagreement); -1 when it did not speculate.
+  float spec_acceptance() const { return spec_acc_; }
   float last_decode_ms(int* launches);
 
  private:
@@ -202,7 +205,8 @@ class State {
   bool spec_drafts_ = false;  // this call speculates with d_drafts_
   void *sx_ = nullptr, *sxn_ = nullptr, *sq_ = nullptr, *satt_ = nullptr, *sffh_ = nullptr;
   float* slog_ = nullptr;
-  int *sdrawn_ = nullptr, *sdecided_ = nullptr;
+  int *sdrawn_ = nullptr, *sdecided_ = nullptr;  // sdecided_: (F) the accepted count n of each frame
+  float spec_acc_ = -1.f;  // share of the last call's levels taken from the verification pass
   void* sfm_ = nullptr;  // scratch frame-mean rows of the sampler (the spec path writes its own)
   void print_trace();
 

@@ -143,10 +143,19 @@ void Stream::token_half(const int32_t* style, const ChunkOpts& o, int32_t* llm_o
   g.codec_offset = c.codec_offset;
   g.teacher = o.teacher;
   g.use_graph = o.use_graph;
-  g.speculative = o.speculative;
+  MRT_REQUIRE(o.speculative >= 0 && o.speculative <= 2, "generate_chunk: speculative must be 0, 1 or 2");
+  g.speculative = o.speculative == 1 || (o.speculative == 2 && spec_pause_ == 0);
   const size_t n = static_cast<size_t>(c.chunk_frames) * c.levels;
   llm_tmp_.resize(n);
   st.generate(nullptr, g, llm_tmp_.data());  // waits for the chunk's ids
+  if (o.speculative == 2) {
+    if (spec_pause_ > 0) {
+      --spec_pause_;
+    } else {
+      const float acc = st.spec_acceptance();
+      if (acc >= 0.f && acc < kSpecMinAcceptance) spec_pause_ = kSpecPause;
+    }
+  }
   if (llm_out) std::copy(llm_tmp_.begin(), llm_tmp_.end(), llm_out);
 
   // llm_to_rvq (system.cpp:289-292) and the context roll (system.cpp:315-333).

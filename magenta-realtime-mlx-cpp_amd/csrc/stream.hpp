@@ -55,7 +55,12 @@ struct ChunkOpts {
   bool pipeline_encoder = false;
   bool use_graph = true;
   const int32_t* teacher = nullptr;  // host (chunk_frames, levels) ids fed in place of the draws
-  bool speculative = false;          // drafts: the previous chunk's tokens of the same frame
+  // Speculative depth decoding, drafts = the previous chunk's tokens of the
+  // same frame: 0 off, 1 on, 2 adaptive (speculate while the last speculative
+  // chunk took at least kSpecMinAcceptance of its levels from the
+  // verification pass; after one below, decode kSpecPause chunks plainly,
+  // then try again).
+  int speculative = 0;
 };
 
 // SystemState's token context (system.h:124-160) resident in device memory,
@@ -64,6 +69,9 @@ struct ChunkOpts {
 // rolled into the context; with pipeline_encoder the next chunk's encoder is
 // enqueued before returning (system.cpp:334-370) and reused when the next
 // call's style matches.
+constexpr float kSpecMinAcceptance = 0.25f;
+constexpr int kSpecPause = 4;
+
 class Stream {
  public:
   Stream(Model& m, const StreamConfig& cfg);
@@ -113,6 +121,7 @@ class Stream {
   std::vector<int32_t> pre_style_;
   std::vector<int32_t> llm_tmp_;
   uint64_t seed_base_ = 0;
+  int spec_pause_ = 0;  // adaptive speculation: chunks left to decode plainly
 };
 
 }  // namespace mrt

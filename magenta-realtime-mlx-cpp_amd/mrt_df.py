@@ -213,6 +213,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_state_write": (i32, [vp, i32, i32, vp, sz]),
         "mrt_df_state_set_cache_length": (i32, [vp, i32, i32]),
         "mrt_df_state_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(i32)]),
+        "mrt_df_state_spec_acceptance": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
         "mrt_stream_config_default": (None, [ctypes.POINTER(_StreamConfig)]),
         "mrt_chunk_opts_default": (None, [ctypes.POINTER(_ChunkOpts)]),
         "mrt_df_stream_create": (i32, [vp, ctypes.POINTER(_StreamConfig), ctypes.POINTER(vp)]),
@@ -464,6 +465,13 @@ class State:
         _check(self.lib, self.lib.mrt_df_state_decode_time(self._h, ctypes.byref(ms), ctypes.byref(n)))
         return float(ms.value), int(n.value)
 
+    def spec_acceptance(self) -> float:
+        """Share of the last generate_tokens call's levels taken from the
+        speculative verification pass (-1: it did not speculate)."""
+        a = ctypes.c_float()
+        _check(self.lib, self.lib.mrt_df_state_spec_acceptance(self._h, ctypes.byref(a)))
+        return float(a.value)
+
     def stream_handle(self) -> int:
         s = ctypes.c_void_p()
         _check(self.lib, self.lib.mrt_df_state_stream(self._h, ctypes.byref(s)))
@@ -536,7 +544,7 @@ class StreamConfig:
 
 @dataclasses.dataclass
 class ChunkOptions:
-    """GenerateChunkOptions (system.h:86-121) without the speculative path."""
+    """GenerateChunkOptions (system.h:86-121)."""
 
     temperature: float = 1.1
     top_k: int = 40
@@ -544,7 +552,7 @@ class ChunkOptions:
     seed: Optional[int] = None
     pipeline_encoder: bool = False
     use_graph: bool = True
-    speculative: bool = False
+    speculative: int = 0  # 0 off, 1 on, 2 adaptive (see mrt_chunk_opts)
 
 
 class Stream:
@@ -584,7 +592,7 @@ class Stream:
                        seed=0 if opts.seed is None else opts.seed & ((1 << 64) - 1),
                        pipeline_encoder=1 if opts.pipeline_encoder else 0,
                        use_graph=1 if opts.use_graph else 0, teacher=None,
-                       speculative=1 if opts.speculative else 0)
+                       speculative=int(opts.speculative))
         keep = []
         if teacher is not None:
             tt = np.ascontiguousarray(teacher, dtype=np.int32)

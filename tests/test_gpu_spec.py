@@ -86,16 +86,23 @@ def test_speculative_tiny(tiny, use_graph):
     # first call: no drafts, ordinary decode (one frame launch per frame)
     first = st.generate_tokens(tiny["tok"], _opts(mrt_df, F, C, 7, True, use_graph=use_graph))
     assert st.decode_time()[1] == F
+    assert st.spec_acceptance() == -1.0  # no drafts yet: plain decode
     # speculating with unrelated drafts (another seed): tokens from their own logits
     rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"))
     o2 = _opts(mrt_df, F, C, 8, True, use_graph=use_graph)
     second = st.generate_tokens(None, o2, record=rec)
     assert st.decode_time()[1] == F * L  # temporal step + 15 depth steps per frame
+    acc2 = st.spec_acceptance()
+    # levels from the pass: per frame, the agreeing prefix with the drafts plus its first disagreement
+    eq = second == first
+    pre = np.where(eq.all(1), L, np.argmin(eq, 1))
+    assert acc2 == pytest.approx(float(np.minimum(pre + 1, L).sum()) / (F * L))
     _check_against_oracle(tiny, tiny["w"], tiny["ocfg"], tiny["tok"], second, rec["slices"].cpu().numpy(), o2)
     # drafts = a decode of the same chunk and seed: nearly all accepted
     rec3 = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"))
     third = st.generate_tokens(None, o2, record=rec3)
     assert (third == second).mean() >= 0.9, (third, second)
+    assert st.spec_acceptance() >= 0.9
     _check_against_oracle(tiny, tiny["w"], tiny["ocfg"], tiny["tok"], third, rec3["slices"].cpu().numpy(), o2)
     lo = 2 + C * np.arange(L)
     for t in (first, second, third):

@@ -242,3 +242,34 @@ def test_stream_audio_matches_oracle(tiny, pipeline):
     s.close()
     codec.close()
     big.close()
+
+
+def test_stream_adaptive_speculation(tiny):
+    """speculative = 2: a speculative chunk whose levels came from the
+    verification pass less than a quarter of the time makes the next 4
+    chunks decode plainly (one frame launch per frame), then speculation is
+    tried again.  The expected mode of every chunk is replayed from the
+    acceptance each speculative chunk reported."""
+    mrt_df = tiny["mrt_df"]
+    s = _stream(tiny)
+    F, L = 4, 16
+    pause, modes, accs = 0, [], []
+    for i in range(9):
+        o = mrt_df.ChunkOptions(temperature=1.1, top_k=4, guidance_weight=5.0, speculative=2)  # seed: base + index
+        s.generate_chunk(tiny["style_a"], o)
+        launches = s.state.decode_time()[1]
+        acc = s.state.spec_acceptance()
+        spec = launches == F * L
+        assert launches in (F, F * L)
+        modes.append(spec)
+        accs.append(acc)
+        # the policy, replayed: the first chunk has no drafts; a paused chunk decodes plainly
+        want = i > 0 and pause == 0
+        assert spec == want, (i, modes, accs)
+        if pause > 0:
+            pause -= 1
+        elif spec and acc < 0.25:
+            pause = 4
+        assert (acc >= 0.0) == spec
+    print("modes", modes, "acceptance", [round(a, 3) for a in accs], flush=True)
+    s.close()
