@@ -227,6 +227,8 @@ void Coca::plan_gemm(const float* x, int M, const Lin& l, float* y, const float*
 Coca::~Coca() {
   (void)hipSetDevice(device);
   if (stream) (void)hipStreamSynchronize(stream);
+  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+  if (graph_) (void)hipGraphDestroy(graph_);
   if (subs_dev_) (void)hipFree(subs_dev_);
   for (void* p : allocs_) (void)hipFree(p);
   if (h_stage_) (void)hipHostFree(h_stage_);
@@ -235,20 +237,11 @@ Coca::~Coca() {
   if (stream) (void)hipStreamDestroy(stream);
 }
 
-void Coca::embed_text(const int32_t* ids, const float* padding, float* emb) {
+// Every kernel of one prompt, from the embedding to the pooler's output
+// projection (ids_ and mask_ already on the device).
+void Coca::enqueue_text() {
   const CocaConfig& c = cfg;
   const int L = c.max_text_len, D = c.d_model, HD = c.num_heads * c.d_head;
-  MRT_REQUIRE(ids && padding, "musiccoca: null ids / padding");
-  for (int i = 0; i < L; ++i) MRT_REQUIRE(ids[i] >= 0 && ids[i] < c.vocab_size, "musiccoca: token id out of range");
-  MRT_HIP_CHECK(hipSetDevice(device));
-  MRT_HIP_CHECK(hipStreamSynchronize(stream));  // staging reuse
-  int32_t* hs = h_stage_;
-  float* hm = reinterpret_cast<float*>(h_stage_ + L);
-  std::copy(ids, ids + L, hs);
-  for (int i = 0; i < L; ++i) hm[i] = padding[i] * -1e9f;  // musiccoca.cpp:279-284
-  MRT_HIP_CHECK(hipMemcpyAsync(ids_, hs, L * 4, hipMemcpyHostToDevice, stream));
-  MRT_HIP_CHECK(hipMemcpyAsync(mask_, hm, L * 4, hipMemcpyHostToDevice, stream));
-  MRT_HIP_CHECK(hipEventRecord(ev_[0], stream));
   coca_embed(ids_, L, emb_table_, c.vocab_size, D, std::sqrt(static_cast<float>(D)), x_, stream);
   size_t s = 0;
   for (int i = 0; i < c.num_layers; ++i) {
@@ -277,7 +270,41 @@ void Coca::embed_text(const int32_t* ids, const float* padding, float* emb) {
   coca_attention(pq_buf_, PD, pkv_buf_, 2 * PD, pkv_buf_ + PD, 2 * PD, 1, L, c.num_heads, c.pooler_d_head, pscale_,
                  0.0f, nullptr, patt_, stream);
   conv_launch(steps_[s].L, steps_[s].tiles_m, steps_[s].tiles_n, stream);  // pooler o
+}
+
+void Coca::embed_text(const int32_t* ids, const float* padding, float* emb) {
+  const CocaConfig& c = cfg;
+  const int L = c.max_text_len, D = c.d_model;
+  MRT_REQUIRE(ids && padding, "musiccoca: null ids / padding");
+  for (int i = 0; i < L; ++i) MRT_REQUIRE(ids[i] >= 0 && ids[i] < c.vocab_size, "musiccoca: token id out of range");
+  MRT_HIP_CHECK(hipSetDevice(device));
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));  // staging reuse; capture starts on an idle stream
+  if (calls_ == 1 && !graph_exec_) {  // second call: capture the fixed launch sequence once
+    MRT_HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    try {
+      enqueue_text();
+    } catch (...) {
+      hipGraph_t g = nullptr;
+      (void)hipStreamEndCapture(stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    MRT_HIP_CHECK(hipStreamEndCapture(stream, &graph_));
+    MRT_HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+  }
+  int32_t* hs = h_stage_;
+  float* hm = reinterpret_cast<float*>(h_stage_ + L);
+  std::copy(ids, ids + L, hs);
+  for (int i = 0; i < L; ++i) hm[i] = padding[i] * -1e9f;  // musiccoca.cpp:279-284
+  MRT_HIP_CHECK(hipMemcpyAsync(ids_, hs, L * 4, hipMemcpyHostToDevice, stream));
+  MRT_HIP_CHECK(hipMemcpyAsync(mask_, hm, L * 4, hipMemcpyHostToDevice, stream));
+  MRT_HIP_CHECK(hipEventRecord(ev_[0], stream));
+  if (graph_exec_)
+    MRT_HIP_CHECK(hipGraphLaunch(graph_exec_, stream));
+  else
+    enqueue_text();
   MRT_HIP_CHECK(hipEventRecord(ev_[1], stream));
+  ++calls_;
   timed_ = true;
   if (emb) {
     MRT_HIP_CHECK(hipMemcpyAsync(emb, emb_, D * 4, hipMemcpyDeviceToHost, stream));

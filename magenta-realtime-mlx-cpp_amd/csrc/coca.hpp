@@ -52,7 +52,10 @@ class Coca {
   hipStream_t stream = nullptr;
 
   // MusicCoCaEncoder::embed_text for one prompt: ids / padding host
-  // (max_text_len), padding 1.0 = padded; emb host (d_model) or null.
+  // (max_text_len), padding 1.0 = padded; emb host (d_model) or null.  Every
+  // prompt runs the same launch sequence (max_text_len rows): the first call
+  // enqueues it directly, the second captures it into a HIP graph, and that
+  // call and every later one replay the graph.
   void embed_text(const int32_t* ids, const float* padding, float* emb);
   // StyleModel::tokenize of the last embedding (or of `emb` when non-null):
   // tokens host (rvq_depth).
@@ -74,6 +77,7 @@ class Coca {
     const float* w;  // packed weights of its single sub-problem
   };
   Lin pack(const TensorSource& w, const std::vector<std::string>& names, int in);
+  void enqueue_text();
   void plan_gemm(const float* x, int M, const Lin& l, float* y, const float* res, int act);
   float* dalloc(size_t floats);
 
@@ -97,6 +101,9 @@ class Coca {
   float* partial_ = nullptr;
   hipEvent_t ev_[2] = {nullptr, nullptr};
   bool timed_ = false;
+  int calls_ = 0;  // embed_text calls so far
+  hipGraph_t graph_ = nullptr;
+  hipGraphExec_t graph_exec_ = nullptr;
 };
 
 }  // namespace mrt

@@ -848,7 +848,9 @@ __device__ __forceinline__ int block_argmax(const float (&w)[kDrawPer], int C, i
   return arg;
 }
 
-// k-th largest key of the candidates (ties counted), by a most-significant-
+// Threshold key of the top-k set: the k-th largest key of the candidates
+// (ties counted), or a smaller key with no candidate key between the two (so
+// {key >= threshold} is the same set), by a most-significant-
 // byte-first radix select: each pass counts the candidates into per-wave
 // 256-bin LDS histograms, and after one barrier every wave scans the four
 // histograms itself, so the selected digit needs no broadcast.  Pass p uses
@@ -887,12 +889,13 @@ __device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[kDrawPer]
     }
     const unsigned own = cs[0] + cs[1] + cs[2] + cs[3];
     unsigned above = dpp_prefix_sum(own) - own;  // keys in the groups above
-    int bin = -1, before = 0;
+    int bin = -1, before = 0, count = 0;
 #pragma unroll
     for (int i = 3; i >= 0; --i) {
       if (bin < 0 && above < (unsigned)need && above + cs[i] >= (unsigned)need) {
         bin = 4 * g + i;
         before = (int)above;
+        count = (int)cs[i];
       }
       above += cs[i];
     }
@@ -903,6 +906,16 @@ __device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[kDrawPer]
     mask |= 255u << shift;
     need -= __builtin_amdgcn_readlane(before, src);
     if (trace != nullptr && tid == 0) trace[kDrawTrace + 5 + pass] = wall_clock64();
+    // When the selected bin holds exactly the remaining rank, every key in it
+    // belongs to the set, so {key >= prefix} (lower digits zero) is the set
+    // {key >= k-th largest key}: the remaining passes are skipped.  The
+    // threshold this prefix gives must be finite, and the +0 key is left to
+    // the full select so that -0 compares equal to it exactly as there.  The
+    // decision is the same in every wave (same histograms, lane-uniform
+    // values).
+    if (pass < 3 && __builtin_amdgcn_readlane(count, src) == need && prefix != 0x80000000u &&
+        __builtin_isfinite(key_float(prefix)))
+      return prefix;
   }
   return prefix;
 }

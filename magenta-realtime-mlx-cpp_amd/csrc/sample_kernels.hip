@@ -6,8 +6,9 @@
 // Philox-4x32-10 noise.  When the winner over every candidate is itself in the
 // top-k set it is the answer; otherwise the top-k threshold (the k-th largest
 // value, counting ties, i.e. min(topk(x, k)) of decode.cpp:119-120) is found
-// by a 32-step bitwise radix select over order-preserving float keys, each
-// step counting with a DPP wave sum.
+// by a bitwise radix select over order-preserving float keys (at most 32
+// steps, each counting with a DPP wave sum; it stops once exactly k keys lie
+// at or above the prefix).
 #include <cmath>
 
 #include "device_utils.hpp"
@@ -128,7 +129,12 @@ __device__ __forceinline__ int wave_draw_rows(const float* __restrict__ l0, cons
         int cnt = 0;
 #pragma unroll
         for (int t = 0; t < kMaxPerLane; ++t) cnt += key[t] >= cand ? 1 : 0;
-        if (dpp_sum_i(cnt) >= p.top_k) prefix = cand;
+        const int n = dpp_sum_i(cnt);
+        if (n >= p.top_k) prefix = cand;
+        // exactly k keys at or above cand: {key >= cand} is already the top-k
+        // set (no tie straddles it), so the lower bits are not needed; the
+        // threshold must be finite and not +0 (-0 compares equal to +0)
+        if (n == p.top_k && cand != 0x80000000u && __builtin_isfinite(key_float(cand))) break;
       }
       const float thr = key_float(prefix);
 #pragma unroll

@@ -93,3 +93,31 @@ def test_musiccoca_full_size(gpu_available):
     _check(sm, cfg, w, [list(rng.integers(2, cfg.vocab_size, 12))])
     assert sm.embed_time() > 0
     sm.close()
+
+
+@pytest.mark.parametrize("size", ["tiny", "full"])
+def test_musiccoca_graph_replays_match_eager(gpu_available, size):
+    """The first embed_text enqueues its kernels directly, the second captures
+    them into a HIP graph and later calls replay it: every replay, with eager
+    work (RVQ tokenisation) and host synchronisation between them, gives
+    bit-identical embeddings to the direct launches of a second model."""
+    import mrt_df
+    cfg = mrt_df.CocaConfig.tiny() if size == "tiny" else mrt_df.CocaConfig()
+    w = synth_bundle.make_coca_weights(cfg)
+    rng = np.random.default_rng(3)
+    prompts = [M.text_ids(list(rng.integers(2, cfg.vocab_size, n)), cfg.max_text_len) for n in (9, 30)]
+    sm = mrt_df.StyleModel(w, cfg)
+    eager = []
+    for ids, pad in prompts:  # one direct call per model: the eager results
+        ref = mrt_df.StyleModel(w, cfg)
+        eager.append(ref.embed_text(ids, pad))
+        ref.close()
+    first = sm.embed_text(*prompts[0])  # direct
+    np.testing.assert_array_equal(first, eager[0])
+    for rep in range(4):  # capture on the first of these, replays after
+        i = (rep + 1) % 2
+        print(f"{size}: call {rep + 2}, prompt {i}", flush=True)
+        got = sm.embed_text(*prompts[i])
+        np.testing.assert_array_equal(got, eager[i])
+        sm.tokenize()
+    sm.close()
