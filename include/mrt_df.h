@@ -420,7 +420,9 @@ int mrt_coca_create_from_tensors(int n, const char* const* names, const float* c
                                  int device, mrt_coca** out);
 void mrt_coca_destroy(mrt_coca* h);
 /* MusicCoCaEncoder::embed_text of one prompt: ids (max_text_len) int32 and
- * padding (max_text_len) float, host -> embedding (d_model) float, host. */
+ * padding (max_text_len) float, host -> embedding (d_model) float, host.
+ * The second call on a handle captures the launch sequence into a HIP graph
+ * that later calls replay (same results as the direct launches). */
 int mrt_coca_embed_text(mrt_coca* h, const int32_t* ids, const float* padding, float* embedding);
 /* StyleModel::tokenize: embedding host (d_model), or NULL for the last
  * mrt_coca_embed_text result -> tokens (rvq_depth) int32, host. */
