@@ -96,6 +96,83 @@ __global__ __launch_bounds__(kT) void k_coca_attention(const float* __restrict__
   }
 }
 
+// The same attention for a block of 4 queries of one head (self-attention of
+// the text layers: Sk <= 128, D <= 64, D % 4 == 0): the head's K and V rows
+// are staged in LDS (16-byte global loads) once per block instead of being
+// read from global memory per query.  Wave r owns query row r: its lanes
+// score keys l and l + 64 (rows padded to D + 1 floats: a half-wave's keys sit
+// in distinct banks), the softmax runs in registers, and lane l < D then sums
+// output column l.
+constexpr int kAttQ = 4, kAttSk = 128, kAttD = 64;
+__global__ __launch_bounds__(kT) void k_coca_attention_tile(const float* __restrict__ q, int ldq,
+                                                            const float* __restrict__ k, int ldk,
+                                                            const float* __restrict__ v, int ldv, int Sq, int Sk,
+                                                            int D, float cap, const float* __restrict__ mask,
+                                                            float* __restrict__ out, int ldo) {
+  __shared__ float ks[kAttSk][kAttD + 1];
+  __shared__ float vs[kAttSk][kAttD + 1];
+  __shared__ float qs[kAttQ][kAttD];
+  __shared__ float ps[kAttQ][kAttSk];
+  const int q0 = blockIdx.x * kAttQ, h = blockIdx.y, t = threadIdx.x;
+  const int nq = min(kAttQ, Sq - q0), D4 = D >> 2;
+  for (int i = t; i < Sk * D4; i += kT) {
+    const int j = i / D4, c = 4 * (i - j * D4);
+    const float4 kv = *reinterpret_cast<const float4*>(k + (size_t)j * ldk + h * D + c);
+    const float4 vv = *reinterpret_cast<const float4*>(v + (size_t)j * ldv + h * D + c);
+    ks[j][c] = kv.x;
+    ks[j][c + 1] = kv.y;
+    ks[j][c + 2] = kv.z;
+    ks[j][c + 3] = kv.w;
+    vs[j][c] = vv.x;
+    vs[j][c + 1] = vv.y;
+    vs[j][c + 2] = vv.z;
+    vs[j][c + 3] = vv.w;
+  }
+  for (int i = t; i < nq * D; i += kT) {
+    const int r = i / D, d = i - r * D;
+    qs[r][d] = q[(size_t)(q0 + r) * ldq + h * D + d];
+  }
+  __syncthreads();
+  const int r = t >> 6, l = t & 63;
+  if (r >= nq) return;  // no barrier follows
+  const float scale = 1.0f / sqrtf((float)D);
+  float sc[kAttSk / 64];
+#pragma unroll
+  for (int m = 0; m < kAttSk / 64; ++m) {
+    const int j = l + 64 * m;
+    float s = -INFINITY;
+    if (j < Sk) {
+      float acc = 0.f;
+      for (int d = 0; d < D; ++d) acc += qs[r][d] * ks[j][d];
+      s = acc * scale;
+      if (cap > 0.f) s = cap * tanhf(s / cap);
+      if (mask) s += mask[j];
+    }
+    sc[m] = s;
+  }
+  float mx = sc[0];
+#pragma unroll
+  for (int m = 1; m < kAttSk / 64; ++m) mx = fmaxf(mx, sc[m]);
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  float sum = 0.f;
+#pragma unroll
+  for (int m = 0; m < kAttSk / 64; ++m) {
+    sc[m] = l + 64 * m < Sk ? expf(sc[m] - mx) : 0.f;
+    sum += sc[m];
+  }
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+#pragma unroll
+  for (int m = 0; m < kAttSk / 64; ++m)
+    if (l + 64 * m < Sk) ps[r][l + 64 * m] = sc[m] / sum;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the row's probabilities are in LDS
+  if (l < D) {
+    float acc = 0.f;
+    for (int j = 0; j < Sk; ++j) acc += ps[r][j] * vs[j][l];
+    out[(size_t)(q0 + r) * ldo + h * D + l] = acc;
+  }
+}
+
 // rvq.cpp:24-62, one vector: per level, every code's distance (|r|^2 - 2
 // r.c) + |c|^2 (one thread per code), the first minimum, then residual -=
 // the chosen row.  One workgroup of 1024 threads.
@@ -176,8 +253,15 @@ void layer_norm_rows(const float* x, int rows, int D, const float* w, const floa
 void coca_attention(const float* q, int ldq, const float* k, int ldk, const float* v, int ldv, int Sq, int Sk, int H,
                     int D, const float* qscale, float cap, const float* mask, float* out, hipStream_t s) {
   MRT_REQUIRE(Sk >= 1 && Sk <= kT && D >= 1 && D <= 256, "coca attention: Sk <= 256 and d_head <= 256");
-  hipLaunchKernelGGL(k_coca_attention, dim3(Sq, H), dim3(kT), 0, s, q, ldq, k, ldk, v, ldv, Sk, D, qscale, cap, mask,
-                     out, H * D);
+  if (!qscale && Sk <= kAttSk && D <= kAttD && D % 4 == 0 && ldk % 4 == 0 && ldv % 4 == 0 &&
+      reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0) {
+    // query blocks with the head's K / V in LDS
+    hipLaunchKernelGGL(k_coca_attention_tile, dim3((Sq + kAttQ - 1) / kAttQ, H), dim3(kT), 0, s, q, ldq, k, ldk, v,
+                       ldv, Sq, Sk, D, cap, mask, out, H * D);
+  } else {
+    hipLaunchKernelGGL(k_coca_attention, dim3(Sq, H), dim3(kT), 0, s, q, ldq, k, ldk, v, ldv, Sk, D, qscale, cap,
+                       mask, out, H * D);
+  }
   MRT_HIP_CHECK(hipGetLastError());
 }
 
