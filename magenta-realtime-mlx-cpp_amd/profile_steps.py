@@ -14,6 +14,11 @@ counter runs (FETCH_SIZE / WRITE_SIZE per dispatch) and kernel traces.
 --codec F instead runs N codec decodes of F frames (RVQ ids -> audio, fp32,
 seeded synthetic codec weights) after 2 untimed ones.
 
+    python magenta-realtime-mlx-cpp_amd/profile_steps.py --style [--reps N]
+
+--style instead runs N MusicCoCa text embeddings (one 12-id prompt in 128
+slots, fp32, seeded synthetic weights) after 3 untimed ones.
+
 The copy (torch's device copy of M MiB, M above the 256 MB last-level cache)
 reads and writes exactly M MiB; its counter readings give the scale factor
 between the counters and bytes.
@@ -40,6 +45,7 @@ def main() -> None:
     ap.add_argument("--batched", type=int, default=0, help="streams of a batched decode (0: single stream)")
     ap.add_argument("--frames", type=int, default=50, help="frames of the batched decode")
     ap.add_argument("--codec", type=int, default=0, help="frames of codec decodes (0: Depthformer steps)")
+    ap.add_argument("--style", action="store_true", help="MusicCoCa text embeddings instead")
     a = ap.parse_args()
 
     import torch
@@ -59,6 +65,23 @@ def main() -> None:
             ms.append(codec.decode_time())
         print(f"[profile] codec {a.codec} frames: {np.mean(ms):.3f} ms per decode over {a.reps}", flush=True)
         codec.close()
+        return
+
+    if a.style:
+        ccfg = mrt_df.CocaConfig()
+        sm = mrt_df.StyleModel(synth_bundle.make_coca_weights(ccfg), ccfg)
+        ids = np.zeros(ccfg.max_text_len, np.int32)
+        pad = np.ones(ccfg.max_text_len, np.float32)
+        ids[0], pad[0] = 1, 0
+        ids[1:13], pad[1:13] = np.random.default_rng(5).integers(2, ccfg.vocab_size, 12), 0
+        for _ in range(3):
+            sm.embed_text(ids, pad)
+        ms = []
+        for _ in range(a.reps):
+            sm.embed_text(ids, pad)
+            ms.append(sm.embed_time())
+        print(f"[profile] style model: {np.mean(ms):.3f} ms per embed_text over {a.reps}", flush=True)
+        sm.close()
         return
 
     cfg = mrt_df.Config.bench()
