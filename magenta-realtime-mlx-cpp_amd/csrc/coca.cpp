@@ -289,8 +289,15 @@ void Coca::embed_text(const int32_t* ids, const float* padding, float* emb) {
       if (g) (void)hipGraphDestroy(g);
       throw;
     }
-    MRT_HIP_CHECK(hipStreamEndCapture(stream, &graph_));
-    MRT_HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+    hipGraph_t g = nullptr;
+    MRT_HIP_CHECK(hipStreamEndCapture(stream, &g));
+    const hipError_t e = hipGraphInstantiate(&graph_exec_, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {  // the next call captures again
+      (void)hipGraphDestroy(g);
+      graph_exec_ = nullptr;
+      MRT_HIP_CHECK(e);
+    }
+    graph_ = g;
   }
   int32_t* hs = h_stage_;
   float* hm = reinterpret_cast<float*>(h_stage_ + L);
