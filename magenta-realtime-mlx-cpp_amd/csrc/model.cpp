@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <optional>
 #include <thread>
 
 #include "batch.hpp"
@@ -720,8 +721,10 @@ void State::check_device_error() {
 State::~State() {
   (void)hipSetDevice(m.device);
   if (stream) (void)hipStreamSynchronize(stream);
-  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
-  if (graph_) (void)hipGraphDestroy(graph_);
+  for (DecodeGraph& g : graphs_) {
+    (void)hipGraphExecDestroy(g.exec);
+    (void)hipGraphDestroy(g.graph);
+  }
   for (hipEvent_t e : ev_dec_)
     if (e) (void)hipEventDestroy(e);
   for (void* p : allocs_) (void)hipFree(p);
@@ -889,6 +892,7 @@ void State::temporal_step(const void* in, const void* enc, int f, void* out) {
                        std::to_string(f));
   if (persistent()) {
     reserve_epochs(1);
+    PersistSection gate(m.device, stream);
     launch_temporal_p(in, f, out);
   } else {
     run_temporal(in, f, out);
@@ -914,6 +918,7 @@ void State::depth_step(const void* in, int l, int level, int C, int off, float* 
                            ? static_cast<const char*>(m.lm_head) + static_cast<size_t>(off + C * level) * D * esz()
                            : m.lm_head;
     reserve_epochs(1);
+    PersistSection gate(m.device, stream);
     launch_depth_p(in, l, head, level >= 0 ? C : c.vocab_size, logits, nullptr);
   } else {
     run_depth(in, l, level, C, off, logits);
@@ -967,6 +972,61 @@ int State::sample(const float* slice_dev, const GenOpts& o, int frame, int level
   return h_pinned[0];
 }
 
+void State::enqueue_decode_any(const GenOpts& o) {
+  if (spec_drafts_)
+    enqueue_decode_spec(o);
+  else if (persistent())
+    enqueue_decode_p(o);
+  else
+    enqueue_decode(o);
+}
+
+// The captured decode loop for these options: replayed when a graph with the
+// same key exists, else captured (and the least recently used graph dropped
+// once kMaxDecodeGraphs are held).
+hipGraphExec_t State::decode_graph(const GenOpts& o) {
+  const std::vector<double> key = {
+      (double)o.num_frames, (double)o.rvq_depth, (double)o.temperature, (double)o.top_k,
+      (double)o.guidance_weight, (double)o.codebook, (double)o.codec_offset, o.teacher ? 1.0 : 0.0,
+      spec_drafts_ ? 1.0 : 0.0,
+      (double)reinterpret_cast<uintptr_t>(o.record_slices),
+      (double)reinterpret_cast<uintptr_t>(o.record_temporal),
+      (double)reinterpret_cast<uintptr_t>(o.record_drawn),
+      (double)reinterpret_cast<uintptr_t>(o.record_frame_mean)};
+  for (DecodeGraph& g : graphs_)
+    if (g.key == key) {
+      g.used = ++graph_clock_;
+      return g.exec;
+    }
+  if (graphs_.size() >= kMaxDecodeGraphs) {
+    auto lru = std::min_element(graphs_.begin(), graphs_.end(),
+                                [](const DecodeGraph& a, const DecodeGraph& b) { return a.used < b.used; });
+    MRT_HIP_CHECK(hipStreamSynchronize(stream));  // its last replay has ended
+    (void)hipGraphExecDestroy(lru->exec);
+    (void)hipGraphDestroy(lru->graph);
+    graphs_.erase(lru);
+  }
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));  // capture starts on an idle stream
+  MRT_HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+  hipGraph_t graph = nullptr;
+  try {
+    enqueue_decode_any(o);
+  } catch (...) {
+    (void)hipStreamEndCapture(stream, &graph);
+    if (graph) (void)hipGraphDestroy(graph);
+    throw;
+  }
+  MRT_HIP_CHECK(hipStreamEndCapture(stream, &graph));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    MRT_HIP_CHECK(e);
+  }
+  graphs_.push_back(DecodeGraph{key, graph, exec, ++graph_clock_});
+  return exec;
+}
+
 void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* out_host) {
   const Config& c = m.cfg;
   MRT_REQUIRE(o.num_frames >= 1 && o.num_frames <= F, "generate: num_frames exceeds the state's max_frames");
@@ -1003,51 +1063,19 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
     MRT_HIP_CHECK(hipEventCreate(&ev_dec_[1]));
   }
   dec_launches_ = persistent() ? decode_launches(o) : 0;
-  if (o.use_graph) {
-    const std::vector<double> key = {
-        (double)o.num_frames, (double)o.rvq_depth, (double)o.temperature, (double)o.top_k,
-        (double)o.guidance_weight, (double)o.codebook, (double)o.codec_offset, o.teacher ? 1.0 : 0.0,
-        spec_drafts_ ? 1.0 : 0.0,
-        (double)reinterpret_cast<uintptr_t>(o.record_slices),
-        (double)reinterpret_cast<uintptr_t>(o.record_temporal),
-        (double)reinterpret_cast<uintptr_t>(o.record_drawn),
-        (double)reinterpret_cast<uintptr_t>(o.record_frame_mean)};
-    if (!graph_exec_ || key != graph_key_) {
-      if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
-      if (graph_) (void)hipGraphDestroy(graph_);
-      graph_exec_ = nullptr;
-      graph_ = nullptr;
-      MRT_HIP_CHECK(hipStreamSynchronize(stream));  // capture starts on an idle stream
-      MRT_HIP_CHECK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
-      try {
-        if (spec_drafts_)
-          enqueue_decode_spec(o);
-        else if (persistent())
-          enqueue_decode_p(o);
-        else
-          enqueue_decode(o);
-      } catch (...) {
-        hipGraph_t g = nullptr;
-        (void)hipStreamEndCapture(stream, &g);
-        if (g) (void)hipGraphDestroy(g);
-        throw;
-      }
-      MRT_HIP_CHECK(hipStreamEndCapture(stream, &graph_));
-      MRT_HIP_CHECK(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
-      graph_key_ = key;
-    }
+  hipGraphExec_t exec = o.use_graph ? decode_graph(o) : nullptr;
+  {
+    // persistent grids of other states on this device run before or after
+    // this decode, never beside it
+    std::optional<PersistSection> gate;
+    if (persistent()) gate.emplace(m.device, stream);
     MRT_HIP_CHECK(hipEventRecord(ev_dec_[0], stream));
-    MRT_HIP_CHECK(hipGraphLaunch(graph_exec_, stream));
-  } else {
-    MRT_HIP_CHECK(hipEventRecord(ev_dec_[0], stream));
-    if (spec_drafts_)
-      enqueue_decode_spec(o);
-    else if (persistent())
-      enqueue_decode_p(o);
+    if (exec)
+      MRT_HIP_CHECK(hipGraphLaunch(exec, stream));
     else
-      enqueue_decode(o);
+      enqueue_decode_any(o);
+    MRT_HIP_CHECK(hipEventRecord(ev_dec_[1], stream));
   }
-  MRT_HIP_CHECK(hipEventRecord(ev_dec_[1], stream));
   dec_timed_ = true;
   MRT_HIP_CHECK(hipMemcpyAsync(h_pinned, d_tokens, nt * 4, hipMemcpyDeviceToHost, stream));
   if (spec_drafts_)

@@ -243,10 +243,20 @@ class State {
   int temporal_len_ = 0, depth_len_ = 0;
   bool cross_ready_ = false;
 
-  // captured decode loop
-  hipGraph_t graph_ = nullptr;
-  hipGraphExec_t graph_exec_ = nullptr;
-  std::vector<double> graph_key_;
+  // captured decode loops, one per option key (plain and speculative chunks
+  // of adaptive streaming alternate without re-capturing); least recently
+  // used evicted beyond kMaxDecodeGraphs
+  struct DecodeGraph {
+    std::vector<double> key;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    uint64_t used = 0;
+  };
+  static constexpr size_t kMaxDecodeGraphs = 4;
+  std::vector<DecodeGraph> graphs_;
+  uint64_t graph_clock_ = 0;
+  hipGraphExec_t decode_graph(const GenOpts& o);
+  void enqueue_decode_any(const GenOpts& o);
 };
 
 }  // namespace mrt

@@ -95,8 +95,32 @@ int persist_grid(int H, int num_cu, int* bph);
 
 enum class PersistKernel { Temporal, Depth, Frame };
 // Dynamic LDS bytes of a persistent kernel, after allowing the kernel to use
-// them; 0 if the device cannot give one workgroup that much.
+// them; 0 if the device cannot give one workgroup that much, or cannot keep
+// one such workgroup resident per CU (occupancy query), in which case the
+// caller uses the multi-kernel path.
 size_t persist_prepare(DType dt, PersistKernel kind, int device);
+
+// Persistent grids of different states on one device must not run at the
+// same time: each takes one workgroup per CU and polls words written by the
+// rest of its grid, so two grids splitting the CUs would both wait until the
+// spin limit.  A PersistSection brackets the enqueue of one persistent unit of
+// work (a step launch, or a whole decode: its graph launch or eager launches)
+// on `stream`: it holds the device's gate mutex, makes the stream wait for the
+// device's previous persistent unit (an event), and records that event after
+// the enqueued work.  Units on one device therefore run one after another on
+// the GPU, in the order their sections were entered, whatever host threads and
+// streams enqueue them; the host does not block on the GPU.
+class PersistSection {
+ public:
+  PersistSection(int device, hipStream_t stream);
+  ~PersistSection();
+  PersistSection(const PersistSection&) = delete;
+  PersistSection& operator=(const PersistSection&) = delete;
+
+ private:
+  int device_;
+  hipStream_t stream_;
+};
 
 void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t s);
 

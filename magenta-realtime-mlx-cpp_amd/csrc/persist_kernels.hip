@@ -40,6 +40,7 @@
 //   cross:  workgroup (h, j) owns head h's q rows 4j.., then computes the
 //          softmax partial of key block j (ceil(S / bph) keys); workgroup
 //          (h, 0) combines the bph partials.
+#include <mutex>
 #include <algorithm>
 #include <cmath>
 
@@ -1558,7 +1559,12 @@ bool allow_lds(const void* fn, size_t dyn, int device) {
   if (max_lds <= 0) MRT_HIP_CHECK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device));
   if (attr.sharedSizeBytes + dyn > static_cast<size_t>(max_lds)) return false;
   MRT_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(dyn)));
-  return true;
+  // Every workgroup of the grid polls words that other workgroups write, so all
+  // of them must be resident at once: at least one workgroup with this LDS and
+  // these registers per CU (the grid is at most one per CU).
+  int per_cu = 0;
+  MRT_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPersistThreads, dyn));
+  return per_cu >= 1;
 }
 
 template <typename T>
@@ -1571,6 +1577,36 @@ size_t prepare(PersistKernel kind, int device) {
 }
 
 }  // namespace
+
+namespace {
+
+constexpr int kMaxGateDevices = 64;
+struct DeviceGate {
+  std::mutex mu;
+  hipEvent_t last = nullptr;  // end of the device's latest persistent unit; kept until the process ends
+};
+DeviceGate g_gates[kMaxGateDevices];
+
+}  // namespace
+
+PersistSection::PersistSection(int device, hipStream_t stream) : device_(device), stream_(stream) {
+  MRT_REQUIRE(device >= 0 && device < kMaxGateDevices, "persistent kernels: device index out of range");
+  DeviceGate& g = g_gates[device];
+  g.mu.lock();
+  try {
+    if (!g.last) MRT_HIP_CHECK(hipEventCreateWithFlags(&g.last, hipEventDisableTiming));
+    MRT_HIP_CHECK(hipStreamWaitEvent(stream, g.last, 0));
+  } catch (...) {
+    g.mu.unlock();
+    throw;
+  }
+}
+
+PersistSection::~PersistSection() {
+  DeviceGate& g = g_gates[device_];
+  (void)hipEventRecord(g.last, stream_);
+  g.mu.unlock();
+}
 
 int persist_grid(int H, int num_cu, int* bph_out) {
   int bph = kMaxBph;

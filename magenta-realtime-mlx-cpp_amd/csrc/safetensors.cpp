@@ -25,6 +25,9 @@ std::vector<std::string> TensorSource::keys() const {
 }
 
 void TensorList::add(const std::string& name, const float* data, std::vector<int64_t> shape) {
+  int64_t n = 1;
+  for (int64_t d : shape)
+    if (d < 0 || __builtin_mul_overflow(n, d, &n)) throw Error(1, "host tensor " + name + ": bad shape");
   HostTensor t;
   t.shape = std::move(shape);
   t.data = data;
@@ -200,6 +203,24 @@ float half_to_float(uint16_t h) {
 
 }  // namespace
 
+FileMapping::~FileMapping() {
+  if (base) ::munmap(base, len);
+}
+
+namespace {
+
+// A JSON number that is a non-negative integer no larger than `max`.
+bool as_count(const JVal& v, double max, uint64_t* out) {
+  if (v.kind != JVal::Num || !(v.num >= 0.0) || v.num > max || v.num != static_cast<double>(static_cast<uint64_t>(v.num)))
+    return false;
+  *out = static_cast<uint64_t>(v.num);
+  return true;
+}
+
+constexpr double kMaxDim = 1099511627776.0;  // 2^40 elements along one axis
+
+}  // namespace
+
 SafetensorsFile::SafetensorsFile(const std::string& path) {
   label_ = path;
   int fd = ::open(path.c_str(), O_RDONLY);
@@ -209,36 +230,49 @@ SafetensorsFile::SafetensorsFile(const std::string& path) {
     ::close(fd);
     throw Error(5, "weight bundle: too small: " + path);
   }
-  map_len_ = static_cast<size_t>(st.st_size);
-  map_base_ = ::mmap(nullptr, map_len_, PROT_READ, MAP_PRIVATE, fd, 0);
+  const size_t map_len = static_cast<size_t>(st.st_size);
+  void* mapped = ::mmap(nullptr, map_len, PROT_READ, MAP_PRIVATE, fd, 0);
   ::close(fd);
-  if (map_base_ == MAP_FAILED) {
-    map_base_ = nullptr;
-    throw Error(5, "weight bundle: mmap failed: " + path);
-  }
-  const uint8_t* base = static_cast<const uint8_t*>(map_base_);
+  if (mapped == MAP_FAILED) throw Error(5, "weight bundle: mmap failed: " + path);
+  map_file_.base = mapped;
+  map_file_.len = map_len;
+  const uint8_t* base = static_cast<const uint8_t*>(mapped);
   uint64_t hlen = 0;
   for (int i = 0; i < 8; ++i) hlen |= static_cast<uint64_t>(base[i]) << (8 * i);
-  if (hlen > map_len_ - 8) throw Error(5, "weight bundle: bad header length: " + path);
+  if (hlen > map_len - 8) throw Error(5, "weight bundle: bad header length: " + path);
   JParser jp(reinterpret_cast<const char*>(base + 8), reinterpret_cast<const char*>(base + 8 + hlen));
   JVal root = jp.parse();
   if (root.kind != JVal::Obj) throw Error(5, "weight bundle: header is not an object");
   const uint8_t* data = base + 8 + hlen;
-  const size_t data_len = map_len_ - 8 - hlen;
+  const size_t data_len = map_len - 8 - hlen;
   for (auto& kv : root.obj) {
     if (kv.first == "__metadata__") continue;
     const JVal* dt = field(kv.second, "dtype");
     const JVal* sh = field(kv.second, "shape");
     const JVal* off = field(kv.second, "data_offsets");
-    if (!dt || !sh || !off || off->arr.size() != 2) throw Error(5, "weight bundle: bad entry " + kv.first);
+    if (!dt || !sh || !off || dt->kind != JVal::Str || sh->kind != JVal::Arr || off->kind != JVal::Arr ||
+        off->arr.size() != 2)
+      throw Error(5, "weight bundle: bad entry " + kv.first);
+    size_t esz = 0;
+    if (dt->str == "F32") esz = 4;
+    else if (dt->str == "BF16" || dt->str == "F16") esz = 2;
+    else throw Error(5, "weight bundle: unsupported dtype " + dt->str + " for " + kv.first);
     HostTensor t;
-    for (auto& d : sh->arr) t.shape.push_back(static_cast<int64_t>(d.num));
-    const size_t b0 = static_cast<size_t>(off->arr[0].num), b1 = static_cast<size_t>(off->arr[1].num);
-    if (b1 < b0 || b1 > data_len) throw Error(5, "weight bundle: offsets out of range for " + kv.first);
-    const int64_t n = t.numel();
+    uint64_t n = 1;
+    for (auto& d : sh->arr) {
+      uint64_t dim = 0;
+      if (!as_count(d, kMaxDim, &dim)) throw Error(5, "weight bundle: bad dimension in shape of " + kv.first);
+      if (__builtin_mul_overflow(n, dim, &n)) throw Error(5, "weight bundle: element count overflows for " + kv.first);
+      t.shape.push_back(static_cast<int64_t>(dim));
+    }
+    uint64_t b0 = 0, b1 = 0, bytes = 0;
+    if (!as_count(off->arr[0], static_cast<double>(data_len), &b0) ||
+        !as_count(off->arr[1], static_cast<double>(data_len), &b1) || b1 < b0)
+      throw Error(5, "weight bundle: offsets out of range for " + kv.first);
+    if (__builtin_mul_overflow(n, static_cast<uint64_t>(esz), &bytes) || bytes != b1 - b0)
+      throw Error(5, "weight bundle: size mismatch " + kv.first);
     const uint8_t* src = data + b0;
-    if (dt->str == "F32") {
-      if (b1 - b0 != static_cast<size_t>(n) * 4) throw Error(5, "weight bundle: size mismatch " + kv.first);
+    if (esz == 4) {
       if (reinterpret_cast<uintptr_t>(src) % 4 == 0) {
         t.data = reinterpret_cast<const float*>(src);
       } else {
@@ -247,25 +281,18 @@ SafetensorsFile::SafetensorsFile(const std::string& path) {
         t.data = buf->data();
         widened_.push_back(std::move(buf));
       }
-    } else if (dt->str == "BF16" || dt->str == "F16") {
-      if (b1 - b0 != static_cast<size_t>(n) * 2) throw Error(5, "weight bundle: size mismatch " + kv.first);
+    } else {
       auto buf = std::make_unique<std::vector<float>>(n);
-      for (int64_t i = 0; i < n; ++i) {
+      for (uint64_t i = 0; i < n; ++i) {
         uint16_t h;
         std::memcpy(&h, src + 2 * i, 2);
         (*buf)[i] = dt->str == "BF16" ? bf2f(h) : half_to_float(h);
       }
       t.data = buf->data();
       widened_.push_back(std::move(buf));
-    } else {
-      throw Error(5, "weight bundle: unsupported dtype " + dt->str + " for " + kv.first);
     }
     map_[kv.first] = t;
   }
-}
-
-SafetensorsFile::~SafetensorsFile() {
-  if (map_base_) ::munmap(map_base_, map_len_);
 }
 
 }  // namespace mrt

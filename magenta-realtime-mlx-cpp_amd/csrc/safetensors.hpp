@@ -35,16 +35,28 @@ class TensorSource {
   std::string label_;
 };
 
+// A read-only file mapping, unmapped by its destructor (so also when the
+// reader's constructor throws after mapping).
+struct FileMapping {
+  void* base = nullptr;
+  size_t len = 0;
+  FileMapping() = default;
+  FileMapping(const FileMapping&) = delete;
+  FileMapping& operator=(const FileMapping&) = delete;
+  ~FileMapping();
+};
+
 // Memory-maps a bundle file; F32 tensors are used in place, BF16/F16 are
-// widened to fp32 copies.
+// widened to fp32 copies.  Every entry is validated before use: dtype known,
+// each dimension an integer in [0, 2^40], the element count and its byte size
+// free of overflow, and the byte size equal to the entry's data_offsets span,
+// which must lie inside the file.
 class SafetensorsFile : public TensorSource {
  public:
   explicit SafetensorsFile(const std::string& path);
-  ~SafetensorsFile() override;
 
  private:
-  void* map_base_ = nullptr;
-  size_t map_len_ = 0;
+  FileMapping map_file_;
   std::vector<std::unique_ptr<std::vector<float>>> widened_;
 };
 

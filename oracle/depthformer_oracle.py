@@ -297,15 +297,20 @@ class OracleDepthformer:
         return self.linear(self.P.r(gelu_approx(a, self.P) * b), prefix + ".wo")
 
     def _heads(self, y: np.ndarray) -> np.ndarray:
+        """(B, T, H*D) -> (B, T, H, D) -> (B, H, T, D) (modules.cpp:251-253, 264-269)."""
         B, T, _ = y.shape
         return y.reshape(B, T, self.cfg.num_heads, self.cfg.d_kv).transpose(0, 2, 1, 3)
+
+    def _merge_heads(self, o: np.ndarray) -> np.ndarray:
+        """(B, H, T, D) -> (B, T, H, D) -> (B, T, H*D) (modules.cpp:291-293)."""
+        B, _, T, _ = o.shape
+        return o.transpose(0, 2, 1, 3).reshape(B, T, self.cfg.num_heads * self.cfg.d_kv)
 
     def mha(self, x: np.ndarray, prefix: str, *, context: Optional[np.ndarray] = None,
             mask: Optional[np.ndarray] = None, bias: Optional[np.ndarray] = None,
             past: Optional[Tuple[np.ndarray, np.ndarray]] = None,
             cross: Optional[Tuple[np.ndarray, np.ndarray]] = None):
         """MultiHeadAttention::forward (modules.cpp:243-295). Returns (out, (k, v))."""
-        B, T, _ = x.shape
         q = self._heads(self.linear(x, prefix + ".q_proj"))
         if cross is not None:
             k, v = cross  # modules.cpp:258-261: cached cross K/V reused verbatim
@@ -324,8 +329,7 @@ class OracleDepthformer:
         elif mask is not None:
             attn_mask = mask
         o = sdpa(q, k, v, attn_mask, self.P)
-        o = o.transpose(0, 2, 1, 3).reshape(B, T, self.cfg.num_heads * self.cfg.d_kv)
-        return self.linear(o, prefix + ".o_proj"), (k, v)
+        return self.linear(self._merge_heads(o), prefix + ".o_proj"), (k, v)
 
     def project_kv(self, context: np.ndarray, prefix: str):
         """MultiHeadAttention::project_kv (modules.cpp:323-333)."""

@@ -98,6 +98,56 @@ def test_bundle_offsets_out_of_range(lib, tmp_path):
     assert code == MRT_ERR_FORMAT and "out of range" in msg
 
 
+def _raw_bundle(tmp_path, entries, data_len=16, name="raw.safetensors"):
+    hdr = json.dumps(entries).encode()
+    p = tmp_path / name
+    p.write_bytes(struct.pack("<Q", len(hdr)) + hdr + b"\x00" * data_len)
+    return p
+
+
+@pytest.mark.parametrize("shape,why", [
+    ([2 ** 44, 1024, 256], "bad dimension"),        # beyond 2^40 along one axis
+    ([2 ** 40, 2 ** 40, 2 ** 40], "overflows"),     # each axis allowed, the product wraps 64 bits
+    ([-4], "bad dimension"),
+    ([2.5], "bad dimension"),
+    (["4"], "bad dimension"),
+])
+def test_bundle_rejects_bad_shapes(lib, tmp_path, shape, why):
+    """A header shape must be non-negative integers whose element count and byte
+    size do not overflow, and the bytes must equal the data_offsets span: a
+    codebook entry of shape [2^44, 1024, 256] over 0 bytes is refused before any
+    reader trusts its size."""
+    p = _raw_bundle(tmp_path, {"codebooks": {"dtype": "F32", "shape": shape, "data_offsets": [0, 0]}})
+    code, msg, h = _create_path(lib, p)
+    assert code == MRT_ERR_FORMAT and why in msg and not h.value, msg
+
+
+def test_bundle_size_must_equal_offsets_span(lib, tmp_path):
+    p = _raw_bundle(tmp_path, {"w": {"dtype": "F32", "shape": [2], "data_offsets": [0, 16]}})
+    code, msg, _ = _create_path(lib, p)
+    assert code == MRT_ERR_FORMAT and "size mismatch" in msg
+    p = _raw_bundle(tmp_path, {"w": {"dtype": "BF16", "shape": [4], "data_offsets": [0, 16]}}, name="b.safetensors")
+    code, msg, _ = _create_path(lib, p)
+    assert code == MRT_ERR_FORMAT and "size mismatch" in msg
+    p = _raw_bundle(tmp_path, {"w": {"dtype": "F32", "shape": [1], "data_offsets": [-4, 0]}}, name="n.safetensors")
+    code, msg, _ = _create_path(lib, p)
+    assert code == MRT_ERR_FORMAT and "out of range" in msg
+
+
+def test_codec_codebooks_with_huge_shape_are_refused(lib, tmp_path):
+    """The codec's codebooks file goes through the same reader: a (2^44, 1024,
+    256) codebook over no bytes is refused while the files are read."""
+    dec = _raw_bundle(tmp_path, {"w": {"dtype": "F32", "shape": [4], "data_offsets": [0, 16]}}, name="dec.safetensors")
+    cbs = _raw_bundle(tmp_path, {"codebooks": {"dtype": "F32", "shape": [2 ** 44, 1024, 256], "data_offsets": [0, 0]}},
+                      name="cb.safetensors")
+    c = mrt_df._CodecConfig()
+    lib.mrt_codec_config_default(ctypes.byref(c))
+    h = ctypes.c_void_p()
+    code = lib.mrt_codec_create(str(dec).encode(), str(cbs).encode(), ctypes.byref(c), 0, ctypes.byref(h))
+    msg = lib.mrt_last_error().decode()
+    assert code == MRT_ERR_FORMAT and "bad dimension" in msg and not h.value, msg
+
+
 def test_bundle_missing_key(lib, tmp_path):
     cfg = mrt_df.Config.tiny()
     w = synth_bundle.make_weights(cfg, seed=1)

@@ -249,3 +249,40 @@ def test_batch_full_size_32_streams(full):
     np.testing.assert_array_equal(g, eager)
     lo = 2 + C * np.arange(16)
     assert ((g >= lo) & (g < lo + C)).all()
+
+
+@pytest.mark.parametrize("B", [8, 32])
+def test_batch_encoder_full_size(full, B):
+    """Encoder prefill of B streams at the benchmark dims (2B x 1006 rows, each
+    stream its own random context and style).  These are the shapes that take
+    the 256 x 256-tile GEMM (k_gemm_big: outputs <= 4096 wide with >= 512 tiles):
+    the QKV projection (3072 wide) at 8 and 32 streams, and the O and FFN-down
+    projections (1024 wide) at 32.  Every stream's rows must be bit-exact with a
+    single-stream encode of the same tokens (smaller tiles, the same k order per
+    output), and stream 0 within the bf16 tolerance of the oracle's encoder."""
+    import system
+    import torch
+    mrt_df, O = full["mrt_df"], full["O"]
+    scfg = system.SystemConfig()
+    S = full["cfg"].max_encoder_length
+    rows = 2 * B * S
+    assert ((rows + 255) // 256) * (3072 // 256) >= 512  # the QKV projection's tile count
+    rng = np.random.default_rng(1000 + B)
+    toks = []
+    for _ in range(B):
+        ctx = rng.integers(0, 1024, size=(scfg.context_frames, 16)).astype(np.int32)
+        style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+        toks.append(system.build_encoder_inputs(ctx, scfg, style))
+    b = mrt_df.Batch(full["model"], B, max_frames=1)
+    b.encode(np.concatenate(toks, axis=0))
+    enc = b.read_enc_out()
+    torch.cuda.synchronize()
+    b.close()
+    st = full["model"].new_state(max_frames=1)
+    for s in range(B):
+        st.encode(toks[s])
+        one = st.read(mrt_df.BUF_ENC_OUT)
+        assert torch.equal(enc[2 * s:2 * s + 2], one), s
+    st.close()
+    om = O.OracleDepthformer(full["w"], O.DepthformerConfig(**dataclasses.asdict(full["cfg"])), mode="bf16")
+    assert rel(enc[0:2].float().cpu().numpy(), om.encode(toks[0])) <= BF16_TOL

@@ -4,10 +4,13 @@ C ABI: seeded weights (seed 1234), encoder tokens and teacher tokens per the
 benchmark's synthetic-input recipe, two teacher-forced frames (32 depth
 steps) per dtype.
 
-Tolerances (norm-wise relative error): fp32 <= 1e-4, bf16 <= 2e-2; fp32
-teacher-forced argmax agreement >= 99 %; bf16 agreement no lower than the
-bf16-vs-fp32 agreement of the oracle itself (bf16 rounding noise bounds it);
-teacher tokens fed back and frame means bit-exact.  The persistent kernels run
+Tolerances (norm-wise relative error): fp32 <= 1e-4, bf16 <= 2e-2 per level
+slice; fp32 teacher-forced argmax agreement >= 99 %; in bf16 every argmax flip
+must be a near-tie (top-2 margin <= 2 x that draw's guided-logit error);
+teacher tokens fed back and frame means bit-exact; a device draw that differs
+from the oracle sampler's must be an ulp-level tie of its scaled + noise.
+Besides two frames of every path, the whole 50-frame chunk runs teacher-forced
+in both dtypes through the frame kernel (the benchmarked kernel in bf16).  The persistent kernels run
 at these dims (grid 256, one workgroup per CU), so this is the parity check of
 the benchmarked kernels: the decode loop as one launch per frame (default) and
 as one launch per step plus the sampling kernel (MRT_FRAME_KERNEL=0), and the
@@ -20,6 +23,7 @@ import dataclasses
 
 import numpy as np
 import pytest
+from draw_check import assert_argmax_flips_are_near_ties, assert_draws
 
 pytestmark = pytest.mark.gpu
 
@@ -124,22 +128,18 @@ def test_full_size_teacher_forced(env, dtype, tol, path):
     else:
         # Two bf16 evaluations of the same model differ by bf16 rounding noise
         # (~1e-2 relative after 36 layers), and guidance weight 5 turns that into
-        # argmax flips wherever the top-2 margin is small: the oracle's own bf16
-        # restatement agrees with its fp32 restatement on ~81 % of these 32 draws
-        # with random weights.  The HIP bf16 path must do no worse than that floor.
+        # argmax flips wherever the top-2 margin is small.  Every flip must be
+        # such a near-tie: margin <= 2 x that draw's guided-logit error.
+        assert_argmax_flips_are_near_ties(g["slices"], o["slices"])
         o32 = _oracle_cached(env, "fp32")
-        floor = (_guided_argmax(o["slices"]) == _guided_argmax(o32["slices"])).mean()
-        assert agree >= floor - 2 / 32, (agree, floor)
         assert rel(g["slices"], o32["slices"]) <= tol
     np.testing.assert_array_equal(g["frame_mean"], o["frame_mean"])
     # The device draw given its own logits: the oracle's sampler (CFG, top-k 40,
-    # T 1.1, Philox Gumbel noise) on the recorded slices; one near-tie flip of
-    # the 32 draws is tolerated (noise evaluated by different log routines).
+    # T 1.1, Philox Gumbel noise) on the recorded slices; a disagreement passes
+    # only as an ulp-level tie of the oracle's scaled + noise (draw_check).
     O = env["O"]
-    exp = np.array([[2 + 1024 * l + O.sample_level(O.cfg_combine(g["slices"][f, l], 5.0), temperature=1.1, top_k=40,
-                                                   seed=5, frame=f, level=l)
-                     for l in range(16)] for f in range(FRAMES)])
-    assert (g["drawn"] == exp).mean() >= 31 / 32, (g["drawn"], exp)
+    guided = np.array([[O.cfg_combine(g["slices"][f, l], 5.0) for l in range(16)] for f in range(FRAMES)])
+    assert_draws(O, g["drawn"], guided, temperature=1.1, top_k=40, seed=5, offset=2, codebook=1024, max_ties=1)
     # every draw falls in its level's 1024-id range
     lo = 2 + 1024 * np.arange(16)[None, :]
     assert ((g["drawn"] >= lo) & (g["drawn"] < lo + 1024)).all()
@@ -213,50 +213,66 @@ def test_full_size_device_draws(env, fp32_model, temperature, top_k):
     drawn = rec["drawn"].cpu().numpy()
     st.close()
     np.testing.assert_array_equal(toks, drawn)
-    exp = np.array([[2 + C * l + O.sample_level(O.cfg_combine(sl[f, l], 5.0), temperature=temperature, top_k=top_k,
-                                                seed=11, frame=f, level=l)
-                     for l in range(L)] for f in range(F)])
-    assert (drawn == exp).mean() >= 31 / 32, (drawn, exp)
+    guided = np.array([[O.cfg_combine(sl[f, l], 5.0) for l in range(L)] for f in range(F)])
+    assert_draws(O, drawn, guided, temperature=temperature, top_k=top_k, seed=11, offset=2, codebook=C, max_ties=1)
 
 
-def test_full_chunk_fp32_teacher_forced(env, fp32_model):
-    """The whole 2 s chunk in fp32 (50 frames x 16 levels through the frame
-    kernel), teacher-forced on uniform-random tokens: every level's logits, every
-    temporal output, the temporal K/V rings of the first and last layer after
-    the chunk and the depth K/V rings of the last frame against the oracle
-    (norm-wise rel-err <= 1e-4), CFG argmax agreement >= 99 %."""
+@pytest.fixture(scope="module")
+def bf16_model(env):
+    m = env["mrt_df"].Depthformer(env["w"], env["cfg"], dtype="bf16")
+    yield m
+    m.close()
+
+
+@pytest.mark.parametrize("dtype,tol", [("fp32", 1e-4), ("bf16", 2e-2)])
+def test_full_chunk_teacher_forced(env, fp32_model, bf16_model, dtype, tol):
+    """The whole 2 s chunk (50 frames x 16 levels through the frame kernel, the
+    benchmarked kernel in bf16), teacher-forced on uniform-random tokens: every
+    level's logits per (frame, level) slice, every temporal output, the temporal
+    K/V rings of the first and last layer after the chunk and the depth K/V
+    rings of the last frame against the oracle in the same dtype (norm-wise
+    rel-err <= 1e-4 fp32, <= 2e-2 bf16); the frame means bit-exact; CFG argmax
+    agreement >= 99 % in fp32, and in bf16 every flip a near-tie."""
     import torch
     mrt_df, O = env["mrt_df"], env["O"]
+    model = fp32_model if dtype == "fp32" else bf16_model
     F, L, C, D = 50, 16, 1024, env["cfg"].d_model
     rng = np.random.default_rng(42)
     teacher = (2 + C * np.arange(L)[None, :] + rng.integers(0, C, (F, L))).astype(np.int32)
-    st = fp32_model.new_state(max_frames=F)
+    st = model.new_state(max_frames=F)
     rec = dict(slices=torch.zeros((F, L, 2, C), dtype=torch.float32, device="cuda"),
-               temporal=torch.zeros((F, 2, D), dtype=torch.float32, device="cuda"))
+               temporal=torch.zeros((F, 2, D), dtype=model.torch_dtype, device="cuda"),
+               frame_mean=torch.zeros((F, 2, D), dtype=model.torch_dtype, device="cuda"))
     opts = mrt_df.GenOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40, guidance_weight=5.0,
                              seed=5, codebook_size=C, codec_offset=2)
     toks = st.generate_tokens(env["tok"], opts, teacher=teacher, record=rec)
     np.testing.assert_array_equal(toks, teacher)
     sl = rec["slices"].cpu().numpy()
-    tp = rec["temporal"].cpu().numpy()
+    tp = rec["temporal"].float().cpu().numpy()
+    fm = rec["frame_mean"].float().cpu().numpy()
     nt = env["cfg"].num_temporal_layers
-    tk = {i: (st.read(mrt_df.BUF_TEMPORAL_K, i).cpu().numpy(), st.read(mrt_df.BUF_TEMPORAL_V, i).cpu().numpy())
-          for i in (0, nt - 1)}
-    dk = {i: (st.read(mrt_df.BUF_DEPTH_K, i).cpu().numpy(), st.read(mrt_df.BUF_DEPTH_V, i).cpu().numpy())
-          for i in (0, env["cfg"].num_depth_layers - 1)}
+    rd = lambda which, i: st.read(which, i).float().cpu().numpy()
+    tk = {i: (rd(mrt_df.BUF_TEMPORAL_K, i), rd(mrt_df.BUF_TEMPORAL_V, i)) for i in (0, nt - 1)}
+    dk = {i: (rd(mrt_df.BUF_DEPTH_K, i), rd(mrt_df.BUF_DEPTH_V, i)) for i in (0, env["cfg"].num_depth_layers - 1)}
     st.close()
-    om = O.OracleDepthformer(env["w"], O.DepthformerConfig(**dataclasses.asdict(env["cfg"])), mode="fp32")
+    om = O.OracleDepthformer(env["w"], O.DepthformerConfig(**dataclasses.asdict(env["cfg"])), mode=dtype)
     orec = {}
     o = O.GenerateOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40, guidance_weight=5.0, seed=5,
                           codebook_size=C, codec_offset=2)
-    O.generate_tokens(om, env["tok"], o, teacher=teacher, record=orec, enc_out=_oracle_cached(env, "fp32")["enc_out"])
-    errs = [rel(sl[f, l], orec["slices"][f, l]) for f in range(F) for l in range(L)]
-    assert max(errs) <= 1e-4, max(errs)
-    assert rel(tp, orec["temporal_out"]) <= 1e-4
-    assert (_guided_argmax(sl) == _guided_argmax(orec["slices"])).mean() >= 0.99
+    O.generate_tokens(om, env["tok"], o, teacher=teacher, record=orec, enc_out=_oracle_cached(env, dtype)["enc_out"])
+    errs = np.array([[rel(sl[f, l], orec["slices"][f, l]) for l in range(L)] for f in range(F)])
+    assert errs.max() <= tol, (errs.max(), np.unravel_index(errs.argmax(), errs.shape))
+    terrs = [rel(tp[f], orec["temporal_out"][f]) for f in range(F)]
+    assert max(terrs) <= tol, (max(terrs), int(np.argmax(terrs)))
+    np.testing.assert_array_equal(fm, orec["frame_mean"])
+    if dtype == "fp32":
+        assert (_guided_argmax(sl) == _guided_argmax(orec["slices"])).mean() >= 0.99
+    else:
+        agree = assert_argmax_flips_are_near_ties(sl, orec["slices"])
+        print(f"bf16 50-frame chunk: max slice rel-err {errs.max():.3e}, argmax agreement {agree:.3f}")
     for i, (k, v) in tk.items():
-        assert rel(k, orec["temporal_cache"][i]["k"]) <= 1e-4, i
-        assert rel(v, orec["temporal_cache"][i]["v"]) <= 1e-4, i
+        assert rel(k, orec["temporal_cache"][i]["k"]) <= tol, i
+        assert rel(v, orec["temporal_cache"][i]["v"]) <= tol, i
     for i, (k, v) in dk.items():
-        assert rel(k, orec["depth_cache"][i]["k"]) <= 1e-4, i
-        assert rel(v, orec["depth_cache"][i]["v"]) <= 1e-4, i
+        assert rel(k, orec["depth_cache"][i]["k"]) <= tol, i
+        assert rel(v, orec["depth_cache"][i]["v"]) <= tol, i

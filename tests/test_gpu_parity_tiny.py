@@ -10,6 +10,7 @@ import dataclasses
 
 import numpy as np
 import pytest
+from draw_check import assert_draws, check_draw
 
 pytestmark = pytest.mark.gpu
 
@@ -240,7 +241,7 @@ def test_sample_level_matches_oracle(env):
     for C, k, T in [(8, 4, 1.1), (1024, 40, 1.1), (1024, 40, 0.0), (1000, 0, 0.7), (300, 40, 2.0),
                     (1024, 1024, 1.0), (64, 1, 1.0)]:
         opts = _opts(env, codebook_size=C, top_k=k, temperature=T, seed=int(rng.integers(1 << 40)))
-        agree = 0
+        ties = 0
         for trial in range(40):
             sl = (rng.standard_normal((2, C)) * 3).astype(np.float32)
             if trial % 7 == 0:
@@ -248,7 +249,58 @@ def test_sample_level_matches_oracle(env):
             level = trial % 16
             got = st.sample_level(torch.tensor(sl, device="cuda"), opts, frame=trial, level=level)
             g = O.cfg_combine(sl, opts.guidance_weight)
-            exp = opts.codec_offset + C * level + O.sample_level(
-                g, temperature=T, top_k=k, seed=opts.seed, frame=trial, level=level)
-            agree += got == exp
-        assert agree >= 39, (C, k, T, agree)
+            # a disagreement passes only as an ulp-level tie of scaled + noise
+            exp, msg = check_draw(O, g, got - opts.codec_offset - C * level, temperature=T, top_k=k,
+                                  seed=opts.seed, frame=trial, level=level)
+            assert msg is None, (C, k, T, trial, msg)
+            ties += got != opts.codec_offset + C * level + exp
+        assert ties <= 1, (C, k, T, ties)
+
+
+@pytest.mark.parametrize("dtype,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_multi_kernel_decode_path(env, monkeypatch, dtype, tol):
+    """MRT_DECODE_PATH=layers (read when a state is created): the multi-kernel
+    decode (one GEMV kernel per projection, split cross attention with a
+    combine, the sampling kernel) that runs where the persistent kernels'
+    conditions fail.  Teacher-forced against the oracle, then free-running
+    draws against the oracle sampler on the logits it recorded."""
+    monkeypatch.setenv("MRT_DECODE_PATH", "layers")
+    opts = _opts(env)
+    teacher = _teacher(env, opts.num_frames)
+    gt, grec = _gpu_generate(env, dtype, opts, teacher)
+    ot, orec = _oracle_generate(env, dtype, opts, teacher)
+    np.testing.assert_array_equal(gt, teacher)
+    assert rel(grec["temporal"], orec["temporal_out"]) <= tol
+    assert rel(grec["slices"], orec["slices"]) <= tol
+    np.testing.assert_array_equal(grec["frame_mean"], orec["frame_mean"])
+    O = env["O"]
+    free, frec = _gpu_generate(env, dtype, _opts(env, seed=321))
+    guided = np.array([[O.cfg_combine(frec["slices"][f, l], 5.0) for l in range(16)] for f in range(opts.num_frames)])
+    np.testing.assert_array_equal(frec["drawn"], free)
+    assert_draws(O, free, guided, temperature=1.1, top_k=4, seed=321, offset=2, codebook=env["C"], max_ties=1)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_bundle_file_decodes_like_host_tensors(env, tmp_path, dtype):
+    """A model created from a .safetensors bundle file (the reference's
+    WeightBundle path, weights.cpp:118-133) decodes bit for bit like one created
+    from the same tensors in host memory."""
+    import synth_bundle
+    mrt_df = env["mrt_df"]
+    p = tmp_path / "tiny.safetensors"
+    synth_bundle.write_bundle(p, env["w"])
+    opts = _opts(env, seed=77)
+    a = _gpu_generate(env, dtype, opts)
+    mf = mrt_df.Depthformer(str(p), env["cfg"], dtype=dtype)
+    st = mf.new_state(max_frames=opts.num_frames)
+    toks = st.generate_tokens(env["tok"], opts)
+    enc = st.read(mrt_df.BUF_ENC_OUT).float().cpu().numpy()
+    st.close()
+    mf.close()
+    mh = _model(env, dtype)
+    sh = mh.new_state(max_frames=opts.num_frames)
+    sh.encode(env["tok"])
+    np.testing.assert_array_equal(enc, sh.read(mrt_df.BUF_ENC_OUT).float().cpu().numpy())
+    sh.close()
+    mh.close()
+    np.testing.assert_array_equal(toks, a[0])

@@ -6,11 +6,10 @@ accepted up to the first level whose draw differs, and the rest is decoded
 step by step.  Checks (bf16):
   * every token is the oracle sampler's draw from the logits recorded for it
     (per-(frame, level) noise, CFG, temperature, top-k);
-  * those logits match the oracle's decode teacher-forced with the same tokens
-    (norm-wise rel-err over all recorded logits <= 2e-2; single 1024-entry
-    slices carry bf16 rounding noise of the same size, up to ~2.1e-2 at the
-    benchmark dims): the verification pass, the depth K/V it leaves for the
-    continuation and the frame mean are right whatever was accepted;
+  * those logits match the oracle's decode teacher-forced with the same tokens,
+    per (frame, level) slice (see _check_against_oracle for the bounds): the
+    verification pass, the depth K/V it leaves for the continuation and the
+    frame mean are right whatever was accepted;
   * with drafts equal to a decode of the same chunk and seed, nearly every
     draft is accepted and the tokens agree with it;
   * the first call of a state (no drafts) and an fp32 model decode as usual.
@@ -22,6 +21,7 @@ import dataclasses
 
 import numpy as np
 import pytest
+from draw_check import assert_draws
 
 pytestmark = pytest.mark.gpu
 
@@ -61,20 +61,35 @@ def _opts(mrt_df, F, C, seed, spec, **kw):
                              codec_offset=2, speculative=spec, use_graph=kw.get("use_graph", True))
 
 
-def _check_against_oracle(env, model_w, ocfg, enc_tokens, toks, sl, opts, mode="bf16"):
+def _check_against_oracle(env, model_w, ocfg, enc_tokens, toks, sl, opts):
+    """Every token is the oracle sampler's draw from its recorded logits (or an
+    ulp-level tie of scaled + noise); the recorded logits against the oracle
+    teacher-forced on the same tokens, per (frame, level) slice:
+      * <= 2e-2 against the fp32 oracle: the bf16 path's error against exact
+        arithmetic meets the bf16 tolerance on every slice;
+      * <= 2e-2 * sqrt(2) against the bf16 oracle: two independent bf16
+        evaluations, each within 2e-2 of the exact logits with uncorrelated
+        rounding, differ by about sqrt(2) times that (the plain step path on
+        the same tokens reaches 2.08e-2 against the bf16 oracle at the
+        benchmark dims, with 1.72e-2 against fp32);
+      * <= 2e-2 against the bf16 oracle over all slices together."""
     O = env["O"]
     F, L, C = toks.shape[0], toks.shape[1], opts.codebook_size
-    exp = np.array([[2 + C * l + O.sample_level(O.cfg_combine(sl[f, l], opts.guidance_weight),
-                                                temperature=opts.temperature, top_k=opts.top_k, seed=opts.seed,
-                                                frame=f, level=l)
-                     for l in range(L)] for f in range(F)])
-    assert (toks == exp).mean() >= 0.99, (toks, exp)
-    om = O.OracleDepthformer(model_w, ocfg, mode=mode)
-    orec = {}
+    guided = np.array([[O.cfg_combine(sl[f, l], opts.guidance_weight) for l in range(L)] for f in range(F)])
+    assert_draws(O, toks, guided, temperature=opts.temperature, top_k=opts.top_k, seed=opts.seed, offset=2,
+                 codebook=C, max_ties=max(1, F * L // 32))
     o = O.GenerateOptions(num_frames=F, rvq_depth=L, temperature=opts.temperature, top_k=opts.top_k,
                           guidance_weight=opts.guidance_weight, seed=opts.seed, codebook_size=C, codec_offset=2)
-    O.generate_tokens(om, enc_tokens, o, teacher=toks, record=orec)
-    assert rel(sl, orec["slices"]) <= BF16_TOL
+    orec = {}
+    for mode in ("bf16", "fp32"):
+        orec[mode] = {}
+        O.generate_tokens(O.OracleDepthformer(model_w, ocfg, mode=mode), enc_tokens, o, teacher=toks,
+                          record=orec[mode])
+    per32 = max(rel(sl[f, l], orec["fp32"]["slices"][f, l]) for f in range(F) for l in range(L))
+    per16 = max(rel(sl[f, l], orec["bf16"]["slices"][f, l]) for f in range(F) for l in range(L))
+    assert per32 <= BF16_TOL, per32
+    assert per16 <= BF16_TOL * np.sqrt(2.0), per16
+    assert rel(sl, orec["bf16"]["slices"]) <= BF16_TOL
 
 
 @pytest.mark.parametrize("use_graph", [True, False])

@@ -32,7 +32,9 @@ import synth_bundle
 
 
 def micro_cfg():
-    return O.DepthformerConfig(vocab_size=2 + 4 * 4, d_model=64, d_kv=64, d_ff=64, num_heads=1,
+    # two heads of 32 with d_model 64: the brute force splits heads by hand, so a
+    # transposed (T, D, H) split or a wrong bias column shows up
+    return O.DepthformerConfig(vocab_size=2 + 4 * 4, d_model=64, d_kv=32, d_ff=64, num_heads=2,
                                num_encoder_layers=1, num_temporal_layers=1, num_depth_layers=1,
                                max_encoder_length=8, rvq_depth=4)
 
@@ -78,6 +80,7 @@ def b_gelu(x):
 
 
 def b_attend(q, keys, vals, bias):
+    """One head: softmax(q.k + bias) . v, scale 1.0 (modules.cpp:289-290)."""
     s = [sum(q[d] * k[d] for d in range(len(q))) + b for k, b in zip(keys, bias)]
     m = max(s)
     e = [math.exp(v - m) for v in s]
@@ -85,19 +88,32 @@ def b_attend(q, keys, vals, bias):
     return [sum(e[j] / z * vals[j][d] for j in range(len(vals))) for d in range(len(q))]
 
 
-def b_decoder_step(w, p, x, past_k, past_v, bias, enc=None):
-    """One decoder layer for one query row (H = 1, d_kv = d_model = 64)."""
+def b_mha(q, keys, vals, bias, H):
+    """H heads over full-width rows.  Head h owns elements [h*D, (h+1)*D) of every
+    projection row -- the (B, T, H, D) reshape of modules.cpp:251-253 -- and its
+    bias is column h of the per-key bias rows (``bias[j][h]``).  The heads'
+    outputs are concatenated in head order (modules.cpp:291-293)."""
+    D = len(q) // H
+    out = []
+    for h in range(H):
+        sl = slice(h * D, (h + 1) * D)
+        out += b_attend(q[sl], [k[sl] for k in keys], [v[sl] for v in vals], [b[h] for b in bias])
+    return out
+
+
+def b_decoder_step(w, p, x, past_k, past_v, bias, H, enc=None):
+    """One decoder layer for one query row; ``bias[j][h]`` is key j's bias for head h."""
     W = lambda k: w[f"{p}.{k}.weight"].tolist()
     xn = b_rms(x, w[f"{p}.pre_self_attn_norm.weight"].tolist())
     q, k, v = b_lin(W("self_attn.q_proj"), xn), b_lin(W("self_attn.k_proj"), xn), b_lin(W("self_attn.v_proj"), xn)
-    o = b_attend(q, past_k + [k], past_v + [v], bias)
+    o = b_mha(q, past_k + [k], past_v + [v], bias, H)
     y = [a + b for a, b in zip(x, b_lin(W("self_attn.o_proj"), o))]
     if enc is not None:
         yn = b_rms(y, w[f"{p}.pre_cross_attn_norm.weight"].tolist())
         cq = b_lin(W("cross_attn.q_proj"), yn)
         ck = [b_lin(W("cross_attn.k_proj"), e) for e in enc]
         cv = [b_lin(W("cross_attn.v_proj"), e) for e in enc]
-        co = b_attend(cq, ck, cv, [0.0] * len(enc))
+        co = b_mha(cq, ck, cv, [[0.0] * H] * len(enc), H)
         y = [a + b for a, b in zip(y, b_lin(W("cross_attn.o_proj"), co))]
     yn = b_rms(y, w[f"{p}.pre_ffn_norm.weight"].tolist())
     g, u = b_lin(W("ffn.wi_0"), yn), b_lin(W("ffn.wi_1"), yn)
@@ -116,8 +132,8 @@ def test_depth_layer_bruteforce(micro):
         got, (k, v), _ = om.decoder_layer(embs[:, l:l + 1], "depth_layers", 0, bias=om.depth_bias(l),
                                           past=None if l == 0 else (cache[0]["k"], cache[0]["v"]))
         cache[0]["k"], cache[0]["v"] = k, v
-        bias = [table[l - j, 0] for j in range(l + 1)]  # bucket(n) = n for n < 16
-        exp, bk, bv = b_decoder_step(w, "depth_layers.0", embs[0, l].tolist(), pk, pv, bias)
+        bias = [table[l - j].tolist() for j in range(l + 1)]  # bucket(n) = n for n < 16
+        exp, bk, bv = b_decoder_step(w, "depth_layers.0", embs[0, l].tolist(), pk, pv, bias, cfg.num_heads)
         pk.append(bk)
         pv.append(bv)
         np.testing.assert_allclose(got[0, 0], exp, rtol=1e-10, atol=1e-10)
@@ -140,9 +156,9 @@ def test_temporal_layer_bruteforce(micro):
         cache[0]["k"], cache[0]["v"] = k, v
         if ckv is not None:
             cache[0]["ck"], cache[0]["cv"] = ckv
-        bias = [table[f - j, 0] for j in range(f + 1)]
+        bias = [table[f - j].tolist() for j in range(f + 1)]
         exp, bk, bv = b_decoder_step(w, "temporal_layers.0", embs[0, f].tolist(), pk, pv, bias,
-                                     enc=enc[0].tolist())
+                                     cfg.num_heads, enc=enc[0].tolist())
         pk.append(bk)
         pv.append(bv)
         np.testing.assert_allclose(got[0, 0], exp, rtol=1e-10, atol=1e-10)
@@ -160,7 +176,7 @@ def test_encoder_layer_bruteforce(micro):
     vs = [b_lin(W("self_attn.v_proj"), r) for r in xn]
     for t in range(5):
         q = b_lin(W("self_attn.q_proj"), xn[t])
-        o = b_attend(q, ks, vs, [0.0] * 5)  # bidirectional, no bias
+        o = b_mha(q, ks, vs, [[0.0] * cfg.num_heads] * 5, cfg.num_heads)  # bidirectional, no bias
         y = [a + b for a, b in zip(x[0, t].tolist(), b_lin(W("self_attn.o_proj"), o))]
         yn = b_rms(y, w[f"{p}.pre_ffn_norm.weight"].tolist())
         h = [b_gelu(a) * b for a, b in zip(b_lin(W("ffn.wi_0"), yn), b_lin(W("ffn.wi_1"), yn))]
@@ -216,11 +232,13 @@ def test_kv_rows_are_prefix_projections(tiny):
     for l in range(5):
         om.depth_step(embs[:, l:l + 1], cache, l)
     xn = om.norm(embs, "depth_layers.0.pre_self_attn_norm")
-    k = om._heads(om.linear(xn, "depth_layers.0.self_attn.k_proj"))
-    v = om._heads(om.linear(xn, "depth_layers.0.self_attn.v_proj"))
-    np.testing.assert_allclose(cache[0]["k"], k, rtol=1e-12, atol=1e-12)
-    np.testing.assert_allclose(cache[0]["v"], v, rtol=1e-12, atol=1e-12)
+    k = om.linear(xn, "depth_layers.0.self_attn.k_proj")
+    v = om.linear(xn, "depth_layers.0.self_attn.v_proj")
     assert cache[0]["k"].shape == (2, cfg.num_heads, 5, cfg.d_kv)
+    D = cfg.d_kv
+    for h in range(cfg.num_heads):  # head h holds projection elements [h*D, (h+1)*D)
+        np.testing.assert_allclose(cache[0]["k"][:, h], k[:, :, h * D:(h + 1) * D], rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(cache[0]["v"][:, h], v[:, :, h * D:(h + 1) * D], rtol=1e-12, atol=1e-12)
 
 
 def test_ring_mask_equals_concat(tiny):
@@ -306,14 +324,15 @@ def _depth_mismatch(om, w, cfg):
                                           past=None if l == 0 else (cache[0]["k"], cache[0]["v"]))
         cache[0]["k"], cache[0]["v"] = k, v
         exp, bk, bv = b_decoder_step(w, "depth_layers.0", embs[0, l].tolist(), pk, pv,
-                                     [table[l - j, 0] for j in range(l + 1)])
+                                     [table[l - j].tolist() for j in range(l + 1)], cfg.num_heads)
         pk.append(bk)
         pv.append(bv)
         worst = max(worst, float(np.abs(got[0, 0] - np.array(exp)).max()))
     return worst
 
 
-@pytest.mark.parametrize("mutation", ["sdpa_scale", "bias_offset", "gate_up_swapped", "norm_eps_outside"])
+@pytest.mark.parametrize("mutation", ["sdpa_scale", "bias_offset", "gate_up_swapped", "norm_eps_outside",
+                                      "head_split_transposed", "bias_head_reversed"])
 def test_planted_mistakes_are_caught(micro, monkeypatch, mutation):
     cfg, w, om = micro
     assert _depth_mismatch(om, w, cfg) < 1e-10
@@ -333,4 +352,20 @@ def test_planted_mistakes_are_caught(micro, monkeypatch, mutation):
     elif mutation == "norm_eps_outside":
         monkeypatch.setattr(O, "rms_norm",
                             lambda x, g, eps, P: P.r(x / (np.sqrt(np.mean(x * x, -1, keepdims=True)) + 1e-1) * g))
+    elif mutation == "head_split_transposed":
+        # (B, T, D, H) split with the matching merge: self-consistent, wrong layout
+        H, D = cfg.num_heads, cfg.d_kv
+
+        def split(y):
+            B, T, _ = y.shape
+            return y.reshape(B, T, D, H).transpose(0, 3, 1, 2)
+
+        def merge(o):
+            B, _, T, _ = o.shape
+            return o.transpose(0, 2, 3, 1).reshape(B, T, H * D)
+        monkeypatch.setattr(om, "_heads", split)
+        monkeypatch.setattr(om, "_merge_heads", merge)
+    elif mutation == "bias_head_reversed":
+        real_b = om.depth_bias
+        monkeypatch.setattr(om, "depth_bias", lambda i, **kw: real_b(i, **kw)[:, ::-1])
     assert _depth_mismatch(om, w, cfg) > 1e-4
