@@ -17,7 +17,9 @@
  *   - A model handle owns the weights; a state handle owns one decode stream's
  *     encoder output, cross-attention K/V, ring KV caches, scratch and HIP
  *     stream.  Calls on one state are not thread-safe; distinct states may be
- *     driven from distinct threads.
+ *     driven from distinct threads.  Their persistent kernels (one workgroup
+ *     per CU) never run side by side: each decode or step launch of a state
+ *     waits on the device for the previous one of any state on that device.
  */
 #ifndef MRT_DF_H_
 #define MRT_DF_H_
@@ -179,6 +181,14 @@ int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches);
  * first disagreement); -1 when that call did not speculate.  No counterpart
  * in the reference. */
 int mrt_df_state_spec_acceptance(mrt_df_state* st, float* acceptance);
+
+/* Measurement, no counterpart in the reference: the device's read bandwidth
+ * in GB/s (1e9 B/s) for a `bytes` buffer (>= 1 MiB, multiple of 16) read
+ * `passes` times (1..1000) after one warm pass, timed with HIP events.  A
+ * buffer well below the 256 MB last-level cache of MI355X measures that cache
+ * (the MALL); one of several GB measures HBM.  Allocates and frees the buffer;
+ * for the benchmark's roofline peaks. */
+int mrt_probe_read_bandwidth(int device, size_t bytes, int passes, float* gbps);
 
 /* State buffers exposed for parity checks (device-to-device copies). */
 #define MRT_BUF_ENC_OUT 0     /* (rows, enc_len, d_model)                       */

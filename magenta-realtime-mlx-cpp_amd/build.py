@@ -29,6 +29,7 @@ SOURCES = [
     "spec_kernels.hip",
     "codec_kernels.hip",
     "coca_kernels.hip",
+    "probe_kernels.hip",
     "safetensors.cpp",
     "model.cpp",
     "stream.cpp",

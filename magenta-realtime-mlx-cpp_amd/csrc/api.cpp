@@ -344,6 +344,13 @@ int mrt_df_state_spec_acceptance(mrt_df_state* st, float* acceptance) {
   });
 }
 
+int mrt_probe_read_bandwidth(int device, size_t bytes, int passes, float* gbps) {
+  return guarded([&] {
+    if (!gbps) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *gbps = mrt::probe_read_bandwidth(device, bytes, passes);
+  });
+}
+
 int mrt_df_state_buffer_bytes(mrt_df_state* st, int which, size_t* bytes) {
   return guarded([&] {
     if (!bytes) throw mrt::Error(MRT_ERR_INVALID, "null argument");

@@ -142,4 +142,8 @@ void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const Gem
 void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s,
                   bool allow_mfma = true);
 
+// Read bandwidth (GB/s, 1e9 B/s) of `passes` reads of a `bytes` device buffer
+// after one warm pass (probe_kernels.hip).
+float probe_read_bandwidth(int device, size_t bytes, int passes);
+
 }  // namespace mrt

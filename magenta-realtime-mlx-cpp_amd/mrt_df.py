@@ -171,6 +171,15 @@ class GenOptions:
 _lib = None
 
 
+def read_bandwidth(nbytes: int, passes: int, device: int = 0) -> float:
+    """Device read bandwidth in GB/s of `passes` reads of an `nbytes` buffer
+    after one warm pass (mrt_probe_read_bandwidth)."""
+    lib = load_library()
+    out = ctypes.c_float()
+    _check(lib, lib.mrt_probe_read_bandwidth(device, nbytes, passes, ctypes.byref(out)))
+    return float(out.value)
+
+
 def header_functions(path: pathlib.Path = HEADER) -> list:
     """Names of the functions include/mrt_df.h declares."""
     text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
@@ -192,6 +201,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_config_base": (None, [ctypes.POINTER(_Config)]),
         "mrt_df_config_large": (None, [ctypes.POINTER(_Config)]),
         "mrt_df_create": (i32, [ctypes.c_char_p, ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),
+        "mrt_probe_read_bandwidth": (i32, [i32, sz, i32, ctypes.POINTER(ctypes.c_float)]),
         "mrt_df_create_from_tensors": (i32, [i32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(vp),
                                              ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_int32),
                                              ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),

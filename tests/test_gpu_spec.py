@@ -65,14 +65,18 @@ def _check_against_oracle(env, model_w, ocfg, enc_tokens, toks, sl, opts):
     """Every token is the oracle sampler's draw from its recorded logits (or an
     ulp-level tie of scaled + noise); the recorded logits against the oracle
     teacher-forced on the same tokens, per (frame, level) slice:
-      * <= 2e-2 against the fp32 oracle: the bf16 path's error against exact
-        arithmetic meets the bf16 tolerance on every slice;
-      * <= 2e-2 * sqrt(2) against the bf16 oracle: two independent bf16
-        evaluations, each within 2e-2 of the exact logits with uncorrelated
+      * <= B against the fp32 oracle: the bf16 path's error against exact
+        arithmetic;
+      * <= B * sqrt(2) against the bf16 oracle: two independent bf16
+        evaluations, each within B of the exact logits with uncorrelated
         rounding, differ by about sqrt(2) times that (the plain step path on
         the same tokens reaches 2.08e-2 against the bf16 oracle at the
         benchmark dims, with 1.72e-2 against fp32);
-      * <= 2e-2 against the bf16 oracle over all slices together."""
+      * <= 2e-2 against the bf16 oracle over all slices together.
+    B is the bf16 tolerance 2e-2 for slices of the benchmark's 1024 codes.
+    A slice of a few codes (8 in the tiny model) makes a relative norm of
+    single values: there B = max(2e-2, 2 x the largest per-slice error of the
+    oracle's own bf16 restatement against its fp32 one on the same decode)."""
     O = env["O"]
     F, L, C = toks.shape[0], toks.shape[1], opts.codebook_size
     guided = np.array([[O.cfg_combine(sl[f, l], opts.guidance_weight) for l in range(L)] for f in range(F)])
@@ -87,8 +91,12 @@ def _check_against_oracle(env, model_w, ocfg, enc_tokens, toks, sl, opts):
                           record=orec[mode])
     per32 = max(rel(sl[f, l], orec["fp32"]["slices"][f, l]) for f in range(F) for l in range(L))
     per16 = max(rel(sl[f, l], orec["bf16"]["slices"][f, l]) for f in range(F) for l in range(L))
-    assert per32 <= BF16_TOL, per32
-    assert per16 <= BF16_TOL * np.sqrt(2.0), per16
+    bound = BF16_TOL
+    if C < 256:
+        noise = max(rel(orec["bf16"]["slices"][f, l], orec["fp32"]["slices"][f, l]) for f in range(F) for l in range(L))
+        bound = max(BF16_TOL, 2.0 * noise)
+    assert per32 <= bound, (per32, bound)
+    assert per16 <= bound * np.sqrt(2.0), (per16, bound)
     assert rel(sl, orec["bf16"]["slices"]) <= BF16_TOL
 
 
