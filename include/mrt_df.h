@@ -166,6 +166,21 @@ int mrt_df_generate_tokens(mrt_df_state* st, const int32_t* enc_tokens, const mr
  * codec_offset + codebook*level + index to *token (host). */
 int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts* opts, int frame,
                         int level, int32_t* token);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid it).  The
+ * draw of mrt_df_sample_level without a state: `slice_dev` is the same
+ * (2, codebook) fp32 DEVICE array, the LLM id goes to token_dev[0] (DEVICE
+ * int32), the work is enqueued on `hip_stream` (a hipStream_t of the model's
+ * device; NULL = the null stream) and the call returns without waiting.  The
+ * seed word and the fed-back embedding rows the draw kernel writes live in a
+ * fixed 32 KiB device array of the library (one per device, held until the
+ * process ends), so d_model * element size * 6 + 256 must be <= 32768 (fp32:
+ * d_model <= 1354; bf16: the draw kernel's own limit, 2048), else
+ * MRT_ERR_INVALID.  Calls that overlap
+ * on one device race on that array.  Allocates nothing; shares the draw kernel
+ * of mrt_df_sample_level, so tokens are identical. */
+int mrt_df_sample_level_noalloc(mrt_df* h, const float* slice_dev, const mrt_gen_opts* opts, int frame, int level,
+                                int32_t* token_dev, void* hip_stream);
 
 /* Instrumentation, no counterpart in the reference (its CLI times whole
  * chunks on the host, cli/main.cpp:459-505): GPU time in ms of the decode

@@ -330,6 +330,15 @@ int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts
   });
 }
 
+int mrt_df_sample_level_noalloc(mrt_df* h, const float* slice_dev, const mrt_gen_opts* opts, int frame, int level,
+                                int32_t* token_dev, void* hip_stream) {
+  return guarded([&] {
+    if (!h || !slice_dev || !opts || !token_dev) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    h->model->sample_noalloc(slice_dev, to_opts(opts), frame, level, token_dev,
+                             static_cast<hipStream_t>(hip_stream));
+  });
+}
+
 int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches) {
   return guarded([&] {
     if (!ms) throw mrt::Error(MRT_ERR_INVALID, "null argument");

@@ -142,6 +142,14 @@ void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const Gem
 void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s,
                   bool allow_mfma = true);
 
+// One draw as sample_level, allocating nothing: the seed and the feedback rows
+// go to a fixed per-device scratch array of noalloc_scratch_bytes() bytes
+// (sample_kernels.hip); the token is written to token[0].  Throws if d_model
+// needs more scratch.  Calls that overlap on one device race on the scratch.
+size_t noalloc_scratch_bytes();
+void sample_level_noalloc(DType dt, int device, const void* emb, int D, const float* logits, const SampleParams& p,
+                          uint64_t seed, int frame, int level, int* token, hipStream_t s);
+
 // Read bandwidth (GB/s, 1e9 B/s) of `passes` reads of a `bytes` device buffer
 // after one warm pass (probe_kernels.hip).
 float probe_read_bandwidth(int device, size_t bytes, int passes);

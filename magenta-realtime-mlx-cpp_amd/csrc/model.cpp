@@ -951,6 +951,18 @@ void State::enqueue_decode(const GenOpts& o) {
   }
 }
 
+void Model::sample_noalloc(const float* slice_dev, const GenOpts& o, int frame, int level, int32_t* token_dev,
+                           hipStream_t stream) const {
+  MRT_REQUIRE(o.codebook >= 1 && o.codebook <= 1024, "sample: codebook_size must be in [1, 1024]");
+  MRT_REQUIRE(level >= 0 && level < o.rvq_depth && frame >= 0, "sample: frame/level out of range");
+  MRT_REQUIRE(o.codec_offset >= 0 && o.codec_offset + o.codebook * o.rvq_depth <= cfg.vocab_size,
+              "sample: codec levels exceed the vocabulary");
+  MRT_REQUIRE(o.temperature >= 0.0f, "sample: temperature must be >= 0");
+  MRT_HIP_CHECK(hipSetDevice(device));
+  SampleParams sp{o.guidance_weight, o.temperature, o.top_k, o.codebook, o.codec_offset, o.rvq_depth, nullptr};
+  sample_level_noalloc(dt, device, emb, cfg.d_model, slice_dev, sp, o.seed, frame, level, token_dev, stream);
+}
+
 int State::sample(const float* slice_dev, const GenOpts& o, int frame, int level) {
   const Config& c = m.cfg;
   MRT_REQUIRE(o.codebook >= 1 && o.codebook <= 1024, "sample: codebook_size must be in [1, 1024]");

@@ -62,6 +62,8 @@ struct DecoderLayerW {
   const void *norm_sa, *wqkv, *wo, *norm_ca, *wq_c, *wo_c, *norm_ff, *w01, *wo2;
 };
 
+struct GenOpts;
+
 class Model {
  public:
   Model(const TensorSource& src, const Config& cfg, DType dt, int device);
@@ -89,6 +91,12 @@ class Model {
   size_t weight_bytes = 0;
 
   static constexpr int kBucketTable = 4096;
+
+  // One draw as State::sample without a state and without allocating: the
+  // (2, codebook) fp32 device slice in, the LLM id to token_dev[0], enqueued
+  // on `stream` (no wait).  Scratch is the library's fixed per-device array.
+  void sample_noalloc(const float* slice_dev, const GenOpts& o, int frame, int level, int32_t* token_dev,
+                      hipStream_t stream) const;
 
  private:
   std::vector<void*> allocs_;

@@ -10,6 +10,7 @@
 // steps, each counting with a DPP wave sum; it stops once exactly k keys lie
 // at or above the prefix).
 #include <cmath>
+#include <mutex>
 
 #include "device_utils.hpp"
 #include "kernels.hpp"
@@ -289,6 +290,63 @@ void sample_levels(DType dt, int streams, const float* logits, const SampleParam
                        tstride, teacher, tokens, drawn, (const bf16*)emb, D, (bf16*)next_in, (bf16*)fsum,
                        (bf16*)frame_mean);
   MRT_HIP_CHECK(hipGetLastError());
+}
+
+// ---- the draw without library allocations ---------------------------------------------
+namespace {
+
+// Scratch of sample_level_noalloc on each device: the draw's seed word at
+// offset 0, then the three feedback row pairs k_sample writes (next depth
+// input, frame sum, frame mean: 2 x d_model elements each, model dtype) from
+// offset 256.  Every call on a device shares its copy, which keeps the last
+// call's contents.
+constexpr size_t kNoAllocBytes = 32 * 1024;
+constexpr size_t kNoAllocRows = 256;
+__device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+constexpr int kMaxNoAllocDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_ptr[kMaxNoAllocDevices];  // device address of `scratch`, per device
+
+__global__ void k_store_seed(uint64_t* dst, uint64_t seed) { *dst = seed; }
+
+}  // namespace
+
+size_t noalloc_scratch_bytes() { return kNoAllocBytes; }
+
+// The device address of `scratch` on `device` (the current device), looked up
+// once per device.  The host-side name of a __device__ array is not its device
+// address, so kernels only ever receive this pointer.
+static unsigned char* scratch_on(int device) {
+  MRT_REQUIRE(device >= 0 && device < kMaxNoAllocDevices, "sample_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    MRT_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[device] = static_cast<unsigned char*>(ptr);
+  }
+  return g_scratch_ptr[device];
+}
+
+void sample_level_noalloc(DType dt, int device, const void* emb, int D, const float* logits, const SampleParams& p,
+                          uint64_t seed, int frame, int level, int* token, hipStream_t s) {
+  const size_t esz = dt == DType::F32 ? 4 : 2;
+  const size_t need = kNoAllocRows + 3 * 2 * static_cast<size_t>(D) * esz;
+  if (need > kNoAllocBytes)
+    throw Error(1, "sample_noalloc: d_model " + std::to_string(D) + " needs " + std::to_string(need) +
+                       " bytes of scratch, more than the fixed " + std::to_string(kNoAllocBytes));
+  unsigned char* base = scratch_on(device);
+  uint64_t* seed_dev = reinterpret_cast<uint64_t*>(base);
+  unsigned char* rows = base + kNoAllocRows;
+  const size_t row_pair = 2 * static_cast<size_t>(D) * esz;
+  hipLaunchKernelGGL(k_store_seed, dim3(1), dim3(1), 0, s, seed_dev, seed);
+  MRT_HIP_CHECK(hipGetLastError());
+  SampleParams sp = p;
+  sp.seed = seed_dev;
+  sp.noise = nullptr;
+  sp.decided = nullptr;
+  sample_level(dt, logits, sp, frame, level, 0, nullptr, token, nullptr, emb, D, rows, rows + row_pair,
+               rows + 2 * row_pair, s);
 }
 
 }  // namespace mrt

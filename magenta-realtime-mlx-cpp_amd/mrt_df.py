@@ -202,6 +202,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_config_large": (None, [ctypes.POINTER(_Config)]),
         "mrt_df_create": (i32, [ctypes.c_char_p, ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),
         "mrt_probe_read_bandwidth": (i32, [i32, sz, i32, ctypes.POINTER(ctypes.c_float)]),
+        "mrt_df_sample_level_noalloc": (i32, [vp, vp, ctypes.POINTER(_GenOpts), i32, i32, vp, vp]),
         "mrt_df_create_from_tensors": (i32, [i32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(vp),
                                              ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_int32),
                                              ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),
