@@ -147,6 +147,32 @@ int mrt_df_temporal_step(mrt_df_state* st, const void* frame_emb, const void* en
 int mrt_df_depth_step(mrt_df_state* st, const void* tok_emb, int depth_idx, int level,
                       int codebook_size, int codec_offset, float* logits);
 
+/* The two steps with the reference's optional `position_bias` argument
+ * (temporal_step / depth_step, model.cpp:322-330, 516-525): position_bias is a
+ * DEVICE (num_heads, idx + 1) model-dtype array -- the reference's
+ * (1, H, 1, idx + 1) -- used instead of the rel-pos bias of the state's
+ * tables; idx is frame_idx / depth_idx.  Otherwise as mrt_df_temporal_step /
+ * mrt_df_depth_step. */
+int mrt_df_temporal_step_with_bias(mrt_df_state* st, const void* frame_emb, const void* enc_out, int frame_idx,
+                                   const void* position_bias, void* out);
+int mrt_df_depth_step_with_bias(mrt_df_state* st, const void* tok_emb, int depth_idx, const void* position_bias,
+                                int level, int codebook_size, int codec_offset, float* logits);
+
+/* Depthformer::precompute_temporal_biases / precompute_depth_biases
+ * (model.cpp:302-320): kind 0 = temporal, 1 = depth.  Writes the biases of
+ * steps 0..n-1 back to back into `out` (DEVICE, model dtype,
+ * num_heads * n * (n + 1) / 2 elements): step f's (num_heads, f + 1) block --
+ * the reference's f-th (1, H, 1, f + 1) array -- starts at element
+ * num_heads * f * (f + 1) / 2, so `out + that` is step f's position_bias.
+ * Waits for the result. */
+int mrt_df_precompute_biases(mrt_df* h, int kind, int n, void* out);
+
+/* Empties the state's temporal (kind 0) or depth (kind 1) KV cache, as
+ * replacing it with empty_temporal_cache() / empty_depth_cache() does in the
+ * reference (model.cpp:275-300): the next step of that kind must be at index 0.
+ * The cross-attention K/V of the last encode stay. */
+int mrt_df_state_reset_cache(mrt_df_state* st, int kind);
+
 /* generate_tokens (depthformer/decode.cpp:239-573), with the speculative
  * path of decode.cpp:380-446 when opts->speculative applies:
  * enc_tokens (rows, enc_len) host int32 (NULL: reuse the last encode) ->
@@ -181,6 +207,19 @@ int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts
  * of mrt_df_sample_level, so tokens are identical. */
 int mrt_df_sample_level_noalloc(mrt_df* h, const float* slice_dev, const mrt_gen_opts* opts, int frame, int level,
                                 int32_t* token_dev, void* hip_stream);
+
+/* Depthformer::depth_forward_full (depthformer/model.cpp:243-268, model.h:94):
+ * the depth decoder as one pass over k_len positions (1..rvq_depth) of both
+ * CFG rows, decoder_norm and lm_head.  token_embeddings: DEVICE (2, k_len,
+ * d_model) model dtype.  position_bias: NULL for the rel-pos bias of the
+ * k_len x k_len block at query offset 0 (the reference's default), or DEVICE
+ * (num_heads, k_len, k_len) model dtype -- the reference's (1, H, k, k).
+ * causal != 0 masks keys after the query (modules.cpp:197-209).  Writes
+ * DEVICE fp32 (2, k_len, vocab_size) logits (each rounded to the model dtype,
+ * as lm_head's output).  The state's caches are not touched; waits for the
+ * result. */
+int mrt_df_depth_forward_full(mrt_df_state* st, const void* token_embeddings, int k_len, const void* position_bias,
+                              int causal, float* logits);
 
 /* Instrumentation, no counterpart in the reference (its CLI times whole
  * chunks on the host, cli/main.cpp:459-505): GPU time in ms of the decode

@@ -314,6 +314,33 @@ int mrt_df_depth_step(mrt_df_state* st, const void* tok_emb, int depth_idx, int 
   });
 }
 
+int mrt_df_temporal_step_with_bias(mrt_df_state* st, const void* frame_emb, const void* enc_out, int frame_idx,
+                                   const void* position_bias, void* out) {
+  return guarded([&] {
+    if (!frame_emb || !out || !position_bias) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    S(st).temporal_step(frame_emb, enc_out, frame_idx, out, position_bias);
+  });
+}
+
+int mrt_df_depth_step_with_bias(mrt_df_state* st, const void* tok_emb, int depth_idx, const void* position_bias,
+                                int level, int codebook_size, int codec_offset, float* logits) {
+  return guarded([&] {
+    if (!tok_emb || !logits || !position_bias) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    S(st).depth_step(tok_emb, depth_idx, level, codebook_size, codec_offset, logits, position_bias);
+  });
+}
+
+int mrt_df_precompute_biases(mrt_df* h, int kind, int n, void* out) {
+  return guarded([&] {
+    if (!h || !out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    h->model->precompute_biases(kind, n, out);
+  });
+}
+
+int mrt_df_state_reset_cache(mrt_df_state* st, int kind) {
+  return guarded([&] { S(st).reset_cache(kind); });
+}
+
 int mrt_df_generate_tokens(mrt_df_state* st, const int32_t* enc_tokens, const mrt_gen_opts* opts,
                            int32_t* out_tokens) {
   return guarded([&] {
@@ -327,6 +354,14 @@ int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts
   return guarded([&] {
     if (!slice || !opts || !token) throw mrt::Error(MRT_ERR_INVALID, "null argument");
     *token = S(st).sample(slice, to_opts(opts), frame, level);
+  });
+}
+
+int mrt_df_depth_forward_full(mrt_df_state* st, const void* token_embeddings, int k_len, const void* position_bias,
+                              int causal, float* logits) {
+  return guarded([&] {
+    if (!token_embeddings || !logits) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    S(st).depth_forward_full(token_embeddings, k_len, position_bias, causal != 0, logits);
   });
 }
 

@@ -301,7 +301,8 @@ __global__ __launch_bounds__(64) void k_self_attn(const T* __restrict__ Q, const
                                                   const T* __restrict__ Vc, int H, int Lmax, int len,
                                                   int qpos, const int* __restrict__ qpos_ptr, int pos_rows,
                                                   const T* __restrict__ bias_tab,
-                                                  const int* __restrict__ buckets, T* __restrict__ out) {
+                                                  const int* __restrict__ buckets, const T* __restrict__ bias_row,
+                                                  T* __restrict__ out) {
   using S = St<T>;
   constexpr int V = S::kVec;
   const int bh = blockIdx.x, b = bh / H, h = bh - b * H, lane = threadIdx.x;
@@ -333,7 +334,7 @@ __global__ __launch_bounds__(64) void k_self_attn(const T* __restrict__ Q, const
 #pragma unroll
       for (int e = 0; e < V; ++e) sc = fmaf(qs[d + e], S::ld(ke[e]), sc);
     }
-    sc += S::ld(bias_tab[buckets[qpos - j] * H + h]);
+    sc += bias_row != nullptr ? S::ld(bias_row[h * len + j]) : S::ld(bias_tab[buckets[qpos - j] * H + h]);
     ps[j] = sc;
     mx = fmaxf(mx, sc);
   }
@@ -349,6 +350,42 @@ __global__ __launch_bounds__(64) void k_self_attn(const T* __restrict__ Q, const
   float o = 0.f;
   for (int j = 0; j < len; ++j) o = fmaf(ps[j], S::ld(Vp[(size_t)j * 64 + lane]), o);
   out[(size_t)b * HD + h * 64 + lane] = S::st(o / sum);
+}
+
+// Full-sequence self attention (depth_forward_full, model.cpp:243-268): one
+// 64-lane block per (row m = b*K + i, head h); lane j scores key j, lane d
+// then sums dimension d of the softmax-weighted values.
+template <typename T>
+__global__ __launch_bounds__(64) void k_full_attn(const T* __restrict__ qkv, int K, int H,
+                                                  const T* __restrict__ explicit_bias,
+                                                  const T* __restrict__ bias_tab, const int* __restrict__ buckets,
+                                                  int causal, T* __restrict__ out) {
+  using S = St<T>;
+  const int mh = blockIdx.x, m = mh / H, h = mh - m * H, lane = threadIdx.x;
+  const int b = m / K, i = m - b * K;
+  const int HD = H * 64, ld = 3 * HD;
+  __shared__ float qs[64];
+  __shared__ float ps[64];
+  qs[lane] = S::ld(qkv[(size_t)m * ld + h * 64 + lane]);
+  __syncthreads();
+  const int len = causal ? i + 1 : K;
+  float sc = -INFINITY;
+  if (lane < len) {
+    const T* kr = qkv + (size_t)(b * K + lane) * ld + HD + h * 64;
+    float acc = 0.f;
+    for (int d = 0; d < 64; ++d) acc = fmaf(qs[d], S::ld(kr[d]), acc);
+    const float bias = explicit_bias != nullptr ? S::ld(explicit_bias[((size_t)h * K + i) * K + lane])
+                                                : S::ld(bias_tab[buckets[max(i - lane, 0)] * H + h]);
+    sc = acc + bias;
+  }
+  const float mx = wave_max(sc);
+  const float p = lane < len ? expf(sc - mx) : 0.f;
+  const float sum = wave_sum(p);
+  ps[lane] = p;
+  __syncthreads();
+  float o = 0.f;
+  for (int j = 0; j < len; ++j) o = fmaf(ps[j], S::ld(qkv[(size_t)(b * K + j) * ld + 2 * HD + h * 64 + lane]), o);
+  out[(size_t)m * HD + h * 64 + lane] = S::st(o / sum);
 }
 
 // Partial softmax-attention of one (row, head) over one block of keys.
@@ -449,26 +486,66 @@ __global__ void k_embed_fill(const T* __restrict__ emb, int D, int id, T* __rest
 
 void self_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H, int Lmax,
                int len, int qpos, const void* bias_tab, const int* buckets, void* out,
-               hipStream_t s) {
+               hipStream_t s, const void* bias_row) {
   MRT_REQUIRE(len >= 1 && len <= kMaxSelfLen && len <= Lmax, "self_attn: bad cache length");
   MRT_REQUIRE(qpos >= len - 1, "self_attn: query precedes keys");
-  self_attn_at(dt, nb, Q, Kc, Vc, H, Lmax, len, qpos, nullptr, bias_tab, buckets, out, s);
+  self_attn_at(dt, nb, Q, Kc, Vc, H, Lmax, len, qpos, nullptr, bias_tab, buckets, out, s, 0, bias_row);
 }
 
 void self_attn_at(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H, int Lmax, int len,
                   int qpos, const int* qpos_ptr, const void* bias_tab, const int* buckets, void* out,
-                  hipStream_t s, int pos_rows) {
+                  hipStream_t s, int pos_rows, const void* bias_row) {
   MRT_REQUIRE(qpos_ptr == nullptr || Lmax <= kMaxSelfLen, "self_attn: ring longer than the kernel's score buffer");
   MRT_REQUIRE(pos_rows == 0 || (nb % pos_rows == 0 && nb / pos_rows <= Lmax && Lmax <= kMaxSelfLen),
               "self_attn: positions exceed the ring");
+  MRT_REQUIRE(bias_row == nullptr || (qpos_ptr == nullptr && pos_rows == 0),
+              "self_attn: an explicit bias needs a host-known query position");
   if (dt == DType::F32)
     hipLaunchKernelGGL(k_self_attn<float>, dim3(nb * H), dim3(64), 0, s, (const float*)Q,
                        (const float*)Kc, (const float*)Vc, H, Lmax, len, qpos, qpos_ptr, pos_rows,
-                       (const float*)bias_tab, buckets, (float*)out);
+                       (const float*)bias_tab, buckets, (const float*)bias_row, (float*)out);
   else
     hipLaunchKernelGGL(k_self_attn<bf16>, dim3(nb * H), dim3(64), 0, s, (const bf16*)Q,
                        (const bf16*)Kc, (const bf16*)Vc, H, Lmax, len, qpos, qpos_ptr, pos_rows,
-                       (const bf16*)bias_tab, buckets, (bf16*)out);
+                       (const bf16*)bias_tab, buckets, (const bf16*)bias_row, (bf16*)out);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+namespace {
+
+// Step f's bias rows (H, f + 1) at element H * f * (f + 1) / 2:
+// out[..][h][j] = table[bucket[f - j], h] for j <= f.
+template <typename T>
+__global__ void k_bias_rows(const T* __restrict__ table, const int* __restrict__ buckets, int H, int n,
+                            T* __restrict__ out) {
+  const int f = blockIdx.x;
+  T* o = out + (size_t)H * f * (f + 1) / 2;
+  for (int e = threadIdx.x; e < H * (f + 1); e += blockDim.x) {
+    const int h = e / (f + 1), j = e - h * (f + 1);
+    o[e] = table[buckets[f - j] * H + h];
+  }
+}
+
+}  // namespace
+
+void bias_rows(DType dt, const void* table, const int* buckets, int H, int n, void* out, hipStream_t s) {
+  MRT_REQUIRE(n >= 1 && H >= 1, "bias_rows: empty request");
+  if (dt == DType::F32)
+    hipLaunchKernelGGL(k_bias_rows<float>, dim3(n), dim3(256), 0, s, (const float*)table, buckets, H, n, (float*)out);
+  else
+    hipLaunchKernelGGL(k_bias_rows<bf16>, dim3(n), dim3(256), 0, s, (const bf16*)table, buckets, H, n, (bf16*)out);
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void full_attn(DType dt, int nb, int K, int H, const void* qkv, const void* explicit_bias, const void* bias_tab,
+               const int* buckets, bool causal, void* out, hipStream_t s) {
+  MRT_REQUIRE(nb >= 1 && K >= 1 && K <= 64, "full_attn: K must be in [1, 64]");
+  if (dt == DType::F32)
+    hipLaunchKernelGGL(k_full_attn<float>, dim3(nb * K * H), dim3(64), 0, s, (const float*)qkv, K, H,
+                       (const float*)explicit_bias, (const float*)bias_tab, buckets, causal ? 1 : 0, (float*)out);
+  else
+    hipLaunchKernelGGL(k_full_attn<bf16>, dim3(nb * K * H), dim3(64), 0, s, (const bf16*)qkv, K, H,
+                       (const bf16*)explicit_bias, (const bf16*)bias_tab, buckets, causal ? 1 : 0, (bf16*)out);
   MRT_HIP_CHECK(hipGetLastError());
 }
 

@@ -88,6 +88,8 @@ struct GemmOut {
     } else if (a.kind == GemmEpi::Resid) {
       T* p = C + (size_t)m * N + n;
       *p = S::st(S::ld(*p) + S::rnd(acc));
+    } else if (a.kind == GemmEpi::StoreF32) {
+      static_cast<float*>(a.C)[(size_t)m * N + n] = S::rnd(acc);
     } else {  // CrossKV
       const int lk = n / a.HD, nn = n - lk * a.HD;
       const int h = nn >> 6, d = nn & 63;

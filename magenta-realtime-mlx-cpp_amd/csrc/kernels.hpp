@@ -45,16 +45,28 @@ void gemv_geglu(DType dt, int nb, const void* W01, int F, int K, const void* X, 
 // ---- decode attention -------------------------------------------------------
 // Self-attention of the query at ring position qpos over slots 0..len-1,
 // scale 1.0, additive bias table[bucket[qpos - j], h] (modules.cpp:243-295).
+// bias_row: an explicit bias (H, len) model dtype replacing the table lookup.
 void self_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H,
                int Lmax, int len, int qpos, const void* bias_tab, const int* buckets,
-               void* out, hipStream_t s);
+               void* out, hipStream_t s, const void* bias_row = nullptr);
 // The same with the query position read on the device from *qpos_ptr when it
 // is non-null (len = qpos + 1; the caller keeps it below Lmax).
 // pos_rows > 0 instead attends all positions of one frame at once: query row
 // b is position b / pos_rows of ring row b % pos_rows, causal (len = pos + 1).
 void self_attn_at(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H, int Lmax, int len,
                   int qpos, const int* qpos_ptr, const void* bias_tab, const int* buckets, void* out,
-                  hipStream_t s, int pos_rows = 0);
+                  hipStream_t s, int pos_rows = 0, const void* bias_row = nullptr);
+// The rel-pos bias of steps 0..n-1 (precompute_{temporal,depth}_biases,
+// model.cpp:302-320) back to back: step f's (H, f + 1) block at element
+// H * f * (f + 1) / 2, entry [h][j] = table[bucket(f - j), h].
+void bias_rows(DType dt, const void* table, const int* buckets, int H, int n, void* out, hipStream_t s);
+// Self-attention of all K positions of nb sequences at once (the full-sequence
+// depth pass): qkv (nb*K, 3*HD) rows m = b*K + i, [q | k | v]; query (b, i)
+// attends keys (b, j) for j <= i (causal) or all j < K, with the bias
+// explicit[(h*K + i)*K + j] when `explicit_bias` is set, else
+// bias_tab[buckets[max(i - j, 0)] * H + h]; scale 1.0; out (nb*K, HD).  K <= 64.
+void full_attn(DType dt, int nb, int K, int H, const void* qkv, const void* explicit_bias, const void* bias_tab,
+               const int* buckets, bool causal, void* out, hipStream_t s);
 // Cross-attention over S encoder keys (no bias/mask), split over key blocks.
 // ``part`` needs nb*H*nsplit*66 floats.
 void cross_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc, int H,
@@ -128,6 +140,7 @@ enum class GemmEpi : int {
   Geglu = 2,    // B packed like gemv_geglu; C (M, N/2)
   CrossKV = 3,  // n = (layer*2 + kv)*HD + h*64 + d; m = b*S + s ->
                 //   C[(((layer*2+kv)*nb + b)*H + h)*S + s][d]
+  StoreF32 = 4, // C (M, N) fp32, each value rounded to the model dtype first (logits)
 };
 struct GemmEpiArgs {
   GemmEpi kind = GemmEpi::Store;

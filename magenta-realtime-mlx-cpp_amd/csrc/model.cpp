@@ -343,14 +343,18 @@ State::State(Model& model, int rows_, int max_frames, int enc_len)
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_err_), 64, hipHostMallocDefault));
   *h_err_ = 0;
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_seed_), 64, hipHostMallocDefault));
-  if (m.dt == DType::BF16) {  // speculative decoding (verification pass over 2 L rows)
+  {  // rows of the full-sequence depth pass and the speculative verification pass (2 L rows)
     const size_t R2 = 2 * L;
-    d_drafts_ = static_cast<int*>(dalloc(static_cast<size_t>(F) * L * 4));
     sx_ = dalloc(R2 * D * e);
     sxn_ = dalloc(R2 * std::max(D, FF) * e);
-    sq_ = dalloc(R2 * HD * e);
+    sqkv_ = dalloc(R2 * 3 * HD * e);
     satt_ = dalloc(R2 * HD * e);
     sffh_ = dalloc(R2 * FF * e);
+  }
+  if (m.dt == DType::BF16) {  // speculative decoding
+    const size_t R2 = 2 * L;
+    d_drafts_ = static_cast<int*>(dalloc(static_cast<size_t>(F) * L * 4));
+    sq_ = dalloc(R2 * HD * e);
     slog_ = static_cast<float*>(dalloc(R2 * 1024 * 4));
     sdrawn_ = static_cast<int*>(dalloc(L * 4));
     sdecided_ = static_cast<int*>(dalloc(static_cast<size_t>(F) * 4));
@@ -570,15 +574,17 @@ StepArgs State::depth_args(const void* in, int l, const void* head_w, int head_r
   return a;
 }
 
-void State::launch_temporal_p(const void* in, int f, void* out) {
+void State::launch_temporal_p(const void* in, int f, void* out, const void* bias) {
   StepArgs a = temporal_args(in, f, out);
+  a.bias_row = bias;
   if (d_trace_ && f == 1) a.trace = d_trace_;
   launch_step(m.dt, a, persist_grid_, lds_t_, stream);
 }
 
 void State::launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits,
-                           float* rec_slice) {
+                           float* rec_slice, const void* bias) {
   StepArgs a = depth_args(in, l, head_w, head_rows, logits, rec_slice);
+  a.bias_row = bias;
   launch_step(m.dt, a, persist_grid_, lds_d_, stream);
 }
 
@@ -837,7 +843,7 @@ void State::project_cross(const void* src) {
 }
 
 // One temporal step on the device (model.cpp:493-513 eager semantics).
-void State::run_temporal(const void* in, int f, void* out) {
+void State::run_temporal(const void* in, int f, void* out, const void* bias) {
   const Config& c = m.cfg;
   const DType dt = m.dt;
   const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads;
@@ -845,7 +851,7 @@ void State::run_temporal(const void* in, int f, void* out) {
   for (int i = 0; i < c.num_temporal_layers; ++i) {
     const DecoderLayerW& L = m.tmp[i];
     gemv_qkv(dt, rows, L.wqkv, HD, D, out, D, {L.norm_sa}, q, tk(i), tv(i), H, F, f, stream);
-    self_attn(dt, rows, q, tk(i), tv(i), H, F, f + 1, f, m.tbias, m.tbuckets, attn, stream);
+    self_attn(dt, rows, q, tk(i), tv(i), H, F, f + 1, f, m.tbias, m.tbuckets, attn, stream, bias);
     gemv_resid(dt, rows, L.wo, D, HD, attn, HD, {}, out, D, stream);
     gemv_store(dt, rows, L.wq_c, HD, D, out, D, {L.norm_ca}, q, HD, stream);
     cross_attn(dt, rows, q, ck(i), cv(i), H, S, attn, part, nsplit, stream);
@@ -857,7 +863,40 @@ void State::run_temporal(const void* in, int f, void* out) {
 
 // One depth step on the device (model.cpp:638-658): 4 layers, decoder_norm,
 // lm_head (full vocabulary or one level's rows).
-void State::run_depth(const void* in, int l, int level, int C, int off, float* logits) {
+// Depthformer::depth_forward_full (model.cpp:243-268): the depth stack over k
+// positions of both rows in one pass (rows m = b*k + i), causal unless asked
+// otherwise, with the rel-pos bias of the k x k block or an explicit
+// (H, k, k) one, then decoder_norm and lm_head over the whole vocabulary.
+// The caches are not touched (the reference discards the pass's K/V).
+void State::depth_forward_full(const void* emb, int k, const void* bias, bool causal, float* logits) {
+  const Config& c = m.cfg;
+  const DType dt = m.dt;
+  MRT_REQUIRE(k >= 1 && k <= c.rvq_depth, "depth_forward_full: k_len must be in [1, rvq_depth]");
+  const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads, M = rows * k;
+  MRT_HIP_CHECK(hipSetDevice(m.device));
+  copy(sx_, emb, static_cast<size_t>(M) * D * esz());
+  auto gemm_to = [&](const void* A, const void* W, int N, int K, GemmEpi kind, void* C) {
+    GemmEpiArgs e;
+    e.kind = kind;
+    e.C = C;
+    gemm(dt, A, W, M, N, K, e, stream);
+  };
+  for (int i = 0; i < c.num_depth_layers; ++i) {
+    const DecoderLayerW& W = m.dep[i];
+    rmsnorm_rows(dt, sx_, W.norm_sa, 1e-6f, M, D, sxn_, stream);
+    gemm_to(sxn_, W.wqkv, 3 * HD, D, GemmEpi::Store, sqkv_);
+    full_attn(dt, rows, k, H, sqkv_, bias, m.dbias, m.dbuckets, causal, satt_, stream);
+    gemm_to(satt_, W.wo, D, HD, GemmEpi::Resid, sx_);
+    rmsnorm_rows(dt, sx_, W.norm_ff, 1e-6f, M, D, sxn_, stream);
+    gemm_to(sxn_, W.w01, 2 * FF, D, GemmEpi::Geglu, sffh_);
+    gemm_to(sffh_, W.wo2, D, FF, GemmEpi::Resid, sx_);
+  }
+  rmsnorm_rows(dt, sx_, m.dec_norm, 1e-6f, M, D, sxn_, stream);
+  gemm_to(sxn_, m.lm_head, c.vocab_size, D, GemmEpi::StoreF32, logits);
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+}
+
+void State::run_depth(const void* in, int l, int level, int C, int off, float* logits, const void* bias) {
   const Config& c = m.cfg;
   const DType dt = m.dt;
   const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads, L = c.rvq_depth;
@@ -865,7 +904,7 @@ void State::run_depth(const void* in, int l, int level, int C, int off, float* l
   for (int i = 0; i < c.num_depth_layers; ++i) {
     const DecoderLayerW& W = m.dep[i];
     gemv_qkv(dt, rows, W.wqkv, HD, D, x, D, {W.norm_sa}, q, dk(i), dv(i), H, L, l, stream);
-    self_attn(dt, rows, q, dk(i), dv(i), H, L, l + 1, l, m.dbias, m.dbuckets, attn, stream);
+    self_attn(dt, rows, q, dk(i), dv(i), H, L, l + 1, l, m.dbias, m.dbuckets, attn, stream, bias);
     gemv_resid(dt, rows, W.wo, D, HD, attn, HD, {}, x, D, stream);
     gemv_geglu(dt, rows, W.w01, FF, D, x, D, {W.norm_ff}, ffh, FF, stream);
     gemv_resid(dt, rows, W.wo2, D, FF, ffh, FF, {}, x, D, stream);
@@ -878,7 +917,7 @@ void State::run_depth(const void* in, int l, int level, int C, int off, float* l
   }
 }
 
-void State::temporal_step(const void* in, const void* enc, int f, void* out) {
+void State::temporal_step(const void* in, const void* enc, int f, void* out, const void* bias) {
   MRT_REQUIRE(f >= 0 && f < F, "temporal_step: frame_idx out of range for this state");
   MRT_HIP_CHECK(hipSetDevice(m.device));
   if (f == 0) {
@@ -893,14 +932,14 @@ void State::temporal_step(const void* in, const void* enc, int f, void* out) {
   if (persistent()) {
     reserve_epochs(1);
     PersistSection gate(m.device, stream);
-    launch_temporal_p(in, f, out);
+    launch_temporal_p(in, f, out, bias);
   } else {
-    run_temporal(in, f, out);
+    run_temporal(in, f, out, bias);
   }
   temporal_len_ = f + 1;
 }
 
-void State::depth_step(const void* in, int l, int level, int C, int off, float* logits) {
+void State::depth_step(const void* in, int l, int level, int C, int off, float* logits, const void* bias) {
   const Config& c = m.cfg;
   MRT_REQUIRE(l >= 0 && l < c.rvq_depth, "depth_step: depth_idx out of range");
   if (level >= 0) {
@@ -919,11 +958,35 @@ void State::depth_step(const void* in, int l, int level, int C, int off, float* 
                            : m.lm_head;
     reserve_epochs(1);
     PersistSection gate(m.device, stream);
-    launch_depth_p(in, l, head, level >= 0 ? C : c.vocab_size, logits, nullptr);
+    launch_depth_p(in, l, head, level >= 0 ? C : c.vocab_size, logits, nullptr, bias);
   } else {
-    run_depth(in, l, level, C, off, logits);
+    run_depth(in, l, level, C, off, logits, bias);
   }
   depth_len_ = l + 1;
+}
+
+void State::reset_cache(int kind) {
+  MRT_REQUIRE(kind == 0 || kind == 1, "reset_cache: kind must be 0 (temporal) or 1 (depth)");
+  if (kind == 0)
+    temporal_len_ = 0;
+  else
+    depth_len_ = 0;
+}
+
+void Model::precompute_biases(int kind, int n, void* out) const {
+  MRT_REQUIRE(kind == 0 || kind == 1, "precompute_biases: kind must be 0 (temporal) or 1 (depth)");
+  MRT_REQUIRE(n >= 1 && n < kBucketTable, "precompute_biases: n out of range");
+  MRT_HIP_CHECK(hipSetDevice(device));
+  hipStream_t s = nullptr;
+  MRT_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  try {
+    bias_rows(dt, kind == 0 ? tbias : dbias, kind == 0 ? tbuckets : dbuckets, cfg.num_heads, n, out, s);
+    MRT_HIP_CHECK(hipStreamSynchronize(s));
+  } catch (...) {
+    (void)hipStreamDestroy(s);
+    throw;
+  }
+  MRT_HIP_CHECK(hipStreamDestroy(s));
 }
 
 void State::enqueue_decode(const GenOpts& o) {

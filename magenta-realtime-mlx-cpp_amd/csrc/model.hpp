@@ -97,6 +97,10 @@ class Model {
   // on `stream` (no wait).  Scratch is the library's fixed per-device array.
   void sample_noalloc(const float* slice_dev, const GenOpts& o, int frame, int level, int32_t* token_dev,
                       hipStream_t stream) const;
+  // precompute_{temporal,depth}_biases (model.cpp:302-320): kind 0 temporal,
+  // 1 depth; steps 0..n-1 back to back into the device buffer `out` (step f's
+  // (H, f + 1) block at element H f (f + 1) / 2).  Waits for the result.
+  void precompute_biases(int kind, int n, void* out) const;
 
  private:
   std::vector<void*> allocs_;
@@ -153,10 +157,19 @@ class State {
   int* enc_tokens_dev() const { return d_enc_tok; }
   int* tokens_dev() const { return d_tokens; }
   void project_cross(const void* enc_out_dev);
-  void temporal_step(const void* in, const void* enc_out, int frame_idx, void* out);
+  // bias: the reference's optional position_bias, (H, idx + 1) model dtype
+  // device rows replacing the rel-pos table lookup, or nullptr.
+  void temporal_step(const void* in, const void* enc_out, int frame_idx, void* out, const void* bias = nullptr);
   void depth_step(const void* in, int depth_idx, int level, int codebook, int codec_offset,
-                  float* logits);
+                  float* logits, const void* bias = nullptr);
+  // Drops the temporal (kind 0) or depth (kind 1) cache contents: the next step
+  // of that kind must be at index 0 (empty_{temporal,depth}_cache, model.cpp:275-300).
+  void reset_cache(int kind);
+
   void generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* out_host);
+  // Full-sequence depth pass over k positions (model.cpp:243-268): emb (2, k, D)
+  // model dtype, bias (H, k, k) model dtype or nullptr, logits (2, k, vocab) fp32.
+  void depth_forward_full(const void* emb, int k, const void* bias, bool causal, float* logits);
   // CFG + temperature/top-k draw over one level slice (rows 0/1, C entries)
   // held in a device fp32 buffer; returns the LLM id.
   int sample(const float* slice_dev, const GenOpts& o, int frame, int level);
@@ -181,8 +194,9 @@ class State {
   StepArgs temporal_args(const void* in, int f, void* out) const;
   StepArgs depth_args(const void* in, int l, const void* head_w, int head_rows, float* logits,
                       float* rec_slice) const;
-  void launch_temporal_p(const void* in, int f, void* out);
-  void launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits, float* rec_slice);
+  void launch_temporal_p(const void* in, int f, void* out, const void* bias = nullptr);
+  void launch_depth_p(const void* in, int l, const void* head_w, int head_rows, float* logits, float* rec_slice,
+                      const void* bias = nullptr);
   void launch_frame_p(const GenOpts& o, int f);
   void enqueue_decode_p(const GenOpts& o);
   void enqueue_decode_spec(const GenOpts& o);
@@ -211,7 +225,7 @@ class State {
   int* d_drafts_ = nullptr;
   int prev_frames_ = 0;  // frames of the tokens left by the last generate (0: none)
   bool spec_drafts_ = false;  // this call speculates with d_drafts_
-  void *sx_ = nullptr, *sxn_ = nullptr, *sq_ = nullptr, *satt_ = nullptr, *sffh_ = nullptr;
+  void *sx_ = nullptr, *sxn_ = nullptr, *sq_ = nullptr, *satt_ = nullptr, *sffh_ = nullptr, *sqkv_ = nullptr;
   float* slog_ = nullptr;
   int *sdrawn_ = nullptr, *sdecided_ = nullptr;  // sdecided_: (F) the accepted count n of each frame
   float spec_acc_ = -1.f;  // share of the last call's levels taken from the verification pass
@@ -225,8 +239,9 @@ class State {
   char* dv(int i) const;
   char* ck(int i) const;
   char* cv(int i) const;
-  void run_temporal(const void* in, int f, void* out);
-  void run_depth(const void* in, int l, int level, int codebook, int codec_offset, float* logits);
+  void run_temporal(const void* in, int f, void* out, const void* bias = nullptr);
+  void run_depth(const void* in, int l, int level, int codebook, int codec_offset, float* logits,
+                 const void* bias = nullptr);
   void enqueue_decode(const GenOpts& o);
   void copy(void* dst, const void* src, size_t bytes);
 

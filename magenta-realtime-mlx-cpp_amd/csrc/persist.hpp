@@ -62,6 +62,7 @@ struct StepArgs {
   int pos, Lmax;  // ring slot written this step; ring size
   const void* bias_tab;
   const int* buckets;
+  const void* bias_row;  // explicit self-attention bias (H, pos + 1) model dtype, or nullptr (table)
   const void* in;   // (2, D) model-dtype rows (plain)
   void* out;        // (2, D) rows: temporal output
   int S;            // encoder length

@@ -664,7 +664,10 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
       for (int d = 0; d < 64; ++d) acc = fmaf(qs[b * 64 + d], ks[b * 64 + d], acc);
       sc = acc;
     }
-    if (lane < len) sc += S::ld(ld_g(static_cast<const T*>(a.bias_tab) + ld_g(a.buckets + pos - lane) * a.H + h));
+    if (lane < len)
+      sc += a.bias_row != nullptr
+                ? S::ld(ld_g(static_cast<const T*>(a.bias_row) + h * len + lane))
+                : S::ld(ld_g(static_cast<const T*>(a.bias_tab) + ld_g(a.buckets + pos - lane) * a.H + h));
     const float m = dpp_max(sc);
     const float p = lane < len ? expf(sc - m) : 0.f;
     const float l = dpp_sum(p);

@@ -203,6 +203,11 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_create": (i32, [ctypes.c_char_p, ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),
         "mrt_probe_read_bandwidth": (i32, [i32, sz, i32, ctypes.POINTER(ctypes.c_float)]),
         "mrt_df_sample_level_noalloc": (i32, [vp, vp, ctypes.POINTER(_GenOpts), i32, i32, vp, vp]),
+        "mrt_df_depth_forward_full": (i32, [vp, vp, i32, vp, i32, vp]),
+        "mrt_df_temporal_step_with_bias": (i32, [vp, vp, vp, i32, vp, vp]),
+        "mrt_df_depth_step_with_bias": (i32, [vp, vp, i32, vp, i32, i32, i32, vp]),
+        "mrt_df_precompute_biases": (i32, [vp, i32, i32, vp]),
+        "mrt_df_state_reset_cache": (i32, [vp, i32]),
         "mrt_df_create_from_tensors": (i32, [i32, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(vp),
                                              ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_int32),
                                              ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),
@@ -333,6 +338,16 @@ class Depthformer:
                 ctypes.byref(h)))
         self._h = h
 
+    def precompute_biases(self, kind: str, n: int):
+        """precompute_{temporal,depth}_biases(n): a list of n device tensors, the
+        f-th of shape (H, f + 1) in the model dtype (views of one buffer)."""
+        torch = _torch()
+        H = self.config.num_heads
+        buf = torch.empty(H * n * (n + 1) // 2, dtype=self.torch_dtype, device=f"cuda:{self.device}")
+        torch.cuda.synchronize(self.device)
+        _check(self.lib, self.lib.mrt_df_precompute_biases(self._h, {"temporal": 0, "depth": 1}[kind], n, _dptr(buf)))
+        return [buf[H * f * (f + 1) // 2: H * (f + 1) * (f + 2) // 2].view(H, f + 1) for f in range(n)]
+
     @property
     def torch_dtype(self):
         torch = _torch()
@@ -371,26 +386,32 @@ class State:
             raise ValueError(f"tokens must be {(self.rows, self.enc_len)}, got {t.shape}")
         _check(self.lib, self.lib.mrt_df_encode(self._h, _i32_ptr(t)))
 
-    def temporal_step(self, frame_emb, frame_idx: int, enc_out=None, out=None, sync: bool = True):
+    def temporal_step(self, frame_emb, frame_idx: int, enc_out=None, out=None, sync: bool = True,
+                      position_bias=None):
         """One temporal step on the state's stream.  With sync=False the call only
         enqueues: the inputs must already be complete and the caller orders later
-        reads of `out` after the state's stream."""
+        reads of `out` after the state's stream.  position_bias: optional (H,
+        frame_idx + 1) device tensor in the model dtype (the reference's explicit bias)."""
         torch = _torch()
         if out is None:
             out = torch.empty_like(frame_emb)
         if sync:
             self._sync_torch()
-        _check(self.lib, self.lib.mrt_df_temporal_step(
-            self._h, _dptr(frame_emb), _dptr(enc_out) if enc_out is not None else None, frame_idx,
-            _dptr(out)))
+        enc = _dptr(enc_out) if enc_out is not None else None
+        if position_bias is None:
+            _check(self.lib, self.lib.mrt_df_temporal_step(self._h, _dptr(frame_emb), enc, frame_idx, _dptr(out)))
+        else:
+            _check(self.lib, self.lib.mrt_df_temporal_step_with_bias(self._h, _dptr(frame_emb), enc, frame_idx,
+                                                                     _dptr(position_bias), _dptr(out)))
         if sync:
             self.sync()
         return out
 
     def depth_step(self, tok_emb, depth_idx: int, level: Optional[int] = None,
-                   codebook_size: int = 1024, codec_offset: int = 2, out=None, sync: bool = True):
+                   codebook_size: int = 1024, codec_offset: int = 2, out=None, sync: bool = True,
+                   position_bias=None):
         """One depth step; logits of the level slice (or the full vocabulary when
-        level is None).  sync=False as for temporal_step."""
+        level is None).  sync=False and position_bias as for temporal_step."""
         torch = _torch()
         cfg = self.model.config
         n = codebook_size if level is not None else cfg.vocab_size
@@ -398,9 +419,14 @@ class State:
             out = torch.empty((self.rows, n), dtype=torch.float32, device=tok_emb.device)
         if sync:
             self._sync_torch()
-        _check(self.lib, self.lib.mrt_df_depth_step(
-            self._h, _dptr(tok_emb), depth_idx, -1 if level is None else level, codebook_size,
-            codec_offset, _dptr(out)))
+        lv = -1 if level is None else level
+        if position_bias is None:
+            _check(self.lib, self.lib.mrt_df_depth_step(self._h, _dptr(tok_emb), depth_idx, lv, codebook_size,
+                                                        codec_offset, _dptr(out)))
+        else:
+            _check(self.lib, self.lib.mrt_df_depth_step_with_bias(self._h, _dptr(tok_emb), depth_idx,
+                                                                  _dptr(position_bias), lv, codebook_size,
+                                                                  codec_offset, _dptr(out)))
         if sync:
             self.sync()
         return out
@@ -468,6 +494,24 @@ class State:
 
     def set_cache_length(self, kind: int, length: int) -> None:
         _check(self.lib, self.lib.mrt_df_state_set_cache_length(self._h, kind, length))
+
+    def reset_cache(self, kind: str) -> None:
+        """Empty the "temporal" or "depth" KV cache (empty_*_cache)."""
+        _check(self.lib, self.lib.mrt_df_state_reset_cache(self._h, {"temporal": 0, "depth": 1}[kind]))
+
+    def depth_forward_full(self, embs, position_bias=None, causal: bool = True):
+        """Depthformer::depth_forward_full: embs (2, k, d_model) device tensor in
+        the model dtype -> (2, k, vocab) fp32 logits (a new device tensor).
+        position_bias: None (the k x k rel-pos block) or (H, k, k) device tensor."""
+        torch = _torch()
+        k = int(embs.shape[1])
+        out = torch.empty((2, k, self.model.config.vocab_size), dtype=torch.float32,
+                          device=f"cuda:{self.model.device}")
+        self._sync_torch()
+        _check(self.lib, self.lib.mrt_df_depth_forward_full(
+            self._h, _dptr(embs.contiguous()), k, _dptr(position_bias.contiguous()) if position_bias is not None else None,
+            1 if causal else 0, _dptr(out)))
+        return out
 
     def decode_time(self):
         """(GPU ms, persistent launches) of the decode section of the last

@@ -405,11 +405,13 @@ class OracleDepthformer:
 
     # -- steps -- model.cpp:322-659 -------------------------------------------
     def temporal_step(self, frame_emb: np.ndarray, enc_out: np.ndarray,
-                      cache: List[LayerCache], frame_idx: int) -> np.ndarray:
-        """Eager temporal_step (model.cpp:493-513): 20 layers, no final norm."""
+                      cache: List[LayerCache], frame_idx: int,
+                      position_bias: Optional[np.ndarray] = None) -> np.ndarray:
+        """Eager temporal_step (model.cpp:493-513): 20 layers, no final norm.
+        position_bias (1, H, 1, frame_idx + 1) replaces the rel-pos bias (model.cpp:330-332)."""
         if len(cache) != self.cfg.num_temporal_layers:
             raise RuntimeError("temporal_step: cache size mismatch")  # model.cpp:326-328
-        bias = self.temporal_bias(frame_idx)
+        bias = self.temporal_bias(frame_idx) if position_bias is None else position_bias
         first = frame_idx == 0
         x = frame_emb
         for i, lc in enumerate(cache):
@@ -424,11 +426,12 @@ class OracleDepthformer:
         return x
 
     def depth_step(self, tok_emb: np.ndarray, cache: List[LayerCache],
-                   depth_idx: int) -> np.ndarray:
-        """Eager depth_step (model.cpp:638-658): 4 layers + decoder_norm + lm_head."""
+                   depth_idx: int, position_bias: Optional[np.ndarray] = None) -> np.ndarray:
+        """Eager depth_step (model.cpp:638-658): 4 layers + decoder_norm + lm_head.
+        position_bias (1, H, 1, depth_idx + 1) replaces the rel-pos bias (model.cpp:523-525)."""
         if len(cache) != self.cfg.num_depth_layers:
             raise RuntimeError("depth_step: cache size mismatch")  # model.cpp:519-521
-        bias = self.depth_bias(depth_idx)
+        bias = self.depth_bias(depth_idx) if position_bias is None else position_bias
         first = depth_idx == 0
         x = tok_emb
         for i, lc in enumerate(cache):
@@ -439,10 +442,12 @@ class OracleDepthformer:
         logits = self.linear(x, "lm_head")
         return logits[:, 0, :]
 
-    def depth_forward_full(self, embs: np.ndarray, causal: bool = True) -> np.ndarray:
-        """Full-sequence depth pass (model.cpp:243-268) -> (B, K, V)."""
+    def depth_forward_full(self, embs: np.ndarray, causal: bool = True,
+                           position_bias: Optional[np.ndarray] = None) -> np.ndarray:
+        """Full-sequence depth pass (model.cpp:243-268) -> (B, K, V); position_bias
+        (1, H, K, K) replaces the rel-pos block of query offset 0 (model.cpp:248-250)."""
         K = embs.shape[1]
-        bias = self.depth_bias(0, key_length=K, query_length=K)
+        bias = self.depth_bias(0, key_length=K, query_length=K) if position_bias is None else position_bias
         mask = causal_mask(K) if causal else None
         if mask is not None:
             mask = self.P.r(mask)
