@@ -129,7 +129,9 @@ def step_length_table(state, model, cfg, stream, esz, reps=10):
     """depth_step at every cache length 0..15 and temporal_step at lengths 0, 10,
     .., 40, 49: the cache is declared to hold `pos` entries before each launch,
     so one launch is timed at one length (HIP events over `reps` launches).
-    Back-to-back depth steps find their 105 MB of weights in the 256 MB MALL."""
+    The depth step's 105 MB of weights re-read back to back exceed what the
+    last-level cache keeps (memory_probe: 64 MiB re-reads run from it, 105 MiB
+    ones at the HBM rate), so they stream from HBM."""
     import torch
     g = torch.Generator(device="cpu").manual_seed(7)
     x = torch.randn(2, cfg.d_model, generator=g).to(device="cuda", dtype=model.torch_dtype)
@@ -504,6 +506,27 @@ def bench_encoder(model, cfg, batches=(1, 8, 32), reps=3):
     return res
 
 
+def memory_probe():
+    """Read bandwidth of the device's last-level cache (MALL) and of HBM, by
+    mrt_probe_read_bandwidth: repeated reads of a 32 MiB buffer (cache
+    resident), of 64 and 105 MiB (the depth stack's 105 MB of bf16 weights)
+    and of 4 GiB (streams from HBM).  GB/s = 1e9 B/s."""
+    import mrt_df
+    MB = 1 << 20
+    res = {}
+    for mb, passes in ((32, 100), (64, 50), (105, 40), (4096, 2)):
+        res[f"read_{mb}MiB_GBs"] = round(mrt_df.read_bandwidth(mb * MB, passes), 1)
+    res["mall_GBs"] = res["read_32MiB_GBs"]
+    res["hbm_GBs"] = res["read_4096MiB_GBs"]
+    # the depth stack counts as cache-resident only if re-reading a buffer of
+    # its size runs at least twice the HBM rate
+    res["depth_stack_mall_resident"] = res["read_105MiB_GBs"] >= 2.0 * res["hbm_GBs"]
+    print(f"[bench] memory probe: 32 MiB {res['read_32MiB_GBs']:.0f} GB/s, 64 MiB {res['read_64MiB_GBs']:.0f}, "
+          f"105 MiB {res['read_105MiB_GBs']:.0f}, 4 GiB {res['read_4096MiB_GBs']:.0f} GB/s", file=sys.stderr,
+          flush=True)
+    return res
+
+
 def load_traffic(name):
     """HBM bytes per launch of a kernel measured with rocprofv3 FETCH_SIZE /
     WRITE_SIZE, scaled by a copy of known size (profiles/<name>.json), or None."""
@@ -514,46 +537,87 @@ def load_traffic(name):
         return None
 
 
-def cpu_baseline(weights, cfg, enc_tokens, budget_s=20.0):
-    """Time the numpy restatement (fp32) on a bounded sample of the same chunk."""
+def cpu_model() -> str:
+    """The host CPU's model name (lscpu, else /proc/cpuinfo)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(weights, cfg, enc_tokens):
+    """The CPU restatement of the reference algorithm (MLX is unavailable here),
+    fp32, timed on this host at 1 thread and at every core available to it:
+    the encoder in numpy (BLAS threads limited with threadpoolctl), the decode
+    steps in C with OpenMP (oracle/df_cpu.c, checked against the numpy oracle).
+    A bounded sample scaled to one chunk: one of the 12 encoder layers and one
+    of the 20 cross K/V projections over the 2 x 1006 rows, one temporal step
+    (ring position 25) and one frame's 16 depth steps with level-sliced heads;
+    chunk = 12 layers + 20 projections + 50 temporal steps + 50 x 16 depth steps."""
     import dataclasses
+    from threadpoolctl import threadpool_limits
     from oracle import depthformer_oracle as O
-    om = O.OracleDepthformer(weights, O.DepthformerConfig(**dataclasses.asdict(cfg)), mode="fp32")
-    t0 = time.perf_counter()
-    enc = om.encode(enc_tokens)
-    t_enc = time.perf_counter() - t0
-    cache = om.empty_temporal_cache()
-    x = om.embed(np.zeros((2, 1), dtype=np.int64))
-    t_temporal, t_depth, n_t, n_d = 0.0, 0.0, 0, 0
-    t_start = time.perf_counter()
-    f = 0
-    while (time.perf_counter() - t_start) < budget_s - t_enc and f < 50:
-        t1 = time.perf_counter()
-        y = om.temporal_step(x, enc, cache, f)
-        t_temporal += time.perf_counter() - t1
-        n_t += 1
-        dcache = om.empty_depth_cache()
-        d_in = y
-        for l in range(cfg.rvq_depth):
-            t1 = time.perf_counter()
-            om.depth_step(d_in, dcache, l)
-            t_depth += time.perf_counter() - t1
-            n_d += 1
-            d_in = om.embed(np.full((2, 1), 2 + 1024 * l, dtype=np.int64))
-        f += 1
-    chunk_s = t_enc + 50 * (t_temporal / n_t) + 800 * (t_depth / n_d)
+    from oracle import df_cpu
+    ocfg = O.DepthformerConfig(**dataclasses.asdict(cfg))
+    om = O.OracleDepthformer(weights, ocfg, mode="fp32")
+    cm = df_cpu.CpuDepthformer(weights, ocfg, max_frames=50)
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
-    threads = int(os.environ.get("OMP_NUM_THREADS", cores))
+    n_all = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    x0 = om.embed(enc_tokens) + O.sinusoidal_position_embedding(cfg.max_encoder_length, cfg.d_model)[None]
+    x0 = x0.astype(np.float32)
+    rng = np.random.default_rng(7)
+    out = {}
+    for n in sorted({1, n_all}):
+        df_cpu.CpuDepthformer.set_threads(n)
+        with threadpool_limits(limits=n):
+            t0 = time.perf_counter()
+            xl = om.encoder_layer(x0, 0)
+            t_layer = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            kv = om.project_kv(xl, "temporal_layers.0.cross_attn")
+            t_cross = time.perf_counter() - t0
+        cm.set_cross([kv] * cfg.num_temporal_layers)
+        x = rng.standard_normal((2, cfg.d_model)).astype(np.float32)
+        t0 = time.perf_counter()
+        y = cm.temporal_step(x, 25)
+        t_temporal = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for l in range(cfg.rvq_depth):
+            cm.depth_step(y if l == 0 else x, l, level=l)
+        t_frame_depth = time.perf_counter() - t0
+        chunk_s = (cfg.num_encoder_layers * t_layer + cfg.num_temporal_layers * t_cross + 50 * t_temporal
+                   + 50 * t_frame_depth)
+        out[n] = {"value": 800.0 / chunk_s, "chunk_ms": chunk_s * 1e3, "encoder_layer_ms": t_layer * 1e3,
+                  "cross_kv_ms": t_cross * 1e3, "temporal_step_ms": t_temporal * 1e3,
+                  "depth_steps_16_ms": t_frame_depth * 1e3}
+        print(f"[bench] CPU restatement at {n} thread(s): {chunk_s * 1e3:.0f} ms per chunk "
+              f"(encoder layer {t_layer * 1e3:.0f} ms, temporal step {t_temporal * 1e3:.1f} ms, "
+              f"16 depth steps {t_frame_depth * 1e3:.1f} ms)", file=sys.stderr, flush=True)
     return {
-        "value": 800.0 / chunk_s,
+        "value": out[n_all]["value"],
         "unit": "RVQ tokens/s",
-        "cores": min(cores, threads),
+        "cores": n_all,
         "kind": "port",
-        "sample": (f"numpy fp32 restatement: 1 encoder pass + {n_t} temporal steps + {n_d} depth "
-                   f"steps, extrapolated to one 50x16 chunk ({chunk_s * 1e3:.0f} ms/chunk)"),
+        "cpu_model": cpu_model(),
+        "threads_1": out[1],
+        f"threads_{n_all}": out[n_all],
+        "sample": ("CPU restatement of the reference algorithm, fp32 (MLX unavailable): encoder in numpy, decode "
+                   "steps in C/OpenMP; 1 encoder layer + 1 cross K/V projection + 1 temporal step + 16 depth "
+                   "steps timed, scaled to 12 layers + 20 projections + 50 temporal + 800 depth steps"),
     }
 
 
@@ -565,7 +629,6 @@ def main():
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-batched", action="store_true", help="skip the 32-stream, encoder-prefill, speculative, codec and style-model figures")
     ap.add_argument("--session", default="device", choices=["device", "host"],
@@ -646,6 +709,22 @@ def main():
                 "timing": "HIP events around the decode section of each timed chunk (frame launches + one "
                           "Gumbel-table kernel per chunk) / frames"}
         roof["frac"] = roof["achieved"] / HBM_PEAK_GBS
+        # per-part peaks: the temporal stack and cross K/V stream from HBM; the
+        # depth steps' bytes count at the measured MALL rate only where the
+        # depth stack is cache-resident (memory_probe)
+        mem = memory_probe()
+        t_b = float(np.mean([step_bytes(cfg, "temporal", f, esz=esz) for f in range(frames)]))
+        d_b = fb - t_b
+        d_peak = mem["mall_GBs"] if mem["depth_stack_mall_resident"] else HBM_PEAK_GBS
+        blended = fb / (t_b / HBM_PEAK_GBS + d_b / d_peak)
+        roof["parts"] = {"temporal_step": {"bytes": t_b, "peak": HBM_PEAK_GBS, "source": "HBM"},
+                         "depth_steps_and_draws": {"bytes": d_b, "peak": d_peak,
+                                                   "source": "MALL" if mem["depth_stack_mall_resident"] else
+                                                   "HBM (a 105 MiB re-read runs at the HBM rate: the depth "
+                                                   "stack is not cache-resident)"}}
+        roof["peak_blended"] = blended
+        roof["frac_blended"] = roof["achieved"] / blended
+        roof["memory_probe"] = mem
         print(f"[bench] frame kernel {f_us:.1f} us/launch ({roof['achieved']:.0f} GB/s); decode "
               f"{np.mean(dec):.2f} ms/chunk", file=sys.stderr, flush=True)
     else:
@@ -675,7 +754,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         enc = system.build_encoder_inputs(sess.context, scfg, style)
-        cpu = cpu_baseline(weights, cfg, enc, budget_s=args.cpu_budget)
+        cpu = cpu_baseline(weights, cfg, enc)
 
     out = {
         "metric": "RVQ tokens/s per 2 s chunk (batch 1, 2 CFG rows)",
