@@ -286,3 +286,46 @@ def test_batch_encoder_full_size(full, B):
     st.close()
     om = O.OracleDepthformer(full["w"], O.DepthformerConfig(**dataclasses.asdict(full["cfg"])), mode="bf16")
     assert rel(enc[0:2].float().cpu().numpy(), om.encode(toks[0])) <= BF16_TOL
+
+
+def test_batch_32_streams_full_chunk_teacher_forced(full):
+    """32 streams at the benchmark dims through the whole 50-frame chunk,
+    teacher-forced: streams 0 and 31 (own contexts, styles and teacher tokens)
+    against the bf16 oracle per (frame, level) slice (<= 2e-2), their temporal
+    outputs (<= 2e-2), and the teacher-forced CFG argmax with every flip a
+    near-tie of bf16 noise; every fed-back token is the teacher's."""
+    import torch
+    import system
+    from draw_check import assert_argmax_flips_are_near_ties
+    mrt_df, O = full["mrt_df"], full["O"]
+    B, F, L, C, D = 32, 50, 16, 1024, full["cfg"].d_model
+    scfg = system.SystemConfig()
+    rng = np.random.default_rng(2024)
+    toks = []
+    for _ in range(B):
+        ctx = rng.integers(0, 1024, size=(scfg.context_frames, 16)).astype(np.int32)
+        style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+        toks.append(system.build_encoder_inputs(ctx, scfg, style))
+    teacher = _teacher(rng, B, F, C)
+    b = mrt_df.Batch(full["model"], B, max_frames=F)
+    rec = dict(slices=torch.zeros((F, L, 2 * B, C), dtype=torch.float32, device="cuda"),
+               temporal=torch.zeros((F, 2 * B, D), dtype=torch.bfloat16, device="cuda"))
+    opts = mrt_df.GenOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40, guidance_weight=5.0, seed=0,
+                             codebook_size=C, codec_offset=2)
+    out = b.generate_tokens(np.concatenate(toks, axis=0), opts, seeds=list(range(B)), teacher=teacher, record=rec)
+    np.testing.assert_array_equal(out, teacher)
+    b.close()
+    om = O.OracleDepthformer(full["w"], O.DepthformerConfig(**dataclasses.asdict(full["cfg"])), mode="bf16")
+    o = O.GenerateOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40, guidance_weight=5.0, seed=0,
+                          codebook_size=C, codec_offset=2)
+    for s in (0, B - 1):
+        sl = rec["slices"][:, :, 2 * s:2 * s + 2].cpu().numpy()
+        tp = rec["temporal"][:, 2 * s:2 * s + 2].float().cpu().numpy()
+        orec = {}
+        O.generate_tokens(om, toks[s], o, teacher=teacher[s], record=orec)
+        errs = np.array([[rel(sl[f, l], orec["slices"][f, l]) for l in range(L)] for f in range(F)])
+        assert errs.max() <= BF16_TOL, (s, errs.max(), np.unravel_index(errs.argmax(), errs.shape))
+        terrs = [rel(tp[f], orec["temporal_out"][f]) for f in range(F)]
+        assert max(terrs) <= BF16_TOL, (s, max(terrs))
+        agree = assert_argmax_flips_are_near_ties(sl, orec["slices"])
+        print(f"stream {s}: max slice rel-err {errs.max():.3e}, argmax agreement {agree:.3f}")
