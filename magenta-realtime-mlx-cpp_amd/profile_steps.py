@@ -19,6 +19,12 @@ seeded synthetic codec weights) after 2 untimed ones.
 --style instead runs N MusicCoCa text embeddings (one 12-id prompt in 128
 slots, fp32, seeded synthetic weights) after 3 untimed ones.
 
+    python magenta-realtime-mlx-cpp_amd/profile_steps.py --encoder B [--reps N]
+
+--encoder B instead runs N encoder prefills of B streams (2B x 1006 rows: the
+12 layers and the cross K/V projection of the 20 temporal layers) after one
+untimed one, for matrix-core counter runs.
+
 The copy (torch's device copy of M MiB, M above the 256 MB last-level cache)
 reads and writes exactly M MiB; its counter readings give the scale factor
 between the counters and bytes.
@@ -46,6 +52,7 @@ def main() -> None:
     ap.add_argument("--frames", type=int, default=50, help="frames of the batched decode")
     ap.add_argument("--codec", type=int, default=0, help="frames of codec decodes (0: Depthformer steps)")
     ap.add_argument("--style", action="store_true", help="MusicCoCa text embeddings instead")
+    ap.add_argument("--encoder", type=int, default=0, help="streams of encoder-only prefills (0: none)")
     a = ap.parse_args()
 
     import torch
@@ -87,6 +94,24 @@ def main() -> None:
     cfg = mrt_df.Config.bench()
     model = mrt_df.Depthformer(synth_bundle.make_weights(cfg, seed=a.seed, threads=16), cfg, dtype="bf16")
     scfg = system.SystemConfig()
+    if a.encoder:
+        rng = np.random.default_rng(11)
+        toks = []
+        for _ in range(a.encoder):
+            ctx = rng.integers(0, 1024, size=(scfg.context_frames, 16)).astype(np.int32)
+            style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
+            toks.append(system.build_encoder_inputs(ctx, scfg, style))
+        b = mrt_df.Batch(model, a.encoder, max_frames=1)
+        enc = np.concatenate(toks, axis=0)
+        b.encode(enc)
+        torch.cuda.synchronize()
+        for _ in range(a.reps):
+            b.encode(enc)
+        torch.cuda.synchronize()
+        print(f"[profile] {a.reps} encoder prefills of {a.encoder} streams", flush=True)
+        b.close()
+        model.close()
+        return
     if a.batched:
         rng = np.random.default_rng(7)
         toks = []
