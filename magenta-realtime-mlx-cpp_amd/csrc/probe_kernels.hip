@@ -1,10 +1,12 @@
 // Read-bandwidth probe of the device's memory hierarchy, for the roofline
 // figures of the benchmark: a buffer of `bytes` is read `passes` times by a
-// grid of 8 workgroups per CU with 16-byte loads, four independent loads in
-// flight per thread.  A buffer well below the 256 MB last-level cache (MALL)
-// of MI355X is served from it after the first pass; a buffer of several GB
-// streams from HBM on every pass.  The loaded words are folded into one value
-// that is stored only if it equals a constant, so no load is dropped.
+// grid of 8 workgroups per CU.  Each workgroup reads contiguous 32 KiB tiles
+// (8 16-byte loads per thread, all issued before any is consumed), so every
+// buffer size keeps the same number of loads in flight.  A buffer that the
+// 256 MB last-level cache (MALL) of MI355X retains is served from it after
+// the first pass; a buffer of several GB streams from HBM on every pass.  The
+// loaded words are folded into one value that is stored only if it equals a
+// constant, so no load is dropped.
 #include "common.hpp"
 #include "device_utils.hpp"
 #include "kernels.hpp"
@@ -12,20 +14,26 @@
 namespace mrt {
 namespace {
 
+constexpr int kSweepUnroll = 8;
+
 __global__ __launch_bounds__(256) void k_read_sweep(const uint4* __restrict__ p, size_t n16, int passes,
                                                     unsigned* __restrict__ sink) {
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t tile = (size_t)blockDim.x * kSweepUnroll;
+  const size_t step = (size_t)gridDim.x * tile;
   uint32_t acc = 0;
   for (int r = 0; r < passes; ++r) {
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (; i + 3 * stride < n16; i += 4 * stride) {
-      const uint4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
-      // every word of every load is used, so no load is narrowed
-      acc ^= (a.x ^ a.y ^ a.z ^ a.w) + (b.x ^ b.y ^ b.z ^ b.w) + (c.x ^ c.y ^ c.z ^ c.w) + (d.x ^ d.y ^ d.z ^ d.w);
-    }
-    for (; i < n16; i += stride) {
-      const uint4 a = p[i];
-      acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    for (size_t base = (size_t)blockIdx.x * tile + threadIdx.x; base < n16; base += step) {
+      uint4 v[kSweepUnroll];
+      // clamped indices keep every load in bounds and unconditional; the
+      // values of clamped lanes are discarded below
+#pragma unroll
+      for (int u = 0; u < kSweepUnroll; ++u) v[u] = p[min(base + (size_t)u * blockDim.x, n16 - 1)];
+#pragma unroll
+      for (int u = 0; u < kSweepUnroll; ++u) {
+        // every word of every load is used, so no load is narrowed
+        const uint32_t f = (v[u].x ^ v[u].y) + (v[u].z ^ v[u].w);
+        acc ^= base + (size_t)u * blockDim.x < n16 ? f : 0u;
+      }
     }
   }
   if (acc == 0x9e3779b9u) sink[0] = acc;

@@ -25,6 +25,12 @@ slots, fp32, seeded synthetic weights) after 3 untimed ones.
 12 layers and the cross K/V projection of the 20 temporal layers) after one
 untimed one, for matrix-core counter runs.
 
+    python magenta-realtime-mlx-cpp_amd/profile_steps.py --read-sweep
+
+--read-sweep instead measures the device's read bandwidth (mrt_probe_read_bandwidth:
+one warm pass, then repeated reads of one buffer) at buffer sizes from 16 MiB to
+4 GiB, to locate where re-reads stop being served by the 256 MB last-level cache.
+
 The copy (torch's device copy of M MiB, M above the 256 MB last-level cache)
 reads and writes exactly M MiB; its counter readings give the scale factor
 between the counters and bytes.
@@ -53,7 +59,16 @@ def main() -> None:
     ap.add_argument("--codec", type=int, default=0, help="frames of codec decodes (0: Depthformer steps)")
     ap.add_argument("--style", action="store_true", help="MusicCoCa text embeddings instead")
     ap.add_argument("--encoder", type=int, default=0, help="streams of encoder-only prefills (0: none)")
+    ap.add_argument("--read-sweep", action="store_true", help="read bandwidth against buffer size instead")
     a = ap.parse_args()
+
+    if a.read_sweep:
+        import mrt_df
+        for mib in (16, 32, 48, 64, 72, 80, 88, 96, 98, 104, 112, 128, 130, 160, 192, 224, 256, 384, 1024, 4096):
+            passes = max(2, min(200, (8 << 10) // mib))  # about 8 GiB read per size
+            gbs = mrt_df.read_bandwidth(mib << 20, passes)
+            print(f"[profile] read {mib:5d} MiB x {passes:3d} passes: {gbs:8.1f} GB/s", flush=True)
+        return
 
     import torch
     import mrt_df
