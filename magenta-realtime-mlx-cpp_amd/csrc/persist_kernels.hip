@@ -146,6 +146,97 @@ __device__ __forceinline__ int dpp_min_i(int v) {
   return __builtin_amdgcn_readlane(v, 63);
 }
 
+// ---- transposed wave sums ----------------------------------------------------------
+//
+// N values per lane are summed over the 64 lanes by a butterfly that halves
+// the value list at each lane bit (5, 4, 3, 2, 1, 0) while it doubles the
+// lanes each partial covers: lanes with the bit clear keep the first half,
+// lanes with it set the second half (the list padded with zeros to an even
+// length), and each adds what its partner across the bit sends.  Once one
+// value is left, the remaining bits add the partner's copy.  N values cost
+// about N + log2(64) exchanges instead of 6 N, and the exchanges of one step
+// are independent.  Bits 5 and 4 exchange with v_permlane32_swap /
+// v_permlane16_swap, bits 3..0 with DPP (row mirror, half-row mirror, quad
+// permutes); every DPP source lane lies in the same 16-lane row.
+
+// Lane bit M's partner value (M <= 8).
+template <int M>
+__device__ __forceinline__ float dpp_partner(float v) {
+  constexpr int ctrl = M == 8 ? 0x140 : M == 4 ? 0x141 : M == 2 ? 0x4E : 0xB1;
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xf, 0xf, false));
+}
+
+// For M = 32 or 16: a[l] + a[l ^ M] on lanes whose bit M is clear, b[l ^ M] +
+// b[l] on the others (with a == b: the pair sum on every lane).
+template <int M>
+__device__ __forceinline__ float swap_add(float a, float b) {
+  if constexpr (M == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    static_assert(M == 16, "swap_add: lane bit 5 or 4");
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
+// One butterfly step over lane bit M on a list of L values.
+template <int M, int L, int NMAX>
+__device__ __forceinline__ void tsum_step(float (&v)[NMAX]) {
+  if constexpr (L == 1) {
+    if constexpr (M >= 16)
+      v[0] = swap_add<M>(v[0], v[0]);
+    else
+      v[0] += dpp_partner<M>(v[0]);
+  } else {
+    constexpr int H = (L + 1) / 2;
+    const bool hi = (threadIdx.x & M) != 0;
+#pragma unroll
+    for (int j = 0; j < H; ++j) {
+      const float a = v[j], b = j + H < L ? v[j + H] : 0.f;
+      if constexpr (M >= 16) {
+        v[j] = swap_add<M>(a, b);
+      } else {
+        const float keep = hi ? b : a, send = hi ? a : b;
+        v[j] = keep + dpp_partner<M>(send);
+      }
+    }
+  }
+}
+
+constexpr int half_up(int n) { return (n + 1) / 2; }
+
+// Sums each of v[0..N) over the wave; on return v[0] of every lane is the
+// total of one value slot (or of padding, zero); tsum_lane locates slot s.
+template <int N, int NMAX>
+__device__ __forceinline__ void tsum(float (&v)[NMAX]) {
+  constexpr int L1 = half_up(N), L2 = half_up(L1), L3 = half_up(L2), L4 = half_up(L3), L5 = half_up(L4);
+  tsum_step<32, N>(v);
+  tsum_step<16, L1>(v);
+  tsum_step<8, L2>(v);
+  tsum_step<4, L3>(v);
+  tsum_step<2, L4>(v);
+  tsum_step<1, L5>(v);
+}
+
+// A lane that holds the total of value slot s (s < N) after tsum<N>: the
+// halves are taken greedily, so the lane never lands on padding.
+template <int N>
+__host__ __device__ constexpr int tsum_lane(int s) {
+  int l = 0, n = N;
+  for (int m = 32; m >= 1; m >>= 1) {
+    if (n > 1) {
+      const int h = (n + 1) / 2;
+      if (s >= h) {
+        s -= h;
+        l |= m;
+      }
+      n = h;
+    }
+  }
+  return l;
+}
+
 // 1/sqrt(x) for x > 0: the hardware estimate refined by one Newton-Raphson
 // step, y (1.5 - x y^2 / 2), to about 1 ulp.
 __device__ __forceinline__ float rsqrt_nr(float x) {
@@ -354,13 +445,11 @@ __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, 
       s0 = fmaf(v0[i], v0[i], s0);
       s1 = fmaf(v1[i], v1[i], s1);
     }
-    s0 = dpp_sum(s0);
-    s1 = dpp_sum(s1);
+    // both rows' wave sums at once: row 0's total in lanes 0..31, row 1's in 32..63
+    float t[2] = {s0, s1};
+    tsum<2>(t);
     const int wid = tid >> 6;
-    if ((tid & 63) == 0) {
-      red[wid] = s0;
-      red[4 + wid] = s1;
-    }
+    if ((tid & 31) == 0) red[4 * ((tid >> 5) & 1) + wid] = t[0];
     __syncthreads();
     const float4 ra = *reinterpret_cast<const float4*>(red);
     const float4 rb = *reinterpret_cast<const float4*>(red + 4);
@@ -468,22 +557,38 @@ __device__ __forceinline__ void dot_batch(const uint4 (&buf)[kNBuf], int b0, int
       }
     }
   }
-  // Row r's sums go to lane r, so the epilogue runs once for all rows.
+  // Row r's sums go to lane r, so the epilogue runs once for all rows.  The
+  // 2P sums of every row are reduced together (transposed), value k = (r P +
+  // p) 2 + c; rows past nb hold zeros.  A single row reduces its 2P values only.
   float v[P][2];
+  if (nb == 1) {
+    float t[2 * P];
 #pragma unroll
-  for (int p = 0; p < P; ++p) v[p][0] = v[p][1] = 0.f;
+    for (int p = 0; p < P; ++p) {
+      t[2 * p] = acc[0][p][0];
+      t[2 * p + 1] = acc[0][p][1];
+    }
+    tsum<2 * P>(t);
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    if (r < nb) {
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) v[p][c] = __shfl(t[0], tsum_lane<2 * P>(2 * p + c), 64);
+  } else {
+    constexpr int N = 2 * P * R;
+    float t[N];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        const float s0 = dpp_sum(acc[r][p][0]), s1 = dpp_sum(acc[r][p][1]);
-        if (lane == r) {
-          v[p][0] = s0;
-          v[p][1] = s1;
-        }
+        t[(r * P + p) * 2] = acc[r][p][0];
+        t[(r * P + p) * 2 + 1] = acc[r][p][1];
       }
-    }
+    tsum<N>(t);
+    const int row = min(lane, R - 1);
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) v[p][c] = __shfl(t[0], tsum_lane<N>((row * P + p) * 2 + c), 64);
   }
   epi(b0 + lane, lane < nb, v);
 }
