@@ -529,6 +529,24 @@ def memory_probe():
     return res
 
 
+def frame_handoffs(cfg, levels=16):
+    """Dependent phase hand-offs in one frame-kernel launch: per temporal layer
+    QKV -> attention -> O -> cross q -> cross partials -> cross combine -> cross O
+    -> up -> down (9), per depth layer QKV -> attention -> O -> up -> down (5),
+    and per level the head logits and the drawn token (2)."""
+    return 9 * cfg.num_temporal_layers + levels * (5 * cfg.num_depth_layers + 2)
+
+
+def handoff_probe(grid):
+    """The hand-off floor measured by mrt_probe_handoff (an all-gather of 1024
+    tagged words among the persistent grid's workgroups, 2000 rounds) and
+    mrt_probe_pingpong (workgroup 0 <-> the grid's last workgroup)."""
+    import mrt_df
+    return {"allgather_us": round(mrt_df.handoff_latency(grid, 1024, 2000), 3),
+            "pingpong_one_way_us": round(mrt_df.pingpong_latency(grid - 1, 2000), 3),
+            "workgroups": grid, "words": 1024}
+
+
 def load_traffic(name):
     """HBM bytes per launch of a kernel measured with rocprofv3 FETCH_SIZE /
     WRITE_SIZE, scaled by a copy of known size (profiles/<name>.json), or None."""
@@ -734,6 +752,16 @@ def main():
         roof["peak_blended"] = blended
         roof["frac_blended"] = roof["achieved"] / blended
         roof["memory_probe"] = mem
+        # the latency floor of the dependent hand-off chain: phases x the measured
+        # all-gather among the persistent grid (one workgroup per CU)
+        hp = handoff_probe(min(256, torch.cuda.get_device_properties(0).multi_processor_count))
+        n_ho = frame_handoffs(cfg)
+        roof["latency_floor"] = {"handoffs_per_launch": n_ho, **hp,
+                                 "floor_us": round(n_ho * hp["allgather_us"], 1),
+                                 "frac": n_ho * hp["allgather_us"] / f_us}
+        print(f"[bench] hand-off probe: all-gather {hp['allgather_us']:.3f} us, ping-pong {hp['pingpong_one_way_us']:.3f} "
+              f"us; {n_ho} hand-offs per frame -> floor {n_ho * hp['allgather_us']:.0f} us "
+              f"({100 * n_ho * hp['allgather_us'] / f_us:.0f} % of the frame)", file=sys.stderr, flush=True)
         print(f"[bench] frame kernel {f_us:.1f} us/launch ({roof['achieved']:.0f} GB/s); decode "
               f"{np.mean(dec):.2f} ms/chunk", file=sys.stderr, flush=True)
     else:

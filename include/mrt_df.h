@@ -244,6 +244,19 @@ int mrt_df_state_spec_acceptance(mrt_df_state* st, float* acceptance);
  * for the benchmark's roofline peaks. */
 int mrt_probe_read_bandwidth(int device, size_t bytes, int passes, float* gbps);
 
+/* Measurement, no counterpart in the reference: the latency floor of one phase
+ * hand-off of the persistent kernels.  mrt_probe_handoff: microseconds per
+ * round of an all-gather of `words` (workgroups..1024, a multiple of
+ * `workgroups`, at most 256 per workgroup) tagged 64-bit words among
+ * `workgroups` (1..CU count) workgroups -- each stores its share with
+ * agent-scope atomics, then polls all words -- over `rounds` (1..100000)
+ * rounds.  mrt_probe_pingpong: one-way microseconds of a word bounced
+ * `rounds` times between workgroups 0 and `peer` (1..CU count - 1).  Both
+ * allocate and free a 16 KiB buffer; every poll is bounded (a spin limit
+ * returns MRT_ERR_HIP). */
+int mrt_probe_handoff(int device, int workgroups, int words, int rounds, float* us_per_round);
+int mrt_probe_pingpong(int device, int peer, int rounds, float* us_one_way);
+
 /* State buffers exposed for parity checks (device-to-device copies). */
 #define MRT_BUF_ENC_OUT 0     /* (rows, enc_len, d_model)                       */
 #define MRT_BUF_CROSS_K 1     /* layer: (rows, heads, enc_len, d_kv)            */

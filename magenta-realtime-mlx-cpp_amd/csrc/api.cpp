@@ -395,6 +395,20 @@ int mrt_probe_read_bandwidth(int device, size_t bytes, int passes, float* gbps) 
   });
 }
 
+int mrt_probe_handoff(int device, int workgroups, int words, int rounds, float* us_per_round) {
+  return guarded([&] {
+    if (!us_per_round) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *us_per_round = mrt::probe_handoff(device, workgroups, words, rounds);
+  });
+}
+
+int mrt_probe_pingpong(int device, int peer, int rounds, float* us_one_way) {
+  return guarded([&] {
+    if (!us_one_way) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *us_one_way = mrt::probe_pingpong(device, peer, rounds);
+  });
+}
+
 int mrt_df_state_buffer_bytes(mrt_df_state* st, int which, size_t* bytes) {
   return guarded([&] {
     if (!bytes) throw mrt::Error(MRT_ERR_INVALID, "null argument");

@@ -1,5 +1,6 @@
-// Read-bandwidth probe of the device's memory hierarchy, for the roofline
-// figures of the benchmark: a buffer of `bytes` is read `passes` times by a
+// Probes of the device for the roofline figures of the benchmark.
+//
+// Read bandwidth of the memory hierarchy: a buffer of `bytes` is read `passes` times by a
 // grid of 8 workgroups per CU.  Each workgroup reads contiguous 32 KiB tiles
 // (8 16-byte loads per thread, all issued before any is consumed), so every
 // buffer size keeps the same number of loads in flight.  A buffer that the
@@ -37,6 +38,73 @@ __global__ __launch_bounds__(256) void k_read_sweep(const uint4* __restrict__ p,
     }
   }
   if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+// Hand-off latency of the persistent kernels' phases.  k_handoff runs rounds of
+// an all-gather of tagged 64-bit words among the grid's workgroups: in round r
+// each workgroup stores its words / G words {r, index} with agent-scope
+// atomic stores, then polls all `words` words with agent-scope atomic loads
+// until each carries round r or later -- one phase hand-off of the step
+// kernels.  k_pingpong bounces one word between workgroup 0 and workgroup
+// `peer` (one thread each).  Every poll gives up after kSpinLimit rounds and
+// flags an error, so both kernels always end.
+__device__ __forceinline__ uint64_t probe_aload(const uint64_t* p) {
+  return __hip_atomic_load((const MRT_GLOBAL uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void probe_astore(uint64_t* p, uint64_t v) {
+  __hip_atomic_store((MRT_GLOBAL uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(256) void k_handoff(uint64_t* __restrict__ w, int words, int rounds,
+                                                 uint64_t* __restrict__ clk, int* __restrict__ err) {
+  const int G = gridDim.x, b = blockIdx.x, t = threadIdx.x;
+  const int per = words / G;
+  const uint64_t t0 = wall_clock64();
+  for (int r = 1; r <= rounds; ++r) {
+    if (t < per) probe_astore(w + b * per + t, ((uint64_t)r << 32) | (uint32_t)(b * per + t));
+    uint32_t pend = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (t + 256 * i < words) pend |= 1u << i;
+    uint32_t spins = 0;
+    while (pend != 0) {
+      uint64_t v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if ((pend >> i) & 1u) v[i] = probe_aload(w + t + 256 * i);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (((pend >> i) & 1u) && (v[i] >> 32) >= (uint64_t)r) pend &= ~(1u << i);
+      if (pend != 0 && ++spins > kSpinLimit) {
+        __hip_atomic_store((MRT_GLOBAL int*)err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+    __syncthreads();
+    if (__hip_atomic_load((const MRT_GLOBAL int*)err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+  }
+  if (b == 0 && t == 0) clk[0] = wall_clock64() - t0;
+}
+
+__global__ void k_pingpong(uint64_t* __restrict__ w, int rounds, int peer, uint64_t* __restrict__ clk,
+                           int* __restrict__ err) {
+  if (threadIdx.x != 0 || (blockIdx.x != 0 && (int)blockIdx.x != peer)) return;
+  const bool first = blockIdx.x == 0;
+  uint64_t* mine = w + (first ? 0 : 16);  // separate 128-byte lines
+  const uint64_t* theirs = w + (first ? 16 : 0);
+  const uint64_t t0 = wall_clock64();
+  for (int i = 1; i <= rounds; ++i) {
+    if (first) probe_astore(mine, (uint64_t)i);
+    uint32_t spins = 0;
+    while (probe_aload(theirs) < (uint64_t)i) {
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store((MRT_GLOBAL int*)err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+    }
+    if (!first) probe_astore(mine, (uint64_t)i);
+  }
+  if (first) clk[0] = wall_clock64() - t0;
 }
 
 }  // namespace
@@ -83,6 +151,79 @@ float probe_read_bandwidth(int device, size_t bytes, int passes) {
   }
   release();
   return static_cast<float>(static_cast<double>(bytes) * passes / (ms * 1e-3) / 1e9);
+}
+
+namespace {
+
+// Runs one probe launch on a fresh zeroed 16 KiB word buffer and returns the
+// time its workgroup 0 measured on the device's wall clock, in microseconds.
+template <class Launch>
+double probe_ticks_us(int device, Launch launch) {
+  MRT_HIP_CHECK(hipSetDevice(device));
+  int khz = 0;
+  MRT_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, device));
+  MRT_REQUIRE(khz > 0, "probe: the device reports no wall-clock rate");
+  uint64_t* w = nullptr;
+  uint64_t* clk = nullptr;
+  int* err = nullptr;
+  hipStream_t s = nullptr;
+  auto release = [&]() {
+    if (s) (void)hipStreamDestroy(s);
+    if (w) (void)hipFree(w);
+    if (clk) (void)hipFree(clk);
+    if (err) (void)hipFree(err);
+  };
+  uint64_t ticks = 0;
+  int e = 0;
+  try {
+    MRT_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&w), 16384));
+    MRT_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&clk), 64));
+    MRT_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&err), 64));
+    MRT_HIP_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    MRT_HIP_CHECK(hipMemsetAsync(w, 0, 16384, s));
+    MRT_HIP_CHECK(hipMemsetAsync(clk, 0, 64, s));
+    MRT_HIP_CHECK(hipMemsetAsync(err, 0, 64, s));
+    launch(w, clk, err, s);
+    MRT_HIP_CHECK(hipGetLastError());
+    MRT_HIP_CHECK(hipMemcpyAsync(&ticks, clk, sizeof ticks, hipMemcpyDeviceToHost, s));
+    MRT_HIP_CHECK(hipMemcpyAsync(&e, err, sizeof e, hipMemcpyDeviceToHost, s));
+    MRT_HIP_CHECK(hipStreamSynchronize(s));
+  } catch (...) {
+    release();
+    throw;
+  }
+  release();
+  if (e != 0) throw Error(3, "probe: a poll reached its spin limit (the workgroups were not all resident)");
+  return static_cast<double>(ticks) * 1000.0 / khz;  // microseconds
+}
+
+}  // namespace
+
+float probe_handoff(int device, int workgroups, int words, int rounds) {
+  MRT_HIP_CHECK(hipSetDevice(device));
+  int num_cu = 0;
+  MRT_HIP_CHECK(hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, device));
+  MRT_REQUIRE(workgroups >= 1 && workgroups <= num_cu, "probe: workgroups must be in [1, CU count]");
+  MRT_REQUIRE(words >= workgroups && words <= 1024 && words % workgroups == 0,
+              "probe: words must be a multiple of workgroups, at most 1024");
+  MRT_REQUIRE(words / workgroups <= 256, "probe: at most 256 words per workgroup (one per thread)");
+  MRT_REQUIRE(rounds >= 1 && rounds <= 100000, "probe: rounds must be in [1, 100000]");
+  const double us = probe_ticks_us(device, [&](uint64_t* w, uint64_t* clk, int* err, hipStream_t s) {
+    hipLaunchKernelGGL(k_handoff, dim3(workgroups), dim3(256), 0, s, w, words, rounds, clk, err);
+  });
+  return static_cast<float>(us / rounds);
+}
+
+float probe_pingpong(int device, int peer, int rounds) {
+  MRT_HIP_CHECK(hipSetDevice(device));
+  int num_cu = 0;
+  MRT_HIP_CHECK(hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, device));
+  MRT_REQUIRE(peer >= 1 && peer < num_cu, "probe: peer must be in [1, CU count)");
+  MRT_REQUIRE(rounds >= 1 && rounds <= 100000, "probe: rounds must be in [1, 100000]");
+  const double us = probe_ticks_us(device, [&](uint64_t* w, uint64_t* clk, int* err, hipStream_t s) {
+    hipLaunchKernelGGL(k_pingpong, dim3(peer + 1), dim3(64), 0, s, w, rounds, peer, clk, err);
+  });
+  return static_cast<float>(us / (2.0 * rounds));
 }
 
 }  // namespace mrt

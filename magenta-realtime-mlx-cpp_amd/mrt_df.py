@@ -180,6 +180,25 @@ def read_bandwidth(nbytes: int, passes: int, device: int = 0) -> float:
     return float(out.value)
 
 
+def handoff_latency(workgroups: int, words: int, rounds: int, device: int = 0) -> float:
+    """Microseconds per round of an all-gather of ``words`` tagged words among
+    ``workgroups`` workgroups, the hand-off of one persistent-kernel phase
+    (mrt_probe_handoff)."""
+    lib = load_library()
+    out = ctypes.c_float()
+    _check(lib, lib.mrt_probe_handoff(device, workgroups, words, rounds, ctypes.byref(out)))
+    return float(out.value)
+
+
+def pingpong_latency(peer: int, rounds: int, device: int = 0) -> float:
+    """One-way microseconds of a word bounced between workgroups 0 and ``peer``
+    (mrt_probe_pingpong)."""
+    lib = load_library()
+    out = ctypes.c_float()
+    _check(lib, lib.mrt_probe_pingpong(device, peer, rounds, ctypes.byref(out)))
+    return float(out.value)
+
+
 def header_functions(path: pathlib.Path = HEADER) -> list:
     """Names of the functions include/mrt_df.h declares."""
     text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
@@ -202,6 +221,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_config_large": (None, [ctypes.POINTER(_Config)]),
         "mrt_df_create": (i32, [ctypes.c_char_p, ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),
         "mrt_probe_read_bandwidth": (i32, [i32, sz, i32, ctypes.POINTER(ctypes.c_float)]),
+        "mrt_probe_handoff": (i32, [i32, i32, i32, i32, ctypes.POINTER(ctypes.c_float)]),
+        "mrt_probe_pingpong": (i32, [i32, i32, i32, ctypes.POINTER(ctypes.c_float)]),
         "mrt_df_sample_level_noalloc": (i32, [vp, vp, ctypes.POINTER(_GenOpts), i32, i32, vp, vp]),
         "mrt_df_depth_forward_full": (i32, [vp, vp, i32, vp, i32, vp]),
         "mrt_df_temporal_step_with_bias": (i32, [vp, vp, vp, i32, vp, vp]),

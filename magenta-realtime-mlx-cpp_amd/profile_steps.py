@@ -31,6 +31,13 @@ untimed one, for matrix-core counter runs.
 one warm pass, then repeated reads of one buffer) at buffer sizes from 16 MiB to
 4 GiB, to locate where re-reads stop being served by the 256 MB last-level cache.
 
+    python magenta-realtime-mlx-cpp_amd/profile_steps.py --handoff
+
+--handoff instead measures the latency floor of the persistent kernels' phase
+hand-offs: one word bounced between workgroup 0 and workgroups on other CUs
+(mrt_probe_pingpong), and all-gathers of tagged words among 8..256 workgroups
+(mrt_probe_handoff), the shape of one phase of the frame kernel at 256 / 1024.
+
 The copy (torch's device copy of M MiB, M above the 256 MB last-level cache)
 reads and writes exactly M MiB; its counter readings give the scale factor
 between the counters and bytes.
@@ -60,7 +67,21 @@ def main() -> None:
     ap.add_argument("--style", action="store_true", help="MusicCoCa text embeddings instead")
     ap.add_argument("--encoder", type=int, default=0, help="streams of encoder-only prefills (0: none)")
     ap.add_argument("--read-sweep", action="store_true", help="read bandwidth against buffer size instead")
+    ap.add_argument("--handoff", action="store_true", help="hand-off latency probes instead")
     a = ap.parse_args()
+
+    if a.handoff:
+        import mrt_df
+        for peer in (1, 2, 4, 7, 8, 16, 64, 255):
+            us = mrt_df.pingpong_latency(peer, 2000)
+            print(f"[profile] ping-pong workgroup 0 <-> {peer:3d}: one-way {us:.3f} us", flush=True)
+        for g in (8, 32, 64, 128, 256):
+            for words in (256, 1024):
+                if words >= g and words // g <= 256:
+                    us = mrt_df.handoff_latency(g, words, 2000)
+                    print(f"[profile] all-gather {g:3d} workgroups x {words:4d} words: {us:.3f} us per round",
+                          flush=True)
+        return
 
     if a.read_sweep:
         import mrt_df
