@@ -230,6 +230,13 @@ int mrt_df_depth_forward_full(mrt_df_state* st, const void* token_embeddings, in
  * kernel, num_frames * (1 + rvq_depth) with one launch per step, 0 on the
  * per-layer path.  Waits for the section to finish. */
 int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches);
+/* Instrumentation, no counterpart in the reference: with MRT_TRACE_PHASES set
+ * when the state was created, the persistent kernels' workgroup 0 stamps the
+ * device wall clock at every phase boundary of frame 1 of a decode (its
+ * temporal step, then depth level 1).  Copies the 2 x 512 raw stamps of the
+ * last decode into `out` (n >= 1024 words; zero = not reached) and the clock
+ * rate in MHz into *clock_mhz.  MRT_ERR_INVALID when tracing is off. */
+int mrt_df_state_phase_trace(mrt_df_state* st, uint64_t* out, int n, float* clock_mhz);
 /* Share of the last mrt_df_generate_tokens call's RVQ levels whose token came
  * from the speculative verification pass (accepted drafts plus each frame's
  * first disagreement); -1 when that call did not speculate.  No counterpart

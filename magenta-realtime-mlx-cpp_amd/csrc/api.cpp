@@ -381,6 +381,13 @@ int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches) {
   });
 }
 
+int mrt_df_state_phase_trace(mrt_df_state* st, uint64_t* out, int n, float* clock_mhz) {
+  return guarded([&] {
+    if (!out || !clock_mhz) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    *clock_mhz = S(st).phase_trace(out, n);
+  });
+}
+
 int mrt_df_state_spec_acceptance(mrt_df_state* st, float* acceptance) {
   return guarded([&] {
     if (!acceptance) throw mrt::Error(MRT_ERR_INVALID, "null argument");

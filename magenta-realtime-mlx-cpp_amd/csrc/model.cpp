@@ -221,6 +221,17 @@ Model::Model(const TensorSource& src, const Config& c, DType dtype, int dev)
     }
     tbuckets = static_cast<const int*>(upload_i32(tb));
     dbuckets = static_cast<const int*>(upload_i32(db));
+    const size_t n_rows = static_cast<size_t>(H) * kBiasRows * (kBiasRows + 1) / 2;
+    void* t = nullptr;
+    void* d = nullptr;
+    MRT_HIP_CHECK(hipMalloc(&t, n_rows * esz));
+    allocs_.push_back(t);
+    MRT_HIP_CHECK(hipMalloc(&d, n_rows * esz));
+    allocs_.push_back(d);
+    precompute_biases(0, kBiasRows, t);
+    precompute_biases(1, kBiasRows, d);
+    tbias_rows = t;
+    dbias_rows = d;
   }
 
   for (int i = 0; i < cfg.num_encoder_layers; ++i) {
@@ -538,8 +549,7 @@ StepArgs State::temporal_args(const void* in, int f, void* out) const {
   a.bph = bph_;
   a.pos = f;
   a.Lmax = F;
-  a.bias_tab = m.tbias;
-  a.buckets = m.tbuckets;
+  a.bias_rows = m.tbias_rows;
   a.in = in;
   a.out = out;
   a.S = S;
@@ -561,8 +571,7 @@ StepArgs State::depth_args(const void* in, int l, const void* head_w, int head_r
   a.bph = bph_;
   a.pos = l;
   a.Lmax = c.rvq_depth;
-  a.bias_tab = m.dbias;
-  a.buckets = m.dbuckets;
+  a.bias_rows = m.dbias_rows;
   a.in = in;
   a.S = S;
   a.dec_norm = m.dec_norm;
@@ -1178,6 +1187,16 @@ float State::last_decode_ms(int* launches) {
   MRT_HIP_CHECK(hipEventElapsedTime(&ms, ev_dec_[0], ev_dec_[1]));
   if (launches) *launches = dec_launches_;
   return ms;
+}
+
+float State::phase_trace(uint64_t* out, int n) {
+  MRT_REQUIRE(d_trace_ != nullptr, "phase trace: the state was created without MRT_TRACE_PHASES");
+  MRT_REQUIRE(n >= 2 * kTraceSlots, "phase trace: the output holds fewer than 2 x 512 words");
+  MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  MRT_HIP_CHECK(hipMemcpy(out, d_trace_, 2 * kTraceSlots * sizeof(uint64_t), hipMemcpyDeviceToHost));
+  int khz = 0;
+  MRT_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, m.device));
+  return static_cast<float>(khz) / 1000.f;
 }
 
 void* State::buffer(int which, int layer, size_t* bytes) {

@@ -86,6 +86,12 @@ class Model {
   const int* tbuckets = nullptr;   // bucket of distance n, n < kBucketTable
   const int* dbuckets = nullptr;
   const void* wkv_cross = nullptr; // (Lt * 2 * HD, D): [layer][k|v] rows
+  // Self-attention bias rows of positions 0..kBiasRows-1, model dtype, as
+  // precompute_biases lays them out (position p's (H, p + 1) block at element
+  // H p (p + 1) / 2): the persistent kernels read one element per key.
+  const void* tbias_rows = nullptr;
+  const void* dbias_rows = nullptr;
+  static constexpr int kBiasRows = 64;
   std::vector<EncoderLayerW> enc;
   std::vector<DecoderLayerW> tmp, dep;
   size_t weight_bytes = 0;
@@ -186,6 +192,10 @@ class State {
   // pass (accepted drafts and the first disagreement); -1 when it did not speculate.
   float spec_acceptance() const { return spec_acc_; }
   float last_decode_ms(int* launches);
+  // Raw per-phase timeline of workgroup 0 (MRT_TRACE_PHASES set at state
+  // creation): 2 x kTraceSlots device wall-clock stamps, the temporal step and
+  // depth level 1 of frame 1 of the last decode.  Returns the clock in MHz.
+  float phase_trace(uint64_t* out, int n);
 
  private:
   // Persistent-kernel decode path: one launch per step (API steps) or per

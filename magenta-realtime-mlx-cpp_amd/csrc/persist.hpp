@@ -60,9 +60,8 @@ struct StepArgs {
   int cross;   // temporal step (has cross attention)
   int D, HD, H, F, bph;
   int pos, Lmax;  // ring slot written this step; ring size
-  const void* bias_tab;
-  const int* buckets;
-  const void* bias_row;  // explicit self-attention bias (H, pos + 1) model dtype, or nullptr (table)
+  const void* bias_rows;  // default self-attention bias: position p's (H, p + 1) block at H p (p + 1) / 2
+  const void* bias_row;   // explicit self-attention bias (H, pos + 1) model dtype, or nullptr (bias_rows)
   const void* in;   // (2, D) model-dtype rows (plain)
   void* out;        // (2, D) rows: temporal output
   int S;            // encoder length

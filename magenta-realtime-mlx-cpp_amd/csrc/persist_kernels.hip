@@ -661,6 +661,8 @@ __device__ __forceinline__ int krot(int slot, int chunk) {
 // LDS region with the calling wave; `lim` bytes from src are readable.  ROT:
 // store the slots rotated (K).  The LDS destination of a lane is fixed by the
 // instruction (16 bytes per lane), so the rotation picks the source chunk.
+// Lanes past the n slots do not copy, so the region from slot n on is left
+// as it is (the attention writes the current slot there meanwhile).
 template <typename T, bool ROT>
 __device__ __forceinline__ void stage_slots(const T* src, int n, long lim, T* region) {
   constexpr int kRow = 64 * (int)sizeof(T);
@@ -668,12 +670,14 @@ __device__ __forceinline__ void stage_slots(const T* src, int n, long lim, T* re
   const int bytes = n * kRow;
   for (int off = 0; off < bytes; off += 1024) {
     long o = off + lane * 16;
-    if constexpr (ROT) {
-      const int j = (int)(o / kRow), pch = (int)(o % kRow) / 16;  // slot, stored chunk
-      o = (long)j * kRow + ((pch - j) & (kChunks<T> - 1)) * 16;
+    if (o < bytes) {
+      if constexpr (ROT) {
+        const int j = (int)(o / kRow), pch = (int)(o % kRow) / 16;  // slot, stored chunk
+        o = (long)j * kRow + ((pch - j) & (kChunks<T> - 1)) * 16;
+      }
+      o = min(o, lim - 16);
+      lds_copy16(reinterpret_cast<const char*>(src) + o, reinterpret_cast<char*>(region) + off);
     }
-    o = min(o, lim - 16);
-    lds_copy16(reinterpret_cast<const char*>(src) + o, reinterpret_cast<char*>(region) + off);
   }
 }
 
@@ -703,21 +707,20 @@ __device__ __forceinline__ float pv_sum(const float* p, const T* v, int n, float
   return (o0 + o1) + (o2 + o3);
 }
 
-// Self attention of head h over ring slots 0..pos (scale 1.0, bias
-// table[bucket[pos - j], h]; modules.cpp:243-295).  q and slot pos come as
-// tagged words of this launch; slots before pos are in LDS, region
-// (kind, row) = `cap` slots x 64 at hist + (kind * 2 + row) * cap * 64 (kind
-// 0 = K, 1 = V).  They were staged there from the global ring (slots written
-// by earlier launches) or, `resident`, written by this function at earlier
-// steps of the same launch: it then also stores slot pos for the next step.
+// Self attention of head h over ring slots 0..pos (scale 1.0, additive bias;
+// modules.cpp:243-295).  q and slot pos come as tagged words of this launch;
+// slots before pos are in LDS, region (kind, row) = `cap` slots x 64 at hist
+// + (kind * 2 + row) * cap * 64 (kind 0 = K, 1 = V).  They were staged there
+// from the global ring (slots written by earlier launches) or, `resident`,
+// written by this function at earlier steps of the same launch.  Slot pos is
+// written there too, so every key is read the same way.  `pbias`: lane j's
+// bias for key j (j <= pos) in waves 0 and 1, loaded ahead (attn_bias).
 template <typename T>
 __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, int h, uint32_t tag, uint32_t out_tag,
-                                                    T* hist, int cap, bool resident, float* sm) {
+                                                    T* hist, int cap, bool resident, float pbias, float* sm) {
   using S = St<T>;
   constexpr int V = S::kVec;
   float* qs = sm;        // [2][64]
-  float* ks = sm + 128;  // [2][64]  slot pos
-  float* vs = sm + 256;  // [2][64]  slot pos
   float* ps = sm + 384;  // [2][64]
   float* os = sm + 512;  // [2][64]
   const int tid = threadIdx.x, wid = uniform(tid >> 6), lane = tid & 63;
@@ -738,9 +741,10 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
       __builtin_amdgcn_s_sleep(1);
     }
     const float v0 = LL<T>::get(w, 0), v1 = LL<T>::get(w, 1);
-    d[lane] = v0;
-    d[64 + lane] = v1;
-    if (resident && wid > 0) {  // keep slot pos of K (wave 1, rotated) / V (wave 2) for later steps
+    if (wid == 0) {
+      d[lane] = v0;
+      d[64 + lane] = v1;
+    } else {  // slot pos of K (wave 1, rotated) / V (wave 2), read below and, resident, by later steps
       const int e = wid == 1 ? krot<T>(pos, lane / V) * V + lane % V : lane;
       T* slot = hist + ((wid - 1) * 2) * rs + pos * 64 + e;
       slot[0] = S::st(v0);
@@ -752,7 +756,7 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
   if (wid < 2) {
     const int b = wid;
     float sc = -INFINITY;
-    if (lane < pos) {
+    if (lane < len) {
       const T* kr = hist + b * rs + lane * 64;
       float acc = 0.f;
 #pragma unroll
@@ -762,23 +766,14 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
 #pragma unroll
         for (int e = 0; e < V; ++e) acc = fmaf(qs[b * 64 + i * V + e], S::ld(ke[e]), acc);
       }
-      sc = acc;
-    } else if (lane == pos) {
-      float acc = 0.f;
-#pragma unroll 16
-      for (int d = 0; d < 64; ++d) acc = fmaf(qs[b * 64 + d], ks[b * 64 + d], acc);
-      sc = acc;
+      sc = acc + pbias;
     }
-    if (lane < len)
-      sc += a.bias_row != nullptr
-                ? S::ld(ld_g(static_cast<const T*>(a.bias_row) + h * len + lane))
-                : S::ld(ld_g(static_cast<const T*>(a.bias_tab) + ld_g(a.buckets + pos - lane) * a.H + h));
     const float m = dpp_max(sc);
     const float p = lane < len ? expf(sc - m) : 0.f;
     const float l = dpp_sum(p);
     ps[b * 64 + lane] = p;
     // the same wave reads ps back: LDS operations of a wave complete in order
-    const float o = pv_sum<T>(ps + b * 64, hist + (2 + b) * rs + lane, pos, ps[b * 64 + pos] * vs[b * 64 + lane]);
+    const float o = pv_sum<T>(ps + b * 64, hist + (2 + b) * rs + lane, len, 0.f);
     os[b * 64 + lane] = o / l;
   }
   __syncthreads();
@@ -1264,6 +1259,14 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     if (act) LL<T>::put(a.ll.x, sD.row(wid, t), S::rnd(x0 + S::rnd(s[0][0])), S::rnd(x1 + S::rnd(s[0][1])), tg);
   };
 
+  // the attention workgroups' bias of key j = lane (the same for every layer
+  // of the step), loaded ahead so that no dependent load sits in the attention
+  float pbias = 0.f;
+  if (jpart == 0 && wid < 2 && lane <= io.pos) {
+    const T* row = a.bias_row != nullptr ? static_cast<const T*>(a.bias_row)
+                                         : static_cast<const T*>(a.bias_rows) + (size_t)H * io.pos * (io.pos + 1) / 2;
+    pbias = S::ld(ld_g(row + h * (io.pos + 1) + lane));
+  }
   uint32_t x_tag = io.in_tag;
   for (int li = 0; li < a.nlayers; ++li) {
     const bool first = li == 0, last = li + 1 == a.nlayers;
@@ -1337,7 +1340,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     const T* wo = static_cast<const T*>(a.st.wo) + li * eO;
     if (jpart == 0) {
       self_attention_head<T>(a, io.pos, h, tag(base + kPhQKV), tag(base + kPhAtt), lhist, io.resident ? io.cap : 64,
-                             io.resident, sm);
+                             io.resident, pbias, sm);
       MRT_TP;
       if (CROSS) stage_cross();  // the history has been read (barrier above)
     }

@@ -250,6 +250,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_state_write": (i32, [vp, i32, i32, vp, sz]),
         "mrt_df_state_set_cache_length": (i32, [vp, i32, i32]),
         "mrt_df_state_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(i32)]),
+        "mrt_df_state_phase_trace": (i32, [vp, ctypes.POINTER(ctypes.c_uint64), i32, ctypes.POINTER(ctypes.c_float)]),
         "mrt_df_state_spec_acceptance": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
         "mrt_stream_config_default": (None, [ctypes.POINTER(_StreamConfig)]),
         "mrt_chunk_opts_default": (None, [ctypes.POINTER(_ChunkOpts)]),
@@ -540,6 +541,15 @@ class State:
         ms, n = ctypes.c_float(), ctypes.c_int()
         _check(self.lib, self.lib.mrt_df_state_decode_time(self._h, ctypes.byref(ms), ctypes.byref(n)))
         return float(ms.value), int(n.value)
+
+    def phase_trace(self):
+        """(raw stamps (2, 512) uint64, clock MHz) of the last decode's frame 1
+        (temporal step, depth level 1), recorded when MRT_TRACE_PHASES was set
+        at state creation (mrt_df_state_phase_trace)."""
+        buf = (ctypes.c_uint64 * 1024)()
+        mhz = ctypes.c_float()
+        _check(self.lib, self.lib.mrt_df_state_phase_trace(self._h, buf, 1024, ctypes.byref(mhz)))
+        return np.frombuffer(buf, dtype=np.uint64).reshape(2, 512).copy(), float(mhz.value)
 
     def spec_acceptance(self) -> float:
         """Share of the last generate_tokens call's levels taken from the

@@ -38,6 +38,13 @@ hand-offs: one word bounced between workgroup 0 and workgroups on other CUs
 (mrt_probe_pingpong), and all-gathers of tagged words among 8..256 workgroups
 (mrt_probe_handoff), the shape of one phase of the frame kernel at 256 / 1024.
 
+    python magenta-realtime-mlx-cpp_amd/profile_steps.py --timeline
+
+--timeline instead sets MRT_TRACE_PHASES, decodes a 50-frame chunk once untimed
+and once traced, and prints workgroup 0's per-phase timeline of frame 1 (the
+temporal step's first 14 layers and depth level 1), labelled by phase part, as
+averages per layer (mrt_df_state_phase_trace).
+
 The copy (torch's device copy of M MiB, M above the 256 MB last-level cache)
 reads and writes exactly M MiB; its counter readings give the scale factor
 between the counters and bytes.
@@ -68,7 +75,11 @@ def main() -> None:
     ap.add_argument("--encoder", type=int, default=0, help="streams of encoder-only prefills (0: none)")
     ap.add_argument("--read-sweep", action="store_true", help="read bandwidth against buffer size instead")
     ap.add_argument("--handoff", action="store_true", help="hand-off latency probes instead")
+    ap.add_argument("--timeline", action="store_true", help="per-phase timeline of one frame instead")
     a = ap.parse_args()
+    if a.timeline:
+        import os
+        os.environ["MRT_TRACE_PHASES"] = "1"  # read when the state is created
 
     if a.handoff:
         import mrt_df
@@ -169,6 +180,18 @@ def main() -> None:
     ctx = np.stack([rng.integers(0, 1024, scfg.context_frames) + 0 for _ in range(16)], axis=1)
     style = scfg.style_offset + 1024 * np.arange(6) + rng.integers(0, 1024, 6)
     st.encode(system.build_encoder_inputs(ctx, scfg, style))
+    if a.timeline:
+        opts = mrt_df.GenOptions(num_frames=scfg.chunk_frames, rvq_depth=cfg.rvq_depth, temperature=1.1, top_k=40,
+                                 guidance_weight=5.0, seed=a.seed, use_graph=False)
+        st.generate_tokens(None, opts)
+        st.generate_tokens(None, opts)
+        ms, launches = st.decode_time()
+        trace, mhz = st.phase_trace()
+        print(f"[profile] traced decode of {scfg.chunk_frames} frames: {ms:.2f} ms, {launches} launches", flush=True)
+        print_timeline(trace, mhz, cfg)
+        st.close()
+        model.close()
+        return
 
     n = a.copy_mib * (1 << 20) // 4
     src = torch.ones(n, dtype=torch.float32, device="cuda")
@@ -198,6 +221,77 @@ def main() -> None:
     print(f"[profile] decode of {scfg.chunk_frames} frames: {launches} persistent launches, {ms:.2f} ms", flush=True)
     st.close()
     model.close()
+
+
+# Trace points of workgroup 0 = (head 0, part 0) per decoder layer, in order
+# (persist_kernels.hip run_stack: three per activation load -- start, poll
+# complete, norm and barrier done -- and one after each GEMV, head 0's
+# attention and the cross-attention partial / combine).
+_DEPTH_LAYER = ["QKV issue", "QKV poll", "QKV norm", "QKV GEMV", "attention",
+                "O issue", "O poll", "O barrier", "O GEMV",
+                "up issue", "up poll", "up norm", "up GEMV",
+                "down issue", "down poll", "down barrier", "down GEMV"]
+_TEMPORAL_LAYER = (_DEPTH_LAYER[:9] + ["cross-q issue", "cross-q poll", "cross-q norm", "cross-q GEMV",
+                                       "cross partial", "cross combine",
+                                       "cross-O issue", "cross-O poll", "cross-O barrier", "cross-O GEMV"]
+                   + _DEPTH_LAYER[9:])
+_TRACE_START, _TRACE_END, _TRACE_DONE = 509, 510, 511
+
+
+def _layer_deltas(row, t0, labels, nlayers):
+    """Per-layer deltas (us) between consecutive stamps; the first delta of a
+    layer runs from the previous layer's last stamp (t0 for layer 0)."""
+    n = len(labels)
+    out = []
+    prev = t0
+    for li in range(nlayers):
+        pts = row[li * n:(li + 1) * n]
+        if len(pts) < n or (pts == 0).any():
+            break
+        d = np.diff(np.concatenate([[prev], pts]).astype(np.int64))
+        out.append(d)
+        prev = pts[-1]
+    return np.array(out, dtype=np.float64), prev
+
+
+def print_timeline(trace, mhz, cfg):
+    to_us = 1.0 / mhz
+    # temporal step of frame 1: 400 stamps cover the first 14 of its layers
+    t = trace[0]
+    tl, _ = _layer_deltas(t, t[_TRACE_START], _TEMPORAL_LAYER, 14)
+    tot_t = (int(t[_TRACE_DONE]) - int(t[_TRACE_START])) * to_us
+    print(f"[profile] temporal step of frame 1: {tot_t:.2f} us total; mean over its first {len(tl)} layers:", flush=True)
+    for lab, v in zip(_TEMPORAL_LAYER, tl.mean(0) * to_us):
+        print(f"[profile]   {lab:16s} {v:6.2f} us", flush=True)
+    print(f"[profile]   {'layer':16s} {tl.sum(1).mean() * to_us:6.2f} us", flush=True)
+    # depth level 1 of frame 1: 4 layers, then the head's activation load
+    d = trace[1]
+    dl, last = _layer_deltas(d, d[_TRACE_START], _DEPTH_LAYER, cfg.num_depth_layers)
+    tot_d = (int(d[_TRACE_DONE]) - int(d[_TRACE_START])) * to_us
+    print(f"[profile] depth level 1 of frame 1: {tot_d:.2f} us total; mean over its {len(dl)} layers:", flush=True)
+    for lab, v in zip(_DEPTH_LAYER, dl.mean(0) * to_us):
+        print(f"[profile]   {lab:16s} {v:6.2f} us", flush=True)
+    print(f"[profile]   {'layer':16s} {dl.sum(1).mean() * to_us:6.2f} us", flush=True)
+    k = cfg.num_depth_layers * len(_DEPTH_LAYER)
+    h = d[k:k + 3].astype(np.int64)
+    if (h > 0).all():
+        print(f"[profile]   {'head issue':16s} {(h[0] - int(last)) * to_us:6.2f} us", flush=True)
+        print(f"[profile]   {'head poll':16s} {(h[1] - h[0]) * to_us:6.2f} us", flush=True)
+        print(f"[profile]   {'head norm':16s} {(h[2] - h[1]) * to_us:6.2f} us", flush=True)
+        print(f"[profile]   {'head GEMV + logit gather':16s} {(int(d[_TRACE_END]) - h[2]) * to_us:6.2f} us", flush=True)
+        print(f"[profile]   {'draw + publish':16s} {(int(d[_TRACE_DONE]) - int(d[_TRACE_END])) * to_us:6.2f} us",
+              flush=True)
+        # inside the draw (sample_block): stamps after the guided logits, the argmax, the count of
+        # candidates above it, the radix-select fallback (if taken), the publish, and each radix pass
+        names = ["scaled+noise", "argmax", "count", "fallback", "publish", "radix 1", "radix 2", "radix 3", "radix 4"]
+        marks = [f"{nm} {(int(v) - int(d[_TRACE_END])) * to_us:.2f}" for nm, v in zip(names, d[490:499]) if v]
+        print("[profile]   draw stamps (us after the logit gather): " + ", ".join(marks), flush=True)
+    # phase-part totals per depth level
+    groups = {"issue next weights": ["issue"], "poll (hand-off + weights)": ["poll"],
+              "norm / barrier": ["norm", "barrier"], "GEMV + stores": ["GEMV"], "attention (head 0)": ["attention"]}
+    for name, keys in groups.items():
+        cols = [i for i, lab in enumerate(_DEPTH_LAYER) if any(lab.endswith(k) or lab == k for k in keys)]
+        print(f"[profile] depth level, {name}: {dl[:, cols].sum(1).sum() * to_us:.2f} us", flush=True)
 
 
 if __name__ == "__main__":
