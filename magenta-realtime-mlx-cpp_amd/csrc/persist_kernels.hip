@@ -1596,7 +1596,11 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   const int L = fa.levels, C = fa.codebook, D = ad.D;
   const int code0 = 16 * (at.nlayers + 1), per_step = 16 * (ad.nlayers + 1);
   float fs[kDrawPer] = {};  // frame sum (workgroup 0)
-  if (c.blk == 0) draw_clear(c.sel_hist);  // ordered before the first draw by the gather's barriers
+  DrawPrefetch pf{};        // noise of the next draw (workgroup 0), loaded a level ahead
+  if (c.blk == 0) {
+    draw_clear(c.sel_hist);  // ordered before the first draw by the gather's barriers
+    draw_prefetch(C, ad.noise, ad.teacher, ad.frame * L, pf);
+  }
   int tok = 0;
   prefetch_qkv<T, false>(c, ad, 0);
   for (int l = 0; l < L; ++l) {
@@ -1618,25 +1622,27 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     const uint32_t tg_logit = c.tag(base + 16 * ad.nlayers + kPhLogit);
     const uint32_t tg_tok = c.tag(base + 16 * ad.nlayers + kPhToken);
     run_head<T>(c, ad, hw, x_tag, tg_logit, trace);
-    if (l + 1 < L) prefetch_qkv<T, false>(c, ad, 0);
+    if (c.blk != 0 && l + 1 < L) prefetch_qkv<T, false>(c, ad, 0);
     if (c.blk == 0) {
+      // Nothing is loaded between the head and the gather: a wave's memory
+      // operations retire in order, so the gather's polls would wait for them.
       if (l + 1 == L && threadIdx.x == 0) astore(ad.ll.seq, c.ep + 1u);  // every workgroup has started
       const int slot = ad.frame * L + l;
-      DrawPrefetch pf;
-      draw_prefetch(C, ad.noise + (size_t)l * C, ad.teacher, slot, pf);
-      // the previous level's token joins the frame sum while the logits arrive
-      if (l > 0) frame_sum_add<T>(fs, static_cast<const T*>(ad.emb), tok, D, l == 1);
       __syncthreads();
       float* lg = c.xsb[c.xsel ^ 1];
       gather_logits<T>(ad, tg_logit, lg, nullptr, fa.rec_slices ? fa.rec_slices + (size_t)l * 2 * C : nullptr);
       if (trace != nullptr && threadIdx.x == 0) trace[kTraceEnd] = wall_clock64();
+      if (l + 1 < L) prefetch_qkv<T, false>(c, ad, 0);  // lands during the draw
       tok = sample_block<T>(ad.sp, l, slot, pf, ad.teacher != nullptr, ad.tokens, ad.drawn,
                             l + 1 < L ? ad.ll.tok : nullptr, tg_tok, lg, c.sel_hist, c.sel_res, trace);
       if (trace != nullptr && threadIdx.x == 0) trace[kTraceDone] = wall_clock64();
-      if (l + 1 == L) {
-        frame_sum_add<T>(fs, static_cast<const T*>(ad.emb), tok, D, L == 1);
+      // this level's token joins the frame sum (the embedding row is the next
+      // level's input too), and the next draw's noise is loaded a level ahead
+      frame_sum_add<T>(fs, static_cast<const T*>(ad.emb), tok, D, l == 0);
+      if (l + 1 < L)
+        draw_prefetch(C, ad.noise + (size_t)(l + 1) * C, ad.teacher, slot + 1, pf);
+      else
         frame_mean_store<T>(fs, L, static_cast<T*>(ad.fmean), D);
-      }
     } else if (l + 1 < L) {
       // every workgroup waits for the draw (one word, polled by one lane)
       __shared__ int tok_s;
