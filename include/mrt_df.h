@@ -256,12 +256,12 @@ int mrt_probe_read_bandwidth(int device, size_t bytes, int passes, float* gbps);
  * round of an all-gather of `words` (workgroups..1024, a multiple of
  * `workgroups`, at most 256 per workgroup) tagged 64-bit words among
  * `workgroups` (1..CU count) workgroups -- each stores its share with
- * agent-scope atomics, then polls all words -- over `rounds` (1..100000)
- * rounds.  mrt_probe_pingpong: one-way microseconds of a word bounced
+ * agent-scope atomics, waits `delay` (0..256) rounds of s_sleep(1) (64 clocks
+ * each), then polls all words -- over `rounds` (1..100000) rounds.  mrt_probe_pingpong: one-way microseconds of a word bounced
  * `rounds` times between workgroups 0 and `peer` (1..CU count - 1).  Both
  * allocate and free a 16 KiB buffer; every poll is bounded (a spin limit
  * returns MRT_ERR_HIP). */
-int mrt_probe_handoff(int device, int workgroups, int words, int rounds, float* us_per_round);
+int mrt_probe_handoff(int device, int workgroups, int words, int rounds, int delay, float* us_per_round);
 int mrt_probe_pingpong(int device, int peer, int rounds, float* us_one_way);
 
 /* State buffers exposed for parity checks (device-to-device copies). */

@@ -402,10 +402,10 @@ int mrt_probe_read_bandwidth(int device, size_t bytes, int passes, float* gbps) 
   });
 }
 
-int mrt_probe_handoff(int device, int workgroups, int words, int rounds, float* us_per_round) {
+int mrt_probe_handoff(int device, int workgroups, int words, int rounds, int delay, float* us_per_round) {
   return guarded([&] {
     if (!us_per_round) throw mrt::Error(MRT_ERR_INVALID, "null argument");
-    *us_per_round = mrt::probe_handoff(device, workgroups, words, rounds);
+    *us_per_round = mrt::probe_handoff(device, workgroups, words, rounds, delay);
   });
 }
 

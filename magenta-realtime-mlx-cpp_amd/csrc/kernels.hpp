@@ -167,9 +167,10 @@ void sample_level_noalloc(DType dt, int device, const void* emb, int D, const fl
 // after one warm pass (probe_kernels.hip).
 float probe_read_bandwidth(int device, size_t bytes, int passes);
 // Microseconds per round of an all-gather of `words` tagged words among
-// `workgroups` workgroups (one phase hand-off of the persistent kernels), and
+// `workgroups` workgroups (one phase hand-off of the persistent kernels; `delay`
+// rounds of s_sleep(1) before each round's first poll), and
 // the one-way latency of a word bounced between workgroups 0 and `peer`.
-float probe_handoff(int device, int workgroups, int words, int rounds);
+float probe_handoff(int device, int workgroups, int words, int rounds, int delay);
 float probe_pingpong(int device, int peer, int rounds);
 
 }  // namespace mrt

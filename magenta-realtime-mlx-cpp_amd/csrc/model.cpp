@@ -435,6 +435,7 @@ void State::setup_persistent() {
   };
   tstack_ = stack(m.tmp, true);
   dstack_ = stack(m.dep, false);
+  if (const char* d = std::getenv("MRT_POLL_DELAY")) poll_delay_ = std::max(0, std::min(256, std::atoi(d)));
   if (std::getenv("MRT_TRACE_PHASES")) {
     d_trace_ = static_cast<uint64_t*>(dalloc(2 * kTraceSlots * sizeof(uint64_t)));
     MRT_HIP_CHECK(hipMemset(d_trace_, 0, 2 * kTraceSlots * sizeof(uint64_t)));
@@ -509,6 +510,7 @@ LLBufs State::ll_bufs() const {
   l.seq = reinterpret_cast<uint32_t*>(tail);
   l.tok = tail + 16;
   l.err = reinterpret_cast<int*>(tail + 32);
+  l.poll_delay = poll_delay_;
   return l;
 }
 

@@ -227,6 +227,7 @@ class State {
   int* h_err_ = nullptr;        // pinned
   uint64_t* h_seed_ = nullptr;  // pinned: the draw seed of a generate / sample call
   uint64_t* d_trace_ = nullptr; // 2 x kTraceSlots when MRT_TRACE_PHASES is set
+  int poll_delay_ = 4;          // s_sleep(1) rounds before a hand-off's first poll (MRT_POLL_DELAY)
   hipEvent_t ev_dec_[2] = {nullptr, nullptr};  // around the decode section of generate
   int dec_launches_ = 0;
   bool dec_timed_ = false;

@@ -46,6 +46,7 @@ struct LLBufs {
   uint64_t* tok;    // token drawn by workgroup 0 (frame kernel)
   uint32_t* seq;    // launch counter (tag epoch), advanced by each launch
   int* err;         // set when a poll exceeds its spin limit
+  int poll_delay;   // s_sleep(1) rounds before the first poll of a hand-off
 };
 // tag = (epoch << kTagShift) | phase code: codes stay below 1 << kTagShift,
 // and the host zeroes every word and restarts the epoch at 1 before the

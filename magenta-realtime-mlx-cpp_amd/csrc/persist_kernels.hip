@@ -90,6 +90,13 @@ __device__ __forceinline__ P pick3(int i, P p0, P p1, P p2) {
   return i == 0 ? p0 : i == 1 ? p1 : p2;
 }
 
+// Waits n rounds of s_sleep(1) (64 clocks each) before a hand-off's first poll:
+// polls issued before the producers' stores can have landed only congest the
+// memory side and delay the words they wait for.
+__device__ __forceinline__ void poll_wait(int n) {
+  for (int i = 0; i < n; ++i) __builtin_amdgcn_s_sleep(1);
+}
+
 __device__ __forceinline__ bool spin_failed(uint32_t& spins, int* err) {
   if ((++spins & 255u) == 0) {
     if (aload(err) != 0 || spins > kSpinLimit) {
@@ -314,7 +321,7 @@ struct Act {
 template <typename T, int NPER, bool KEEP>
 __device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t tag, float* xs,
                                             float (&v0)[NPER], float (&v1)[NPER], const Side& sd, float& r0,
-                                            float& r1, int* err) {
+                                            float& r1, int* err, int delay) {
   constexpr int NW = LL<T>::kWords;
   const int tid = threadIdx.x;
   uint64_t w[NPER][NW];
@@ -330,6 +337,7 @@ __device__ __forceinline__ void ll_load_vec(const uint64_t* src, int K, uint32_t
     r1 = St<T>::ld(ld_g(p + sd.stride + sd.row));
   }
   uint32_t spins = 0;
+  if (pend != 0 || side_pend) poll_wait(delay);
   while (pend != 0 || side_pend) {
 #pragma unroll
     for (int i = 0; i < NPER; ++i)
@@ -406,7 +414,7 @@ __device__ __forceinline__ void load_gamma(const T* g, int K, Gamma<T, NPER>& ou
 template <typename T, int NPER, bool NORM>
 __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, int K, uint32_t tag,
                                          const Gamma<T, NPER>& gk, float* xs, float* red, const Side& sd, float& r0,
-                                         float& r1, int* err, uint64_t* trace, int& tp, int& lc, int stride) {
+                                         float& r1, int* err, int delay, uint64_t* trace, int& tp, int& lc, int stride) {
   using S = St<T>;
   const int tid = threadIdx.x;
   if (trace != nullptr && blockIdx.x == 0 && tid == 0 && lc < 16) trace[kLoadTrace + lc] = wall_clock64();
@@ -430,9 +438,9 @@ __device__ __forceinline__ void load_act(const uint64_t* ll, const void* plain, 
       v1[i] = in ? S::ld(w1[i]) : 0.f;
       if constexpr (!NORM) Act<T>::put(xs, tid + i * kPersistThreads, v0[i], v1[i]);
     }
-    ll_load_vec<T, NPER, NORM>(nullptr, 0, 0, xs, v0, v1, sd, r0, r1, err);
+    ll_load_vec<T, NPER, NORM>(nullptr, 0, 0, xs, v0, v1, sd, r0, r1, err, delay);
   } else {
-    ll_load_vec<T, NPER, NORM>(ll, K, tag, xs, v0, v1, sd, r0, r1, err);
+    ll_load_vec<T, NPER, NORM>(ll, K, tag, xs, v0, v1, sd, r0, r1, err, delay);
   }
   if (trace != nullptr && blockIdx.x == 0 && (tid & 63) == 0 && lc < 16) trace[kWaveTrace + 4 * lc + (tid >> 6)] = wall_clock64();
   ++lc;
@@ -622,12 +630,13 @@ __device__ __forceinline__ int geglu_row(int j, int p) { return (j >> 5) * 64 + 
 // Polls `n` (<= 256) tagged elements src[i] into LDS floats dst0[i], dst1[i].
 template <typename T>
 __device__ __forceinline__ void ll_load_small(const uint64_t* src, int n, uint32_t tag, float* dst0, float* dst1,
-                                              int* err) {
+                                              int* err, int delay) {
   constexpr int NW = LL<T>::kWords;
   const int tid = threadIdx.x;
   if (tid >= n) return;
   uint64_t w[NW];
   uint32_t spins = 0;
+  poll_wait(delay);
   for (;;) {
 #pragma unroll
     for (int r = 0; r < NW; ++r) w[r] = aload(src + LL<T>::idx(tid, r));
@@ -731,6 +740,7 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
     constexpr int NW = LL<T>::kWords;
     uint64_t w[NW];
     uint32_t spins = 0;
+    poll_wait(a.ll.poll_delay);
     for (;;) {
 #pragma unroll
       for (int r = 0; r < NW; ++r) w[r] = aload(src + LL<T>::idx(lane, r));
@@ -793,7 +803,7 @@ __device__ __forceinline__ void cross_partial(const StepArgs& a, int h, int j, u
   float* wm = sm + 640;  // [4]
   float* wl = sm + 644;  // [4]
   const int tid = threadIdx.x, wid = uniform(tid >> 6), lane = tid & 63;
-  ll_load_small<T>(a.ll.q + h * 64, 64, q_tag, qs, qs + 64, a.ll.err);
+  ll_load_small<T>(a.ll.q + h * 64, 64, q_tag, qs, qs + 64, a.ll.err, a.ll.poll_delay);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's K/V copies have landed
   __syncthreads();
   const int chunk = (a.S + a.bph - 1) / a.bph;
@@ -851,6 +861,7 @@ __device__ __forceinline__ void cross_combine(const StepArgs& a, int h, uint32_t
     uint64_t wm[kMaxBph], wl[kMaxBph], wv[kMaxBph];
     uint32_t pend = (1u << a.bph) - 1u;
     uint32_t spins = 0;
+    poll_wait(a.ll.poll_delay);
     while (pend != 0) {
 #pragma unroll
       for (int j = 0; j < kMaxBph; ++j) {
@@ -1303,7 +1314,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     if (CROSS && jpart != 0) stage_cross();
     // ---- QKV of head h's slice (weights already in flight)
     xs = c.next_xs();
-    load_act<T, 4, true>(a.ll.x, in_plain, D, x_tag, c.gq, xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
+    load_act<T, 4, true>(a.ll.x, in_plain, D, x_tag, c.gq, xs, red, no_side, r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp,
                          c.lcnt, in_stride);
     gemv_rows<T, NVD, 1, NT>(c.buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs,
                              [&](int t, bool act, const float (&s)[1][2]) {
@@ -1348,7 +1359,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     // ---- attention output projection + residual
     xs = c.next_xs();
     load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhAtt), c.gq, xs, red,
-                          side_x(a.ll.x, in_plain, x_tag, in_stride), r0, r1, a.ll.err, io.trace, c.tp, c.lcnt, 0);
+                          side_x(a.ll.x, in_plain, x_tag, in_stride), r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp, c.lcnt, 0);
     gemv_rows<T, NVD, 1, NT>(c.buf, wo, HD, sD.nw(wid), rowD, xs,
                              [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhO)); });
     MRT_TP;
@@ -1361,7 +1372,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
       load_gamma<T, 4>(static_cast<const T*>(a.st.norm_ca) + (size_t)li * D, D, gc);
       fetch_batch<T, NVD, 1, NT>(c.buf, wqc, D, 0, min(kNBuf / NVD, ncq), cq_row);
       xs = c.next_xs();
-      load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gc, xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
+      load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gc, xs, red, no_side, r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp,
                            c.lcnt, 0);
       gemv_rows<T, NVD, 1, NT>(c.buf, wqc, D, ncq, cq_row, xs, [&](int t, bool act, const float (&s)[1][2]) {
         if (act) LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(s[0][0]), S::rnd(s[0][1]), tag(base + kPhCQ));
@@ -1376,7 +1387,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
       }
       xs = c.next_xs();
       load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhCC), c.gq, xs, red,
-                            side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, io.trace, c.tp, c.lcnt, 0);
+                            side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp, c.lcnt, 0);
       gemv_rows<T, NVD, 1, NT>(c.buf, woc, HD, sD.nw(wid), rowD, xs,
                                [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhCO)); });
       MRT_TP;
@@ -1389,7 +1400,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     load_gamma<T, 4>(static_cast<const T*>(a.st.norm_ff) + (size_t)li * D, D, gf);
     fetch_batch<T, NVD, 2, NT>(c.buf, w01, D, 0, min(kNBuf / (2 * NVD), sF.nw(wid)), rowF);
     xs = c.next_xs();
-    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gf, xs, red, no_side, r0, r1, a.ll.err, io.trace, c.tp,
+    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gf, xs, red, no_side, r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp,
                          c.lcnt, 0);
     gemv_rows<T, NVD, 2, NT>(c.buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, bool act, const float (&s)[2][2]) {
       const float g0 = gelu_t<T>(S::rnd(s[0][0])), g1 = gelu_t<T>(S::rnd(s[0][1]));
@@ -1403,7 +1414,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     xs = c.next_xs();
     const Gamma<T, kMaxPersistK / kPersistThreads> nog{};  // no norm
     load_act<T, kMaxPersistK / kPersistThreads, false>(a.ll.h, nullptr, F, tag(base + kPhUp), nog, xs, red,
-                                                       side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, io.trace,
+                                                       side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, a.ll.poll_delay, io.trace,
                                                        c.tp, c.lcnt, 0);
     const bool tagged_out = !last || io.out_tagged;
     gemv_rows<T, NVF, 1, NT>(c.buf, wo2, F, sD.nw(wid), rowD, xs, [&](int t, bool act, const float (&s)[1][2]) {
@@ -1443,7 +1454,7 @@ __device__ __forceinline__ void run_head(Ctx<T>& c, const StepArgs& a, const T* 
   const Side no_side{nullptr, nullptr, 0u, -1, 0};
   float r0 = 0.f, r1 = 0.f;
   float* xs = c.next_xs();
-  load_act<T, 4, true>(a.ll.x, nullptr, a.D, x_tag, c.gq, xs, c.red, no_side, r0, r1, a.ll.err, trace, c.tp,
+  load_act<T, 4, true>(a.ll.x, nullptr, a.D, x_tag, c.gq, xs, c.red, no_side, r0, r1, a.ll.err, a.ll.poll_delay, trace, c.tp,
                        c.lcnt, 0);
   gemv_rows<T, NVD, 1, false>(c.buf, hw, a.D, sH.nw(wid), rowH, xs, [&](int t, bool act, const float (&s)[1][2]) {
     if (act) {
@@ -1476,6 +1487,7 @@ __device__ __forceinline__ void gather_logits(const StepArgs& a, uint32_t tg, fl
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (base_i + (int)threadIdx.x + u * kPersistThreads < n2) pend |= 1u << u;
+    if (base_i == 0) poll_wait(a.ll.poll_delay);
     while (pend != 0) {
 #pragma unroll
       for (int u = 0; u < 8; ++u)
@@ -1649,6 +1661,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       if (threadIdx.x == 0) {
         uint32_t spins = 0;
         uint64_t w;
+        poll_wait(ad.ll.poll_delay);
         for (;;) {
           w = aload(ad.ll.tok);
           if (ll_tag(w) == tg_tok || spin_failed(spins, ad.ll.err)) break;

@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void k_read_sweep(const uint4* __restrict__ p,
 // each workgroup stores its words / G words {r, index} with agent-scope
 // atomic stores, then polls all `words` words with agent-scope atomic loads
 // until each carries round r or later -- one phase hand-off of the step
-// kernels.  k_pingpong bounces one word between workgroup 0 and workgroup
+// kernels.  `delay` rounds of s_sleep(1) precede each round's first poll.  k_pingpong bounces one word between workgroup 0 and workgroup
 // `peer` (one thread each).  Every poll gives up after kSpinLimit rounds and
 // flags an error, so both kernels always end.
 __device__ __forceinline__ uint64_t probe_aload(const uint64_t* p) {
@@ -55,7 +55,7 @@ __device__ __forceinline__ void probe_astore(uint64_t* p, uint64_t v) {
   __hip_atomic_store((MRT_GLOBAL uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__global__ __launch_bounds__(256) void k_handoff(uint64_t* __restrict__ w, int words, int rounds,
+__global__ __launch_bounds__(256) void k_handoff(uint64_t* __restrict__ w, int words, int rounds, int delay,
                                                  uint64_t* __restrict__ clk, int* __restrict__ err) {
   const int G = gridDim.x, b = blockIdx.x, t = threadIdx.x;
   const int per = words / G;
@@ -67,6 +67,7 @@ __global__ __launch_bounds__(256) void k_handoff(uint64_t* __restrict__ w, int w
     for (int i = 0; i < 4; ++i)
       if (t + 256 * i < words) pend |= 1u << i;
     uint32_t spins = 0;
+    for (int i = 0; i < delay; ++i) __builtin_amdgcn_s_sleep(1);  // 64 clocks each, before the first poll
     while (pend != 0) {
       uint64_t v[4];
 #pragma unroll
@@ -199,7 +200,7 @@ double probe_ticks_us(int device, Launch launch) {
 
 }  // namespace
 
-float probe_handoff(int device, int workgroups, int words, int rounds) {
+float probe_handoff(int device, int workgroups, int words, int rounds, int delay) {
   MRT_HIP_CHECK(hipSetDevice(device));
   int num_cu = 0;
   MRT_HIP_CHECK(hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, device));
@@ -208,8 +209,9 @@ float probe_handoff(int device, int workgroups, int words, int rounds) {
               "probe: words must be a multiple of workgroups, at most 1024");
   MRT_REQUIRE(words / workgroups <= 256, "probe: at most 256 words per workgroup (one per thread)");
   MRT_REQUIRE(rounds >= 1 && rounds <= 100000, "probe: rounds must be in [1, 100000]");
+  MRT_REQUIRE(delay >= 0 && delay <= 256, "probe: delay must be in [0, 256]");
   const double us = probe_ticks_us(device, [&](uint64_t* w, uint64_t* clk, int* err, hipStream_t s) {
-    hipLaunchKernelGGL(k_handoff, dim3(workgroups), dim3(256), 0, s, w, words, rounds, clk, err);
+    hipLaunchKernelGGL(k_handoff, dim3(workgroups), dim3(256), 0, s, w, words, rounds, delay, clk, err);
   });
   return static_cast<float>(us / rounds);
 }

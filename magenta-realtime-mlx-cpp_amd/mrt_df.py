@@ -180,13 +180,14 @@ def read_bandwidth(nbytes: int, passes: int, device: int = 0) -> float:
     return float(out.value)
 
 
-def handoff_latency(workgroups: int, words: int, rounds: int, device: int = 0) -> float:
+def handoff_latency(workgroups: int, words: int, rounds: int, delay: int = 0, device: int = 0) -> float:
     """Microseconds per round of an all-gather of ``words`` tagged words among
-    ``workgroups`` workgroups, the hand-off of one persistent-kernel phase
+    ``workgroups`` workgroups, the hand-off of one persistent-kernel phase,
+    with ``delay`` rounds of s_sleep(1) before each first poll
     (mrt_probe_handoff)."""
     lib = load_library()
     out = ctypes.c_float()
-    _check(lib, lib.mrt_probe_handoff(device, workgroups, words, rounds, ctypes.byref(out)))
+    _check(lib, lib.mrt_probe_handoff(device, workgroups, words, rounds, delay, ctypes.byref(out)))
     return float(out.value)
 
 
@@ -221,7 +222,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_config_large": (None, [ctypes.POINTER(_Config)]),
         "mrt_df_create": (i32, [ctypes.c_char_p, ctypes.POINTER(_Config), i32, i32, ctypes.POINTER(vp)]),
         "mrt_probe_read_bandwidth": (i32, [i32, sz, i32, ctypes.POINTER(ctypes.c_float)]),
-        "mrt_probe_handoff": (i32, [i32, i32, i32, i32, ctypes.POINTER(ctypes.c_float)]),
+        "mrt_probe_handoff": (i32, [i32, i32, i32, i32, i32, ctypes.POINTER(ctypes.c_float)]),
         "mrt_probe_pingpong": (i32, [i32, i32, i32, ctypes.POINTER(ctypes.c_float)]),
         "mrt_df_sample_level_noalloc": (i32, [vp, vp, ctypes.POINTER(_GenOpts), i32, i32, vp, vp]),
         "mrt_df_depth_forward_full": (i32, [vp, vp, i32, vp, i32, vp]),

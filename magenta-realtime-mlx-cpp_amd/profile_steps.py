@@ -36,7 +36,8 @@ one warm pass, then repeated reads of one buffer) at buffer sizes from 16 MiB to
 --handoff instead measures the latency floor of the persistent kernels' phase
 hand-offs: one word bounced between workgroup 0 and workgroups on other CUs
 (mrt_probe_pingpong), and all-gathers of tagged words among 8..256 workgroups
-(mrt_probe_handoff), the shape of one phase of the frame kernel at 256 / 1024.
+(mrt_probe_handoff), the shape of one phase of the frame kernel at 256 / 1024,
+also with the first poll of each round delayed.
 
     python magenta-realtime-mlx-cpp_amd/profile_steps.py --timeline
 
@@ -92,6 +93,10 @@ def main() -> None:
                     us = mrt_df.handoff_latency(g, words, 2000)
                     print(f"[profile] all-gather {g:3d} workgroups x {words:4d} words: {us:.3f} us per round",
                           flush=True)
+        for delay in (4, 8, 12, 16, 20, 24, 32):
+            us = mrt_df.handoff_latency(256, 1024, 2000, delay)
+            print(f"[profile] all-gather 256 workgroups x 1024 words, first poll after {delay:2d} x 64 clocks: "
+                  f"{us:.3f} us per round", flush=True)
         return
 
     if a.read_sweep:
