@@ -436,6 +436,7 @@ void State::setup_persistent() {
   tstack_ = stack(m.tmp, true);
   dstack_ = stack(m.dep, false);
   if (const char* d = std::getenv("MRT_POLL_DELAY")) poll_delay_ = std::max(0, std::min(256, std::atoi(d)));
+  if (const char* q = std::getenv("MRT_QKV_TABLE")) qkv_table_on_ = std::string(q) != "0";
   if (std::getenv("MRT_TRACE_PHASES")) {
     d_trace_ = static_cast<uint64_t*>(dalloc(2 * kTraceSlots * sizeof(uint64_t)));
     MRT_HIP_CHECK(hipMemset(d_trace_, 0, 2 * kTraceSlots * sizeof(uint64_t)));
@@ -623,6 +624,7 @@ void State::launch_frame_p(const GenOpts& o, int f) {
   fa.levels = L;
   fa.rec_slices = o.record_slices ? o.record_slices + static_cast<size_t>(f) * L * rows * C : nullptr;
   fa.rec_temporal = o.record_temporal ? static_cast<char*>(o.record_temporal) + f * row_bytes : nullptr;
+  fa.qkv_table = qkv_table_;
   launch_frame(m.dt, fa, persist_grid_, lds_f_, stream);
 }
 
@@ -984,6 +986,49 @@ void State::reset_cache(int kind) {
     depth_len_ = 0;
 }
 
+const void* Model::depth_qkv_table(int codebook, int offset, hipStream_t s) {
+  const int L = cfg.rvq_depth, D = cfg.d_model, HD = cfg.hd();
+  if (L < 2 || cfg.num_depth_layers < 1) return nullptr;
+  MRT_REQUIRE(codebook >= 1 && offset >= 0 && offset + codebook * L <= cfg.vocab_size,
+              "depth q/k/v table: codec levels exceed the vocabulary");
+  std::lock_guard<std::mutex> lock(qkv_mu_);
+  for (const QkvTable& t : qkv_tables_)
+    if (t.codebook == codebook && t.offset == offset) return t.rows;
+  const int rows = (L - 1) * codebook;
+  std::vector<int> ids(static_cast<size_t>(rows));
+  for (int l = 0; l + 1 < L; ++l)
+    for (int c = 0; c < codebook; ++c) ids[static_cast<size_t>(l) * codebook + c] = offset + codebook * l + c;
+  MRT_HIP_CHECK(hipSetDevice(device));
+  void* out = nullptr;
+  void *x = nullptr, *xn = nullptr, *d_ids = nullptr;
+  auto release = [&]() {
+    if (x) (void)hipFree(x);
+    if (xn) (void)hipFree(xn);
+    if (d_ids) (void)hipFree(d_ids);
+  };
+  try {
+    MRT_HIP_CHECK(hipMalloc(&out, static_cast<size_t>(rows) * 3 * HD * esz));
+    allocs_.push_back(out);
+    MRT_HIP_CHECK(hipMalloc(&x, static_cast<size_t>(rows) * D * esz));
+    MRT_HIP_CHECK(hipMalloc(&xn, static_cast<size_t>(rows) * D * esz));
+    MRT_HIP_CHECK(hipMalloc(&d_ids, ids.size() * sizeof(int)));
+    MRT_HIP_CHECK(hipMemcpyAsync(d_ids, ids.data(), ids.size() * sizeof(int), hipMemcpyHostToDevice, s));
+    embed_rows(dt, emb, D, static_cast<const int*>(d_ids), rows, x, s);
+    rmsnorm_rows(dt, x, dep[0].norm_sa, 1e-6f, rows, D, xn, s);
+    GemmEpiArgs e;
+    e.kind = GemmEpi::Store;
+    e.C = out;
+    gemm(dt, xn, dep[0].wqkv, rows, 3 * HD, D, e, s);
+    MRT_HIP_CHECK(hipStreamSynchronize(s));
+  } catch (...) {
+    release();
+    throw;
+  }
+  release();
+  qkv_tables_.push_back(QkvTable{codebook, offset, out});
+  return out;
+}
+
 void Model::precompute_biases(int kind, int n, void* out) const {
   MRT_REQUIRE(kind == 0 || kind == 1, "precompute_biases: kind must be 0 (temporal) or 1 (depth)");
   MRT_REQUIRE(n >= 1 && n < kBucketTable, "precompute_biases: n out of range");
@@ -1149,6 +1194,8 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
     MRT_HIP_CHECK(hipEventCreate(&ev_dec_[1]));
   }
   dec_launches_ = persistent() ? decode_launches(o) : 0;
+  // built once per (codebook, offset) before any capture; waits for the stream then
+  qkv_table_ = frame_kernel_ && qkv_table_on_ ? m.depth_qkv_table(o.codebook, o.codec_offset, stream) : nullptr;
   hipGraphExec_t exec = o.use_graph ? decode_graph(o) : nullptr;
   {
     // persistent grids of other states on this device run before or after

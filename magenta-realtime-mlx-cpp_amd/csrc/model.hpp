@@ -8,6 +8,7 @@
 
 #include <memory>
 #include <string>
+#include <mutex>
 #include <vector>
 
 #include "common.hpp"
@@ -108,8 +109,23 @@ class Model {
   // (H, f + 1) block at element H f (f + 1) / 2).  Waits for the result.
   void precompute_biases(int kind, int n, void* out) const;
 
+  // The first depth layer's q | k | v of every token the decode feeds back at
+  // levels 1..rvq_depth-1: row ((l - 1) * codebook + c) is
+  // round(Wqkv0 . rmsnorm(emb(offset + codebook * (l - 1) + c))), 3 * HD
+  // model-dtype values -- the layer-0 projection of depth step l when its input
+  // is that token's embedding on both rows.  Built on first use for a
+  // (codebook, offset) pair, on `s` (waits for it; never during a capture), and
+  // kept until the model is destroyed.  nullptr when levels < 2.
+  const void* depth_qkv_table(int codebook, int offset, hipStream_t s);
+
  private:
   std::vector<void*> allocs_;
+  struct QkvTable {
+    int codebook, offset;
+    void* rows;
+  };
+  std::mutex qkv_mu_;
+  std::vector<QkvTable> qkv_tables_;
   const void* upload(const std::vector<float>& host);
   const void* upload_i32(const std::vector<int>& host);
 };
@@ -228,6 +244,8 @@ class State {
   uint64_t* h_seed_ = nullptr;  // pinned: the draw seed of a generate / sample call
   uint64_t* d_trace_ = nullptr; // 2 x kTraceSlots when MRT_TRACE_PHASES is set
   int poll_delay_ = 4;          // s_sleep(1) rounds before a hand-off's first poll (MRT_POLL_DELAY)
+  bool qkv_table_on_ = true;    // frame kernel: layer-0 q/k/v of fed tokens from the model's table (MRT_QKV_TABLE=0: off)
+  const void* qkv_table_ = nullptr;  // the table of the current generate call, or nullptr
   hipEvent_t ev_dec_[2] = {nullptr, nullptr};  // around the decode section of generate
   int dec_launches_ = 0;
   bool dec_timed_ = false;

@@ -135,6 +135,9 @@ struct FrameArgs {
   int codebook, levels;
   float* rec_slices;   // (levels, 2, codebook) copies of the logits, or nullptr
   void* rec_temporal;  // (2, D) copy of the temporal output, or nullptr
+  // Layer 0's q | k | v of every fed-back token (Model::depth_qkv_table for
+  // this codebook and codec offset), or nullptr: computed at every level.
+  const void* qkv_table;
 };
 // The frame kernel keeps the depth K/V history in LDS: it needs
 // depth layers * levels <= kMaxResidentSlots.

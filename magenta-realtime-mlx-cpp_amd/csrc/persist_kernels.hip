@@ -724,9 +724,14 @@ __device__ __forceinline__ float pv_sum(const float* p, const T* v, int n, float
 // written by this function at earlier steps of the same launch.  Slot pos is
 // written there too, so every key is read the same way.  `pbias`: lane j's
 // bias for key j (j <= pos) in waves 0 and 1, loaded ahead (attn_bias).
+// `qkv_row` non-null: q, k and v of both rows are that table row's (the
+// layer-0 projection of a known token), loaded instead of polled, and slot
+// pos of the global ring (`ring`: this layer's K, V at +eRing) is written here.
 template <typename T>
 __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, int h, uint32_t tag, uint32_t out_tag,
-                                                    T* hist, int cap, bool resident, float pbias, float* sm) {
+                                                    T* hist, int cap, bool resident, float pbias, float* sm,
+                                                    const T* qkv_row = nullptr, T* ring = nullptr,
+                                                    size_t eRing = 0) {
   using S = St<T>;
   constexpr int V = S::kVec;
   float* qs = sm;        // [2][64]
@@ -735,22 +740,34 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
   const int tid = threadIdx.x, wid = uniform(tid >> 6), lane = tid & 63;
   const int len = pos + 1, rs = cap * 64;
   if (wid < 3) {  // waves 0, 1, 2 fetch q, k, v of head h
-    const uint64_t* src = pick3<const uint64_t*>(wid, a.ll.q, a.ll.k, a.ll.v) + h * 64;
     float* d = sm + wid * 128;
-    constexpr int NW = LL<T>::kWords;
-    uint64_t w[NW];
-    uint32_t spins = 0;
-    poll_wait(a.ll.poll_delay);
-    for (;;) {
+    float v0, v1;
+    if (qkv_row != nullptr) {
+      const T e = ld_g(qkv_row + wid * a.HD + h * 64 + lane);
+      v0 = v1 = S::ld(e);
+      if (wid > 0) {  // the global ring slot of both rows (read by later launches)
+        T* slot = ring + (wid - 1) * eRing + ((size_t)h * a.Lmax + pos) * 64 + lane;
+        st_g(slot, e);
+        st_g(slot + (size_t)a.H * a.Lmax * 64, e);
+      }
+    } else {
+      const uint64_t* src = pick3<const uint64_t*>(wid, a.ll.q, a.ll.k, a.ll.v) + h * 64;
+      constexpr int NW = LL<T>::kWords;
+      uint64_t w[NW];
+      uint32_t spins = 0;
+      poll_wait(a.ll.poll_delay);
+      for (;;) {
 #pragma unroll
-      for (int r = 0; r < NW; ++r) w[r] = aload(src + LL<T>::idx(lane, r));
-      bool ok = true;
+        for (int r = 0; r < NW; ++r) w[r] = aload(src + LL<T>::idx(lane, r));
+        bool ok = true;
 #pragma unroll
-      for (int r = 0; r < NW; ++r) ok = ok && ll_tag(w[r]) == tag;
-      if (ok || spin_failed(spins, a.ll.err)) break;
-      __builtin_amdgcn_s_sleep(1);
+        for (int r = 0; r < NW; ++r) ok = ok && ll_tag(w[r]) == tag;
+        if (ok || spin_failed(spins, a.ll.err)) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      v0 = LL<T>::get(w, 0);
+      v1 = LL<T>::get(w, 1);
     }
-    const float v0 = LL<T>::get(w, 0), v1 = LL<T>::get(w, 1);
     if (wid == 0) {
       d[lane] = v0;
       d[64 + lane] = v1;
@@ -1199,6 +1216,8 @@ struct StackIO {
   int cap;               // LDS slots per (K|V, row) region
   int pos;               // ring slot written by this step
   uint64_t* trace;       // timeline of workgroup 0, or nullptr
+  const void* qkv_row;   // layer 0's q | k | v (3 HD model-dtype values, both rows), or nullptr: computed
+  bool qkv_ready;        // c.buf holds layer 0's first QKV batch (prefetch_qkv)
 };
 
 // Rows of wave `wid` for the QKV phase: local t = wid + 4i < 3*rps ->
@@ -1312,7 +1331,17 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
       }
     };
     if (CROSS && jpart != 0) stage_cross();
-    // ---- QKV of head h's slice (weights already in flight)
+    // ---- QKV of head h's slice (weights already in flight), unless layer 0's
+    // q/k/v come from a table row: the attention workgroups then read their
+    // head's slice there and the others go on to the output projection.
+    const bool tbl = first && io.qkv_row != nullptr;
+    if (tbl) {
+      MRT_TP;  // the QKV phase's four trace points, so a timeline keeps its layout
+      MRT_TP;
+      MRT_TP;
+      MRT_TP;
+    } else {
+    if (first && !io.qkv_ready) prefetch_qkv<T, NT>(c, a, 0);
     xs = c.next_xs();
     load_act<T, 4, true>(a.ll.x, in_plain, D, x_tag, c.gq, xs, red, no_side, r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp,
                          c.lcnt, in_stride);
@@ -1346,12 +1375,13 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
              (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32));
       }
     }
+    }  // QKV phase
     // Head h's attention in workgroup (h, 0), then the next phase's weights:
     // its polls would otherwise also wait for those loads.
     const T* wo = static_cast<const T*>(a.st.wo) + li * eO;
     if (jpart == 0) {
       self_attention_head<T>(a, io.pos, h, tag(base + kPhQKV), tag(base + kPhAtt), lhist, io.resident ? io.cap : 64,
-                             io.resident, pbias, sm);
+                             io.resident, pbias, sm, tbl ? static_cast<const T*>(io.qkv_row) : nullptr, ring_k, eRing);
       MRT_TP;
       if (CROSS) stage_cross();  // the history has been read (barrier above)
     }
@@ -1566,7 +1596,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     return;
   }
   if (a.trace != nullptr && c.blk == 0 && threadIdx.x == 0) a.trace[kTraceStart] = wall_clock64();
-  StackIO io{a.in, a.D, 0u, CROSS ? a.out : nullptr, !CROSS, 0, false, 64, a.pos, a.trace};
+  StackIO io{a.in, a.D, 0u, CROSS ? a.out : nullptr, !CROSS, 0, false, 64, a.pos, a.trace, nullptr, true};
   const uint32_t x_tag = run_stack<T, CROSS>(c, a, io);
   if constexpr (!CROSS) {
     const T* hw = static_cast<const T*>(a.head_w);
@@ -1601,7 +1631,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   if (!ok) return;
   if (at.trace != nullptr && c.blk == 0 && threadIdx.x == 0) at.trace[kTraceStart] = wall_clock64();
   // ---- temporal step
-  StackIO tio{at.in, at.D, 0u, fa.rec_temporal, true, 0, false, 64, at.pos, at.trace};
+  StackIO tio{at.in, at.D, 0u, fa.rec_temporal, true, 0, false, 64, at.pos, at.trace, nullptr, true};
   uint32_t x_tag = run_stack<T, true>(c, at, tio);
   if (at.trace != nullptr && c.blk == 0 && threadIdx.x == 0) at.trace[kTraceEnd] = at.trace[kTraceDone] = wall_clock64();
   // ---- depth steps
@@ -1623,10 +1653,16 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       if (trace != nullptr && c.blk == 0 && threadIdx.x == 0) trace[kTraceStart] = wall_clock64();
     }
     const int base = code0 + l * per_step;
-    StackIO io{nullptr, 0, x_tag, nullptr, true, base, true, L, l, trace};
+    StackIO io{nullptr, 0, x_tag, nullptr, true, base, true, L, l, trace, nullptr, true};
     if (l > 0) {
       io.in_plain = static_cast<const T*>(ad.emb) + (size_t)tok * D;  // both rows: emb(token)
       io.in_stride = 0;
+      // layer 0's q/k/v of the fed token from the table (no QKV weights were
+      // prefetched for it); a token outside level l - 1 takes the computed path
+      const int cb = tok - ad.sp.codec_offset - C * (l - 1);
+      io.qkv_ready = fa.qkv_table == nullptr;
+      if (fa.qkv_table != nullptr && cb >= 0 && cb < C)
+        io.qkv_row = static_cast<const T*>(fa.qkv_table) + ((size_t)(l - 1) * C + cb) * 3 * ad.HD;
     }
     x_tag = run_stack<T, false>(c, ad, io);
     const T* hw = static_cast<const T*>(ad.head_w) + (size_t)l * C * D;
@@ -1634,7 +1670,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     const uint32_t tg_logit = c.tag(base + 16 * ad.nlayers + kPhLogit);
     const uint32_t tg_tok = c.tag(base + 16 * ad.nlayers + kPhToken);
     run_head<T>(c, ad, hw, x_tag, tg_logit, trace);
-    if (c.blk != 0 && l + 1 < L) prefetch_qkv<T, false>(c, ad, 0);
+    if (c.blk != 0 && l + 1 < L && fa.qkv_table == nullptr) prefetch_qkv<T, false>(c, ad, 0);
     if (c.blk == 0) {
       // Nothing is loaded between the head and the gather: a wave's memory
       // operations retire in order, so the gather's polls would wait for them.
@@ -1644,7 +1680,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       float* lg = c.xsb[c.xsel ^ 1];
       gather_logits<T>(ad, tg_logit, lg, nullptr, fa.rec_slices ? fa.rec_slices + (size_t)l * 2 * C : nullptr);
       if (trace != nullptr && threadIdx.x == 0) trace[kTraceEnd] = wall_clock64();
-      if (l + 1 < L) prefetch_qkv<T, false>(c, ad, 0);  // lands during the draw
+      if (l + 1 < L && fa.qkv_table == nullptr) prefetch_qkv<T, false>(c, ad, 0);  // lands during the draw
       tok = sample_block<T>(ad.sp, l, slot, pf, ad.teacher != nullptr, ad.tokens, ad.drawn,
                             l + 1 < L ? ad.ll.tok : nullptr, tg_tok, lg, c.sel_hist, c.sel_res, trace);
       if (trace != nullptr && threadIdx.x == 0) trace[kTraceDone] = wall_clock64();
