@@ -533,8 +533,13 @@ def frame_handoffs(cfg, levels=16):
     """Dependent phase hand-offs in one frame-kernel launch: per temporal layer
     QKV -> attention -> O -> cross q -> cross partials -> cross combine -> cross O
     -> up -> down (9), per depth layer QKV -> attention -> O -> up -> down (5),
-    and per level the head logits and the drawn token (2)."""
-    return 9 * cfg.num_temporal_layers + levels * (5 * cfg.num_depth_layers + 2)
+    and per level the head logits and the drawn token (2).  With the layer-0
+    q/k/v table (the default; MRT_QKV_TABLE=0 turns it off) levels 1.. skip
+    layer 0's QKV hand-off."""
+    n = 9 * cfg.num_temporal_layers + levels * (5 * cfg.num_depth_layers + 2)
+    if os.environ.get("MRT_QKV_TABLE", "1") != "0":
+        n -= levels - 1
+    return n
 
 
 def handoff_probe(grid):
