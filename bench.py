@@ -655,7 +655,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30, help="timed chunks")
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16", "fp32"])
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
@@ -719,13 +719,13 @@ def main():
     total_s = time.perf_counter() - t_all
     ms = sorted(wall)
     mean_ms = float(np.mean(wall))
-    ab = algorithmic_bytes(cfg, esz=2 if args.dtype == "bf16" else 4)
+    ab = algorithmic_bytes(cfg, esz=4 if args.dtype == "fp32" else 2)
     gpu_mean = float(np.mean(gpu))
     achieved = ab["chunk"] / (gpu_mean * 1e-3) / 1e9
     print(f"[bench] chunk ms mean {mean_ms:.2f} p50 {percentile(ms, 50):.2f} p99 {percentile(ms, 99):.2f}; "
           f"gpu {gpu_mean:.2f} ms; {achieved:.0f} GB/s", file=sys.stderr, flush=True)
 
-    esz = 2 if args.dtype == "bf16" else 4
+    esz = 4 if args.dtype == "fp32" else 2
     frames = scfg.chunk_frames
     if launches == frames:  # one persistent launch per frame
         fb = float(np.mean([frame_bytes(cfg, f, esz=esz) for f in range(frames)]))

@@ -39,8 +39,10 @@ extern "C" {
 #define MRT_ERR_FORMAT 5      /* malformed bundle                       */
 #define MRT_ERR_INTERNAL 6
 
+/* Model storage dtypes: the reference's fp32 | bf16 | fp16 (dtype.cpp:35-49). */
 #define MRT_DTYPE_F32 0
 #define MRT_DTYPE_BF16 1
+#define MRT_DTYPE_F16 2
 
 /* DepthformerConfig (src/magenta_realtime_mlx/depthformer/model.h:47-68). */
 typedef struct mrt_df_config {

@@ -101,7 +101,8 @@ void from_config(const mrt::Config& k, mrt_df_config* c) {
 mrt::DType to_dtype(int d) {
   if (d == MRT_DTYPE_F32) return mrt::DType::F32;
   if (d == MRT_DTYPE_BF16) return mrt::DType::BF16;
-  throw mrt::Error(MRT_ERR_INVALID, "unknown dtype " + std::to_string(d) + "; expected fp32|bf16");
+  if (d == MRT_DTYPE_F16) return mrt::DType::F16;
+  throw mrt::Error(MRT_ERR_INVALID, "unknown dtype " + std::to_string(d) + "; expected fp32|fp16|bf16");
 }
 
 mrt::GenOpts to_opts(const mrt_gen_opts* opts) {
@@ -260,7 +261,7 @@ int mrt_df_get_config(const mrt_df* h, mrt_df_config* cfg, int* dtype) {
   return guarded([&] {
     if (!h || !h->model) throw mrt::Error(MRT_ERR_INVALID, "null model handle");
     if (cfg) from_config(h->model->cfg, cfg);
-    if (dtype) *dtype = h->model->dt == mrt::DType::F32 ? MRT_DTYPE_F32 : MRT_DTYPE_BF16;
+    if (dtype) *dtype = static_cast<int>(h->model->dt);
   });
 }
 

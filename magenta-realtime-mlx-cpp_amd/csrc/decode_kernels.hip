@@ -229,33 +229,20 @@ void launch_gemv_t(const void* W, int nout, int K, const void* X, int ldx, NormA
 
 void gemv_store(DType dt, int nb, const void* W, int N, int K, const void* X, int ldx,
                 NormArg norm, void* Y, int ldy, hipStream_t s) {
-  if (dt == DType::F32) {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 1>(W, N, K, X, ldx, norm,
-                                                     EpiStore<float, NB>{static_cast<float*>(Y), ldy}, s)));
-  } else {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 1>(W, N, K, X, ldx, norm,
-                                                    EpiStore<bf16, NB>{static_cast<bf16*>(Y), ldy}, s)));
-  }
+  MRT_DTYPE_DISPATCH(dt, MRT_NB_DISPATCH(nb, (launch_gemv_t<T, NB, 1>(W, N, K, X, ldx, norm,
+                                                                      EpiStore<T, NB>{static_cast<T*>(Y), ldy}, s))));
 }
 
 void gemv_f32(DType dt, int nb, const void* W, int N, int K, const void* X, int ldx,
               NormArg norm, float* Y, int ldy, hipStream_t s) {
-  if (dt == DType::F32) {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 1>(W, N, K, X, ldx, norm, EpiF32<float, NB>{Y, ldy}, s)));
-  } else {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 1>(W, N, K, X, ldx, norm, EpiF32<bf16, NB>{Y, ldy}, s)));
-  }
+  MRT_DTYPE_DISPATCH(dt, MRT_NB_DISPATCH(nb, (launch_gemv_t<T, NB, 1>(W, N, K, X, ldx, norm,
+                                                                      EpiF32<T, NB>{Y, ldy}, s))));
 }
 
 void gemv_resid(DType dt, int nb, const void* W, int N, int K, const void* X, int ldx,
                 NormArg norm, void* R, int ldr, hipStream_t s) {
-  if (dt == DType::F32) {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 1>(W, N, K, X, ldx, norm,
-                                                     EpiResid<float, NB>{static_cast<float*>(R), ldr}, s)));
-  } else {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 1>(W, N, K, X, ldx, norm,
-                                                    EpiResid<bf16, NB>{static_cast<bf16*>(R), ldr}, s)));
-  }
+  MRT_DTYPE_DISPATCH(dt, MRT_NB_DISPATCH(nb, (launch_gemv_t<T, NB, 1>(W, N, K, X, ldx, norm,
+                                                                      EpiResid<T, NB>{static_cast<T*>(R), ldr}, s))));
 }
 
 void gemv_qkv(DType dt, int nb, const void* W, int HD, int K, const void* X, int ldx,
@@ -263,31 +250,18 @@ void gemv_qkv(DType dt, int nb, const void* W, int HD, int K, const void* X, int
               hipStream_t s) {
   MRT_REQUIRE(HD == H * 64, "gemv_qkv: head dim must be 64");
   MRT_REQUIRE(pos >= 0 && pos < Lmax, "gemv_qkv: ring position out of range");
-  if (dt == DType::F32) {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 1>(
-                            W, 3 * HD, K, X, ldx, norm,
-                            EpiQKV<float, NB>{static_cast<float*>(Q), static_cast<float*>(Kc),
-                                              static_cast<float*>(Vc), HD, H, Lmax, pos},
-                            s)));
-  } else {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 1>(
-                            W, 3 * HD, K, X, ldx, norm,
-                            EpiQKV<bf16, NB>{static_cast<bf16*>(Q), static_cast<bf16*>(Kc),
-                                             static_cast<bf16*>(Vc), HD, H, Lmax, pos},
-                            s)));
-  }
+  MRT_DTYPE_DISPATCH(dt, MRT_NB_DISPATCH(nb, (launch_gemv_t<T, NB, 1>(
+                                                 W, 3 * HD, K, X, ldx, norm,
+                                                 EpiQKV<T, NB>{static_cast<T*>(Q), static_cast<T*>(Kc),
+                                                               static_cast<T*>(Vc), HD, H, Lmax, pos},
+                                                 s))));
 }
 
 void gemv_geglu(DType dt, int nb, const void* W01, int F, int K, const void* X, int ldx,
                 NormArg norm, void* Hout, int ldh, hipStream_t s) {
   MRT_REQUIRE(F % 32 == 0, "gemv_geglu: d_ff must be a multiple of 32");
-  if (dt == DType::F32) {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<float, NB, 2>(W01, F, K, X, ldx, norm,
-                                                     EpiGeglu<float, NB>{static_cast<float*>(Hout), ldh}, s)));
-  } else {
-    MRT_NB_DISPATCH(nb, (launch_gemv_t<bf16, NB, 2>(W01, F, K, X, ldx, norm,
-                                                    EpiGeglu<bf16, NB>{static_cast<bf16*>(Hout), ldh}, s)));
-  }
+  MRT_DTYPE_DISPATCH(dt, MRT_NB_DISPATCH(nb, (launch_gemv_t<T, NB, 2>(W01, F, K, X, ldx, norm,
+                                                                      EpiGeglu<T, NB>{static_cast<T*>(Hout), ldh}, s))));
 }
 
 // ---- self-attention over the ring KV ----------------------------------------------
@@ -500,14 +474,9 @@ void self_attn_at(DType dt, int nb, const void* Q, const void* Kc, const void* V
               "self_attn: positions exceed the ring");
   MRT_REQUIRE(bias_row == nullptr || (qpos_ptr == nullptr && pos_rows == 0),
               "self_attn: an explicit bias needs a host-known query position");
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_self_attn<float>, dim3(nb * H), dim3(64), 0, s, (const float*)Q,
-                       (const float*)Kc, (const float*)Vc, H, Lmax, len, qpos, qpos_ptr, pos_rows,
-                       (const float*)bias_tab, buckets, (const float*)bias_row, (float*)out);
-  else
-    hipLaunchKernelGGL(k_self_attn<bf16>, dim3(nb * H), dim3(64), 0, s, (const bf16*)Q,
-                       (const bf16*)Kc, (const bf16*)Vc, H, Lmax, len, qpos, qpos_ptr, pos_rows,
-                       (const bf16*)bias_tab, buckets, (const bf16*)bias_row, (bf16*)out);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_self_attn<T>, dim3(nb * H), dim3(64), 0, s, (const T*)Q, (const T*)Kc,
+                                            (const T*)Vc, H, Lmax, len, qpos, qpos_ptr, pos_rows,
+                                            (const T*)bias_tab, buckets, (const T*)bias_row, (T*)out));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
@@ -530,22 +499,17 @@ __global__ void k_bias_rows(const T* __restrict__ table, const int* __restrict__
 
 void bias_rows(DType dt, const void* table, const int* buckets, int H, int n, void* out, hipStream_t s) {
   MRT_REQUIRE(n >= 1 && H >= 1, "bias_rows: empty request");
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_bias_rows<float>, dim3(n), dim3(256), 0, s, (const float*)table, buckets, H, n, (float*)out);
-  else
-    hipLaunchKernelGGL(k_bias_rows<bf16>, dim3(n), dim3(256), 0, s, (const bf16*)table, buckets, H, n, (bf16*)out);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_bias_rows<T>, dim3(n), dim3(256), 0, s, (const T*)table, buckets, H, n,
+                                            (T*)out));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
 void full_attn(DType dt, int nb, int K, int H, const void* qkv, const void* explicit_bias, const void* bias_tab,
                const int* buckets, bool causal, void* out, hipStream_t s) {
   MRT_REQUIRE(nb >= 1 && K >= 1 && K <= 64, "full_attn: K must be in [1, 64]");
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_full_attn<float>, dim3(nb * K * H), dim3(64), 0, s, (const float*)qkv, K, H,
-                       (const float*)explicit_bias, (const float*)bias_tab, buckets, causal ? 1 : 0, (float*)out);
-  else
-    hipLaunchKernelGGL(k_full_attn<bf16>, dim3(nb * K * H), dim3(64), 0, s, (const bf16*)qkv, K, H,
-                       (const bf16*)explicit_bias, (const bf16*)bias_tab, buckets, causal ? 1 : 0, (bf16*)out);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_full_attn<T>, dim3(nb * K * H), dim3(64), 0, s, (const T*)qkv, K, H,
+                                            (const T*)explicit_bias, (const T*)bias_tab, buckets, causal ? 1 : 0,
+                                            (T*)out));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
@@ -558,29 +522,19 @@ void cross_attn(DType dt, int nb, const void* Q, const void* Kc, const void* Vc,
                 void* out, float* part, int nsplit, hipStream_t s) {
   MRT_REQUIRE(S >= 1, "cross_attn: empty encoder output");
   MRT_REQUIRE((S + nsplit - 1) / nsplit <= kMaxCrossChunk, "cross_attn: key block too large");
-  if (dt == DType::F32) {
-    hipLaunchKernelGGL(k_cross_part<float>, dim3(nb * H * nsplit), dim3(64), 0, s, (const float*)Q,
-                       (const float*)Kc, (const float*)Vc, H, S, nsplit, part);
-    hipLaunchKernelGGL(k_cross_combine<float>, dim3(nb * H), dim3(64), 0, s, part, H, nsplit,
-                       (float*)out);
-  } else {
-    hipLaunchKernelGGL(k_cross_part<bf16>, dim3(nb * H * nsplit), dim3(64), 0, s, (const bf16*)Q,
-                       (const bf16*)Kc, (const bf16*)Vc, H, S, nsplit, part);
-    hipLaunchKernelGGL(k_cross_combine<bf16>, dim3(nb * H), dim3(64), 0, s, part, H, nsplit,
-                       (bf16*)out);
-  }
+  MRT_DTYPE_DISPATCH(dt, {
+    hipLaunchKernelGGL(k_cross_part<T>, dim3(nb * H * nsplit), dim3(64), 0, s, (const T*)Q, (const T*)Kc,
+                       (const T*)Vc, H, S, nsplit, part);
+    hipLaunchKernelGGL(k_cross_combine<T>, dim3(nb * H), dim3(64), 0, s, part, H, nsplit, (T*)out);
+  });
   MRT_HIP_CHECK(hipGetLastError());
 }
 
 void embed_rows(DType dt, const void* emb, int D, const int* ids, int rows, void* out,
                 hipStream_t s) {
   if (rows <= 0) return;
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_embed_rows<float>, dim3(rows), dim3(256), 0, s, (const float*)emb, D, ids,
-                       (float*)out);
-  else
-    hipLaunchKernelGGL(k_embed_rows<bf16>, dim3(rows), dim3(256), 0, s, (const bf16*)emb, D, ids,
-                       (bf16*)out);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_embed_rows<T>, dim3(rows), dim3(256), 0, s, (const T*)emb, D, ids,
+                                            (T*)out));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
@@ -601,12 +555,8 @@ void copy_dev(void* dst, const void* src, size_t bytes, hipStream_t s) {
 }
 
 void embed_fill(DType dt, const void* emb, int D, int id, int rows, void* out, hipStream_t s) {
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_embed_fill<float>, dim3(rows), dim3(256), 0, s, (const float*)emb, D, id,
-                       (float*)out);
-  else
-    hipLaunchKernelGGL(k_embed_fill<bf16>, dim3(rows), dim3(256), 0, s, (const bf16*)emb, D, id,
-                       (bf16*)out);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_embed_fill<T>, dim3(rows), dim3(256), 0, s, (const T*)emb, D, id,
+                                            (T*)out));
   MRT_HIP_CHECK(hipGetLastError());
 }
 

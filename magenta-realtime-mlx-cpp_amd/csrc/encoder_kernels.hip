@@ -3,9 +3,9 @@
 // temporal layer (modules.cpp:448-455) as one wide GEMM.
 //
 // GEMM operands are both K-contiguous ("NT": activations (M, K) row-major,
-// weights (N, K) row-major as the bundle stores them).  bf16 uses
-// v_mfma_f32_32x32x16_bf16 with a 128x128x64 LDS-double-buffered tile; fp32
-// uses a VALU tile (parity mode).
+// weights (N, K) row-major as the bundle stores them).  bf16 and fp16 use
+// v_mfma_f32_32x32x16_{bf16,f16} with LDS-double-buffered tiles; fp32 uses a
+// VALU tile (parity mode).
 #include <cmath>
 
 #include "device_utils.hpp"
@@ -107,7 +107,7 @@ struct GemmOut {
   }
 };
 
-// ---- VALU tiled GEMM (fp32 parity path; also a bf16 fallback) ---------------------
+// ---- VALU tiled GEMM (fp32 parity path; also the 16-bit fallback) -----------------
 // 64x64 tile, BK 16, 256 threads, 4x4 outputs per thread at rows ty+16i and
 // columns tx+16j, so columns j and j+2 form a packed gate/up pair.
 template <typename T>
@@ -159,13 +159,31 @@ __global__ __launch_bounds__(256) void k_gemm_valu(const T* __restrict__ A, cons
   }
 }
 
-// ---- bf16 MFMA GEMM ------------------------------------------------------------------
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+// ---- 16-bit MFMA GEMM ----------------------------------------------------------------
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+
+// The 32x32x16 matrix instruction of each 16-bit storage type (fp32 accumulators).
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static f32x16_t mma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<f16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static f32x16_t mma(v8 a, v8 b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
 
 constexpr int kBN = 128, kBK = 64, kStages = 2;
 
-// LDS rows of a tile are 64 bf16 = 8 chunks of 16 bytes; chunk c of row r is
+// LDS rows of a tile are 64 elements = 8 chunks of 16 bytes; chunk c of row r is
 // stored at chunk c ^ swz(r), so the 32 rows x 2 chunks of an MFMA fragment
 // read (and 16 consecutive lanes of any ds_read_b128) fall in distinct banks.
 __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
@@ -173,7 +191,7 @@ __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
 // s_waitcnt immediate waiting for vmcnt <= n (expcnt and lgkmcnt left alone).
 constexpr int vm_wait_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
-// C = A B^T (A (M, K), B (N, K) bf16, fp32 accumulation) with the GemmOut
+// C = A B^T (A (M, K), B (N, K) 16-bit, fp32 accumulation) with the GemmOut
 // epilogue.  Tile BM x 128 x 64, 4 waves in a 2x2 grid (wave tile BM/2 x 64 =
 // (BM/64) x 2 MFMA 32x32x16 tiles).  Tiles stream global -> LDS with direct
 // 16-byte loads (global_load_lds) through a kStages-deep ring: tile
@@ -182,12 +200,13 @@ constexpr int vm_wait_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 <<
 // barrier.  Two stages (64 / 48 KB of LDS) leave room for 2-3 blocks per CU,
 // which hides more latency than a deeper ring in one block (measured).  Rows
 // past M read row M - 1 (their results are not stored).
-// Operand fragments of v_mfma_f32_32x32x16_bf16: lane l holds row (l % 32)
+// Operand fragments of v_mfma_f32_32x32x16_{bf16,f16}: lane l holds row (l % 32)
 // and k = 8*(l / 32) .. +7 of both A (32x16) and B^T (32x16); the 16
 // accumulators of lane l hold column l % 32, rows 8*(r/4) + 4*(l/32) + r%4.
-template <int BM>
-__global__ __launch_bounds__(256) void k_gemm_mfma(const bf16* __restrict__ A, const bf16* __restrict__ B,
-                                                   int M, int N, int K, GemmOut<bf16> out) {
+template <typename T, int BM>
+__global__ __launch_bounds__(256) void k_gemm_mfma(const T* __restrict__ A, const T* __restrict__ B,
+                                                   int M, int N, int K, GemmOut<T> out) {
+  typedef typename Mfma<T>::v8 v8;
   constexpr int MI = BM / 64;                        // MFMA tiles per wave in M
   constexpr int kStageBytes = (BM + kBN) * 128;      // A rows then B rows, 128 bytes each
   constexpr int LA = BM / 32 + kBN / 32;             // load instructions per wave per tile
@@ -207,14 +226,14 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const bf16* __restrict__ A, c
     for (int q = 0; q < BM / 32; ++q) {
       const int r = wid * (BM / 4) + q * 8 + r8;
       const int gm = min(m0 + r, M - 1);
-      const bf16* src = A + (size_t)gm * K + ktc * kBK + ((p ^ swz(r)) << 3);
+      const T* src = A + (size_t)gm * K + ktc * kBK + ((p ^ swz(r)) << 3);
       __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)src,
                                        (MRT_LDS void*)(st + (wid * (BM / 4) + q * 8) * 128), 16, 0, 0);
     }
 #pragma unroll
     for (int q = 0; q < kBN / 32; ++q) {
       const int r = wid * (kBN / 4) + q * 8 + r8;
-      const bf16* src = B + (size_t)(n0 + r) * K + ktc * kBK + ((p ^ swz(r)) << 3);
+      const T* src = B + (size_t)(n0 + r) * K + ktc * kBK + ((p ^ swz(r)) << 3);
       __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)src,
                                        (MRT_LDS void*)(st + BM * 128 + (wid * (kBN / 4) + q * 8) * 128), 16, 0, 0);
     }
@@ -239,22 +258,22 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const bf16* __restrict__ A, c
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       const int c = 2 * ks + lh;
-      bf16x8_t a[MI], b[2];
+      v8 a[MI], b[2];
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int r = wm * (BM / 2) + i * 32 + lr;
-        a[i] = *reinterpret_cast<const bf16x8_t*>(st + r * 128 + ((c ^ swz(r)) << 4));
+        a[i] = *reinterpret_cast<const v8*>(st + r * 128 + ((c ^ swz(r)) << 4));
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int r = wn * 64 + j * 32 + lr;
-        b[j] = *reinterpret_cast<const bf16x8_t*>(st + BM * 128 + r * 128 + ((c ^ swz(r)) << 4));
+        b[j] = *reinterpret_cast<const v8*>(st + BM * 128 + r * 128 + ((c ^ swz(r)) << 4));
       }
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = Mfma<T>::mma(a[i], b[j], acc[i][j]);
     }
   }
   __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));  // no copy into LDS outlives the block
@@ -282,16 +301,16 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const bf16* __restrict__ A, c
   }
 }
 
-template <int BM>
-void launch_gemm_mfma(const bf16* A, const bf16* B, int M, int N, int K, const GemmOut<bf16>& out, hipStream_t s) {
+template <typename T, int BM>
+void launch_gemm_mfma(const T* A, const T* B, int M, int N, int K, const GemmOut<T>& out, hipStream_t s) {
   constexpr size_t lds = (size_t)kStages * (BM + kBN) * 128;
   static bool allowed = false;  // dynamic LDS above 64 KB needs an explicit allowance
   if (!allowed) {
-    MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mfma<BM>),
+    MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mfma<T, BM>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     allowed = true;
   }
-  hipLaunchKernelGGL((k_gemm_mfma<BM>), dim3(N / kBN, (M + BM - 1) / BM), dim3(256), lds, s, A, B, M, N, K, out);
+  hipLaunchKernelGGL((k_gemm_mfma<T, BM>), dim3(N / kBN, (M + BM - 1) / BM), dim3(256), lds, s, A, B, M, N, K, out);
 }
 
 // Large-M GEMM (the encoder of several streams): 256 x 256 x 64 tiles, 16
@@ -302,10 +321,12 @@ void launch_gemm_mfma(const bf16* A, const bf16* B, int M, int N, int K, const G
 // M read row M - 1 (not stored); N % 256 == 0.
 constexpr int kGB = 256;                 // block tile, M and N
 constexpr int kGBWaves = 16;
-constexpr int kGBStage = 2 * kGB * 128;  // A rows then B rows, 128 bytes (64 bf16) each
+constexpr int kGBStage = 2 * kGB * 128;  // A rows then B rows, 128 bytes (64 elements) each
 
-__global__ __launch_bounds__(64 * kGBWaves) void k_gemm_big(const bf16* __restrict__ A, const bf16* __restrict__ B,
-                                                            int M, int N, int K, GemmOut<bf16> out) {
+template <typename T>
+__global__ __launch_bounds__(64 * kGBWaves) void k_gemm_big(const T* __restrict__ A, const T* __restrict__ B,
+                                                            int M, int N, int K, GemmOut<T> out) {
+  typedef typename Mfma<T>::v8 v8;
   constexpr int RW = kGB / kGBWaves;  // rows of A (and of B) each wave loads per stage
   constexpr int LA = 2 * RW / 8;      // load instructions per wave per stage (8 rows each)
   extern __shared__ __align__(16) unsigned char lds[];
@@ -322,14 +343,14 @@ __global__ __launch_bounds__(64 * kGBWaves) void k_gemm_big(const bf16* __restri
     for (int q = 0; q < RW / 8; ++q) {
       const int r = wid * RW + q * 8 + r8;
       const int gm = min(m0 + r, M - 1);
-      const bf16* src = A + (size_t)gm * K + ktc * kBK + ((p ^ swz(r)) << 3);
+      const T* src = A + (size_t)gm * K + ktc * kBK + ((p ^ swz(r)) << 3);
       __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)src, (MRT_LDS void*)(st + (wid * RW + q * 8) * 128),
                                        16, 0, 0);
     }
 #pragma unroll
     for (int q = 0; q < RW / 8; ++q) {
       const int r = wid * RW + q * 8 + r8;
-      const bf16* src = B + (size_t)(n0 + r) * K + ktc * kBK + ((p ^ swz(r)) << 3);
+      const T* src = B + (size_t)(n0 + r) * K + ktc * kBK + ((p ^ swz(r)) << 3);
       __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)src,
                                        (MRT_LDS void*)(st + kGB * 128 + (wid * RW + q * 8) * 128), 16, 0, 0);
     }
@@ -354,22 +375,22 @@ __global__ __launch_bounds__(64 * kGBWaves) void k_gemm_big(const bf16* __restri
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       const int c = 2 * ks + lh;
-      bf16x8_t a[2], b[2];
+      v8 a[2], b[2];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int r = wm * 64 + i * 32 + lr;
-        a[i] = *reinterpret_cast<const bf16x8_t*>(st + r * 128 + ((c ^ swz(r)) << 4));
+        a[i] = *reinterpret_cast<const v8*>(st + r * 128 + ((c ^ swz(r)) << 4));
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int r = wn * 64 + j * 32 + lr;
-        b[j] = *reinterpret_cast<const bf16x8_t*>(st + kGB * 128 + r * 128 + ((c ^ swz(r)) << 4));
+        b[j] = *reinterpret_cast<const v8*>(st + kGB * 128 + r * 128 + ((c ^ swz(r)) << 4));
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = Mfma<T>::mma(a[i], b[j], acc[i][j]);
     }
   }
   __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));  // no copy into LDS outlives the block
@@ -397,15 +418,16 @@ __global__ __launch_bounds__(64 * kGBWaves) void k_gemm_big(const bf16* __restri
   }
 }
 
-void launch_gemm_big(const bf16* A, const bf16* B, int M, int N, int K, const GemmOut<bf16>& out, hipStream_t s) {
+template <typename T>
+void launch_gemm_big(const T* A, const T* B, int M, int N, int K, const GemmOut<T>& out, hipStream_t s) {
   constexpr size_t lds = (size_t)kStages * kGBStage;
   static bool allowed = false;  // dynamic LDS above 64 KB needs an explicit allowance
   if (!allowed) {
-    MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_big),
+    MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_big<T>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     allowed = true;
   }
-  hipLaunchKernelGGL(k_gemm_big, dim3(N / kGB, (M + kGB - 1) / kGB), dim3(64 * kGBWaves), lds, s, A, B, M, N, K, out);
+  hipLaunchKernelGGL(k_gemm_big<T>, dim3(N / kGB, (M + kGB - 1) / kGB), dim3(64 * kGBWaves), lds, s, A, B, M, N, K, out);
 }
 
 // ---- encoder self-attention (bidirectional, no mask, no bias, scale 1.0) -------------
@@ -469,38 +491,40 @@ __global__ __launch_bounds__(64) void k_enc_attn(const T* __restrict__ qkv, int 
   }
 }
 
-// ---- bf16 encoder self-attention on MFMA --------------------------------------------
+// ---- 16-bit encoder self-attention on MFMA ------------------------------------------
 // Flash attention for one (row, head) and 128 queries per workgroup (32 per
 // wave), keys in tiles of 64 staged in LDS.  Scores are computed transposed,
-// S^T = K Q^T (v_mfma_f32_32x32x16_bf16), so lane l owns query l % 32 and
+// S^T = K Q^T (v_mfma_f32_32x32x16_{bf16,f16}), so lane l owns query l % 32 and
 // the online-softmax rescale is per lane.  The output is also accumulated
 // transposed, O^T += V^T P^T, with P^T taken straight from the score
 // accumulators: lane l's accumulators of a 16-key step hold keys
 // {4h..4h+3, 8+4h..8+4h+3} (h = l / 32), so V^T is staged with the key order
 // inside every 16-key block permuted the same way (swap of key bits 2 and 3).
 // Scores and the softmax are fp32; P enters the second product as the sum of
-// two bf16 parts (hi + lo, ~16 significant bits), as close to the fp32
-// probabilities of the reference's fused attention as bf16 MFMA allows.
+// two parts in the storage type (hi + lo: ~16 significant bits for bf16, ~22
+// for fp16), as close to the fp32 probabilities of the reference's fused
+// attention as 16-bit MFMA allows.
 constexpr int kAQ = 128, kAK = 64, kALD = 64 + 8;  // queries, keys per tile, padded LDS row
-typedef float f32x8_t __attribute__((ext_vector_type(8)));
 
-__global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ qkv, int S, int H,
-                                                       bf16* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) bf16 Ks[2][kAK * kALD];
-  __shared__ __attribute__((aligned(16))) bf16 Vt[2][64 * kALD];
+template <typename T>
+__global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv, int S, int H,
+                                                       T* __restrict__ out) {
+  typedef typename Mfma<T>::v8 v8;
+  __shared__ __attribute__((aligned(16))) T Ks[2][kAK * kALD];
+  __shared__ __attribute__((aligned(16))) T Vt[2][64 * kALD];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int bh = blockIdx.y, b = bh / H, h = bh - b * H;
   const int HD = H * 64, ld = 3 * HD;
-  const bf16* base = qkv + (size_t)b * S * ld + h * 64;
+  const T* base = qkv + (size_t)b * S * ld + h * 64;
   const int lq = lane & 31, hf = lane >> 5;
   const int q = blockIdx.x * kAQ + wid * 32 + lq;
 
   // Q^T fragments (B operand): lane l holds Q[q][16 s + 8 hf .. +7].
-  bf16x8_t qf[4];
+  v8 qf[4];
   {
-    const bf16* qr = base + (size_t)min(q, S - 1) * ld;
+    const T* qr = base + (size_t)min(q, S - 1) * ld;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const bf16x8_t*>(qr + 16 * s + 8 * hf);
+    for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const v8*>(qr + 16 * s + 8 * hf);
   }
   // Tile staging: thread t moves 16 bytes of K and of V for keys t/8 and
   // 32 + t/8, dims 8 (t % 8) .. +7.
@@ -510,7 +534,7 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
     for (int i = 0; i < 2; ++i) {
       const int key = kb + (tid >> 3) + 32 * i, c = (tid & 7) * 8;
       if (key < S) {
-        const bf16* row = base + (size_t)key * ld;
+        const T* row = base + (size_t)key * ld;
         rk[i] = *reinterpret_cast<const uint4*>(row + HD + c);
         rv[i] = *reinterpret_cast<const uint4*>(row + 2 * HD + c);
       } else {
@@ -525,7 +549,7 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
       const int key = (tid >> 3) + 32 * i, c = (tid & 7) * 8;
       *reinterpret_cast<uint4*>(&Ks[buf][key * kALD + c]) = rk[i];
       const int slot = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
-      const bf16* v = reinterpret_cast<const bf16*>(&rv[i]);
+      const T* v = reinterpret_cast<const T*>(&rv[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) Vt[buf][(c + e) * kALD + slot] = v[e];
     }
@@ -553,8 +577,8 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
       for (int r = 0; r < 16; ++r) sc[t][r] = 0.f;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&Ks[cur][(32 * t + lq) * kALD + 16 * s + 8 * hf]);
-        sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[s], sc[t], 0, 0, 0);
+        const v8 a = *reinterpret_cast<const v8*>(&Ks[cur][(32 * t + lq) * kALD + 16 * s + 8 * hf]);
+        sc[t] = Mfma<T>::mma(a, qf[s], sc[t]);
       }
     }
     float mt = -INFINITY;
@@ -570,7 +594,7 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
     const float mn = fmaxf(m, mt);
     const float corr = expf(m - mn);
     float ps = 0.f;
-    bf16x8_t pb[4], pl[4];  // P^T = hi + lo (bf16 each) for the four 16-key steps
+    v8 pb[4], pl[4];  // P^T = hi + lo (storage type each) for the four 16-key steps
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       f32x8_t pv;
@@ -579,8 +603,8 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
         pv[i] = expf(sc[g >> 1][8 * (g & 1) + i] - mn);
         ps += pv[i];
       }
-      pb[g] = __builtin_convertvector(pv, bf16x8_t);  // packed round-to-nearest-even conversions
-      pl[g] = __builtin_convertvector(pv - __builtin_convertvector(pb[g], f32x8_t), bf16x8_t);
+      pb[g] = __builtin_convertvector(pv, v8);  // round-to-nearest-even conversions
+      pl[g] = __builtin_convertvector(pv - __builtin_convertvector(pb[g], f32x8_t), v8);
     }
     ps += __shfl_xor(ps, 32, 64);
     lsum = lsum * corr + ps;
@@ -593,15 +617,15 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&Vt[cur][(32 * t + lq) * kALD + 16 * s + 8 * hf]);
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[s], acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pl[s], acc[t], 0, 0, 0);
+        const v8 a = *reinterpret_cast<const v8*>(&Vt[cur][(32 * t + lq) * kALD + 16 * s + 8 * hf]);
+        acc[t] = Mfma<T>::mma(a, pb[s], acc[t]);
+        acc[t] = Mfma<T>::mma(a, pl[s], acc[t]);
       }
     if (j + 1 < ntiles) sstore(cur ^ 1);
     __syncthreads();
   }
   if (q < S) {
-    bf16* orow = out + ((size_t)b * S + q) * HD + h * 64;
+    T* orow = out + ((size_t)b * S + q) * HD + h * 64;
     const float inv = 1.0f / lsum;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -609,8 +633,8 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
       for (int g = 0; g < 4; ++g) {
         const int d = 32 * t + 8 * g + 4 * hf;
         uint2 w;
-        w.x = (uint32_t)f2bf(acc[t][4 * g] * inv) | ((uint32_t)f2bf(acc[t][4 * g + 1] * inv) << 16);
-        w.y = (uint32_t)f2bf(acc[t][4 * g + 2] * inv) | ((uint32_t)f2bf(acc[t][4 * g + 3] * inv) << 16);
+        w.x = St<T>::bits(acc[t][4 * g] * inv) | (St<T>::bits(acc[t][4 * g + 1] * inv) << 16);
+        w.y = St<T>::bits(acc[t][4 * g + 2] * inv) | (St<T>::bits(acc[t][4 * g + 3] * inv) << 16);
         *reinterpret_cast<uint2*>(orow + d) = w;
       }
   }
@@ -620,26 +644,43 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const bf16* __restrict__ 
 
 void encoder_embed(DType dt, const void* emb, const void* pe, const int* tok, int M, int S, int D,
                    void* x, hipStream_t s) {
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_encoder_embed<float>, dim3(M), dim3(256), 0, s, (const float*)emb,
-                       (const float*)pe, tok, S, D, (float*)x);
-  else
-    hipLaunchKernelGGL(k_encoder_embed<bf16>, dim3(M), dim3(256), 0, s, (const bf16*)emb,
-                       (const bf16*)pe, tok, S, D, (bf16*)x);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_encoder_embed<T>, dim3(M), dim3(256), 0, s, (const T*)emb,
+                                            (const T*)pe, tok, S, D, (T*)x));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
 void rmsnorm_rows(DType dt, const void* x, const void* g, float eps, int M, int D, void* y,
                   hipStream_t s) {
   const bool reg = D <= 256 * kNormPer;
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(reg ? k_rmsnorm_rows_reg<float> : k_rmsnorm_rows<float>, dim3(M), dim3(256), 0, s,
-                       (const float*)x, (const float*)g, eps, D, (float*)y);
-  else
-    hipLaunchKernelGGL(reg ? k_rmsnorm_rows_reg<bf16> : k_rmsnorm_rows<bf16>, dim3(M), dim3(256), 0, s,
-                       (const bf16*)x, (const bf16*)g, eps, D, (bf16*)y);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(reg ? k_rmsnorm_rows_reg<T> : k_rmsnorm_rows<T>, dim3(M), dim3(256), 0,
+                                            s, (const T*)x, (const T*)g, eps, D, (T*)y));
   MRT_HIP_CHECK(hipGetLastError());
 }
+
+namespace {
+
+template <typename T>
+void gemm_t(const T* A, const T* B, int M, int N, int K, const GemmEpiArgs& e, hipStream_t s, bool allow_mfma) {
+  GemmOut<T> out{e, N};
+  if constexpr (sizeof(T) == 2) {
+    if (allow_mfma && N % kBN == 0 && K % kBK == 0) {
+      // 256 x 256 tiles for outputs up to 4096 wide when they still give >= 2
+      // tiles per CU of a 256-CU part (measured: faster there, slower for the
+      // 5632- and 40960-wide outputs, where 2-3 smaller blocks per CU hide more
+      // latency); 128-row tiles when those give >= 1.5 tiles per CU, else 64-row
+      if (N % kGB == 0 && N <= 4096 && (long)((M + kGB - 1) / kGB) * (N / kGB) >= 512)
+        launch_gemm_big<T>(A, B, M, N, K, out, s);
+      else if ((long)((M + 127) / 128) * (N / kBN) >= 384)
+        launch_gemm_mfma<T, 128>(A, B, M, N, K, out, s);
+      else
+        launch_gemm_mfma<T, 64>(A, B, M, N, K, out, s);
+      return;
+    }
+  }
+  hipLaunchKernelGGL(k_gemm_valu<T>, dim3((N + 63) / 64, (M + 63) / 64), dim3(256), 0, s, A, B, M, N, K, out);
+}
+
+}  // namespace
 
 void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const GemmEpiArgs& e,
           hipStream_t s, bool allow_mfma) {
@@ -647,41 +688,27 @@ void gemm(DType dt, const void* A, const void* B, int M, int N, int K, const Gem
   if (e.kind == GemmEpi::Geglu) MRT_REQUIRE(N % 64 == 0, "gemm: gated-GELU needs N % 64 == 0");
   if (e.kind == GemmEpi::CrossKV)
     MRT_REQUIRE(e.HD == e.H * 64 && N % e.HD == 0 && M == e.nb * e.S, "gemm: bad cross-KV shape");
-  if (dt == DType::BF16 && allow_mfma && N % kBN == 0 && K % kBK == 0) {
-    GemmOut<bf16> out{e, N};
-    // 256 x 256 tiles for outputs up to 4096 wide when they still give >= 2
-    // tiles per CU of a 256-CU part (measured: faster there, slower for the
-    // 5632- and 40960-wide outputs, where 2-3 smaller blocks per CU hide more
-    // latency); 128-row tiles when those give >= 1.5 tiles per CU, else 64-row
-    if (N % kGB == 0 && N <= 4096 && (long)((M + kGB - 1) / kGB) * (N / kGB) >= 512)
-      launch_gemm_big((const bf16*)A, (const bf16*)B, M, N, K, out, s);
-    else if ((long)((M + 127) / 128) * (N / kBN) >= 384)
-      launch_gemm_mfma<128>((const bf16*)A, (const bf16*)B, M, N, K, out, s);
-    else
-      launch_gemm_mfma<64>((const bf16*)A, (const bf16*)B, M, N, K, out, s);
-  } else if (dt == DType::BF16) {
-    GemmOut<bf16> out{e, N};
-    hipLaunchKernelGGL(k_gemm_valu<bf16>, dim3((N + 63) / 64, (M + 63) / 64), dim3(256), 0, s,
-                       (const bf16*)A, (const bf16*)B, M, N, K, out);
-  } else {
-    GemmOut<float> out{e, N};
-    hipLaunchKernelGGL(k_gemm_valu<float>, dim3((N + 63) / 64, (M + 63) / 64), dim3(256), 0, s,
-                       (const float*)A, (const float*)B, M, N, K, out);
-  }
+  MRT_DTYPE_DISPATCH(dt, gemm_t<T>(static_cast<const T*>(A), static_cast<const T*>(B), M, N, K, e, s, allow_mfma));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
-void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s, bool allow_mfma) {
-  if (dt == DType::BF16 && allow_mfma) {
-    hipLaunchKernelGGL(k_enc_attn_mfma, dim3((S + kAQ - 1) / kAQ, nb * H), dim3(256), 0, s, (const bf16*)qkv, S, H,
-                       (bf16*)out);
-  } else {
-    dim3 grid((S + 63) / 64, nb * H);
-    if (dt == DType::F32)
-      hipLaunchKernelGGL(k_enc_attn<float>, grid, dim3(64), 0, s, (const float*)qkv, S, H, (float*)out);
-    else
-      hipLaunchKernelGGL(k_enc_attn<bf16>, grid, dim3(64), 0, s, (const bf16*)qkv, S, H, (bf16*)out);
+namespace {
+
+template <typename T>
+void encoder_attn_t(const T* qkv, int nb, int S, int H, T* out, hipStream_t s, bool allow_mfma) {
+  if constexpr (sizeof(T) == 2) {
+    if (allow_mfma) {
+      hipLaunchKernelGGL(k_enc_attn_mfma<T>, dim3((S + kAQ - 1) / kAQ, nb * H), dim3(256), 0, s, qkv, S, H, out);
+      return;
+    }
   }
+  hipLaunchKernelGGL(k_enc_attn<T>, dim3((S + 63) / 64, nb * H), dim3(64), 0, s, qkv, S, H, out);
+}
+
+}  // namespace
+
+void encoder_attn(DType dt, const void* qkv, int nb, int S, int H, void* out, hipStream_t s, bool allow_mfma) {
+  MRT_DTYPE_DISPATCH(dt, encoder_attn_t<T>(static_cast<const T*>(qkv), nb, S, H, static_cast<T*>(out), s, allow_mfma));
   MRT_HIP_CHECK(hipGetLastError());
 }
 

@@ -1,7 +1,7 @@
 // Host-side launchers for the Depthformer HIP kernels (gfx950).
 //
 // Conventions shared by every launcher:
-//   * ``T`` is the model storage type selected by ``DType`` (fp32 or bf16);
+//   * ``T`` is the model storage type selected by ``DType`` (fp32, bf16 or fp16);
 //     all accumulation is fp32.
 //   * Linear weights are (out, in) row-major, exactly as the bundle stores
 //     them (modules.h:74-76), so a GEMV row is one contiguous dot product.

@@ -67,10 +67,11 @@ void convert(DType dt, const float* src, size_t n, void* dst) {
     std::memcpy(dst, src, n * 4);
     return;
   }
-  bf16* d = static_cast<bf16*>(dst);
+  uint16_t* d = static_cast<uint16_t*>(dst);
+  uint16_t (*cvt)(float) = dt == DType::BF16 ? f2bf : f2h_host;
   const unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
   if (n < (1u << 20) || nt == 1) {
-    for (size_t i = 0; i < n; ++i) d[i] = f2bf(src[i]);
+    for (size_t i = 0; i < n; ++i) d[i] = cvt(src[i]);
     return;
   }
   std::vector<std::thread> th;
@@ -79,7 +80,7 @@ void convert(DType dt, const float* src, size_t n, void* dst) {
     const size_t a = t * per, b = std::min(n, a + per);
     if (a >= b) break;
     th.emplace_back([=] {
-      for (size_t i = a; i < b; ++i) d[i] = f2bf(src[i]);
+      for (size_t i = a; i < b; ++i) d[i] = cvt(src[i]);
     });
   }
   for (auto& x : th) x.join();

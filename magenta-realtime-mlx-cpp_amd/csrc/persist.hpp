@@ -32,7 +32,7 @@ struct DecStack {
 };
 
 // Hand-off buffers of one state: 64-bit words {payload (low 32), tag (high
-// 32)}.  bf16 models pack both CFG rows of an element in one payload; fp32
+// 32)}.  16-bit models pack both CFG rows of an element in one payload; fp32
 // models use one word per row, row 1 at +kMaxPersistK.
 struct LLBufs {
   uint64_t* x;      // residual stream (2 * kMaxPersistK words)

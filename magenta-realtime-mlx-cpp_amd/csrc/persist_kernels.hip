@@ -263,19 +263,19 @@ __device__ __forceinline__ uint64_t ll_word(uint32_t payload, uint32_t tag) {
 }
 __device__ __forceinline__ uint32_t ll_tag(uint64_t w) { return static_cast<uint32_t>(w >> 32); }
 
-// Element k (both rows) of a tagged vector: bf16 -> one word, fp32 -> one
-// word per row (row 1 at +kMaxPersistK).
+// Element k (both rows) of a tagged vector: 16-bit types -> one word (row r
+// in payload bits 16r..16r+15), fp32 -> one word per row (row 1 at
+// +kMaxPersistK).
 template <typename T>
-struct LL;
-template <>
-struct LL<bf16> {
+struct LL {
+  static_assert(sizeof(T) == 2, "16-bit storage types");
   static constexpr int kWords = 1;
   __device__ static int idx(int k, int) { return k; }
   __device__ static void put(uint64_t* b, int k, float v0, float v1, uint32_t tag) {
-    astore(b + k, ll_word((uint32_t)f2bf(v0) | ((uint32_t)f2bf(v1) << 16), tag));
+    astore(b + k, ll_word(St<T>::bits(v0) | (St<T>::bits(v1) << 16), tag));
   }
   __device__ static float get(const uint64_t (&w)[1], int r) {
-    return bf2f(static_cast<bf16>((static_cast<uint32_t>(w[0]) >> (16 * r)) & 0xffffu));
+    return St<T>::unbits((static_cast<uint32_t>(w[0]) >> (16 * r)) & 0xffffu);
   }
 };
 template <>
@@ -300,7 +300,7 @@ struct Side {
 };
 
 // Activation rows in LDS, stored in the model dtype (row 1 at +kMaxPersistK
-// elements): bf16 rows feed v_dot2c_f32_bf16 directly.
+// elements): 16-bit rows feed v_dot2_f32_bf16 / v_dot2_f32_f16 directly.
 template <typename T>
 struct Act {
   __device__ static void put(float* xs, int k, float v0, float v1) {
@@ -506,7 +506,7 @@ __device__ __forceinline__ void fetch_batch(uint4 (&buf)[kNBuf], const T* W, int
   }
 }
 
-// acc += w . x over one 16-byte chunk (8 bf16 or 4 fp32 elements).
+// acc += w . x over one 16-byte chunk (8 16-bit or 4 fp32 elements).
 template <typename T>
 struct Dot;
 template <>
@@ -514,6 +514,19 @@ struct Dot<bf16> {
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
   __device__ static float d2(uint32_t w, uint32_t x, float a) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, w), __builtin_bit_cast(bf2, x), a, false);
+  }
+  __device__ static float acc(float a, const uint4& w, const uint4& x) {
+    a = d2(w.x, x.x, a);
+    a = d2(w.y, x.y, a);
+    a = d2(w.z, x.z, a);
+    return d2(w.w, x.w, a);
+  }
+};
+template <>
+struct Dot<f16> {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  __device__ static float d2(uint32_t w, uint32_t x, float a) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w), __builtin_bit_cast(h2, x), a, false);
   }
   __device__ static float acc(float a, const uint4& w, const uint4& x) {
     a = d2(w.x, x.x, a);
@@ -1367,8 +1380,9 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
       T* dst = ring_k + kv * eRing + (((size_t)rb * H + h) * a.Lmax + io.pos) * 64 + jpart * rps + 4 * g4;
       const float* v = &c.kvst[kv][rb][4 * g4];
       if constexpr (sizeof(T) == 2) {
-        st_g(reinterpret_cast<uint64_t*>(dst), (uint64_t)f2bf(v[0]) | ((uint64_t)f2bf(v[1]) << 16) |
-                                                   ((uint64_t)f2bf(v[2]) << 32) | ((uint64_t)f2bf(v[3]) << 48));
+        st_g(reinterpret_cast<uint64_t*>(dst), (uint64_t)St<T>::bits(v[0]) | ((uint64_t)St<T>::bits(v[1]) << 16) |
+                                                   ((uint64_t)St<T>::bits(v[2]) << 32) |
+                                                   ((uint64_t)St<T>::bits(v[3]) << 48));
       } else {
         st_g(reinterpret_cast<uint64_t*>(dst), (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32));
         st_g(reinterpret_cast<uint64_t*>(dst) + 1,
@@ -1783,29 +1797,23 @@ int persist_grid(int H, int num_cu, int* bph_out) {
 }
 
 size_t persist_prepare(DType dt, PersistKernel kind, int device) {
-  return dt == DType::F32 ? prepare<float>(kind, device) : prepare<bf16>(kind, device);
+  size_t r = 0;
+  MRT_DTYPE_DISPATCH(dt, r = prepare<T>(kind, device));
+  return r;
 }
 
 void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t s) {
-  if (dt == DType::F32) {
+  MRT_DTYPE_DISPATCH(dt, {
     if (a.cross)
-      hipLaunchKernelGGL((k_step<float, true>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+      hipLaunchKernelGGL((k_step<T, true>), dim3(grid), dim3(kPersistThreads), lds, s, a);
     else
-      hipLaunchKernelGGL((k_step<float, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
-  } else {
-    if (a.cross)
-      hipLaunchKernelGGL((k_step<bf16, true>), dim3(grid), dim3(kPersistThreads), lds, s, a);
-    else
-      hipLaunchKernelGGL((k_step<bf16, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
-  }
+      hipLaunchKernelGGL((k_step<T, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+  });
   MRT_HIP_CHECK(hipGetLastError());
 }
 
 void launch_frame(DType dt, const FrameArgs& a, int grid, size_t lds, hipStream_t s) {
-  if (dt == DType::F32)
-    hipLaunchKernelGGL((k_frame<float>), dim3(grid), dim3(kPersistThreads), lds, s, a);
-  else
-    hipLaunchKernelGGL((k_frame<bf16>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL((k_frame<T>), dim3(grid), dim3(kPersistThreads), lds, s, a));
   MRT_HIP_CHECK(hipGetLastError());
 }
 

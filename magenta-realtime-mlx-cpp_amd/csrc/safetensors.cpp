@@ -175,32 +175,6 @@ const JVal* field(const JVal& o, const char* name) {
   return nullptr;
 }
 
-float half_to_float(uint16_t h) {
-  const uint32_t sign = (h & 0x8000u) << 16;
-  uint32_t exp = (h >> 10) & 0x1f, man = h & 0x3ff;
-  uint32_t u;
-  if (exp == 0) {
-    if (man == 0) {
-      u = sign;
-    } else {
-      exp = 127 - 15 + 1;
-      while ((man & 0x400) == 0) {
-        man <<= 1;
-        --exp;
-      }
-      man &= 0x3ff;
-      u = sign | (exp << 23) | (man << 13);
-    }
-  } else if (exp == 31) {
-    u = sign | 0x7f800000u | (man << 13);
-  } else {
-    u = sign | ((exp + 127 - 15) << 23) | (man << 13);
-  }
-  float f;
-  std::memcpy(&f, &u, 4);
-  return f;
-}
-
 }  // namespace
 
 FileMapping::~FileMapping() {
@@ -286,7 +260,7 @@ SafetensorsFile::SafetensorsFile(const std::string& path) {
       for (uint64_t i = 0; i < n; ++i) {
         uint16_t h;
         std::memcpy(&h, src + 2 * i, 2);
-        (*buf)[i] = dt->str == "BF16" ? bf2f(h) : half_to_float(h);
+        (*buf)[i] = dt->str == "BF16" ? bf2f(h) : h2f_host(h);
       }
       t.data = buf->data();
       widened_.push_back(std::move(buf));

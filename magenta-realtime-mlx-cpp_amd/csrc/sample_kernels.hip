@@ -281,14 +281,9 @@ void sample_levels(DType dt, int streams, const float* logits, const SampleParam
   MRT_REQUIRE(p.codebook >= 1 && p.codebook <= 64 * kMaxPerLane, "sample: codebook must be <= 1024");
   MRT_REQUIRE(streams >= 1, "sample: no streams");
   MRT_REQUIRE(D >= 1 && D <= 256 * kFeedPer, "sample: d_model must be in [1, 2048]");
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_sample<float>, dim3(streams), dim3(256), 0, s, logits, p, frame, frame_ptr, level, slot,
-                       tstride, teacher, tokens, drawn, (const float*)emb, D, (float*)next_in, (float*)fsum,
-                       (float*)frame_mean);
-  else
-    hipLaunchKernelGGL(k_sample<bf16>, dim3(streams), dim3(256), 0, s, logits, p, frame, frame_ptr, level, slot,
-                       tstride, teacher, tokens, drawn, (const bf16*)emb, D, (bf16*)next_in, (bf16*)fsum,
-                       (bf16*)frame_mean);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_sample<T>, dim3(streams), dim3(256), 0, s, logits, p, frame, frame_ptr,
+                                            level, slot, tstride, teacher, tokens, drawn, (const T*)emb, D,
+                                            (T*)next_in, (T*)fsum, (T*)frame_mean));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
@@ -330,7 +325,7 @@ static unsigned char* scratch_on(int device) {
 
 void sample_level_noalloc(DType dt, int device, const void* emb, int D, const float* logits, const SampleParams& p,
                           uint64_t seed, int frame, int level, int* token, hipStream_t s) {
-  const size_t esz = dt == DType::F32 ? 4 : 2;
+  const size_t esz = dtype_size(dt);
   const size_t need = kNoAllocRows + 3 * 2 * static_cast<size_t>(D) * esz;
   if (need > kNoAllocBytes)
     throw Error(1, "sample_noalloc: d_model " + std::to_string(D) + " needs " + std::to_string(need) +

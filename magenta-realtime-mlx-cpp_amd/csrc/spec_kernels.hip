@@ -77,33 +77,22 @@ __global__ void k_spec_record(const float* __restrict__ all, const float* __rest
 
 void spec_inputs(DType dt, const void* t_out, const void* emb, const int* draft, int L, int D, void* out,
                  hipStream_t s) {
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_spec_inputs<float>, dim3(2 * L), dim3(256), 0, s, (const float*)t_out, (const float*)emb,
-                       draft, D, (float*)out);
-  else
-    hipLaunchKernelGGL(k_spec_inputs<bf16>, dim3(2 * L), dim3(256), 0, s, (const bf16*)t_out, (const bf16*)emb, draft,
-                       D, (bf16*)out);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_spec_inputs<T>, dim3(2 * L), dim3(256), 0, s, (const T*)t_out,
+                                            (const T*)emb, draft, D, (T*)out));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
 void spec_accept(DType dt, const int* drawn, const int* draft, int L, int* tokens, int* decided, const void* emb,
                  int D, void* next_in, hipStream_t s) {
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_spec_accept<float>, dim3(1), dim3(256), 0, s, drawn, draft, L, tokens, decided,
-                       (const float*)emb, D, (float*)next_in);
-  else
-    hipLaunchKernelGGL(k_spec_accept<bf16>, dim3(1), dim3(256), 0, s, drawn, draft, L, tokens, decided,
-                       (const bf16*)emb, D, (bf16*)next_in);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_spec_accept<T>, dim3(1), dim3(256), 0, s, drawn, draft, L, tokens,
+                                            decided, (const T*)emb, D, (T*)next_in));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
 void frame_mean_tokens(DType dt, const int* tokens, int L, const void* emb, int D, void* out, hipStream_t s) {
   const dim3 grid((D + 255) / 256);
-  if (dt == DType::F32)
-    hipLaunchKernelGGL(k_frame_mean_tokens<float>, grid, dim3(256), 0, s, tokens, L, (const float*)emb, D,
-                       (float*)out);
-  else
-    hipLaunchKernelGGL(k_frame_mean_tokens<bf16>, grid, dim3(256), 0, s, tokens, L, (const bf16*)emb, D, (bf16*)out);
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_frame_mean_tokens<T>, grid, dim3(256), 0, s, tokens, L, (const T*)emb, D,
+                                            (T*)out));
   MRT_HIP_CHECK(hipGetLastError());
 }
 

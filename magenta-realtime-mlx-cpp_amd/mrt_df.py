@@ -23,7 +23,23 @@ LIB_PATH = HERE / "libmrt_df.so"
 HEADER = HERE.parent / "include" / "mrt_df.h"
 
 MRT_OK = 0
-DTYPE_F32, DTYPE_BF16 = 0, 1
+DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
+
+
+def parse_dtype(name: str) -> str:
+    """``parse_dtype`` (dtype.cpp:35-49): case-insensitive fp32 | fp16 | bf16 and
+    their aliases -> the canonical name; anything else raises ValueError."""
+    n = str(name).lower()
+    if n in ("fp32", "float32", "f32"):
+        return "fp32"
+    if n in ("fp16", "float16", "f16", "half"):
+        return "fp16"
+    if n in ("bf16", "bfloat16"):
+        return "bf16"
+    raise ValueError(f'unknown dtype "{name}"; expected fp32|fp16|bf16')
+
+
+_DTYPE_CODE = {"fp32": DTYPE_F32, "bf16": DTYPE_BF16, "fp16": DTYPE_F16}
 BUF_ENC_OUT, BUF_CROSS_K, BUF_CROSS_V = 0, 1, 2
 BUF_TEMPORAL_K, BUF_TEMPORAL_V, BUF_DEPTH_K, BUF_DEPTH_V = 3, 4, 5, 6
 BUF_ENC_TOKENS = 7
@@ -335,11 +351,9 @@ class Depthformer:
     def __init__(self, weights, config: Config, dtype: str = "bf16", device: int = 0):
         self.lib = load_library()
         self.config = config
-        self.dtype = dtype
+        self.dtype = dtype = parse_dtype(dtype)
         self.device = device
-        d = {"fp32": DTYPE_F32, "float32": DTYPE_F32, "bf16": DTYPE_BF16, "bfloat16": DTYPE_BF16}
-        if dtype not in d:
-            raise ValueError(f'unknown dtype "{dtype}"; expected fp32|bf16')
+        d = _DTYPE_CODE
         h = ctypes.c_void_p()
         cfg = config.to_c()
         if isinstance(weights, (str, os.PathLike)):
@@ -374,7 +388,7 @@ class Depthformer:
     @property
     def torch_dtype(self):
         torch = _torch()
-        return torch.float32 if self.dtype in ("fp32", "float32") else torch.bfloat16
+        return {"fp32": torch.float32, "bf16": torch.bfloat16, "fp16": torch.float16}[self.dtype]
 
     def new_state(self, rows: int = 2, max_frames: int = 50, enc_len: Optional[int] = None) -> "State":
         return State(self, rows, max_frames, enc_len or self.config.max_encoder_length)

@@ -17,6 +17,9 @@ Precision modes (``mode``):
     op output the reference materialises in the model dtype is rounded to bf16
     (round-to-nearest-even), mirroring MLX's per-op bf16 outputs.  Matmul and
     softmax accumulate in float32 as MLX does.
+  * ``"fp16"`` -- the same with IEEE binary16 rounding (numpy's float16 cast:
+    ties to even, subnormals kept, overflow to inf), like ``--dtype fp16``
+    (dtype.cpp:40-41).
 
 How each part is pinned (see tests/test_oracle_*.py):
   * relative_position_bucket        -- closed form (identity below num_buckets/2)
@@ -116,11 +119,17 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     return out
 
 
+def round_fp16(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest binary16 (ties to even); float32 out."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
 class Precision:
     """Storage/compute precision of the restatement (see module docstring)."""
 
     def __init__(self, mode: str):
-        if mode not in ("fp64", "fp32", "bf16"):
+        if mode not in ("fp64", "fp32", "bf16", "fp16"):
             raise ValueError(f"unknown mode {mode!r}")
         self.mode = mode
         self.dtype = np.float64 if mode == "fp64" else np.float32
@@ -130,6 +139,8 @@ class Precision:
         x = np.asarray(x, dtype=self.dtype)
         if self.mode == "bf16":
             return round_bf16(x)
+        if self.mode == "fp16":
+            return round_fp16(x)
         return x
 
     def c(self, v: float):

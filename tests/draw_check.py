@@ -87,7 +87,7 @@ FLIP_SIGMAS = 8.0
 
 def assert_argmax_flips_are_near_ties(got_slices, ref_slices, w=5.0):
     """Teacher-forced CFG argmax of ``got`` against ``ref`` ((F, L, 2, C) slices).
-    Two bf16 evaluations differ by rounding noise spread over every candidate,
+    Two 16-bit evaluations differ by rounding noise spread over every candidate,
     which guidance weight w amplifies; an argmax may flip only where the
     reference's top-1 / top-2 margin is within ``FLIP_SIGMAS`` times the RMS of
     that draw's guided-logit error.  (Bounding the margin by the draw's largest

@@ -9,7 +9,7 @@
     bias reproduces the implicit call bit for bit, and a random bias matches
     the oracle's step with the same bias (persistent and multi-kernel paths);
   * the cache reset (empty_{temporal,depth}_cache, model.cpp:275-300).
-Tolerances: fp32 <= 1e-4, bf16 <= 2e-2 norm-wise relative error.
+Tolerances: fp32 <= 1e-4, bf16 <= 2e-2, fp16 <= 5e-3 norm-wise relative error.
 """
 
 from __future__ import annotations
@@ -21,7 +21,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-TOL = {"fp32": 1e-4, "bf16": 2e-2}
+TOL = {"fp32": 1e-4, "bf16": 2e-2, "fp16": 5e-3}
 
 
 def rel(a, b):
@@ -44,7 +44,7 @@ def _dev(torch, a, dt):
     return torch.tensor(np.asarray(a, dtype=np.float32), device="cuda").to(dt)
 
 
-@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("dtype", ["fp32", "bf16", "fp16"])
 @pytest.mark.parametrize("k,causal", [(16, True), (5, True), (16, False)])
 def test_depth_forward_full_matches_oracle(tiny, dtype, k, causal):
     import torch
@@ -74,7 +74,7 @@ def test_depth_forward_full_matches_oracle(tiny, dtype, k, causal):
     m.close()
 
 
-@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("dtype", ["fp32", "bf16", "fp16"])
 def test_depth_forward_full_equals_step_chain_at_benchmark_dims(gpu_available, dtype):
     """model.h:27-31: the full causal pass is the parity target of the step
     chain.  Benchmark dims: the pass's logits at position i against the
@@ -101,7 +101,7 @@ def test_depth_forward_full_equals_step_chain_at_benchmark_dims(gpu_available, d
     m.close()
 
 
-@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("dtype", ["fp32", "bf16", "fp16"])
 def test_precomputed_biases_equal_oracle(tiny, dtype):
     mrt_df, O = tiny["mrt_df"], tiny["O"]
     m = mrt_df.Depthformer(tiny["w"], tiny["cfg"], dtype=dtype)
@@ -113,7 +113,7 @@ def test_precomputed_biases_equal_oracle(tiny, dtype):
     m.close()
 
 
-@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("dtype", ["fp32", "bf16", "fp16"])
 @pytest.mark.parametrize("path", ["persistent", "layers"])
 def test_steps_with_explicit_bias(tiny, monkeypatch, dtype, path):
     import torch

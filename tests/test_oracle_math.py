@@ -100,6 +100,29 @@ def test_round_bf16_vs_torch():
     np.testing.assert_array_equal(got, exp)
 
 
+def test_round_fp16_closed_forms():
+    """binary16 rounding of the fp16 mode: every half value is fixed, midpoints
+    between neighbours go to the even one, the overflow and underflow edges sit
+    where IEEE 754 puts them, and torch's conversion agrees on random data."""
+    halves = np.arange(0x10000, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    fin = halves[np.isfinite(halves)].astype(np.float32)
+    np.testing.assert_array_equal(O.round_fp16(fin), fin)
+    pos = np.sort(np.unique(fin[fin >= 0]))
+    lo, hi = pos[:-1].astype(np.float64), pos[1:].astype(np.float64)
+    mid = ((lo + hi) / 2).astype(np.float32)  # exact in float32
+    even = np.where((pos[:-1].astype(np.float16).view(np.uint16) & 1) == 0, lo, hi).astype(np.float32)
+    np.testing.assert_array_equal(O.round_fp16(mid), even)
+    np.testing.assert_array_equal(O.round_fp16(-mid), -even)
+    edge = np.array([65519.996, 65520.0, 2.0 ** -25, np.nextafter(np.float32(2.0 ** -25), 1), 2.0 ** -24 * 1.5],
+                    dtype=np.float32)
+    np.testing.assert_array_equal(O.round_fp16(edge), np.array([65504.0, np.inf, 0.0, 2.0 ** -24, 2.0 ** -23],
+                                                               dtype=np.float32))
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(100000).astype(np.float32) * 100
+    np.testing.assert_array_equal(O.round_fp16(x), torch.tensor(x).to(torch.float16).to(torch.float32).numpy())
+    assert O.Precision("fp16").r(np.float32(1.0 + 2.0 ** -12)) == np.float32(1.0)  # ties to even at 1 + 2^-11 / 2
+
+
 # ---- sampling pieces (decode.cpp:71-148) ----------------------------------------------
 
 def test_cfg_combine_properties():
