@@ -40,6 +40,16 @@ def parse_dtype(name: str) -> str:
 
 
 _DTYPE_CODE = {"fp32": DTYPE_F32, "bf16": DTYPE_BF16, "fp16": DTYPE_F16}
+
+
+def dtype_code(name: str) -> int:
+    """The ABI's MRT_DTYPE_* code of a dtype name (any alias parse_dtype accepts)."""
+    return _DTYPE_CODE[parse_dtype(name)]
+
+
+def dtype_name(code: int) -> str:
+    """``dtype_name`` (dtype.cpp:51-56) of an ABI dtype code; "unsupported" otherwise."""
+    return {v: k for k, v in _DTYPE_CODE.items()}.get(code, "unsupported")
 BUF_ENC_OUT, BUF_CROSS_K, BUF_CROSS_V = 0, 1, 2
 BUF_TEMPORAL_K, BUF_TEMPORAL_V, BUF_DEPTH_K, BUF_DEPTH_V = 3, 4, 5, 6
 BUF_ENC_TOKENS = 7

@@ -185,6 +185,36 @@ def test_unknown_dtype(lib, tmp_path):
     assert code == MRT_ERR_INVALID and "dtype" in msg
 
 
+def test_parse_dtype_spellings():
+    """The dtype flag (dtype.cpp:35-56), cases of the reference's
+    tests/test_dtype.cpp:24-50: every spelling, case-insensitive, maps to its
+    ABI code; nonsense raises; names round-trip."""
+    for name in ("fp32", "float32", "F32", "f32"):
+        assert mrt_df.dtype_code(name) == mrt_df.DTYPE_F32
+    for name in ("fp16", "float16", "Half", "f16"):
+        assert mrt_df.dtype_code(name) == mrt_df.DTYPE_F16
+    for name in ("bf16", "bfloat16", "BF16"):
+        assert mrt_df.dtype_code(name) == mrt_df.DTYPE_BF16
+    for bad in ("int8", "", "bf32"):
+        with pytest.raises(ValueError, match="expected fp32\\|fp16\\|bf16"):
+            mrt_df.parse_dtype(bad)
+    for name in ("fp32", "fp16", "bf16"):
+        assert mrt_df.dtype_name(mrt_df.dtype_code(name)) == name
+    assert mrt_df.dtype_name(7) == "unsupported"
+
+
+def test_fp16_code_passes_the_dtype_check(lib, tmp_path):
+    """MRT_DTYPE_F16 is accepted by mrt_df_create (the error, if any, comes
+    from the device, not the dtype check)."""
+    cfg = mrt_df.Config.tiny()
+    p = tmp_path / "ok.safetensors"
+    synth_bundle.write_bundle(p, synth_bundle.make_weights(cfg, seed=1))
+    code, msg, h = _create_path(lib, p, cfg, dtype=mrt_df.DTYPE_F16)
+    assert code in (0, MRT_ERR_HIP), msg
+    if code == 0:
+        lib.mrt_df_destroy(h)
+
+
 def test_valid_bundle_reaches_the_device(lib, tmp_path):
     """A complete bundle passes every host check; without a GPU the first
     device call fails with MRT_ERR_HIP, with one it loads."""
