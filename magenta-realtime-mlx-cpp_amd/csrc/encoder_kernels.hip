@@ -6,7 +6,11 @@
 // weights (N, K) row-major as the bundle stores them).  bf16 and fp16 use
 // v_mfma_f32_32x32x16_{bf16,f16} with LDS-double-buffered tiles; fp32 uses a
 // VALU tile (parity mode).
+#include <atomic>
 #include <cmath>
+#include <mutex>
+#include <set>
+#include <utility>
 
 #include "device_utils.hpp"
 #include "kernels.hpp"
@@ -191,19 +195,108 @@ __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
 // s_waitcnt immediate waiting for vmcnt <= n (expcnt and lgkmcnt left alone).
 constexpr int vm_wait_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
+// Workgroup barrier of the global -> LDS rings: every LDS read this wave has
+// issued has returned (so another wave may refill that stage after the
+// barrier), then the waves meet.  Unlike __syncthreads() it does not wait for
+// this wave's loads still in flight to later stages (a release fence would
+// wait for every outstanding LDS write, direct-to-LDS loads included): the
+// stage about to be read is awaited with an explicit vmcnt before it.  The
+// asm is a compiler barrier for memory operations.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Epilogue of the MFMA GEMMs.  Accumulator r of tile (i, j) of a lane holds
+// row mb + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4 and column
+// nb + 32 j + lane % 32 (j = 0 / 1: gate / up columns of a gated-GELU pair).
+// The kind is resolved once per tile, and the residual epilogue loads every
+// residual before it stores anything: with the loads and stores of one
+// element interleaved, each load would wait for the previous element's store.
+template <typename T, int MI>
+__device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x16_t (&acc)[MI][2], int M, int mb,
+                                              int nb) {
+  using St_ = St<T>;
+  const int lane = threadIdx.x & 63, col = lane & 31, rl = 4 * (lane >> 5);
+  const int N = out.N;
+  T* C = static_cast<T*>(out.a.C);
+  auto row = [&](int i, int r) { return mb + 32 * i + 8 * (r >> 2) + rl + (r & 3); };
+  switch (out.a.kind) {
+    case GemmEpi::Geglu:
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (row(i, r) < M) out.put_geglu(row(i, r), nb + col, acc[i][0][r], acc[i][1][r]);
+      break;
+    case GemmEpi::Resid:
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          T old[16];  // rows past M load row M - 1 (unconditional loads, issued together)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) old[r] = C[(size_t)min(row(i, r), M - 1) * N + nb + 32 * j + col];
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (row(i, r) < M)
+              C[(size_t)row(i, r) * N + nb + 32 * j + col] = St_::st(St_::ld(old[r]) + St_::rnd(acc[i][j][r]));
+        }
+      break;
+    case GemmEpi::Store:
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (row(i, r) < M) C[(size_t)row(i, r) * N + nb + 32 * j + col] = St_::st(acc[i][j][r]);
+      break;
+    case GemmEpi::StoreF32:
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (row(i, r) < M)
+              static_cast<float*>(out.a.C)[(size_t)row(i, r) * N + nb + 32 * j + col] = St_::rnd(acc[i][j][r]);
+      break;
+    default: {  // CrossKV: column n = (layer*2 + kv)*HD + h*64 + d, row m = b*S + s
+      size_t cbase[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int n = nb + 32 * j + col, lk = n / out.a.HD, nn = n - lk * out.a.HD;
+        cbase[j] = (((size_t)lk * out.a.nb) * out.a.H + (nn >> 6)) * out.a.S * 64 + (nn & 63);
+      }
+      const size_t bstride = (size_t)out.a.H * out.a.S * 64;
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = row(i, r);
+          if (m < M) {
+            const int b = m / out.a.S, sp = m - b * out.a.S;
+            const size_t ro = (size_t)b * bstride + (size_t)sp * 64;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) C[cbase[j] + ro] = St_::st(acc[i][j][r]);
+          }
+        }
+    }
+  }
+}
+
 // C = A B^T (A (M, K), B (N, K) 16-bit, fp32 accumulation) with the GemmOut
 // epilogue.  Tile BM x 128 x 64, 4 waves in a 2x2 grid (wave tile BM/2 x 64 =
 // (BM/64) x 2 MFMA 32x32x16 tiles).  Tiles stream global -> LDS with direct
-// 16-byte loads (global_load_lds) through a kStages-deep ring: tile
-// j + kStages - 1 is requested while tile j is multiplied, and a wave waits
-// only for its own loads of tile j (vmcnt counts in order) before the
-// barrier.  Two stages (64 / 48 KB of LDS) leave room for 2-3 blocks per CU,
-// which hides more latency than a deeper ring in one block (measured).  Rows
-// past M read row M - 1 (their results are not stored).
+// 16-byte loads (global_load_lds) through an S-deep ring: tile j + S - 1 is
+// requested while tile j is multiplied, and a wave waits only for its own
+// loads of tile j (vmcnt counts in order) before the barrier.  Where the grid
+// fills every CU twice, two stages (64 / 48 KB of LDS) leave room for 2-3
+// blocks per CU, which hides more latency than a deeper ring in one block
+// (measured); a grid of at most one tile per CU instead takes a deep ring in
+// its one block.  Rows past M read row M - 1 (their results are not stored).
 // Operand fragments of v_mfma_f32_32x32x16_{bf16,f16}: lane l holds row (l % 32)
 // and k = 8*(l / 32) .. +7 of both A (32x16) and B^T (32x16); the 16
 // accumulators of lane l hold column l % 32, rows 8*(r/4) + 4*(l/32) + r%4.
-template <typename T, int BM>
+template <typename T, int BM, int S>
 __global__ __launch_bounds__(256) void k_gemm_mfma(const T* __restrict__ A, const T* __restrict__ B,
                                                    int M, int N, int K, GemmOut<T> out) {
   typedef typename Mfma<T>::v8 v8;
@@ -216,11 +309,11 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const T* __restrict__ A, cons
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
   const int nk = K / kBK;
 
-  // tile kt -> stage kt % kStages; wave w loads rows [w*BM/4, +BM/4) of A and
+  // tile kt -> stage kt % S; wave w loads rows [w*BM/4, +BM/4) of A and
   // [w*32, +32) of B, 8 rows (1 KB) per instruction
   auto issue = [&](int kt) {
     const int ktc = min(kt, nk - 1);  // past the end: reload the last tile into a free stage
-    unsigned char* st = lds + (kt % kStages) * kStageBytes;
+    unsigned char* st = lds + (kt % S) * kStageBytes;
     const int r8 = lane >> 3, p = lane & 7;
 #pragma unroll
     for (int q = 0; q < BM / 32; ++q) {
@@ -248,69 +341,76 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const T* __restrict__ A, cons
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
 #pragma unroll
-  for (int kt = 0; kt < kStages - 1; ++kt) issue(kt);
+  for (int kt = 0; kt < S - 1; ++kt) issue(kt);
   const int lr = lane & 31, lh = lane >> 5;
   for (int kt = 0; kt < nk; ++kt) {
-    __builtin_amdgcn_s_waitcnt(vm_wait_imm((kStages - 2) * LA));  // this wave's loads of tile kt have landed
-    __syncthreads();  // every wave's loads of tile kt; every wave is done with tile kt - 1
-    issue(kt + kStages - 1);
-    const unsigned char* st = lds + (kt % kStages) * kStageBytes;
+    __builtin_amdgcn_s_waitcnt(vm_wait_imm((S - 2) * LA));  // this wave's loads of tile kt have landed
+    ring_barrier();  // every wave's loads of tile kt; every wave is done with tile kt - 1
+    issue(kt + S - 1);
+    const unsigned char* st = lds + (kt % S) * kStageBytes;
+    // every fragment of the tile is read before the first product, so the
+    // LDS latency is paid once per tile, not once per 16-deep step
+    v8 a[kBK / 16][MI], b[kBK / 16][2];
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       const int c = 2 * ks + lh;
-      v8 a[MI], b[2];
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int r = wm * (BM / 2) + i * 32 + lr;
-        a[i] = *reinterpret_cast<const v8*>(st + r * 128 + ((c ^ swz(r)) << 4));
+        a[ks][i] = *reinterpret_cast<const v8*>(st + r * 128 + ((c ^ swz(r)) << 4));
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int r = wn * 64 + j * 32 + lr;
-        b[j] = *reinterpret_cast<const v8*>(st + BM * 128 + r * 128 + ((c ^ swz(r)) << 4));
+        b[ks][j] = *reinterpret_cast<const v8*>(st + BM * 128 + r * 128 + ((c ^ swz(r)) << 4));
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the products
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks)
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-          acc[i][j] = Mfma<T>::mma(a[i], b[j], acc[i][j]);
-    }
+          acc[i][j] = Mfma<T>::mma(a[ks][i], b[ks][j], acc[i][j]);
   }
   __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));  // no copy into LDS outlives the block
 
-  const int col_l = lane & 31, row_l = 4 * (lane >> 5);
-  if (out.a.kind == GemmEpi::Geglu) {
-    const int n = n0 + wn * 64 + col_l;  // gate column; up is n + 32
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
-        if (m < M) out.put_geglu(m, n, acc[i][0][r], acc[i][1][r]);
-      }
-  } else {
-#pragma unroll
-    for (int i = 0; i < MI; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
-          if (m < M) out.put(m, n0 + wn * 64 + j * 32 + col_l, acc[i][j][r]);
-        }
-  }
+  mfma_epilogue<T, MI>(out, acc, M, m0 + wm * (BM / 2), n0 + wn * 64);
 }
 
-template <typename T, int BM>
-void launch_gemm_mfma(const T* A, const T* B, int M, int N, int K, const GemmOut<T>& out, hipStream_t s) {
-  constexpr size_t lds = (size_t)kStages * (BM + kBN) * 128;
-  static bool allowed = false;  // dynamic LDS above 64 KB needs an explicit allowance
-  if (!allowed) {
-    MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_mfma<T, BM>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    allowed = true;
+// Dynamic LDS above 64 KB needs an explicit allowance, once per kernel and device.
+void allow_dynamic_lds(const void* fn, size_t bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  MRT_HIP_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> g(mu);
+  if (done.count({fn, dev})) return;
+  MRT_HIP_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
+  done.insert({fn, dev});
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  constexpr int kMaxDev = 64;
+  static std::atomic<int> cache[kMaxDev] = {};
+  int dev = 0;
+  MRT_HIP_CHECK(hipGetDevice(&dev));
+  int v = (dev >= 0 && dev < kMaxDev) ? cache[dev].load(std::memory_order_relaxed) : 0;
+  if (v == 0) {
+    MRT_HIP_CHECK(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev));
+    if (dev >= 0 && dev < kMaxDev) cache[dev].store(v, std::memory_order_relaxed);
   }
-  hipLaunchKernelGGL((k_gemm_mfma<T, BM>), dim3(N / kBN, (M + BM - 1) / BM), dim3(256), lds, s, A, B, M, N, K, out);
+  return v;
+}
+
+template <typename T, int BM, int S = kStages>
+void launch_gemm_mfma(const T* A, const T* B, int M, int N, int K, const GemmOut<T>& out, hipStream_t s) {
+  static_assert((S - 2) * (BM / 32 + kBN / 32) < 64, "vmcnt holds at most 63 outstanding loads");
+  constexpr size_t lds = (size_t)S * (BM + kBN) * 128;
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_mfma<T, BM, S>), lds);
+  hipLaunchKernelGGL((k_gemm_mfma<T, BM, S>), dim3(N / kBN, (M + BM - 1) / BM), dim3(256), lds, s, A, B, M, N, K, out);
 }
 
 // Large-M GEMM (the encoder of several streams): 256 x 256 x 64 tiles, 16
@@ -369,9 +469,11 @@ __global__ __launch_bounds__(64 * kGBWaves) void k_gemm_big(const T* __restrict_
   const int lr = lane & 31, lh = lane >> 5;
   for (int kt = 0; kt < nk; ++kt) {
     __builtin_amdgcn_s_waitcnt(vm_wait_imm((kStages - 2) * LA));  // this wave's loads of tile kt have landed
-    __syncthreads();  // every wave's loads of tile kt; every wave is done with tile kt - 1
+    ring_barrier();  // every wave's loads of tile kt; every wave is done with tile kt - 1
     issue(kt + kStages - 1);
     const unsigned char* st = lds + (kt % kStages) * kGBStage;
+    // one 16-deep step at a time: 16 waves leave 128 registers a lane, and
+    // reading further ahead spills
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       const int c = 2 * ks + lh;
@@ -395,38 +497,13 @@ __global__ __launch_bounds__(64 * kGBWaves) void k_gemm_big(const T* __restrict_
   }
   __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));  // no copy into LDS outlives the block
 
-  const int col_l = lane & 31, row_l = 4 * (lane >> 5);
-  if (out.a.kind == GemmEpi::Geglu) {
-    const int n = n0 + wn * 64 + col_l;  // gate column; up is n + 32
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
-        if (m < M) out.put_geglu(m, n, acc[i][0][r], acc[i][1][r]);
-      }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + row_l + (r & 3);
-          if (m < M) out.put(m, n0 + wn * 64 + j * 32 + col_l, acc[i][j][r]);
-        }
-  }
+  mfma_epilogue<T, 2>(out, acc, M, m0 + wm * 64, n0 + wn * 64);
 }
 
 template <typename T>
 void launch_gemm_big(const T* A, const T* B, int M, int N, int K, const GemmOut<T>& out, hipStream_t s) {
   constexpr size_t lds = (size_t)kStages * kGBStage;
-  static bool allowed = false;  // dynamic LDS above 64 KB needs an explicit allowance
-  if (!allowed) {
-    MRT_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_big<T>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    allowed = true;
-  }
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_big<T>), lds);
   hipLaunchKernelGGL(k_gemm_big<T>, dim3(N / kGB, (M + kGB - 1) / kGB), dim3(64 * kGBWaves), lds, s, A, B, M, N, K, out);
 }
 
@@ -500,11 +577,13 @@ __global__ __launch_bounds__(64) void k_enc_attn(const T* __restrict__ qkv, int 
 // accumulators: lane l's accumulators of a 16-key step hold keys
 // {4h..4h+3, 8+4h..8+4h+3} (h = l / 32), so V^T is staged with the key order
 // inside every 16-key block permuted the same way (swap of key bits 2 and 3).
-// Scores and the softmax are fp32; P enters the second product as the sum of
+// Scores and the softmax are fp32, the exponentials taken as 2^(s log2 e)
+// with v_exp_f32 (as fused attention kernels do); P enters the second product as the sum of
 // two parts in the storage type (hi + lo: ~16 significant bits for bf16, ~22
 // for fp16), as close to the fp32 probabilities of the reference's fused
 // attention as 16-bit MFMA allows.
 constexpr int kAQ = 128, kAK = 64, kALD = 64 + 8;  // queries, keys per tile, padded LDS row
+constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv, int S, int H,
@@ -587,12 +666,12 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int key = kb + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
-        sc[t][r] = key < S ? sc[t][r] : -INFINITY;
+        sc[t][r] = key < S ? sc[t][r] * kLog2e : -INFINITY;
         mt = fmaxf(mt, sc[t][r]);
       }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float mn = fmaxf(m, mt);
-    const float corr = expf(m - mn);
+    const float corr = __builtin_amdgcn_exp2f(m - mn);
     float ps = 0.f;
     v8 pb[4], pl[4];  // P^T = hi + lo (storage type each) for the four 16-key steps
 #pragma unroll
@@ -600,7 +679,7 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
       f32x8_t pv;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        pv[i] = expf(sc[g >> 1][8 * (g & 1) + i] - mn);
+        pv[i] = __builtin_amdgcn_exp2f(sc[g >> 1][8 * (g & 1) + i] - mn);
         ps += pv[i];
       }
       pb[g] = __builtin_convertvector(pv, v8);  // round-to-nearest-even conversions
@@ -664,13 +743,19 @@ void gemm_t(const T* A, const T* B, int M, int N, int K, const GemmEpiArgs& e, h
   GemmOut<T> out{e, N};
   if constexpr (sizeof(T) == 2) {
     if (allow_mfma && N % kBN == 0 && K % kBK == 0) {
-      // 256 x 256 tiles for outputs up to 4096 wide when they still give >= 2
-      // tiles per CU of a 256-CU part (measured: faster there, slower for the
-      // 5632- and 40960-wide outputs, where 2-3 smaller blocks per CU hide more
-      // latency); 128-row tiles when those give >= 1.5 tiles per CU, else 64-row
-      if (N % kGB == 0 && N <= 4096 && (long)((M + kGB - 1) / kGB) * (N / kGB) >= 512)
+      // Measured on MI355X (256 CUs) at 2 x 1006 x {1, 8, 32} rows: 256 x 256
+      // tiles for outputs up to 4096 wide once they give about one tile per
+      // CU (slower for the 5632- and 40960-wide outputs, where 2-3 smaller
+      // blocks per CU hide more latency); a grid of at most one 64-row tile
+      // per CU takes the 4-deep ring; else 128-row tiles when those give >= 1.5
+      // tiles per CU, else 64-row tiles.
+      const long cus = device_cus();
+      const long t256 = (long)((M + kGB - 1) / kGB) * (N / kGB), t64 = (long)((M + 63) / 64) * (N / kBN);
+      if (N % kGB == 0 && N <= 4096 && t256 >= cus - cus / 8)
         launch_gemm_big<T>(A, B, M, N, K, out, s);
-      else if ((long)((M + 127) / 128) * (N / kBN) >= 384)
+      else if (t64 <= cus)
+        launch_gemm_mfma<T, 64, 4>(A, B, M, N, K, out, s);
+      else if ((long)((M + 127) / 128) * (N / kBN) >= 3 * cus / 2)
         launch_gemm_mfma<T, 128>(A, B, M, N, K, out, s);
       else
         launch_gemm_mfma<T, 64>(A, B, M, N, K, out, s);
