@@ -436,7 +436,28 @@ void State::setup_persistent() {
   };
   tstack_ = stack(m.tmp, true);
   dstack_ = stack(m.dep, false);
-  if (const char* d = std::getenv("MRT_POLL_DELAY")) poll_delay_ = std::max(0, std::min(256, std::atoi(d)));
+  // First-poll delays per PollSite, measured on MI355X at the benchmark dims
+  // (bf16 frame kernel, sweep of 0..48 per site): the layer inputs of the
+  // q/k/v and output projections are polled at once, the gated-GELU input and
+  // output after 16 rounds (their producers finish last), the cross partials'
+  // query after 8, the head logits at once, the rest after 4.  MRT_POLL_DELAY=n
+  // sets every site, MRT_POLL_DELAYS a comma-separated list in PollSite order
+  // (missing entries keep their value).
+  static constexpr uint8_t kDefaultDelay[kPollSites] = {0, 4, 0, 4, 8, 4, 4, 16, 16, 4, 0, 4};
+  uint8_t* dl = poll_delay_;
+  std::copy(kDefaultDelay, kDefaultDelay + kPollSites, dl);
+  if (const char* d = std::getenv("MRT_POLL_DELAY"))
+    std::fill(dl, dl + kPollSites, static_cast<uint8_t>(std::max(0, std::min(255, std::atoi(d)))));
+  if (const char* d = std::getenv("MRT_POLL_DELAYS")) {
+    const char* c = d;
+    for (int i = 0; i < kPollSites; ++i) {
+      char* end = nullptr;
+      const long v = std::strtol(c, &end, 10);
+      if (end != c) dl[i] = static_cast<uint8_t>(std::max(0L, std::min(255L, v)));
+      if (*end != ',') break;
+      c = end + 1;
+    }
+  }
   if (const char* q = std::getenv("MRT_QKV_TABLE")) qkv_table_on_ = std::string(q) != "0";
   if (std::getenv("MRT_TRACE_PHASES")) {
     d_trace_ = static_cast<uint64_t*>(dalloc(2 * kTraceSlots * sizeof(uint64_t)));
@@ -512,7 +533,7 @@ LLBufs State::ll_bufs() const {
   l.seq = reinterpret_cast<uint32_t*>(tail);
   l.tok = tail + 16;
   l.err = reinterpret_cast<int*>(tail + 32);
-  l.poll_delay = poll_delay_;
+  std::memcpy(l.delay, poll_delay_, kPollSites);
   return l;
 }
 

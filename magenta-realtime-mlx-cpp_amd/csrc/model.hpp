@@ -243,7 +243,7 @@ class State {
   int* h_err_ = nullptr;        // pinned
   uint64_t* h_seed_ = nullptr;  // pinned: the draw seed of a generate / sample call
   uint64_t* d_trace_ = nullptr; // 2 x kTraceSlots when MRT_TRACE_PHASES is set
-  int poll_delay_ = 4;          // s_sleep(1) rounds before a hand-off's first poll (MRT_POLL_DELAY)
+  uint8_t poll_delay_[kPollSites];  // per poll site: s_sleep(1) rounds before a hand-off's first poll
   bool qkv_table_on_ = true;    // frame kernel: layer-0 q/k/v of fed tokens from the model's table (MRT_QKV_TABLE=0: off)
   const void* qkv_table_ = nullptr;  // the table of the current generate call, or nullptr
   hipEvent_t ev_dec_[2] = {nullptr, nullptr};  // around the decode section of generate

@@ -31,6 +31,25 @@ struct DecStack {
   void* ring;           // self K/V ring: layer i K at 2i*m, V at (2i+1)*m, m = 2*H*Lmax*64
 };
 
+// Poll sites of the persistent kernels; each waits its own number of
+// s_sleep(1) rounds (64 clocks each) before the first poll of its hand-off.
+enum PollSite : int {
+  kPollQKV = 0,     // layer input before the q/k/v projection
+  kPollAttn,        // a head's q, k, v before its self attention
+  kPollO,           // attention output before the output projection
+  kPollCrossQ,      // layer input before the cross-attention query projection
+  kPollCrossPart,   // a head's cross query before a key block's partial
+  kPollCrossComb,   // the key-block partials before their combination
+  kPollCrossO,      // cross-attention output before its projection
+  kPollUp,          // layer input before the gated-GELU projection
+  kPollDown,        // gated-GELU output before the down projection
+  kPollHead,        // stack output before the head
+  kPollLogits,      // head logits before the draw (workgroup 0)
+  kPollToken,       // the drawn token before the next depth level
+  kPollSites
+};
+static_assert(kPollSites <= 16, "LLBufs::delay holds 16 sites");
+
 // Hand-off buffers of one state: 64-bit words {payload (low 32), tag (high
 // 32)}.  16-bit models pack both CFG rows of an element in one payload; fp32
 // models use one word per row, row 1 at +kMaxPersistK.
@@ -46,7 +65,7 @@ struct LLBufs {
   uint64_t* tok;    // token drawn by workgroup 0 (frame kernel)
   uint32_t* seq;    // launch counter (tag epoch), advanced by each launch
   int* err;         // set when a poll exceeds its spin limit
-  int poll_delay;   // s_sleep(1) rounds before the first poll of a hand-off
+  uint8_t delay[16];  // per PollSite: s_sleep(1) rounds before the first poll of a hand-off
 };
 // tag = (epoch << kTagShift) | phase code: codes stay below 1 << kTagShift,
 // and the host zeroes every word and restarts the epoch at 1 before the

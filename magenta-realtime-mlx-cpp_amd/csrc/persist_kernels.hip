@@ -768,7 +768,7 @@ __device__ __forceinline__ void self_attention_head(const StepArgs& a, int pos, 
       constexpr int NW = LL<T>::kWords;
       uint64_t w[NW];
       uint32_t spins = 0;
-      poll_wait(a.ll.poll_delay);
+      poll_wait(a.ll.delay[kPollAttn]);
       for (;;) {
 #pragma unroll
         for (int r = 0; r < NW; ++r) w[r] = aload(src + LL<T>::idx(lane, r));
@@ -833,7 +833,7 @@ __device__ __forceinline__ void cross_partial(const StepArgs& a, int h, int j, u
   float* wm = sm + 640;  // [4]
   float* wl = sm + 644;  // [4]
   const int tid = threadIdx.x, wid = uniform(tid >> 6), lane = tid & 63;
-  ll_load_small<T>(a.ll.q + h * 64, 64, q_tag, qs, qs + 64, a.ll.err, a.ll.poll_delay);
+  ll_load_small<T>(a.ll.q + h * 64, 64, q_tag, qs, qs + 64, a.ll.err, a.ll.delay[kPollCrossPart]);
   __builtin_amdgcn_s_waitcnt(0);  // this wave's K/V copies have landed
   __syncthreads();
   const int chunk = (a.S + a.bph - 1) / a.bph;
@@ -891,7 +891,7 @@ __device__ __forceinline__ void cross_combine(const StepArgs& a, int h, uint32_t
     uint64_t wm[kMaxBph], wl[kMaxBph], wv[kMaxBph];
     uint32_t pend = (1u << a.bph) - 1u;
     uint32_t spins = 0;
-    poll_wait(a.ll.poll_delay);
+    poll_wait(a.ll.delay[kPollCrossComb]);
     while (pend != 0) {
 #pragma unroll
       for (int j = 0; j < kMaxBph; ++j) {
@@ -1356,7 +1356,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     } else {
     if (first && !io.qkv_ready) prefetch_qkv<T, NT>(c, a, 0);
     xs = c.next_xs();
-    load_act<T, 4, true>(a.ll.x, in_plain, D, x_tag, c.gq, xs, red, no_side, r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp,
+    load_act<T, 4, true>(a.ll.x, in_plain, D, x_tag, c.gq, xs, red, no_side, r0, r1, a.ll.err, a.ll.delay[kPollQKV], io.trace, c.tp,
                          c.lcnt, in_stride);
     gemv_rows<T, NVD, 1, NT>(c.buf, wqkv0 + li * eQKV, D, nqkv, qkv_row, xs,
                              [&](int t, bool act, const float (&s)[1][2]) {
@@ -1403,7 +1403,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     // ---- attention output projection + residual
     xs = c.next_xs();
     load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhAtt), c.gq, xs, red,
-                          side_x(a.ll.x, in_plain, x_tag, in_stride), r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp, c.lcnt, 0);
+                          side_x(a.ll.x, in_plain, x_tag, in_stride), r0, r1, a.ll.err, a.ll.delay[kPollO], io.trace, c.tp, c.lcnt, 0);
     gemv_rows<T, NVD, 1, NT>(c.buf, wo, HD, sD.nw(wid), rowD, xs,
                              [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhO)); });
     MRT_TP;
@@ -1416,7 +1416,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
       load_gamma<T, 4>(static_cast<const T*>(a.st.norm_ca) + (size_t)li * D, D, gc);
       fetch_batch<T, NVD, 1, NT>(c.buf, wqc, D, 0, min(kNBuf / NVD, ncq), cq_row);
       xs = c.next_xs();
-      load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gc, xs, red, no_side, r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp,
+      load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gc, xs, red, no_side, r0, r1, a.ll.err, a.ll.delay[kPollCrossQ], io.trace, c.tp,
                            c.lcnt, 0);
       gemv_rows<T, NVD, 1, NT>(c.buf, wqc, D, ncq, cq_row, xs, [&](int t, bool act, const float (&s)[1][2]) {
         if (act) LL<T>::put(a.ll.q, cq_row(t, 0), S::rnd(s[0][0]), S::rnd(s[0][1]), tag(base + kPhCQ));
@@ -1431,7 +1431,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
       }
       xs = c.next_xs();
       load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhCC), c.gq, xs, red,
-                            side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp, c.lcnt, 0);
+                            side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, a.ll.delay[kPollCrossO], io.trace, c.tp, c.lcnt, 0);
       gemv_rows<T, NVD, 1, NT>(c.buf, woc, HD, sD.nw(wid), rowD, xs,
                                [&](int t, bool act, const float (&s)[1][2]) { resid_put(t, act, s, tag(base + kPhCO)); });
       MRT_TP;
@@ -1444,7 +1444,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     load_gamma<T, 4>(static_cast<const T*>(a.st.norm_ff) + (size_t)li * D, D, gf);
     fetch_batch<T, NVD, 2, NT>(c.buf, w01, D, 0, min(kNBuf / (2 * NVD), sF.nw(wid)), rowF);
     xs = c.next_xs();
-    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gf, xs, red, no_side, r0, r1, a.ll.err, a.ll.poll_delay, io.trace, c.tp,
+    load_act<T, 4, true>(a.ll.x, nullptr, D, x_tag, gf, xs, red, no_side, r0, r1, a.ll.err, a.ll.delay[kPollUp], io.trace, c.tp,
                          c.lcnt, 0);
     gemv_rows<T, NVD, 2, NT>(c.buf, w01, D, sF.nw(wid), rowF, xs, [&](int t, bool act, const float (&s)[2][2]) {
       const float g0 = gelu_t<T>(S::rnd(s[0][0])), g1 = gelu_t<T>(S::rnd(s[0][1]));
@@ -1458,7 +1458,7 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     xs = c.next_xs();
     const Gamma<T, kMaxPersistK / kPersistThreads> nog{};  // no norm
     load_act<T, kMaxPersistK / kPersistThreads, false>(a.ll.h, nullptr, F, tag(base + kPhUp), nog, xs, red,
-                                                       side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, a.ll.poll_delay, io.trace,
+                                                       side_x(a.ll.x, nullptr, x_tag, 0), r0, r1, a.ll.err, a.ll.delay[kPollDown], io.trace,
                                                        c.tp, c.lcnt, 0);
     const bool tagged_out = !last || io.out_tagged;
     gemv_rows<T, NVF, 1, NT>(c.buf, wo2, F, sD.nw(wid), rowD, xs, [&](int t, bool act, const float (&s)[1][2]) {
@@ -1498,7 +1498,7 @@ __device__ __forceinline__ void run_head(Ctx<T>& c, const StepArgs& a, const T* 
   const Side no_side{nullptr, nullptr, 0u, -1, 0};
   float r0 = 0.f, r1 = 0.f;
   float* xs = c.next_xs();
-  load_act<T, 4, true>(a.ll.x, nullptr, a.D, x_tag, c.gq, xs, c.red, no_side, r0, r1, a.ll.err, a.ll.poll_delay, trace, c.tp,
+  load_act<T, 4, true>(a.ll.x, nullptr, a.D, x_tag, c.gq, xs, c.red, no_side, r0, r1, a.ll.err, a.ll.delay[kPollHead], trace, c.tp,
                        c.lcnt, 0);
   gemv_rows<T, NVD, 1, false>(c.buf, hw, a.D, sH.nw(wid), rowH, xs, [&](int t, bool act, const float (&s)[1][2]) {
     if (act) {
@@ -1531,7 +1531,7 @@ __device__ __forceinline__ void gather_logits(const StepArgs& a, uint32_t tg, fl
 #pragma unroll
     for (int u = 0; u < 8; ++u)
       if (base_i + (int)threadIdx.x + u * kPersistThreads < n2) pend |= 1u << u;
-    if (base_i == 0) poll_wait(a.ll.poll_delay);
+    if (base_i == 0) poll_wait(a.ll.delay[kPollLogits]);
     while (pend != 0) {
 #pragma unroll
       for (int u = 0; u < 8; ++u)
@@ -1711,7 +1711,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       if (threadIdx.x == 0) {
         uint32_t spins = 0;
         uint64_t w;
-        poll_wait(ad.ll.poll_delay);
+        poll_wait(ad.ll.delay[kPollToken]);
         for (;;) {
           w = aload(ad.ll.tok);
           if (ll_tag(w) == tg_tok || spin_failed(spins, ad.ll.err)) break;
