@@ -67,6 +67,8 @@ def algorithmic_bytes(cfg, esz=2, rows=2, frames=50, enc_len=1006, codebook=1024
     depth_kv = sum(cfg.num_depth_layers * kv_row * (l + 1) for l in range(L)) * frames
     temporal_kv = sum(cfg.num_temporal_layers * kv_row * (f + 1) for f in range(frames))
     total = frames * (temporal_step + L * depth_step) + depth_kv + temporal_kv
+    if os.environ.get("MRT_QKV_TABLE", "1") != "0":  # levels 1..: a table row for layer 0's q/k/v (frame_bytes)
+        total -= frames * (L - 1) * ((3 * HD * D + D) * esz - 3 * HD * esz)
     return dict(depth_step=depth_step, temporal_step=temporal_step, chunk=total)
 
 
@@ -81,14 +83,22 @@ def step_bytes(cfg, kind, pos, esz=2, rows=2, codebook=1024, enc_len=1006):
     return (ab["depth_step"] if kind == "depth" else ab["temporal_step"]) + kv
 
 
-def frame_bytes(cfg, f, esz=2, rows=2, codebook=1024, enc_len=1006):
+def frame_bytes(cfg, f, esz=2, rows=2, codebook=1024, enc_len=1006, qkv_table=None):
     """Algorithmic bytes of one frame launch (frame f of the chunk): the
     temporal step at ring position f, the rvq_depth depth steps at positions
     0..L-1, the Gumbel noise of the frame's draws (L x codebook fp32) and the
-    L - 1 fed-back embedding rows."""
+    L - 1 fed-back embedding rows.  With the layer-0 q/k/v table (the default;
+    MRT_QKV_TABLE=0 turns it off) levels 1.. read one table row (q | k | v of
+    the fed token) instead of depth layer 0's q/k/v weights and its norm."""
     L = cfg.rvq_depth
+    if qkv_table is None:
+        qkv_table = os.environ.get("MRT_QKV_TABLE", "1") != "0"
     b = step_bytes(cfg, "temporal", f, esz=esz, rows=rows, codebook=codebook, enc_len=enc_len)
     b += sum(step_bytes(cfg, "depth", l, esz=esz, rows=rows, codebook=codebook, enc_len=enc_len) for l in range(L))
+    if qkv_table:
+        HD, D = cfg.num_heads * cfg.d_kv, cfg.d_model
+        b -= (L - 1) * (3 * HD * D + D) * esz
+        b += (L - 1) * 3 * HD * esz
     return b + L * codebook * 4 + (L - 1) * cfg.d_model * esz
 
 
