@@ -49,6 +49,7 @@ Batch::Batch(Model& model, int streams, int max_frames, int enc_len)
   t_in_ = dalloc(R * D * e);
   d_in_ = dalloc(R * D * e);
   xn_ = dalloc(R * std::max(D, FF) * e);
+  ssq_ = static_cast<float*>(dalloc(static_cast<size_t>(R) * (D / 16) * 4));
   q_ = dalloc(R * HD * e);
   att_ = dalloc(R * HD * e);
   ffh_ = dalloc(R * FF * e);
@@ -107,34 +108,42 @@ void Batch::temporal_stack(int f, const int* fptr) {
   for (int i = 0; i < c.num_temporal_layers; ++i) {
     const DecoderLayerW& W = m.tmp[i];
     char *tk = ring(tkv_, i, 0, F), *tv = ring(tkv_, i, 1, F);
-    rmsnorm_rows(DType::BF16, t_in_, W.norm_sa, 1e-6f, R, D, xn_, stream);
-    bgemm_qkv(xn_, R, D, W.wqkv, HD, q_, tk, tv, H, F, f, fptr, stream);
+    // layer 0's input is the frame mean (no row partials): a plain norm pass
+    if (i == 0) {
+      rmsnorm_rows(DType::BF16, t_in_, W.norm_sa, 1e-6f, R, D, xn_, stream);
+      bgemm_qkv(xn_, R, D, W.wqkv, HD, q_, tk, tv, H, F, f, fptr, stream);
+    } else {
+      bgemm_qkv(t_in_, R, D, W.wqkv, HD, q_, tk, tv, H, F, f, fptr, stream, norm(W.norm_sa));
+    }
     self_attn_at(DType::BF16, R, q_, tk, tv, H, F, f + 1, f, fptr, m.tbias, m.tbuckets, att_, stream);
-    bgemm_resid(att_, R, HD, W.wo, D, t_in_, D, stream);
-    rmsnorm_rows(DType::BF16, t_in_, W.norm_ca, 1e-6f, R, D, xn_, stream);
-    bgemm_store(xn_, R, D, W.wq_c, HD, q_, HD, stream);
+    bgemm_resid(att_, R, HD, W.wo, D, t_in_, D, stream, ssq_);
+    bgemm_store(t_in_, R, D, W.wq_c, HD, q_, HD, stream, norm(W.norm_ca));
     cross_attn_rows(q_, ring(enc_.cross, i, 0, S), ring(enc_.cross, i, 1, S), R, H, S, att_, stream);
-    bgemm_resid(att_, R, HD, W.wo_c, D, t_in_, D, stream);
-    rmsnorm_rows(DType::BF16, t_in_, W.norm_ff, 1e-6f, R, D, xn_, stream);
-    bgemm_geglu(xn_, R, D, W.w01, FF, ffh_, FF, stream);
-    bgemm_resid(ffh_, R, FF, W.wo2, D, t_in_, D, stream);
+    bgemm_resid(att_, R, HD, W.wo_c, D, t_in_, D, stream, ssq_);
+    bgemm_geglu(t_in_, R, D, W.w01, FF, ffh_, FF, stream, norm(W.norm_ff));
+    bgemm_resid(ffh_, R, FF, W.wo2, D, t_in_, D, stream, ssq_);
   }
 }
 
 // Depth step l of every row in place on x (model.cpp:638-651 per row).
-void Batch::depth_stack(void* x, int l) {
+// x_partials: the row partials of x are those the last bgemm_resid left
+// (the temporal step's output), else layer 0 normalises in its own pass.
+void Batch::depth_stack(void* x, int l, bool x_partials) {
   const Config& c = m.cfg;
   const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads, L = c.rvq_depth;
   for (int i = 0; i < c.num_depth_layers; ++i) {
     const DecoderLayerW& W = m.dep[i];
     char *dk = ring(dkv_, i, 0, L), *dv = ring(dkv_, i, 1, L);
-    rmsnorm_rows(DType::BF16, x, W.norm_sa, 1e-6f, R, D, xn_, stream);
-    bgemm_qkv(xn_, R, D, W.wqkv, HD, q_, dk, dv, H, L, l, nullptr, stream);
+    if (i == 0 && !x_partials) {
+      rmsnorm_rows(DType::BF16, x, W.norm_sa, 1e-6f, R, D, xn_, stream);
+      bgemm_qkv(xn_, R, D, W.wqkv, HD, q_, dk, dv, H, L, l, nullptr, stream);
+    } else {
+      bgemm_qkv(x, R, D, W.wqkv, HD, q_, dk, dv, H, L, l, nullptr, stream, norm(W.norm_sa));
+    }
     self_attn_at(DType::BF16, R, q_, dk, dv, H, L, l + 1, l, nullptr, m.dbias, m.dbuckets, att_, stream);
-    bgemm_resid(att_, R, HD, W.wo, D, x, D, stream);
-    rmsnorm_rows(DType::BF16, x, W.norm_ff, 1e-6f, R, D, xn_, stream);
-    bgemm_geglu(xn_, R, D, W.w01, FF, ffh_, FF, stream);
-    bgemm_resid(ffh_, R, FF, W.wo2, D, x, D, stream);
+    bgemm_resid(att_, R, HD, W.wo, D, x, D, stream, ssq_);
+    bgemm_geglu(x, R, D, W.w01, FF, ffh_, FF, stream, norm(W.norm_ff));
+    bgemm_resid(ffh_, R, FF, W.wo2, D, x, D, stream, ssq_);
   }
 }
 
@@ -153,10 +162,14 @@ void Batch::enqueue_frame(const GenOpts& o, int f, bool dynamic) {
   if (o.record_temporal) copy_dev(static_cast<char*>(o.record_temporal) + f * row_bytes, t_in_, row_bytes, stream);
   for (int l = 0; l < L; ++l) {
     void* x = l == 0 ? t_in_ : d_in_;
-    depth_stack(x, l);
-    rmsnorm_rows(DType::BF16, x, m.dec_norm, 1e-6f, R, D, xn_, stream);
+    depth_stack(x, l, l == 0 && c.num_temporal_layers > 0);
     const char* head = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset + C * l) * D * 2;
-    bgemm_f32(xn_, R, D, head, C, logits_, C, stream);
+    if (c.num_depth_layers > 0) {
+      bgemm_f32(x, R, D, head, C, logits_, C, stream, norm(m.dec_norm));
+    } else {
+      rmsnorm_rows(DType::BF16, x, m.dec_norm, 1e-6f, R, D, xn_, stream);
+      bgemm_f32(xn_, R, D, head, C, logits_, C, stream);
+    }
     if (o.record_slices)
       copy_dev(o.record_slices + (static_cast<size_t>(f) * L + l) * R * C, logits_, static_cast<size_t>(R) * C * 4,
                stream);

@@ -15,15 +15,30 @@ namespace mrt {
 
 constexpr int kBatchRows = 64;  // activation rows of one batched step (32 streams)
 
+// RMSNorm (eps, weights g) of a GEMM's input rows applied as they are loaded:
+// X then holds the raw residual rows, whose sums of squares are the K / 16
+// partials per row (row-major, K / 16 a row) that the bgemm_resid which last
+// wrote them left at ssq.  g == nullptr: X is used as it is.
+struct BNorm {
+  const void* g = nullptr;
+  const float* ssq = nullptr;
+  float eps = 0.f;
+};
+
 // Skinny GEMMs Y (M x N) = X (M x K) . W^T, bf16 in, fp32 accumulation, M <= 64,
 // K % 32 == 0 (batch_kernels.hip).  Epilogues as the batch-1 GEMVs.
-void bgemm_store(const void* X, int M, int K, const void* W, int N, void* Y, int ldy, hipStream_t s);
-void bgemm_f32(const void* X, int M, int K, const void* W, int N, float* Y, int ldy, hipStream_t s);
-void bgemm_resid(const void* X, int M, int K, const void* W, int N, void* R, int ldr, hipStream_t s);
+void bgemm_store(const void* X, int M, int K, const void* W, int N, void* Y, int ldy, hipStream_t s,
+                 const BNorm& norm = {});
+void bgemm_f32(const void* X, int M, int K, const void* W, int N, float* Y, int ldy, hipStream_t s,
+               const BNorm& norm = {});
+// R += X . W^T (rounded as the batch-1 residual); ssq non-null: each updated
+// row's sums of squares over its 16-column tiles, (M, N / 16) floats.
+void bgemm_resid(const void* X, int M, int K, const void* W, int N, void* R, int ldr, hipStream_t s,
+                 float* ssq = nullptr);
 // W = [Wq; Wk; Wv] (3 HD rows): q -> Q (M, HD); k, v -> ring slot pos (or
 // *pos_ptr when non-null) of caches laid out (M, H, Lmax, 64).
 void bgemm_qkv(const void* X, int M, int K, const void* W, int HD, void* Q, void* Kc, void* Vc, int H, int Lmax, int pos,
-               const int* pos_ptr, hipStream_t s);
+               const int* pos_ptr, hipStream_t s, const BNorm& norm = {});
 // The same for rows m = P * pos + r (positions of one stream's frame, P CFG
 // rows each): k / v -> slot pos of ring row r (P, H, Lmax, 64).
 void bgemm_qkv_pos(const void* X, int M, int K, const void* W, int HD, void* Q, void* Kc, void* Vc, int H, int Lmax,
@@ -33,7 +48,8 @@ void bgemm_qkv_pos(const void* X, int M, int K, const void* W, int HD, void* Q, 
 void bgemm_f32_grouped(const void* X, int rows, int K, const void* W, long w_group_stride, int N, float* Y, int ldy,
                        int groups, hipStream_t s);
 // Gated GELU over the 32-row packed wi_0 / wi_1 matrix (2F rows) -> (M, F).
-void bgemm_geglu(const void* X, int M, int K, const void* W01, int F, void* Hout, int ldh, hipStream_t s);
+void bgemm_geglu(const void* X, int M, int K, const void* W01, int F, void* Hout, int ldh, hipStream_t s,
+                 const BNorm& norm = {});
 
 // Cross attention (no bias, no mask, scale 1) of every (row, head) over S <=
 // 1024 encoder keys, caches laid out (rows, H, S, 64); out (rows, H * 64).
@@ -73,7 +89,9 @@ class Batch {
  private:
   void enqueue_frame(const GenOpts& o, int f, bool dynamic);
   void temporal_stack(int f, const int* fptr);
-  void depth_stack(void* x, int l);
+  void depth_stack(void* x, int l, bool x_partials);
+  // the norm (weights g) of a GEMM input whose row partials are at ssq_
+  BNorm norm(const void* g) const { return BNorm{g, ssq_, 1e-6f}; }
   void* dalloc(size_t bytes);
   char* ring(void* base, int layer, int kv, int len) const;
 
@@ -82,6 +100,7 @@ class Batch {
   bool encoded_ = false;
   void *tkv_ = nullptr, *dkv_ = nullptr;
   void *t_in_ = nullptr, *d_in_ = nullptr, *xn_ = nullptr, *q_ = nullptr, *att_ = nullptr, *ffh_ = nullptr;
+  float* ssq_ = nullptr;  // row partials of the last residual update: (R, d_model / 16)
   void* fsum_ = nullptr;
   float* logits_ = nullptr;
   float* noise_ = nullptr;  // (B, F, L, 1024) Gumbel noise of the current call

@@ -8,6 +8,7 @@
 // activations (R x K, at most 360 KB) are read by every block from L2; the
 // weights stream from HBM/MALL once per step.
 #include <algorithm>
+#include <type_traits>
 
 #include "batch.hpp"
 #include "device_utils.hpp"
@@ -39,14 +40,19 @@ struct BF32 {
 };
 
 // Residual update; the residual values are read at the start of the kernel
-// (pre), so the epilogue does not wait for them.
+// (pre), so the epilogue does not wait for them.  `ssq` non-null: the sum of
+// squares of each updated row over the block's 16 columns goes to
+// ssq[m * ntiles + tile], the partials a normalised consumer reads (BNorm).
 struct BResid {
   bf16* r;
   int ldr;
+  float* ssq;
   static constexpr bool kPre = true;
   __device__ float pre(int m, int n) const { return St<bf16>::ld(r[(size_t)m * ldr + n]); }
-  __device__ void operator()(int m, int n, const float (&v)[1], float x) const {
-    r[(size_t)m * ldr + n] = St<bf16>::st(x + St<bf16>::rnd(v[0]));
+  __device__ float operator()(int m, int n, const float (&v)[1], float x) const {
+    const bf16 y = St<bf16>::st(x + St<bf16>::rnd(v[0]));
+    r[(size_t)m * ldr + n] = y;
+    return St<bf16>::ld(y);
   }
 };
 
@@ -110,6 +116,37 @@ __device__ __forceinline__ int bg_geglu_row(int j, int p) { return (j >> 5) * 64
 // Wave w of the 8 takes k-steps w, w + 8, ...; the 8 partial tiles are summed
 // in wave order.  Rows past M are zero, columns past nout re-read the last row
 // and are not stored.
+// RMSNorm of the activation rows applied as they are loaded (modules.cpp
+// RMSNorm, as rmsnorm_rows): row m of X is the raw residual, its sum of squares
+// the `parts` partials at ssq + m * parts (summed in order), element k scaled
+// to bf16(bf16(x * inv) * g[k]) with inv = 1 / sqrt(ss / K + eps).
+struct BNormDev {
+  const bf16* g;
+  const float* ssq;
+  int parts;
+  float eps;
+};
+
+// Sum over each 16-lane row of a wave, complete in the row's last lane.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, true));   // quad [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, true));   // quad [2,3,0,1]
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x114, 0xf, 0xf, true));  // row_shr:4
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x118, 0xf, 0xf, true));  // row_shr:8
+  return v;
+}
+
+// Eight bf16 activations scaled by the row's inverse RMS and the norm weights.
+__device__ __forceinline__ uint4 norm8(uint4 x, uint4 g, float inv) {
+  const bf16* xe = reinterpret_cast<const bf16*>(&x);
+  const bf16* ge = reinterpret_cast<const bf16*>(&g);
+  uint4 out;
+  bf16* oe = reinterpret_cast<bf16*>(&out);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) oe[e] = St<bf16>::st(St<bf16>::rnd(St<bf16>::ld(xe[e]) * inv) * St<bf16>::ld(ge[e]));
+  return out;
+}
+
 template <class Epi, class = void>
 struct HasPre {
   static constexpr bool value = false;
@@ -124,10 +161,10 @@ struct HasPre<Epi, decltype((void)Epi::kPre)> {
 // tile + ntiles * ms, on the same XCD when ntiles % 8 == 0 (blocks are dealt to
 // the 8 XCDs in turn), so the weight tile comes from HBM once and from that
 // XCD's L2 for the others.
-template <int P, int MT, class Epi>
+template <int P, int MT, bool NORM, class Epi>
 __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X, int M, int K,
                                                       const bf16* __restrict__ W, int nout, int ntiles, Epi epi,
-                                                      long w_group_stride) {
+                                                      long w_group_stride, BNormDev nrm) {
   // blockIdx.y = group g (grouped launch): rows [g M, g M + M) of X against
   // W + g * w_group_stride, outputs at rows g M + m
   const int grow = blockIdx.y * M;
@@ -155,6 +192,34 @@ __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X
     xin[t] = m < M;
     xrow[t] = X + (size_t)min(m, M - 1) * K + kg * 8;
   }
+  float inv[MT];
+  const bf16* grow_g = nullptr;
+  if constexpr (NORM) {
+    // eight lanes per row: with 64 partials lane q sums [8 q, 8 q + 8) in
+    // order (other counts: lane 0 sums them all), and the eight sums meet by
+    // lane exchange (the same total in each lane)
+    __shared__ float inv_s[kRows];
+    const int r = tid >> 3, q = tid & 7;
+    float ss = 0.f;
+    if (r < kRows) {
+      const float* sp = nrm.ssq + (size_t)(grow + min(m0 + r, M - 1)) * nrm.parts;
+      if (nrm.parts == 64) {
+        const float4 u = *reinterpret_cast<const float4*>(sp + 8 * q);
+        const float4 w = *reinterpret_cast<const float4*>(sp + 8 * q + 4);
+        ss = ((((((u.x + u.y) + u.z) + u.w) + w.x) + w.y) + w.z) + w.w;
+      } else if (q == 0) {
+        for (int t = 0; t < nrm.parts; ++t) ss += sp[t];
+      }
+    }
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 4);
+    if (r < kRows && q == 0) inv_s[r] = 1.0f / sqrtf(ss / (float)K + nrm.eps);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < MT; ++t) inv[t] = inv_s[16 * t + c16];
+    grow_g = nrm.g + kg * 8;
+  }
   float pre[kPer];
   if constexpr (HasPre<Epi>::value) {
 #pragma unroll
@@ -171,7 +236,7 @@ __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X
 
   const int nks = K / 32;
   for (int s0 = wid; s0 < nks; s0 += kBgWaves * kBgChunk) {
-    uint4 b[kBgChunk][P], a[kBgChunk][MT];
+    uint4 b[kBgChunk][P], a[kBgChunk][MT], gk[NORM ? kBgChunk : 1];
 #pragma unroll
     for (int c = 0; c < kBgChunk; ++c) {
       const int ks = s0 + kBgWaves * c;
@@ -180,11 +245,16 @@ __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X
         for (int p = 0; p < P; ++p) b[c][p] = ld_g16(wrow[p] + ks * 32);
 #pragma unroll
         for (int t = 0; t < MT; ++t) a[c][t] = xin[t] ? ld_g16(xrow[t] + ks * 32) : make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (NORM) gk[c] = ld_g16(grow_g + ks * 32);
       }
     }
 #pragma unroll
     for (int c = 0; c < kBgChunk; ++c) {
       if (s0 + kBgWaves * c < nks) {
+        if constexpr (NORM) {
+#pragma unroll
+          for (int t = 0; t < MT; ++t) a[c][t] = norm8(a[c][t], gk[c], inv[t]);
+        }
 #pragma unroll
         for (int p = 0; p < P; ++p)
 #pragma unroll
@@ -212,14 +282,28 @@ __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X
       v[i][p] = a;
     }
   }
+  if constexpr (std::is_same<Epi, BResid>::value) {
+    // lanes 16 r .. 16 r + 15 of a wave hold the 16 columns of one output row
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int idx = tid + kBgThreads * i, m = m0 + idx / kBgCols, n = idx % kBgCols;
-    if (idx >= kOut || m >= M || j0 + n >= nout) continue;
-    if constexpr (HasPre<Epi>::value)
-      epi(grow + m, j0 + n, v[i], pre[i]);
-    else
-      epi(grow + m, j0 + n, v[i]);
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = tid + kBgThreads * i, m = m0 + idx / kBgCols, n = idx % kBgCols;
+      const bool ok = idx < kOut && m < M && j0 + n < nout;
+      const float y = ok ? epi(grow + m, j0 + n, v[i], pre[i]) : 0.f;
+      if (epi.ssq != nullptr) {
+        const float ss = row16_sum(y * y);
+        if (ok && n == kBgCols - 1) epi.ssq[(size_t)(grow + m) * ntiles + tile] = ss;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = tid + kBgThreads * i, m = m0 + idx / kBgCols, n = idx % kBgCols;
+      if (idx >= kOut || m >= M || j0 + n >= nout) continue;
+      if constexpr (HasPre<Epi>::value)
+        epi(grow + m, j0 + n, v[i], pre[i]);
+      else
+        epi(grow + m, j0 + n, v[i]);
+    }
   }
 }
 
@@ -227,23 +311,41 @@ __global__ __launch_bounds__(kBgThreads) void k_bgemm(const bf16* __restrict__ X
 // outputs) split the rows until there are 256 blocks, one per CU; wider
 // outputs keep all rows in a block (measured faster: each block then reads the
 // activations once for twice the columns' work).
-template <int P, class Epi>
-void launch_bgemm(const bf16* X, int M, int K, const bf16* W, int nout, const Epi& epi, hipStream_t s, int groups = 1,
-                  long w_group_stride = 0) {
-  MRT_REQUIRE(M >= 1 && M <= kBatchRows, "batched GEMM: rows must be in [1, 64]");
-  MRT_REQUIRE(K % 32 == 0 && K >= 32, "batched GEMM: K must be a multiple of 32");
-  MRT_REQUIRE(nout >= 1 && groups >= 1, "batched GEMM: no outputs");
+template <int P, bool NORM, class Epi>
+void launch_bgemm_t(const bf16* X, int M, int K, const bf16* W, int nout, const Epi& epi, hipStream_t s, int groups,
+                    long w_group_stride, const BNormDev& nrm) {
   const int ntiles = (nout + kBgCols - 1) / kBgCols, mtiles = (M + 15) / 16;
   int ms = 1;
   while (ntiles < 128 && ms < 4 && ms < mtiles && ntiles * ms < 256) ms *= 2;
   const dim3 grid(ntiles * ms, groups), block(kBgThreads);
   if (ms == 1)
-    hipLaunchKernelGGL((k_bgemm<P, 4, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi, w_group_stride);
+    hipLaunchKernelGGL((k_bgemm<P, 4, NORM, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi, w_group_stride,
+                       nrm);
   else if (ms == 2)
-    hipLaunchKernelGGL((k_bgemm<P, 2, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi, w_group_stride);
+    hipLaunchKernelGGL((k_bgemm<P, 2, NORM, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi, w_group_stride,
+                       nrm);
   else
-    hipLaunchKernelGGL((k_bgemm<P, 1, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi, w_group_stride);
+    hipLaunchKernelGGL((k_bgemm<P, 1, NORM, Epi>), grid, block, 0, s, X, M, K, W, nout, ntiles, epi, w_group_stride,
+                       nrm);
   MRT_HIP_CHECK(hipGetLastError());
+}
+
+// nrm.g non-null: X holds raw residual rows normalised on load (BNormDev),
+// their sums of squares the K / 16 partials per row a BResid GEMM of width K
+// wrote.
+template <int P, class Epi>
+void launch_bgemm(const bf16* X, int M, int K, const bf16* W, int nout, const Epi& epi, hipStream_t s, int groups = 1,
+                  long w_group_stride = 0, const BNorm& norm = {}) {
+  MRT_REQUIRE(M >= 1 && M <= kBatchRows, "batched GEMM: rows must be in [1, 64]");
+  MRT_REQUIRE(K % 32 == 0 && K >= 32, "batched GEMM: K must be a multiple of 32");
+  MRT_REQUIRE(nout >= 1 && groups >= 1, "batched GEMM: no outputs");
+  if (norm.g != nullptr) {
+    MRT_REQUIRE(norm.ssq != nullptr && groups == 1, "batched GEMM: a normalised input needs its row partials");
+    const BNormDev d{static_cast<const bf16*>(norm.g), norm.ssq, K / kBgCols, norm.eps};
+    launch_bgemm_t<P, true>(X, M, K, W, nout, epi, s, groups, w_group_stride, d);
+  } else {
+    launch_bgemm_t<P, false>(X, M, K, W, nout, epi, s, groups, w_group_stride, BNormDev{nullptr, nullptr, 0, 0.f});
+  }
 }
 
 // Cross attention of one (row, head) over all S encoder keys (no bias, no
@@ -377,24 +479,25 @@ void cross_attn_rows(const void* Q, const void* Kc, const void* Vc, int rows, in
   MRT_HIP_CHECK(hipGetLastError());
 }
 
-void bgemm_store(const void* X, int M, int K, const void* W, int N, void* Y, int ldy, hipStream_t s) {
+void bgemm_store(const void* X, int M, int K, const void* W, int N, void* Y, int ldy, hipStream_t s, const BNorm& norm) {
   launch_bgemm<1>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W), N, BStore{static_cast<bf16*>(Y), ldy},
-                  s);
+                  s, 1, 0, norm);
 }
 
-void bgemm_f32(const void* X, int M, int K, const void* W, int N, float* Y, int ldy, hipStream_t s) {
-  launch_bgemm<1>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W), N, BF32{Y, ldy}, s);
+void bgemm_f32(const void* X, int M, int K, const void* W, int N, float* Y, int ldy, hipStream_t s, const BNorm& norm) {
+  launch_bgemm<1>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W), N, BF32{Y, ldy}, s, 1, 0, norm);
 }
 
-void bgemm_resid(const void* X, int M, int K, const void* W, int N, void* R, int ldr, hipStream_t s) {
-  launch_bgemm<1>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W), N, BResid{static_cast<bf16*>(R), ldr},
-                  s);
+void bgemm_resid(const void* X, int M, int K, const void* W, int N, void* R, int ldr, hipStream_t s, float* ssq) {
+  MRT_REQUIRE(ssq == nullptr || N % kBgCols == 0, "batched GEMM: row partials need whole 16-column tiles");
+  launch_bgemm<1>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W), N,
+                  BResid{static_cast<bf16*>(R), ldr, ssq}, s);
 }
 
 void bgemm_qkv(const void* X, int M, int K, const void* W, int HD, void* Q, void* Kc, void* Vc, int H, int Lmax, int pos,
-               const int* pos_ptr, hipStream_t s) {
+               const int* pos_ptr, hipStream_t s, const BNorm& norm) {
   BQKV e{static_cast<bf16*>(Q), static_cast<bf16*>(Kc), static_cast<bf16*>(Vc), HD, H, Lmax, pos, pos_ptr};
-  launch_bgemm<1>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W), 3 * HD, e, s);
+  launch_bgemm<1>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W), 3 * HD, e, s, 1, 0, norm);
 }
 
 void bgemm_qkv_pos(const void* X, int M, int K, const void* W, int HD, void* Q, void* Kc, void* Vc, int H, int Lmax,
@@ -410,10 +513,11 @@ void bgemm_f32_grouped(const void* X, int rows, int K, const void* W, long w_gro
                   w_group_stride);
 }
 
-void bgemm_geglu(const void* X, int M, int K, const void* W01, int F, void* Hout, int ldh, hipStream_t s) {
+void bgemm_geglu(const void* X, int M, int K, const void* W01, int F, void* Hout, int ldh, hipStream_t s,
+                 const BNorm& norm) {
   MRT_REQUIRE(F % 32 == 0, "batched GEMM: d_ff must be a multiple of 32 (packed gate/up groups)");
   launch_bgemm<2>(static_cast<const bf16*>(X), M, K, static_cast<const bf16*>(W01), F,
-                  BGeglu{static_cast<bf16*>(Hout), ldh}, s);
+                  BGeglu{static_cast<bf16*>(Hout), ldh}, s, 1, 0, norm);
 }
 
 }  // namespace mrt
