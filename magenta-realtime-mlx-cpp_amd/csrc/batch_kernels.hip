@@ -21,7 +21,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBgCols = 16;   // output columns per block
-constexpr int kBgChunk = 4;   // k-steps (of 32) whose loads a wave keeps in flight (8: 243.6 ms, 4: 238.7 ms per 32-stream chunk)
+constexpr int kBgChunk = 1;   // k-steps (of 32) per loop step of a wave: fewer live registers (per 32-stream chunk: 8: 243.6 ms, 4: 238.7, 2: 234.2, 1: 232.2)
 constexpr int kBgWaves = 8;   // waves per block, splitting K
 constexpr int kBgThreads = 64 * kBgWaves;
 
