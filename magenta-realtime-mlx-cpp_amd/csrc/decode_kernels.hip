@@ -293,10 +293,54 @@ __global__ __launch_bounds__(64) void k_self_attn(const T* __restrict__ Q, const
   const int HD = H * 64;
   __shared__ float qs[64];
   __shared__ float ps[kMaxSelfLen];
-  qs[lane] = S::ld(Q[(size_t)b * HD + h * 64 + lane]);
-  __syncthreads();
   const T* Kp = Kc + ((size_t)rb * H + h) * Lmax * 64;
   const T* Vp = Vc + ((size_t)rb * H + h) * Lmax * 64;
+  if (len <= 64) {
+    // One key per lane: the bias, K row and V row of key j = lane are all
+    // requested before any is used (one round trip), V goes to LDS, and the
+    // sums run in the order of the general path below (identical results).
+    __shared__ __align__(16) T vs[64 * 64];
+    const int j = lane;
+    const bool live = j < len;
+    const int jc = min(j, len - 1);
+    const float qv = S::ld(Q[(size_t)b * HD + h * 64 + lane]);
+    int bk = 0;
+    float bias = 0.f;
+    if (bias_row != nullptr)
+      bias = S::ld(bias_row[h * len + jc]);
+    else
+      bk = buckets[qpos - jc];
+    uint4 kv[64 / V], vv[64 / V];
+#pragma unroll
+    for (int i = 0; i < 64 / V; ++i) {
+      kv[i] = *reinterpret_cast<const uint4*>(Kp + (size_t)jc * 64 + i * V);
+      vv[i] = *reinterpret_cast<const uint4*>(Vp + (size_t)jc * 64 + i * V);
+    }
+    if (bias_row == nullptr) bias = S::ld(bias_tab[bk * H + h]);
+    qs[lane] = qv;
+#pragma unroll
+    for (int i = 0; i < 64 / V; ++i) *reinterpret_cast<uint4*>(vs + j * 64 + i * V) = vv[i];
+    __syncthreads();
+    float sc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 64 / V; ++i) {
+      const T* ke = reinterpret_cast<const T*>(&kv[i]);
+#pragma unroll
+      for (int e = 0; e < V; ++e) sc = fmaf(qs[i * V + e], S::ld(ke[e]), sc);
+    }
+    sc += bias;
+    const float m = wave_max(live ? sc : -INFINITY);
+    const float pj = live ? expf(sc - m) : 0.f;
+    ps[j] = pj;
+    const float sum = wave_sum(pj);
+    __syncthreads();
+    float o = 0.f;
+    for (int t = 0; t < len; ++t) o = fmaf(ps[t], S::ld(vs[t * 64 + lane]), o);
+    out[(size_t)b * HD + h * 64 + lane] = S::st(o / sum);
+    return;
+  }
+  qs[lane] = S::ld(Q[(size_t)b * HD + h * 64 + lane]);
+  __syncthreads();
   float mx = -INFINITY;
   for (int j = lane; j < len; j += 64) {
     const T* kr = Kp + (size_t)j * 64;
