@@ -593,70 +593,78 @@ def cpu_model() -> str:
 
 def cpu_baseline(weights, cfg, enc_tokens):
     """The CPU restatement of the reference algorithm (MLX is unavailable here),
-    fp32, timed on this host at 1 thread and at every core available to it:
-    the encoder in numpy (BLAS threads limited with threadpoolctl), the decode
-    steps in C with OpenMP (oracle/df_cpu.c, checked against the numpy oracle).
-    A bounded sample scaled to one chunk: one of the 12 encoder layers and one
-    of the 20 cross K/V projections over the 2 x 1006 rows, one temporal step
-    (ring position 25) and one frame's 16 depth steps with level-sliced heads;
-    chunk = 12 layers + 20 projections + 50 temporal steps + 50 x 16 depth steps."""
+    fp32, in C with OpenMP (oracle/df_cpu.c, checked against the numpy oracle),
+    timed on this host.  `value` is ONE WHOLE CHUNK at every core available to
+    the process: Depthformer::encode of the 2 x 1006 encoder ids (12 layers),
+    the cross K/V of the 20 temporal layers, then the 50-frame x 16-level
+    free-running decode with the streaming options (top-k 40, T 1.1, CFG w 5),
+    level-sliced heads.  `threads_1` is a 1-thread sample of the same work
+    scaled to a chunk: one encoder layer (x 12), one layer's cross K/V (x 20)
+    and one decoded frame (x 50)."""
     import dataclasses
-    from threadpoolctl import threadpool_limits
     from oracle import depthformer_oracle as O
     from oracle import df_cpu
     ocfg = O.DepthformerConfig(**dataclasses.asdict(cfg))
-    om = O.OracleDepthformer(weights, ocfg, mode="fp32")
-    cm = df_cpu.CpuDepthformer(weights, ocfg, max_frames=50)
     try:
         cores = len(os.sched_getaffinity(0))
     except AttributeError:
         cores = os.cpu_count() or 1
     n_all = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
-    x0 = om.embed(enc_tokens) + O.sinusoidal_position_embedding(cfg.max_encoder_length, cfg.d_model)[None]
-    x0 = x0.astype(np.float32)
-    rng = np.random.default_rng(7)
-    out = {}
-    H, S = cfg.num_heads, cfg.max_encoder_length
-    kv = rng.standard_normal((2, H, S, 64)).astype(np.float32)
-    cm.set_cross([(kv, kv)] * cfg.num_temporal_layers)
-    for n in sorted({1, n_all}):
-        # the C steps first: numpy's BLAS threads keep spinning for a while
-        # after a call and would take cores from the OpenMP team
-        df_cpu.CpuDepthformer.set_threads(n)
-        x = rng.standard_normal((2, cfg.d_model)).astype(np.float32)
-        t0 = time.perf_counter()
-        y = cm.temporal_step(x, 25)
-        t_temporal = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        for l in range(cfg.rvq_depth):
-            cm.depth_step(y if l == 0 else x, l, level=l)
-        t_frame_depth = time.perf_counter() - t0
-        with threadpool_limits(limits=n):
-            t0 = time.perf_counter()
-            xl = om.encoder_layer(x0, 0)
-            t_layer = time.perf_counter() - t0
-            t0 = time.perf_counter()
-            om.project_kv(xl, "temporal_layers.0.cross_attn")
-            t_cross = time.perf_counter() - t0
-        chunk_s = (cfg.num_encoder_layers * t_layer + cfg.num_temporal_layers * t_cross + 50 * t_temporal
-                   + 50 * t_frame_depth)
-        out[n] = {"value": 800.0 / chunk_s, "chunk_ms": chunk_s * 1e3, "encoder_layer_ms": t_layer * 1e3,
-                  "cross_kv_ms": t_cross * 1e3, "temporal_step_ms": t_temporal * 1e3,
-                  "depth_steps_16_ms": t_frame_depth * 1e3}
-        print(f"[bench] CPU restatement at {n} thread(s): {chunk_s * 1e3:.0f} ms per chunk "
-              f"(encoder layer {t_layer * 1e3:.0f} ms, temporal step {t_temporal * 1e3:.1f} ms, "
-              f"16 depth steps {t_frame_depth * 1e3:.1f} ms)", file=sys.stderr, flush=True)
+    opts = O.GenerateOptions(num_frames=50, rvq_depth=cfg.rvq_depth, temperature=1.1, top_k=40, guidance_weight=5.0,
+                             seed=1, codebook_size=1024, codec_offset=2)
+    cm = df_cpu.CpuDepthformer(weights, ocfg, max_frames=50)
+    # the whole chunk at every core
+    df_cpu.CpuDepthformer.set_threads(n_all)
+    t0 = time.perf_counter()
+    enc = cm.encode(enc_tokens)
+    t_enc = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    cm.set_cross_from_encoder(enc)
+    t_cross = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    toks = cm.generate(opts)
+    t_dec = time.perf_counter() - t0
+    lo = 2 + 1024 * np.arange(cfg.rvq_depth)[None, :]
+    assert ((toks >= lo) & (toks < lo + 1024)).all()
+    chunk_s = t_enc + t_cross + t_dec
+    whole = {"value": 800.0 / chunk_s, "chunk_ms": chunk_s * 1e3, "encoder_ms": t_enc * 1e3,
+             "cross_kv_ms": t_cross * 1e3, "decode_50_frames_ms": t_dec * 1e3}
+    print(f"[bench] CPU restatement, one whole chunk at {n_all} threads: {chunk_s * 1e3:.0f} ms (encoder "
+          f"{t_enc * 1e3:.0f} ms, cross K/V {t_cross * 1e3:.0f} ms, 50 frames {t_dec * 1e3:.0f} ms)",
+          file=sys.stderr, flush=True)
+    # a 1-thread sample: one encoder layer, one layer's cross K/V, one frame
+    df_cpu.CpuDepthformer.set_threads(1)
+    c1 = df_cpu.CpuDepthformer(weights, dataclasses.replace(ocfg, num_encoder_layers=1), max_frames=50)
+    t0 = time.perf_counter()
+    e1 = c1.encode(enc_tokens)
+    t_layer = time.perf_counter() - t0
+    S, HD = enc_tokens.shape[1], cfg.num_heads * cfg.d_kv
+    ck = np.empty((1, 2, cfg.num_heads, S, 64), np.float32)
+    cv = np.empty_like(ck)
+    t0 = time.perf_counter()
+    c1.lib.df_cross_kv(e1.ctypes.data, S, 1, cfg.d_model, HD, c1.ckw.ctypes.data, c1.cvw.ctypes.data,
+                       ck.ctypes.data, cv.ctypes.data)
+    t_cross1 = time.perf_counter() - t0
+    cm.set_cross_from_encoder(enc)
+    t0 = time.perf_counter()
+    cm.generate(dataclasses.replace(opts, num_frames=1))
+    t_frame = time.perf_counter() - t0
+    one_s = cfg.num_encoder_layers * t_layer + cfg.num_temporal_layers * t_cross1 + 50 * t_frame
+    print(f"[bench] CPU restatement at 1 thread (sampled): {one_s * 1e3:.0f} ms per chunk (encoder layer "
+          f"{t_layer * 1e3:.0f} ms, one frame {t_frame * 1e3:.0f} ms)", file=sys.stderr, flush=True)
     return {
-        "value": out[n_all]["value"],
+        "value": whole["value"],
         "unit": "RVQ tokens/s",
         "cores": n_all,
         "kind": "port",
         "cpu_model": cpu_model(),
-        "threads_1": out[1],
-        f"threads_{n_all}": out[n_all],
-        "sample": ("CPU restatement of the reference algorithm, fp32 (MLX unavailable): encoder in numpy, decode "
-                   "steps in C/OpenMP; 1 encoder layer + 1 cross K/V projection + 1 temporal step + 16 depth "
-                   "steps timed, scaled to 12 layers + 20 projections + 50 temporal + 800 depth steps"),
+        f"threads_{n_all}": whole,
+        "threads_1": {"value": 800.0 / one_s, "chunk_ms": one_s * 1e3, "encoder_layer_ms": t_layer * 1e3,
+                      "cross_kv_layer_ms": t_cross1 * 1e3, "frame_ms": t_frame * 1e3, "sampled": True},
+        "sample": (f"one whole chunk of the CPU restatement of the reference algorithm at {n_all} threads, fp32 "
+                   "(MLX unavailable): C/OpenMP encoder over 2 x 1006 ids, cross K/V of 20 layers, 50 free-running "
+                   "frames x 16 levels with level-sliced heads and the streaming draw options; threads_1 is a "
+                   "sample (1 encoder layer, 1 cross K/V layer, 1 frame) scaled to a chunk"),
     }
 
 

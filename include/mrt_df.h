@@ -19,7 +19,10 @@
  *     stream.  Calls on one state are not thread-safe; distinct states may be
  *     driven from distinct threads.  Their persistent kernels (one workgroup
  *     per CU) never run side by side: each decode or step launch of a state
- *     waits on the device for the previous one of any state on that device.
+ *     waits on the device for the previous one of any state on that device
+ *     (and so do the hand-off probes below).  This ordering holds among the
+ *     calls of one process: persistent work of two processes sharing a GPU
+ *     is not ordered by this library.
  */
 #ifndef MRT_DF_H_
 #define MRT_DF_H_
@@ -160,6 +163,21 @@ int mrt_df_temporal_step_with_bias(mrt_df_state* st, const void* frame_emb, cons
 int mrt_df_depth_step_with_bias(mrt_df_state* st, const void* tok_emb, int depth_idx, const void* position_bias,
                                 int level, int codebook_size, int codec_offset, float* logits);
 
+/* Depthformer::token_embedding() (depthformer/model.h:127) applied to ids,
+ * as the decode loop embeds every fed token (decode.cpp:366-368, 476-477;
+ * Embedding::operator(), modules.cpp:110-112): writes the n rows
+ * emb[ids[i]] -- (n, d_model) model dtype -- to the DEVICE buffer `out`.
+ * ids: host int32, each in [0, vocab_size) (else MRT_ERR_INVALID, nothing
+ * written).  Enqueued on `hip_stream` (NULL = the null stream); waits for it. */
+int mrt_df_embed_tokens(mrt_df* h, const int32_t* ids, int n, void* out, void* hip_stream);
+
+/* Depthformer::position_embedding(seq_len) (model.cpp:215-224): the first
+ * seq_len rows of the fp32 sinusoid table (model.cpp:54-80) as DEVICE fp32
+ * (seq_len, d_model).  seq_len > max_encoder_length fails with
+ * MRT_ERR_INVALID "seq_len exceeds max_encoder_length" (the reference's
+ * std::out_of_range).  Synchronous. */
+int mrt_df_position_embedding(mrt_df* h, int seq_len, float* out);
+
 /* Depthformer::precompute_temporal_biases / precompute_depth_biases
  * (model.cpp:302-320): kind 0 = temporal, 1 = depth.  Writes the biases of
  * steps 0..n-1 back to back into `out` (DEVICE, model dtype,
@@ -200,13 +218,14 @@ int mrt_df_sample_level(mrt_df_state* st, const float* slice, const mrt_gen_opts
  * (2, codebook) fp32 DEVICE array, the LLM id goes to token_dev[0] (DEVICE
  * int32), the work is enqueued on `hip_stream` (a hipStream_t of the model's
  * device; NULL = the null stream) and the call returns without waiting.  The
- * seed word and the fed-back embedding rows the draw kernel writes live in a
- * fixed 32 KiB device array of the library (one per device, held until the
- * process ends), so d_model * element size * 6 + 256 must be <= 32768 (fp32:
- * d_model <= 1354; bf16: the draw kernel's own limit, 2048), else
- * MRT_ERR_INVALID.  Calls that overlap
- * on one device race on that array.  Allocates nothing; shares the draw kernel
- * of mrt_df_sample_level, so tokens are identical. */
+ * seed travels by value in the kernel arguments.  The fed-back embedding rows
+ * the draw kernel also writes (discarded here) live in a fixed 32 KiB device
+ * array of the library (one per device, held until the process ends), so
+ * d_model * element size * 6 + 256 must be <= 32768 (fp32: d_model <= 1354;
+ * bf16: the draw kernel's own limit, 2048), else MRT_ERR_INVALID.  Calls that
+ * overlap on one device share that array, but each still writes the token of
+ * its own slice, seed, frame and level.  Allocates nothing; shares the draw
+ * kernel of mrt_df_sample_level, so tokens are identical. */
 int mrt_df_sample_level_noalloc(mrt_df* h, const float* slice_dev, const mrt_gen_opts* opts, int frame, int level,
                                 int32_t* token_dev, void* hip_stream);
 
@@ -232,6 +251,43 @@ int mrt_df_depth_forward_full(mrt_df_state* st, const void* token_embeddings, in
  * kernel, num_frames * (1 + rvq_depth) with one launch per step, 0 on the
  * per-layer path.  Waits for the section to finish. */
 int mrt_df_state_decode_time(mrt_df_state* st, float* ms, int* launches);
+/* Depthformer::compile_for_inference (model.cpp:697-...), per state: prepares
+ * the decode for `opts` before the first real call, so that call pays no
+ * one-time work.  Builds the layer-0 q/k/v table for the options' codebook and
+ * codec offset, captures and instantiates the decode graph (opts->use_graph;
+ * with opts->speculative the speculative graph as well) and launches every
+ * kernel of the path once, through untimed decodes on the state's encoder
+ * output (on an encoding of PAD ids when there is none, which is then
+ * dropped: encode or pass enc_tokens before generating).  opts->teacher and
+ * the record buffers are ignored.  The KV caches and the speculative draft
+ * history are left as before the call; waits for the work. */
+int mrt_df_state_compile(mrt_df_state* st, const mrt_gen_opts* opts);
+
+/* The per-chunk split of the reference's MRT_PROFILE_DECODE breakdown
+ * (decode.cpp:36-49, 529-565) for the last mrt_df_generate_tokens call on a
+ * state, in GPU milliseconds.  total_ms is mrt_df_state_decode_time's figure;
+ * encoder_ms the state's last encoder pass (-1 if none was timed); bias_ms 0
+ * (the rel-pos biases are precomputed once per model); temporal_ms / depth_ms
+ * / sample_ms sum over the frames the temporal step, the 16 depth steps with
+ * their head logits, and the draws (CFG, top-k, sampling, embedding feedback),
+ * from workgroup 0's device wall-clock stamps inside the frame kernel, taken
+ * only while profiling is on (MRT_PROFILE_DECODE non-empty when the state is
+ * created, or mrt_df_state_set_profile); -1 when the last call took none (the
+ * per-step and speculative paths).  frames = the frames stamped. */
+typedef struct mrt_decode_profile {
+  float total_ms;
+  float encoder_ms;
+  float bias_ms;
+  float temporal_ms;
+  float depth_ms;
+  float sample_ms;
+  int32_t frames;
+} mrt_decode_profile;
+/* Turns the frame kernel's phase stamps on or off for later decodes. */
+int mrt_df_state_set_profile(mrt_df_state* st, int on);
+/* Waits for the last decode; fills *out.  MRT_ERR_INVALID before any decode. */
+int mrt_df_state_decode_profile(mrt_df_state* st, mrt_decode_profile* out);
+
 /* Instrumentation, no counterpart in the reference: with MRT_TRACE_PHASES set
  * when the state was created, the persistent kernels' workgroup 0 stamps the
  * device wall clock at every phase boundary of frame 1 of a decode (its
@@ -360,6 +416,13 @@ int mrt_df_stream_generate_chunk(mrt_df_stream* s, const int32_t* style, const m
  * applies when the previous call of the stream also produced audio. */
 int mrt_df_stream_generate_chunk_audio(mrt_df_stream* s, const int32_t* style, const mrt_chunk_opts* opts,
                                        int32_t* llm_out, int32_t* rvq_out, float* audio_out);
+/* compile_for_inference for a stream (system.cpp:130 calls it once after
+ * loading): mrt_df_state_compile of the stream's state with the decode
+ * options of a chunk under `opts`, after building the encoder inputs of the
+ * current context (masked style) and running the encoder, unless a pipelined
+ * encoder output is held.  The context and chunk index are unchanged. */
+int mrt_df_stream_compile(mrt_df_stream* s, const mrt_chunk_opts* opts);
+
 /* Attach a codec (not owned; NULL detaches) to a stream.  Its rvq_levels and
  * codebook_size must equal the stream's and its max_frames must be at least
  * chunk_frames + crossfade_frames.  The codec must outlive the stream or be

@@ -389,6 +389,45 @@ int mrt_df_state_phase_trace(mrt_df_state* st, uint64_t* out, int n, float* cloc
   });
 }
 
+int mrt_df_state_set_profile(mrt_df_state* st, int on) {
+  return guarded([&] { S(st).set_profile(on != 0); });
+}
+
+int mrt_df_state_decode_profile(mrt_df_state* st, mrt_decode_profile* out) {
+  return guarded([&] {
+    if (!out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    const mrt::State::DecodeProfile p = S(st).decode_profile();
+    out->total_ms = p.total_ms;
+    out->encoder_ms = p.encoder_ms;
+    out->bias_ms = 0.f;
+    out->temporal_ms = p.temporal_ms;
+    out->depth_ms = p.depth_ms;
+    out->sample_ms = p.sample_ms;
+    out->frames = p.frames;
+  });
+}
+
+int mrt_df_state_compile(mrt_df_state* st, const mrt_gen_opts* opts) {
+  return guarded([&] {
+    if (!opts) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    S(st).compile(to_opts(opts));
+  });
+}
+
+int mrt_df_embed_tokens(mrt_df* h, const int32_t* ids, int n, void* out, void* hip_stream) {
+  return guarded([&] {
+    if (!h || !h->model || (n > 0 && (!ids || !out))) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    h->model->embed_tokens(ids, n, out, static_cast<hipStream_t>(hip_stream));
+  });
+}
+
+int mrt_df_position_embedding(mrt_df* h, int seq_len, float* out) {
+  return guarded([&] {
+    if (!h || !h->model || (seq_len > 0 && !out)) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    h->model->position_embedding(seq_len, out);
+  });
+}
+
 int mrt_df_state_spec_acceptance(mrt_df_state* st, float* acceptance) {
   return guarded([&] {
     if (!acceptance) throw mrt::Error(MRT_ERR_INVALID, "null argument");
@@ -509,6 +548,13 @@ int mrt_df_stream_generate_chunk_audio(mrt_df_stream* s, const int32_t* style, c
   return guarded([&] {
     if (!opts || !audio_out) throw mrt::Error(MRT_ERR_INVALID, "null argument");
     SS(s).generate_chunk_audio(style, to_chunk_opts(opts), llm_out, rvq_out, audio_out);
+  });
+}
+
+int mrt_df_stream_compile(mrt_df_stream* s, const mrt_chunk_opts* opts) {
+  return guarded([&] {
+    if (!opts) throw mrt::Error(MRT_ERR_INVALID, "null argument");
+    SS(s).compile(to_chunk_opts(opts));
   });
 }
 

@@ -89,7 +89,7 @@ struct SampleParams {
   int codebook;       // C: entries per level
   int codec_offset;   // first id of level 0
   int rvq_depth;      // L
-  const uint64_t* seed;  // device pointer to the draw seed (one per stream)
+  const uint64_t* seed;  // device pointer to the draw seed (one per stream), or nullptr: seed_value
   // Optional tabulated noise: noise[((stream * noise_frames + frame) * rvq_depth
   // + level) * codebook + i] = gumbel(seed[stream], frame, level, i).
   const float* noise = nullptr;
@@ -98,6 +98,9 @@ struct SampleParams {
   // decoding); the sampler then only feeds emb(token) to next_in (no draw, no
   // frame sum) and the depth step returns at once.
   const int* decided = nullptr;
+  // The draw seed of stream 0 when `seed` is nullptr (passed by value, so
+  // calls that share no device buffer cannot see each other's seeds).
+  uint64_t seed_value = 0;
 };
 
 // One CFG stream: rows (0, 1) of ``logits`` (nb=2, C) level slice.

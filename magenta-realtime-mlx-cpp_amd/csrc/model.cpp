@@ -207,8 +207,10 @@ Model::Model(const TensorSource& src, const Config& c, DType dtype, int dev)
   emb = upload(vec("token_embedding.weight", {V, D}));
   lm_head = upload(vec("lm_head.weight", {V, D}));
   {
-    // The fp32 table is cast to the model dtype before the add (model.cpp:232-236).
-    pe = upload(sinusoid(cfg.max_encoder_length, cfg.d_model));
+    // The fp32 table is cast to the model dtype before the add (model.cpp:232-236);
+    // the fp32 values stay on the host for position_embedding.
+    pe_host_ = sinusoid(cfg.max_encoder_length, cfg.d_model);
+    pe = upload(pe_host_);
   }
   enc_norm = upload(vec("encoder_norm.weight", {D}));
   dec_norm = upload(vec("decoder_norm.weight", {D}));
@@ -222,6 +224,8 @@ Model::Model(const TensorSource& src, const Config& c, DType dtype, int dev)
     }
     tbuckets = static_cast<const int*>(upload_i32(tb));
     dbuckets = static_cast<const int*>(upload_i32(db));
+    // the persistent kernels read row pos < kMaxPersistLen of these tables
+    static_assert(kBiasRows >= kMaxPersistLen, "bias rows must cover every persistent ring position");
     const size_t n_rows = static_cast<size_t>(H) * kBiasRows * (kBiasRows + 1) / 2;
     void* t = nullptr;
     void* d = nullptr;
@@ -302,6 +306,42 @@ Model::Model(const TensorSource& src, const Config& c, DType dtype, int dev)
 Model::~Model() {
   (void)hipSetDevice(device);
   for (void* p : allocs_) (void)hipFree(p);
+  if (embed_ids_host_) (void)hipHostFree(embed_ids_host_);
+}
+
+void Model::embed_tokens(const int32_t* ids, int n, void* out, hipStream_t s) {
+  MRT_REQUIRE(n >= 0, "token_embedding: negative id count");
+  for (int i = 0; i < n; ++i)
+    MRT_REQUIRE(ids[i] >= 0 && ids[i] < cfg.vocab_size, "token_embedding: token id out of range");
+  if (n == 0) return;
+  MRT_HIP_CHECK(hipSetDevice(device));
+  std::lock_guard<std::mutex> lock(embed_mu_);
+  if (embed_ids_dev_ == nullptr) {
+    void* d = nullptr;
+    MRT_HIP_CHECK(hipMalloc(&d, kEmbedChunk * sizeof(int)));
+    allocs_.push_back(d);
+    embed_ids_dev_ = static_cast<int*>(d);
+    MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&embed_ids_host_), kEmbedChunk * sizeof(int),
+                                hipHostMallocDefault));
+  }
+  const size_t row = static_cast<size_t>(cfg.d_model) * esz;
+  for (int i0 = 0; i0 < n; i0 += kEmbedChunk) {
+    const int k = std::min(kEmbedChunk, n - i0);
+    std::memcpy(embed_ids_host_, ids + i0, static_cast<size_t>(k) * sizeof(int));
+    MRT_HIP_CHECK(hipMemcpyAsync(embed_ids_dev_, embed_ids_host_, static_cast<size_t>(k) * sizeof(int),
+                                 hipMemcpyHostToDevice, s));
+    embed_rows(dt, emb, cfg.d_model, embed_ids_dev_, k, static_cast<char*>(out) + i0 * row, s);
+    MRT_HIP_CHECK(hipStreamSynchronize(s));  // the staging is reused by the next chunk and call
+  }
+}
+
+void Model::position_embedding(int seq_len, float* out) const {
+  MRT_REQUIRE(seq_len >= 0, "position_embedding: negative seq_len");
+  if (seq_len > cfg.max_encoder_length) throw Error(1, "seq_len exceeds max_encoder_length");
+  if (seq_len == 0) return;
+  MRT_HIP_CHECK(hipSetDevice(device));
+  MRT_HIP_CHECK(hipMemcpy(out, pe_host_.data(), static_cast<size_t>(seq_len) * cfg.d_model * sizeof(float),
+                          hipMemcpyHostToDevice));
 }
 
 // ---------------------------------------------------------------------------
@@ -355,6 +395,9 @@ State::State(Model& model, int rows_, int max_frames, int enc_len)
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_err_), 64, hipHostMallocDefault));
   *h_err_ = 0;
   MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_seed_), 64, hipHostMallocDefault));
+  d_prof_ = static_cast<uint64_t*>(dalloc(static_cast<size_t>(F) * 4 * sizeof(uint64_t)));
+  MRT_HIP_CHECK(hipHostMalloc(reinterpret_cast<void**>(&h_prof_), static_cast<size_t>(F) * 4 * sizeof(uint64_t),
+                              hipHostMallocDefault));
   {  // rows of the full-sequence depth pass and the speculative verification pass (2 L rows)
     const size_t R2 = 2 * L;
     sx_ = dalloc(R2 * D * e);
@@ -459,6 +502,7 @@ void State::setup_persistent() {
     }
   }
   if (const char* q = std::getenv("MRT_QKV_TABLE")) qkv_table_on_ = std::string(q) != "0";
+  if (const char* pr = std::getenv("MRT_PROFILE_DECODE")) profile_ = pr[0] != '\0';
   if (std::getenv("MRT_TRACE_PHASES")) {
     d_trace_ = static_cast<uint64_t*>(dalloc(2 * kTraceSlots * sizeof(uint64_t)));
     MRT_HIP_CHECK(hipMemset(d_trace_, 0, 2 * kTraceSlots * sizeof(uint64_t)));
@@ -647,6 +691,7 @@ void State::launch_frame_p(const GenOpts& o, int f) {
   fa.rec_slices = o.record_slices ? o.record_slices + static_cast<size_t>(f) * L * rows * C : nullptr;
   fa.rec_temporal = o.record_temporal ? static_cast<char*>(o.record_temporal) + f * row_bytes : nullptr;
   fa.qkv_table = qkv_table_;
+  fa.prof = profile_ ? d_prof_ : nullptr;
   launch_frame(m.dt, fa, persist_grid_, lds_f_, stream);
 }
 
@@ -768,6 +813,9 @@ State::~State() {
   }
   for (hipEvent_t e : ev_dec_)
     if (e) (void)hipEventDestroy(e);
+  for (hipEvent_t e : ev_enc_)
+    if (e) (void)hipEventDestroy(e);
+  if (h_prof_) (void)hipHostFree(h_prof_);
   for (void* p : allocs_) (void)hipFree(p);
   if (h_pinned) (void)hipHostFree(h_pinned);
   if (h_err_) (void)hipHostFree(h_err_);
@@ -868,7 +916,14 @@ void State::encode_device() {
   b.effh = effh;
   b.enc_out = enc_out;
   b.cross = cross;
+  if (!ev_enc_[0]) {
+    MRT_HIP_CHECK(hipEventCreate(&ev_enc_[0]));
+    MRT_HIP_CHECK(hipEventCreate(&ev_enc_[1]));
+  }
+  MRT_HIP_CHECK(hipEventRecord(ev_enc_[0], stream));
   run_encoder(m, b, stream);
+  MRT_HIP_CHECK(hipEventRecord(ev_enc_[1], stream));
+  enc_timed_ = true;
   cross_ready_ = true;
 }
 
@@ -1016,37 +1071,31 @@ const void* Model::depth_qkv_table(int codebook, int offset, hipStream_t s) {
   std::lock_guard<std::mutex> lock(qkv_mu_);
   for (const QkvTable& t : qkv_tables_)
     if (t.codebook == codebook && t.offset == offset) return t.rows;
-  const int rows = (L - 1) * codebook;
-  std::vector<int> ids(static_cast<size_t>(rows));
-  for (int l = 0; l + 1 < L; ++l)
-    for (int c = 0; c < codebook; ++c) ids[static_cast<size_t>(l) * codebook + c] = offset + codebook * l + c;
+  // Tables are never evicted (a captured decode graph holds its table's
+  // address); past the cap the decode computes layer 0 instead.
+  if (qkv_tables_.size() >= kMaxQkvTables) return nullptr;
   MRT_HIP_CHECK(hipSetDevice(device));
+  // Row r = (l - 1) * codebook + c is the token offset + codebook (l - 1) + c =
+  // offset + r: the rows' inputs are the embedding rows offset .. offset + rows,
+  // normalised in chunks through a workspace the model keeps.
+  const int rows = (L - 1) * codebook;
+  if (qkv_ws_ == nullptr) {
+    MRT_HIP_CHECK(hipMalloc(&qkv_ws_, static_cast<size_t>(kQkvChunkRows) * D * esz));
+    allocs_.push_back(qkv_ws_);
+  }
   void* out = nullptr;
-  void *x = nullptr, *xn = nullptr, *d_ids = nullptr;
-  auto release = [&]() {
-    if (x) (void)hipFree(x);
-    if (xn) (void)hipFree(xn);
-    if (d_ids) (void)hipFree(d_ids);
-  };
-  try {
-    MRT_HIP_CHECK(hipMalloc(&out, static_cast<size_t>(rows) * 3 * HD * esz));
-    allocs_.push_back(out);
-    MRT_HIP_CHECK(hipMalloc(&x, static_cast<size_t>(rows) * D * esz));
-    MRT_HIP_CHECK(hipMalloc(&xn, static_cast<size_t>(rows) * D * esz));
-    MRT_HIP_CHECK(hipMalloc(&d_ids, ids.size() * sizeof(int)));
-    MRT_HIP_CHECK(hipMemcpyAsync(d_ids, ids.data(), ids.size() * sizeof(int), hipMemcpyHostToDevice, s));
-    embed_rows(dt, emb, D, static_cast<const int*>(d_ids), rows, x, s);
-    rmsnorm_rows(dt, x, dep[0].norm_sa, 1e-6f, rows, D, xn, s);
+  MRT_HIP_CHECK(hipMalloc(&out, static_cast<size_t>(rows) * 3 * HD * esz));
+  allocs_.push_back(out);
+  for (int r0 = 0; r0 < rows; r0 += kQkvChunkRows) {
+    const int n = std::min(kQkvChunkRows, rows - r0);
+    const char* x = static_cast<const char*>(emb) + (static_cast<size_t>(offset) + r0) * D * esz;
+    rmsnorm_rows(dt, x, dep[0].norm_sa, 1e-6f, n, D, qkv_ws_, s);
     GemmEpiArgs e;
     e.kind = GemmEpi::Store;
-    e.C = out;
-    gemm(dt, xn, dep[0].wqkv, rows, 3 * HD, D, e, s);
-    MRT_HIP_CHECK(hipStreamSynchronize(s));
-  } catch (...) {
-    release();
-    throw;
+    e.C = static_cast<char*>(out) + static_cast<size_t>(r0) * 3 * HD * esz;
+    gemm(dt, qkv_ws_, dep[0].wqkv, n, 3 * HD, D, e, s);
   }
-  release();
+  MRT_HIP_CHECK(hipStreamSynchronize(s));
   qkv_tables_.push_back(QkvTable{codebook, offset, out});
   return out;
 }
@@ -1141,7 +1190,7 @@ hipGraphExec_t State::decode_graph(const GenOpts& o) {
   const std::vector<double> key = {
       (double)o.num_frames, (double)o.rvq_depth, (double)o.temperature, (double)o.top_k,
       (double)o.guidance_weight, (double)o.codebook, (double)o.codec_offset, o.teacher ? 1.0 : 0.0,
-      spec_drafts_ ? 1.0 : 0.0,
+      spec_drafts_ ? 1.0 : 0.0, profile_ ? 1.0 : 0.0,
       (double)reinterpret_cast<uintptr_t>(o.record_slices),
       (double)reinterpret_cast<uintptr_t>(o.record_temporal),
       (double)reinterpret_cast<uintptr_t>(o.record_drawn),
@@ -1232,6 +1281,11 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
     MRT_HIP_CHECK(hipEventRecord(ev_dec_[1], stream));
   }
   dec_timed_ = true;
+  // the frame kernel's phase stamps (the speculative path runs per-step launches)
+  prof_frames_ = profile_ && persistent() && frame_kernel_ && !spec_drafts_ ? o.num_frames : 0;
+  if (prof_frames_ > 0)
+    MRT_HIP_CHECK(hipMemcpyAsync(h_prof_, d_prof_, static_cast<size_t>(prof_frames_) * 4 * sizeof(uint64_t),
+                                 hipMemcpyDeviceToHost, stream));
   MRT_HIP_CHECK(hipMemcpyAsync(h_pinned, d_tokens, nt * 4, hipMemcpyDeviceToHost, stream));
   if (spec_drafts_)
     MRT_HIP_CHECK(hipMemcpyAsync(h_pinned + nt, sdecided_, static_cast<size_t>(o.num_frames) * 4,
@@ -1258,6 +1312,62 @@ float State::last_decode_ms(int* launches) {
   MRT_HIP_CHECK(hipEventElapsedTime(&ms, ev_dec_[0], ev_dec_[1]));
   if (launches) *launches = dec_launches_;
   return ms;
+}
+
+State::DecodeProfile State::decode_profile() {
+  DecodeProfile r;
+  int launches = 0;
+  r.total_ms = last_decode_ms(&launches);
+  if (enc_timed_) {
+    MRT_HIP_CHECK(hipEventSynchronize(ev_enc_[1]));
+    MRT_HIP_CHECK(hipEventElapsedTime(&r.encoder_ms, ev_enc_[0], ev_enc_[1]));
+  }
+  r.frames = prof_frames_;
+  if (prof_frames_ > 0) {
+    int khz = 0;
+    MRT_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, m.device));
+    MRT_REQUIRE(khz > 0, "decode profile: the device reports no wall-clock rate");
+    double t = 0, d = 0, w = 0;
+    for (int f = 0; f < prof_frames_; ++f) {
+      const uint64_t* q = h_prof_ + 4 * f;
+      t += static_cast<double>(q[1] - q[0]);
+      d += static_cast<double>(q[2] - q[1]) - static_cast<double>(q[3]);
+      w += static_cast<double>(q[3]);
+    }
+    const double ms = 1.0 / khz;  // one tick in ms
+    r.temporal_ms = static_cast<float>(t * ms);
+    r.depth_ms = static_cast<float>(d * ms);
+    r.sample_ms = static_cast<float>(w * ms);
+  }
+  return r;
+}
+
+void State::compile(const GenOpts& o) {
+  MRT_HIP_CHECK(hipSetDevice(m.device));
+  const bool had_cross = cross_ready_;
+  const int tl = temporal_len_, dl = depth_len_;
+  if (!had_cross) {  // an encoding of PAD ids, dropped afterwards
+    MRT_HIP_CHECK(hipMemsetAsync(d_enc_tok, 0, static_cast<size_t>(rows) * S * sizeof(int), stream));
+    encode_device();
+  }
+  GenOpts g = o;
+  g.teacher = nullptr;
+  g.record_slices = nullptr;
+  g.record_temporal = nullptr;
+  g.record_drawn = nullptr;
+  g.record_frame_mean = nullptr;
+  std::vector<int32_t> tmp(static_cast<size_t>(std::max(o.num_frames, 1)) * std::max(o.rvq_depth, 1));
+  prev_frames_ = 0;
+  generate(nullptr, g, tmp.data());
+  if (g.speculative && speculating(g)) generate(nullptr, g, tmp.data());  // the speculative graph too
+  cross_ready_ = had_cross;
+  temporal_len_ = tl;
+  depth_len_ = dl;
+  prev_frames_ = 0;  // the dry run's tokens are no drafts
+  spec_acc_ = -1.f;
+  dec_timed_ = false;
+  enc_timed_ = false;
+  prof_frames_ = 0;
 }
 
 float State::phase_trace(uint64_t* out, int n) {

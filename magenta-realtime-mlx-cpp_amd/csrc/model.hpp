@@ -104,6 +104,14 @@ class Model {
   // on `stream` (no wait).  Scratch is the library's fixed per-device array.
   void sample_noalloc(const float* slice_dev, const GenOpts& o, int frame, int level, int32_t* token_dev,
                       hipStream_t stream) const;
+  // Depthformer::token_embedding()(ids) (model.h:127, modules.cpp:110-112),
+  // as the decode loop embeds every fed token (decode.cpp:366-368, 476-477):
+  // rows emb[ids[i]] (model dtype) of n host ids into the device buffer
+  // `out` (n, d_model), enqueued on `s`; waits for it.
+  void embed_tokens(const int32_t* ids, int n, void* out, hipStream_t s);
+  // Depthformer::position_embedding(seq_len) (model.cpp:215-224): the first
+  // seq_len rows of the fp32 sinusoid table into the device buffer `out`.
+  void position_embedding(int seq_len, float* out) const;
   // precompute_{temporal,depth}_biases (model.cpp:302-320): kind 0 temporal,
   // 1 depth; steps 0..n-1 back to back into the device buffer `out` (step f's
   // (H, f + 1) block at element H f (f + 1) / 2).  Waits for the result.
@@ -115,8 +123,15 @@ class Model {
   // model-dtype values -- the layer-0 projection of depth step l when its input
   // is that token's embedding on both rows.  Built on first use for a
   // (codebook, offset) pair, on `s` (waits for it; never during a capture), and
-  // kept until the model is destroyed.  nullptr when levels < 2.
+  // kept until the model is destroyed: (rvq_depth - 1) * codebook * 3 * HD
+  // elements (94 MB in bf16 at d_model 1024, codebook 1024), plus a
+  // kQkvChunkRows x d_model build workspace allocated once.  The first build
+  // for a pair allocates its table (hipMalloc) and frees nothing.  At most
+  // kMaxQkvTables pairs get a table; nullptr for any other pair and when
+  // levels < 2 (the decode then computes layer 0).
   const void* depth_qkv_table(int codebook, int offset, hipStream_t s);
+  static constexpr size_t kMaxQkvTables = 4;
+  static constexpr int kQkvChunkRows = 2048;
 
  private:
   std::vector<void*> allocs_;
@@ -126,6 +141,12 @@ class Model {
   };
   std::mutex qkv_mu_;
   std::vector<QkvTable> qkv_tables_;
+  void* qkv_ws_ = nullptr;  // build workspace of the tables (kQkvChunkRows x d_model)
+  std::vector<float> pe_host_;  // fp32 sinusoid table (max_encoder_length, d_model)
+  static constexpr int kEmbedChunk = 4096;
+  std::mutex embed_mu_;
+  int* embed_ids_dev_ = nullptr;       // kEmbedChunk ids, allocated at the first embed_tokens
+  int32_t* embed_ids_host_ = nullptr;  // pinned staging of the same
   const void* upload(const std::vector<float>& host);
   const void* upload_i32(const std::vector<int>& host);
 };
@@ -208,6 +229,25 @@ class State {
   // pass (accepted drafts and the first disagreement); -1 when it did not speculate.
   float spec_acceptance() const { return spec_acc_; }
   float last_decode_ms(int* launches);
+  // Depthformer::compile_for_inference (model.cpp:709-...): prepares this
+  // state's decode for options `o` ahead of the first real call -- the layer-0
+  // q/k/v table, the captured decode graph (o.use_graph) and the first launch of
+  // every kernel on the path -- by one untimed decode (two when o.speculative,
+  // so the speculative graph is captured too) on the current encoder output, or
+  // on an encoding of PAD ids when there is none.  Afterwards the caches and the
+  // draft history are as before (no encoder output stays if there was none).
+  void compile(const GenOpts& o);
+  // Per-phase GPU times of the last generate call (the MRT_PROFILE_DECODE
+  // breakdown of decode.cpp:36-49, 529-565).  The temporal / depth / draw split
+  // comes from workgroup 0's wall-clock stamps inside the frame kernel, taken
+  // while profiling is on (MRT_PROFILE_DECODE set when the state was created,
+  // or set_profile); -1 where the last call did not record it.
+  struct DecodeProfile {
+    float total_ms = -1.f, encoder_ms = -1.f, temporal_ms = -1.f, depth_ms = -1.f, sample_ms = -1.f;
+    int frames = 0;
+  };
+  void set_profile(bool on) { profile_ = on; }
+  DecodeProfile decode_profile();
   // Raw per-phase timeline of workgroup 0 (MRT_TRACE_PHASES set at state
   // creation): 2 x kTraceSlots device wall-clock stamps, the temporal step and
   // depth level 1 of frame 1 of the last decode.  Returns the clock in MHz.
@@ -247,6 +287,12 @@ class State {
   bool qkv_table_on_ = true;    // frame kernel: layer-0 q/k/v of fed tokens from the model's table (MRT_QKV_TABLE=0: off)
   const void* qkv_table_ = nullptr;  // the table of the current generate call, or nullptr
   hipEvent_t ev_dec_[2] = {nullptr, nullptr};  // around the decode section of generate
+  hipEvent_t ev_enc_[2] = {nullptr, nullptr};  // around the last encoder pass
+  bool enc_timed_ = false;
+  bool profile_ = false;           // frame kernel phase stamps (MRT_PROFILE_DECODE)
+  uint64_t* d_prof_ = nullptr;     // (F, 4) stamps of the last decode
+  uint64_t* h_prof_ = nullptr;     // pinned copy
+  int prof_frames_ = 0;            // frames stamped by the last decode (0: none)
   int dec_launches_ = 0;
   bool dec_timed_ = false;
   // speculative decoding: drafts (the previous call's tokens), the

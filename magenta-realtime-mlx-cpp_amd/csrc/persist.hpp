@@ -157,6 +157,10 @@ struct FrameArgs {
   // Layer 0's q | k | v of every fed-back token (Model::depth_qkv_table for
   // this codebook and codec offset), or nullptr: computed at every level.
   const void* qkv_table;
+  // Optional per-frame phase stamps of workgroup 0 (device wall clock):
+  // [start, temporal stack done, end, ticks spent in the draws] at
+  // prof + 4 * frame; nullptr: none taken.
+  uint64_t* prof;
 };
 // The frame kernel keeps the depth K/V history in LDS: it needs
 // depth layers * levels <= kMaxResidentSlots.

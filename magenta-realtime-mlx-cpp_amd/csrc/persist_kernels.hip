@@ -1644,10 +1644,15 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   __syncthreads();
   if (!ok) return;
   if (at.trace != nullptr && c.blk == 0 && threadIdx.x == 0) at.trace[kTraceStart] = wall_clock64();
+  // phase stamps of workgroup 0 (fa.prof): start, temporal done, draw ticks
+  const bool prof = fa.prof != nullptr && c.blk == 0;
+  uint64_t p_start = 0, p_temporal = 0, p_draw = 0;
+  if (prof) p_start = wall_clock64();
   // ---- temporal step
   StackIO tio{at.in, at.D, 0u, fa.rec_temporal, true, 0, false, 64, at.pos, at.trace, nullptr, true};
   uint32_t x_tag = run_stack<T, true>(c, at, tio);
   if (at.trace != nullptr && c.blk == 0 && threadIdx.x == 0) at.trace[kTraceEnd] = at.trace[kTraceDone] = wall_clock64();
+  if (prof) p_temporal = wall_clock64();
   // ---- depth steps
   const int L = fa.levels, C = fa.codebook, D = ad.D;
   const int code0 = 16 * (at.nlayers + 1), per_step = 16 * (ad.nlayers + 1);
@@ -1694,6 +1699,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       float* lg = c.xsb[c.xsel ^ 1];
       gather_logits<T>(ad, tg_logit, lg, nullptr, fa.rec_slices ? fa.rec_slices + (size_t)l * 2 * C : nullptr);
       if (trace != nullptr && threadIdx.x == 0) trace[kTraceEnd] = wall_clock64();
+      const uint64_t p_gathered = prof ? wall_clock64() : 0;
       if (l + 1 < L && fa.qkv_table == nullptr) prefetch_qkv<T, false>(c, ad, 0);  // lands during the draw
       tok = sample_block<T>(ad.sp, l, slot, pf, ad.teacher != nullptr, ad.tokens, ad.drawn,
                             l + 1 < L ? ad.ll.tok : nullptr, tg_tok, lg, c.sel_hist, c.sel_res, trace);
@@ -1705,6 +1711,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
         draw_prefetch(C, ad.noise + (size_t)(l + 1) * C, ad.teacher, slot + 1, pf);
       else
         frame_mean_store<T>(fs, L, static_cast<T*>(ad.fmean), D);
+      if (prof) p_draw += wall_clock64() - p_gathered;
     } else if (l + 1 < L) {
       // every workgroup waits for the draw (one word, polled by one lane)
       __shared__ int tok_s;
@@ -1723,6 +1730,13 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
       __syncthreads();
       tok = tok_s;
     }
+  }
+  if (prof && threadIdx.x == 0) {
+    uint64_t* o = fa.prof + 4 * ad.frame;
+    st_g(o, p_start);
+    st_g(o + 1, p_temporal);
+    st_g(o + 2, (uint64_t)wall_clock64());
+    st_g(o + 3, p_draw);
   }
 }
 

@@ -11,6 +11,7 @@
 #include "common.hpp"
 #include "device_utils.hpp"
 #include "kernels.hpp"
+#include "persist.hpp"
 
 namespace mrt {
 namespace {
@@ -211,6 +212,8 @@ float probe_handoff(int device, int workgroups, int words, int rounds, int delay
   MRT_REQUIRE(rounds >= 1 && rounds <= 100000, "probe: rounds must be in [1, 100000]");
   MRT_REQUIRE(delay >= 0 && delay <= 256, "probe: delay must be in [0, 256]");
   const double us = probe_ticks_us(device, [&](uint64_t* w, uint64_t* clk, int* err, hipStream_t s) {
+    // its workgroups poll each other, like a persistent grid's: never beside one
+    PersistSection gate(device, s);
     hipLaunchKernelGGL(k_handoff, dim3(workgroups), dim3(256), 0, s, w, words, rounds, delay, clk, err);
   });
   return static_cast<float>(us / rounds);
@@ -223,6 +226,7 @@ float probe_pingpong(int device, int peer, int rounds) {
   MRT_REQUIRE(peer >= 1 && peer < num_cu, "probe: peer must be in [1, CU count)");
   MRT_REQUIRE(rounds >= 1 && rounds <= 100000, "probe: rounds must be in [1, 100000]");
   const double us = probe_ticks_us(device, [&](uint64_t* w, uint64_t* clk, int* err, hipStream_t s) {
+    PersistSection gate(device, s);
     hipLaunchKernelGGL(k_pingpong, dim3(peer + 1), dim3(64), 0, s, w, rounds, peer, clk, err);
   });
   return static_cast<float>(us / (2.0 * rounds));

@@ -174,7 +174,8 @@ __device__ __forceinline__ int wave_draw(const float* __restrict__ logits, const
   const float* nz = p.noise != nullptr
                         ? p.noise + (((size_t)stream * p.noise_frames + frame) * p.rvq_depth + level) * C
                         : nullptr;
-  return wave_draw_rows(l0, l0 + C, nz, p.temperature != 0.0f ? p.seed[stream] : 0, p, frame, level);
+  const uint64_t seed = p.seed != nullptr ? p.seed[stream] : p.seed_value;
+  return wave_draw_rows(l0, l0 + C, nz, p.temperature != 0.0f ? seed : 0, p, frame, level);
 }
 
 // Every level of one frame drawn at once (block l draws level l from logit
@@ -184,7 +185,8 @@ __global__ __launch_bounds__(64) void k_draw_levels(const float* __restrict__ lo
   const int l = blockIdx.x, C = p.codebook;
   const float* l0 = logits + (size_t)(2 * l) * C;
   const float* nz = p.noise != nullptr ? p.noise + ((size_t)frame * p.rvq_depth + l) * C : nullptr;
-  const int bi = wave_draw_rows(l0, l0 + C, nz, p.temperature != 0.0f ? p.seed[0] : 0, p, frame, l);
+  const uint64_t seed = p.seed != nullptr ? p.seed[0] : p.seed_value;
+  const int bi = wave_draw_rows(l0, l0 + C, nz, p.temperature != 0.0f ? seed : 0, p, frame, l);
   if (threadIdx.x == 0) drawn[l] = p.codec_offset + l * C + bi;
 }
 
@@ -290,10 +292,12 @@ void sample_levels(DType dt, int streams, const float* logits, const SampleParam
 // ---- the draw without library allocations ---------------------------------------------
 namespace {
 
-// Scratch of sample_level_noalloc on each device: the draw's seed word at
-// offset 0, then the three feedback row pairs k_sample writes (next depth
-// input, frame sum, frame mean: 2 x d_model elements each, model dtype) from
-// offset 256.  Every call on a device shares its copy, which keeps the last
+// Scratch of sample_level_noalloc on each device: the three feedback row
+// pairs k_sample writes (next depth input, frame sum, frame mean: 2 x d_model
+// elements each, model dtype) from offset 256 (the first 256 bytes are
+// unused).  The caller discards them; the seed travels by value in the
+// kernel arguments, so calls that overlap on one device still draw their own
+// tokens.  Every call on a device shares its copy, which keeps the last
 // call's contents.
 constexpr size_t kNoAllocBytes = 32 * 1024;
 constexpr size_t kNoAllocRows = 256;
@@ -302,8 +306,6 @@ __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
 constexpr int kMaxNoAllocDevices = 64;
 std::mutex g_scratch_mu;
 unsigned char* g_scratch_ptr[kMaxNoAllocDevices];  // device address of `scratch`, per device
-
-__global__ void k_store_seed(uint64_t* dst, uint64_t seed) { *dst = seed; }
 
 }  // namespace
 
@@ -331,13 +333,11 @@ void sample_level_noalloc(DType dt, int device, const void* emb, int D, const fl
     throw Error(1, "sample_noalloc: d_model " + std::to_string(D) + " needs " + std::to_string(need) +
                        " bytes of scratch, more than the fixed " + std::to_string(kNoAllocBytes));
   unsigned char* base = scratch_on(device);
-  uint64_t* seed_dev = reinterpret_cast<uint64_t*>(base);
   unsigned char* rows = base + kNoAllocRows;
   const size_t row_pair = 2 * static_cast<size_t>(D) * esz;
-  hipLaunchKernelGGL(k_store_seed, dim3(1), dim3(1), 0, s, seed_dev, seed);
-  MRT_HIP_CHECK(hipGetLastError());
   SampleParams sp = p;
-  sp.seed = seed_dev;
+  sp.seed = nullptr;
+  sp.seed_value = seed;
   sp.noise = nullptr;
   sp.decided = nullptr;
   sample_level(dt, logits, sp, frame, level, 0, nullptr, token, nullptr, emb, D, rows, rows + row_pair,

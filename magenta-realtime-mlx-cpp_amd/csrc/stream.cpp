@@ -114,6 +114,34 @@ void Stream::build_and_encode(const int32_t* style) {
   st.encode_device();
 }
 
+// The decode options of a chunk (GenerateChunkOptions -> GenerateOptions,
+// system.cpp:236-260).
+GenOpts Stream::gen_opts(const ChunkOpts& o) const {
+  const StreamConfig& c = cfg;
+  MRT_REQUIRE(o.speculative >= 0 && o.speculative <= 2, "generate_chunk: speculative must be 0, 1 or 2");
+  GenOpts g;
+  g.num_frames = c.chunk_frames;
+  g.rvq_depth = c.levels;
+  g.temperature = o.temperature;
+  g.top_k = o.top_k;
+  g.guidance_weight = o.guidance_weight;
+  g.seed = o.has_seed ? o.seed : seed_base_ + static_cast<uint64_t>(chunk_index);
+  g.codebook = c.codebook;
+  g.codec_offset = c.codec_offset;
+  g.teacher = o.teacher;
+  g.use_graph = o.use_graph;
+  g.speculative = o.speculative != 0;
+  return g;
+}
+
+void Stream::compile(const ChunkOpts& o) {
+  MRT_HIP_CHECK(hipSetDevice(st.m.device));
+  // the encoder inputs of the current context (masked style) and the encoder
+  // itself run once too, unless a pipelined encoder output must be kept
+  if (!pre_valid_) build_and_encode(nullptr);
+  st.compile(gen_opts(o));
+}
+
 // Encoder (or the pipelined one), decode, llm_to_rvq and the roll; returns
 // with the state's stream idle.
 void Stream::token_half(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out) {
@@ -132,18 +160,7 @@ void Stream::token_half(const int32_t* style, const ChunkOpts& o, int32_t* llm_o
   pre_valid_ = false;
   if (!reuse) build_and_encode(style);
 
-  GenOpts g;
-  g.num_frames = c.chunk_frames;
-  g.rvq_depth = c.levels;
-  g.temperature = o.temperature;
-  g.top_k = o.top_k;
-  g.guidance_weight = o.guidance_weight;
-  g.seed = o.has_seed ? o.seed : seed_base_ + static_cast<uint64_t>(chunk_index);
-  g.codebook = c.codebook;
-  g.codec_offset = c.codec_offset;
-  g.teacher = o.teacher;
-  g.use_graph = o.use_graph;
-  MRT_REQUIRE(o.speculative >= 0 && o.speculative <= 2, "generate_chunk: speculative must be 0, 1 or 2");
+  GenOpts g = gen_opts(o);
   g.speculative = o.speculative == 1 || (o.speculative == 2 && spec_pause_ == 0);
   const size_t n = static_cast<size_t>(c.chunk_frames) * c.levels;
   llm_tmp_.resize(n);

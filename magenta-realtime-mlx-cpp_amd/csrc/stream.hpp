@@ -86,6 +86,9 @@ class Stream {
   // style: host (style_depth) ids or null (masked).  llm_out / rvq_out: host
   // (chunk_frames, levels) or null.
   void generate_chunk(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out);
+  // compile_for_inference for this stream's chunks (State::compile with the
+  // chunk's decode options); the context and chunk index are not touched.
+  void compile(const ChunkOpts& o);
   // The whole System::generate_chunk (system.cpp:177-440): the token half,
   // then the codec decode of [the crossfade frame, the chunk] on the attached
   // codec's stream (overlapping the pipelined encoder of the next chunk) and
@@ -103,6 +106,7 @@ class Stream {
   void upload_style(const int32_t* style);
   void build_and_encode(const int32_t* style);
   void token_half(const int32_t* style, const ChunkOpts& o, int32_t* llm_out, int32_t* rvq_out);
+  GenOpts gen_opts(const ChunkOpts& o) const;
   void kick_pipeline(const int32_t* style);
   Codec* codec_ = nullptr;
   int* d_codec_tok_ = nullptr;

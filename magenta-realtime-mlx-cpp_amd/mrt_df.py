@@ -90,6 +90,11 @@ class _GenOpts(ctypes.Structure):
     ]
 
 
+class _DecodeProfile(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_float) for n in ("total_ms", "encoder_ms", "bias_ms", "temporal_ms", "depth_ms",
+                                               "sample_ms")] + [("frames", ctypes.c_int32)]
+
+
 class _StreamConfig(ctypes.Structure):
     _fields_ = [(f, ctypes.c_int32) for f in (
         "chunk_frames", "context_frames", "codebook_size", "encoder_codec_rvq_depth",
@@ -279,6 +284,12 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "mrt_df_state_decode_time": (i32, [vp, ctypes.POINTER(ctypes.c_float), ctypes.POINTER(i32)]),
         "mrt_df_state_phase_trace": (i32, [vp, ctypes.POINTER(ctypes.c_uint64), i32, ctypes.POINTER(ctypes.c_float)]),
         "mrt_df_state_spec_acceptance": (i32, [vp, ctypes.POINTER(ctypes.c_float)]),
+        "mrt_df_state_set_profile": (i32, [vp, i32]),
+        "mrt_df_state_decode_profile": (i32, [vp, ctypes.POINTER(_DecodeProfile)]),
+        "mrt_df_state_compile": (i32, [vp, ctypes.POINTER(_GenOpts)]),
+        "mrt_df_stream_compile": (i32, [vp, ctypes.POINTER(_ChunkOpts)]),
+        "mrt_df_embed_tokens": (i32, [vp, ctypes.POINTER(ctypes.c_int32), i32, vp, vp]),
+        "mrt_df_position_embedding": (i32, [vp, i32, vp]),
         "mrt_stream_config_default": (None, [ctypes.POINTER(_StreamConfig)]),
         "mrt_chunk_opts_default": (None, [ctypes.POINTER(_ChunkOpts)]),
         "mrt_df_stream_create": (i32, [vp, ctypes.POINTER(_StreamConfig), ctypes.POINTER(vp)]),
@@ -394,6 +405,26 @@ class Depthformer:
         torch.cuda.synchronize(self.device)
         _check(self.lib, self.lib.mrt_df_precompute_biases(self._h, {"temporal": 0, "depth": 1}[kind], n, _dptr(buf)))
         return [buf[H * f * (f + 1) // 2: H * (f + 1) * (f + 2) // 2].view(H, f + 1) for f in range(n)]
+
+    def token_embedding(self, ids, out=None):
+        """Depthformer::token_embedding()(ids) (model.h:127): a (len(ids), d_model)
+        device tensor in the model dtype, rows emb[ids] (mrt_df_embed_tokens)."""
+        torch = _torch()
+        a = np.ascontiguousarray(np.asarray(ids).reshape(-1), dtype=np.int32)
+        if out is None:
+            out = torch.empty((a.size, self.config.d_model), dtype=self.torch_dtype, device=f"cuda:{self.device}")
+        torch.cuda.synchronize(self.device)
+        _check(self.lib, self.lib.mrt_df_embed_tokens(self._h, _i32_ptr(a), a.size, _dptr(out), None))
+        return out
+
+    def position_embedding(self, seq_len: int):
+        """Depthformer::position_embedding(seq_len) (model.cpp:215-224): the fp32
+        sinusoid rows (seq_len, d_model) as a device tensor."""
+        torch = _torch()
+        out = torch.empty((seq_len, self.config.d_model), dtype=torch.float32, device=f"cuda:{self.device}")
+        torch.cuda.synchronize(self.device)
+        _check(self.lib, self.lib.mrt_df_position_embedding(self._h, seq_len, _dptr(out)))
+        return out
 
     @property
     def torch_dtype(self):
@@ -576,6 +607,24 @@ class State:
         _check(self.lib, self.lib.mrt_df_state_phase_trace(self._h, buf, 1024, ctypes.byref(mhz)))
         return np.frombuffer(buf, dtype=np.uint64).reshape(2, 512).copy(), float(mhz.value)
 
+    def compile_for_inference(self, opts: GenOptions) -> None:
+        """Depthformer::compile_for_inference for this state's decode with
+        ``opts`` (mrt_df_state_compile): the q/k/v table, the captured graph and
+        the first launch of every kernel happen here, not in the first chunk."""
+        o = self._opts(opts)
+        _check(self.lib, self.lib.mrt_df_state_compile(self._h, ctypes.byref(o)))
+
+    def set_profile(self, on: bool = True) -> None:
+        """Phase stamps of the frame kernel for later decodes (mrt_df_state_set_profile)."""
+        _check(self.lib, self.lib.mrt_df_state_set_profile(self._h, 1 if on else 0))
+
+    def decode_profile(self) -> dict:
+        """The MRT_PROFILE_DECODE split of the last generate_tokens call (GPU ms):
+        total, encoder, bias, temporal, depth, sample; -1 where not recorded."""
+        p = _DecodeProfile()
+        _check(self.lib, self.lib.mrt_df_state_decode_profile(self._h, ctypes.byref(p)))
+        return {n: (int(getattr(p, n)) if n == "frames" else float(getattr(p, n))) for n, _ in p._fields_}
+
     def spec_acceptance(self) -> float:
         """Share of the last generate_tokens call's levels taken from the
         speculative verification pass (-1: it did not speculate)."""
@@ -692,18 +741,28 @@ class Stream:
         (chunk_frames * samples_per_frame, 2) float32)."""
         return self.generate_chunk(style, opts, teacher, audio=True)
 
+    @staticmethod
+    def _chunk_opts(opts: ChunkOptions) -> _ChunkOpts:
+        return _ChunkOpts(temperature=opts.temperature, top_k=opts.top_k, guidance_weight=opts.guidance_weight,
+                          has_seed=0 if opts.seed is None else 1,
+                          seed=0 if opts.seed is None else opts.seed & ((1 << 64) - 1),
+                          pipeline_encoder=1 if opts.pipeline_encoder else 0,
+                          use_graph=1 if opts.use_graph else 0, teacher=None,
+                          speculative=int(opts.speculative))
+
+    def compile_for_inference(self, opts: ChunkOptions) -> None:
+        """compile_for_inference for this stream's chunks (mrt_df_stream_compile,
+        system.cpp:130): the first chunk then pays no one-time work."""
+        o = self._chunk_opts(opts)
+        _check(self.lib, self.lib.mrt_df_stream_compile(self._h, ctypes.byref(o)))
+
     def generate_chunk(self, style: Optional[Sequence[int]], opts: ChunkOptions,
                        teacher: Optional[np.ndarray] = None, audio: bool = False):
         """Returns (llm ids, rvq codes), both (chunk_frames, levels) int32
         (and the chunk's audio with ``audio``)."""
         cfg = self.cfg
         shape = (cfg.chunk_frames, cfg.decoder_codec_rvq_depth)
-        o = _ChunkOpts(temperature=opts.temperature, top_k=opts.top_k, guidance_weight=opts.guidance_weight,
-                       has_seed=0 if opts.seed is None else 1,
-                       seed=0 if opts.seed is None else opts.seed & ((1 << 64) - 1),
-                       pipeline_encoder=1 if opts.pipeline_encoder else 0,
-                       use_graph=1 if opts.use_graph else 0, teacher=None,
-                       speculative=int(opts.speculative))
+        o = self._chunk_opts(opts)
         keep = []
         if teacher is not None:
             tt = np.ascontiguousarray(teacher, dtype=np.int32)

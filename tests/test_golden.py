@@ -6,10 +6,12 @@ restatement).  GPU: the HIP path, called through the C ABI, matches it to the
 path's tolerances: fp32 <= 1e-4 and bf16 <= 2e-2 norm-wise relative error,
 teacher tokens fed back bit-exactly, >= 99 % of the free-running fp32 draws
 equal; fp32 argmax agreement >= 99 %; bf16 >= 95 % with every disagreement a
-near-tie (top-1/top-2 margin within twice that draw's logit error: 8 codes
-per level leave such ties).  The same near-tie rule, with no floor on the
-agreement, is what the bf16 tests at the benchmark dims apply: between two bf16
-evaluations a flat >= 99 % is not attainable with random weights and guidance 5.
+near-tie (top-1/top-2 margin within FLIP_SIGMAS = 8 x the RMS of that draw's
+guided-logit error, draw_check.assert_argmax_flips_are_near_ties: 8 codes per
+level leave such ties).  At the benchmark dims the bf16 tests apply the same
+near-tie rule with a floor relative to the oracle's own bf16 agreement with
+fp32 (chunk_check): between two bf16 evaluations a flat >= 99 % is not
+attainable with random weights and guidance 5.
 """
 
 from __future__ import annotations
@@ -93,7 +95,8 @@ def test_hip_matches_fixture_teacher_forced(gpu_available, gen, fx, dtype, tol):
         assert (ga == oa).mean() >= 0.99
     else:
         # 8 candidates and guidance 5 leave near-ties at this size: every flip's
-        # top-1/top-2 margin must be within the bf16 noise of that draw's guided logits
+        # top-1/top-2 margin must be within FLIP_SIGMAS x the RMS of that draw's
+        # guided-logit error
         agree = assert_argmax_flips_are_near_ties(sl, fx[f"{dtype}_tf_slices"])
         assert agree >= 0.95
     np.testing.assert_array_equal(rec["frame_mean"].float().cpu().numpy(), fx[f"{dtype}_tf_frame_mean"])

@@ -6,9 +6,12 @@ steps) per dtype.
 
 Tolerances (norm-wise relative error): fp32 <= 1e-4, bf16 <= 2e-2, fp16 <= 5e-3
 per level slice (fp16's unit roundoff 2^-11 is 8x below bf16's 2^-8); fp32
-teacher-forced argmax agreement >= 99 %; in bf16 and fp16 every argmax flip
-must be a near-tie (the oracle's top-1 / top-2 margin <= 8 x the RMS of that
-draw's guided-logit error, draw_check.assert_argmax_flips_are_near_ties);
+teacher-forced argmax agreement >= 99 %; in bf16 and fp16 the agreement with the
+fp32 oracle is at least the oracle's own 16-bit restatement's less a slack, and
+every argmax flip must be a near-tie (the oracle's top-1 / top-2 margin <=
+FLIP_SIGMAS = 8 x the RMS of that draw's guided-logit error,
+draw_check.assert_argmax_flips_are_near_ties); the 50-frame bf16 chunk meets
+chunk_check.assert_bf16_chunk against the fp32 and bf16 oracles;
 teacher tokens fed back and frame means bit-exact; a device draw that differs
 from the oracle sampler's must be an ulp-level tie of its scaled + noise.
 Besides two frames of every path, the whole 50-frame chunk runs teacher-forced
@@ -25,6 +28,7 @@ import dataclasses
 
 import numpy as np
 import pytest
+from chunk_check import argmax_agreement, assert_bf16_chunk
 from draw_check import assert_argmax_flips_are_near_ties, assert_draws
 
 pytestmark = pytest.mark.gpu
@@ -100,6 +104,7 @@ def _hip(env, dtype, path="frame"):
 
 
 _ORACLE = {}
+_CHUNK = {}  # the 50-frame oracle records per dtype (the bf16 chunk test compares with fp32's)
 
 
 def _oracle_cached(env, dtype):
@@ -132,10 +137,14 @@ def test_full_size_teacher_forced(env, dtype, tol, path):
         # Two 16-bit evaluations of the same model differ by rounding noise
         # (~1e-2 relative after 36 layers), and guidance weight 5 turns that into
         # argmax flips wherever the top-2 margin is small.  Every flip must be
-        # such a near-tie: margin <= 2 x that draw's guided-logit error.
+        # such a near-tie (margin <= FLIP_SIGMAS x the RMS of that draw's
+        # guided-logit error), and the agreement with the fp32 oracle may fall
+        # below the oracle's own 16-bit restatement's by at most 4 of the 32
+        # draws (a systematic bias that flips many near-ties fails here).
         assert_argmax_flips_are_near_ties(g["slices"], o["slices"])
         o32 = _oracle_cached(env, "fp32")
         assert rel(g["slices"], o32["slices"]) <= tol
+        assert argmax_agreement(g["slices"], o32["slices"]) >= argmax_agreement(o["slices"], o32["slices"]) - 4 / 32
     np.testing.assert_array_equal(g["frame_mean"], o["frame_mean"])
     # The device draw given its own logits: the oracle's sampler (CFG, top-k 40,
     # T 1.1, Philox Gumbel noise) on the recorded slices; a disagreement passes
@@ -166,23 +175,27 @@ def test_full_size_step_entry_points(env, dtype, tol):
     D, C = env["cfg"].d_model, 1024
     dev = lambda a: torch.tensor(np.asarray(a, dtype=np.float32), dtype=m.torch_dtype, device="cuda")
     for f in range(FRAMES):
-        t_in = om.embed(np.zeros((2,), dtype=np.int64)) if f == 0 else o["frame_mean"][f - 1]
-        out = st.temporal_step(dev(t_in), f).float().cpu().numpy()
+        # the fed tokens are embedded by the library (token_embedding, model.h:127),
+        # as the reference's loop does (decode.cpp:366-368, 476-477)
+        t_in = m.token_embedding([0, 0]) if f == 0 else dev(o["frame_mean"][f - 1])
+        out = st.temporal_step(t_in, f).float().cpu().numpy()
         assert rel(out, o["temporal_out"][f]) <= tol, f
         cache = om.empty_depth_cache()
         for l in range(16):
-            x = o["temporal_out"][f] if l == 0 else om.embed(np.full((2,), env["teacher"][f, l - 1], dtype=np.int64))
+            tok = env["teacher"][f, l - 1] if l > 0 else None
+            x = o["temporal_out"][f] if l == 0 else om.embed(np.full((2,), tok, dtype=np.int64))
+            xd = dev(x) if l == 0 else m.token_embedding([tok, tok])
             lo = 2 + C * l
             if f == 0 and l % 4 == 0:
                 exp = om.depth_step(np.asarray(x, dtype=np.float32)[:, None], cache, l)
-                got = st.depth_step(dev(x), l).cpu().numpy()
+                got = st.depth_step(xd, l).cpu().numpy()
                 assert got.shape == (2, env["cfg"].vocab_size)
                 assert rel(got, exp) <= tol, (f, l)
                 assert rel(got[:, lo:lo + C], o["slices"][f, l]) <= tol, (f, l)
             else:
                 if f == 0:
                     om.depth_step(np.asarray(x, dtype=np.float32)[:, None], cache, l)
-                got = st.depth_step(dev(x), l, level=l, codebook_size=C, codec_offset=2).cpu().numpy()
+                got = st.depth_step(xd, l, level=l, codebook_size=C, codec_offset=2).cpu().numpy()
                 assert rel(got, o["slices"][f, l]) <= tol, (f, l)
     st.close()
     m.close()
@@ -263,16 +276,38 @@ def test_full_chunk_teacher_forced(env, fp32_model, bf16_model, dtype, tol):
     o = O.GenerateOptions(num_frames=F, rvq_depth=L, temperature=1.1, top_k=40, guidance_weight=5.0, seed=5,
                           codebook_size=C, codec_offset=2)
     O.generate_tokens(om, env["tok"], o, teacher=teacher, record=orec, enc_out=_oracle_cached(env, dtype)["enc_out"])
+    _CHUNK[dtype] = orec
     errs = np.array([[rel(sl[f, l], orec["slices"][f, l]) for l in range(L)] for f in range(F)])
-    assert errs.max() <= tol, (errs.max(), np.unravel_index(errs.argmax(), errs.shape))
+    if dtype == "fp32":
+        assert errs.max() <= tol, (errs.max(), np.unravel_index(errs.argmax(), errs.shape))
     terrs = [rel(tp[f], orec["temporal_out"][f]) for f in range(F)]
     assert max(terrs) <= tol, (max(terrs), int(np.argmax(terrs)))
+    # The temporal_step entry point (one persistent launch) at every ring
+    # position 0..49 on the oracle's own inputs: emb(PAD) at frame 0, then the
+    # oracle's frame means.
+    m = model
+    st = m.new_state(max_frames=F)
+    st.encode(env["tok"])
+    dev = lambda a: torch.tensor(np.asarray(a, dtype=np.float32), dtype=m.torch_dtype, device="cuda")
+    eerrs = []
+    for f in range(F):
+        t_in = m.token_embedding([0, 0]) if f == 0 else dev(orec["frame_mean"][f - 1])
+        eerrs.append(rel(st.temporal_step(t_in, f).float().cpu().numpy(), orec["temporal_out"][f]))
+    st.close()
+    assert max(eerrs) <= tol, (max(eerrs), int(np.argmax(eerrs)))
     np.testing.assert_array_equal(fm, orec["frame_mean"])
     if dtype == "fp32":
         assert (_guided_argmax(sl) == _guided_argmax(orec["slices"])).mean() >= 0.99
     else:
-        agree = assert_argmax_flips_are_near_ties(sl, orec["slices"])
-        print(f"bf16 50-frame chunk: max slice rel-err {errs.max():.3e}, argmax agreement {agree:.3f}")
+        # against the fp32 oracle on the same tokens (chunk_check): every slice
+        # within 2e-2, the chunk's error no larger than the bf16 oracle's own
+        if "fp32" not in _CHUNK:
+            _CHUNK["fp32"] = {}
+            O.generate_tokens(O.OracleDepthformer(env["w"], O.DepthformerConfig(**dataclasses.asdict(env["cfg"])),
+                                                  mode="fp32"), env["tok"], o, teacher=teacher,
+                              record=_CHUNK["fp32"], enc_out=_oracle_cached(env, "fp32")["enc_out"])
+        figs = assert_bf16_chunk(sl, orec["slices"], _CHUNK["fp32"]["slices"])
+        print(f"bf16 50-frame chunk: {figs}")
     for i, (k, v) in tk.items():
         assert rel(k, orec["temporal_cache"][i]["k"]) <= tol, i
         assert rel(v, orec["temporal_cache"][i]["v"]) <= tol, i
