@@ -374,9 +374,10 @@ typedef struct mrt_chunk_opts {
   int32_t use_graph;        /* replay the decode loop from a captured hipGraph */
   const int32_t* teacher;   /* optional host (chunk_frames, levels) ids fed back instead of draws */
   int32_t speculative;      /* speculative depth decoding, drafts = the previous chunk's tokens:
-                               0 off, 1 on, 2 adaptive (speculate while the last speculative chunk
-                               took >= 1/4 of its levels from the verification pass; after one below,
-                               4 chunks plain, then try again) */
+                               0 off, 1 on, 2 adaptive (a chunk speculates its first 2 frames only;
+                               when >= 1/4 of those levels came from the verification pass, whole
+                               chunks speculate while that holds; after a miss, 4 chunks plain
+                               before the next probe, doubling per further miss up to 64) */
 } mrt_chunk_opts;
 
 typedef struct mrt_df_stream mrt_df_stream;

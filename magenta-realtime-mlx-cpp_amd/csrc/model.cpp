@@ -599,9 +599,14 @@ void State::reserve_epochs(uint32_t n) {
   epochs_used_ += n;
 }
 
+int State::spec_count(const GenOpts& o) const {
+  if (!spec_drafts_) return 0;
+  return o.spec_frames > 0 ? std::min(o.spec_frames, o.num_frames) : o.num_frames;
+}
+
 int State::decode_launches(const GenOpts& o) const {
-  if (spec_drafts_) return o.num_frames * o.rvq_depth;  // temporal + L - 1 depth steps per frame
-  return frame_kernel_ ? o.num_frames : o.num_frames * (1 + o.rvq_depth);
+  const int ns = spec_count(o);  // speculative frames: temporal + L - 1 depth steps each
+  return ns * o.rvq_depth + (o.num_frames - ns) * (frame_kernel_ ? 1 : 1 + o.rvq_depth);
 }
 
 StepArgs State::temporal_args(const void* in, int f, void* out) const {
@@ -702,26 +707,33 @@ void State::launch_frame_p(const GenOpts& o, int f) {
 void State::enqueue_decode_p(const GenOpts& o) {
   const Config& c = m.cfg;
   const int D = c.d_model, C = o.codebook, L = o.rvq_depth;
-  const size_t row_bytes = static_cast<size_t>(rows) * D * esz();
   embed_fill(m.dt, m.emb, D, 0, rows, t_in, stream);
   gumbel_table(d_seed, o.num_frames, L, C, noise_, stream);
   SampleParams sp{o.guidance_weight, o.temperature, o.top_k, C, o.codec_offset, L, d_seed};
-  for (int f = 0; f < o.num_frames; ++f) {
-    if (frame_kernel_) {
-      launch_frame_p(o, f);
-    } else {
-      launch_temporal_p(t_in, f, t_out);
-      if (o.record_temporal) copy(static_cast<char*>(o.record_temporal) + f * row_bytes, t_out, row_bytes);
-      for (int l = 0; l < L; ++l) {
-        const char* head = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset + C * l) * D * esz();
-        float* rec = o.record_slices ? o.record_slices + (static_cast<size_t>(f) * L + l) * rows * C : nullptr;
-        launch_depth_p(l == 0 ? t_out : d_in, l, head, C, slice, rec);
-        sample_level(m.dt, slice, sp, f, l, f * L + l, o.teacher ? d_teacher : nullptr, d_tokens, o.record_drawn,
-                     m.emb, D, d_in, fsum, t_in, stream);
-      }
+  for (int f = 0; f < o.num_frames; ++f) enqueue_plain_frame(o, f, sp);
+}
+
+// Frame f of the plain persistent decode: one frame-kernel launch, or one
+// launch per step plus the sampling kernel; t_in holds the frame's input
+// (emb(PAD) or the previous frame mean) and receives this frame's mean.
+void State::enqueue_plain_frame(const GenOpts& o, int f, const SampleParams& sp) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, C = o.codebook, L = o.rvq_depth;
+  const size_t row_bytes = static_cast<size_t>(rows) * D * esz();
+  if (frame_kernel_) {
+    launch_frame_p(o, f);
+  } else {
+    launch_temporal_p(t_in, f, t_out);
+    if (o.record_temporal) copy(static_cast<char*>(o.record_temporal) + f * row_bytes, t_out, row_bytes);
+    for (int l = 0; l < L; ++l) {
+      const char* head = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset + C * l) * D * esz();
+      float* rec = o.record_slices ? o.record_slices + (static_cast<size_t>(f) * L + l) * rows * C : nullptr;
+      launch_depth_p(l == 0 ? t_out : d_in, l, head, C, slice, rec);
+      sample_level(m.dt, slice, sp, f, l, f * L + l, o.teacher ? d_teacher : nullptr, d_tokens, o.record_drawn,
+                   m.emb, D, d_in, fsum, t_in, stream);
     }
-    if (o.record_frame_mean) copy(static_cast<char*>(o.record_frame_mean) + f * row_bytes, t_in, row_bytes);
   }
+  if (o.record_frame_mean) copy(static_cast<char*>(o.record_frame_mean) + f * row_bytes, t_in, row_bytes);
 }
 
 // Speculation runs when asked for, on the bf16 persistent path, with drafts
@@ -754,7 +766,12 @@ void State::enqueue_decode_spec(const GenOpts& o) {
   SampleParams sp_rest = sp_all;
   sp_rest.noise_frames = o.num_frames;  // one stream: noise row (frame * L + level)
   const char* head0 = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset) * D * esz();
+  const int ns = spec_count(o);
   for (int f = 0; f < o.num_frames; ++f) {
+    if (f >= ns) {  // past the speculated frames: the plain decode
+      enqueue_plain_frame(o, f, sp);
+      continue;
+    }
     int* tok = d_tokens + static_cast<size_t>(f) * L;
     launch_temporal_p(t_in, f, t_out);
     if (o.record_temporal) copy(static_cast<char*>(o.record_temporal) + f * row_bytes, t_out, row_bytes);
@@ -1190,7 +1207,7 @@ hipGraphExec_t State::decode_graph(const GenOpts& o) {
   const std::vector<double> key = {
       (double)o.num_frames, (double)o.rvq_depth, (double)o.temperature, (double)o.top_k,
       (double)o.guidance_weight, (double)o.codebook, (double)o.codec_offset, o.teacher ? 1.0 : 0.0,
-      spec_drafts_ ? 1.0 : 0.0, profile_ ? 1.0 : 0.0,
+      spec_drafts_ ? 1.0 : 0.0, (double)spec_count(o), profile_ ? 1.0 : 0.0,
       (double)reinterpret_cast<uintptr_t>(o.record_slices),
       (double)reinterpret_cast<uintptr_t>(o.record_temporal),
       (double)reinterpret_cast<uintptr_t>(o.record_drawn),
@@ -1287,18 +1304,19 @@ void State::generate(const int32_t* enc_tokens_host, const GenOpts& o, int32_t* 
     MRT_HIP_CHECK(hipMemcpyAsync(h_prof_, d_prof_, static_cast<size_t>(prof_frames_) * 4 * sizeof(uint64_t),
                                  hipMemcpyDeviceToHost, stream));
   MRT_HIP_CHECK(hipMemcpyAsync(h_pinned, d_tokens, nt * 4, hipMemcpyDeviceToHost, stream));
-  if (spec_drafts_)
-    MRT_HIP_CHECK(hipMemcpyAsync(h_pinned + nt, sdecided_, static_cast<size_t>(o.num_frames) * 4,
-                                 hipMemcpyDeviceToHost, stream));
+  const int nspec = spec_count(o);
+  if (nspec > 0)
+    MRT_HIP_CHECK(hipMemcpyAsync(h_pinned + nt, sdecided_, static_cast<size_t>(nspec) * 4, hipMemcpyDeviceToHost,
+                                 stream));
   MRT_HIP_CHECK(hipStreamSynchronize(stream));
   check_device_error();
   print_trace();
   std::memcpy(out_host, h_pinned, nt * 4);
   spec_acc_ = -1.f;
-  if (spec_drafts_) {  // levels 0..n of frame f came from the verification pass (n = L: all)
+  if (nspec > 0) {  // levels 0..n of frame f came from the verification pass (n = L: all)
     long from_pass = 0;
-    for (int f = 0; f < o.num_frames; ++f) from_pass += std::min(h_pinned[nt + f] + 1, o.rvq_depth);
-    spec_acc_ = static_cast<float>(from_pass) / static_cast<float>(nt);
+    for (int f = 0; f < nspec; ++f) from_pass += std::min(h_pinned[nt + f] + 1, o.rvq_depth);
+    spec_acc_ = static_cast<float>(from_pass) / static_cast<float>(static_cast<long>(nspec) * o.rvq_depth);
   }
   temporal_len_ = o.num_frames;
   depth_len_ = o.rvq_depth;

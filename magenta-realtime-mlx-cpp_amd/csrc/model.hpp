@@ -178,6 +178,9 @@ struct GenOpts {
   // Speculative depth decoding (decode.cpp:150-237, 380-446) with the previous
   // call's tokens as the drafts: bf16 persistent path, no teacher.
   bool speculative = false;
+  // Speculate only the first spec_frames frames (0: every frame); the rest of
+  // the chunk decodes as usual.  The stream's adaptive mode probes with it.
+  int spec_frames = 0;
   float* record_slices = nullptr;    // device (F, L, rows, C)
   void* record_temporal = nullptr;   // device (F, rows, D)
   int* record_drawn = nullptr;       // device (F, L)
@@ -267,6 +270,8 @@ class State {
   void enqueue_decode_p(const GenOpts& o);
   void enqueue_decode_spec(const GenOpts& o);
   bool speculating(const GenOpts& o) const;
+  int spec_count(const GenOpts& o) const;  // frames of this call that speculate
+  void enqueue_plain_frame(const GenOpts& o, int f, const SampleParams& sp);
   int decode_launches(const GenOpts& o) const;
   void reserve_epochs(uint32_t n);
   void check_device_error();

@@ -251,9 +251,11 @@ __device__ __forceinline__ float rsqrt_nr(float x) {
   return y * fmaf(-0.5f * x * y, y, 1.5f);
 }
 
-// Value of `v` held by lane `src` (src - lane is wave-uniform).
+// Value of `v` held by lane `src` (src - lane is wave-uniform): the lane's own
+// value when they coincide (no LDS round trip), else a lane shuffle.
 __device__ __forceinline__ float from_lane(float v, int src) {
-  return src == (int)(threadIdx.x & 63) ? v : __shfl(v, src & 63, 64);
+  if (uniform(src - (int)(threadIdx.x & 63)) == 0) return v;
+  return __shfl(v, src & 63, 64);
 }
 
 // ---- tagged words -------------------------------------------------------------------
@@ -479,9 +481,11 @@ constexpr int kNBuf = 12;  // 16-byte weight registers per thread
 
 // Loads the rows of one batch (R rows of P parts; row indices wave-uniform)
 // into registers; 16-byte chunks past the end of a row are zero.  (The zero
-// fill makes the compiler wait for older loads of the wave before each row;
-// with vmcnt in order, that staggering keeps the next poll from queueing
-// behind a whole batch, which measured faster than issuing every load at once.)
+// fill makes the compiler wait for older memory operations of the wave before
+// each row -- the previous phase's result stores too, a store round trip --
+// so at most a few loads per wave are in flight at a time.  Unconditional
+// loads with no such waits measured slower: with vmcnt in order, the next
+// poll then queues behind every weight load of the phase.)
 template <typename T, int NV, int P, bool NT, class RowOf>
 __device__ __forceinline__ void fetch_batch(uint4 (&buf)[kNBuf], const T* W, int K, int b0, int nb, RowOf row_of) {
   constexpr int V = St<T>::kVec;
@@ -590,10 +594,12 @@ __device__ __forceinline__ void dot_batch(const uint4 (&buf)[kNBuf], int b0, int
       t[2 * p + 1] = acc[0][p][1];
     }
     tsum<2 * P>(t);
+    // each total sits in a known lane: read it into a scalar, no LDS round trip
 #pragma unroll
     for (int p = 0; p < P; ++p)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) v[p][c] = __shfl(t[0], tsum_lane<2 * P>(2 * p + c), 64);
+      for (int c = 0; c < 2; ++c)
+        v[p][c] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t[0]), tsum_lane<2 * P>(2 * p + c)));
   } else {
     constexpr int N = 2 * P * R;
     float t[N];
@@ -1596,9 +1602,11 @@ __device__ __forceinline__ bool start(Ctx<T>& c, const LLBufs& ll, int bph) {
 
 // One step launch (the temporal_step / depth_step API): a decoder stack, then
 // for depth the level-sliced head with the logits copied to a.logits.
-template <typename T, bool CROSS>
+template <typename T, bool CROSS, bool TRACE>
 __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_step(StepArgs a) {
   MRT_DECLARE_LDS(T);
+  // the timeline of workgroup 0 exists only in the TRACE instance
+  uint64_t* const trace = TRACE ? a.trace : nullptr;
   const bool ok = start<T>(c, a.ll, a.bph);
   if (a.nlayers > 0) prefetch_qkv<T, CROSS>(c, a, 0);
   __syncthreads();
@@ -1609,14 +1617,14 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
     if (c.blk == 0 && threadIdx.x == 0) astore(a.ll.seq, c.ep + 1u);
     return;
   }
-  if (a.trace != nullptr && c.blk == 0 && threadIdx.x == 0) a.trace[kTraceStart] = wall_clock64();
-  StackIO io{a.in, a.D, 0u, CROSS ? a.out : nullptr, !CROSS, 0, false, 64, a.pos, a.trace, nullptr, true};
+  if (trace != nullptr && c.blk == 0 && threadIdx.x == 0) trace[kTraceStart] = wall_clock64();
+  StackIO io{a.in, a.D, 0u, CROSS ? a.out : nullptr, !CROSS, 0, false, 64, a.pos, trace, nullptr, true};
   const uint32_t x_tag = run_stack<T, CROSS>(c, a, io);
   if constexpr (!CROSS) {
     const T* hw = static_cast<const T*>(a.head_w);
     prefetch_head<T>(c, a, hw);
     const uint32_t tg = c.tag(16 * a.nlayers + kPhLogit);
-    run_head<T>(c, a, hw, x_tag, tg, a.trace);
+    run_head<T>(c, a, hw, x_tag, tg, trace);
     if (c.blk == 0 && threadIdx.x == 0) astore(a.ll.seq, c.ep + 1u);  // every workgroup has started
     if (c.blk == 0) {
       __syncthreads();
@@ -1625,7 +1633,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   } else {
     if (c.blk == 0 && threadIdx.x == 0) astore(a.ll.seq, c.ep + 1u);  // every workgroup has read the epoch
   }
-  if (a.trace != nullptr && c.blk == 0 && threadIdx.x == 0) a.trace[kTraceEnd] = a.trace[kTraceDone] = wall_clock64();
+  if (trace != nullptr && c.blk == 0 && threadIdx.x == 0) trace[kTraceEnd] = trace[kTraceDone] = wall_clock64();
 }
 
 // One frame of the decode loop in one launch (decode.cpp:339-486): the
@@ -1634,24 +1642,27 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
 // token as a tagged word; every workgroup then reads that token's embedding
 // row as the next depth input.  The depth K/V history stays in the LDS of the
 // attention workgroups; ring slots are still written to memory.
-template <typename T>
+template <typename T, bool TRACE>
 __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_frame(FrameArgs fa) {
   MRT_DECLARE_LDS(T);
   const StepArgs& at = fa.t;
   const StepArgs& ad = fa.d;
+  // the timelines of workgroup 0 exist only in the TRACE instance
+  uint64_t* const t_trace = TRACE ? at.trace : nullptr;
+  uint64_t* const d_trace = TRACE ? ad.trace : nullptr;
   const bool ok = start<T>(c, at.ll, at.bph);
   prefetch_qkv<T, true>(c, at, 0);
   __syncthreads();
   if (!ok) return;
-  if (at.trace != nullptr && c.blk == 0 && threadIdx.x == 0) at.trace[kTraceStart] = wall_clock64();
+  if (t_trace != nullptr && c.blk == 0 && threadIdx.x == 0) t_trace[kTraceStart] = wall_clock64();
   // phase stamps of workgroup 0 (fa.prof): start, temporal done, draw ticks
   const bool prof = fa.prof != nullptr && c.blk == 0;
   uint64_t p_start = 0, p_temporal = 0, p_draw = 0;
   if (prof) p_start = wall_clock64();
   // ---- temporal step
-  StackIO tio{at.in, at.D, 0u, fa.rec_temporal, true, 0, false, 64, at.pos, at.trace, nullptr, true};
+  StackIO tio{at.in, at.D, 0u, fa.rec_temporal, true, 0, false, 64, at.pos, t_trace, nullptr, true};
   uint32_t x_tag = run_stack<T, true>(c, at, tio);
-  if (at.trace != nullptr && c.blk == 0 && threadIdx.x == 0) at.trace[kTraceEnd] = at.trace[kTraceDone] = wall_clock64();
+  if (t_trace != nullptr && c.blk == 0 && threadIdx.x == 0) t_trace[kTraceEnd] = t_trace[kTraceDone] = wall_clock64();
   if (prof) p_temporal = wall_clock64();
   // ---- depth steps
   const int L = fa.levels, C = fa.codebook, D = ad.D;
@@ -1665,7 +1676,7 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   int tok = 0;
   prefetch_qkv<T, false>(c, ad, 0);
   for (int l = 0; l < L; ++l) {
-    uint64_t* trace = l == 1 ? ad.trace : nullptr;  // timeline of level 1
+    uint64_t* trace = l == 1 ? d_trace : nullptr;  // timeline of level 1
     if (l == 1) {
       c.tp = 0;
       c.lcnt = 0;
@@ -1761,13 +1772,18 @@ bool allow_lds(const void* fn, size_t dyn, int device) {
   return per_cu >= 1;
 }
 
+template <typename T, bool TRACE>
+const void* persist_fn(PersistKernel kind) {
+  return kind == PersistKernel::Temporal ? reinterpret_cast<const void*>(&k_step<T, true, TRACE>)
+         : kind == PersistKernel::Depth  ? reinterpret_cast<const void*>(&k_step<T, false, TRACE>)
+                                         : reinterpret_cast<const void*>(&k_frame<T, TRACE>);
+}
+
 template <typename T>
 size_t prepare(PersistKernel kind, int device) {
-  const void* fn = kind == PersistKernel::Temporal ? reinterpret_cast<const void*>(&k_step<T, true>)
-                   : kind == PersistKernel::Depth  ? reinterpret_cast<const void*>(&k_step<T, false>)
-                                                   : reinterpret_cast<const void*>(&k_frame<T>);
   const size_t n = lds_bytes<T>();
-  return allow_lds(fn, n, device) ? n : 0;
+  // both the plain and the traced instance must fit (the traced one runs with MRT_TRACE_PHASES)
+  return allow_lds(persist_fn<T, false>(kind), n, device) && allow_lds(persist_fn<T, true>(kind), n, device) ? n : 0;
 }
 
 }  // namespace
@@ -1817,17 +1833,28 @@ size_t persist_prepare(DType dt, PersistKernel kind, int device) {
 }
 
 void launch_step(DType dt, const StepArgs& a, int grid, size_t lds, hipStream_t s) {
+  const bool tr = a.trace != nullptr;
   MRT_DTYPE_DISPATCH(dt, {
-    if (a.cross)
-      hipLaunchKernelGGL((k_step<T, true>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+    if (a.cross && tr)
+      hipLaunchKernelGGL((k_step<T, true, true>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+    else if (a.cross)
+      hipLaunchKernelGGL((k_step<T, true, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+    else if (tr)
+      hipLaunchKernelGGL((k_step<T, false, true>), dim3(grid), dim3(kPersistThreads), lds, s, a);
     else
-      hipLaunchKernelGGL((k_step<T, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+      hipLaunchKernelGGL((k_step<T, false, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
   });
   MRT_HIP_CHECK(hipGetLastError());
 }
 
 void launch_frame(DType dt, const FrameArgs& a, int grid, size_t lds, hipStream_t s) {
-  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL((k_frame<T>), dim3(grid), dim3(kPersistThreads), lds, s, a));
+  const bool tr = a.t.trace != nullptr || a.d.trace != nullptr;
+  MRT_DTYPE_DISPATCH(dt, {
+    if (tr)
+      hipLaunchKernelGGL((k_frame<T, true>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+    else
+      hipLaunchKernelGGL((k_frame<T, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
+  });
   MRT_HIP_CHECK(hipGetLastError());
 }
 

@@ -162,6 +162,7 @@ void Stream::token_half(const int32_t* style, const ChunkOpts& o, int32_t* llm_o
 
   GenOpts g = gen_opts(o);
   g.speculative = o.speculative == 1 || (o.speculative == 2 && spec_pause_ == 0);
+  if (o.speculative == 2 && !spec_full_) g.spec_frames = kSpecProbeFrames;  // a probe
   const size_t n = static_cast<size_t>(c.chunk_frames) * c.levels;
   llm_tmp_.resize(n);
   st.generate(nullptr, g, llm_tmp_.data());  // waits for the chunk's ids
@@ -169,8 +170,15 @@ void Stream::token_half(const int32_t* style, const ChunkOpts& o, int32_t* llm_o
     if (spec_pause_ > 0) {
       --spec_pause_;
     } else {
-      const float acc = st.spec_acceptance();
-      if (acc >= 0.f && acc < kSpecMinAcceptance) spec_pause_ = kSpecPause;
+      const float acc = st.spec_acceptance();  // -1: no drafts yet (first chunk)
+      if (acc >= kSpecMinAcceptance) {
+        spec_full_ = true;
+        spec_backoff_ = kSpecPause;
+      } else if (acc >= 0.f) {
+        spec_full_ = false;
+        spec_pause_ = spec_backoff_;
+        spec_backoff_ = std::min(2 * spec_backoff_, kSpecMaxPause);
+      }
     }
   }
   if (llm_out) std::copy(llm_tmp_.begin(), llm_tmp_.end(), llm_out);

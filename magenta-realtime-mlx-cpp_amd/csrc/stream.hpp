@@ -56,10 +56,12 @@ struct ChunkOpts {
   bool use_graph = true;
   const int32_t* teacher = nullptr;  // host (chunk_frames, levels) ids fed in place of the draws
   // Speculative depth decoding, drafts = the previous chunk's tokens of the
-  // same frame: 0 off, 1 on, 2 adaptive (speculate while the last speculative
-  // chunk took at least kSpecMinAcceptance of its levels from the
-  // verification pass; after one below, decode kSpecPause chunks plainly,
-  // then try again).
+  // same frame: 0 off, 1 on, 2 adaptive: a chunk speculates only its first
+  // kSpecProbeFrames frames (the rest decodes plainly); when at least
+  // kSpecMinAcceptance of the probed levels came from the verification pass,
+  // whole chunks speculate while their acceptance stays at or above it.  After
+  // a probe or chunk below it, kSpecPause chunks decode plainly before the
+  // next probe, doubling after each further miss up to kSpecMaxPause.
   int speculative = 0;
 };
 
@@ -71,6 +73,8 @@ struct ChunkOpts {
 // call's style matches.
 constexpr float kSpecMinAcceptance = 0.25f;
 constexpr int kSpecPause = 4;
+constexpr int kSpecMaxPause = 64;
+constexpr int kSpecProbeFrames = 2;
 
 class Stream {
  public:
@@ -125,7 +129,9 @@ class Stream {
   std::vector<int32_t> pre_style_;
   std::vector<int32_t> llm_tmp_;
   uint64_t seed_base_ = 0;
-  int spec_pause_ = 0;  // adaptive speculation: chunks left to decode plainly
+  int spec_pause_ = 0;          // adaptive speculation: chunks left to decode plainly
+  int spec_backoff_ = kSpecPause;  // the pause after the next miss
+  bool spec_full_ = false;     // the last speculation met kSpecMinAcceptance: whole chunks
 };
 
 }  // namespace mrt

@@ -245,31 +245,38 @@ def test_stream_audio_matches_oracle(tiny, pipeline):
 
 
 def test_stream_adaptive_speculation(tiny):
-    """speculative = 2: a speculative chunk whose levels came from the
-    verification pass less than a quarter of the time makes the next 4
-    chunks decode plainly (one frame launch per frame), then speculation is
-    tried again.  The expected mode of every chunk is replayed from the
-    acceptance each speculative chunk reported."""
+    """speculative = 2: a chunk speculates only its first 2 frames (a probe;
+    the other frames take one frame launch each); when at least a quarter of
+    the probed levels came from the verification pass, whole chunks
+    speculate while that holds; after a miss, 4 chunks decode plainly before
+    the next probe, 8 after a further miss, and so on.  The expected mode and
+    launch count of every chunk are replayed from the acceptance each
+    speculating chunk reported, and the acceptance is taken over the
+    speculated frames only."""
     mrt_df = tiny["mrt_df"]
     s = _stream(tiny)
-    F, L = 4, 16
-    pause, modes, accs = 0, [], []
-    for i in range(9):
+    F, L, probe = 4, 16, 2
+    pause, backoff, full, modes, accs = 0, 4, False, [], []
+    for i in range(12):
         o = mrt_df.ChunkOptions(temperature=1.1, top_k=4, guidance_weight=5.0, speculative=2)  # seed: base + index
         s.generate_chunk(tiny["style_a"], o)
         launches = s.state.decode_time()[1]
         acc = s.state.spec_acceptance()
-        spec = launches == F * L
-        assert launches in (F, F * L)
-        modes.append(spec)
+        modes.append(launches)
         accs.append(acc)
         # the policy, replayed: the first chunk has no drafts; a paused chunk decodes plainly
-        want = i > 0 and pause == 0
-        assert spec == want, (i, modes, accs)
+        spec = i > 0 and pause == 0
+        want = (F * L if full else probe * L + (F - probe)) if spec else F
+        assert launches == want, (i, modes, accs)
+        assert (acc >= 0.0) == spec
+        if spec and not full:
+            # the probe's share comes from its 2 speculated frames: a multiple of 1 / 32
+            assert abs(acc * probe * L - round(acc * probe * L)) < 1e-6
         if pause > 0:
             pause -= 1
-        elif spec and acc < 0.25:
-            pause = 4
-        assert (acc >= 0.0) == spec
-    print("modes", modes, "acceptance", [round(a, 3) for a in accs], flush=True)
+        elif acc >= 0.25:
+            full, backoff = True, 4
+        elif acc >= 0.0:
+            full, pause, backoff = False, backoff, min(2 * backoff, 64)
+    print("launches", modes, "acceptance", [round(a, 3) for a in accs], flush=True)
     s.close()
