@@ -479,19 +479,19 @@ void State::setup_persistent() {
   };
   tstack_ = stack(m.tmp, true);
   dstack_ = stack(m.dep, false);
-  // First-poll delays per PollSite, measured on MI355X at the benchmark dims
-  // (bf16 frame kernel, sweep of 0..48 per site): the layer inputs of the
-  // q/k/v and output projections are polled at once, the gated-GELU input and
-  // output after 16 rounds (their producers finish last), the cross partials'
-  // query after 8, the head logits at once, the rest after 4.  MRT_POLL_DELAY=n
+  // First-poll delays per PollSite and stack (temporal, depth), measured on
+  // MI355X at the benchmark dims (bf16 frame kernel, greedy per-site sweeps
+  // over 0..32, each value timed next to the current best in one process):
+  // the layer inputs of the q/k/v, output and gated-GELU projections and the
+  // head logits are polled at once, the gated-GELU output after 24 rounds (its
+  // producers finish last), the cross-attention query input after 16, the
+  // cross partials' query and the head input after 8, the rest after 4.  A
+  // separate sweep per stack found the same values for both.  MRT_POLL_DELAY=n
   // sets every site, MRT_POLL_DELAYS a comma-separated list in PollSite order
+  // for both stacks, MRT_POLL_DELAYS_T / MRT_POLL_DELAYS_D for one stack
   // (missing entries keep their value).
-  static constexpr uint8_t kDefaultDelay[kPollSites] = {0, 4, 0, 4, 8, 4, 4, 16, 16, 4, 0, 4};
-  uint8_t* dl = poll_delay_;
-  std::copy(kDefaultDelay, kDefaultDelay + kPollSites, dl);
-  if (const char* d = std::getenv("MRT_POLL_DELAY"))
-    std::fill(dl, dl + kPollSites, static_cast<uint8_t>(std::max(0, std::min(255, std::atoi(d)))));
-  if (const char* d = std::getenv("MRT_POLL_DELAYS")) {
+  static constexpr uint8_t kDefaultDelay[kPollSites] = {0, 4, 0, 16, 8, 4, 4, 0, 24, 8, 0, 4};
+  auto parse = [](const char* d, uint8_t* dl) {
     const char* c = d;
     for (int i = 0; i < kPollSites; ++i) {
       char* end = nullptr;
@@ -500,6 +500,14 @@ void State::setup_persistent() {
       if (*end != ',') break;
       c = end + 1;
     }
+  };
+  for (int k = 0; k < 2; ++k) {
+    uint8_t* dl = poll_delay_[k];
+    std::copy(kDefaultDelay, kDefaultDelay + kPollSites, dl);
+    if (const char* d = std::getenv("MRT_POLL_DELAY"))
+      std::fill(dl, dl + kPollSites, static_cast<uint8_t>(std::max(0, std::min(255, std::atoi(d)))));
+    if (const char* d = std::getenv("MRT_POLL_DELAYS")) parse(d, dl);
+    if (const char* d = std::getenv(k == 0 ? "MRT_POLL_DELAYS_T" : "MRT_POLL_DELAYS_D")) parse(d, dl);
   }
   if (const char* q = std::getenv("MRT_QKV_TABLE")) qkv_table_on_ = std::string(q) != "0";
   if (const char* pr = std::getenv("MRT_PROFILE_DECODE")) profile_ = pr[0] != '\0';
@@ -561,7 +569,7 @@ void State::print_trace() {
   }
 }
 
-LLBufs State::ll_bufs() const {
+LLBufs State::ll_bufs(int stack) const {
   uint64_t* b = static_cast<uint64_t*>(ll_block_);
   const size_t vec = kLLVecWords;
   LLBufs l;
@@ -577,7 +585,7 @@ LLBufs State::ll_bufs() const {
   l.seq = reinterpret_cast<uint32_t*>(tail);
   l.tok = tail + 16;
   l.err = reinterpret_cast<int*>(tail + 32);
-  std::memcpy(l.delay, poll_delay_, kPollSites);
+  std::memcpy(l.delay, poll_delay_[stack], kPollSites);
   return l;
 }
 
@@ -627,7 +635,7 @@ StepArgs State::temporal_args(const void* in, int f, void* out) const {
   a.in = in;
   a.out = out;
   a.S = S;
-  a.ll = ll_bufs();
+  a.ll = ll_bufs(0);
   return a;
 }
 
@@ -653,7 +661,7 @@ StepArgs State::depth_args(const void* in, int l, const void* head_w, int head_r
   a.head_rows = head_rows;
   a.logits = logits;
   a.rec_slice = rec_slice;
-  a.ll = ll_bufs();
+  a.ll = ll_bufs(1);
   return a;
 }
 

@@ -280,7 +280,7 @@ class State {
   void* ll_block_ = nullptr;
   size_t ll_words_ = 0;
   uint32_t epochs_used_ = 0;   // launches since the hand-off words were zeroed
-  LLBufs ll_bufs() const;
+  LLBufs ll_bufs(int stack = 1) const;  // hand-off words; delays of stack 0 (temporal) or 1 (depth)
   void reset_handoff();
   DecStack tstack_{}, dstack_{};  // temporal / depth stacks with this state's caches
   size_t lds_t_ = 0, lds_d_ = 0, lds_f_ = 0;  // dynamic LDS of the persistent kernels
@@ -288,7 +288,7 @@ class State {
   int* h_err_ = nullptr;        // pinned
   uint64_t* h_seed_ = nullptr;  // pinned: the draw seed of a generate / sample call
   uint64_t* d_trace_ = nullptr; // 2 x kTraceSlots when MRT_TRACE_PHASES is set
-  uint8_t poll_delay_[kPollSites];  // per poll site: s_sleep(1) rounds before a hand-off's first poll
+  uint8_t poll_delay_[2][kPollSites];  // per stack (temporal, depth) and poll site: s_sleep(1) rounds before a hand-off's first poll
   bool qkv_table_on_ = true;    // frame kernel: layer-0 q/k/v of fed tokens from the model's table (MRT_QKV_TABLE=0: off)
   const void* qkv_table_ = nullptr;  // the table of the current generate call, or nullptr
   hipEvent_t ev_dec_[2] = {nullptr, nullptr};  // around the decode section of generate
