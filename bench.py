@@ -324,6 +324,33 @@ def bench_speculative(model, cfg, enc, reps=3, seed=1234):
     return res
 
 
+def bench_decode_profile(model, enc, reps=3, seed=1234):
+    """The per-chunk phase split of decode.cpp's MRT_PROFILE_DECODE
+    (decode.cpp:36-49, 529-565) for one 50-frame chunk: the encoder pass and
+    the decode section by the state's HIP events, the decode's temporal / depth /
+    draw parts from the frame kernel's device-clock stamps (workgroup 0, every
+    frame), averaged over `reps` chunks after one capturing call."""
+    import mrt_df
+    st = model.new_state(max_frames=50)
+    opts = mrt_df.GenOptions(num_frames=50, rvq_depth=16, temperature=1.1, top_k=40, guidance_weight=5.0,
+                             seed=seed, codebook_size=1024, codec_offset=2, use_graph=True)
+    st.set_profile(True)
+    st.generate_tokens(enc, opts)
+    runs = []
+    for _ in range(reps):
+        st.generate_tokens(enc, opts)
+        runs.append(st.decode_profile())
+    st.close()
+    res = {k: (float(np.mean([r[k] for r in runs])) if k != "frames" else runs[0][k]) for k in runs[0]}
+    res["note"] = ("total_ms = the decode section and encoder_ms = the encoder pass, by the state's HIP events; "
+                   "temporal / depth / sample are the frame kernel's device-clock stamps summed over the frames "
+                   "(depth = the 16 levels' depth layers and head GEMVs, sample = the draws)")
+    print(f"[bench] decode profile (ms per chunk): decode {res['total_ms']:.2f}, encoder {res['encoder_ms']:.2f}, "
+          f"temporal {res['temporal_ms']:.2f}, depth {res['depth_ms']:.2f}, sample {res['sample_ms']:.2f}",
+          file=sys.stderr, flush=True)
+    return res
+
+
 def bench_concurrent_batches(model, batches=2, streams=32, chunks=3, seed=1234):
     """Serving capacity: `batches` independent Batch objects of `streams`
     streams each, every one on its own HIP stream, driven from one host
@@ -801,6 +828,10 @@ def main():
                 "algorithmic_bytes_per_launch": dk["bytes"], "launch_us": dk["us"],
                 "launches_timed": dk["launches"]}
 
+    prof = None
+    if roof is not None and roof.get("kernel", "").startswith("k_frame"):
+        prof = bench_decode_profile(model, system.build_encoder_inputs(sess.context, scfg, style))
+
     batched = encoder = spec = codec = full = style_res = None
     if not args.no_batched and args.dtype == "bf16":
         full = bench_full_chunk(model, cfg)
@@ -843,6 +874,7 @@ def main():
                            "algorithmic_bytes": ab["chunk"],
                            "unit_of_work": "one chunk (encoder + 50 temporal + 800 depth steps)"},
         "decode_ms_per_chunk": float(np.mean(dec)),
+        "decode_profile": prof,
         "depth_step_kernel": {"launch_us": dk["us"], "achieved_GBs": dk["GBs"],
                               "algorithmic_bytes_per_launch": dk["bytes"],
                               "traffic": load_traffic("depth_step_traffic"), "by_cache_len": lens["depth"]},
