@@ -59,6 +59,49 @@ __global__ __launch_bounds__(256) void k_rmsnorm_rows_reg(const T* __restrict__ 
   }
 }
 
+// One wave per row of D = 64 V NV elements (V per 16-byte chunk): a lane keeps
+// its NV chunks in registers between the sum of squares and the scaling, and
+// the row's sum is one wave reduction (no LDS, no barrier); four rows per block.
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void k_rmsnorm_rows_wave(const T* __restrict__ x, const T* __restrict__ g,
+                                                           float eps, int M, int D, T* __restrict__ y) {
+  using S = St<T>;
+  constexpr int V = S::kVec;
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);  // wave-uniform
+  if (r >= M) return;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)r * D);
+  const uint4* gr = reinterpret_cast<const uint4*>(g);
+  uint4 v[NV], gv[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = xr[lane + 64 * i];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) gv[i] = gr[lane + 64 * i];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const T* e = reinterpret_cast<const T*>(&v[i]);
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+      const float f = S::ld(e[k]);
+      ss += f * f;
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  uint4* yr = reinterpret_cast<uint4*>(y + (size_t)r * D);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const T* e = reinterpret_cast<const T*>(&v[i]);
+    const T* ge = reinterpret_cast<const T*>(&gv[i]);
+    uint4 o;
+    T* oe = reinterpret_cast<T*>(&o);
+#pragma unroll
+    for (int k = 0; k < V; ++k) oe[k] = S::st(S::rnd(S::ld(e[k]) * inv) * S::ld(ge[k]));
+    yr[lane + 64 * i] = o;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_rmsnorm_rows(const T* __restrict__ x, const T* __restrict__ g,
                                                       float eps, int D, T* __restrict__ y) {
@@ -577,13 +620,22 @@ __global__ __launch_bounds__(64) void k_enc_attn(const T* __restrict__ qkv, int 
 // accumulators: lane l's accumulators of a 16-key step hold keys
 // {4h..4h+3, 8+4h..8+4h+3} (h = l / 32), so V^T is staged with the key order
 // inside every 16-key block permuted the same way (swap of key bits 2 and 3).
-// Scores and the softmax are fp32, the exponentials taken as 2^(s log2 e)
-// with v_exp_f32 (as fused attention kernels do); P enters the second product as the sum of
-// two parts in the storage type (hi + lo: ~16 significant bits for bf16, ~22
-// for fp16), as close to the fp32 probabilities of the reference's fused
-// attention as 16-bit MFMA allows.
+// Scores and the softmax are fp32, the exponentials taken as
+// 2^(s log2 e - m log2 e) with one fma and v_exp_f32 (as fused attention
+// kernels do), keys past S masked only in the last tile; P enters the second
+// product as the sum of two parts in the storage type (hi + lo: ~16
+// significant bits for bf16, ~22 for fp16), as close to the fp32
+// probabilities of the reference's fused attention as 16-bit MFMA allows (P
+// rounded once to bf16 measured 2.02e-2 on a level slice of the bf16
+// two-frame decode against the oracle's 2e-2 bound).
 constexpr int kAQ = 128, kAK = 64, kALD = 64 + 8;  // queries, keys per tile, padded LDS row
 constexpr float kLog2e = 1.4426950408889634f;
+
+// Element offset of 8-key chunk `ch` in row `dim` of the staged V^T: chunks are
+// XOR-swizzled by dim / 8, so the transposed 2-byte stores of 8 dims 8 apart
+// fall in different banks (2-way instead of 8-way), while the padded rows keep
+// the 16-byte fragment reads of 8 consecutive dims conflict-free.
+__device__ __forceinline__ int vt_chunk(int ch, int dim) { return (ch ^ ((dim >> 3) & 7)) << 3; }
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv, int S, int H,
@@ -606,23 +658,20 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
     for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const v8*>(qr + 16 * s + 8 * hf);
   }
   // Tile staging: thread t moves 16 bytes of K and of V for keys t/8 and
-  // 32 + t/8, dims 8 (t % 8) .. +7.
-  uint4 rk[2], rv[2];
-  auto gload = [&](int kb) {
+  // 32 + t/8, dims 8 (t % 8) .. +7.  Keys past S re-read key S - 1 (finite;
+  // their scores are masked), so no load is conditional.  Two register sets
+  // keep the loads of tiles j + 1 and j + 2 in flight while tile j is used.
+  typedef uint4 Regs[2];
+  auto gload = [&](Regs& rk, Regs& rv, int kb) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int key = kb + (tid >> 3) + 32 * i, c = (tid & 7) * 8;
-      if (key < S) {
-        const T* row = base + (size_t)key * ld;
-        rk[i] = *reinterpret_cast<const uint4*>(row + HD + c);
-        rv[i] = *reinterpret_cast<const uint4*>(row + 2 * HD + c);
-      } else {
-        rk[i] = make_uint4(0u, 0u, 0u, 0u);
-        rv[i] = make_uint4(0u, 0u, 0u, 0u);
-      }
+      const int key = min(kb + (tid >> 3) + 32 * i, S - 1), c = (tid & 7) * 8;
+      const T* row = base + (size_t)key * ld;
+      rk[i] = *reinterpret_cast<const uint4*>(row + HD + c);
+      rv[i] = *reinterpret_cast<const uint4*>(row + 2 * HD + c);
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](const Regs& rk, const Regs& rv, int buf) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int key = (tid >> 3) + 32 * i, c = (tid & 7) * 8;
@@ -630,7 +679,7 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
       const int slot = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
       const T* v = reinterpret_cast<const T*>(&rv[i]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[buf][(c + e) * kALD + slot] = v[e];
+      for (int e = 0; e < 8; ++e) Vt[buf][(c + e) * kALD + vt_chunk(slot >> 3, c + e) + (slot & 7)] = v[e];
     }
   };
 
@@ -641,13 +690,17 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
   float m = -INFINITY, lsum = 0.f;
 
-  gload(0);
-  sstore(0);
-  __syncthreads();
   const int ntiles = (S + kAK - 1) / kAK;
-  for (int j = 0; j < ntiles; ++j) {
+  Regs k0, v0, k1, v1;
+  gload(k0, v0, 0);
+  if (ntiles > 1) gload(k1, v1, kAK);
+  sstore(k0, v0, 0);
+  __syncthreads();
+  // tile j from LDS buffer j % 2; (fk, fv) is free and takes tile j + 2,
+  // (nk, nv) holds tile j + 1 and goes to the other buffer at the end
+  auto tile = [&](int j, Regs& fk, Regs& fv, const Regs& nk, const Regs& nv) {
     const int cur = j & 1, kb = j * kAK;
-    if (j + 1 < ntiles) gload(kb + kAK);
+    if (j + 2 < ntiles) gload(fk, fv, kb + 2 * kAK);
     // S^T for keys kb + 32 t + (8 (r/4) + 4 hf + r%4), query q
     f32x16_t sc[2];
 #pragma unroll
@@ -661,17 +714,25 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
       }
     }
     float mt = -INFINITY;
+    if (kb + kAK <= S) {  // a full tile (wave-uniform): no key to mask
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kb + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
-        sc[t][r] = key < S ? sc[t][r] * kLog2e : -INFINITY;
-        mt = fmaxf(mt, sc[t][r]);
-      }
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[t][r]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
+          sc[t][r] = key < S ? sc[t][r] : -INFINITY;
+          mt = fmaxf(mt, sc[t][r]);
+        }
+    }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mn = fmaxf(m, mt);
-    const float corr = __builtin_amdgcn_exp2f(m - mn);
+    const float mn = fmaxf(m, mt);  // raw-score running max (key 0 is never masked)
+    const float mns = mn * kLog2e;
+    const float corr = __builtin_amdgcn_exp2f(fmaf(m, kLog2e, -mns));
     float ps = 0.f;
     v8 pb[4], pl[4];  // P^T = hi + lo (storage type each) for the four 16-key steps
 #pragma unroll
@@ -679,7 +740,7 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
       f32x8_t pv;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        pv[i] = __builtin_amdgcn_exp2f(sc[g >> 1][8 * (g & 1) + i] - mn);
+        pv[i] = __builtin_amdgcn_exp2f(fmaf(sc[g >> 1][8 * (g & 1) + i], kLog2e, -mns));
         ps += pv[i];
       }
       pb[g] = __builtin_convertvector(pv, v8);  // round-to-nearest-even conversions
@@ -696,12 +757,16 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const v8 a = *reinterpret_cast<const v8*>(&Vt[cur][(32 * t + lq) * kALD + 16 * s + 8 * hf]);
+        const v8 a = *reinterpret_cast<const v8*>(&Vt[cur][(32 * t + lq) * kALD + vt_chunk(2 * s + hf, 32 * t + lq)]);
         acc[t] = Mfma<T>::mma(a, pb[s], acc[t]);
         acc[t] = Mfma<T>::mma(a, pl[s], acc[t]);
       }
-    if (j + 1 < ntiles) sstore(cur ^ 1);
+    if (j + 1 < ntiles) sstore(nk, nv, cur ^ 1);
     __syncthreads();
+  };
+  for (int j = 0; j < ntiles; j += 2) {
+    tile(j, k0, v0, k1, v1);
+    if (j + 1 < ntiles) tile(j + 1, k1, v1, k0, v0);
   }
   if (q < S) {
     T* orow = out + ((size_t)b * S + q) * HD + h * 64;
@@ -728,8 +793,37 @@ void encoder_embed(DType dt, const void* emb, const void* pe, const int* tok, in
   MRT_HIP_CHECK(hipGetLastError());
 }
 
+namespace {
+
+// The wave-per-row norm for rows of 64 V NV elements (NV <= 4) on 16-byte
+// aligned pointers; false when the shape or alignment does not fit.
+template <typename T>
+bool rmsnorm_rows_wave(const T* x, const T* g, float eps, int M, int D, T* y, hipStream_t s) {
+  constexpr int W = 64 * St<T>::kVec;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(g) |
+                         reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+  if (!aligned || D % W != 0 || D / W < 1 || D / W > 4) return false;
+  const dim3 grid((M + 3) / 4), block(256);
+  switch (D / W) {
+    case 1: hipLaunchKernelGGL((k_rmsnorm_rows_wave<T, 1>), grid, block, 0, s, x, g, eps, M, D, y); break;
+    case 2: hipLaunchKernelGGL((k_rmsnorm_rows_wave<T, 2>), grid, block, 0, s, x, g, eps, M, D, y); break;
+    case 3: hipLaunchKernelGGL((k_rmsnorm_rows_wave<T, 3>), grid, block, 0, s, x, g, eps, M, D, y); break;
+    default: hipLaunchKernelGGL((k_rmsnorm_rows_wave<T, 4>), grid, block, 0, s, x, g, eps, M, D, y); break;
+  }
+  return true;
+}
+
+}  // namespace
+
 void rmsnorm_rows(DType dt, const void* x, const void* g, float eps, int M, int D, void* y,
                   hipStream_t s) {
+  bool done = false;
+  MRT_DTYPE_DISPATCH(dt, done = rmsnorm_rows_wave<T>(static_cast<const T*>(x), static_cast<const T*>(g), eps, M, D,
+                                                      static_cast<T*>(y), s));
+  if (done) {
+    MRT_HIP_CHECK(hipGetLastError());
+    return;
+  }
   const bool reg = D <= 256 * kNormPer;
   MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(reg ? k_rmsnorm_rows_reg<T> : k_rmsnorm_rows<T>, dim3(M), dim3(256), 0,
                                             s, (const T*)x, (const T*)g, eps, D, (T*)y));
