@@ -249,12 +249,12 @@ __device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt
 
 // Epilogue of the MFMA GEMMs.  Accumulator r of tile (i, j) of a lane holds
 // row mb + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4 and column
-// nb + 32 j + lane % 32 (j = 0 / 1: gate / up columns of a gated-GELU pair).
+// nb + 32 j + lane % 32 (j = 2p / 2p + 1: gate / up columns of gated-GELU pair p).
 // The kind is resolved once per tile, and the residual epilogue loads every
 // residual before it stores anything: with the loads and stores of one
 // element interleaved, each load would wait for the previous element's store.
-template <typename T, int MI>
-__device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x16_t (&acc)[MI][2], int M, int mb,
+template <typename T, int MI, int NJ = 2>
+__device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x16_t (&acc)[MI][NJ], int M, int mb,
                                               int nb) {
   using St_ = St<T>;
   const int lane = threadIdx.x & 63, col = lane & 31, rl = 4 * (lane >> 5);
@@ -263,17 +263,21 @@ __device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x1
   auto row = [&](int i, int r) { return mb + 32 * i + 8 * (r >> 2) + rl + (r & 3); };
   switch (out.a.kind) {
     case GemmEpi::Geglu:
+      if constexpr (NJ % 2 == 0) {
 #pragma unroll
-      for (int i = 0; i < MI; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (row(i, r) < M) out.put_geglu(row(i, r), nb + col, acc[i][0][r], acc[i][1][r]);
+          for (int pj = 0; pj < NJ / 2; ++pj)
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (row(i, r) < M) out.put_geglu(row(i, r), nb + 64 * pj + col, acc[i][2 * pj][r], acc[i][2 * pj + 1][r]);
+      }
       break;
     case GemmEpi::Resid:
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NJ; ++j) {
           T old[16];  // rows past M load row M - 1 (unconditional loads, issued together)
 #pragma unroll
           for (int r = 0; r < 16; ++r) old[r] = C[(size_t)min(row(i, r), M - 1) * N + nb + 32 * j + col];
@@ -287,7 +291,7 @@ __device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x1
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
             if (row(i, r) < M) C[(size_t)row(i, r) * N + nb + 32 * j + col] = St_::st(acc[i][j][r]);
@@ -296,16 +300,16 @@ __device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x1
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
             if (row(i, r) < M)
               static_cast<float*>(out.a.C)[(size_t)row(i, r) * N + nb + 32 * j + col] = St_::rnd(acc[i][j][r]);
       break;
     default: {  // CrossKV: column n = (layer*2 + kv)*HD + h*64 + d, row m = b*S + s
-      size_t cbase[2];
+      size_t cbase[NJ];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NJ; ++j) {
         const int n = nb + 32 * j + col, lk = n / out.a.HD, nn = n - lk * out.a.HD;
         cbase[j] = (((size_t)lk * out.a.nb) * out.a.H + (nn >> 6)) * out.a.S * 64 + (nn & 63);
       }
@@ -319,7 +323,7 @@ __device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x1
             const int b = m / out.a.S, sp = m - b * out.a.S;
             const size_t ro = (size_t)b * bstride + (size_t)sp * 64;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) C[cbase[j] + ro] = St_::st(acc[i][j][r]);
+            for (int j = 0; j < NJ; ++j) C[cbase[j] + ro] = St_::st(acc[i][j][r]);
           }
         }
     }
@@ -327,8 +331,8 @@ __device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x1
 }
 
 // C = A B^T (A (M, K), B (N, K) 16-bit, fp32 accumulation) with the GemmOut
-// epilogue.  Tile BM x 128 x 64, 4 waves in a 2x2 grid (wave tile BM/2 x 64 =
-// (BM/64) x 2 MFMA 32x32x16 tiles).  Tiles stream global -> LDS with direct
+// epilogue.  Tile BM x BN x 64, 4 waves in a 2x2 grid (wave tile BM/2 x BN/2 =
+// (BM/64) x (BN/64) MFMA 32x32x16 tiles).  Tiles stream global -> LDS with direct
 // 16-byte loads (global_load_lds) through an S-deep ring: tile j + S - 1 is
 // requested while tile j is multiplied, and a wave waits only for its own
 // loads of tile j (vmcnt counts in order) before the barrier.  Where the grid
@@ -339,17 +343,23 @@ __device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x1
 // Operand fragments of v_mfma_f32_32x32x16_{bf16,f16}: lane l holds row (l % 32)
 // and k = 8*(l / 32) .. +7 of both A (32x16) and B^T (32x16); the 16
 // accumulators of lane l hold column l % 32, rows 8*(r/4) + 4*(l/32) + r%4.
-template <typename T, int BM, int S>
-__global__ __launch_bounds__(256) void k_gemm_mfma(const T* __restrict__ A, const T* __restrict__ B,
+// Blocks per CU the register budget is sized for: two wherever the LDS ring
+// leaves room for two (at most 80 KB), else one.
+constexpr int gemm_min_blocks(int BM, int S, int BN) { return S * (BM + BN) * 128 <= 80 * 1024 ? 2 : 1; }
+
+template <typename T, int BM, int S, int BN>
+__global__ __launch_bounds__(256, gemm_min_blocks(BM, S, BN)) void k_gemm_mfma(const T* __restrict__ A,
+                                                                               const T* __restrict__ B,
                                                    int M, int N, int K, GemmOut<T> out) {
   typedef typename Mfma<T>::v8 v8;
   constexpr int MI = BM / 64;                        // MFMA tiles per wave in M
-  constexpr int kStageBytes = (BM + kBN) * 128;      // A rows then B rows, 128 bytes each
-  constexpr int LA = BM / 32 + kBN / 32;             // load instructions per wave per tile
+  constexpr int NJ = BN / 64;                        // MFMA tiles per wave in N
+  constexpr int kStageBytes = (BM + BN) * 128;       // A rows then B rows, 128 bytes each
+  constexpr int LA = BM / 32 + BN / 32;              // load instructions per wave per tile
   extern __shared__ __align__(16) unsigned char lds[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid >> 1, wn = wid & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * kBN;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int nk = K / kBK;
 
   // tile kt -> stage kt % S; wave w loads rows [w*BM/4, +BM/4) of A and
@@ -367,19 +377,19 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const T* __restrict__ A, cons
                                        (MRT_LDS void*)(st + (wid * (BM / 4) + q * 8) * 128), 16, 0, 0);
     }
 #pragma unroll
-    for (int q = 0; q < kBN / 32; ++q) {
-      const int r = wid * (kBN / 4) + q * 8 + r8;
+    for (int q = 0; q < BN / 32; ++q) {
+      const int r = wid * (BN / 4) + q * 8 + r8;
       const T* src = B + (size_t)(n0 + r) * K + ktc * kBK + ((p ^ swz(r)) << 3);
       __builtin_amdgcn_global_load_lds((const MRT_GLOBAL void*)src,
-                                       (MRT_LDS void*)(st + BM * 128 + (wid * (kBN / 4) + q * 8) * 128), 16, 0, 0);
+                                       (MRT_LDS void*)(st + BM * 128 + (wid * (BN / 4) + q * 8) * 128), 16, 0, 0);
     }
   };
 
-  f32x16_t acc[MI][2];
+  f32x16_t acc[MI][NJ];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -393,7 +403,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const T* __restrict__ A, cons
     const unsigned char* st = lds + (kt % S) * kStageBytes;
     // every fragment of the tile is read before the first product, so the
     // LDS latency is paid once per tile, not once per 16-deep step
-    v8 a[kBK / 16][MI], b[kBK / 16][2];
+    v8 a[kBK / 16][MI], b[kBK / 16][NJ];
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
       const int c = 2 * ks + lh;
@@ -403,8 +413,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const T* __restrict__ A, cons
         a[ks][i] = *reinterpret_cast<const v8*>(st + r * 128 + ((c ^ swz(r)) << 4));
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int r = wn * 64 + j * 32 + lr;
+      for (int j = 0; j < NJ; ++j) {
+        const int r = wn * (BN / 2) + j * 32 + lr;
         b[ks][j] = *reinterpret_cast<const v8*>(st + BM * 128 + r * 128 + ((c ^ swz(r)) << 4));
       }
     }
@@ -414,12 +424,12 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const T* __restrict__ A, cons
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < NJ; ++j)
           acc[i][j] = Mfma<T>::mma(a[ks][i], b[ks][j], acc[i][j]);
   }
   __builtin_amdgcn_s_waitcnt(vm_wait_imm(0));  // no copy into LDS outlives the block
 
-  mfma_epilogue<T, MI>(out, acc, M, m0 + wm * (BM / 2), n0 + wn * 64);
+  mfma_epilogue<T, MI, NJ>(out, acc, M, m0 + wm * (BM / 2), n0 + wn * (BN / 2));
 }
 
 // Dynamic LDS above 64 KB needs an explicit allowance, once per kernel and device.
@@ -448,12 +458,16 @@ int device_cus() {
   return v;
 }
 
-template <typename T, int BM, int S = kStages>
+template <typename T, int BM, int S = kStages, int BN = kBN>
 void launch_gemm_mfma(const T* A, const T* B, int M, int N, int K, const GemmOut<T>& out, hipStream_t s) {
-  static_assert((S - 2) * (BM / 32 + kBN / 32) < 64, "vmcnt holds at most 63 outstanding loads");
-  constexpr size_t lds = (size_t)S * (BM + kBN) * 128;
-  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_mfma<T, BM, S>), lds);
-  hipLaunchKernelGGL((k_gemm_mfma<T, BM, S>), dim3(N / kBN, (M + BM - 1) / BM), dim3(256), lds, s, A, B, M, N, K, out);
+  static_assert((S - 2) * (BM / 32 + BN / 32) < 64, "vmcnt holds at most 63 outstanding loads");
+  static_assert(BM % 64 == 0 && BN % 64 == 0, "wave tiles are whole 32x32 MFMA tiles");
+  constexpr size_t lds = (size_t)S * (BM + BN) * 128;
+  static_assert(lds <= 160 * 1024, "LDS of one CU");
+  MRT_REQUIRE(N % BN == 0, "gemm: N is not a multiple of the tile width");
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_mfma<T, BM, S, BN>), lds);
+  hipLaunchKernelGGL((k_gemm_mfma<T, BM, S, BN>), dim3(N / BN, (M + BM - 1) / BM), dim3(256), lds, s, A, B, M, N, K,
+                     out);
 }
 
 // Large-M GEMM (the encoder of several streams): 256 x 256 x 64 tiles, 16
@@ -638,7 +652,9 @@ constexpr float kLog2e = 1.4426950408889634f;
 __device__ __forceinline__ int vt_chunk(int ch, int dim) { return (ch ^ ((dim >> 3) & 7)) << 3; }
 
 template <typename T>
-__global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv, int S, int H,
+// Three blocks per CU (3 waves per SIMD: the register budget is 170), which
+// measured faster than the compiler's 196 registers at two.
+__global__ __launch_bounds__(256, 3) void k_enc_attn_mfma(const T* __restrict__ qkv, int S, int H,
                                                        T* __restrict__ out) {
   typedef typename Mfma<T>::v8 v8;
   __shared__ __attribute__((aligned(16))) T Ks[2][kAK * kALD];
@@ -658,20 +674,25 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
     for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const v8*>(qr + 16 * s + 8 * hf);
   }
   // Tile staging: thread t moves 16 bytes of K and of V for keys t/8 and
-  // 32 + t/8, dims 8 (t % 8) .. +7.  Keys past S re-read key S - 1 (finite;
-  // their scores are masked), so no load is conditional.  Two register sets
-  // keep the loads of tiles j + 1 and j + 2 in flight while tile j is used.
-  typedef uint4 Regs[2];
-  auto gload = [&](Regs& rk, Regs& rv, int kb) {
+  // 32 + t/8, dims 8 (t % 8) .. +7; keys past S are zero.  (Clamping those
+  // keys to S - 1 instead, with no conditional load, made the compiler keep
+  // the Q fragments in scratch memory.)
+  uint4 rk[2], rv[2];
+  auto gload = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int key = min(kb + (tid >> 3) + 32 * i, S - 1), c = (tid & 7) * 8;
-      const T* row = base + (size_t)key * ld;
-      rk[i] = *reinterpret_cast<const uint4*>(row + HD + c);
-      rv[i] = *reinterpret_cast<const uint4*>(row + 2 * HD + c);
+      const int key = kb + (tid >> 3) + 32 * i, c = (tid & 7) * 8;
+      if (key < S) {
+        const T* row = base + (size_t)key * ld;
+        rk[i] = *reinterpret_cast<const uint4*>(row + HD + c);
+        rv[i] = *reinterpret_cast<const uint4*>(row + 2 * HD + c);
+      } else {
+        rk[i] = make_uint4(0u, 0u, 0u, 0u);
+        rv[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
     }
   };
-  auto sstore = [&](const Regs& rk, const Regs& rv, int buf) {
+  auto sstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int key = (tid >> 3) + 32 * i, c = (tid & 7) * 8;
@@ -690,17 +711,13 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
   float m = -INFINITY, lsum = 0.f;
 
-  const int ntiles = (S + kAK - 1) / kAK;
-  Regs k0, v0, k1, v1;
-  gload(k0, v0, 0);
-  if (ntiles > 1) gload(k1, v1, kAK);
-  sstore(k0, v0, 0);
+  gload(0);
+  sstore(0);
   __syncthreads();
-  // tile j from LDS buffer j % 2; (fk, fv) is free and takes tile j + 2,
-  // (nk, nv) holds tile j + 1 and goes to the other buffer at the end
-  auto tile = [&](int j, Regs& fk, Regs& fv, const Regs& nk, const Regs& nv) {
+  const int ntiles = (S + kAK - 1) / kAK;
+  for (int j = 0; j < ntiles; ++j) {
     const int cur = j & 1, kb = j * kAK;
-    if (j + 2 < ntiles) gload(fk, fv, kb + 2 * kAK);
+    if (j + 1 < ntiles) gload(kb + kAK);
     // S^T for keys kb + 32 t + (8 (r/4) + 4 hf + r%4), query q
     f32x16_t sc[2];
 #pragma unroll
@@ -761,12 +778,8 @@ __global__ __launch_bounds__(256) void k_enc_attn_mfma(const T* __restrict__ qkv
         acc[t] = Mfma<T>::mma(a, pb[s], acc[t]);
         acc[t] = Mfma<T>::mma(a, pl[s], acc[t]);
       }
-    if (j + 1 < ntiles) sstore(nk, nv, cur ^ 1);
+    if (j + 1 < ntiles) sstore(cur ^ 1);
     __syncthreads();
-  };
-  for (int j = 0; j < ntiles; j += 2) {
-    tile(j, k0, v0, k1, v1);
-    if (j + 1 < ntiles) tile(j + 1, k1, v1, k0, v0);
   }
   if (q < S) {
     T* orow = out + ((size_t)b * S + q) * HD + h * 64;
@@ -840,15 +853,27 @@ void gemm_t(const T* A, const T* B, int M, int N, int K, const GemmEpiArgs& e, h
       // Measured on MI355X (256 CUs) at 2 x 1006 x {1, 8, 32} rows: 256 x 256
       // tiles for outputs up to 4096 wide once they give about one tile per
       // CU (slower for the 5632- and 40960-wide outputs, where 2-3 smaller
-      // blocks per CU hide more latency); a grid of at most one 64-row tile
-      // per CU takes the 4-deep ring; else 128-row tiles when those give >= 1.5
-      // tiles per CU, else 64-row tiles.
+      // blocks per CU hide more latency).  Below that every block streams
+      // its operands at the latency of the last-level cache, so the tile is
+      // chosen for the bytes it keeps in flight: a grid of at most one 64-row
+      // tile per CU takes a 6-deep ring (144 KB of LDS); a 128 x 192 tile with
+      // a 3-deep ring where that grid fits the CUs once (not for the
+      // gated-GELU pairs, which need wave tiles of whole 64-column groups);
+      // 192-row tiles where two blocks per CU (80 KB each) cover the grid
+      // once; else 128-row tiles when those give >= 1.5 tiles per CU, else
+      // 64-row tiles.
       const long cus = device_cus();
       const long t256 = (long)((M + kGB - 1) / kGB) * (N / kGB), t64 = (long)((M + 63) / 64) * (N / kBN);
+      const long t128x192 = N % 192 == 0 ? (long)((M + 127) / 128) * (N / 192) : 0;
+      const long t192 = (long)((M + 191) / 192) * (N / kBN);
       if (N % kGB == 0 && N <= 4096 && t256 >= cus - cus / 8)
         launch_gemm_big<T>(A, B, M, N, K, out, s);
       else if (t64 <= cus)
-        launch_gemm_mfma<T, 64, 4>(A, B, M, N, K, out, s);
+        launch_gemm_mfma<T, 64, 6>(A, B, M, N, K, out, s);
+      else if (e.kind != GemmEpi::Geglu && t128x192 > 0 && t128x192 <= cus)
+        launch_gemm_mfma<T, 128, 3, 192>(A, B, M, N, K, out, s);
+      else if (t192 <= 2 * cus)
+        launch_gemm_mfma<T, 192, 2>(A, B, M, N, K, out, s);
       else if ((long)((M + 127) / 128) * (N / kBN) >= 3 * cus / 2)
         launch_gemm_mfma<T, 128>(A, B, M, N, K, out, s);
       else
