@@ -856,7 +856,8 @@ void gemm_t(const T* A, const T* B, int M, int N, int K, const GemmEpiArgs& e, h
       // blocks per CU hide more latency).  Below that every block streams
       // its operands at the latency of the last-level cache, so the tile is
       // chosen for the bytes it keeps in flight: a grid of at most one 64-row
-      // tile per CU takes a 6-deep ring (144 KB of LDS); a 128 x 192 tile with
+      // tile per CU takes a 4-deep ring (96 KB of LDS; 6 deep measured
+      // slower); a 128 x 192 tile with
       // a 3-deep ring where that grid fits the CUs once (not for the
       // gated-GELU pairs, which need wave tiles of whole 64-column groups);
       // 192-row tiles where two blocks per CU (80 KB each) cover the grid
@@ -869,7 +870,7 @@ void gemm_t(const T* A, const T* B, int M, int N, int K, const GemmEpiArgs& e, h
       if (N % kGB == 0 && N <= 4096 && t256 >= cus - cus / 8)
         launch_gemm_big<T>(A, B, M, N, K, out, s);
       else if (t64 <= cus)
-        launch_gemm_mfma<T, 64, 6>(A, B, M, N, K, out, s);
+        launch_gemm_mfma<T, 64, 4>(A, B, M, N, K, out, s);
       else if (e.kind != GemmEpi::Geglu && t128x192 > 0 && t128x192 <= cus)
         launch_gemm_mfma<T, 128, 3, 192>(A, B, M, N, K, out, s);
       else if (t192 <= 2 * cus)
