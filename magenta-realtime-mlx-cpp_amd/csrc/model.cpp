@@ -449,6 +449,8 @@ void State::setup_persistent() {
       codes <= (1 << kTagShift)) {
     lds_f_ = persist_prepare(m.dt, PersistKernel::Frame, m.device);
     frame_kernel_ = lds_f_ > 0;
+    // the levels after a speculative verification pass run in one launch too
+    if (frame_kernel_) lds_l_ = persist_prepare(m.dt, PersistKernel::Levels, m.device);
   }
   const size_t H = c.num_heads;
   // Tagged hand-off words: x, q, k, v, at, h vectors, cross partials, logits,
@@ -613,8 +615,10 @@ int State::spec_count(const GenOpts& o) const {
 }
 
 int State::decode_launches(const GenOpts& o) const {
-  const int ns = spec_count(o);  // speculative frames: temporal + L - 1 depth steps each
-  return ns * o.rvq_depth + (o.num_frames - ns) * (frame_kernel_ ? 1 : 1 + o.rvq_depth);
+  // speculative frames: the temporal step, then one launch of the open levels
+  // (or, without that kernel, L - 1 depth steps)
+  const int ns = spec_count(o);
+  return ns * (lds_l_ > 0 ? 2 : o.rvq_depth) + (o.num_frames - ns) * (frame_kernel_ ? 1 : 1 + o.rvq_depth);
 }
 
 StepArgs State::temporal_args(const void* in, int f, void* out) const {
@@ -802,6 +806,27 @@ void State::enqueue_decode_spec(const GenOpts& o) {
     sp_rest.decided = decided;
     spec_accept(dt, sdrawn_, d_drafts_ + static_cast<size_t>(f) * L, L, tok, decided, m.emb, D, d_in, stream);
     float* rec = o.record_slices ? o.record_slices + static_cast<size_t>(f) * L * rows * C : nullptr;
+    if (lds_l_ > 0) {
+      // the levels after the first disagreement in one persistent launch; the
+      // decided levels' logits come from the verification pass
+      if (rec)
+        for (int l = 0; l < L; ++l) spec_record(slog_, nullptr, decided, l, C, rec + static_cast<size_t>(l) * rows * C, stream);
+      FrameArgs fa{};
+      fa.d = depth_args(nullptr, 0, head0, C, nullptr, nullptr);
+      fa.d.sp = sp;
+      fa.d.sp.decided = decided;
+      fa.d.frame = f;
+      fa.d.tokens = d_tokens;
+      fa.d.emb = m.emb;
+      fa.d.noise = noise_ + static_cast<size_t>(f) * L * C;
+      fa.codebook = C;
+      fa.levels = L;
+      fa.rec_slices = rec;
+      fa.qkv_table = qkv_table_;
+      launch_levels(dt, fa, persist_grid_, lds_l_, stream);
+      frame_mean_tokens(dt, tok, L, m.emb, D, t_in, stream);
+      continue;
+    }
     if (rec) spec_record(slog_, slice, decided, 0, C, rec, stream);
     // the levels after the first disagreement; a decided level's step and
     // draw return at once, its draw feeding the known token on

@@ -283,7 +283,7 @@ class State {
   LLBufs ll_bufs(int stack = 1) const;  // hand-off words; delays of stack 0 (temporal) or 1 (depth)
   void reset_handoff();
   DecStack tstack_{}, dstack_{};  // temporal / depth stacks with this state's caches
-  size_t lds_t_ = 0, lds_d_ = 0, lds_f_ = 0;  // dynamic LDS of the persistent kernels
+  size_t lds_t_ = 0, lds_d_ = 0, lds_f_ = 0, lds_l_ = 0;  // dynamic LDS of the persistent kernels
   float* noise_ = nullptr;         // Gumbel noise of every draw of a decode call
   int* h_err_ = nullptr;        // pinned
   uint64_t* h_seed_ = nullptr;  // pinned: the draw seed of a generate / sample call

@@ -113,7 +113,7 @@ constexpr int kTraceDone = kTraceSlots - 1;
 // device (H * blocks-per-head, bph a power of two in [8, 16]); 0 if unsupported.
 int persist_grid(int H, int num_cu, int* bph);
 
-enum class PersistKernel { Temporal, Depth, Frame };
+enum class PersistKernel { Temporal, Depth, Frame, Levels };
 // Dynamic LDS bytes of a persistent kernel, after allowing the kernel to use
 // them; 0 if the device cannot give one workgroup that much, or cannot keep
 // one such workgroup resident per CU (occupancy query), in which case the
@@ -166,6 +166,11 @@ struct FrameArgs {
 // depth layers * levels <= kMaxResidentSlots.
 constexpr int kMaxResidentSlots = 64;
 void launch_frame(DType dt, const FrameArgs& a, int grid, size_t lds, hipStream_t s);
+// The depth levels after a speculative verification pass, in one launch:
+// levels *a.d.sp.decided + 1 .. a.levels - 1 of frame a.d.frame, each a depth
+// step (history staged from the ring), its head slice and a draw, as in
+// launch_frame; a.t is unused and the frame mean is not formed.
+void launch_levels(DType dt, const FrameArgs& a, int grid, size_t lds, hipStream_t s);
 
 // Gumbel noise of every draw of a decode call: out[(f * L + l) * C + c] =
 // gumbel(seed, f, l, c) for f < frames, l < L, c < C.

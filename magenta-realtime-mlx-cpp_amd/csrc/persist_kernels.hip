@@ -1751,6 +1751,98 @@ __global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu
   }
 }
 
+// The levels after a speculative verification pass, in one launch
+// (decode.cpp:429-446: the depth loop resumes after the first rejected draft).
+// Levels 0..n are decided, n = *d.sp.decided (written before this launch, the
+// same for every workgroup), tokens[frame * levels + n] the last of them; each
+// level n + 1 .. levels - 1 is a depth step on emb(previous token), the
+// level's head slice and workgroup 0's draw, as in k_frame.  The attention
+// workgroups first copy the decided levels' K/V (ring slots 0..n, written by
+// the verification pass in earlier launches) into their LDS history; the
+// levels of this launch then keep theirs in LDS, as k_frame does (ring slots
+// written in this launch are not read back in it: the caches of the XCDs are
+// coherent only between launches).  With every level decided the launch does
+// nothing: no word is tagged and the epoch stays.  The frame mean is left to
+// the caller.
+template <typename T>
+__global__ __launch_bounds__(kPersistThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_levels(FrameArgs fa) {
+  MRT_DECLARE_LDS(T);
+  const StepArgs& ad = fa.d;
+  const int L = fa.levels, C = fa.codebook, D = ad.D;
+  const int n = *ad.sp.decided;
+  const bool ok = start<T>(c, ad.ll, ad.bph);
+  if (n < 0 || n + 1 >= L) return;
+  const bool tbl = fa.qkv_table != nullptr;
+  if (!tbl) prefetch_qkv<T, false>(c, ad, 0);
+  if (c.jpart == 0) {
+    // wave w copies region (kind w / 2, row w % 2) of every layer: slots 0..n
+    const int kind = c.wid >> 1, b = c.wid & 1;
+    const size_t eRing = (size_t)2 * ad.H * ad.Lmax * 64;
+    const long lim = (long)ad.Lmax * 64 * sizeof(T);
+    for (int li = 0; li < ad.nlayers; ++li) {
+      const T* src = static_cast<const T*>(ad.st.ring) + (2 * li + kind) * eRing + (size_t)(b * ad.H + c.h) * ad.Lmax * 64;
+      T* region = c.dyn + (size_t)li * 4 * L * 64 + (size_t)c.wid * L * 64;
+      if (kind == 0)
+        stage_slots<T, true>(src, n + 1, lim, region);
+      else
+        stage_slots<T, false>(src, n + 1, lim, region);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's history copies have landed
+  }
+  __syncthreads();
+  if (!ok) return;
+  const int per_step = 16 * (ad.nlayers + 1);
+  SampleParams sp = ad.sp;
+  sp.decided = nullptr;  // every level drawn here is open
+  DrawPrefetch pf{};
+  if (c.blk == 0) {
+    draw_clear(c.sel_hist);
+    draw_prefetch(C, ad.noise + (size_t)(n + 1) * C, ad.teacher, ad.frame * L + n + 1, pf);
+  }
+  int tok = ad.tokens[(size_t)ad.frame * L + n];
+  uint32_t x_tag = 0;
+  for (int l = n + 1; l < L; ++l) {
+    const int base = l * per_step;
+    StackIO io{static_cast<const T*>(ad.emb) + (size_t)tok * D, 0, x_tag, nullptr, true, base, true, L, l,
+               nullptr, nullptr, !tbl};
+    const int cb = tok - ad.sp.codec_offset - C * (l - 1);
+    if (tbl && cb >= 0 && cb < C) io.qkv_row = static_cast<const T*>(fa.qkv_table) + ((size_t)(l - 1) * C + cb) * 3 * ad.HD;
+    x_tag = run_stack<T, false>(c, ad, io);
+    const T* hw = static_cast<const T*>(ad.head_w) + (size_t)l * C * D;
+    prefetch_head<T>(c, ad, hw);
+    const uint32_t tg_logit = c.tag(base + 16 * ad.nlayers + kPhLogit);
+    const uint32_t tg_tok = c.tag(base + 16 * ad.nlayers + kPhToken);
+    run_head<T>(c, ad, hw, x_tag, tg_logit, nullptr);
+    if (c.blk != 0 && l + 1 < L && !tbl) prefetch_qkv<T, false>(c, ad, 0);
+    if (c.blk == 0) {
+      if (l + 1 == L && threadIdx.x == 0) astore(ad.ll.seq, c.ep + 1u);  // every workgroup has started
+      const int slot = ad.frame * L + l;
+      __syncthreads();
+      float* lg = c.xsb[c.xsel ^ 1];
+      gather_logits<T>(ad, tg_logit, lg, nullptr, fa.rec_slices ? fa.rec_slices + (size_t)l * 2 * C : nullptr);
+      if (l + 1 < L && !tbl) prefetch_qkv<T, false>(c, ad, 0);
+      tok = sample_block<T>(sp, l, slot, pf, ad.teacher != nullptr, ad.tokens, ad.drawn, l + 1 < L ? ad.ll.tok : nullptr,
+                            tg_tok, lg, c.sel_hist, c.sel_res, nullptr);
+      if (l + 1 < L) draw_prefetch(C, ad.noise + (size_t)(l + 1) * C, ad.teacher, slot + 1, pf);
+    } else if (l + 1 < L) {
+      __shared__ int tok_s;
+      if (threadIdx.x == 0) {
+        uint32_t spins = 0;
+        uint64_t w;
+        poll_wait(ad.ll.delay[kPollToken]);
+        for (;;) {
+          w = aload(ad.ll.tok);
+          if (ll_tag(w) == tg_tok || spin_failed(spins, ad.ll.err)) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+        tok_s = ll_tag(w) == tg_tok ? (int)static_cast<uint32_t>(w) : 0;
+      }
+      __syncthreads();
+      tok = tok_s;
+    }
+  }
+}
+
 template <typename T>
 size_t lds_bytes() {
   return 4 * static_cast<size_t>(kRegion) * sizeof(T);
@@ -1776,6 +1868,7 @@ template <typename T, bool TRACE>
 const void* persist_fn(PersistKernel kind) {
   return kind == PersistKernel::Temporal ? reinterpret_cast<const void*>(&k_step<T, true, TRACE>)
          : kind == PersistKernel::Depth  ? reinterpret_cast<const void*>(&k_step<T, false, TRACE>)
+         : kind == PersistKernel::Levels ? reinterpret_cast<const void*>(&k_levels<T>)
                                          : reinterpret_cast<const void*>(&k_frame<T, TRACE>);
 }
 
@@ -1855,6 +1948,13 @@ void launch_frame(DType dt, const FrameArgs& a, int grid, size_t lds, hipStream_
     else
       hipLaunchKernelGGL((k_frame<T, false>), dim3(grid), dim3(kPersistThreads), lds, s, a);
   });
+  MRT_HIP_CHECK(hipGetLastError());
+}
+
+void launch_levels(DType dt, const FrameArgs& a, int grid, size_t lds, hipStream_t s) {
+  MRT_REQUIRE(a.d.sp.decided != nullptr && a.d.tokens != nullptr && a.d.noise != nullptr,
+              "levels launch: the decided count, the token and the noise buffers are required");
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL((k_levels<T>), dim3(grid), dim3(kPersistThreads), lds, s, a));
   MRT_HIP_CHECK(hipGetLastError());
 }
 

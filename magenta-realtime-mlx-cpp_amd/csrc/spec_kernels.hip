@@ -66,10 +66,12 @@ __global__ void k_frame_mean_tokens(const int* __restrict__ tokens, int L, const
 }
 
 // The logits level l was drawn from: the verification pass's rows (2l, 2l+1)
-// when l <= *decided, else the depth step's slice.
+// when l <= *decided, else the depth step's slice (nullptr: left alone, the
+// level's step records its own).
 __global__ void k_spec_record(const float* __restrict__ all, const float* __restrict__ slice,
                               const int* __restrict__ decided, int l, int C, float* __restrict__ dst) {
   const float* src = l <= *decided ? all + (size_t)2 * l * C : slice;
+  if (src == nullptr) return;
   for (int i = threadIdx.x; i < 2 * C; i += blockDim.x) dst[i] = src[i];
 }
 

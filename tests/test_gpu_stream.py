@@ -250,7 +250,8 @@ def test_stream_adaptive_speculation(tiny):
     the probed levels came from the verification pass, whole chunks
     speculate while that holds; after a miss, 4 chunks decode plainly before
     the next probe, 8 after a further miss, and so on.  The expected mode and
-    launch count of every chunk are replayed from the acceptance each
+    launch count (a speculated frame: the temporal step and one launch of
+    its open levels) of every chunk are replayed from the acceptance each
     speculating chunk reported, and the acceptance is taken over the
     speculated frames only."""
     mrt_df = tiny["mrt_df"]
@@ -266,7 +267,8 @@ def test_stream_adaptive_speculation(tiny):
         accs.append(acc)
         # the policy, replayed: the first chunk has no drafts; a paused chunk decodes plainly
         spec = i > 0 and pause == 0
-        want = (F * L if full else probe * L + (F - probe)) if spec else F
+        # a speculated frame: the temporal step and one launch of its open levels
+        want = (F * 2 if full else probe * 2 + (F - probe)) if spec else F
         assert launches == want, (i, modes, accs)
         assert (acc >= 0.0) == spec
         if spec and not full:
