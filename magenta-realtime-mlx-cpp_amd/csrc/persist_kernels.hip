@@ -1349,7 +1349,6 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
           stage_slots<T, false>(src, nk, lim, cst + wid * kRegion);
       }
     };
-    if (CROSS && jpart != 0) stage_cross();
     // ---- QKV of head h's slice (weights already in flight), unless layer 0's
     // q/k/v come from a table row: the attention workgroups then read their
     // head's slice there and the others go on to the output projection.
@@ -1396,6 +1395,10 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
       }
     }
     }  // QKV phase
+    // The cross K/V block of a workgroup that runs no self attention: after the
+    // QKV poll (which would otherwise wait for these copies), while the heads'
+    // attention runs.
+    if (CROSS && jpart != 0) stage_cross();
     // Head h's attention in workgroup (h, 0), then the next phase's weights:
     // its polls would otherwise also wait for those loads.
     const T* wo = static_cast<const T*>(a.st.wo) + li * eO;
