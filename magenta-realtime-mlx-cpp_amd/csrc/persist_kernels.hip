@@ -1326,15 +1326,20 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
     const int in_stride = io.in_stride;
     // ---- stage the ring history and cross K/V block of this layer in LDS
     T* lhist = io.resident ? hist + (size_t)li * 4 * io.cap * 64 : hist;
-    if (!io.resident && jpart == 0 && io.pos > 0) {
+    // ring slots 0..pos-1 of layer lj (written by earlier launches) into the
+    // history regions, by the attention workgroups
+    auto stage_hist = [&](int lj) {
       const int kind = wid >> 1, b = wid & 1;
-      const T* src = ring_k + kind * eRing + (size_t)(b * H + h) * a.Lmax * 64;
+      const T* src = static_cast<const T*>(a.st.ring) + (2 * lj + kind) * eRing + (size_t)(b * H + h) * a.Lmax * 64;
       const long lim = (long)a.Lmax * 64 * sizeof(T);
       if (kind == 0)
         stage_slots<T, true>(src, io.pos, lim, hist + wid * kRegion);
       else
         stage_slots<T, false>(src, io.pos, lim, hist + wid * kRegion);
-    }
+    };
+    // with cross attention, layers after the first were staged at the end of
+    // the previous layer's cross attention
+    if (!io.resident && jpart == 0 && io.pos > 0 && (!CROSS || first)) stage_hist(li);
     auto stage_cross = [&]() {
       const int chunk = (a.S + bph - 1) / bph, kb0 = jpart * chunk;
       const int nk = max(0, min(chunk, a.S - kb0));
@@ -1437,6 +1442,10 @@ __device__ __forceinline__ uint32_t run_stack(Ctx<T>& c, const StepArgs& a, cons
       if (jpart == 0) {
         cross_combine<T>(a, h, tag(base + kPhCP), tag(base + kPhCC), sm);
         MRT_TP;
+        // the staged cross K/V has been read (barrier in cross_partial): the
+        // next layer's history copies go out now, so that its QKV poll does
+        // not wait for them
+        if (!io.resident && !last && io.pos > 0) stage_hist(li + 1);
       }
       xs = c.next_xs();
       load_act<T, 4, false>(a.ll.at, nullptr, HD, tag(base + kPhCC), c.gq, xs, red,
