@@ -940,6 +940,7 @@ __device__ __forceinline__ void cross_combine(const StepArgs& a, int h, uint32_t
 // ---- sampling -------------------------------------------------------------------
 
 constexpr int kDrawPer = 1024 / kPersistThreads;  // candidates and d_model elements per thread
+constexpr int kChainSteps = 3;  // restricted-argmax steps of a draw before its radix select
 constexpr int kHistWords = 3 * 4 * 256;           // 3 rotating buffers x 4 per-wave 256-bin histograms
 
 // Loads of a draw that do not depend on the logits (issued before the gather).
@@ -1078,8 +1079,9 @@ __device__ __forceinline__ uint32_t radix_select(const uint32_t (&key)[kDrawPer]
 // path: A = argmax of v + g over all candidates is that answer whenever A is
 // in the top-k set, i.e. fewer than k values are strictly greater than v_A
 // (every candidate of the set is a candidate of the full argmax, and A is the
-// smallest index attaining its maximum).  Otherwise the k-th largest value is
-// found by radix select and the masked argmax is taken.  The fed token is
+// smallest index attaining its maximum).  Otherwise up to kChainSteps
+// restricted argmaxes (below), and only then the k-th largest value by radix
+// select and the masked argmax.  The fed token is
 // published (`tok_word`, tagged, when non-null) as soon as it is known.
 // Returns the fed token (the same in every thread).
 template <typename T>
@@ -1126,9 +1128,29 @@ __device__ __forceinline__ int sample_block(const SampleParams& p, int level, in
       for (int t = 0; t < kPer; ++t) n += __popcll(__ballot(tid + kPersistThreads * t < C && v[t] > va));
       if ((tid & 63) == 0) wres[8 + wid] = n;
       __syncthreads();
-      const int greater = wres[8] + wres[9] + wres[10] + wres[11];
+      int greater = wres[8] + wres[9] + wres[10] + wres[11];
       tpoint(2);
-      if (greater >= p.top_k) {  // the unmasked winner is outside the top-k set
+      // Chain steps: while the winner B is outside the top-k set (at least k
+      // values are strictly greater than v_B, so the k-th largest value is
+      // too), the set lies within {v > v_B}, and the winner over that subset
+      // is the answer as soon as it is in the set itself (the smallest index
+      // attaining the maximum over a superset that lies in the set).  Each
+      // step strictly shrinks the subset; after kChainSteps the radix select
+      // below finds the threshold instead.
+      for (int step = 0; step < kChainSteps && greater >= p.top_k; ++step) {
+        const float vb = __fdiv_rn(guided(arg), p.temperature);
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) w[t] = v[t] > vb ? v[t] + pf.gn[t] : -INFINITY;
+        arg = block_argmax(w, C, wres);
+        const float vn = __fdiv_rn(guided(arg), p.temperature);
+        int m = 0;
+#pragma unroll
+        for (int t = 0; t < kPer; ++t) m += __popcll(__ballot(tid + kPersistThreads * t < C && v[t] > vn));
+        if ((tid & 63) == 0) wres[8 + wid] = m;
+        __syncthreads();
+        greater = wres[8] + wres[9] + wres[10] + wres[11];
+      }
+      if (greater >= p.top_k) {  // the winner is still outside the top-k set
         uint32_t key[kPer];
 #pragma unroll
         for (int t = 0; t < kPer; ++t) key[t] = (tid + kPersistThreads * t < C) ? float_key(v[t]) : 0u;

@@ -1,4 +1,5 @@
-"""The early stop of the top-k threshold selects in the draw kernels, checked
+"""The early stop of the top-k threshold selects in the draw kernels and the
+restricted-argmax chain of the frame kernel's draw, checked
 as an algorithm on the CPU (numpy models of the two device selects; the
 device code itself is checked draw by draw against the oracle sampler in the
 GPU tests).
@@ -118,3 +119,56 @@ def test_normal_logits_stop_after_two_or_three_bytes(k):
     rng = np.random.default_rng(1)
     passes = [byte_select((rng.normal(0, 2.0, 1024) / 1.1).astype(np.float32), k)[1] for _ in range(300)]
     assert max(passes) <= 2 or np.mean(np.array(passes) <= 2) > 0.95
+
+
+def _masked_argmax(v, g, k):
+    """The reference's draw: argmax of v + g over {v >= k-th largest v}, the
+    smallest index among equal maxima (decode.cpp:119-125, mx::argmax)."""
+    keep = v >= np.sort(v)[::-1][k - 1]
+    w = np.where(keep, v + g, -np.inf).astype(np.float32)
+    return int(np.argmax(w))
+
+
+def chain_draw(v, g, k, steps):
+    """The frame kernel's draw (sample_block): the unmasked winner, then up to
+    `steps` winners restricted to {v > v_prev}, each accepted once fewer than k
+    values exceed it; else the exact threshold (the radix select's set).
+    Returns (index, the number of restricted steps taken, fell back)."""
+    w = (v + g).astype(np.float32)
+    a = int(np.argmax(w))
+    taken = 0
+    while (v > v[a]).sum() >= k:
+        if taken == steps:
+            return _masked_argmax(v, g, k), taken, True
+        w = np.where(v > v[a], (v + g).astype(np.float32), -np.inf)
+        a = int(np.argmax(w))
+        taken += 1
+    return a, taken, False
+
+
+def test_chain_steps_give_the_masked_draw():
+    """Every draw of the restricted-argmax chain equals the reference's masked
+    draw, on rows with ties in v and in v + g, signed zeros, denormals and
+    huge values, for chain lengths 0..3 (0: the fast path, then the select)."""
+    rng = np.random.default_rng(2)
+    taken_seen = set()
+    for i, (v, k) in enumerate(_rows(rng, 1500)):
+        if i % 3 == 0:
+            g = rng.choice([0.0, 0.5, 1.0], v.size).astype(np.float32)  # ties in v + g
+        else:
+            g = (-np.log(-np.log(rng.random(v.size)))).astype(np.float32)
+        want = _masked_argmax(v, g, k)
+        for steps in (0, 1, 3):
+            got, taken, _ = chain_draw(v, g, k, steps)
+            assert got == want, (i, k, steps)
+            taken_seen.add(taken)
+    assert {0, 1, 2, 3} <= taken_seen  # every chain length was exercised
+
+
+def test_chain_steps_spare_most_selects_on_flat_logits():
+    """Flat guided logits (the random-weight benchmark's): the chain of 3
+    settles most draws that miss the fast path without the radix select."""
+    rng = np.random.default_rng(3)
+    fell = [chain_draw((rng.normal(0, 1.0, 1024) / 1.1).astype(np.float32),
+                       (-np.log(-np.log(rng.random(1024)))).astype(np.float32), 40, 3)[2] for _ in range(400)]
+    assert np.mean(fell) < 0.2
