@@ -4,7 +4,8 @@
 // One workgroup per stream; its first wave draws, with the level's C logits
 // (C <= 1024) in registers, 16 per lane.  The draw is Gumbel-max over the kept entries with
 // Philox-4x32-10 noise.  When the winner over every candidate is itself in the
-// top-k set it is the answer; otherwise the top-k threshold (the k-th largest
+// top-k set it is the answer; else up to 3 winners over {v > v_previous
+// winner} are tried the same way; otherwise the top-k threshold (the k-th largest
 // value, counting ties, i.e. min(topk(x, k)) of decode.cpp:119-120) is found
 // by a bitwise radix select over order-preserving float keys (at most 32
 // steps, each counting with a DPP wave sum; it stops once exactly k keys lie
@@ -19,6 +20,7 @@ namespace mrt {
 namespace {
 
 constexpr int kMaxPerLane = 16;  // C <= 1024
+constexpr int kChainSteps = 3;   // restricted-argmax steps of a draw before its radix select
 constexpr int kFeedPer = 8;      // d_model elements per thread in the feedback (d_model <= 2048)
 
 // Sum over the 64 lanes with DPP (row shifts and broadcasts, no LDS
@@ -119,6 +121,33 @@ __device__ __forceinline__ int wave_draw_rows(const float* __restrict__ l0, cons
 #pragma unroll
       for (int t = 0; t < kMaxPerLane; ++t) above += (lane + 64 * t < C && v[t] > va) ? 1 : 0;
       done = dpp_sum_i(above) < p.top_k;
+      // Restricted steps: while the winner is outside the top-k set, the set
+      // lies within {v > v_winner}; the winner over that subset is the answer
+      // once it is in the set (it maximises over a superset of the set,
+      // smallest index first).  Each step shrinks the subset strictly.
+      for (int step = 0; step < kChainSteps && !done; ++step) {
+        best = -INFINITY;
+        bi = 0x7fffffff;
+#pragma unroll
+        for (int t = 0; t < kMaxPerLane; ++t) {
+          const int c = lane + 64 * t;
+          const float w = v[t] + gn[t];
+          if (c < C && v[t] > va && (w > best || bi == 0x7fffffff)) {
+            best = w;
+            bi = c;
+          }
+        }
+        wave_argmax(best, bi);
+        va = 0.f;
+#pragma unroll
+        for (int t = 0; t < kMaxPerLane; ++t)
+          if (lane + 64 * t == bi) va = v[t];
+        va = __shfl(va, bi & 63, 64);
+        above = 0;
+#pragma unroll
+        for (int t = 0; t < kMaxPerLane; ++t) above += (lane + 64 * t < C && v[t] > va) ? 1 : 0;
+        done = dpp_sum_i(above) < p.top_k;
+      }
     }
     if (!done && p.top_k > 0 && p.top_k < C) {
       uint32_t key[kMaxPerLane];
