@@ -347,7 +347,23 @@ __device__ __forceinline__ void mfma_epilogue(const GemmOut<T>& out, const f32x1
 // leaves room for two (at most 80 KB), else one.
 constexpr int gemm_min_blocks(int BM, int S, int BN) { return S * (BM + BN) * 128 <= 80 * 1024 ? 2 : 1; }
 
-template <typename T, int BM, int S, int BN>
+// Tile of block L of a 1-D grid in the XCD-grouped order: blocks are dealt to
+// the 8 XCDs in turn (L % 8), each XCD takes a contiguous range of tile ids,
+// and tile ids run down GM row tiles before the next column tile, so the
+// blocks that one XCD runs together share GM A tiles and a few B tiles in its
+// L2.  A bijection of [0, tm * tn).
+__device__ __forceinline__ void grouped_tile(int L, int tm, int tn, int GM, int& mt, int& nt) {
+  const int tiles = tm * tn, x = L & 7, q = tiles >> 3, rem = tiles & 7;
+  const int pid = x * q + min(x, rem) + (L >> 3);
+  const int g = pid / (GM * tn), first = g * GM, gsz = min(tm - first, GM);
+  const int w = pid - g * GM * tn;
+  mt = first + w % gsz;
+  nt = w / gsz;
+}
+
+// GM = 0: block (x, y) of a 2-D grid computes tile (y, x); GM > 0: a 1-D grid
+// in the grouped_tile order.
+template <typename T, int BM, int S, int BN, int GM>
 __global__ __launch_bounds__(256, gemm_min_blocks(BM, S, BN)) void k_gemm_mfma(const T* __restrict__ A,
                                                                                const T* __restrict__ B,
                                                    int M, int N, int K, GemmOut<T> out) {
@@ -359,7 +375,9 @@ __global__ __launch_bounds__(256, gemm_min_blocks(BM, S, BN)) void k_gemm_mfma(c
   extern __shared__ __align__(16) unsigned char lds[];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid >> 1, wn = wid & 1;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  int mt = blockIdx.y, nt = blockIdx.x;
+  if constexpr (GM > 0) grouped_tile(blockIdx.x, (M + BM - 1) / BM, N / BN, GM, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
   const int nk = K / kBK;
 
   // tile kt -> stage kt % S; wave w loads rows [w*BM/4, +BM/4) of A and
@@ -458,16 +476,18 @@ int device_cus() {
   return v;
 }
 
-template <typename T, int BM, int S = kStages, int BN = kBN>
+template <typename T, int BM, int S = kStages, int BN = kBN, int GM = 0>
 void launch_gemm_mfma(const T* A, const T* B, int M, int N, int K, const GemmOut<T>& out, hipStream_t s) {
   static_assert((S - 2) * (BM / 32 + BN / 32) < 64, "vmcnt holds at most 63 outstanding loads");
   static_assert(BM % 64 == 0 && BN % 64 == 0, "wave tiles are whole 32x32 MFMA tiles");
   constexpr size_t lds = (size_t)S * (BM + BN) * 128;
   static_assert(lds <= 160 * 1024, "LDS of one CU");
   MRT_REQUIRE(N % BN == 0, "gemm: N is not a multiple of the tile width");
-  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_mfma<T, BM, S, BN>), lds);
-  hipLaunchKernelGGL((k_gemm_mfma<T, BM, S, BN>), dim3(N / BN, (M + BM - 1) / BM), dim3(256), lds, s, A, B, M, N, K,
-                     out);
+  allow_dynamic_lds(reinterpret_cast<const void*>(&k_gemm_mfma<T, BM, S, BN, GM>), lds);
+  const long tm = (M + BM - 1) / BM, tn = N / BN;
+  MRT_REQUIRE(GM == 0 || tm * tn <= 0x7fffffffL, "gemm: too many tiles");
+  const dim3 grid = GM > 0 ? dim3(static_cast<unsigned>(tm * tn)) : dim3(tn, tm);
+  hipLaunchKernelGGL((k_gemm_mfma<T, BM, S, BN, GM>), grid, dim3(256), lds, s, A, B, M, N, K, out);
 }
 
 // Large-M GEMM (the encoder of several streams): 256 x 256 x 64 tiles, 16
@@ -651,11 +671,93 @@ constexpr float kLog2e = 1.4426950408889634f;
 // the 16-byte fragment reads of 8 consecutive dims conflict-free.
 __device__ __forceinline__ int vt_chunk(int ch, int dim) { return (ch ^ ((dim >> 3) & 7)) << 3; }
 
+// Scores of one 64-key tile from the staged K rows: sc[t] holds S^T for keys
+// 32 t + 8 (r / 4) + 4 hf + r % 4 of the tile, query lq.
 template <typename T>
-// Three blocks per CU (3 waves per SIMD: the register budget is 170), which
-// measured faster than the compiler's 196 registers at two.
-__global__ __launch_bounds__(256, 3) void k_enc_attn_mfma(const T* __restrict__ qkv, int S, int H,
-                                                       T* __restrict__ out) {
+__device__ __forceinline__ void attn_scores(const T* Ks, const typename Mfma<T>::v8 (&qf)[4], int lq, int hf,
+                                            f32x16_t (&sc)[2]) {
+  typedef typename Mfma<T>::v8 v8;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[t][r] = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const v8 a = *reinterpret_cast<const v8*>(&Ks[(32 * t + lq) * kALD + 16 * s + 8 * hf]);
+      sc[t] = Mfma<T>::mma(a, qf[s], sc[t]);
+    }
+  }
+}
+
+// Online-softmax step of one tile (keys kb ..): running max m, sum lsum and
+// output accumulators acc, with the tile's V^T staged in Vt.
+template <typename T>
+__device__ __forceinline__ void attn_update(f32x16_t (&sc)[2], int kb, int S, int lq, int hf, const T* Vt, float& m,
+                                            float& lsum, f32x16_t (&acc)[2]) {
+  typedef typename Mfma<T>::v8 v8;
+  float mt = -INFINITY;
+  if (kb + kAK <= S) {  // a full tile (wave-uniform): no key to mask
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[t][r]);
+  } else {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
+        sc[t][r] = key < S ? sc[t][r] : -INFINITY;
+        mt = fmaxf(mt, sc[t][r]);
+      }
+  }
+  mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+  const float mn = fmaxf(m, mt);  // raw-score running max (key 0 is never masked)
+  const float mns = mn * kLog2e;
+  const float corr = __builtin_amdgcn_exp2f(fmaf(m, kLog2e, -mns));
+  float ps = 0.f;
+  v8 pb[4], pl[4];  // P^T = hi + lo (storage type each) for the four 16-key steps
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    f32x8_t pv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      pv[i] = __builtin_amdgcn_exp2f(fmaf(sc[g >> 1][8 * (g & 1) + i], kLog2e, -mns));
+      ps += pv[i];
+    }
+    pb[g] = __builtin_convertvector(pv, v8);  // round-to-nearest-even conversions
+    pl[g] = __builtin_convertvector(pv - __builtin_convertvector(pb[g], f32x8_t), v8);
+  }
+  ps += __shfl_xor(ps, 32, 64);
+  lsum = lsum * corr + ps;
+  m = mn;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] *= corr;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const v8 a = *reinterpret_cast<const v8*>(&Vt[(32 * t + lq) * kALD + vt_chunk(2 * s + hf, 32 * t + lq)]);
+      acc[t] = Mfma<T>::mma(a, pb[s], acc[t]);
+      acc[t] = Mfma<T>::mma(a, pl[s], acc[t]);
+    }
+}
+
+// AHEAD = false: tile j + 1's K and V are loaded while tile j is processed.
+// Sized for three blocks per CU (3 waves per SIMD: the register budget is
+// 170), which measured faster than the compiler's 196 registers at two.
+// AHEAD = true (grids of at most two blocks per CU, where one wave per SIMD
+// has no other wave to hide its latencies): the scores of tile j + 1 are
+// computed before tile j's softmax, so the two dependency chains overlap in
+// the wave; K is staged two tiles ahead and V one.  Both run the same
+// arithmetic on every query (attn_scores / attn_update over the tiles in
+// order), so their outputs are bit-equal and a stream's rows do not depend
+// on the batch it is encoded in.
+template <typename T, bool AHEAD>
+__global__ __launch_bounds__(256, AHEAD ? 2 : 3) void k_enc_attn_mfma(const T* __restrict__ qkv, int S, int H,
+                                                                     T* __restrict__ out) {
   typedef typename Mfma<T>::v8 v8;
   __shared__ __attribute__((aligned(16))) T Ks[2][kAK * kALD];
   __shared__ __attribute__((aligned(16))) T Vt[2][64 * kALD];
@@ -673,30 +775,30 @@ __global__ __launch_bounds__(256, 3) void k_enc_attn_mfma(const T* __restrict__ 
 #pragma unroll
     for (int s = 0; s < 4; ++s) qf[s] = *reinterpret_cast<const v8*>(qr + 16 * s + 8 * hf);
   }
-  // Tile staging: thread t moves 16 bytes of K and of V for keys t/8 and
-  // 32 + t/8, dims 8 (t % 8) .. +7; keys past S are zero.  (Clamping those
-  // keys to S - 1 instead, with no conditional load, made the compiler keep
-  // the Q fragments in scratch memory.)
+  // Tile staging: thread t moves 16 bytes of K (part 1 of the q/k/v row) or V
+  // (part 2) for keys t/8 and 32 + t/8, dims 8 (t % 8) .. +7; keys past S are
+  // zero.  (Clamping those keys to S - 1 instead, with no conditional load,
+  // made the compiler keep the Q fragments in scratch memory.)
   uint4 rk[2], rv[2];
-  auto gload = [&](int kb) {
+  auto gload = [&](uint4 (&r)[2], int kb, int part) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int key = kb + (tid >> 3) + 32 * i, c = (tid & 7) * 8;
-      if (key < S) {
-        const T* row = base + (size_t)key * ld;
-        rk[i] = *reinterpret_cast<const uint4*>(row + HD + c);
-        rv[i] = *reinterpret_cast<const uint4*>(row + 2 * HD + c);
-      } else {
-        rk[i] = make_uint4(0u, 0u, 0u, 0u);
-        rv[i] = make_uint4(0u, 0u, 0u, 0u);
-      }
+      r[i] = key < S ? *reinterpret_cast<const uint4*>(base + (size_t)key * ld + part * HD + c)
+                     : make_uint4(0u, 0u, 0u, 0u);
     }
   };
-  auto sstore = [&](int buf) {
+  auto kstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int key = (tid >> 3) + 32 * i, c = (tid & 7) * 8;
       *reinterpret_cast<uint4*>(&Ks[buf][key * kALD + c]) = rk[i];
+    }
+  };
+  auto vstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int key = (tid >> 3) + 32 * i, c = (tid & 7) * 8;
       const int slot = (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
       const T* v = reinterpret_cast<const T*>(&rv[i]);
 #pragma unroll
@@ -710,76 +812,47 @@ __global__ __launch_bounds__(256, 3) void k_enc_attn_mfma(const T* __restrict__ 
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.f;
   float m = -INFINITY, lsum = 0.f;
-
-  gload(0);
-  sstore(0);
-  __syncthreads();
   const int ntiles = (S + kAK - 1) / kAK;
+
+  gload(rk, 0, 1);
+  gload(rv, 0, 2);
+  kstore(0);
+  vstore(0);
+  if constexpr (AHEAD) {
+    if (ntiles > 1) {
+      gload(rk, kAK, 1);
+      kstore(1);
+    }
+  }
+  __syncthreads();
+  f32x16_t sc[2];
+  if constexpr (AHEAD) attn_scores<T>(Ks[0], qf, lq, hf, sc);
   for (int j = 0; j < ntiles; ++j) {
     const int cur = j & 1, kb = j * kAK;
-    if (j + 1 < ntiles) gload(kb + kAK);
-    // S^T for keys kb + 32 t + (8 (r/4) + 4 hf + r%4), query q
-    f32x16_t sc[2];
+    if constexpr (AHEAD) {
+      if (j + 2 < ntiles) gload(rk, kb + 2 * kAK, 1);
+      if (j + 1 < ntiles) gload(rv, kb + kAK, 2);
+      f32x16_t sn[2];
+      if (j + 1 < ntiles) attn_scores<T>(Ks[cur ^ 1], qf, lq, hf, sn);
+      attn_update<T>(sc, kb, S, lq, hf, Vt[cur], m, lsum, acc);
+      if (j + 2 < ntiles) kstore(cur);
+      if (j + 1 < ntiles) vstore(cur ^ 1);
+      __syncthreads();
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sc[t][r] = 0.f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const v8 a = *reinterpret_cast<const v8*>(&Ks[cur][(32 * t + lq) * kALD + 16 * s + 8 * hf]);
-        sc[t] = Mfma<T>::mma(a, qf[s], sc[t]);
-      }
-    }
-    float mt = -INFINITY;
-    if (kb + kAK <= S) {  // a full tile (wave-uniform): no key to mask
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[t][r]);
+      for (int t = 0; t < 2; ++t) sc[t] = sn[t];
     } else {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb + 32 * t + 8 * (r >> 2) + 4 * hf + (r & 3);
-          sc[t][r] = key < S ? sc[t][r] : -INFINITY;
-          mt = fmaxf(mt, sc[t][r]);
-        }
-    }
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float mn = fmaxf(m, mt);  // raw-score running max (key 0 is never masked)
-    const float mns = mn * kLog2e;
-    const float corr = __builtin_amdgcn_exp2f(fmaf(m, kLog2e, -mns));
-    float ps = 0.f;
-    v8 pb[4], pl[4];  // P^T = hi + lo (storage type each) for the four 16-key steps
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      f32x8_t pv;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        pv[i] = __builtin_amdgcn_exp2f(fmaf(sc[g >> 1][8 * (g & 1) + i], kLog2e, -mns));
-        ps += pv[i];
+      if (j + 1 < ntiles) {
+        gload(rk, kb + kAK, 1);
+        gload(rv, kb + kAK, 2);
       }
-      pb[g] = __builtin_convertvector(pv, v8);  // round-to-nearest-even conversions
-      pl[g] = __builtin_convertvector(pv - __builtin_convertvector(pb[g], f32x8_t), v8);
-    }
-    ps += __shfl_xor(ps, 32, 64);
-    lsum = lsum * corr + ps;
-    m = mn;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[t][r] *= corr;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const v8 a = *reinterpret_cast<const v8*>(&Vt[cur][(32 * t + lq) * kALD + vt_chunk(2 * s + hf, 32 * t + lq)]);
-        acc[t] = Mfma<T>::mma(a, pb[s], acc[t]);
-        acc[t] = Mfma<T>::mma(a, pl[s], acc[t]);
+      attn_scores<T>(Ks[cur], qf, lq, hf, sc);
+      attn_update<T>(sc, kb, S, lq, hf, Vt[cur], m, lsum, acc);
+      if (j + 1 < ntiles) {
+        kstore(cur ^ 1);
+        vstore(cur ^ 1);
       }
-    if (j + 1 < ntiles) sstore(cur ^ 1);
-    __syncthreads();
+      __syncthreads();
+    }
   }
   if (q < S) {
     T* orow = out + ((size_t)b * S + q) * HD + h * 64;
@@ -851,9 +924,14 @@ void gemm_t(const T* A, const T* B, int M, int N, int K, const GemmEpiArgs& e, h
   if constexpr (sizeof(T) == 2) {
     if (allow_mfma && N % kBN == 0 && K % kBK == 0) {
       // Measured on MI355X (256 CUs) at 2 x 1006 x {1, 8, 32} rows: 256 x 256
-      // tiles for outputs up to 4096 wide once they give about one tile per
-      // CU (slower for the 5632- and 40960-wide outputs, where 2-3 smaller
-      // blocks per CU hide more latency).  Below that every block streams
+      // tiles of 16 waves for outputs up to 4096 wide once they give about
+      // one tile per CU (slower for the 5632- and 40960-wide outputs, where
+      // 2-3 smaller blocks per CU hide more latency); for the wider outputs
+      // other than the gated-GELU pairs (the 40960-wide cross K/V projection)
+      // 256 x 256 tiles of 4 waves with 128 x 128 wave tiles (half the LDS
+      // fragment reads per product) in the XCD-grouped order: 280 -> 234 us
+      // at one stream, 7.35 -> 6.41 ms at 32 (the gated-GELU output measured
+      // slower with them).  Below that every block streams
       // its operands at the latency of the last-level cache, so the tile is
       // chosen for the bytes it keeps in flight: a grid of at most one 64-row
       // tile per CU takes a 4-deep ring (96 KB of LDS; 6 deep measured
@@ -869,6 +947,8 @@ void gemm_t(const T* A, const T* B, int M, int N, int K, const GemmEpiArgs& e, h
       const long t192 = (long)((M + 191) / 192) * (N / kBN);
       if (N % kGB == 0 && N <= 4096 && t256 >= cus - cus / 8)
         launch_gemm_big<T>(A, B, M, N, K, out, s);
+      else if (e.kind != GemmEpi::Geglu && N % 256 == 0 && N > 4096 && t256 >= cus)
+        launch_gemm_mfma<T, 256, 2, 256, 4>(A, B, M, N, K, out, s);
       else if (t64 <= cus)
         launch_gemm_mfma<T, 64, 4>(A, B, M, N, K, out, s);
       else if (e.kind != GemmEpi::Geglu && t128x192 > 0 && t128x192 <= cus)
@@ -903,7 +983,14 @@ template <typename T>
 void encoder_attn_t(const T* qkv, int nb, int S, int H, T* out, hipStream_t s, bool allow_mfma) {
   if constexpr (sizeof(T) == 2) {
     if (allow_mfma) {
-      hipLaunchKernelGGL(k_enc_attn_mfma<T>, dim3((S + kAQ - 1) / kAQ, nb * H), dim3(256), 0, s, qkv, S, H, out);
+      // Measured on MI355X at 1006 keys: one stream (256 blocks) 40.3 -> 34.0 us
+      // with the score-ahead variant; at 32 streams the plain one is as fast
+      // with three blocks per CU.
+      const dim3 grid((S + kAQ - 1) / kAQ, nb * H);
+      if ((long)grid.x * grid.y <= 2L * device_cus())
+        hipLaunchKernelGGL((k_enc_attn_mfma<T, true>), grid, dim3(256), 0, s, qkv, S, H, out);
+      else
+        hipLaunchKernelGGL((k_enc_attn_mfma<T, false>), grid, dim3(256), 0, s, qkv, S, H, out);
       return;
     }
   }
