@@ -931,7 +931,13 @@ void gemm_t(const T* A, const T* B, int M, int N, int K, const GemmEpiArgs& e, h
       // 256 x 256 tiles of 4 waves with 128 x 128 wave tiles (half the LDS
       // fragment reads per product) in the XCD-grouped order: 280 -> 234 us
       // at one stream, 7.35 -> 6.41 ms at 32 (the gated-GELU output measured
-      // slower with them).  Below that every block streams
+      // slower with them).  The XCD-grouped order also serves the 64-row
+      // tiles of one stream (O 12.6 -> 11.5 us, FFN down 25.3 -> 23.6 us),
+      // the 1024-wide output of K <= 1024 at 32 streams on 192-row tiles
+      // (the attention output projection: 249 -> 210 us against k_gemm_big;
+      // the FFN down projection, K = 2816, is as fast on k_gemm_big) and the
+      // gated-GELU output past two 192-row blocks per CU (1077 -> 998 us at
+      // 32 streams).  Below that every block streams
       // its operands at the latency of the last-level cache, so the tile is
       // chosen for the bytes it keeps in flight: a grid of at most one 64-row
       // tile per CU takes a 4-deep ring (96 KB of LDS; 6 deep measured
@@ -945,16 +951,21 @@ void gemm_t(const T* A, const T* B, int M, int N, int K, const GemmEpiArgs& e, h
       const long t256 = (long)((M + kGB - 1) / kGB) * (N / kGB), t64 = (long)((M + 63) / 64) * (N / kBN);
       const long t128x192 = N % 192 == 0 ? (long)((M + 127) / 128) * (N / 192) : 0;
       const long t192 = (long)((M + 191) / 192) * (N / kBN);
-      if (N % kGB == 0 && N <= 4096 && t256 >= cus - cus / 8)
-        launch_gemm_big<T>(A, B, M, N, K, out, s);
-      else if (e.kind != GemmEpi::Geglu && N % 256 == 0 && N > 4096 && t256 >= cus)
+      if (N % kGB == 0 && N <= 4096 && t256 >= cus - cus / 8) {
+        if (N == 1024 && K <= 1024)
+          launch_gemm_mfma<T, 192, 2, 128, 2>(A, B, M, N, K, out, s);
+        else
+          launch_gemm_big<T>(A, B, M, N, K, out, s);
+      } else if (e.kind != GemmEpi::Geglu && N % 256 == 0 && N > 4096 && t256 >= cus)
         launch_gemm_mfma<T, 256, 2, 256, 4>(A, B, M, N, K, out, s);
       else if (t64 <= cus)
-        launch_gemm_mfma<T, 64, 4>(A, B, M, N, K, out, s);
+        launch_gemm_mfma<T, 64, 4, 128, 4>(A, B, M, N, K, out, s);
       else if (e.kind != GemmEpi::Geglu && t128x192 > 0 && t128x192 <= cus)
         launch_gemm_mfma<T, 128, 3, 192>(A, B, M, N, K, out, s);
       else if (t192 <= 2 * cus)
         launch_gemm_mfma<T, 192, 2>(A, B, M, N, K, out, s);
+      else if (e.kind == GemmEpi::Geglu)
+        launch_gemm_mfma<T, 192, 2, 128, 4>(A, B, M, N, K, out, s);
       else if ((long)((M + 127) / 128) * (N / kBN) >= 3 * cus / 2)
         launch_gemm_mfma<T, 128>(A, B, M, N, K, out, s);
       else
