@@ -67,8 +67,10 @@ def algorithmic_bytes(cfg, esz=2, rows=2, frames=50, enc_len=1006, codebook=1024
     depth_kv = sum(cfg.num_depth_layers * kv_row * (l + 1) for l in range(L)) * frames
     temporal_kv = sum(cfg.num_temporal_layers * kv_row * (f + 1) for f in range(frames))
     total = frames * (temporal_step + L * depth_step) + depth_kv + temporal_kv
-    if os.environ.get("MRT_QKV_TABLE", "1") != "0":  # levels 1..: a table row for layer 0's q/k/v (frame_bytes)
-        total -= frames * (L - 1) * ((3 * HD * D + D) * esz - 3 * HD * esz)
+    if os.environ.get("MRT_QKV_TABLE", "1") != "0":
+        # levels 1..: one table row per stream (q | k | v of its fed token)
+        # instead of depth layer 0's q/k/v weights and norm (frame_bytes)
+        total -= frames * (L - 1) * ((3 * HD * D + D) * esz - (rows // 2) * 3 * HD * esz)
     return dict(depth_step=depth_step, temporal_step=temporal_step, chunk=total)
 
 

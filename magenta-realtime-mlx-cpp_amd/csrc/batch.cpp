@@ -128,13 +128,17 @@ void Batch::temporal_stack(int f, const int* fptr) {
 // Depth step l of every row in place on x (model.cpp:638-651 per row).
 // x_partials: the row partials of x are those the last bgemm_resid left
 // (the temporal step's output), else layer 0 normalises in its own pass.
-void Batch::depth_stack(void* x, int l, bool x_partials) {
+// qkv_fed: layer 0's q and ring slot l were written by the previous level's
+// draw from the q/k/v table (x = emb(token), a function of the token alone).
+void Batch::depth_stack(void* x, int l, bool x_partials, bool qkv_fed) {
   const Config& c = m.cfg;
   const int D = c.d_model, HD = c.hd(), FF = c.d_ff, H = c.num_heads, L = c.rvq_depth;
   for (int i = 0; i < c.num_depth_layers; ++i) {
     const DecoderLayerW& W = m.dep[i];
     char *dk = ring(dkv_, i, 0, L), *dv = ring(dkv_, i, 1, L);
-    if (i == 0 && !x_partials) {
+    if (i == 0 && qkv_fed) {
+      // nothing to compute: q / k / v are in place
+    } else if (i == 0 && !x_partials) {
       rmsnorm_rows(DType::BF16, x, W.norm_sa, 1e-6f, R, D, xn_, stream);
       bgemm_qkv(xn_, R, D, W.wqkv, HD, q_, dk, dv, H, L, l, nullptr, stream);
     } else {
@@ -158,11 +162,23 @@ void Batch::enqueue_frame(const GenOpts& o, int f, bool dynamic) {
   const int* fptr = dynamic ? d_frame_ : nullptr;
   const size_t row_bytes = static_cast<size_t>(R) * D * 2;
   SampleParams sp{o.guidance_weight, o.temperature, o.top_k, C, o.codec_offset, L, d_seeds_, noise_, F};
+  QkvFeed feed;
+  if (qkv_tab_ != nullptr) {
+    feed.table = qkv_tab_;
+    feed.q = q_;
+    feed.kc = ring(dkv_, 0, 0, c.rvq_depth);
+    feed.vc = ring(dkv_, 0, 1, c.rvq_depth);
+    feed.HD = c.hd();
+    feed.H = c.num_heads;
+    feed.Lmax = c.rvq_depth;
+    feed.offset = o.codec_offset;
+    feed.rows = (L - 1) * C;
+  }
   temporal_stack(f, fptr);
   if (o.record_temporal) copy_dev(static_cast<char*>(o.record_temporal) + f * row_bytes, t_in_, row_bytes, stream);
   for (int l = 0; l < L; ++l) {
     void* x = l == 0 ? t_in_ : d_in_;
-    depth_stack(x, l, l == 0 && c.num_temporal_layers > 0);
+    depth_stack(x, l, l == 0 && c.num_temporal_layers > 0, l > 0 && qkv_tab_ != nullptr);
     const char* head = static_cast<const char*>(m.lm_head) + static_cast<size_t>(o.codec_offset + C * l) * D * 2;
     if (c.num_depth_layers > 0) {
       bgemm_f32(x, R, D, head, C, logits_, C, stream, norm(m.dec_norm));
@@ -174,7 +190,8 @@ void Batch::enqueue_frame(const GenOpts& o, int f, bool dynamic) {
       copy_dev(o.record_slices + (static_cast<size_t>(f) * L + l) * R * C, logits_, static_cast<size_t>(R) * C * 4,
                stream);
     sample_levels(DType::BF16, B, logits_, sp, f, fptr, l, dynamic ? l : f * L + l, F * L,
-                  o.teacher ? d_teacher_ : nullptr, d_tokens_, nullptr, m.emb, D, d_in_, fsum_, t_in_, stream);
+                  o.teacher ? d_teacher_ : nullptr, d_tokens_, nullptr, m.emb, D, d_in_, fsum_, t_in_, stream,
+                  qkv_tab_ != nullptr ? &feed : nullptr);
   }
   if (dynamic) advance_counter(d_frame_, stream);
 }
@@ -207,6 +224,23 @@ void Batch::generate(const int32_t* enc_tokens_host, const GenOpts& o, const uin
     MRT_HIP_CHECK(hipMemcpyAsync(d_teacher_, t, nt * 4, hipMemcpyHostToDevice, stream));
   }
   MRT_HIP_CHECK(hipStreamSynchronize(stream));
+  // Depth layer 0 of levels 1.. reads the model's q/k/v table row of the fed
+  // token (built once per codec levels, before any capture) when every fed
+  // token lies in it: drawn tokens always do, teacher tokens are checked.
+  bool in_table = c.num_depth_layers > 0 && L >= 2;
+  if (o.teacher != nullptr) {
+    const size_t per = static_cast<size_t>(o.num_frames) * L;
+    for (int b = 0; b < B && in_table; ++b)
+      for (int f = 0; f < o.num_frames && in_table; ++f)
+        for (int l = 0; l + 1 < L; ++l) {
+          const int id = o.teacher[b * per + static_cast<size_t>(f) * L + l];
+          if (id < o.codec_offset + l * o.codebook || id >= o.codec_offset + (l + 1) * o.codebook) {
+            in_table = false;
+            break;
+          }
+        }
+  }
+  qkv_tab_ = in_table ? m.depth_qkv_table(o.codebook, o.codec_offset, stream) : nullptr;
 
   const bool graph = o.use_graph && !o.record_slices && !o.record_temporal;
   MRT_HIP_CHECK(hipEventRecord(ev_[0], stream));
@@ -217,7 +251,8 @@ void Batch::generate(const int32_t* enc_tokens_host, const GenOpts& o, const uin
   embed_fill(DType::BF16, m.emb, c.d_model, 0, R, t_in_, stream);
   if (graph) {
     const std::vector<double> key = {(double)L, (double)o.temperature, (double)o.top_k, (double)o.guidance_weight,
-                                     (double)o.codebook, (double)o.codec_offset, o.teacher ? 1.0 : 0.0};
+                                     (double)o.codebook, (double)o.codec_offset, o.teacher ? 1.0 : 0.0,
+                                     qkv_tab_ != nullptr ? 1.0 : 0.0};
     if (!graph_exec_ || key != graph_key_) {
       if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
       if (graph_) (void)hipGraphDestroy(graph_);

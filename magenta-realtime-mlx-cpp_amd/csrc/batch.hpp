@@ -89,7 +89,7 @@ class Batch {
  private:
   void enqueue_frame(const GenOpts& o, int f, bool dynamic);
   void temporal_stack(int f, const int* fptr);
-  void depth_stack(void* x, int l, bool x_partials);
+  void depth_stack(void* x, int l, bool x_partials, bool qkv_fed = false);
   // the norm (weights g) of a GEMM input whose row partials are at ssq_
   BNorm norm(const void* g) const { return BNorm{g, ssq_, 1e-6f}; }
   void* dalloc(size_t bytes);
@@ -101,6 +101,9 @@ class Batch {
   void *tkv_ = nullptr, *dkv_ = nullptr;
   void *t_in_ = nullptr, *d_in_ = nullptr, *xn_ = nullptr, *q_ = nullptr, *att_ = nullptr, *ffh_ = nullptr;
   float* ssq_ = nullptr;  // row partials of the last residual update: (R, d_model / 16)
+  // the model's depth layer-0 q/k/v table of the current call's codec levels,
+  // or nullptr (layer 0 computed at every level)
+  const void* qkv_tab_ = nullptr;
   void* fsum_ = nullptr;
   float* logits_ = nullptr;
   float* noise_ = nullptr;  // (B, F, L, 1024) Gumbel noise of the current call

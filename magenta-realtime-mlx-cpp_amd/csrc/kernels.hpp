@@ -119,9 +119,23 @@ void sample_level(DType dt, const float* logits, const SampleParams& p, int fram
 // feedback rows 2b and 2b + 1 of next_in / fsum / frame_mean).  frame_ptr
 // non-null: the frame index is read from it on the device and the slot
 // advances by frame * rvq_depth.
+// feed non-null (levels 0 .. L - 2): the fed token's row of a depth layer-0
+// q/k/v table (row = token - offset, 3 HD model-dtype values q | k | v) is
+// written for both rows of the stream: q into q (rows, HD), k and v into ring
+// slot level + 1 of the caches kc / vc (rows, H, Lmax, 64), so the next
+// level's layer 0 needs no norm or projection.  The caller passes a feed only
+// when every fed token lies in the table (drawn tokens always do).
+struct QkvFeed {
+  const void* table = nullptr;
+  void* q = nullptr;
+  void* kc = nullptr;
+  void* vc = nullptr;
+  int HD = 0, H = 0, Lmax = 0, offset = 0, rows = 0;
+};
 void sample_levels(DType dt, int streams, const float* logits, const SampleParams& p, int frame,
                    const int* frame_ptr, int level, int slot, int tstride, const int* teacher, int* tokens,
-                   int* drawn, const void* emb, int D, void* next_in, void* fsum, void* frame_mean, hipStream_t s);
+                   int* drawn, const void* emb, int D, void* next_in, void* fsum, void* frame_mean, hipStream_t s,
+                   const QkvFeed* feed = nullptr);
 
 // Every level of one frame drawn at once from logits (levels, 2, C) (one
 // stream, noise (F, L, C) tabulated or computed from p.seed[0]):

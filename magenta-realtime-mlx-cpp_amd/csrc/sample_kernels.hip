@@ -228,7 +228,8 @@ template <typename T>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_sample(
     const float* __restrict__ logits, SampleParams p, int frame, const int* __restrict__ frame_ptr, int level,
     int slot, int tstride, const int* __restrict__ teacher, int* __restrict__ tokens, int* __restrict__ drawn,
-    const T* __restrict__ emb, int D, T* __restrict__ next_in, T* __restrict__ fsum, T* __restrict__ fmean) {
+    const T* __restrict__ emb, int D, T* __restrict__ next_in, T* __restrict__ fsum, T* __restrict__ fmean,
+    QkvFeed feed) {
   using S = St<T>;
   __shared__ int fed_s;
   const int tid = threadIdx.x;
@@ -289,6 +290,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       fm[D + d] = m;
     }
   }
+  // the next level's depth layer-0 q/k/v from the table, for both rows
+  const int row = fed_s - feed.offset;
+  if (feed.table != nullptr && level + 1 < L && row >= 0 && row < feed.rows) {
+    const int HD = feed.HD;
+    const T* src = static_cast<const T*>(feed.table) + (size_t)row * 3 * HD;
+    for (int n = tid; n < 3 * HD; n += 256) {
+      const T v = src[n];
+      const int which = n / HD, nn = n - which * HD;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int m = 2 * stream + b;
+        if (which == 0) {
+          static_cast<T*>(feed.q)[(size_t)m * HD + nn] = v;
+        } else {
+          T* cache = static_cast<T*>(which == 1 ? feed.kc : feed.vc);
+          cache[(((size_t)m * feed.H + (nn >> 6)) * feed.Lmax + level + 1) * 64 + (nn & 63)] = v;
+        }
+      }
+    }
+  }
 }
 
 }  // namespace
@@ -308,13 +329,18 @@ void draw_levels(const float* logits, const SampleParams& p, int frame, int leve
 
 void sample_levels(DType dt, int streams, const float* logits, const SampleParams& p, int frame,
                    const int* frame_ptr, int level, int slot, int tstride, const int* teacher, int* tokens,
-                   int* drawn, const void* emb, int D, void* next_in, void* fsum, void* frame_mean, hipStream_t s) {
+                   int* drawn, const void* emb, int D, void* next_in, void* fsum, void* frame_mean, hipStream_t s,
+                   const QkvFeed* feed) {
   MRT_REQUIRE(p.codebook >= 1 && p.codebook <= 64 * kMaxPerLane, "sample: codebook must be <= 1024");
   MRT_REQUIRE(streams >= 1, "sample: no streams");
   MRT_REQUIRE(D >= 1 && D <= 256 * kFeedPer, "sample: d_model must be in [1, 2048]");
+  const QkvFeed fd = feed != nullptr ? *feed : QkvFeed{};
+  if (fd.table != nullptr)
+    MRT_REQUIRE(fd.q && fd.kc && fd.vc && fd.HD == fd.H * 64 && fd.Lmax >= p.rvq_depth && fd.rows >= 0,
+                "sample: bad q/k/v feed");
   MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_sample<T>, dim3(streams), dim3(256), 0, s, logits, p, frame, frame_ptr,
                                             level, slot, tstride, teacher, tokens, drawn, (const T*)emb, D,
-                                            (T*)next_in, (T*)fsum, (T*)frame_mean));
+                                            (T*)next_in, (T*)fsum, (T*)frame_mean, fd));
   MRT_HIP_CHECK(hipGetLastError());
 }
 
