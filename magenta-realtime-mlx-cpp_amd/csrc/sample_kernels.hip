@@ -22,6 +22,7 @@ namespace {
 constexpr int kMaxPerLane = 16;  // C <= 1024
 constexpr int kChainSteps = 3;   // restricted-argmax steps of a draw before its radix select
 constexpr int kFeedPer = 8;      // d_model elements per thread in the feedback (d_model <= 2048)
+constexpr int kQkvPer = 8;       // q (k, v) table elements per thread (heads x 64 <= 2048)
 
 // Sum over the 64 lanes with DPP (row shifts and broadcasts, no LDS
 // crossbar); every lane active; the result is wave-uniform.
@@ -269,12 +270,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   __syncthreads();
   // Token feedback (decode.cpp:476-484): both CFG rows take emb(fed); the
   // frame sum accumulates in the model dtype; at the last level the mean is
-  // the sum divided by L in the model dtype.
+  // the sum divided by L in the model dtype.  With a q/k/v feed, the fed
+  // token's table row (the next level's depth layer-0 q | k | v) is written
+  // for both rows too.  Every load of the token's rows is issued before the
+  // first store: the stores could alias them as far as the compiler knows, so
+  // interleaved they would serialise the round trips.
   const T* e = emb + (size_t)fed_s * D;
   const float Lf = S::rnd((float)L);
   T ev[kFeedPer];
 #pragma unroll
   for (int i = 0; i < kFeedPer; ++i) ev[i] = e[min(tid + 256 * i, D - 1)];
+  const int row = fed_s - feed.offset;
+  const bool fed_qkv = feed.table != nullptr && level + 1 < L && row >= 0 && row < feed.rows;
+  const int HD = feed.HD;
+  T qv[3][kQkvPer];  // q, k, v: elements tid + 256 i of each
+  if (fed_qkv) {
+    const T* src = static_cast<const T*>(feed.table) + (size_t)row * 3 * HD;
+#pragma unroll
+    for (int w = 0; w < 3; ++w)
+#pragma unroll
+      for (int i = 0; i < kQkvPer; ++i)
+        if (tid + 256 * i < HD) qv[w][i] = src[w * HD + tid + 256 * i];
+  }
 #pragma unroll
   for (int i = 0; i < kFeedPer; ++i) {
     const int d = tid + 256 * i;
@@ -290,23 +307,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       fm[D + d] = m;
     }
   }
-  // the next level's depth layer-0 q/k/v from the table, for both rows
-  const int row = fed_s - feed.offset;
-  if (feed.table != nullptr && level + 1 < L && row >= 0 && row < feed.rows) {
-    const int HD = feed.HD;
-    const T* src = static_cast<const T*>(feed.table) + (size_t)row * 3 * HD;
-    for (int n = tid; n < 3 * HD; n += 256) {
-      const T v = src[n];
-      const int which = n / HD, nn = n - which * HD;
+  if (fed_qkv) {
+    T* q = static_cast<T*>(feed.q);
+    T* kc = static_cast<T*>(feed.kc);
+    T* vc = static_cast<T*>(feed.vc);
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int m = 2 * stream + b;
-        if (which == 0) {
-          static_cast<T*>(feed.q)[(size_t)m * HD + nn] = v;
-        } else {
-          T* cache = static_cast<T*>(which == 1 ? feed.kc : feed.vc);
-          cache[(((size_t)m * feed.H + (nn >> 6)) * feed.Lmax + level + 1) * 64 + (nn & 63)] = v;
-        }
+    for (int b = 0; b < 2; ++b) {
+      const size_t m = 2 * stream + b;
+#pragma unroll
+      for (int i = 0; i < kQkvPer; ++i) {
+        const int nn = tid + 256 * i;
+        if (nn >= HD) continue;
+        const size_t slot = ((m * feed.H + (nn >> 6)) * feed.Lmax + level + 1) * 64 + (nn & 63);
+        q[m * HD + nn] = qv[0][i];
+        kc[slot] = qv[1][i];
+        vc[slot] = qv[2][i];
       }
     }
   }
@@ -336,7 +351,8 @@ void sample_levels(DType dt, int streams, const float* logits, const SampleParam
   MRT_REQUIRE(D >= 1 && D <= 256 * kFeedPer, "sample: d_model must be in [1, 2048]");
   const QkvFeed fd = feed != nullptr ? *feed : QkvFeed{};
   if (fd.table != nullptr)
-    MRT_REQUIRE(fd.q && fd.kc && fd.vc && fd.HD == fd.H * 64 && fd.Lmax >= p.rvq_depth && fd.rows >= 0,
+    MRT_REQUIRE(fd.q && fd.kc && fd.vc && fd.HD == fd.H * 64 && fd.HD <= 256 * kQkvPer &&
+                    fd.Lmax >= p.rvq_depth && fd.rows >= 0,
                 "sample: bad q/k/v feed");
   MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_sample<T>, dim3(streams), dim3(256), 0, s, logits, p, frame, frame_ptr,
                                             level, slot, tstride, teacher, tokens, drawn, (const T*)emb, D,
