@@ -745,19 +745,15 @@ __device__ __forceinline__ void attn_update(f32x16_t (&sc)[2], int kb, int S, in
     }
 }
 
-// AHEAD = false: tile j + 1's K and V are loaded while tile j is processed.
-// Sized for three blocks per CU (3 waves per SIMD: the register budget is
-// 170), which measured faster than the compiler's 196 registers at two.
-// AHEAD = true (grids of at most two blocks per CU, where one wave per SIMD
-// has no other wave to hide its latencies): the scores of tile j + 1 are
-// computed before tile j's softmax, so the two dependency chains overlap in
-// the wave; K is staged two tiles ahead and V one.  Both run the same
-// arithmetic on every query (attn_scores / attn_update over the tiles in
-// order), so their outputs are bit-equal and a stream's rows do not depend
-// on the batch it is encoded in.
-template <typename T, bool AHEAD>
-__global__ __launch_bounds__(256, AHEAD ? 2 : 3) void k_enc_attn_mfma(const T* __restrict__ qkv, int S, int H,
-                                                                     T* __restrict__ out) {
+// Tile j + 1's K and V are loaded (K rows first, then V rows) while tile j is
+// processed.  Sized for three blocks per CU (3 waves per SIMD: the register
+// budget is 170), which measured faster than the compiler's 196 registers at
+// two.  Every query runs attn_scores / attn_update over the tiles in order,
+// the same arithmetic whatever the grid, so a stream's rows do not depend on
+// the batch it is encoded in.
+template <typename T>
+__global__ __launch_bounds__(256, 3) void k_enc_attn_mfma(const T* __restrict__ qkv, int S, int H,
+                                                       T* __restrict__ out) {
   typedef typename Mfma<T>::v8 v8;
   __shared__ __attribute__((aligned(16))) T Ks[2][kAK * kALD];
   __shared__ __attribute__((aligned(16))) T Vt[2][64 * kALD];
@@ -818,41 +814,21 @@ __global__ __launch_bounds__(256, AHEAD ? 2 : 3) void k_enc_attn_mfma(const T* _
   gload(rv, 0, 2);
   kstore(0);
   vstore(0);
-  if constexpr (AHEAD) {
-    if (ntiles > 1) {
-      gload(rk, kAK, 1);
-      kstore(1);
-    }
-  }
   __syncthreads();
-  f32x16_t sc[2];
-  if constexpr (AHEAD) attn_scores<T>(Ks[0], qf, lq, hf, sc);
   for (int j = 0; j < ntiles; ++j) {
     const int cur = j & 1, kb = j * kAK;
-    if constexpr (AHEAD) {
-      if (j + 2 < ntiles) gload(rk, kb + 2 * kAK, 1);
-      if (j + 1 < ntiles) gload(rv, kb + kAK, 2);
-      f32x16_t sn[2];
-      if (j + 1 < ntiles) attn_scores<T>(Ks[cur ^ 1], qf, lq, hf, sn);
-      attn_update<T>(sc, kb, S, lq, hf, Vt[cur], m, lsum, acc);
-      if (j + 2 < ntiles) kstore(cur);
-      if (j + 1 < ntiles) vstore(cur ^ 1);
-      __syncthreads();
-#pragma unroll
-      for (int t = 0; t < 2; ++t) sc[t] = sn[t];
-    } else {
-      if (j + 1 < ntiles) {
-        gload(rk, kb + kAK, 1);
-        gload(rv, kb + kAK, 2);
-      }
-      attn_scores<T>(Ks[cur], qf, lq, hf, sc);
-      attn_update<T>(sc, kb, S, lq, hf, Vt[cur], m, lsum, acc);
-      if (j + 1 < ntiles) {
-        kstore(cur ^ 1);
-        vstore(cur ^ 1);
-      }
-      __syncthreads();
+    if (j + 1 < ntiles) {
+      gload(rk, kb + kAK, 1);
+      gload(rv, kb + kAK, 2);
     }
+    f32x16_t sc[2];
+    attn_scores<T>(Ks[cur], qf, lq, hf, sc);
+    attn_update<T>(sc, kb, S, lq, hf, Vt[cur], m, lsum, acc);
+    if (j + 1 < ntiles) {
+      kstore(cur ^ 1);
+      vstore(cur ^ 1);
+    }
+    __syncthreads();
   }
   if (q < S) {
     T* orow = out + ((size_t)b * S + q) * HD + h * 64;
@@ -994,14 +970,7 @@ template <typename T>
 void encoder_attn_t(const T* qkv, int nb, int S, int H, T* out, hipStream_t s, bool allow_mfma) {
   if constexpr (sizeof(T) == 2) {
     if (allow_mfma) {
-      // Measured on MI355X at 1006 keys: one stream (256 blocks) 40.3 -> 34.0 us
-      // with the score-ahead variant; at 32 streams the plain one is as fast
-      // with three blocks per CU.
-      const dim3 grid((S + kAQ - 1) / kAQ, nb * H);
-      if ((long)grid.x * grid.y <= 2L * device_cus())
-        hipLaunchKernelGGL((k_enc_attn_mfma<T, true>), grid, dim3(256), 0, s, qkv, S, H, out);
-      else
-        hipLaunchKernelGGL((k_enc_attn_mfma<T, false>), grid, dim3(256), 0, s, qkv, S, H, out);
+      hipLaunchKernelGGL(k_enc_attn_mfma<T>, dim3((S + kAQ - 1) / kAQ, nb * H), dim3(256), 0, s, qkv, S, H, out);
       return;
     }
   }
