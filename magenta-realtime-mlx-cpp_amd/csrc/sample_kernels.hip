@@ -15,6 +15,7 @@
 
 #include "device_utils.hpp"
 #include "kernels.hpp"
+#include "draw_block.hpp"
 
 namespace mrt {
 namespace {
@@ -197,17 +198,6 @@ __device__ __forceinline__ int wave_draw_rows(const float* __restrict__ l0, cons
   return bi;
 }
 
-__device__ __forceinline__ int wave_draw(const float* __restrict__ logits, const SampleParams& p, int stream,
-                                         int frame, int level) {
-  const int C = p.codebook;
-  const float* l0 = logits + (size_t)(2 * stream) * C;
-  const float* nz = p.noise != nullptr
-                        ? p.noise + (((size_t)stream * p.noise_frames + frame) * p.rvq_depth + level) * C
-                        : nullptr;
-  const uint64_t seed = p.seed != nullptr ? p.seed[stream] : p.seed_value;
-  return wave_draw_rows(l0, l0 + C, nz, p.temperature != 0.0f ? seed : 0, p, frame, level);
-}
-
 // Every level of one frame drawn at once (block l draws level l from logit
 // rows 2l, 2l + 1; the speculative verification pass): drawn[l] = the LLM id.
 __global__ __launch_bounds__(64) void k_draw_levels(const float* __restrict__ logits, SampleParams p, int frame,
@@ -222,17 +212,20 @@ __global__ __launch_bounds__(64) void k_draw_levels(const float* __restrict__ lo
 
 // Block b draws for stream b: logits rows (2b, 2b + 1), seed p.seed[b], token
 // slots slot + b * tstride; a non-null frame_ptr supplies the frame index.
-// Wave 0 draws; all four waves then write the token's embedding to both rows
-// of next_in and update the frame sum (whose rows they load while the draw
-// runs).
+// The whole block draws (block_draw, the frame kernel's draw) from the two
+// logit rows staged in LDS, then writes the token's embedding to both rows of
+// next_in and updates the frame sum (whose rows it loads before the draw).
 template <typename T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_sample(
+__global__ __launch_bounds__(kDrawThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_sample(
     const float* __restrict__ logits, SampleParams p, int frame, const int* __restrict__ frame_ptr, int level,
     int slot, int tstride, const int* __restrict__ teacher, int* __restrict__ tokens, int* __restrict__ drawn,
     const T* __restrict__ emb, int D, T* __restrict__ next_in, T* __restrict__ fsum, T* __restrict__ fmean,
     QkvFeed feed) {
   using S = St<T>;
-  __shared__ int fed_s;
+  constexpr int kRowsPer = 2 * 1024 / kDrawThreads;  // logit-row elements per thread (codebook <= 1024)
+  __shared__ float lg[2 * 1024];
+  __shared__ __align__(16) unsigned hist[kDrawHistWords];
+  __shared__ int wres[16];
   const int tid = threadIdx.x;
   const int stream = blockIdx.x;
   const int C = p.codebook, L = p.rvq_depth;
@@ -246,7 +239,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // the level's token is already known: only feed it to the next depth step
     // (the frame sum is not kept on this path)
     const T* e = emb + (size_t)tokens[slot] * D;
-    for (int d = tid; d < D; d += 256) {
+    for (int d = tid; d < D; d += kDrawThreads) {
       ni[d] = e[d];
       ni[D + d] = e[d];
     }
@@ -254,20 +247,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   T* fs = fsum + (size_t)(2 * stream) * D;
   T* fm = fmean + (size_t)(2 * stream) * D;
+  // Every load that does not depend on the token, issued before the first
+  // store: the frame sum rows, the level slice's two logit rows, the draw's
+  // noise (tabulated, or computed from the seed) and the teacher id.
   T fv[kFeedPer];
 #pragma unroll
-  for (int i = 0; i < kFeedPer; ++i) fv[i] = fs[min(tid + 256 * i, D - 1)];  // unused at level 0
-  if (tid < 64) {
-    const int bi = wave_draw(logits, p, stream, frame, level);
-    if (tid == 0) {
-      const int drawn_id = p.codec_offset + level * C + bi;
-      const int fed = teacher ? teacher[slot] : drawn_id;
-      tokens[slot] = fed;
-      if (drawn) drawn[slot] = drawn_id;
-      fed_s = fed;
-    }
+  for (int i = 0; i < kFeedPer; ++i) fv[i] = fs[min(tid + kDrawThreads * i, D - 1)];  // unused at level 0
+  const float* l0 = logits + (size_t)(2 * stream) * C;
+  float lv[kRowsPer];
+#pragma unroll
+  for (int i = 0; i < kRowsPer; ++i) lv[i] = l0[min(tid + kDrawThreads * i, 2 * C - 1)];
+  const float* nz = p.noise != nullptr
+                        ? p.noise + (((size_t)stream * p.noise_frames + frame) * p.rvq_depth + level) * C
+                        : nullptr;
+  const uint64_t seed = p.seed != nullptr ? p.seed[stream] : p.seed_value;
+  DrawPrefetch pf;
+#pragma unroll
+  for (int t = 0; t < kDrawPer; ++t) {
+    const int c = tid + kDrawThreads * t;
+    pf.gn[t] = (c < C && p.temperature != 0.0f) ? (nz != nullptr ? nz[c] : gumbel(seed, frame, level, c)) : 0.f;
   }
+  pf.teacher_id = teacher ? teacher[slot] : 0;
+#pragma unroll
+  for (int i = 0; i < kRowsPer; ++i)
+    if (tid + kDrawThreads * i < 2 * C) lg[tid + kDrawThreads * i] = lv[i];
+  draw_clear(hist);
   __syncthreads();
+  const int bi = block_draw(p, pf, lg, hist, wres, [](int) {});
+  const int drawn_id = p.codec_offset + level * C + bi;
+  const int fed = teacher ? pf.teacher_id : drawn_id;
+  if (tid == 0) {
+    tokens[slot] = fed;
+    if (drawn) drawn[slot] = drawn_id;
+  }
   // Token feedback (decode.cpp:476-484): both CFG rows take emb(fed); the
   // frame sum accumulates in the model dtype; at the last level the mean is
   // the sum divided by L in the model dtype.  With a q/k/v feed, the fed
@@ -275,12 +287,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // for both rows too.  Every load of the token's rows is issued before the
   // first store: the stores could alias them as far as the compiler knows, so
   // interleaved they would serialise the round trips.
-  const T* e = emb + (size_t)fed_s * D;
+  const T* e = emb + (size_t)fed * D;
   const float Lf = S::rnd((float)L);
   T ev[kFeedPer];
 #pragma unroll
   for (int i = 0; i < kFeedPer; ++i) ev[i] = e[min(tid + 256 * i, D - 1)];
-  const int row = fed_s - feed.offset;
+  const int row = fed - feed.offset;
   const bool fed_qkv = feed.table != nullptr && level + 1 < L && row >= 0 && row < feed.rows;
   const int HD = feed.HD;
   T qv[3][kQkvPer];  // q, k, v: elements tid + 256 i of each
@@ -354,7 +366,7 @@ void sample_levels(DType dt, int streams, const float* logits, const SampleParam
     MRT_REQUIRE(fd.q && fd.kc && fd.vc && fd.HD == fd.H * 64 && fd.HD <= 256 * kQkvPer &&
                     fd.Lmax >= p.rvq_depth && fd.rows >= 0,
                 "sample: bad q/k/v feed");
-  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_sample<T>, dim3(streams), dim3(256), 0, s, logits, p, frame, frame_ptr,
+  MRT_DTYPE_DISPATCH(dt, hipLaunchKernelGGL(k_sample<T>, dim3(streams), dim3(kDrawThreads), 0, s, logits, p, frame, frame_ptr,
                                             level, slot, tstride, teacher, tokens, drawn, (const T*)emb, D,
                                             (T*)next_in, (T*)fsum, (T*)frame_mean, fd));
   MRT_HIP_CHECK(hipGetLastError());

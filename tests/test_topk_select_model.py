@@ -1,12 +1,12 @@
 """The early stop of the top-k threshold selects in the draw kernels and the
-restricted-argmax chain of the frame kernel's draw, checked
+restricted-argmax chain of the block draw (frame kernel and per-level sampler), checked
 as an algorithm on the CPU (numpy models of the two device selects; the
 device code itself is checked draw by draw against the oracle sampler in the
 GPU tests).
 
 Both selects look for the k-th largest logit (ties counted) over
 order-preserving uint32 keys: the frame kernel byte-wise with histograms, the
-step / batched sampler bit by bit.  Each stops early once the keys at or
+speculative path's per-level wave draw bit by bit.  Each stops early once the keys at or
 above the current prefix (lower digits zero) are exactly the top-k set, and
 the draw then keeps v >= float(prefix).  These tests check that the kept set
 always equals {v >= k-th largest} (decode.cpp:119-121) on rows with ties,
@@ -57,7 +57,7 @@ def byte_select(v, k):
 
 
 def bit_select(v, k):
-    """Bitwise select with the early stop (the step / batched sampler)."""
+    """Bitwise select with the early stop (the wave draw of the speculative verification)."""
     key = _key(v)
     prefix = 0
     for bit in range(31, -1, -1):
