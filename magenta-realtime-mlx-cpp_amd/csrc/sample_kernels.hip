@@ -1,15 +1,14 @@
 // On-device CFG + level-masked top-k temperature sampling and token feedback
 // for one RVQ level (decode.cpp:71-148, 458-484).
 //
-// One workgroup per stream; its first wave draws, with the level's C logits
-// (C <= 1024) in registers, 16 per lane.  The draw is Gumbel-max over the kept entries with
-// Philox-4x32-10 noise.  When the winner over every candidate is itself in the
-// top-k set it is the answer; else up to 3 winners over {v > v_previous
-// winner} are tried the same way; otherwise the top-k threshold (the k-th largest
-// value, counting ties, i.e. min(topk(x, k)) of decode.cpp:119-120) is found
-// by a bitwise radix select over order-preserving float keys (at most 32
-// steps, each counting with a DPP wave sum; it stops once exactly k keys lie
-// at or above the prefix).
+// One 256-thread workgroup per stream (or per level, for the speculative
+// verification pass) runs the block draw of draw_block.hpp, the frame
+// kernel's: Gumbel-max over the kept entries with Philox-4x32-10 noise; when
+// the winner over every candidate is itself in the top-k set it is the
+// answer; else up to 3 winners over {v > v_previous winner} are tried the
+// same way; otherwise the top-k threshold (the k-th largest value, counting
+// ties, i.e. min(topk(x, k)) of decode.cpp:119-120) comes from a byte-wise
+// radix select over order-preserving float keys.
 #include <cmath>
 #include <mutex>
 
@@ -20,194 +19,50 @@
 namespace mrt {
 namespace {
 
-constexpr int kMaxPerLane = 16;  // C <= 1024
-constexpr int kChainSteps = 3;   // restricted-argmax steps of a draw before its radix select
 constexpr int kFeedPer = 8;      // d_model elements per thread in the feedback (d_model <= 2048)
 constexpr int kQkvPer = 8;       // q (k, v) table elements per thread (heads x 64 <= 2048)
 
-// Sum over the 64 lanes with DPP (row shifts and broadcasts, no LDS
-// crossbar); every lane active; the result is wave-uniform.
-__device__ __forceinline__ int dpp_sum_i(int v) {
-  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, true);   // quad_perm [1,0,3,2]
-  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, true);   // quad_perm [2,3,0,1]
-  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, true);  // row_bcast:15
-  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, true);  // row_bcast:31
-  return __builtin_amdgcn_readlane(v, 63);
-}
-
-// argmax with the first index winning ties (mx::argmax semantics).
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+// Stages a draw: the level slice's two logit rows (l0, l0 + C; C <= 1024)
+// into LDS `lg`, the noise of this thread's candidates into pf (the
+// tabulated row nz, or computed from the seed), the radix buffers 0 / 1 of
+// `hist` cleared.  Every load is issued before the first LDS store.  The
+// caller sets pf.teacher_id and orders the draw after a barrier.
+__device__ __forceinline__ void stage_draw(const float* __restrict__ l0, int C, const float* __restrict__ nz,
+                                           uint64_t seed, int frame, int level, float temperature, float* lg,
+                                           DrawPrefetch& pf, unsigned* hist) {
+  constexpr int kRowsPer = 2 * 1024 / kDrawThreads;  // logit-row elements per thread
+  const int tid = threadIdx.x;
+  float lv[kRowsPer];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o, 64);
-    const int oi = __shfl_xor(i, o, 64);
-    if (ov > v || (ov == v && oi < i)) {
-      v = ov;
-      i = oi;
-    }
+  for (int i = 0; i < kRowsPer; ++i) lv[i] = l0[min(tid + kDrawThreads * i, 2 * C - 1)];
+#pragma unroll
+  for (int t = 0; t < kDrawPer; ++t) {
+    const int c = tid + kDrawThreads * t;
+    pf.gn[t] = (c < C && temperature != 0.0f) ? (nz != nullptr ? nz[c] : gumbel(seed, frame, level, c)) : 0.f;
   }
-}
-
-// One draw by one wave (lane = threadIdx.x < 64) over the level's C entries
-// of the CFG rows l0 (conditioned) / l1 (unconditioned); nz: the draw's
-// tabulated noise row, or null to compute gumbel(seed, frame, level, i).
-// Returns the winning index.
-__device__ __forceinline__ int wave_draw_rows(const float* __restrict__ l0, const float* __restrict__ l1,
-                                              const float* __restrict__ nz, uint64_t seed, const SampleParams& p,
-                                              int frame, int level) {
-  const int lane = threadIdx.x;
-  const int C = p.codebook;
-  const float wc = 1.0f + p.guidance_weight;  // decode.cpp:255-256
-  const float wu = p.guidance_weight;
-
-  // Loads are unconditional (indices clamped into range) and all issued
-  // before the first use; entries past C are masked afterwards.
-  float a0[kMaxPerLane], a1[kMaxPerLane], gn[kMaxPerLane];
 #pragma unroll
-  for (int t = 0; t < kMaxPerLane; ++t) {
-    const int c = min(lane + 64 * t, C - 1);
-    a0[t] = l0[c];
-    a1[t] = l1[c];
-  }
-  if (p.temperature != 0.0f && nz != nullptr) {
-#pragma unroll
-    for (int t = 0; t < kMaxPerLane; ++t) gn[t] = nz[min(lane + 64 * t, C - 1)];
-  }
-  float v[kMaxPerLane];
-  {
-    // (1+w)*cond - w*uncond, each product rounded separately (decode.cpp:83-84):
-    // no fused multiply-add here.
-#pragma clang fp contract(off)
-#pragma unroll
-    for (int t = 0; t < kMaxPerLane; ++t) v[t] = lane + 64 * t < C ? wc * a0[t] - wu * a1[t] : -INFINITY;
-  }
-
-  bool done = false;
-  float best = -INFINITY;
-  int bi = 0x7fffffff;
-  if (p.temperature != 0.0f) {
-#pragma unroll
-    for (int t = 0; t < kMaxPerLane; ++t)
-      if (lane + 64 * t < C) v[t] = __fdiv_rn(v[t], p.temperature);
-    if (nz == nullptr) {
-      const uint64_t seed0 = seed;
-#pragma unroll
-      for (int t = 0; t < kMaxPerLane; ++t) {
-        const int c = lane + 64 * t;
-        gn[t] = c < C ? gumbel(seed0, frame, level, c) : 0.f;
-      }
-    }
-    if (p.top_k > 0 && p.top_k < C) {
-      // The Gumbel-max winner A over every candidate is the winner over the
-      // top-k set whenever A is in it, i.e. when fewer than k scaled logits
-      // exceed v_A (ties at the k-th value are kept); only otherwise is the
-      // threshold needed.
-#pragma unroll
-      for (int t = 0; t < kMaxPerLane; ++t) {
-        const int c = lane + 64 * t;
-        const float w = v[t] + gn[t];
-        if (c < C && (w > best || bi == 0x7fffffff)) {
-          best = w;
-          bi = c;
-        }
-      }
-      wave_argmax(best, bi);
-      float va = 0.f;
-#pragma unroll
-      for (int t = 0; t < kMaxPerLane; ++t)
-        if (lane + 64 * t == bi) va = v[t];
-      va = __shfl(va, bi & 63, 64);
-      int above = 0;
-#pragma unroll
-      for (int t = 0; t < kMaxPerLane; ++t) above += (lane + 64 * t < C && v[t] > va) ? 1 : 0;
-      done = dpp_sum_i(above) < p.top_k;
-      // Restricted steps: while the winner is outside the top-k set, the set
-      // lies within {v > v_winner}; the winner over that subset is the answer
-      // once it is in the set (it maximises over a superset of the set,
-      // smallest index first).  Each step shrinks the subset strictly.
-      for (int step = 0; step < kChainSteps && !done; ++step) {
-        best = -INFINITY;
-        bi = 0x7fffffff;
-#pragma unroll
-        for (int t = 0; t < kMaxPerLane; ++t) {
-          const int c = lane + 64 * t;
-          const float w = v[t] + gn[t];
-          if (c < C && v[t] > va && (w > best || bi == 0x7fffffff)) {
-            best = w;
-            bi = c;
-          }
-        }
-        wave_argmax(best, bi);
-        va = 0.f;
-#pragma unroll
-        for (int t = 0; t < kMaxPerLane; ++t)
-          if (lane + 64 * t == bi) va = v[t];
-        va = __shfl(va, bi & 63, 64);
-        above = 0;
-#pragma unroll
-        for (int t = 0; t < kMaxPerLane; ++t) above += (lane + 64 * t < C && v[t] > va) ? 1 : 0;
-        done = dpp_sum_i(above) < p.top_k;
-      }
-    }
-    if (!done && p.top_k > 0 && p.top_k < C) {
-      uint32_t key[kMaxPerLane];
-#pragma unroll
-      for (int t = 0; t < kMaxPerLane; ++t) key[t] = (lane + 64 * t < C) ? float_key(v[t]) : 0u;
-      uint32_t prefix = 0;
-      for (int bit = 31; bit >= 0; --bit) {
-        const uint32_t cand = prefix | (1u << bit);
-        int cnt = 0;
-#pragma unroll
-        for (int t = 0; t < kMaxPerLane; ++t) cnt += key[t] >= cand ? 1 : 0;
-        const int n = dpp_sum_i(cnt);
-        if (n >= p.top_k) prefix = cand;
-        // exactly k keys at or above cand: {key >= cand} is already the top-k
-        // set (no tie straddles it), so the lower bits are not needed; the
-        // threshold must be finite and not +0 (-0 compares equal to +0)
-        if (n == p.top_k && cand != 0x80000000u && __builtin_isfinite(key_float(cand))) break;
-      }
-      const float thr = key_float(prefix);
-#pragma unroll
-      for (int t = 0; t < kMaxPerLane; ++t)
-        if (v[t] < thr) v[t] = -INFINITY;  // decode.cpp:121
-    }
-    if (!done) {
-#pragma unroll
-      for (int t = 0; t < kMaxPerLane; ++t) {
-        const int c = lane + 64 * t;
-        if (c < C && v[t] != -INFINITY) v[t] = v[t] + gn[t];
-      }
-    }
-  }
-  if (!done) {
-    best = -INFINITY;
-    bi = 0x7fffffff;
-#pragma unroll
-    for (int t = 0; t < kMaxPerLane; ++t) {
-      const int c = lane + 64 * t;
-      if (c < C && (v[t] > best || bi == 0x7fffffff)) {  // c ascends: first max wins
-        best = v[t];
-        bi = c;
-      }
-    }
-    wave_argmax(best, bi);
-  }
-
-  return bi;
+  for (int i = 0; i < kRowsPer; ++i)
+    if (tid + kDrawThreads * i < 2 * C) lg[tid + kDrawThreads * i] = lv[i];
+  draw_clear(hist);
 }
 
 // Every level of one frame drawn at once (block l draws level l from logit
-// rows 2l, 2l + 1; the speculative verification pass): drawn[l] = the LLM id.
-__global__ __launch_bounds__(64) void k_draw_levels(const float* __restrict__ logits, SampleParams p, int frame,
-                                                    int* __restrict__ drawn) {
-  const int l = blockIdx.x, C = p.codebook;
-  const float* l0 = logits + (size_t)(2 * l) * C;
+// rows 2l, 2l + 1 with the block draw; the speculative verification pass):
+// drawn[l] = the LLM id.
+__global__ __launch_bounds__(kDrawThreads) void k_draw_levels(const float* __restrict__ logits, SampleParams p,
+                                                              int frame, int* __restrict__ drawn) {
+  __shared__ float lg[2 * 1024];
+  __shared__ __align__(16) unsigned hist[kDrawHistWords];
+  __shared__ int wres[16];
+  const int l = blockIdx.x, C = p.codebook, tid = threadIdx.x;
   const float* nz = p.noise != nullptr ? p.noise + ((size_t)frame * p.rvq_depth + l) * C : nullptr;
-  const uint64_t seed = p.seed != nullptr ? p.seed[0] : p.seed_value;
-  const int bi = wave_draw_rows(l0, l0 + C, nz, p.temperature != 0.0f ? seed : 0, p, frame, l);
-  if (threadIdx.x == 0) drawn[l] = p.codec_offset + l * C + bi;
+  DrawPrefetch pf;
+  stage_draw(logits + (size_t)(2 * l) * C, C, nz, p.seed != nullptr ? p.seed[0] : p.seed_value, frame, l,
+             p.temperature, lg, pf, hist);
+  pf.teacher_id = 0;
+  __syncthreads();
+  const int bi = block_draw(p, pf, lg, hist, wres, [](int) {});
+  if (tid == 0) drawn[l] = p.codec_offset + l * C + bi;
 }
 
 // Block b draws for stream b: logits rows (2b, 2b + 1), seed p.seed[b], token
@@ -222,7 +77,6 @@ __global__ __launch_bounds__(kDrawThreads) __attribute__((amdgpu_waves_per_eu(1,
     const T* __restrict__ emb, int D, T* __restrict__ next_in, T* __restrict__ fsum, T* __restrict__ fmean,
     QkvFeed feed) {
   using S = St<T>;
-  constexpr int kRowsPer = 2 * 1024 / kDrawThreads;  // logit-row elements per thread (codebook <= 1024)
   __shared__ float lg[2 * 1024];
   __shared__ __align__(16) unsigned hist[kDrawHistWords];
   __shared__ int wres[16];
@@ -253,25 +107,13 @@ __global__ __launch_bounds__(kDrawThreads) __attribute__((amdgpu_waves_per_eu(1,
   T fv[kFeedPer];
 #pragma unroll
   for (int i = 0; i < kFeedPer; ++i) fv[i] = fs[min(tid + kDrawThreads * i, D - 1)];  // unused at level 0
-  const float* l0 = logits + (size_t)(2 * stream) * C;
-  float lv[kRowsPer];
-#pragma unroll
-  for (int i = 0; i < kRowsPer; ++i) lv[i] = l0[min(tid + kDrawThreads * i, 2 * C - 1)];
   const float* nz = p.noise != nullptr
                         ? p.noise + (((size_t)stream * p.noise_frames + frame) * p.rvq_depth + level) * C
                         : nullptr;
-  const uint64_t seed = p.seed != nullptr ? p.seed[stream] : p.seed_value;
   DrawPrefetch pf;
-#pragma unroll
-  for (int t = 0; t < kDrawPer; ++t) {
-    const int c = tid + kDrawThreads * t;
-    pf.gn[t] = (c < C && p.temperature != 0.0f) ? (nz != nullptr ? nz[c] : gumbel(seed, frame, level, c)) : 0.f;
-  }
   pf.teacher_id = teacher ? teacher[slot] : 0;
-#pragma unroll
-  for (int i = 0; i < kRowsPer; ++i)
-    if (tid + kDrawThreads * i < 2 * C) lg[tid + kDrawThreads * i] = lv[i];
-  draw_clear(hist);
+  stage_draw(logits + (size_t)(2 * stream) * C, C, nz, p.seed != nullptr ? p.seed[stream] : p.seed_value, frame,
+             level, p.temperature, lg, pf, hist);
   __syncthreads();
   const int bi = block_draw(p, pf, lg, hist, wres, [](int) {});
   const int drawn_id = p.codec_offset + level * C + bi;
@@ -349,8 +191,8 @@ void sample_level(DType dt, const float* logits, const SampleParams& p, int fram
 }
 
 void draw_levels(const float* logits, const SampleParams& p, int frame, int levels, int* drawn, hipStream_t s) {
-  MRT_REQUIRE(p.codebook >= 1 && p.codebook <= 64 * kMaxPerLane, "draw: codebook must be <= 1024");
-  hipLaunchKernelGGL(k_draw_levels, dim3(levels), dim3(64), 0, s, logits, p, frame, drawn);
+  MRT_REQUIRE(p.codebook >= 1 && p.codebook <= kDrawThreads * kDrawPer, "draw: codebook must be <= 1024");
+  hipLaunchKernelGGL(k_draw_levels, dim3(levels), dim3(kDrawThreads), 0, s, logits, p, frame, drawn);
   MRT_HIP_CHECK(hipGetLastError());
 }
 
@@ -358,7 +200,7 @@ void sample_levels(DType dt, int streams, const float* logits, const SampleParam
                    const int* frame_ptr, int level, int slot, int tstride, const int* teacher, int* tokens,
                    int* drawn, const void* emb, int D, void* next_in, void* fsum, void* frame_mean, hipStream_t s,
                    const QkvFeed* feed) {
-  MRT_REQUIRE(p.codebook >= 1 && p.codebook <= 64 * kMaxPerLane, "sample: codebook must be <= 1024");
+  MRT_REQUIRE(p.codebook >= 1 && p.codebook <= kDrawThreads * kDrawPer, "sample: codebook must be <= 1024");
   MRT_REQUIRE(streams >= 1, "sample: no streams");
   MRT_REQUIRE(D >= 1 && D <= 256 * kFeedPer, "sample: d_model must be in [1, 2048]");
   const QkvFeed fd = feed != nullptr ? *feed : QkvFeed{};

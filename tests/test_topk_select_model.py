@@ -1,14 +1,13 @@
 """The early stop of the top-k threshold selects in the draw kernels and the
-restricted-argmax chain of the block draw (frame kernel and per-level sampler), checked
-as an algorithm on the CPU (numpy models of the two device selects; the
-device code itself is checked draw by draw against the oracle sampler in the
-GPU tests).
+restricted-argmax chain of the block draw (draw_block.hpp: the frame kernel and
+the per-level samplers), checked as an algorithm on the CPU (numpy models of
+the device select and chain; the device code itself is checked draw by draw
+against the oracle sampler in the GPU tests).
 
-Both selects look for the k-th largest logit (ties counted) over
-order-preserving uint32 keys: the frame kernel byte-wise with histograms, the
-speculative path's per-level wave draw bit by bit.  Each stops early once the keys at or
-above the current prefix (lower digits zero) are exactly the top-k set, and
-the draw then keeps v >= float(prefix).  These tests check that the kept set
+The select looks for the k-th largest logit (ties counted) over
+order-preserving uint32 keys, byte-wise with histograms.  It stops early once
+the keys at or above the current prefix (lower digits zero) are exactly the
+top-k set, and the draw then keeps v >= float(prefix).  These tests check that the kept set
 always equals {v >= k-th largest} (decode.cpp:119-121) on rows with ties,
 signed zeros, denormals, all-negative and huge values, so the early stop
 cannot change a draw."""
@@ -56,20 +55,6 @@ def byte_select(v, k):
     return v >= _key_float(prefix), 3
 
 
-def bit_select(v, k):
-    """Bitwise select with the early stop (the wave draw of the speculative verification)."""
-    key = _key(v)
-    prefix = 0
-    for bit in range(31, -1, -1):
-        cand = prefix | (1 << bit)
-        n = int((key >= np.uint64(cand)).sum())
-        if n >= k:
-            prefix = cand
-        if n == k and _stop_ok(cand):
-            return v >= _key_float(cand), bit
-    return v >= _key_float(prefix), -1
-
-
 def _rows(rng, n):
     for i in range(n):
         kind = i % 5
@@ -94,8 +79,6 @@ def test_early_stop_keeps_the_top_k_set():
         got, p = byte_select(v, k)
         np.testing.assert_array_equal(got, exact)
         stops.add(p)
-        got, _ = bit_select(v, k)
-        np.testing.assert_array_equal(got, exact)
     assert stops == {0, 1, 2, 3}  # every stopping point was exercised
 
 
@@ -111,7 +94,6 @@ def test_guarded_thresholds_are_left_to_the_full_select():
     for x, k in ((v, 3), (w, 4), (w, 2), (z, 3), (z, 4)):
         exact = x >= np.sort(x)[::-1][k - 1]
         np.testing.assert_array_equal(byte_select(x, k)[0], exact)
-        np.testing.assert_array_equal(bit_select(x, k)[0], exact)
 
 
 @pytest.mark.parametrize("k", [40])
